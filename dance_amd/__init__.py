@@ -1,0 +1,364 @@
+"""dance_amd: MI355X-native (gfx950) GPU Vamana graph construction.
+
+Host-side Python mirror of the reference's builder interface
+(/root/reference/include/gpu_vamana_builder.h). All device work runs in
+libdance_hip.so (hand-written HIP kernels); this module only marshals numpy
+arrays and device pointers across the C ABI. There is no CPU fallback: if the
+library is missing, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libdance_hip.so")
+
+DTYPE_F32, DTYPE_U8, DTYPE_F16 = 0, 1, 2
+INVALID = 0xFFFFFFFF
+
+_u32p = C.POINTER(C.c_uint32)
+_f32p = C.POINTER(C.c_float)
+
+
+class GPUVamanaStats(C.Structure):
+    """Layout of GPUVamanaStats (reference include/gpu_vamana_builder.h:11-28)."""
+
+    _fields_ = [
+        ("medoid_seconds", C.c_double),
+        ("h2d_seconds", C.c_double),
+        ("search_online_insert_seconds", C.c_double),
+        ("reverse_seconds", C.c_double),
+        ("final_prune_seconds", C.c_double),
+        ("d2h_seconds", C.c_double),
+        ("gpu_build_seconds", C.c_double),
+        ("distance_computations", C.c_uint64),
+        ("online_insert_attempts", C.c_uint64),
+        ("online_insert_mutations", C.c_uint64),
+        ("reverse_candidate_overflows", C.c_uint64),
+        ("reverse_proposals", C.c_uint64),
+        ("reverse_touched_rows", C.c_uint64),
+        ("reverse_csr_seconds", C.c_double),
+        ("selective_active_nodes", C.c_uint32),
+    ]
+
+
+class DanceKernelProfile(C.Structure):
+    _fields_ = [
+        ("medoid_ms", C.c_double), ("init_ms", C.c_double), ("search_ms", C.c_double),
+        ("reverse_ms", C.c_double), ("merge_ms", C.c_double), ("prune_ms", C.c_double),
+        ("total_ms", C.c_double),
+        ("iterations", C.c_uint32), ("vector_bytes", C.c_uint32),
+        ("search_dist", C.c_uint64), ("insert_dist", C.c_uint64), ("expansions", C.c_uint64),
+        ("vis_skips", C.c_uint64), ("merge_dist", C.c_uint64), ("prune_dist", C.c_uint64),
+        ("reverse_edges", C.c_uint64), ("touched_rows", C.c_uint64),
+        ("search_bytes", C.c_double), ("merge_bytes", C.c_double), ("prune_bytes", C.c_double),
+        ("reverse_bytes", C.c_double),
+    ]
+
+
+def struct_dict(s: C.Structure) -> dict:
+    return {name: getattr(s, name) for name, _ in s._fields_}
+
+
+# Every symbol the C ABI exports (include/*.h). Tests check the library
+# exports exactly these.
+EXPORTS = [
+    "gpu_vamana_build", "gpu_vamana_build_float",
+    "gpu_vamana_vnew2_build", "gpu_vamana_vnew2_build_float",
+    "gpu_vamana_vnew2_build_device", "gpu_vamana_vnew2_build_device_float",
+    "gpu_vamana_get_last_medoid", "gpu_vamana_get_last_stats",
+    "gpu_vamana_vnew2_get_last_medoid", "gpu_vamana_vnew2_get_last_stats",
+    "dance_vamana_build_resident", "dance_get_last_kernel_profile",
+    "dance_set_profile", "dance_get_profile",
+    "dance_stage_distances", "dance_stage_medoid", "dance_stage_init", "dance_stage_search",
+    "dance_stage_reverse_merge", "dance_stage_prune", "dance_stage_sort_pairs", "dance_stage_scan",
+    "dance_synth_f32", "dance_synth_u8",
+]
+
+_LIB = None
+
+
+def lib() -> C.CDLL:
+    """Loads libdance_hip.so; raises if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run `python -m dance_amd.build` "
+                               "(or __graft_entry__.build()) first")
+        L = C.CDLL(LIB_PATH)
+        u32, f32, vp, i32 = C.c_uint32, C.c_float, C.c_void_p, C.c_int
+        build_args = [vp, u32, u32, u32, u32, u32, u32, _u32p, _u32p]
+        for name in ("gpu_vamana_build", "gpu_vamana_build_float", "gpu_vamana_vnew2_build",
+                     "gpu_vamana_vnew2_build_float"):
+            getattr(L, name).argtypes = build_args
+            getattr(L, name).restype = i32
+        for name in ("gpu_vamana_vnew2_build_device", "gpu_vamana_vnew2_build_device_float"):
+            getattr(L, name).argtypes = [vp, u32, u32, u32, u32, u32, u32, C.POINTER(vp),
+                                         C.POINTER(vp), C.POINTER(vp)]
+            getattr(L, name).restype = i32
+        for name in ("gpu_vamana_get_last_medoid", "gpu_vamana_vnew2_get_last_medoid"):
+            getattr(L, name).restype = u32
+            getattr(L, name).argtypes = []
+        for name in ("gpu_vamana_get_last_stats", "gpu_vamana_vnew2_get_last_stats"):
+            getattr(L, name).argtypes = [C.POINTER(GPUVamanaStats)]
+            getattr(L, name).restype = None
+        L.dance_vamana_build_resident.argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, vp, vp]
+        L.dance_vamana_build_resident.restype = i32
+        L.dance_get_last_kernel_profile.argtypes = [C.POINTER(DanceKernelProfile)]
+        L.dance_get_last_kernel_profile.restype = None
+        L.dance_set_profile.argtypes = [C.c_char_p]
+        L.dance_set_profile.restype = i32
+        L.dance_get_profile.argtypes = []
+        L.dance_get_profile.restype = C.c_char_p
+        L.dance_stage_distances.argtypes = [vp, i32, u32, u32, _u32p, _u32p, C.c_uint64, _f32p]
+        L.dance_stage_medoid.argtypes = [vp, i32, u32, u32, _f32p, _u32p, _u32p]
+        L.dance_stage_init.argtypes = [vp, i32, u32, u32, u32, u32, _u32p, _u32p, _u32p, _u32p, _f32p]
+        L.dance_stage_search.argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, f32, u32,
+                                         _u32p, _u32p, _u32p, _u32p, _f32p]
+        L.dance_stage_reverse_merge.argtypes = [vp, i32, u32, u32, u32, u32, _u32p, _u32p, _f32p,
+                                                u32, u32, _u32p, _u32p]
+        L.dance_stage_prune.argtypes = [vp, i32, u32, u32, u32, u32, u32, f32, _u32p, _u32p, _f32p,
+                                        _u32p, _u32p]
+        L.dance_stage_sort_pairs.argtypes = [_u32p, _u32p, C.c_uint64, u32, _u32p, _u32p]
+        L.dance_stage_scan.argtypes = [_u32p, C.c_uint64, _u32p]
+        for name in ("dance_stage_distances", "dance_stage_medoid", "dance_stage_init",
+                     "dance_stage_search", "dance_stage_reverse_merge", "dance_stage_prune",
+                     "dance_stage_sort_pairs", "dance_stage_scan"):
+            getattr(L, name).restype = i32
+        L.dance_synth_f32.argtypes = [C.c_uint64, u32, u32, u32, u32, f32, i32, _f32p]
+        L.dance_synth_f32.restype = i32
+        L.dance_synth_u8.argtypes = [C.c_uint64, u32, u32, u32, u32, f32, C.POINTER(C.c_uint8)]
+        L.dance_synth_u8.restype = i32
+        _LIB = L
+    return _LIB
+
+
+def _p(a: np.ndarray, ctype):
+    return a.ctypes.data_as(C.POINTER(ctype))
+
+
+def dtype_code(arr: np.ndarray) -> int:
+    if arr.dtype == np.float32:
+        return DTYPE_F32
+    if arr.dtype == np.uint8:
+        return DTYPE_U8
+    if arr.dtype == np.float16:
+        return DTYPE_F16
+    raise TypeError(f"unsupported vector dtype {arr.dtype}")
+
+
+class BuildError(RuntimeError):
+    pass
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise BuildError(f"{what} failed with return code {rc}")
+
+
+@dataclass
+class BuildResult:
+    graph: np.ndarray   # N x R uint32, rows padded with INVALID after the degree
+    degree: np.ndarray  # N uint32
+    medoid: int
+    stats: dict
+    kernel_profile: dict
+
+
+def set_profile(name: str) -> None:
+    _check(lib().dance_set_profile(name.encode()), f"dance_set_profile({name})")
+
+
+def get_profile() -> str:
+    return lib().dance_get_profile().decode()
+
+
+def last_kernel_profile() -> dict:
+    p = DanceKernelProfile()
+    lib().dance_get_last_kernel_profile(C.byref(p))
+    return struct_dict(p)
+
+
+def last_stats() -> dict:
+    s = GPUVamanaStats()
+    lib().gpu_vamana_vnew2_get_last_stats(C.byref(s))
+    return struct_dict(s)
+
+
+def vamana_build(data: np.ndarray, R: int = 64, L: int = 100, C_: int = 80, STEPS: int = 64,
+                 entry: str = "vnew2") -> BuildResult:
+    """gpu_vamana_vnew2_build[_float] on host vectors (uint8 or float32)."""
+    data = np.ascontiguousarray(data)
+    if data.ndim != 2:
+        raise ValueError("data must be N x dim")
+    N, dim = data.shape
+    graph = np.empty((N, R), dtype=np.uint32)
+    degree = np.empty(N, dtype=np.uint32)
+    L_ = lib()
+    if data.dtype == np.float32:
+        fn = L_.gpu_vamana_vnew2_build_float if entry == "vnew2" else L_.gpu_vamana_build_float
+    elif data.dtype == np.uint8:
+        fn = L_.gpu_vamana_vnew2_build if entry == "vnew2" else L_.gpu_vamana_build
+    else:
+        raise TypeError("vamana_build takes uint8 or float32 vectors")
+    rc = fn(data.ctypes.data, N, dim, R, L, C_, STEPS, _p(graph, C.c_uint32), _p(degree, C.c_uint32))
+    _check(rc, "gpu_vamana_vnew2_build")
+    return BuildResult(graph, degree, int(L_.gpu_vamana_vnew2_get_last_medoid()), last_stats(),
+                       last_kernel_profile())
+
+
+def vamana_build_resident(d_data: int, dtype: int, N: int, dim: int, R: int, L: int, C_: int, STEPS: int,
+                          d_graph: int, d_degree: int) -> None:
+    """dance_vamana_build_resident on device pointers (e.g. torch tensor data_ptr())."""
+    _check(lib().dance_vamana_build_resident(d_data, dtype, N, dim, R, L, C_, STEPS, d_graph, d_degree),
+           "dance_vamana_build_resident")
+
+
+# ---------------------------------------------------------------- stage hooks
+
+def stage_distances(data: np.ndarray, a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    data = np.ascontiguousarray(data)
+    a = np.ascontiguousarray(a, dtype=np.uint32)
+    b = np.ascontiguousarray(b, dtype=np.uint32)
+    out = np.empty(a.shape[0], dtype=np.float32)
+    _check(lib().dance_stage_distances(data.ctypes.data, dtype_code(data), data.shape[0], data.shape[1],
+                                       _p(a, C.c_uint32), _p(b, C.c_uint32), a.shape[0],
+                                       _p(out, C.c_float)), "dance_stage_distances")
+    return out
+
+
+def stage_medoid(data: np.ndarray):
+    data = np.ascontiguousarray(data)
+    N = data.shape[0]
+    nc = min(1024, N)
+    scores = np.empty(nc, dtype=np.float32)
+    cands = np.empty(nc, dtype=np.uint32)
+    med = np.zeros(1, dtype=np.uint32)
+    _check(lib().dance_stage_medoid(data.ctypes.data, dtype_code(data), N, data.shape[1],
+                                    _p(scores, C.c_float), _p(cands, C.c_uint32), _p(med, C.c_uint32)),
+           "dance_stage_medoid")
+    return int(med[0]), scores, cands
+
+
+@dataclass
+class GraphState:
+    cur: np.ndarray
+    deg_cur: np.ndarray
+    work: np.ndarray
+    deg_work: np.ndarray
+    wd: np.ndarray
+
+    def copy(self) -> "GraphState":
+        return GraphState(self.cur.copy(), self.deg_cur.copy(), self.work.copy(), self.deg_work.copy(),
+                          self.wd.copy())
+
+    @staticmethod
+    def empty(N: int, R: int, C_: int) -> "GraphState":
+        return GraphState(np.full((N, R), INVALID, np.uint32), np.zeros(N, np.uint32),
+                          np.full((N, C_), INVALID, np.uint32), np.zeros(N, np.uint32),
+                          np.full((N, C_), np.finfo(np.float32).max, np.float32))
+
+
+def _gs_ptrs(g: GraphState):
+    return (_p(g.cur, C.c_uint32), _p(g.deg_cur, C.c_uint32), _p(g.work, C.c_uint32),
+            _p(g.deg_work, C.c_uint32), _p(g.wd, C.c_float))
+
+
+def stage_init(data: np.ndarray, R: int, C_: int) -> GraphState:
+    data = np.ascontiguousarray(data)
+    g = GraphState.empty(data.shape[0], R, C_)
+    _check(lib().dance_stage_init(data.ctypes.data, dtype_code(data), data.shape[0], data.shape[1], R, C_,
+                                  *_gs_ptrs(g)), "dance_stage_init")
+    return g
+
+
+def stage_search(data: np.ndarray, g: GraphState, L: int, steps: int, alpha: float, start: int) -> GraphState:
+    data = np.ascontiguousarray(data)
+    g = g.copy()
+    N, R = g.cur.shape
+    _check(lib().dance_stage_search(data.ctypes.data, dtype_code(data), N, data.shape[1], R, L,
+                                    g.work.shape[1], steps, alpha, start, *_gs_ptrs(g)), "dance_stage_search")
+    return g
+
+
+def stage_reverse_merge(data: np.ndarray, g: GraphState, heavy_threshold: int = 0, heavy_sample: int = 0):
+    data = np.ascontiguousarray(data)
+    g = g.copy()
+    N, R = g.cur.shape
+    offsets = np.zeros(N + 1, dtype=np.uint32)
+    ids = np.zeros(N * R, dtype=np.uint32)
+    _check(lib().dance_stage_reverse_merge(data.ctypes.data, dtype_code(data), N, data.shape[1], R,
+                                           g.work.shape[1], _p(g.work, C.c_uint32), _p(g.deg_work, C.c_uint32),
+                                           _p(g.wd, C.c_float), heavy_threshold, heavy_sample,
+                                           _p(offsets, C.c_uint32), _p(ids, C.c_uint32)),
+           "dance_stage_reverse_merge")
+    return g, offsets, ids[: offsets[-1]]
+
+
+def stage_prune(data: np.ndarray, g: GraphState, min_degree: int, alpha: float) -> GraphState:
+    data = np.ascontiguousarray(data)
+    g = g.copy()
+    N, R = g.cur.shape
+    _check(lib().dance_stage_prune(data.ctypes.data, dtype_code(data), N, data.shape[1], R, g.work.shape[1],
+                                   min_degree, alpha, _p(g.work, C.c_uint32), _p(g.deg_work, C.c_uint32),
+                                   _p(g.wd, C.c_float), _p(g.cur, C.c_uint32), _p(g.deg_cur, C.c_uint32)),
+           "dance_stage_prune")
+    return g
+
+
+def stage_sort_pairs(keys: np.ndarray, vals: np.ndarray, key_bits: int):
+    keys = np.ascontiguousarray(keys, dtype=np.uint32)
+    vals = np.ascontiguousarray(vals, dtype=np.uint32)
+    ok = np.empty_like(keys)
+    ov = np.empty_like(vals)
+    _check(lib().dance_stage_sort_pairs(_p(keys, C.c_uint32), _p(vals, C.c_uint32), keys.shape[0], key_bits,
+                                        _p(ok, C.c_uint32), _p(ov, C.c_uint32)), "dance_stage_sort_pairs")
+    return ok, ov
+
+
+def stage_scan(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.uint32)
+    out = np.empty_like(x)
+    _check(lib().dance_stage_scan(_p(x, C.c_uint32), x.shape[0], _p(out, C.c_uint32)), "dance_stage_scan")
+    return out
+
+
+# ------------------------------------------------------------------ workloads
+
+def synth_f32(seed: int, stream: int, n: int, dim: int, centers: int, sigma: float,
+              normalize: bool = True) -> np.ndarray:
+    out = np.empty((n, dim), dtype=np.float32)
+    _check(lib().dance_synth_f32(seed, stream, n, dim, centers, sigma, int(normalize), _p(out, C.c_float)),
+           "dance_synth_f32")
+    return out
+
+
+def synth_u8(seed: int, stream: int, n: int, dim: int, centers: int, sigma: float) -> np.ndarray:
+    out = np.empty((n, dim), dtype=np.uint8)
+    _check(lib().dance_synth_u8(seed, stream, n, dim, centers, sigma, _p(out, C.c_uint8)), "dance_synth_u8")
+    return out
+
+
+# BASELINE.json configs (synthetic generators of SURVEY 8(d)); stream 0 =
+# base vectors, stream 1 = queries.
+CONFIGS = {
+    "c1": dict(kind="f32", n=100_000, dim=96, centers=0, sigma=1.0, nq=1_000, R=64, L=100, C=80, STEPS=64),
+    "c2": dict(kind="f32", n=1_000_000, dim=96, centers=256, sigma=0.3, nq=10_000, R=64, L=100, C=80, STEPS=64),
+    "c3": dict(kind="f32", n=10_000_000, dim=96, centers=256, sigma=0.3, nq=10_000, R=64, L=100, C=80, STEPS=64),
+    "c4": dict(kind="u8", n=10_000_000, dim=128, centers=1024, sigma=0.3, nq=10_000, R=64, L=100, C=80, STEPS=64),
+}
+
+
+def make_workload(cfg: dict, n: int | None = None, seed: int = 42):
+    n = cfg["n"] if n is None else n
+    if cfg["kind"] == "f32":
+        base = synth_f32(seed, 0, n, cfg["dim"], cfg["centers"], cfg["sigma"], True)
+        q = synth_f32(seed, 1, cfg["nq"], cfg["dim"], cfg["centers"], cfg["sigma"], True)
+    else:
+        base = synth_u8(seed, 0, n, cfg["dim"], cfg["centers"], cfg["sigma"])
+        q = synth_u8(seed, 1, cfg["nq"], cfg["dim"], cfg["centers"], cfg["sigma"])
+    return base, q

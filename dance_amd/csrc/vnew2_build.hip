@@ -1,0 +1,1060 @@
+// Host orchestration of the standard GPU Vamana build and the C ABI of
+// include/gpu_vamana_builder.h + include/dance_hip.h.
+//
+// Build = approximate medoid -> hashed R-regular init -> ITERS x
+//   (search + online robust insert -> reverse edges (stable radix sort by
+//    target) + merge -> RobustPrune, degree fill in the last iteration),
+// the schedule of gpu_vamana_build_impl (/root/reference/src/gpu_vamana_vnew2.cu:2170-2855).
+//
+// Device layout (one allocation each, row-major):
+//   rows   N x stride16 x 16 B   vectors, each row zero-padded to 16 B
+//   cur    N x R   u32            current graph (INV-padded)
+//   work   N x C   u32 + wd N x C f32   candidate rows with distances
+//   keys/vals 2 x 2 x N*R u32     reverse-edge radix sort double buffers
+//   offs   N+1 u32                reverse CSR offsets
+// All kernels run on one stream; stages are timed with HIP events.
+//
+// Algorithmic bytes reported for the roofline (per kernel, summed over the
+// build; V = bytes of one vector row, counted on device by each wave):
+//   search: (search_dist + insert_dist) * V + expansions * (4R + 4)
+//           + N * (V + 4R + 4 + 16C)            (own vector, cur row, work row r/w)
+//   merge : merge_dist * V + reverse_edges * 4 + touched_rows * (V + 16C + 8)
+//   prune : prune_dist * V + (selected rows) * V + N * 24C
+//   reverse (keys + sort): N*R*(4*3) + passes * N*R * 20
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cstddef>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <type_traits>
+#include <utility>
+#include <vector>
+
+#include "../../include/dance_hip.h"
+#include "../../include/gpu_vamana_builder.h"
+#include "prims.h"
+#include "vnew2_kernels.h"
+
+static_assert(sizeof(GPUVamanaStats) == 7 * 8 + 6 * 8 + 8 + 8, "GPUVamanaStats layout");
+static_assert(offsetof(GPUVamanaStats, distance_computations) == 56, "GPUVamanaStats layout");
+static_assert(offsetof(GPUVamanaStats, reverse_csr_seconds) == 104, "GPUVamanaStats layout");
+static_assert(offsetof(GPUVamanaStats, selective_active_nodes) == 112, "GPUVamanaStats layout");
+
+namespace dance {
+
+#define DHIP(call)                                                                                  \
+  do {                                                                                              \
+    hipError_t e_ = (call);                                                                         \
+    if (e_ != hipSuccess) {                                                                         \
+      std::fprintf(stderr, "[dance_hip] HIP error '%s' at %s:%d\n", hipGetErrorString(e_), __FILE__, \
+                   __LINE__);                                                                       \
+      return -1;                                                                                    \
+    }                                                                                               \
+  } while (0)
+
+#define DCHECK(call)            \
+  do {                          \
+    if ((call) != 0) return -1; \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// Profiles (reference CMake DANCE_PROFILE, patch:2400-2462; effective
+// constants of include/gpu_vamana_config.h).
+// ---------------------------------------------------------------------------
+struct Profile {
+  const char* name;
+  bool fp16;
+  uint32_t heavy_threshold, heavy_sample;
+};
+constexpr uint32_t kIters = 4;              // VAMANA_ITERS
+constexpr float kAlpha = 1.2f;              // VAMANA_ALPHA (last iteration only)
+constexpr uint32_t kFinalMinDegree = 64;    // FINAL_MIN_DEGREE
+constexpr uint32_t kWarmupSteps = 64;       // WARMUP_EXPAND_STEPS
+constexpr uint32_t kCoarseIters = 2;        // COARSE_WARMUP_ITERS
+constexpr uint32_t kMedoidCandidates = 1024;
+constexpr uint32_t kMedoidSamples = 4096;
+
+static const Profile kProfiles[] = {
+    {"QUALITY", false, 0, 0},
+    {"FAST_SMALL", true, 0, 0},
+    {"PRO6000_100M", true, 256, 384},
+    {"FILTERED_PAPER", true, 256, 384},
+};
+
+static std::mutex g_mu;
+static int g_profile = -1;
+
+static int profile_index_locked() {
+  if (g_profile < 0) {
+    g_profile = 0;
+    if (const char* e = std::getenv("DANCE_PROFILE")) {
+      for (int i = 0; i < 4; ++i)
+        if (std::strcmp(e, kProfiles[i].name) == 0) g_profile = i;
+    }
+  }
+  return g_profile;
+}
+
+static uint32_t g_last_medoid = 0;
+static GPUVamanaStats g_last_stats{};
+static DanceKernelProfile g_last_prof{};
+
+static double now_sec() {
+  return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+static bool verbose() {
+  const char* e = std::getenv("DANCE_VERBOSE");
+  return e && e[0] && e[0] != '0';
+}
+
+static uint32_t elem_bytes(int dtype) { return dtype == DANCE_F32 ? 4u : dtype == DANCE_F16 ? 2u : 1u; }
+
+// Smallest compiled chunks-per-lane count covering nch chunks.
+static int pick_cpl(uint32_t nch) {
+  const uint32_t need = (nch + 7u) / 8u;
+  static const int opts[] = {1, 2, 3, 4, 8, 16};
+  for (int o : opts)
+    if ((uint32_t)o >= need) return o;
+  return -1;
+}
+
+template <int V>
+using IC = std::integral_constant<int, V>;
+
+template <typename Fn>
+static int with_cpl(int cpl, Fn&& fn) {
+  switch (cpl) {
+    case 1: return fn(IC<1>{});
+    case 2: return fn(IC<2>{});
+    case 3: return fn(IC<3>{});
+    case 4: return fn(IC<4>{});
+    case 8: return fn(IC<8>{});
+    case 16: return fn(IC<16>{});
+  }
+  std::fprintf(stderr, "[dance_hip] unsupported vector width\n");
+  return -1;
+}
+
+template <typename Fn>
+static int with_dt_cpl(int dtype, int cpl, Fn&& fn) {
+  switch (dtype) {
+    case DANCE_F32: return with_cpl(cpl, [&](auto c) { return fn(IC<DANCE_F32>{}, c); });
+    case DANCE_U8: return with_cpl(cpl, [&](auto c) { return fn(IC<DANCE_U8>{}, c); });
+    case DANCE_F16: return with_cpl(cpl, [&](auto c) { return fn(IC<DANCE_F16>{}, c); });
+  }
+  std::fprintf(stderr, "[dance_hip] unsupported dtype %d\n", dtype);
+  return -1;
+}
+
+// ---------------------------------------------------------------------------
+// RAII device memory.
+// ---------------------------------------------------------------------------
+struct DevBuf {
+  void* p = nullptr;
+  size_t bytes = 0;
+  DevBuf() = default;
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  ~DevBuf() {
+    if (p) (void)hipFree(p);
+  }
+  int alloc(size_t b) {
+    if (p) {
+      (void)hipFree(p);
+      p = nullptr;
+    }
+    bytes = b;
+    if (b == 0) return 0;
+    hipError_t e = hipMalloc(&p, b);
+    if (e != hipSuccess) {
+      std::fprintf(stderr, "[dance_hip] hipMalloc(%zu) failed: %s\n", b, hipGetErrorString(e));
+      p = nullptr;
+      return -1;
+    }
+    return 0;
+  }
+  void* release() {
+    void* q = p;
+    p = nullptr;
+    return q;
+  }
+  template <typename T>
+  T* as() const {
+    return static_cast<T*>(p);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Scan / sort drivers.
+// ---------------------------------------------------------------------------
+struct ScanWorkspace {
+  DevBuf buf;
+  std::vector<size_t> level_off;
+  int prepare(size_t n) {
+    level_off.clear();
+    size_t total = 0, m = n;
+    while (true) {
+      const size_t tiles = (m + kScanTile - 1) / kScanTile;
+      level_off.push_back(total);
+      total += tiles;
+      if (tiles <= 1) break;
+      m = tiles;
+    }
+    if (buf.bytes >= total * 4) return 0;
+    return buf.alloc(std::max<size_t>(total * 4, 256));
+  }
+};
+
+static int scan_exclusive_level(uint32_t* d, size_t n, ScanWorkspace& ws, size_t level, hipStream_t s) {
+  if (n == 0) return 0;
+  const size_t tiles = (n + kScanTile - 1) / kScanTile;
+  uint32_t* partial = ws.buf.as<uint32_t>() + ws.level_off[level];
+  hipLaunchKernelGGL(k_scan_tile, dim3((uint32_t)tiles), dim3(kScanThreads), 0, s, d, n, partial);
+  DHIP(hipGetLastError());
+  if (tiles > 1) {
+    DCHECK(scan_exclusive_level(partial, tiles, ws, level + 1, s));
+    hipLaunchKernelGGL(k_scan_add, dim3((uint32_t)tiles), dim3(kScanThreads), 0, s, d, n, partial);
+    DHIP(hipGetLastError());
+  }
+  return 0;
+}
+
+static int scan_exclusive(uint32_t* d, size_t n, ScanWorkspace& ws, hipStream_t s) {
+  DCHECK(ws.prepare(n));
+  return scan_exclusive_level(d, n, ws, 0, s);
+}
+
+struct SortWorkspace {
+  DevBuf hist;
+  ScanWorkspace scan;
+};
+
+// Stable sort of (keys, vals) by the low key_bits bits. Returns the index
+// (0 or 1) of the buffer pair holding the result.
+static int radix_sort_pairs(uint32_t* keys[2], uint32_t* vals[2], size_t n, uint32_t key_bits, SortWorkspace& ws,
+                            hipStream_t s, int* result_index) {
+  int cur = 0;
+  if (n == 0 || key_bits == 0) {
+    *result_index = 0;
+    return 0;
+  }
+  const size_t tiles = (n + kRadixTile - 1) / kRadixTile;
+  if (ws.hist.bytes < tiles * 256 * 4) DCHECK(ws.hist.alloc(tiles * 256 * 4));
+  for (uint32_t shift = 0; shift < key_bits; shift += 8) {
+    hipLaunchKernelGGL(k_radix_hist, dim3((uint32_t)tiles), dim3(kRadixThreads), 0, s, keys[cur], n, shift,
+                       (uint32_t)tiles, ws.hist.as<uint32_t>());
+    DHIP(hipGetLastError());
+    DCHECK(scan_exclusive(ws.hist.as<uint32_t>(), tiles * 256, ws.scan, s));
+    hipLaunchKernelGGL(k_radix_scatter, dim3((uint32_t)tiles), dim3(kRadixThreads), 0, s, keys[cur], vals[cur], n,
+                       shift, (uint32_t)tiles, ws.hist.as<uint32_t>(), keys[cur ^ 1], vals[cur ^ 1]);
+    DHIP(hipGetLastError());
+    cur ^= 1;
+  }
+  *result_index = cur;
+  return 0;
+}
+
+static uint32_t bit_length(uint32_t x) {
+  uint32_t b = 0;
+  while (x) {
+    ++b;
+    x >>= 1;
+  }
+  return b;
+}
+
+// ---------------------------------------------------------------------------
+// Vector upload into the padded row layout.
+// ---------------------------------------------------------------------------
+struct Rows {
+  DevBuf owned;
+  RowSet rs{};
+  int dtype = DANCE_F32;
+  uint32_t N = 0, dim = 0;
+  uint32_t vbytes() const { return dim * elem_bytes(dtype); }
+};
+
+__global__ void k_f32_to_f16_rows(const float* __restrict__ src, uint32_t N, uint32_t dim,
+                                  _Float16* __restrict__ dst, uint32_t dst_stride_elems) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)N * dim) return;
+  const size_t r = i / dim, c = i % dim;
+  dst[r * dst_stride_elems + c] = (_Float16)src[i];  // round to nearest even
+}
+
+static int setup_rows(Rows& out, const void* src, bool src_on_device, int src_dtype, int store_dtype, uint32_t N,
+                      uint32_t dim, hipStream_t s) {
+  out.dtype = store_dtype;
+  out.N = N;
+  out.dim = dim;
+  const size_t row_bytes = (size_t)dim * elem_bytes(store_dtype);
+  const size_t stride = (row_bytes + 15) / 16 * 16;
+  const uint32_t nch = (uint32_t)(stride / 16);
+  out.rs.stride16 = nch;
+  out.rs.nch = nch;
+  const size_t src_row_bytes = (size_t)dim * elem_bytes(src_dtype);
+  if (src_dtype == store_dtype && src_on_device && stride == row_bytes &&
+      (reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
+    out.rs.rows = static_cast<const uint4*>(src);
+    return 0;
+  }
+  DCHECK(out.owned.alloc(stride * N));
+  if (src_dtype == store_dtype) {
+    if (stride != row_bytes) DHIP(hipMemsetAsync(out.owned.p, 0, stride * N, s));
+    DHIP(hipMemcpy2DAsync(out.owned.p, stride, src, row_bytes, row_bytes, N,
+                          src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, s));
+  } else {
+    // fp32 input stored as fp16 (FAST_SMALL): upload, convert on device.
+    DevBuf tmp;
+    const void* fsrc = src;
+    if (!src_on_device) {
+      DCHECK(tmp.alloc(src_row_bytes * N));
+      DHIP(hipMemcpyAsync(tmp.p, src, src_row_bytes * N, hipMemcpyHostToDevice, s));
+      fsrc = tmp.p;
+    }
+    DHIP(hipMemsetAsync(out.owned.p, 0, stride * N, s));
+    const size_t total = (size_t)N * dim;
+    hipLaunchKernelGGL(k_f32_to_f16_rows, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, s,
+                       static_cast<const float*>(fsrc), N, dim, out.owned.as<_Float16>(), (uint32_t)(stride / 2));
+    DHIP(hipGetLastError());
+    DHIP(hipStreamSynchronize(s));
+  }
+  out.rs.rows = out.owned.as<const uint4>();
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Graph state + per-stage launchers.
+// ---------------------------------------------------------------------------
+struct State {
+  uint32_t N = 0, R = 0, C = 0;
+  DevBuf cur, deg_cur, work, deg_work, wd;
+  GraphBufs g() {
+    return GraphBufs{N, R, C, cur.as<uint32_t>(), deg_cur.as<uint32_t>(), work.as<uint32_t>(),
+                     deg_work.as<uint32_t>(), wd.as<float>()};
+  }
+  int alloc(uint32_t N_, uint32_t R_, uint32_t C_, bool with_cur = true) {
+    N = N_;
+    R = R_;
+    C = C_;
+    if (with_cur) DCHECK(cur.alloc((size_t)N * R * 4));
+    DCHECK(deg_cur.alloc((size_t)N * 4));
+    DCHECK(work.alloc((size_t)N * C * 4));
+    DCHECK(deg_work.alloc((size_t)N * 4));
+    DCHECK(wd.alloc((size_t)N * C * 4));
+    return 0;
+  }
+};
+
+static uint32_t round64(uint32_t x) { return (x + 63u) / 64u * 64u; }
+
+static uint32_t wave_grid(uint32_t n) { return (n + kWavesPerBlock - 1) / kWavesPerBlock; }
+
+static int launch_medoid(const Rows& rows, hipStream_t s, float* d_scores, uint32_t* d_cands, uint32_t nc,
+                         uint32_t ns) {
+  const int cpl = pick_cpl(rows.rs.nch);
+  return with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
+    hipLaunchKernelGGL((k_medoid<decltype(dt)::value, decltype(c)::value>), dim3(wave_grid(nc)), dim3(kBlock), 0, s,
+                       rows.rs, rows.N, nc, ns, d_scores, d_cands);
+    DHIP(hipGetLastError());
+    return 0;
+  });
+}
+
+static int launch_init(const Rows& rows, GraphBufs g, hipStream_t s) {
+  const int cpl = pick_cpl(rows.rs.nch);
+  return with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
+    hipLaunchKernelGGL((k_init<decltype(dt)::value, decltype(c)::value>), dim3(wave_grid(g.N)), dim3(kBlock), 0, s,
+                       rows.rs, g);
+    DHIP(hipGetLastError());
+    return 0;
+  });
+}
+
+static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t steps, float alpha, uint32_t start,
+                         VCounters* ctr, hipStream_t s) {
+  const int cpl = pick_cpl(rows.rs.nch);
+  const uint32_t Cp = round64(g.C);
+  const size_t lds = (size_t)kWavesPerBlock * search_lds_words(Cp) * 4;
+  SearchArgs a{rows.rs, g, L, steps, start, alpha, nullptr, ctr};
+  if (L > 256) {
+    std::fprintf(stderr, "[dance_hip] L=%u exceeds the supported maximum 256\n", L);
+    return -1;
+  }
+  return with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
+    constexpr int DT = decltype(dt)::value, CPL = decltype(c)::value;
+    if (L <= 128)
+      hipLaunchKernelGGL((k_search<DT, CPL, 2>), dim3(wave_grid(g.N)), dim3(kBlock), lds, s, a, Cp);
+    else
+      hipLaunchKernelGGL((k_search<DT, CPL, 4>), dim3(wave_grid(g.N)), dim3(kBlock), lds, s, a, Cp);
+    DHIP(hipGetLastError());
+    return 0;
+  });
+}
+
+static int launch_prune(const Rows& rows, GraphBufs g, uint32_t min_degree, float alpha, VCounters* ctr,
+                        hipStream_t s) {
+  const int cpl = pick_cpl(rows.rs.nch);
+  const uint32_t Cp = round64(g.C), Rp = round64(g.R);
+  const size_t lds = (size_t)kWavesPerBlock * prune_lds_words(Cp, Rp) * 4;
+  PruneArgs a{rows.rs, g, min_degree, alpha, nullptr, ctr};
+  return with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
+    hipLaunchKernelGGL((k_prune<decltype(dt)::value, decltype(c)::value>), dim3(wave_grid(g.N)), dim3(kBlock), lds,
+                       s, a, Cp, Rp);
+    DHIP(hipGetLastError());
+    return 0;
+  });
+}
+
+struct ReverseWs {
+  DevBuf keys[2], vals[2], offs;
+  SortWorkspace sort;
+  ScanWorkspace scan;
+  int alloc(uint32_t N, uint32_t R) {
+    const size_t items = (size_t)N * R;
+    for (int i = 0; i < 2; ++i) {
+      DCHECK(keys[i].alloc(std::max<size_t>(items, 1) * 4));
+      DCHECK(vals[i].alloc(std::max<size_t>(items, 1) * 4));
+    }
+    DCHECK(offs.alloc(((size_t)N + 1) * 4));
+    return 0;
+  }
+};
+
+// Reverse CSR in canonical (ascending source) order. Returns the sorted
+// source array through *srcs_out.
+static int build_reverse_csr(GraphBufs g, ReverseWs& ws, hipStream_t s, const uint32_t** srcs_out) {
+  const size_t items = (size_t)g.N * g.R;
+  DHIP(hipMemsetAsync(ws.offs.p, 0, ((size_t)g.N + 1) * 4, s));
+  if (items > 0) {
+    hipLaunchKernelGGL(k_rev_keys, dim3((uint32_t)((items + 255) / 256)), dim3(256), 0, s, g.work, g.deg_work, g.N,
+                       g.R, g.C, ws.keys[0].as<uint32_t>(), ws.vals[0].as<uint32_t>(), ws.offs.as<uint32_t>());
+    DHIP(hipGetLastError());
+  }
+  DCHECK(scan_exclusive(ws.offs.as<uint32_t>(), (size_t)g.N + 1, ws.scan, s));
+  uint32_t* kb[2] = {ws.keys[0].as<uint32_t>(), ws.keys[1].as<uint32_t>()};
+  uint32_t* vb[2] = {ws.vals[0].as<uint32_t>(), ws.vals[1].as<uint32_t>()};
+  int which = 0;
+  DCHECK(radix_sort_pairs(kb, vb, items, bit_length(g.N), ws.sort, s, &which));
+  *srcs_out = vb[which];
+  return 0;
+}
+
+static int launch_merge(const Rows& rows, GraphBufs g, const uint32_t* offs, const uint32_t* srcs,
+                        const Profile& prof, VCounters* ctr, hipStream_t s) {
+  const int cpl = pick_cpl(rows.rs.nch);
+  const uint32_t Cp = round64(g.C);
+  const size_t lds = (size_t)kWavesPerBlock * merge_lds_words(Cp) * 4;
+  MergeArgs a{rows.rs, g, offs, srcs, prof.heavy_threshold, prof.heavy_sample, nullptr, ctr};
+  return with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
+    hipLaunchKernelGGL((k_merge<decltype(dt)::value, decltype(c)::value>), dim3(wave_grid(g.N)), dim3(kBlock), lds,
+                       s, a, Cp);
+    DHIP(hipGetLastError());
+    return 0;
+  });
+}
+
+// ---------------------------------------------------------------------------
+// Full build on resident rows.
+// ---------------------------------------------------------------------------
+struct StageEvents {
+  std::vector<hipEvent_t> ev;
+  ~StageEvents() {
+    for (auto e : ev) (void)hipEventDestroy(e);
+  }
+  hipEvent_t make() {
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    ev.push_back(e);
+    return e;
+  }
+};
+
+static float elapsed_ms(hipEvent_t a, hipEvent_t b) {
+  float ms = 0.f;
+  if (a && b && hipEventElapsedTime(&ms, a, b) == hipSuccess) return ms;
+  return 0.f;
+}
+
+static int validate(uint32_t N, uint32_t dim, uint32_t R, uint32_t L, uint32_t C, uint32_t& STEPS) {
+  if (N == 0 || dim == 0 || R == 0 || L == 0 || C == 0 || STEPS == 0) {
+    std::fprintf(stderr, "[gpu_vamana_build] invalid parameters: N=%u dim=%u R=%u L=%u C=%u STEPS=%u\n", N, dim, R, L,
+                 C, STEPS);
+    return -1;
+  }
+  if (C < R) {
+    std::fprintf(stderr, "[gpu_vamana_build] invalid parameters: C=%u must be >= R=%u\n", C, R);
+    return -1;
+  }
+  if (STEPS > L) {
+    std::fprintf(stderr, "[gpu_vamana_build] STEPS=%u is larger than L=%u, clamp STEPS to L.\n", STEPS, L);
+    STEPS = L;
+  }
+  if (L > 256) {
+    std::fprintf(stderr, "[gpu_vamana_build] L=%u exceeds the supported maximum 256\n", L);
+    return -1;
+  }
+  if ((uint64_t)N * R > 0xFFFFFFFFull) {
+    std::fprintf(stderr, "[gpu_vamana_build] N*R=%llu exceeds 2^32 reverse edges\n",
+                 (unsigned long long)N * R);
+    return -1;
+  }
+  return 0;
+}
+
+// Runs the whole build. On success st.cur/deg_cur hold the graph.
+// Callers hold g_mu and pass the active profile.
+static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint32_t STEPS, const Profile& prof,
+                     State& st, hipStream_t s, GPUVamanaStats* stats, DanceKernelProfile* kp, uint32_t* medoid_out) {
+  const uint32_t N = rows.N;
+  if (pick_cpl(rows.rs.nch) < 0) {
+    std::fprintf(stderr, "[gpu_vamana_build] dim=%u is beyond the supported row width\n", rows.dim);
+    return -1;
+  }
+  DCHECK(st.alloc(N, R, C, st.cur.p == nullptr));
+  ReverseWs rws;
+  DCHECK(rws.alloc(N, R));
+  DevBuf ctr_buf, scores, cands;
+  DCHECK(ctr_buf.alloc(sizeof(VCounters)));
+  DHIP(hipMemsetAsync(ctr_buf.p, 0, sizeof(VCounters), s));
+  VCounters* ctr = ctr_buf.as<VCounters>();
+  GraphBufs g = st.g();
+  StageEvents E;
+  hipEvent_t e0 = E.make(), e_med = E.make(), e_init = E.make();
+  if (!e0 || !e_med || !e_init) return -1;
+  DHIP(hipEventRecord(e0, s));
+
+  // Approximate medoid (vnew2.cu:2359-2479): device scores, host top-1.
+  const double t_med = now_sec();
+  const uint32_t nc = std::min(kMedoidCandidates, N), ns = std::min(kMedoidSamples, N);
+  DCHECK(scores.alloc(nc * 4));
+  DCHECK(cands.alloc(nc * 4));
+  DCHECK(launch_medoid(rows, s, scores.as<float>(), cands.as<uint32_t>(), nc, ns));
+  std::vector<float> hs(nc);
+  std::vector<uint32_t> hc(nc);
+  DHIP(hipMemcpyAsync(hs.data(), scores.p, nc * 4, hipMemcpyDeviceToHost, s));
+  DHIP(hipMemcpyAsync(hc.data(), cands.p, nc * 4, hipMemcpyDeviceToHost, s));
+  DHIP(hipEventRecord(e_med, s));
+  DHIP(hipStreamSynchronize(s));
+  uint32_t best = DANCE_INV;
+  float bs = FLT_MAX;
+  for (uint32_t i = 0; i < nc; ++i)
+    if (hs[i] < bs) {
+      bs = hs[i];
+      best = i;
+    }
+  const uint32_t start = best == DANCE_INV ? 0u : hc[best];
+  if (stats) stats->medoid_seconds = now_sec() - t_med;
+
+  DCHECK(launch_init(rows, g, s));
+  DHIP(hipEventRecord(e_init, s));
+
+  struct IterEv {
+    hipEvent_t s0, s1, r1, m1, p1;
+  };
+  std::vector<IterEv> iev(kIters);
+  for (auto& ie : iev) {
+    ie.s0 = E.make();
+    ie.s1 = E.make();
+    ie.r1 = E.make();
+    ie.m1 = E.make();
+    ie.p1 = E.make();
+    if (!ie.s0 || !ie.s1 || !ie.r1 || !ie.m1 || !ie.p1) return -1;
+  }
+  for (uint32_t it = 0; it < kIters; ++it) {
+    const float alpha = (it + 1 >= kIters) ? kAlpha : 1.0f;
+    uint32_t steps = STEPS;
+    if (it < kCoarseIters && steps > kWarmupSteps) steps = kWarmupSteps;
+    if (verbose())
+      std::printf("[gpu_vamana_build] iteration %u / %u, alpha=%.3f\n", it + 1, kIters, (double)alpha);
+    DHIP(hipEventRecord(iev[it].s0, s));
+    DCHECK(launch_search(rows, g, L, steps, alpha, start, ctr, s));
+    DHIP(hipEventRecord(iev[it].s1, s));
+    const uint32_t* srcs = nullptr;
+    DCHECK(build_reverse_csr(g, rws, s, &srcs));
+    DHIP(hipEventRecord(iev[it].r1, s));
+    DCHECK(launch_merge(rows, g, rws.offs.as<uint32_t>(), srcs, prof, ctr, s));
+    DHIP(hipEventRecord(iev[it].m1, s));
+    const uint32_t md = (it + 1 == kIters) ? kFinalMinDegree : 0u;
+    DCHECK(launch_prune(rows, g, md, alpha, ctr, s));
+    DHIP(hipEventRecord(iev[it].p1, s));
+  }
+  DHIP(hipStreamSynchronize(s));
+  DHIP(hipGetLastError());
+
+  VCounters hc_ctr{};
+  DHIP(hipMemcpy(&hc_ctr, ctr_buf.p, sizeof(VCounters), hipMemcpyDeviceToHost));
+  DanceKernelProfile p{};
+  p.iterations = kIters;
+  p.vector_bytes = rows.vbytes();
+  p.medoid_ms = elapsed_ms(e0, e_med);
+  p.init_ms = elapsed_ms(e_med, e_init);
+  for (uint32_t it = 0; it < kIters; ++it) {
+    p.search_ms += elapsed_ms(iev[it].s0, iev[it].s1);
+    p.reverse_ms += elapsed_ms(iev[it].s1, iev[it].r1);
+    p.merge_ms += elapsed_ms(iev[it].r1, iev[it].m1);
+    p.prune_ms += elapsed_ms(iev[it].m1, iev[it].p1);
+  }
+  p.total_ms = elapsed_ms(e0, iev[kIters - 1].p1);
+  p.search_dist = hc_ctr.search_dist;
+  p.insert_dist = hc_ctr.insert_dist;
+  p.expansions = hc_ctr.expansions;
+  p.vis_skips = hc_ctr.vis_skips;
+  p.merge_dist = hc_ctr.merge_dist;
+  p.prune_dist = hc_ctr.prune_dist;
+  p.reverse_edges = hc_ctr.reverse_edges;
+  p.touched_rows = hc_ctr.touched_rows;
+  const double V = rows.vbytes();
+  p.search_bytes = (double)(p.search_dist + p.insert_dist) * V + (double)p.expansions * (4.0 * R + 4.0) +
+                   (double)kIters * N * (V + 4.0 * R + 4.0 + 16.0 * C);
+  p.merge_bytes = (double)p.merge_dist * V + (double)p.reverse_edges * 4.0 +
+                  (double)p.touched_rows * (V + 16.0 * C + 8.0);
+  p.prune_bytes = (double)p.prune_dist * V + (double)kIters * N * (24.0 * C);
+  const double items = (double)N * R;
+  const double passes = (bit_length(N) + 7) / 8;
+  p.reverse_bytes = (double)kIters * (items * 12.0 + passes * items * 20.0);
+  if (kp) *kp = p;
+  if (stats) {
+    stats->search_online_insert_seconds = p.search_ms * 1e-3;
+    stats->reverse_seconds = (p.reverse_ms + p.merge_ms) * 1e-3;
+    stats->reverse_csr_seconds = p.reverse_ms * 1e-3;
+    stats->final_prune_seconds = p.prune_ms * 1e-3;
+    stats->distance_computations = p.search_dist + p.insert_dist + p.merge_dist + p.prune_dist;
+    stats->online_insert_attempts = hc_ctr.insert_try;
+    stats->online_insert_mutations = hc_ctr.insert_mut;
+    stats->reverse_proposals = p.reverse_edges;
+    stats->reverse_touched_rows = p.touched_rows;
+  }
+  if (medoid_out) *medoid_out = start;
+  if (verbose())
+    std::printf("[gpu_vamana_build] N=%u dim=%u R=%u L=%u C=%u STEPS=%u profile=%s medoid=%u total=%.3f ms\n", N,
+                rows.dim, R, L, C, STEPS, prof.name, start, p.total_ms);
+  return 0;
+}
+
+template <typename HostT>
+static int build_host(const HostT* h_data, int src_dtype, uint32_t N, uint32_t dim, uint32_t R, uint32_t L,
+                      uint32_t C, uint32_t STEPS, uint32_t* h_graph, uint32_t* h_degree, void** keep_data,
+                      uint32_t** keep_graph, uint32_t** keep_degree) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_last_stats = GPUVamanaStats{};
+  const double t0 = now_sec();
+  const bool handoff = keep_data != nullptr;
+  if (h_data == nullptr || (!handoff && (h_graph == nullptr || h_degree == nullptr))) {
+    std::fprintf(stderr, "[gpu_vamana_build] null input pointer.\n");
+    return -1;
+  }
+  DCHECK(validate(N, dim, R, L, C, STEPS));
+  const Profile prof = kProfiles[profile_index_locked()];
+  const int store = (src_dtype == DANCE_F32 && prof.fp16) ? DANCE_F16 : src_dtype;
+  hipStream_t s = nullptr;
+  DHIP(hipStreamCreate(&s));
+  struct StreamGuard {
+    hipStream_t s;
+    ~StreamGuard() {
+      if (s) (void)hipStreamDestroy(s);
+    }
+  } sg{s};
+  GPUVamanaStats stats{};
+  const double th = now_sec();
+  Rows rows;
+  DevBuf handoff_data;
+  if (handoff) {
+    // The hand-off returns the caller-typed vectors (N x dim) in device memory.
+    DCHECK(handoff_data.alloc((size_t)N * dim * sizeof(HostT)));
+    DHIP(hipMemcpyAsync(handoff_data.p, h_data, (size_t)N * dim * sizeof(HostT), hipMemcpyHostToDevice, s));
+    DCHECK(setup_rows(rows, handoff_data.p, true, src_dtype, store, N, dim, s));
+  } else {
+    DCHECK(setup_rows(rows, h_data, false, src_dtype, store, N, dim, s));
+  }
+  DHIP(hipStreamSynchronize(s));
+  stats.h2d_seconds = now_sec() - th;
+  State st;
+  uint32_t medoid = 0;
+  DanceKernelProfile kp{};
+  DCHECK(run_build(rows, R, L, C, STEPS, prof, st, s, &stats, &kp, &medoid));
+  const double td = now_sec();
+  if (handoff) {
+    *keep_data = handoff_data.release();
+    *keep_graph = st.cur.as<uint32_t>();
+    st.cur.release();
+    *keep_degree = st.deg_cur.as<uint32_t>();
+    st.deg_cur.release();
+  } else {
+    DHIP(hipMemcpy(h_graph, st.cur.p, (size_t)N * R * 4, hipMemcpyDeviceToHost));
+    DHIP(hipMemcpy(h_degree, st.deg_cur.p, (size_t)N * 4, hipMemcpyDeviceToHost));
+  }
+  stats.d2h_seconds = now_sec() - td;
+  stats.gpu_build_seconds = now_sec() - t0;
+  g_last_stats = stats;
+  g_last_medoid = medoid;
+  g_last_prof = kp;
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Stage hooks: upload host state, run one production kernel, download.
+// ---------------------------------------------------------------------------
+struct StageCtx {
+  hipStream_t s = nullptr;
+  Rows rows;
+  State st;
+  ~StageCtx() {
+    if (s) (void)hipStreamDestroy(s);
+  }
+  int open(const void* h_data, int dtype, uint32_t N, uint32_t dim) {
+    DHIP(hipStreamCreate(&s));
+    return setup_rows(rows, h_data, false, dtype, dtype, N, dim, s);
+  }
+};
+
+static int up(void* d, const void* h, size_t b, hipStream_t s) {
+  if (b) DHIP(hipMemcpyAsync(d, h, b, hipMemcpyHostToDevice, s));
+  return 0;
+}
+static int down(void* h, const void* d, size_t b, hipStream_t s) {
+  if (b) DHIP(hipMemcpyAsync(h, d, b, hipMemcpyDeviceToHost, s));
+  return 0;
+}
+
+static int upload_state(State& st, uint32_t N, uint32_t R, uint32_t C, const uint32_t* cur, const uint32_t* deg_cur,
+                        const uint32_t* work, const uint32_t* deg_work, const float* wd, hipStream_t s) {
+  DCHECK(st.alloc(N, R, C));
+  if (cur) DCHECK(up(st.cur.p, cur, (size_t)N * R * 4, s));
+  if (deg_cur) DCHECK(up(st.deg_cur.p, deg_cur, (size_t)N * 4, s));
+  DCHECK(up(st.work.p, work, (size_t)N * C * 4, s));
+  DCHECK(up(st.deg_work.p, deg_work, (size_t)N * 4, s));
+  DCHECK(up(st.wd.p, wd, (size_t)N * C * 4, s));
+  return 0;
+}
+
+static int download_state(State& st, uint32_t* cur, uint32_t* deg_cur, uint32_t* work, uint32_t* deg_work, float* wd,
+                          hipStream_t s) {
+  const size_t N = st.N, R = st.R, C = st.C;
+  if (cur) DCHECK(down(cur, st.cur.p, N * R * 4, s));
+  if (deg_cur) DCHECK(down(deg_cur, st.deg_cur.p, N * 4, s));
+  if (work) DCHECK(down(work, st.work.p, N * C * 4, s));
+  if (deg_work) DCHECK(down(deg_work, st.deg_work.p, N * 4, s));
+  if (wd) DCHECK(down(wd, st.wd.p, N * C * 4, s));
+  DHIP(hipStreamSynchronize(s));
+  return 0;
+}
+
+// Pairwise canonical distances: one wave per 64 pairs through batch_dist.
+template <int DT, int CPL>
+__global__ __launch_bounds__(kBlock) void k_pair_dist(RowSet rs, const uint32_t* __restrict__ a,
+                                                      const uint32_t* __restrict__ b, uint64_t n,
+                                                      float* __restrict__ out) {
+  const uint32_t w = threadIdx.x >> 6;
+  const uint64_t base = ((uint64_t)blockIdx.x * kWavesPerBlock + w) * 64;
+  if (base >= n) return;
+  const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;
+  for (uint32_t p = 0; p < 64; p += 8) {
+    const uint64_t k = base + p + grp;
+    const bool act = k < n;
+    uint4 va[CPL], vb[CPL];
+    load_row<CPL>(rs, act ? a[k] : 0u, act, sub, va);
+    load_row<CPL>(rs, act ? b[k] : 0u, act, sub, vb);
+    const float d = octet_finish<DT, CPL>(va, vb);
+    if (act && sub == 0) out[k] = d;
+  }
+}
+
+}  // namespace dance
+
+using namespace dance;
+
+// ===========================================================================
+// Reference ABI
+// ===========================================================================
+extern "C" {
+
+int gpu_vamana_vnew2_build(const uint8_t* h_data, uint32_t N, uint32_t dim, uint32_t R, uint32_t L, uint32_t C,
+                           uint32_t STEPS, uint32_t* h_graph, uint32_t* h_degree) {
+  return build_host<uint8_t>(h_data, DANCE_U8, N, dim, R, L, C, STEPS, h_graph, h_degree, nullptr, nullptr, nullptr);
+}
+
+int gpu_vamana_vnew2_build_float(const float* h_data, uint32_t N, uint32_t dim, uint32_t R, uint32_t L, uint32_t C,
+                                 uint32_t STEPS, uint32_t* h_graph, uint32_t* h_degree) {
+  return build_host<float>(h_data, DANCE_F32, N, dim, R, L, C, STEPS, h_graph, h_degree, nullptr, nullptr, nullptr);
+}
+
+int gpu_vamana_build(const uint8_t* h_data, uint32_t N, uint32_t dim, uint32_t R, uint32_t L, uint32_t C,
+                     uint32_t STEPS, uint32_t* h_graph, uint32_t* h_degree) {
+  return gpu_vamana_vnew2_build(h_data, N, dim, R, L, C, STEPS, h_graph, h_degree);
+}
+
+int gpu_vamana_build_float(const float* h_data, uint32_t N, uint32_t dim, uint32_t R, uint32_t L, uint32_t C,
+                           uint32_t STEPS, uint32_t* h_graph, uint32_t* h_degree) {
+  return gpu_vamana_vnew2_build_float(h_data, N, dim, R, L, C, STEPS, h_graph, h_degree);
+}
+
+int gpu_vamana_vnew2_build_device(const uint8_t* h_data, uint32_t N, uint32_t dim, uint32_t R, uint32_t L, uint32_t C,
+                                  uint32_t STEPS, uint8_t** d_data, uint32_t** d_graph, uint32_t** d_degree) {
+  if (d_data == nullptr || d_graph == nullptr || d_degree == nullptr) {
+    std::fprintf(stderr, "[gpu_vamana_build] null output pointer.\n");
+    return -1;
+  }
+  void* dd = nullptr;
+  int r = build_host<uint8_t>(h_data, DANCE_U8, N, dim, R, L, C, STEPS, nullptr, nullptr, &dd, d_graph, d_degree);
+  if (r == 0) *d_data = static_cast<uint8_t*>(dd);
+  return r;
+}
+
+int gpu_vamana_vnew2_build_device_float(const float* h_data, uint32_t N, uint32_t dim, uint32_t R, uint32_t L,
+                                        uint32_t C, uint32_t STEPS, float** d_data, uint32_t** d_graph,
+                                        uint32_t** d_degree) {
+  if (d_data == nullptr || d_graph == nullptr || d_degree == nullptr) {
+    std::fprintf(stderr, "[gpu_vamana_build] null output pointer.\n");
+    return -1;
+  }
+  void* dd = nullptr;
+  int r = build_host<float>(h_data, DANCE_F32, N, dim, R, L, C, STEPS, nullptr, nullptr, &dd, d_graph, d_degree);
+  if (r == 0) *d_data = static_cast<float*>(dd);
+  return r;
+}
+
+uint32_t gpu_vamana_vnew2_get_last_medoid(void) { return g_last_medoid; }
+void gpu_vamana_vnew2_get_last_stats(GPUVamanaStats* stats) {
+  if (stats) *stats = g_last_stats;
+}
+uint32_t gpu_vamana_get_last_medoid(void) { return g_last_medoid; }
+void gpu_vamana_get_last_stats(GPUVamanaStats* stats) {
+  if (stats) *stats = g_last_stats;
+}
+
+// ===========================================================================
+// Extensions (include/dance_hip.h)
+// ===========================================================================
+int dance_vamana_build_resident(const void* d_data, int dtype, uint32_t N, uint32_t dim, uint32_t R, uint32_t L,
+                                uint32_t C, uint32_t STEPS, uint32_t* d_graph, uint32_t* d_degree) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (d_data == nullptr || d_graph == nullptr || d_degree == nullptr) {
+    std::fprintf(stderr, "[gpu_vamana_build] null input pointer.\n");
+    return -1;
+  }
+  if (dtype != DANCE_F32 && dtype != DANCE_U8 && dtype != DANCE_F16) {
+    std::fprintf(stderr, "[gpu_vamana_build] unsupported dtype %d\n", dtype);
+    return -1;
+  }
+  DCHECK(validate(N, dim, R, L, C, STEPS));
+  const double t0 = now_sec();
+  const Profile prof = kProfiles[profile_index_locked()];
+  const int store = (dtype == DANCE_F32 && prof.fp16) ? DANCE_F16 : dtype;
+  hipStream_t s = nullptr;
+  DHIP(hipStreamCreate(&s));
+  struct StreamGuard {
+    hipStream_t s;
+    ~StreamGuard() {
+      if (s) (void)hipStreamDestroy(s);
+    }
+  } sg{s};
+  Rows rows;
+  DCHECK(setup_rows(rows, d_data, true, dtype, store, N, dim, s));
+  State st;
+  // The caller's graph/degree buffers are the build's current graph.
+  st.cur.p = d_graph;
+  GPUVamanaStats stats{};
+  DanceKernelProfile kp{};
+  uint32_t medoid = 0;
+  int r = run_build(rows, R, L, C, STEPS, prof, st, s, &stats, &kp, &medoid);
+  st.cur.release();
+  if (r != 0) return r;
+  DHIP(hipMemcpyAsync(d_degree, st.deg_cur.p, (size_t)N * 4, hipMemcpyDeviceToDevice, s));
+  DHIP(hipStreamSynchronize(s));
+  stats.gpu_build_seconds = now_sec() - t0;
+  g_last_stats = stats;
+  g_last_medoid = medoid;
+  g_last_prof = kp;
+  return 0;
+}
+
+void dance_get_last_kernel_profile(DanceKernelProfile* p) {
+  if (p) *p = g_last_prof;
+}
+
+int dance_set_profile(const char* name) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (name == nullptr) return -1;
+  for (int i = 0; i < 4; ++i)
+    if (std::strcmp(name, kProfiles[i].name) == 0) {
+      g_profile = i;
+      return 0;
+    }
+  std::fprintf(stderr, "[dance_hip] unknown profile '%s'\n", name);
+  return -1;
+}
+
+const char* dance_get_profile(void) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return kProfiles[profile_index_locked()].name;
+}
+
+int dance_stage_distances(const void* h_data, int dtype, uint32_t N, uint32_t dim, const uint32_t* a,
+                          const uint32_t* b, uint64_t n, float* out) {
+  if (!h_data || !a || !b || !out || N == 0 || dim == 0) return -1;
+  for (uint64_t i = 0; i < n; ++i)
+    if (a[i] >= N || b[i] >= N) {
+      std::fprintf(stderr, "[dance_hip] distance index out of range\n");
+      return -1;
+    }
+  StageCtx cx;
+  DCHECK(cx.open(h_data, dtype, N, dim));
+  DevBuf da, db, dout;
+  DCHECK(da.alloc(std::max<uint64_t>(n, 1) * 4));
+  DCHECK(db.alloc(std::max<uint64_t>(n, 1) * 4));
+  DCHECK(dout.alloc(std::max<uint64_t>(n, 1) * 4));
+  DCHECK(up(da.p, a, n * 4, cx.s));
+  DCHECK(up(db.p, b, n * 4, cx.s));
+  const int cpl = pick_cpl(cx.rows.rs.nch);
+  const uint64_t waves = (n + 63) / 64;
+  DCHECK(with_dt_cpl(dtype, cpl, [&](auto dt, auto c) {
+    if (waves == 0) return 0;
+    hipLaunchKernelGGL((k_pair_dist<decltype(dt)::value, decltype(c)::value>),
+                       dim3((uint32_t)((waves + kWavesPerBlock - 1) / kWavesPerBlock)), dim3(kBlock), 0, cx.s,
+                       cx.rows.rs, da.as<uint32_t>(), db.as<uint32_t>(), n, dout.as<float>());
+    DHIP(hipGetLastError());
+    return 0;
+  }));
+  DCHECK(down(out, dout.p, n * 4, cx.s));
+  DHIP(hipStreamSynchronize(cx.s));
+  return 0;
+}
+
+int dance_stage_medoid(const void* h_data, int dtype, uint32_t N, uint32_t dim, float* scores, uint32_t* cands,
+                       uint32_t* medoid) {
+  if (!h_data || N == 0 || dim == 0) return -1;
+  StageCtx cx;
+  DCHECK(cx.open(h_data, dtype, N, dim));
+  const uint32_t nc = std::min(kMedoidCandidates, N), ns = std::min(kMedoidSamples, N);
+  DevBuf sc, ca;
+  DCHECK(sc.alloc(nc * 4));
+  DCHECK(ca.alloc(nc * 4));
+  DCHECK(launch_medoid(cx.rows, cx.s, sc.as<float>(), ca.as<uint32_t>(), nc, ns));
+  std::vector<float> hs(nc);
+  std::vector<uint32_t> hc(nc);
+  DCHECK(down(hs.data(), sc.p, nc * 4, cx.s));
+  DCHECK(down(hc.data(), ca.p, nc * 4, cx.s));
+  DHIP(hipStreamSynchronize(cx.s));
+  uint32_t best = DANCE_INV;
+  float bs = FLT_MAX;
+  for (uint32_t i = 0; i < nc; ++i)
+    if (hs[i] < bs) {
+      bs = hs[i];
+      best = i;
+    }
+  if (scores) std::memcpy(scores, hs.data(), nc * 4);
+  if (cands) std::memcpy(cands, hc.data(), nc * 4);
+  if (medoid) *medoid = best == DANCE_INV ? 0u : hc[best];
+  return 0;
+}
+
+int dance_stage_init(const void* h_data, int dtype, uint32_t N, uint32_t dim, uint32_t R, uint32_t C, uint32_t* cur,
+                     uint32_t* deg_cur, uint32_t* work, uint32_t* deg_work, float* wd) {
+  if (!h_data || !cur || !deg_cur || !work || !deg_work || !wd || N == 0 || R == 0 || C < R) return -1;
+  StageCtx cx;
+  DCHECK(cx.open(h_data, dtype, N, dim));
+  DCHECK(cx.st.alloc(N, R, C));
+  DCHECK(launch_init(cx.rows, cx.st.g(), cx.s));
+  return download_state(cx.st, cur, deg_cur, work, deg_work, wd, cx.s);
+}
+
+int dance_stage_search(const void* h_data, int dtype, uint32_t N, uint32_t dim, uint32_t R, uint32_t L, uint32_t C,
+                       uint32_t steps, float alpha, uint32_t start, uint32_t* cur, uint32_t* deg_cur, uint32_t* work,
+                       uint32_t* deg_work, float* wd) {
+  if (!h_data || !cur || !deg_cur || !work || !deg_work || !wd || N == 0 || R == 0 || C < R || L == 0 || L > 256)
+    return -1;
+  StageCtx cx;
+  DCHECK(cx.open(h_data, dtype, N, dim));
+  DCHECK(upload_state(cx.st, N, R, C, cur, deg_cur, work, deg_work, wd, cx.s));
+  DCHECK(launch_search(cx.rows, cx.st.g(), L, steps, alpha, start, nullptr, cx.s));
+  return download_state(cx.st, cur, deg_cur, work, deg_work, wd, cx.s);
+}
+
+int dance_stage_reverse_merge(const void* h_data, int dtype, uint32_t N, uint32_t dim, uint32_t R, uint32_t C,
+                              uint32_t* work, uint32_t* deg_work, float* wd, uint32_t heavy_threshold,
+                              uint32_t heavy_sample, uint32_t* offsets, uint32_t* ids) {
+  if (!h_data || !work || !deg_work || !wd || N == 0 || R == 0 || C < R) return -1;
+  StageCtx cx;
+  DCHECK(cx.open(h_data, dtype, N, dim));
+  DCHECK(upload_state(cx.st, N, R, C, nullptr, nullptr, work, deg_work, wd, cx.s));
+  ReverseWs rws;
+  DCHECK(rws.alloc(N, R));
+  const uint32_t* srcs = nullptr;
+  GraphBufs g = cx.st.g();
+  DCHECK(build_reverse_csr(g, rws, cx.s, &srcs));
+  std::vector<uint32_t> off((size_t)N + 1);
+  DCHECK(down(off.data(), rws.offs.p, ((size_t)N + 1) * 4, cx.s));
+  DHIP(hipStreamSynchronize(cx.s));
+  if (offsets) std::memcpy(offsets, off.data(), off.size() * 4);
+  if (ids) DCHECK(down(ids, srcs, (size_t)off[N] * 4, cx.s));
+  Profile prof{"stage", false, heavy_threshold, heavy_sample};
+  DCHECK(launch_merge(cx.rows, g, rws.offs.as<uint32_t>(), srcs, prof, nullptr, cx.s));
+  return download_state(cx.st, nullptr, nullptr, work, deg_work, wd, cx.s);
+}
+
+int dance_stage_prune(const void* h_data, int dtype, uint32_t N, uint32_t dim, uint32_t R, uint32_t C,
+                      uint32_t min_degree, float alpha, uint32_t* work, uint32_t* deg_work, float* wd, uint32_t* cur,
+                      uint32_t* deg_cur) {
+  if (!h_data || !work || !deg_work || !wd || !cur || !deg_cur || N == 0 || R == 0 || C < R) return -1;
+  StageCtx cx;
+  DCHECK(cx.open(h_data, dtype, N, dim));
+  DCHECK(upload_state(cx.st, N, R, C, nullptr, nullptr, work, deg_work, wd, cx.s));
+  DCHECK(launch_prune(cx.rows, cx.st.g(), min_degree, alpha, nullptr, cx.s));
+  return download_state(cx.st, cur, deg_cur, work, deg_work, wd, cx.s);
+}
+
+int dance_stage_sort_pairs(const uint32_t* keys, const uint32_t* vals, uint64_t n, uint32_t key_bits,
+                           uint32_t* out_keys, uint32_t* out_vals) {
+  if (!keys || !vals || !out_keys || !out_vals || key_bits > 32) return -1;
+  hipStream_t s = nullptr;
+  DHIP(hipStreamCreate(&s));
+  struct G {
+    hipStream_t s;
+    ~G() { (void)hipStreamDestroy(s); }
+  } gd{s};
+  DevBuf k[2], v[2];
+  for (int i = 0; i < 2; ++i) {
+    DCHECK(k[i].alloc(std::max<uint64_t>(n, 1) * 4));
+    DCHECK(v[i].alloc(std::max<uint64_t>(n, 1) * 4));
+  }
+  DCHECK(up(k[0].p, keys, n * 4, s));
+  DCHECK(up(v[0].p, vals, n * 4, s));
+  uint32_t* kb[2] = {k[0].as<uint32_t>(), k[1].as<uint32_t>()};
+  uint32_t* vb[2] = {v[0].as<uint32_t>(), v[1].as<uint32_t>()};
+  SortWorkspace ws;
+  int which = 0;
+  DCHECK(radix_sort_pairs(kb, vb, n, key_bits, ws, s, &which));
+  DCHECK(down(out_keys, kb[which], n * 4, s));
+  DCHECK(down(out_vals, vb[which], n * 4, s));
+  DHIP(hipStreamSynchronize(s));
+  return 0;
+}
+
+int dance_stage_scan(const uint32_t* in, uint64_t n, uint32_t* out) {
+  if (!in || !out) return -1;
+  hipStream_t s = nullptr;
+  DHIP(hipStreamCreate(&s));
+  struct G {
+    hipStream_t s;
+    ~G() { (void)hipStreamDestroy(s); }
+  } gd{s};
+  DevBuf d;
+  DCHECK(d.alloc(std::max<uint64_t>(n, 1) * 4));
+  DCHECK(up(d.p, in, n * 4, s));
+  ScanWorkspace ws;
+  DCHECK(scan_exclusive(d.as<uint32_t>(), n, ws, s));
+  DCHECK(down(out, d.p, n * 4, s));
+  DHIP(hipStreamSynchronize(s));
+  return 0;
+}
+
+}  // extern "C"

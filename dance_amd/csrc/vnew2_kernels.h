@@ -1,0 +1,896 @@
+// Device kernels of the standard GPU Vamana build, written for gfx950.
+//
+// One wave64 owns one vertex. Per-vertex state lives where CDNA4 keeps it
+// cheapest: the top-L candidate pool in VGPRs (PS slots per lane, slot
+// s = r*64 + lane), the C-wide work row and scratch lists in LDS, a forgetful
+// visited cache in LDS that skips distance gathers for ids already handled in
+// this search, and the vertex's own vector in VGPRs. Distances are gathered by
+// octets (see wave.h), 16 pairs in flight per wave.
+//
+// Semantics follow /root/reference/src/gpu_vamana_vnew2.cu exactly; each
+// kernel cites the reference kernel it replaces. The visited cache never
+// changes a result: re-inserting an id the pool has already handled is a no-op
+// in the reference's pool (the pool maximum never rises once the pool is full,
+// and distances are a deterministic function of the id).
+#pragma once
+
+#include "wave.h"
+
+namespace dance {
+
+constexpr uint32_t kVisBits = 10;
+constexpr uint32_t kVis = 1u << kVisBits;  // visited cache slots per wave
+constexpr uint32_t kWavesPerBlock = 4;
+constexpr uint32_t kBlock = 64 * kWavesPerBlock;
+
+struct VCounters {
+  unsigned long long search_dist;   // distances computed for pool candidates
+  unsigned long long insert_dist;   // distances computed by the online insert
+  unsigned long long expansions;    // expanded pool entries
+  unsigned long long vis_skips;     // candidates skipped by the visited cache
+  unsigned long long insert_mut;    // online-insert mutations of the work row
+  unsigned long long insert_try;    // online-insert attempts
+  unsigned long long merge_dist;    // reverse-merge distances
+  unsigned long long prune_dist;    // prune pair distances
+  unsigned long long reverse_edges; // reverse proposals
+  unsigned long long touched_rows;  // targets with at least one reverse edge
+  unsigned long long pad[6];
+};
+
+struct GraphBufs {
+  uint32_t N, R, C;
+  uint32_t* cur;       // N x R
+  uint32_t* deg_cur;   // N
+  uint32_t* work;      // N x C
+  uint32_t* deg_work;  // N
+  float* wd;           // N x C
+};
+
+__device__ __forceinline__ bool valid_for(uint32_t id, uint32_t N, uint32_t node) {
+  return id != DANCE_INV && id < N && id != node;
+}
+
+// Distances from a cached vector `av` to up to 64 ids lst[0..n) -> lsd[0..n).
+// Two passes of 8 octets are kept in flight. Returns after lsd is visible.
+template <int DT, int CPL>
+__device__ __forceinline__ void batch_dist(const RowSet& rs, const uint4 (&av)[CPL], const uint32_t* lst,
+                                           float* lsd, uint32_t n, uint32_t grp, uint32_t sub) {
+  for (uint32_t p = 0; p < n; p += 16) {
+    const uint32_t k0 = p + grp, k1 = p + 8 + grp;
+    const bool a0 = k0 < n, a1 = k1 < n;
+    const uint32_t id0 = a0 ? lst[k0] : 0u, id1 = a1 ? lst[k1] : 0u;
+    uint4 b0[CPL], b1[CPL];
+    load_row<CPL>(rs, id0, a0, sub, b0);
+    load_row<CPL>(rs, id1, a1, sub, b1);
+    const float d0 = octet_finish<DT, CPL>(av, b0);
+    const float d1 = octet_finish<DT, CPL>(av, b1);
+    if (sub == 0) {
+      if (a0) lsd[k0] = d0;
+      if (a1) lsd[k1] = d1;
+    }
+  }
+  wave_sync();
+}
+
+// ---------------------------------------------------------------------------
+// Register-resident bounded top-L pool (vnew2.cu:520-734).
+// ---------------------------------------------------------------------------
+template <int PS>
+struct RegPool {
+  uint32_t id[PS];
+  float d[PS];
+  uint32_t expbits;  // bit r: slot r*64+lane expanded
+  uint32_t size;
+  int max_pos;
+  float max_d;
+  uint32_t L;
+
+  __device__ __forceinline__ void init(uint32_t L_) {
+#pragma unroll
+    for (int r = 0; r < PS; ++r) {
+      id[r] = DANCE_INV;
+      d[r] = FLT_MAX;
+    }
+    expbits = 0u;
+    size = 0u;
+    max_pos = -1;
+    max_d = -FLT_MAX;
+    L = L_;
+  }
+
+  __device__ __forceinline__ uint32_t get_id(int pos) const {
+    uint32_t v = DANCE_INV;
+#pragma unroll
+    for (int r = 0; r < PS; ++r)
+      if (r == (pos >> 6)) v = id[r];
+    return rdlane_u(v, pos & 63);
+  }
+  __device__ __forceinline__ float get_d(int pos) const {
+    float v = FLT_MAX;
+#pragma unroll
+    for (int r = 0; r < PS; ++r)
+      if (r == (pos >> 6)) v = d[r];
+    return rdlane_f(v, pos & 63);
+  }
+  __device__ __forceinline__ void set_slot(int pos, uint32_t nid, float nd, uint32_t lane) {
+    if ((int)lane == (pos & 63)) {
+#pragma unroll
+      for (int r = 0; r < PS; ++r)
+        if (r == (pos >> 6)) {
+          id[r] = nid;
+          d[r] = nd;
+        }
+      expbits &= ~(1u << (pos >> 6));
+    }
+  }
+  __device__ __forceinline__ void set_d(int pos, float nd, uint32_t lane) {
+    if ((int)lane == (pos & 63)) {
+#pragma unroll
+      for (int r = 0; r < PS; ++r)
+        if (r == (pos >> 6)) d[r] = nd;
+      expbits &= ~(1u << (pos >> 6));
+    }
+  }
+  __device__ __forceinline__ void set_expanded(int pos, uint32_t lane) {
+    if ((int)lane == (pos & 63)) expbits |= 1u << (pos >> 6);
+  }
+
+  // recompute_max_pos_size_warp: largest distance, lowest slot on ties.
+  __device__ __forceinline__ void recompute_max() {
+    int best = INT_MIN;
+#pragma unroll
+    for (int r = 0; r < PS; ++r) {
+      const bool v = id[r] != DANCE_INV && d[r] == d[r];
+      best = max(best, v ? fkey(d[r]) : INT_MIN);
+    }
+    const int M = wave_max_i(best);
+    if (M == INT_MIN) {
+      max_pos = -1;
+      max_d = -FLT_MAX;
+      return;
+    }
+    int pos = -1;
+#pragma unroll
+    for (int r = 0; r < PS; ++r) {
+      if (pos < 0) {
+        const uint64_t m = wballot(id[r] != DANCE_INV && d[r] == d[r] && fkey(d[r]) == M);
+        if (m) pos = r * 64 + ffs64(m);
+      }
+    }
+    max_pos = pos;
+    max_d = __int_as_float(M);
+  }
+
+  // insert_top_l_state_warp with ENABLE_TOPL_EARLY_REJECT=1. `nid`/`nd` are uniform.
+  __device__ __forceinline__ void insert(uint32_t nid, float nd, uint32_t lane) {
+    if (nid == DANCE_INV) return;
+    if (size >= L && max_pos >= 0 && nd >= max_d) return;
+    int same = -1;
+#pragma unroll
+    for (int r = 0; r < PS; ++r) {
+      if (same < 0) {
+        const uint64_t m = wballot(id[r] == nid);
+        if (m) same = r * 64 + ffs64(m);
+      }
+    }
+    if (same >= 0) {
+      const float cd = get_d(same);
+      if (nd < cd) {
+        set_d(same, nd, lane);
+        if (same == max_pos) recompute_max();
+      }
+      return;
+    }
+    if (size < L) {
+      const int pos = (int)size;
+      set_slot(pos, nid, nd, lane);
+      size++;
+      if (max_pos < 0 || nd > max_d) {
+        max_pos = pos;
+        max_d = nd;
+      }
+      return;
+    }
+    if (max_pos >= 0 && nd < max_d) {
+      set_slot(max_pos, nid, nd, lane);
+      recompute_max();
+    }
+  }
+
+  // select_next_unexpanded_size_warp: smallest distance among unexpanded
+  // entries with distance < FLT_MAX, lowest slot on ties; -1 if none.
+  __device__ __forceinline__ int select() const {
+    int best = INT_MAX;
+#pragma unroll
+    for (int r = 0; r < PS; ++r) {
+      const bool c = id[r] != DANCE_INV && ((expbits >> r) & 1u) == 0u && d[r] < FLT_MAX;
+      best = min(best, c ? fkey(d[r]) : INT_MAX);
+    }
+    const int M = wave_min_i(best);
+    if (M == INT_MAX) return -1;
+    int pos = -1;
+#pragma unroll
+    for (int r = 0; r < PS; ++r) {
+      if (pos < 0) {
+        const bool c = id[r] != DANCE_INV && ((expbits >> r) & 1u) == 0u && d[r] < FLT_MAX;
+        const uint64_t m = wballot(c && fkey(d[r]) == M);
+        if (m) pos = r * 64 + ffs64(m);
+      }
+    }
+    return pos;
+  }
+};
+
+__device__ __forceinline__ uint32_t vis_slot(uint32_t id) { return (id * 0x9E3779B1u) >> (32 - kVisBits); }
+
+struct SearchArgs {
+  RowSet rs;
+  GraphBufs g;
+  uint32_t L, steps, start;
+  float alpha;
+  const uint32_t* order;  // optional processing order (vertex = order[wave])
+  VCounters* ctr;
+};
+
+// Per-wave LDS words of the search kernel.
+__host__ __device__ constexpr uint32_t search_lds_words(uint32_t Cp) { return kVis + 4u * Cp + 128u; }
+
+template <int DT, int CPL, int PS>
+struct SearchWave {
+  const SearchArgs& a;
+  uint32_t node, lane, grp, sub, Cp;
+  uint32_t *vis, *wid, *lst, *lsa, *lsb;
+  float *wdd, *lsd;
+  uint4 av[CPL];
+  RegPool<PS> P;
+  uint32_t wdeg;
+  uint32_t n_search, n_insert, n_skip, n_mut, n_try;
+
+  __device__ SearchWave(const SearchArgs& args, uint32_t node_, uint32_t* base, uint32_t Cp_)
+      : a(args), node(node_), Cp(Cp_) {
+    lane = lane_id();
+    grp = lane >> 3;
+    sub = lane & 7u;
+    vis = base;
+    wid = vis + kVis;
+    wdd = reinterpret_cast<float*>(wid + Cp);
+    lst = reinterpret_cast<uint32_t*>(wdd + Cp);
+    lsd = reinterpret_cast<float*>(lst + 64);
+    lsa = reinterpret_cast<uint32_t*>(lsd + 64);
+    lsb = lsa + Cp;
+    n_search = n_insert = n_skip = n_mut = n_try = 0;
+  }
+
+  // Handles one batch of <= 64 candidates given in insertion order (one per
+  // lane; DANCE_INV = none): visited filter, distances, ordered inserts.
+  __device__ __forceinline__ void process_batch(uint32_t c) {
+    const uint32_t N = a.g.N;
+    const bool v = valid_for(c, N, node);
+    const uint32_t slot = vis_slot(c);
+    const bool seen = v && vis[slot] == c;
+    const bool need = v && !seen;
+    const uint64_t m = wballot(need);
+    const uint32_t n = popc64(m);
+    n_skip += popc64(wballot(seen));
+    if (n == 0) return;
+    if (need) lst[mbcnt64(m)] = c;
+    wave_sync();
+    batch_dist<DT, CPL>(a.rs, av, lst, lsd, n, grp, sub);
+    n_search += n;
+    const uint32_t ck = lane < n ? lst[lane] : DANCE_INV;
+    const float dk = lane < n ? lsd[lane] : FLT_MAX;
+    bool keep = lane < n;
+    if (P.size >= P.L && P.max_pos >= 0) keep = keep && dk < P.max_d;
+    uint64_t km = wballot(keep);
+    while (km) {
+      const int k = ffs64(km);
+      km &= km - 1;
+      P.insert(rdlane_u(ck, k), rdlane_f(dk, k), lane);
+    }
+    if (need) vis[slot] = c;
+    wave_sync();
+  }
+
+  // dynamic_robust_insert_C_warp (vnew2.cu:759-877) on the LDS work row.
+  __device__ __forceinline__ void robust_insert(uint32_t x, float dpx) {
+    const uint32_t N = a.g.N, C = a.g.C;
+    if (x == DANCE_INV || x >= N || x == node) return;
+    n_try++;
+    for (uint32_t b = 0; b < wdeg; b += 64) {
+      const uint32_t i = b + lane;
+      if (wballot(i < wdeg && wid[i] == x)) return;
+    }
+    uint4 xv[CPL];
+    load_row<CPL>(a.rs, x, true, sub, xv);
+    uint32_t nA = 0, nB = 0;
+    float wl = -FLT_MAX;
+    int wp = -1;
+    for (uint32_t b = 0; b < wdeg; b += 64) {
+      const uint32_t i = b + lane;
+      const bool in = i < wdeg;
+      const uint32_t y = in ? wid[i] : DANCE_INV;
+      const float dpy = in ? wdd[i] : 0.0f;
+      const bool v = in && valid_for(y, N, node);
+      const bool ca = v && dpy <= dpx;
+      const bool cb = v && dpy > dpx;
+      const uint64_t ma = wballot(ca), mb = wballot(cb);
+      if (ca) lsa[nA + mbcnt64(ma)] = i;
+      if (cb) lsb[nB + mbcnt64(mb)] = i;
+      nA += popc64(ma);
+      nB += popc64(mb);
+      if (v && dpy > wl) {
+        wl = dpy;
+        wp = (int)i;
+      }
+    }
+    wave_sync();
+    // Occlusion: exists y with d_py <= d_px and alpha * d(y, x) <= d_px.
+    bool occluded = false;
+    for (uint32_t p = 0; p < nA && !occluded; p += 16) {
+      const uint32_t k0 = p + grp, k1 = p + 8 + grp;
+      const bool a0 = k0 < nA, a1 = k1 < nA;
+      const uint32_t y0 = a0 ? wid[lsa[k0]] : 0u, y1 = a1 ? wid[lsa[k1]] : 0u;
+      uint4 b0[CPL], b1[CPL];
+      load_row<CPL>(a.rs, y0, a0, sub, b0);
+      load_row<CPL>(a.rs, y1, a1, sub, b1);
+      const float d0 = octet_finish<DT, CPL>(xv, b0);
+      const float d1 = octet_finish<DT, CPL>(xv, b1);
+      n_insert += min(16u, nA - p);
+      const bool o = sub == 0 && ((a0 && a.alpha * d0 <= dpx) || (a1 && a.alpha * d1 <= dpx));
+      occluded = wballot(o) != 0;
+    }
+    if (occluded) return;
+    // Worst valid entry (largest d_py, lowest slot).
+    const int WK = wave_max_i(wp >= 0 ? fkey(wl) : INT_MIN);
+    int wpos = -1;
+    float wdist = -FLT_MAX;
+    if (WK != INT_MIN) {
+      wpos = (int)wave_min_u((wp >= 0 && fkey(wl) == WK) ? (uint32_t)wp : 0xFFFFFFFFu);
+      wdist = __int_as_float(WK);
+    }
+    // Victim: largest d_py among y with d_py > d_px and alpha * d(x, y) <= d_py.
+    int vk = INT_MIN;
+    uint32_t vs = 0xFFFFFFFFu;
+    for (uint32_t p = 0; p < nB; p += 16) {
+      const uint32_t k0 = p + grp, k1 = p + 8 + grp;
+      const bool a0 = k0 < nB, a1 = k1 < nB;
+      const uint32_t s0 = a0 ? lsb[k0] : 0u, s1 = a1 ? lsb[k1] : 0u;
+      const uint32_t y0 = a0 ? wid[s0] : 0u, y1 = a1 ? wid[s1] : 0u;
+      uint4 b0[CPL], b1[CPL];
+      load_row<CPL>(a.rs, y0, a0, sub, b0);
+      load_row<CPL>(a.rs, y1, a1, sub, b1);
+      const float d0 = octet_finish<DT, CPL>(xv, b0);
+      const float d1 = octet_finish<DT, CPL>(xv, b1);
+      n_insert += min(16u, nB - p);
+      if (sub == 0) {
+        if (a0) {
+          const float dpy = wdd[s0];
+          if (a.alpha * d0 <= dpy && dpy == dpy) {
+            const int key = fkey(dpy);
+            if (key > vk || (key == vk && s0 < vs)) {
+              vk = key;
+              vs = s0;
+            }
+          }
+        }
+        if (a1) {
+          const float dpy = wdd[s1];
+          if (a.alpha * d1 <= dpy && dpy == dpy) {
+            const int key = fkey(dpy);
+            if (key > vk || (key == vk && s1 < vs)) {
+              vk = key;
+              vs = s1;
+            }
+          }
+        }
+      }
+    }
+    const int VK = wave_max_i(vk);
+    int vpos = -1;
+    if (VK != INT_MIN) vpos = (int)wave_min_u(vk == VK ? vs : 0xFFFFFFFFu);
+    if (vpos >= 0) {
+      if (lane == 0) {
+        wid[vpos] = x;
+        wdd[vpos] = dpx;
+      }
+      n_mut++;
+    } else if (wdeg < C) {
+      if (lane == 0) {
+        wid[wdeg] = x;
+        wdd[wdeg] = dpx;
+      }
+      wdeg++;
+      n_mut++;
+    } else if (wpos >= 0 && dpx < wdist) {
+      if (lane == 0) {
+        wid[wpos] = x;
+        wdd[wpos] = dpx;
+      }
+      n_mut++;
+    }
+    wave_sync();
+  }
+
+  __device__ void run() {
+    const GraphBufs& g = a.g;
+    const uint32_t N = g.N, R = g.R, C = g.C;
+    for (uint32_t i = lane; i < kVis; i += 64) vis[i] = DANCE_INV;
+    load_row<CPL>(a.rs, node, true, sub, av);
+    // Work row := current row with its stored distances (vnew2.cu:1186-1212).
+    const uint32_t deg_self = min(g.deg_cur[node], R);
+    const size_t cb = (size_t)node * R, wb = (size_t)node * C;
+    for (uint32_t i = lane; i < Cp; i += 64) {
+      uint32_t nb = DANCE_INV;
+      float dist = FLT_MAX;
+      if (i < deg_self) {
+        nb = g.cur[cb + i];
+        if (valid_for(nb, N, node))
+          dist = g.wd[wb + i];
+        else
+          nb = DANCE_INV;
+      }
+      wid[i] = nb;
+      wdd[i] = dist;
+    }
+    wdeg = deg_self;
+    P.init(a.L);
+    wave_sync();
+    // Entry point (vnew2.cu:1223-1244).
+    process_batch(lane == 0 && a.start < N && a.start != node ? a.start : DANCE_INV);
+    // Own neighbours with stored distances (vnew2.cu:1246-1278).
+    for (uint32_t b = 0; b < deg_self; b += 64) {
+      const uint32_t i = b + lane;
+      const uint32_t nb = i < deg_self ? wid[i] : DANCE_INV;
+      const float dd = i < deg_self ? wdd[i] : FLT_MAX;
+      const bool v = nb != DANCE_INV;
+      uint64_t m = wballot(v);
+      while (m) {
+        const int k = ffs64(m);
+        m &= m - 1;
+        P.insert(rdlane_u(nb, k), rdlane_f(dd, k), lane);
+      }
+      if (v) vis[vis_slot(nb)] = nb;
+      wave_sync();
+    }
+    // INIT_RANDOM_SEEDS hashed seeds (vnew2.cu:1280-1300).
+    process_batch(lane < 8 ? d_det_neighbor(node, lane + 1024u, N) : DANCE_INV);
+    const uint32_t max_steps = min(a.steps, a.L);
+    uint32_t n_exp = 0;
+    for (uint32_t step = 0; step < max_steps; ++step) {
+      const int pos = P.select();
+      if (pos < 0) break;
+      const uint32_t x = P.get_id(pos);
+      const float dx = P.get_d(pos);
+      P.set_expanded(pos, lane);
+      if (x == DANCE_INV || x >= N) break;
+      n_exp++;
+      // Issue the adjacency gather of x before the online insert.
+      const uint32_t degx = min(g.deg_cur[x], R);
+      const size_t xb = (size_t)x * R;
+      const uint32_t c0 = lane < degx ? g.cur[xb + lane] : DANCE_INV;
+      robust_insert(x, dx);
+      process_batch(c0);
+      for (uint32_t b = 64; b < degx; b += 64) {
+        const uint32_t pidx = b + lane;
+        process_batch(pidx < degx ? g.cur[xb + pidx] : DANCE_INV);
+      }
+    }
+    for (uint32_t i = lane; i < C; i += 64) {
+      g.work[wb + i] = wid[i];
+      g.wd[wb + i] = wdd[i];
+    }
+    if (lane == 0) g.deg_work[node] = wdeg;
+    if (a.ctr) {
+      const uint64_t m = wballot(true);
+      if (lane == (uint32_t)ffs64(m)) {
+        atomicAdd(&a.ctr->search_dist, (unsigned long long)n_search);
+        atomicAdd(&a.ctr->insert_dist, (unsigned long long)n_insert);
+        atomicAdd(&a.ctr->expansions, (unsigned long long)n_exp);
+        atomicAdd(&a.ctr->vis_skips, (unsigned long long)n_skip);
+        atomicAdd(&a.ctr->insert_mut, (unsigned long long)n_mut);
+        atomicAdd(&a.ctr->insert_try, (unsigned long long)n_try);
+      }
+    }
+  }
+};
+
+// search_prune_kernel_shared (vnew2.cu:1119-1439).
+template <int DT, int CPL, int PS>
+__global__ __launch_bounds__(kBlock) void k_search(SearchArgs a, uint32_t Cp) {
+  extern __shared__ uint32_t smem[];
+  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t gw = blockIdx.x * kWavesPerBlock + w;
+  if (gw >= a.g.N) return;
+  const uint32_t node = a.order ? a.order[gw] : gw;
+  SearchWave<DT, CPL, PS> sw(a, node, smem + w * search_lds_words(Cp), Cp);
+  sw.run();
+}
+
+// ---------------------------------------------------------------------------
+// RobustPrune with alpha and the last-iteration degree fill
+// (final_prune_kernel_shared, vnew2.cu:1893-2147).
+// ---------------------------------------------------------------------------
+struct PruneArgs {
+  RowSet rs;
+  GraphBufs g;
+  uint32_t min_degree;
+  float alpha;
+  const uint32_t* order;
+  VCounters* ctr;
+};
+
+__host__ __device__ constexpr uint32_t prune_lds_words(uint32_t Cp, uint32_t Rp) { return 4u * Cp + 2u * Rp; }
+
+constexpr uint32_t PR_REMOVED = 1u, PR_INOUT = 2u;
+
+template <int DT, int CPL>
+__global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint32_t Rp) {
+  extern __shared__ uint32_t smem[];
+  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t gw = blockIdx.x * kWavesPerBlock + w;
+  const GraphBufs& g = a.g;
+  if (gw >= g.N) return;
+  const uint32_t node = a.order ? a.order[gw] : gw;
+  const uint32_t N = g.N, R = g.R, C = g.C;
+  const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;
+  uint32_t* sid = smem + w * prune_lds_words(Cp, Rp);
+  float* sd = reinterpret_cast<float*>(sid + Cp);
+  uint32_t* fl = sid + 2 * Cp;
+  uint32_t* lst = sid + 3 * Cp;
+  uint32_t* oid = sid + 4 * Cp;
+  float* od = reinterpret_cast<float*>(oid + Rp);
+  const size_t wb = (size_t)node * C, cb = (size_t)node * R;
+  const uint32_t deg = min(g.deg_work[node], C);
+  for (uint32_t i = lane; i < Cp; i += 64) {
+    uint32_t id = DANCE_INV;
+    float dist = FLT_MAX;
+    uint32_t f = PR_REMOVED;
+    if (i < deg) {
+      id = g.work[wb + i];
+      dist = g.wd[wb + i];
+      if (valid_for(id, N, node) && dist < FLT_MAX)
+        f = 0u;
+      else
+        id = DANCE_INV;
+    }
+    sid[i] = id;
+    sd[i] = dist;
+    fl[i] = f;
+  }
+  wave_sync();
+  uint32_t oc = 0, npair = 0;
+  for (uint32_t round = 0; round < R; ++round) {
+    int best = INT_MAX;
+    for (uint32_t i = lane; i < Cp; i += 64) {
+      const bool ok = (fl[i] & PR_REMOVED) == 0u && sid[i] != DANCE_INV;
+      if (ok) best = min(best, fkey(sd[i]));
+    }
+    const int M = wave_min_i(best);
+    if (M == INT_MAX) break;
+    uint32_t cand = 0xFFFFFFFFu;
+    for (uint32_t i = lane; i < Cp; i += 64) {
+      const bool ok = (fl[i] & PR_REMOVED) == 0u && sid[i] != DANCE_INV && fkey(sd[i]) == M;
+      if (ok) cand = min(cand, i);
+    }
+    const uint32_t pos = wave_min_u(cand);
+    const uint32_t sel = uni_u(sid[pos]);
+    const float seld = uni_f(sd[pos]);
+    if (lane == 0) {
+      oid[oc] = sel;
+      od[oc] = seld;
+    }
+    oc++;
+    if (oc >= R) break;
+    uint32_t nq = 0;
+    for (uint32_t b = 0; b < Cp; b += 64) {
+      const uint32_t i = b + lane;
+      const uint32_t id = sid[i];
+      uint32_t f = fl[i];
+      if (id == sel) f |= PR_REMOVED | PR_INOUT;
+      fl[i] = f;
+      const bool q = (f & PR_REMOVED) == 0u && id != DANCE_INV && seld <= sd[i];
+      const uint64_t m = wballot(q);
+      if (q) lst[nq + mbcnt64(m)] = i;
+      nq += popc64(m);
+    }
+    wave_sync();
+    if (nq == 0) continue;
+    uint4 sv[CPL];
+    load_row<CPL>(a.rs, sel, true, sub, sv);
+    for (uint32_t p = 0; p < nq; p += 16) {
+      const uint32_t k0 = p + grp, k1 = p + 8 + grp;
+      const bool a0 = k0 < nq, a1 = k1 < nq;
+      const uint32_t s0 = a0 ? lst[k0] : 0u, s1 = a1 ? lst[k1] : 0u;
+      uint4 b0[CPL], b1[CPL];
+      load_row<CPL>(a.rs, a0 ? sid[s0] : 0u, a0, sub, b0);
+      load_row<CPL>(a.rs, a1 ? sid[s1] : 0u, a1, sub, b1);
+      const float d0 = octet_finish<DT, CPL>(sv, b0);
+      const float d1 = octet_finish<DT, CPL>(sv, b1);
+      if (sub == 0) {
+        if (a0 && a.alpha * d0 <= sd[s0]) fl[s0] |= PR_REMOVED;
+        if (a1 && a.alpha * d1 <= sd[s1]) fl[s1] |= PR_REMOVED;
+      }
+    }
+    npair += nq;
+    wave_sync();
+  }
+  // Degree fill to min(min_degree, R) with the nearest unused candidates,
+  // occluded ones included (vnew2.cu:2076-2126).
+  const uint32_t md = min(a.min_degree, R);
+  while (oc < md) {
+    int best = INT_MAX;
+    for (uint32_t i = lane; i < Cp; i += 64) {
+      const bool ok = sid[i] != DANCE_INV && (fl[i] & PR_INOUT) == 0u;
+      if (ok) best = min(best, fkey(sd[i]));
+    }
+    const int M = wave_min_i(best);
+    if (M == INT_MAX) break;
+    uint32_t cand = 0xFFFFFFFFu;
+    for (uint32_t i = lane; i < Cp; i += 64) {
+      const bool ok = sid[i] != DANCE_INV && (fl[i] & PR_INOUT) == 0u && fkey(sd[i]) == M;
+      if (ok) cand = min(cand, i);
+    }
+    const uint32_t pos = wave_min_u(cand);
+    const uint32_t pick = uni_u(sid[pos]);
+    if (lane == 0) {
+      oid[oc] = pick;
+      od[oc] = sd[pos];
+    }
+    oc++;
+    for (uint32_t i = lane; i < Cp; i += 64)
+      if (sid[i] == pick) fl[i] |= PR_INOUT;
+    wave_sync();
+  }
+  wave_sync();
+  for (uint32_t i = lane; i < C; i += 64) {
+    g.work[wb + i] = i < oc ? oid[i] : DANCE_INV;
+    g.wd[wb + i] = i < oc ? od[i] : FLT_MAX;
+  }
+  for (uint32_t i = lane; i < R; i += 64) g.cur[cb + i] = i < oc ? oid[i] : DANCE_INV;
+  if (lane == 0) {
+    g.deg_work[node] = oc;
+    g.deg_cur[node] = oc;
+  }
+  if (a.ctr && lane == 0) atomicAdd(&a.ctr->prune_dist, (unsigned long long)npair);
+}
+
+// ---------------------------------------------------------------------------
+// Reverse edges. k_rev_keys emits one (target, source) item per forward slot
+// in source order; a stable LSD radix sort by target then yields every segment
+// in ascending source order. k_merge is reverse_merge_csr_kernel
+// (vnew2.cu:1722-1814) over those canonical segments.
+// ---------------------------------------------------------------------------
+__global__ void k_rev_keys(const uint32_t* __restrict__ work, const uint32_t* __restrict__ deg_work, uint32_t N,
+                           uint32_t R, uint32_t C, uint32_t* __restrict__ keys, uint32_t* __restrict__ vals,
+                           uint32_t* __restrict__ indeg) {
+  const size_t j = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= (size_t)N * R) return;
+  const uint32_t s = (uint32_t)(j / R), i = (uint32_t)(j % R);
+  const uint32_t deg = min(deg_work[s], R);
+  const uint32_t t = i < deg ? work[(size_t)s * C + i] : DANCE_INV;
+  const bool v = t != DANCE_INV && t < N && t != s;
+  keys[j] = v ? t : N;
+  vals[j] = s;
+  if (v) atomicAdd(&indeg[t], 1u);
+}
+
+struct MergeArgs {
+  RowSet rs;
+  GraphBufs g;
+  const uint32_t* offsets;  // N+1
+  const uint32_t* srcs;     // sorted sources
+  uint32_t heavy_threshold, heavy_sample;
+  const uint32_t* order;
+  VCounters* ctr;
+};
+
+__host__ __device__ constexpr uint32_t merge_lds_words(uint32_t Cp) { return 2u * Cp + 128u; }
+
+template <int DT, int CPL>
+__global__ __launch_bounds__(kBlock) void k_merge(MergeArgs a, uint32_t Cp) {
+  extern __shared__ uint32_t smem[];
+  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t gw = blockIdx.x * kWavesPerBlock + w;
+  const GraphBufs& g = a.g;
+  if (gw >= g.N) return;
+  const uint32_t t = a.order ? a.order[gw] : gw;
+  const uint32_t N = g.N, C = g.C;
+  const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;
+  uint32_t* wid = smem + w * merge_lds_words(Cp);
+  float* wdd = reinterpret_cast<float*>(wid + Cp);
+  uint32_t* lst = wid + 2 * Cp;
+  float* lsd = reinterpret_cast<float*>(lst + 64);
+  const uint32_t begin = a.offsets[t], end = a.offsets[t + 1];
+  const uint32_t indeg = end - begin;
+  if (indeg == 0) return;
+  uint32_t count = indeg;
+  if (a.heavy_threshold != 0 && indeg > a.heavy_threshold) {
+    count = min(a.heavy_sample, indeg);
+    if (count == 0) count = 1;
+  }
+  const size_t wb = (size_t)t * C;
+  uint32_t deg = min(g.deg_work[t], C);
+  for (uint32_t i = lane; i < Cp; i += 64) {
+    wid[i] = i < C ? g.work[wb + i] : DANCE_INV;
+    wdd[i] = i < C ? g.wd[wb + i] : -FLT_MAX;
+  }
+  uint4 tv[CPL];
+  load_row<CPL>(a.rs, t, true, sub, tv);
+  wave_sync();
+  bool worst_ok = false;
+  int wpos = -1;
+  float wdist = -FLT_MAX;
+  uint32_t ndist = 0;
+  for (uint32_t b = 0; b < count; b += 64) {
+    const uint32_t k = b + lane;
+    uint32_t src = DANCE_INV;
+    if (k < count) {
+      const uint32_t idx =
+          count < indeg ? begin + (uint32_t)(((unsigned long long)k * indeg) / count) : begin + k;
+      src = a.srcs[idx];
+    }
+    const bool v = valid_for(src, N, t);
+    bool inrow = false;
+    for (uint32_t j = 0; j < deg; ++j) inrow |= wid[j] == src;
+    const bool need = v && !inrow;
+    const uint64_t m = wballot(need);
+    const uint32_t n = popc64(m);
+    if (n == 0) continue;
+    if (need) lst[mbcnt64(m)] = src;
+    wave_sync();
+    batch_dist<DT, CPL>(a.rs, tv, lst, lsd, n, grp, sub);
+    ndist += n;
+    const uint32_t ck = lane < n ? lst[lane] : DANCE_INV;
+    const float dk = lane < n ? lsd[lane] : FLT_MAX;
+    for (uint32_t kk = 0; kk < n; ++kk) {
+      const uint32_t s = rdlane_u(ck, (int)kk);
+      const float ds = rdlane_f(dk, (int)kk);
+      bool dup = false;
+      for (uint32_t bb = 0; bb < deg && !dup; bb += 64) {
+        const uint32_t i = bb + lane;
+        dup = wballot(i < deg && wid[i] == s) != 0;
+      }
+      if (dup) continue;
+      if (deg < C) {
+        if (lane == 0) {
+          wid[deg] = s;
+          wdd[deg] = ds;
+        }
+        deg++;
+        worst_ok = false;
+        wave_sync();
+        continue;
+      }
+      if (!worst_ok) {
+        int best = INT_MIN;
+        for (uint32_t i = lane; i < C; i += 64)
+          if (wdd[i] == wdd[i]) best = max(best, fkey(wdd[i]));
+        const int M = wave_max_i(best);
+        wpos = -1;
+        wdist = -FLT_MAX;
+        if (M != INT_MIN && __int_as_float(M) > -FLT_MAX) {
+          uint32_t cand = 0xFFFFFFFFu;
+          for (uint32_t i = lane; i < C; i += 64)
+            if (wdd[i] == wdd[i] && fkey(wdd[i]) == M) cand = min(cand, i);
+          wpos = (int)wave_min_u(cand);
+          wdist = __int_as_float(M);
+        }
+        worst_ok = true;
+      }
+      if (wpos >= 0 && ds < wdist) {
+        if (lane == 0) {
+          wid[wpos] = s;
+          wdd[wpos] = ds;
+        }
+        worst_ok = false;
+        wave_sync();
+      }
+    }
+  }
+  wave_sync();
+  for (uint32_t i = lane; i < C; i += 64) {
+    g.work[wb + i] = wid[i];
+    g.wd[wb + i] = wdd[i];
+  }
+  if (lane == 0) {
+    g.deg_work[t] = deg;
+    if (a.ctr) {
+      atomicAdd(&a.ctr->merge_dist, (unsigned long long)ndist);
+      atomicAdd(&a.ctr->reverse_edges, (unsigned long long)indeg);
+      atomicAdd(&a.ctr->touched_rows, 1ull);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Approximate medoid (medoid_score_kernel_warp, vnew2.cu:1032-1064): one
+// wave per candidate; distances by octets, summed in sample order by lane 0.
+// ---------------------------------------------------------------------------
+template <int DT, int CPL>
+__global__ __launch_bounds__(kBlock) void k_medoid(RowSet rs, uint32_t N, uint32_t nc, uint32_t ns,
+                                                   float* scores, uint32_t* cands) {
+  __shared__ float buf[kWavesPerBlock][512];
+  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t cw = blockIdx.x * kWavesPerBlock + w;
+  if (cw >= nc) return;
+  const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;
+  const uint32_t c = d_hash_u32(cw * 9973u + 17u) % N;
+  uint4 cv[CPL];
+  load_row<CPL>(rs, c, true, sub, cv);
+  float sum = 0.0f;
+  for (uint32_t base = 0; base < ns; base += 512) {
+    const uint32_t cnt = min(512u, ns - base);
+    for (uint32_t p = 0; p < cnt; p += 16) {
+      const uint32_t k0 = p + grp, k1 = p + 8 + grp;
+      const bool a0 = k0 < cnt, a1 = k1 < cnt;
+      const uint32_t s0 = d_hash_u32((base + k0) * 10007u + 131u) % N;
+      const uint32_t s1 = d_hash_u32((base + k1) * 10007u + 131u) % N;
+      uint4 b0[CPL], b1[CPL];
+      load_row<CPL>(rs, s0, a0, sub, b0);
+      load_row<CPL>(rs, s1, a1, sub, b1);
+      const float d0 = octet_finish<DT, CPL>(cv, b0);
+      const float d1 = octet_finish<DT, CPL>(cv, b1);
+      if (sub == 0) {
+        if (a0) buf[w][k0] = d0;
+        if (a1) buf[w][k1] = d1;
+      }
+    }
+    wave_sync();
+    if (lane == 0) {
+      for (uint32_t k = 0; k < cnt; ++k) {
+        const uint32_t smp = d_hash_u32((base + k) * 10007u + 131u) % N;
+        if (smp == c) continue;
+        sum += buf[w][k];
+      }
+    }
+    wave_sync();
+  }
+  if (lane == 0) {
+    scores[cw] = sum / (float)ns;
+    cands[cw] = c;
+  }
+}
+
+// init_random_graph (vnew2.cu:1066-1117): R hashed neighbours per vertex.
+template <int DT, int CPL>
+__global__ __launch_bounds__(kBlock) void k_init(RowSet rs, GraphBufs g) {
+  __shared__ uint32_t lstb[kWavesPerBlock][64];
+  __shared__ float lsdb[kWavesPerBlock][64];
+  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t node = blockIdx.x * kWavesPerBlock + w;
+  const uint32_t N = g.N, R = g.R, C = g.C;
+  if (node >= N) return;
+  const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;
+  const size_t cb = (size_t)node * R, wb = (size_t)node * C;
+  for (uint32_t i = lane; i < C; i += 64) {
+    g.work[wb + i] = DANCE_INV;
+    g.wd[wb + i] = FLT_MAX;
+  }
+  uint4 nv[CPL];
+  load_row<CPL>(rs, node, true, sub, nv);
+  for (uint32_t b = 0; b < R; b += 64) {
+    const uint32_t i = b + lane;
+    uint32_t nb = i < R ? d_det_neighbor(node, i, N) : DANCE_INV;
+    if (N <= 1 || nb == DANCE_INV || nb >= N || nb == node) nb = DANCE_INV;
+    const bool v = i < R && nb != DANCE_INV;
+    const uint64_t m = wballot(v);
+    const uint32_t n = popc64(m);
+    if (v) lstb[w][mbcnt64(m)] = nb;
+    wave_sync();
+    batch_dist<DT, CPL>(rs, nv, lstb[w], lsdb[w], n, grp, sub);
+    const float dist = v ? lsdb[w][mbcnt64(m)] : FLT_MAX;
+    if (i < R) {
+      g.cur[cb + i] = nb;
+      g.work[wb + i] = nb;
+      g.wd[wb + i] = dist;
+    }
+    wave_sync();
+  }
+  if (lane == 0) {
+    const uint32_t deg = N > 1 ? R : 0u;
+    g.deg_cur[node] = deg;
+    g.deg_work[node] = deg;
+  }
+}
+
+}  // namespace dance

@@ -1,0 +1,189 @@
+// Wave64 primitives and the canonical distance for gfx950 (CDNA4).
+//
+// Distances are computed by "octets": 8 consecutive lanes cooperate on one
+// vector pair, each lane owning the 16-byte chunks sub, sub+8, sub+16, ... of
+// the row (sub = lane & 7). One wave therefore evaluates 8 distances per pass,
+// and every 8-lane load instruction reads whole 128-byte lines.
+//
+// Canonical arithmetic (shared bit for bit with the CPU oracle):
+//   fp32 / fp16 (widened exactly to fp32): p = fmaf(t, t, p), t = a - b, in
+//   ascending element order within the lane's chunks; then the xor-4/2/1 lane
+//   butterfly ((p0+p4)+(p2+p6)) + ((p1+p5)+(p3+p7)).
+//   uint8: exact integer sum of (a-b)^2, converted to fp32 once.
+// The value is symmetric in (a, b): a-b and b-a differ only in sign.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <float.h>
+#include <limits.h>
+
+#define DANCE_INV 0xFFFFFFFFu
+
+enum DanceDType : int { DANCE_F32 = 0, DANCE_U8 = 1, DANCE_F16 = 2 };
+
+__device__ __forceinline__ uint32_t lane_id() {
+  return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+__device__ __forceinline__ uint64_t wballot(bool p) { return (uint64_t)__ballot(p); }
+__device__ __forceinline__ uint32_t mbcnt64(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+__device__ __forceinline__ int ffs64(uint64_t m) { return __ffsll((unsigned long long)m) - 1; }
+__device__ __forceinline__ uint32_t popc64(uint64_t m) { return (uint32_t)__popcll((unsigned long long)m); }
+
+__device__ __forceinline__ int uni_i(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ uint32_t uni_u(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
+__device__ __forceinline__ float uni_f(float v) {
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+__device__ __forceinline__ uint32_t rdlane_u(uint32_t v, int l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
+}
+__device__ __forceinline__ float rdlane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// Orders LDS traffic between lanes of one wave (the wave runs in lockstep;
+// this keeps the compiler from reordering and drains outstanding LDS ops).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
+  return uni_i(v);
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
+  return uni_i(v);
+}
+__device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o));
+  return uni_u(v);
+}
+
+// Reference hashes: vnew2.cu:169-191.
+__device__ __forceinline__ uint32_t d_hash_u32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+__device__ __forceinline__ uint32_t d_det_neighbor(uint32_t node, uint32_t k, uint32_t N) {
+  if (N <= 1) return DANCE_INV;
+  uint32_t v = d_hash_u32(node * 0x9e3779b1u + k * 0x85ebca6bu + 17u) % N;
+  if (v == node) v = (v + 1u) % N;
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Octet distance.
+// ---------------------------------------------------------------------------
+struct RowSet {
+  const uint4* rows;  // device rows, each padded to stride16 16-byte chunks
+  uint32_t stride16;  // chunks per row (row stride / 16 bytes)
+  uint32_t nch;       // chunks that hold data (ceil(dim * elem_bytes / 16))
+};
+
+template <int CPL>
+__device__ __forceinline__ void load_row(const RowSet& rs, uint32_t id, bool active, uint32_t sub,
+                                         uint4 (&v)[CPL]) {
+  const uint4* p = rs.rows + (size_t)id * rs.stride16;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const uint32_t cc = sub + 8u * (uint32_t)c;
+    if (active && cc < rs.nch)
+      v[c] = p[cc];
+    else
+      v[c] = make_uint4(0u, 0u, 0u, 0u);
+  }
+}
+
+__device__ __forceinline__ float fma_sq(float a, float b, float acc) {
+  const float t = a - b;
+  return __builtin_fmaf(t, t, acc);
+}
+
+__device__ __forceinline__ float h2f_lo(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
+}
+__device__ __forceinline__ float h2f_hi(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+template <int DT, int CPL>
+__device__ __forceinline__ float octet_partial_f(const uint4 (&a)[CPL], const uint4 (&b)[CPL]) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    if constexpr (DT == DANCE_F32) {
+      acc = fma_sq(__uint_as_float(a[c].x), __uint_as_float(b[c].x), acc);
+      acc = fma_sq(__uint_as_float(a[c].y), __uint_as_float(b[c].y), acc);
+      acc = fma_sq(__uint_as_float(a[c].z), __uint_as_float(b[c].z), acc);
+      acc = fma_sq(__uint_as_float(a[c].w), __uint_as_float(b[c].w), acc);
+    } else {
+      acc = fma_sq(h2f_lo(a[c].x), h2f_lo(b[c].x), acc);
+      acc = fma_sq(h2f_hi(a[c].x), h2f_hi(b[c].x), acc);
+      acc = fma_sq(h2f_lo(a[c].y), h2f_lo(b[c].y), acc);
+      acc = fma_sq(h2f_hi(a[c].y), h2f_hi(b[c].y), acc);
+      acc = fma_sq(h2f_lo(a[c].z), h2f_lo(b[c].z), acc);
+      acc = fma_sq(h2f_hi(a[c].z), h2f_hi(b[c].z), acc);
+      acc = fma_sq(h2f_lo(a[c].w), h2f_lo(b[c].w), acc);
+      acc = fma_sq(h2f_hi(a[c].w), h2f_hi(b[c].w), acc);
+    }
+  }
+  return acc;
+}
+
+template <int CPL>
+__device__ __forceinline__ int octet_partial_u8(const uint4 (&a)[CPL], const uint4 (&b)[CPL]) {
+  // sum over bytes of a^2 + b^2 - 2ab, exact in 32-bit integers
+  uint32_t sq = 0u, cr = 0u;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    sq = __builtin_amdgcn_udot4(a[c].x, a[c].x, sq, false);
+    sq = __builtin_amdgcn_udot4(b[c].x, b[c].x, sq, false);
+    cr = __builtin_amdgcn_udot4(a[c].x, b[c].x, cr, false);
+    sq = __builtin_amdgcn_udot4(a[c].y, a[c].y, sq, false);
+    sq = __builtin_amdgcn_udot4(b[c].y, b[c].y, sq, false);
+    cr = __builtin_amdgcn_udot4(a[c].y, b[c].y, cr, false);
+    sq = __builtin_amdgcn_udot4(a[c].z, a[c].z, sq, false);
+    sq = __builtin_amdgcn_udot4(b[c].z, b[c].z, sq, false);
+    cr = __builtin_amdgcn_udot4(a[c].z, b[c].z, cr, false);
+    sq = __builtin_amdgcn_udot4(a[c].w, a[c].w, sq, false);
+    sq = __builtin_amdgcn_udot4(b[c].w, b[c].w, sq, false);
+    cr = __builtin_amdgcn_udot4(a[c].w, b[c].w, cr, false);
+  }
+  return (int)(sq - 2u * cr);
+}
+
+// Full distance of a pair held by an octet; every lane of the octet returns it.
+// Must be called by all 64 lanes (the butterfly crosses lanes).
+template <int DT, int CPL>
+__device__ __forceinline__ float octet_finish(const uint4 (&a)[CPL], const uint4 (&b)[CPL]) {
+  if constexpr (DT == DANCE_U8) {
+    int p = octet_partial_u8<CPL>(a, b);
+    p += __shfl_xor(p, 4);
+    p += __shfl_xor(p, 2);
+    p += __shfl_xor(p, 1);
+    return (float)(uint32_t)p;
+  } else {
+    float p = octet_partial_f<DT, CPL>(a, b);
+    p += __shfl_xor(p, 4);
+    p += __shfl_xor(p, 2);
+    p += __shfl_xor(p, 1);
+    return p;
+  }
+}
+
+// Float ordering keys for wave reductions over non-negative distances.
+// NaN never wins, matching the reference's strict float comparisons.
+__device__ __forceinline__ int fkey(float d) { return __float_as_int(d); }

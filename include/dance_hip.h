@@ -1,0 +1,112 @@
+/* Extension entry points of libdance_hip.so beyond the reference's public
+ * headers. The reference ABI itself (gpu_vamana_builder.h,
+ * gpu_vamana_filtered.h) is declared unchanged in the sibling headers; these
+ * entry points serve the bench (device-resident inputs), per-kernel
+ * measurement, and stage-level parity tests. Each stage hook runs exactly the
+ * kernel the production build uses, on host buffers, and cites the reference
+ * kernel it replaces. All return 0 on success and -1 on error (message on
+ * stderr), like the reference ABI. */
+#ifndef DANCE_HIP_H
+#define DANCE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of the vector rows. */
+enum { DANCE_DTYPE_F32 = 0, DANCE_DTYPE_U8 = 1, DANCE_DTYPE_F16 = 2 };
+
+/* Per-kernel timings (HIP events on the build stream) and algorithmic work
+ * counted on the device by each wave. Bytes are algorithmic: one vector row
+ * per distance gathered, plus adjacency and work rows as documented in
+ * dance_amd/csrc/vnew2_build.hip. */
+typedef struct DanceKernelProfile {
+    double medoid_ms, init_ms, search_ms, reverse_ms, merge_ms, prune_ms, total_ms;
+    uint32_t iterations;
+    uint32_t vector_bytes;
+    uint64_t search_dist, insert_dist, expansions, vis_skips;
+    uint64_t merge_dist, prune_dist, reverse_edges, touched_rows;
+    double search_bytes, merge_bytes, prune_bytes, reverse_bytes;
+} DanceKernelProfile;
+
+/* Full standard (vnew2) build with the vectors already resident in device
+ * memory (row-major N x dim of `dtype`) and device outputs d_graph (N x R,
+ * 0xFFFFFFFF-padded rows) and d_degree (N). Same algorithm, parameters and
+ * errors as gpu_vamana_vnew2_build (reference: src/gpu_vamana_vnew2.cu:2170-2855);
+ * used by the bench so the timed region excludes PCIe. */
+int dance_vamana_build_resident(const void *d_data, int dtype, uint32_t num_points, uint32_t dim, uint32_t R,
+                                uint32_t L, uint32_t C, uint32_t STEPS, uint32_t *d_graph, uint32_t *d_degree);
+
+/* Timings and counters of the last build on this process. */
+void dance_get_last_kernel_profile(DanceKernelProfile *profile);
+
+/* Selects the build profile at run time: "QUALITY" (default, fp32 storage),
+ * "FAST_SMALL" (fp16 storage for float input), "PRO6000_100M" and
+ * "FILTERED_PAPER" (fp16 + reverse heavy cap 256/384). Reference: CMake
+ * DANCE_PROFILE, integrations/dance-diskann-78256bba.patch:2400-2462. The
+ * DANCE_PROFILE environment variable sets the initial value. */
+int dance_set_profile(const char *name);
+const char *dance_get_profile(void);
+
+/* ---- stage hooks (host buffers), used by the parity tests ---- */
+
+/* Canonical squared-L2 distances d(a[i], b[i]) (reference distance family,
+ * src/gpu_vamana_vnew2.cu:215-423). */
+int dance_stage_distances(const void *h_data, int dtype, uint32_t num_points, uint32_t dim, const uint32_t *a,
+                          const uint32_t *b, uint64_t n, float *out);
+
+/* medoid_score_kernel_warp + host top-1 (src/gpu_vamana_vnew2.cu:1032-1064, 2359-2479).
+ * scores/cands: min(1024, N) entries. */
+int dance_stage_medoid(const void *h_data, int dtype, uint32_t num_points, uint32_t dim, float *scores,
+                       uint32_t *cands, uint32_t *medoid);
+
+/* init_random_graph (src/gpu_vamana_vnew2.cu:1066-1117). */
+int dance_stage_init(const void *h_data, int dtype, uint32_t num_points, uint32_t dim, uint32_t R, uint32_t C,
+                     uint32_t *cur, uint32_t *deg_cur, uint32_t *work, uint32_t *deg_work, float *wd);
+
+/* One search + online-insert pass over all vertices
+ * (search_prune_kernel_shared, src/gpu_vamana_vnew2.cu:1119-1439). In/out graph state. */
+int dance_stage_search(const void *h_data, int dtype, uint32_t num_points, uint32_t dim, uint32_t R, uint32_t L,
+                       uint32_t C, uint32_t steps, float alpha, uint32_t start, uint32_t *cur, uint32_t *deg_cur,
+                       uint32_t *work, uint32_t *deg_work, float *wd);
+
+/* Reverse CSR + merge (reverse_count/fill_csr_kernel + reverse_merge_csr_kernel,
+ * src/gpu_vamana_vnew2.cu:1604-1661, 1722-1814). offsets (N+1) and ids (N*R)
+ * receive the canonical CSR when non-null. */
+int dance_stage_reverse_merge(const void *h_data, int dtype, uint32_t num_points, uint32_t dim, uint32_t R,
+                              uint32_t C, uint32_t *work, uint32_t *deg_work, float *wd, uint32_t heavy_threshold,
+                              uint32_t heavy_sample, uint32_t *offsets, uint32_t *ids);
+
+/* RobustPrune + degree fill (final_prune_kernel_shared, src/gpu_vamana_vnew2.cu:1893-2147). */
+int dance_stage_prune(const void *h_data, int dtype, uint32_t num_points, uint32_t dim, uint32_t R, uint32_t C,
+                      uint32_t min_degree, float alpha, uint32_t *work, uint32_t *deg_work, float *wd,
+                      uint32_t *cur, uint32_t *deg_cur);
+
+/* Stable radix sort of (key, value) pairs on the low `key_bits` bits
+ * (replaces thrust/CUB primitives of the reference). */
+int dance_stage_sort_pairs(const uint32_t *keys, const uint32_t *vals, uint64_t n, uint32_t key_bits,
+                           uint32_t *out_keys, uint32_t *out_vals);
+
+/* Exclusive prefix sum of n uint32 values (replaces thrust::inclusive_scan,
+ * src/gpu_vamana_vnew2.cu:2576-2577). */
+int dance_stage_scan(const uint32_t *in, uint64_t n, uint32_t *out);
+
+/* ---- synthetic workloads (host, multithreaded, deterministic) ---- */
+
+/* Gaussian-mixture vectors: centers ~ N(0, I) (num_centers = 0: pure N(0, I)),
+ * x = c_k + sigma * eps, optionally L2-normalised. stream selects an
+ * independent sub-stream (0 = base, 1 = queries, ...). fp32 rows. */
+int dance_synth_f32(uint64_t seed, uint32_t stream, uint32_t num_points, uint32_t dim, uint32_t num_centers,
+                    float sigma, int normalize, float *out);
+
+/* uint8 rows clip(round(64 + 24 z), 0, 255) of a Gaussian mixture z. */
+int dance_synth_u8(uint64_t seed, uint32_t stream, uint32_t num_points, uint32_t dim, uint32_t num_centers,
+                   float sigma, uint8_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

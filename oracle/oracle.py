@@ -1,0 +1,244 @@
+"""ctypes front-end of the CPU oracle (liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg use this module as the checker. Product code never imports it.
+
+Parity status of each oracle function (how it is pinned; see tests/test_oracle.py):
+  hash_u32, det_neighbor  pinned: bijectivity via the closed-form inverse of the
+                          xorshift-multiply steps; range/bump properties.
+  distance (f32/f16/u8)   pinned: u8 exact integer; f32/f16 within the fp32
+                          error bound of an fp64 evaluation; symmetry; d(a,a)=0.
+  medoid                  pinned: fp64 brute force of the same candidate/sample
+                          scheme on small N.
+  init_graph              pinned: closed form (hashed neighbours, distances).
+  prune                   pinned: textbook RobustPrune (DiskANN Alg. 2 + fill)
+                          restated independently in Python, plus invariants.
+  reverse_merge           pinned: CSR == transpose of the first-R forward
+                          entries with ascending sources; merge invariants and an
+                          independent Python restatement.
+  search (online insert)  partially pinned: invariants (row = cur row and
+                          expanded nodes, no duplicates/self, capacity C) and the
+                          independent batched GPU implementation; the reference
+                          cannot be executed here, so its exact step semantics
+                          are pinned by source reading only.
+  vnew2_build             pinned end to end by recall@10 against exact
+                          brute-force ground truth.
+  cpu_vamana_build        baseline only (DiskANN restated; parity unpinned:
+                          upstream DiskANN is not available offline).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+INVALID = 0xFFFFFFFF
+DTYPE = {np.dtype(np.float32): 0, np.dtype(np.uint8): 1, np.dtype(np.float16): 2}
+
+_u32p = C.POINTER(C.c_uint32)
+_f32p = C.POINTER(C.c_float)
+_LIB = None
+
+
+def build() -> str:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+def lib() -> C.CDLL:
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        u32, f32, vp, i32, u64 = C.c_uint32, C.c_float, C.c_void_p, C.c_int, C.c_uint64
+        L.oracle_hash_u32.argtypes = [u32]
+        L.oracle_hash_u32.restype = u32
+        L.oracle_det_neighbor.argtypes = [u32, u32, u32]
+        L.oracle_det_neighbor.restype = u32
+        L.oracle_distance.argtypes = [vp, i32, u32, u32, u32]
+        L.oracle_distance.restype = f32
+        L.oracle_distance_many.argtypes = [vp, i32, u32, _u32p, _u32p, u64, _f32p]
+        L.oracle_distance_many.restype = None
+        L.oracle_medoid.argtypes = [vp, i32, u32, u32, _f32p, _u32p]
+        L.oracle_medoid.restype = u32
+        L.oracle_init_graph.argtypes = [vp, i32, u32, u32, u32, u32, _u32p, _u32p, _u32p, _u32p, _f32p]
+        L.oracle_init_graph.restype = None
+        L.oracle_search.argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, f32, u32, _u32p, _u32p, _u32p,
+                                    _u32p, _f32p]
+        L.oracle_search.restype = u64
+        L.oracle_reverse_merge.argtypes = [vp, i32, u32, u32, u32, u32, _u32p, _u32p, _f32p, u32, u32,
+                                           _u32p, _u32p]
+        L.oracle_reverse_merge.restype = u64
+        L.oracle_prune.argtypes = [vp, i32, u32, u32, u32, u32, u32, f32, _u32p, _u32p, _f32p, _u32p, _u32p]
+        L.oracle_prune.restype = None
+        L.oracle_vnew2_build.argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, u32, f32, u32, u32, _u32p,
+                                         _u32p, _u32p]
+        L.oracle_vnew2_build.restype = i32
+        L.oracle_cpu_vamana_build.argtypes = [vp, i32, u32, u32, u32, u32, f32, u32, _u32p, _u32p]
+        L.oracle_cpu_vamana_build.restype = u32
+        L.oracle_beam_search.argtypes = [vp, i32, u32, u32, _u32p, _u32p, u32, u32, vp, u32, u32, u32, _u32p]
+        L.oracle_beam_search.restype = u64
+        L.oracle_bruteforce_knn.argtypes = [vp, i32, u32, u32, vp, u32, u32, _u32p, _f32p]
+        L.oracle_bruteforce_knn.restype = None
+        L.oracle_num_threads.argtypes = []
+        L.oracle_num_threads.restype = i32
+        _LIB = L
+    return _LIB
+
+
+def _p(a, t=C.c_uint32):
+    return a.ctypes.data_as(C.POINTER(t))
+
+
+def _dt(data: np.ndarray) -> int:
+    return DTYPE[data.dtype]
+
+
+def hash_u32(x: int) -> int:
+    return int(lib().oracle_hash_u32(x))
+
+
+def det_neighbor(node: int, k: int, N: int) -> int:
+    return int(lib().oracle_det_neighbor(node, k, N))
+
+
+def distance(data: np.ndarray, a: int, b: int) -> float:
+    data = np.ascontiguousarray(data)
+    return float(np.float32(lib().oracle_distance(data.ctypes.data, _dt(data), data.shape[1], a, b)))
+
+
+def distances(data: np.ndarray, a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    data = np.ascontiguousarray(data)
+    a = np.ascontiguousarray(a, np.uint32)
+    b = np.ascontiguousarray(b, np.uint32)
+    out = np.empty(a.shape[0], np.float32)
+    lib().oracle_distance_many(data.ctypes.data, _dt(data), data.shape[1], _p(a), _p(b), a.shape[0],
+                               _p(out, C.c_float))
+    return out
+
+
+def medoid(data: np.ndarray):
+    data = np.ascontiguousarray(data)
+    nc = min(1024, data.shape[0])
+    scores = np.empty(nc, np.float32)
+    cands = np.empty(nc, np.uint32)
+    m = lib().oracle_medoid(data.ctypes.data, _dt(data), data.shape[0], data.shape[1], _p(scores, C.c_float),
+                            _p(cands))
+    return int(m), scores, cands
+
+
+class State:
+    """Graph state in the device layout: cur N x R, work/wd N x C."""
+
+    def __init__(self, cur, deg_cur, work, deg_work, wd):
+        self.cur, self.deg_cur, self.work, self.deg_work, self.wd = cur, deg_cur, work, deg_work, wd
+
+    @staticmethod
+    def empty(N, R, C_):
+        return State(np.full((N, R), INVALID, np.uint32), np.zeros(N, np.uint32),
+                     np.full((N, C_), INVALID, np.uint32), np.zeros(N, np.uint32),
+                     np.full((N, C_), np.finfo(np.float32).max, np.float32))
+
+    def copy(self):
+        return State(self.cur.copy(), self.deg_cur.copy(), self.work.copy(), self.deg_work.copy(), self.wd.copy())
+
+    def ptrs(self):
+        return _p(self.cur), _p(self.deg_cur), _p(self.work), _p(self.deg_work), _p(self.wd, C.c_float)
+
+
+def init_graph(data: np.ndarray, R: int, C_: int) -> State:
+    data = np.ascontiguousarray(data)
+    s = State.empty(data.shape[0], R, C_)
+    lib().oracle_init_graph(data.ctypes.data, _dt(data), data.shape[0], data.shape[1], R, C_, *s.ptrs())
+    return s
+
+
+def search(data: np.ndarray, s: State, L: int, steps: int, alpha: float, start: int) -> State:
+    data = np.ascontiguousarray(data)
+    s = s.copy()
+    N, R = s.cur.shape
+    lib().oracle_search(data.ctypes.data, _dt(data), N, data.shape[1], R, L, s.work.shape[1], steps, alpha, start,
+                        *s.ptrs())
+    return s
+
+
+def reverse_merge(data: np.ndarray, s: State, heavy_threshold: int = 0, heavy_sample: int = 0):
+    data = np.ascontiguousarray(data)
+    s = s.copy()
+    N, R = s.cur.shape
+    off = np.zeros(N + 1, np.uint32)
+    ids = np.zeros(N * R, np.uint32)
+    n = lib().oracle_reverse_merge(data.ctypes.data, _dt(data), N, data.shape[1], R, s.work.shape[1],
+                                   _p(s.work), _p(s.deg_work), _p(s.wd, C.c_float), heavy_threshold, heavy_sample,
+                                   _p(off), _p(ids))
+    return s, off, ids[:n]
+
+
+def prune(data: np.ndarray, s: State, min_degree: int, alpha: float) -> State:
+    data = np.ascontiguousarray(data)
+    s = s.copy()
+    N, R = s.cur.shape
+    lib().oracle_prune(data.ctypes.data, _dt(data), N, data.shape[1], R, s.work.shape[1], min_degree, alpha,
+                       _p(s.work), _p(s.deg_work), _p(s.wd, C.c_float), _p(s.cur), _p(s.deg_cur))
+    return s
+
+
+def vnew2_build(data: np.ndarray, R=64, L=100, C_=80, STEPS=64, iters=4, alpha=1.2, heavy_threshold=0,
+                heavy_sample=0):
+    data = np.ascontiguousarray(data)
+    N = data.shape[0]
+    graph = np.empty((N, R), np.uint32)
+    deg = np.empty(N, np.uint32)
+    med = np.zeros(1, np.uint32)
+    rc = lib().oracle_vnew2_build(data.ctypes.data, _dt(data), N, data.shape[1], R, L, C_, STEPS, iters, alpha,
+                                  heavy_threshold, heavy_sample, _p(graph), _p(deg), _p(med))
+    if rc != 0:
+        raise ValueError(f"oracle_vnew2_build rejected the parameters (rc={rc})")
+    return graph, deg, int(med[0])
+
+
+def cpu_vamana_build(data: np.ndarray, R=64, L=100, alpha=1.2, maxc=750):
+    data = np.ascontiguousarray(data)
+    N = data.shape[0]
+    graph = np.empty((N, R), np.uint32)
+    deg = np.empty(N, np.uint32)
+    start = lib().oracle_cpu_vamana_build(data.ctypes.data, _dt(data), N, data.shape[1], R, L, alpha, maxc,
+                                          _p(graph), _p(deg))
+    return graph, deg, int(start)
+
+
+def beam_search(data, graph, degree, start, queries, k, L):
+    data = np.ascontiguousarray(data)
+    queries = np.ascontiguousarray(queries, dtype=data.dtype)
+    graph = np.ascontiguousarray(graph, np.uint32)
+    degree = np.ascontiguousarray(degree, np.uint32)
+    out = np.empty((queries.shape[0], k), np.uint32)
+    lib().oracle_beam_search(data.ctypes.data, _dt(data), data.shape[0], data.shape[1], _p(graph), _p(degree),
+                             graph.shape[1], start, queries.ctypes.data, queries.shape[0], k, L, _p(out))
+    return out
+
+
+def bruteforce_knn(data, queries, k):
+    data = np.ascontiguousarray(data)
+    queries = np.ascontiguousarray(queries, dtype=data.dtype)
+    ids = np.empty((queries.shape[0], k), np.uint32)
+    d = np.empty((queries.shape[0], k), np.float32)
+    lib().oracle_bruteforce_knn(data.ctypes.data, _dt(data), data.shape[0], data.shape[1], queries.ctypes.data,
+                                queries.shape[0], k, _p(ids), _p(d, C.c_float))
+    return ids, d
+
+
+def recall_at_k(found: np.ndarray, gt: np.ndarray, k: int = 10) -> float:
+    hits = 0
+    for f, g in zip(found[:, :k], gt[:, :k]):
+        hits += len(set(f.tolist()) & set(g.tolist()))
+    return hits / (gt.shape[0] * k)
+
+
+def num_threads() -> int:
+    return int(lib().oracle_num_threads())

@@ -1,0 +1,175 @@
+"""GPU parity: every HIP stage of the standard build against the CPU oracle,
+bit for bit, on identical inputs (gfx950 only).
+
+Each test feeds the HIP kernel (through the C ABI) and the oracle the same
+seeded input and requires identical outputs: integer ids/degrees exactly and
+fp32 distances bitwise (both sides implement the canonical distance order).
+"""
+import numpy as np
+import pytest
+
+import dance_amd as D
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+INV = 0xFFFFFFFF
+FMAX = np.finfo(np.float32).max
+
+
+def make_data(kind, n, dim, seed=7):
+    rng = np.random.default_rng(seed)
+    if kind == "f32":
+        x = rng.standard_normal((n, dim)).astype(np.float32)
+        return x / np.linalg.norm(x, axis=1, keepdims=True).astype(np.float32)
+    if kind == "f16":
+        return rng.standard_normal((n, dim)).astype(np.float16)
+    return rng.integers(0, 256, (n, dim), dtype=np.uint8)
+
+
+def random_work_state(data, R, C, seed):
+    """Candidate rows with invalid ids, self loops, duplicates and FLT_MAX dists."""
+    rng = np.random.default_rng(seed)
+    N = data.shape[0]
+    s = O.State.empty(N, R, C)
+    ids = rng.integers(0, N, (N, C)).astype(np.uint32)
+    ids[rng.random((N, C)) < 0.08] = INV
+    selfm = rng.random((N, C)) < 0.02
+    ids[selfm] = np.broadcast_to(np.arange(N, dtype=np.uint32)[:, None], (N, C))[selfm]
+    dupm = rng.random((N, C - 1)) < 0.06
+    ids[:, 1:][dupm] = ids[:, :-1][dupm]
+    a = np.repeat(np.arange(N, dtype=np.uint32), C)
+    b = ids.ravel()
+    ok = b < N
+    d = np.full(N * C, FMAX, np.float32)
+    d[ok] = O.distances(data, a[ok], b[ok])
+    d = d.reshape(N, C)
+    d[rng.random((N, C)) < 0.01] = FMAX
+    s.work = ids
+    s.wd = d
+    s.deg_work = rng.integers(0, C + 1, N).astype(np.uint32)
+    return s
+
+
+def to_dance(s):
+    return D.GraphState(s.cur.copy(), s.deg_cur.copy(), s.work.copy(), s.deg_work.copy(), s.wd.copy())
+
+
+def assert_state_equal(g, s, fields=("cur", "deg_cur", "work", "deg_work", "wd")):
+    for f in fields:
+        a, b = getattr(g, f), getattr(s, f)
+        if f == "wd":
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{f} differs at {np.argwhere(a.view(np.uint32) != b.view(np.uint32))[:5]}"
+        else:
+            assert np.array_equal(a, b), f"{f} differs at {np.argwhere(a != b)[:5]}"
+
+
+@pytest.mark.parametrize("kind,dim", [("f32", 96), ("f32", 100), ("f32", 7), ("u8", 128), ("u8", 192),
+                                      ("u8", 33), ("f16", 96), ("f16", 50)])
+def test_distances_bitwise(kind, dim):
+    data = make_data(kind, 3000, dim, seed=dim)
+    rng = np.random.default_rng(1)
+    a = rng.integers(0, 3000, 20000).astype(np.uint32)
+    b = rng.integers(0, 3000, 20000).astype(np.uint32)
+    g = D.stage_distances(data, a, b)
+    o = O.distances(data, a, b)
+    assert np.array_equal(g.view(np.uint32), o.view(np.uint32))
+
+
+@pytest.mark.parametrize("kind,n", [("f32", 5000), ("u8", 3000), ("f32", 700), ("f32", 1)])
+def test_medoid(kind, n):
+    data = make_data(kind, n, 96 if kind == "f32" else 128)
+    gm, gs, gc = D.stage_medoid(data)
+    om, os_, oc = O.medoid(data)
+    assert np.array_equal(gc, oc)
+    assert np.array_equal(gs.view(np.uint32), os_.view(np.uint32))
+    assert gm == om
+
+
+@pytest.mark.parametrize("kind,R,C", [("f32", 64, 80), ("u8", 32, 48), ("f32", 100, 130)])
+def test_init(kind, R, C):
+    data = make_data(kind, 2000, 96 if kind == "f32" else 128)
+    g = D.stage_init(data, R, C)
+    s = O.init_graph(data, R, C)
+    assert_state_equal(g, s)
+
+
+@pytest.mark.parametrize("kind", ["f32", "u8", "f16"])
+@pytest.mark.parametrize("alpha,min_degree", [(1.0, 0), (1.2, 0), (1.2, 64), (1.2, 24)])
+def test_prune_bitexact(kind, alpha, min_degree):
+    dim = {"f32": 96, "u8": 128, "f16": 96}[kind]
+    data = make_data(kind, 2500, dim, seed=3)
+    R, C = 32, 80
+    s0 = random_work_state(data, R, C, seed=11)
+    g = D.stage_prune(data, to_dance(s0), min_degree, alpha)
+    s = O.prune(data, s0, min_degree, alpha)
+    assert_state_equal(g, s)
+
+
+@pytest.mark.parametrize("kind", ["f32", "u8"])
+@pytest.mark.parametrize("heavy", [(0, 0), (8, 12)])
+def test_reverse_merge_bitexact(kind, heavy):
+    dim = 96 if kind == "f32" else 128
+    data = make_data(kind, 3000, dim, seed=5)
+    R, C = 32, 48
+    s0 = random_work_state(data, R, C, seed=21)
+    g, goff, gids = D.stage_reverse_merge(data, to_dance(s0), *heavy)
+    s, ooff, oids = O.reverse_merge(data, s0, *heavy)
+    assert np.array_equal(goff, ooff)
+    assert np.array_equal(gids, oids)
+    assert_state_equal(g, s, ("work", "deg_work", "wd"))
+
+
+@pytest.mark.parametrize("kind,R,L,C,steps", [("f32", 32, 64, 48, 32), ("f32", 64, 100, 80, 64),
+                                              ("u8", 32, 64, 48, 48), ("f32", 16, 150, 40, 100)])
+def test_search_bitexact(kind, R, L, C, steps):
+    dim = 96 if kind == "f32" else 128
+    data = make_data(kind, 3000, dim, seed=9)
+    s0 = O.init_graph(data, R, C)
+    start, _, _ = O.medoid(data)
+    for alpha in (1.0, 1.2):
+        g = D.stage_search(data, to_dance(s0), L, steps, alpha, start)
+        s = O.search(data, s0, L, steps, alpha, start)
+        assert_state_equal(g, s, ("work", "deg_work", "wd"))
+
+
+def test_search_after_iterations():
+    """Search on a pruned (dup-free, converged) graph, not only the random init."""
+    data = make_data("f32", 3000, 96, seed=13)
+    R, L, C, steps = 32, 64, 48, 48
+    start, _, _ = O.medoid(data)
+    s = O.init_graph(data, R, C)
+    for it in range(2):
+        s = O.search(data, s, L, steps, 1.0, start)
+        s, _, _ = O.reverse_merge(data, s)
+        s = O.prune(data, s, 0, 1.0)
+    g = D.stage_search(data, to_dance(s), L, steps, 1.2, start)
+    o = O.search(data, s, L, steps, 1.2, start)
+    assert_state_equal(g, o, ("work", "deg_work", "wd"))
+
+
+@pytest.mark.parametrize("kind,n,R,L,C,steps", [("f32", 3000, 32, 64, 48, 32), ("u8", 3000, 32, 64, 48, 32),
+                                                ("f32", 4000, 64, 100, 80, 64)])
+def test_end_to_end_graph_identical(kind, n, R, L, C, steps):
+    dim = 96 if kind == "f32" else 128
+    data = make_data(kind, n, dim, seed=17)
+    res = D.vamana_build(data, R, L, C, steps)
+    og, od, om = O.vnew2_build(data, R, L, C, steps)
+    assert res.medoid == om
+    assert np.array_equal(res.degree, od)
+    assert np.array_equal(res.graph, og)
+
+
+def test_sort_pairs_and_scan():
+    rng = np.random.default_rng(3)
+    for n, bits in [(1, 8), (4095, 12), (4097, 17), (300000, 20), (70000, 24)]:
+        keys = rng.integers(0, 1 << bits, n).astype(np.uint32)
+        vals = np.arange(n, dtype=np.uint32)
+        ok, ov = D.stage_sort_pairs(keys, vals, bits)
+        order = np.argsort(keys, kind="stable")
+        assert np.array_equal(ok, keys[order])
+        assert np.array_equal(ov, vals[order])
+    for n in (1, 4096, 4097, 5_000_000):
+        x = rng.integers(0, 100, n).astype(np.uint32)
+        ex = np.concatenate([[0], np.cumsum(x, dtype=np.uint64)[:-1]]).astype(np.uint32)
+        assert np.array_equal(D.stage_scan(x), ex)
