@@ -1,0 +1,95 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the
+headers declare with the reference's struct layout, rejects bad parameters
+before touching the device, and the synthetic generators are deterministic."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import dance_amd as D
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    names = set()
+    for h in ("gpu_vamana_builder.h", "dance_hip.h"):
+        text = open(os.path.join(ROOT, "include", h)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"\b([a-z_0-9]+)\s*\(", text):
+            n = m.group(1)
+            if n.startswith(("gpu_vamana", "dance_")):
+                names.add(n)
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = D.lib()
+    declared = header_functions()
+    assert declared == set(D.EXPORTS)
+    out = subprocess.run(["nm", "-D", "--defined-only", D.LIB_PATH], capture_output=True, text=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    missing = declared - exported
+    assert not missing, missing
+    for n in declared:
+        getattr(lib, n)
+
+
+def test_stats_struct_layout():
+    assert C.sizeof(D.GPUVamanaStats) == 120
+    assert D.GPUVamanaStats.distance_computations.offset == 56
+    assert D.GPUVamanaStats.reverse_csr_seconds.offset == 104
+    assert D.GPUVamanaStats.selective_active_nodes.offset == 112
+
+
+def test_parameter_errors_return_minus_one():
+    lib = D.lib()
+    x = np.zeros((16, 8), np.float32)
+    g = np.zeros((16, 8), np.uint32)
+    deg = np.zeros(16, np.uint32)
+    u32p = C.POINTER(C.c_uint32)
+    gp, dp = g.ctypes.data_as(u32p), deg.ctypes.data_as(u32p)
+    # null input, C < R, zero sizes: rejected before any device call
+    assert lib.gpu_vamana_vnew2_build_float(None, 16, 8, 8, 16, 8, 8, gp, dp) == -1
+    assert lib.gpu_vamana_vnew2_build_float(x.ctypes.data, 16, 8, 8, 16, 4, 8, gp, dp) == -1
+    assert lib.gpu_vamana_vnew2_build_float(x.ctypes.data, 0, 8, 8, 16, 8, 8, gp, dp) == -1
+    assert lib.gpu_vamana_vnew2_build(x.ctypes.data, 16, 8, 0, 16, 8, 8, gp, dp) == -1
+    assert lib.gpu_vamana_build_float(x.ctypes.data, 16, 0, 8, 16, 8, 8, gp, dp) == -1
+    assert lib.gpu_vamana_vnew2_build_float(x.ctypes.data, 16, 8, 8, 16, 8, 8, None, dp) == -1
+    assert lib.dance_vamana_build_resident(None, 0, 16, 8, 8, 16, 8, 8, None, None) == -1
+    assert lib.dance_set_profile(b"NOPE") == -1
+
+
+def test_profiles():
+    for p in ("FAST_SMALL", "PRO6000_100M", "FILTERED_PAPER", "QUALITY"):
+        D.set_profile(p)
+        assert D.get_profile() == p
+
+
+def test_synth_deterministic_and_shaped():
+    a = D.synth_f32(42, 0, 5000, 96, 256, 0.3, True)
+    b = D.synth_f32(42, 0, 5000, 96, 256, 0.3, True)
+    assert np.array_equal(a, b)
+    assert np.allclose(np.linalg.norm(a, axis=1), 1.0, atol=1e-5)
+    # rows do not depend on N (each row has its own stream)
+    c = D.synth_f32(42, 0, 100, 96, 256, 0.3, True)
+    assert np.array_equal(a[:100], c)
+    # queries use another stream
+    q = D.synth_f32(42, 1, 100, 96, 256, 0.3, True)
+    assert not np.array_equal(q, c)
+    u = D.synth_u8(42, 0, 3000, 128, 1024, 0.3)
+    assert u.dtype == np.uint8 and u.shape == (3000, 128)
+    assert 40 < u.mean() < 90
+    g = D.synth_f32(42, 0, 20000, 16, 0, 1.0, False)
+    assert abs(g.mean()) < 0.02 and abs(g.std() - 1.0) < 0.02
+
+
+def test_mixture_is_clustered():
+    x = D.synth_f32(42, 0, 4000, 96, 8, 0.3, True)
+    # 8 well-separated components: nearest neighbours are far closer than random pairs
+    d_rand = ((x[:200] - x[200:400]) ** 2).sum(1).mean()
+    d_nn = min(((x[1:] - x[0]) ** 2).sum(1))
+    assert d_nn < 0.5 * d_rand

@@ -1,0 +1,330 @@
+"""Pins the CPU oracle (CPU only; no GPU).
+
+Each oracle function is checked against something it does not share code
+with: closed-form inverses, fp64 evaluations with error bounds, brute force on
+tiny inputs, and independent textbook restatements written here in Python.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+INV = 0xFFFFFFFF
+FMAX = np.finfo(np.float32).max
+M32 = 0xFFFFFFFF
+
+
+# ---------------------------------------------------------------- hashes
+
+def _unxorshift(x, s):
+    # inverse of x ^= x >> s on 32 bits
+    y = x
+    for _ in range(32 // s + 1):
+        y = x ^ (y >> s)
+    return y & M32
+
+
+def _inverse_hash(h):
+    # vnew2.cu:169-177 is xorshift16, *0x7feb352d, xorshift15, *0x846ca68b,
+    # xorshift16; undo each step in reverse order.
+    x = _unxorshift(h, 16)
+    x = (x * pow(0x846CA68B, -1, 1 << 32)) & M32
+    x = _unxorshift(x, 15)
+    x = (x * pow(0x7FEB352D, -1, 1 << 32)) & M32
+    return _unxorshift(x, 16)
+
+
+def test_hash_is_the_documented_bijection():
+    rng = np.random.default_rng(0)
+    xs = [0, 1, 2, 0xFFFFFFFF, 0x80000000] + rng.integers(0, 1 << 32, 2000, dtype=np.uint64).tolist()
+    for x in xs:
+        assert _inverse_hash(O.hash_u32(int(x))) == int(x)
+    assert O.hash_u32(0) == 0
+    # distinct inputs -> distinct outputs (spot check of injectivity)
+    hs = {O.hash_u32(i) for i in range(20000)}
+    assert len(hs) == 20000
+
+
+@pytest.mark.parametrize("N", [2, 3, 7, 1000, 100_003])
+def test_det_neighbor_range_and_bump(N):
+    for node in list(range(min(N, 50))) + [N - 1]:
+        for k in list(range(70)) + [1024, 1031]:
+            v = O.det_neighbor(node, k, N)
+            assert 0 <= v < N and v != node
+            h = O.hash_u32((node * 0x9E3779B1 + k * 0x85EBCA6B + 17) & M32) % N
+            assert v == (h if h != node else (h + 1) % N)
+    assert O.det_neighbor(0, 0, 1) == INV
+
+
+# ---------------------------------------------------------------- distances
+
+@pytest.mark.parametrize("dim", [1, 7, 96, 100, 128, 333])
+def test_distance_f32_within_fp32_bound(dim):
+    rng = np.random.default_rng(dim)
+    x = rng.standard_normal((64, dim)).astype(np.float32)
+    a = rng.integers(0, 64, 500)
+    b = rng.integers(0, 64, 500)
+    got = O.distances(x, a, b).astype(np.float64)
+    exact = ((x[a].astype(np.float64) - x[b].astype(np.float64)) ** 2).sum(1)
+    # |fl(sum) - sum| <= (dim + 2) u sum for a sum of non-negative terms
+    bound = (dim + 3) * 2.0 ** -24 * exact + 1e-30
+    assert np.all(np.abs(got - exact) <= bound)
+    # symmetry (bitwise) and zero self-distance
+    assert np.array_equal(O.distances(x, a, b).view(np.uint32), O.distances(x, b, a).view(np.uint32))
+    assert np.all(O.distances(x, a, a) == 0.0)
+
+
+@pytest.mark.parametrize("dim", [1, 33, 128, 192])
+def test_distance_u8_exact(dim):
+    rng = np.random.default_rng(dim)
+    x = rng.integers(0, 256, (50, dim), dtype=np.uint8)
+    a = rng.integers(0, 50, 300)
+    b = rng.integers(0, 50, 300)
+    exact = ((x[a].astype(np.int64) - x[b].astype(np.int64)) ** 2).sum(1)
+    assert np.array_equal(O.distances(x, a, b), exact.astype(np.float32))
+    # extreme values
+    y = np.zeros((2, dim), np.uint8)
+    y[1] = 255
+    assert O.distance(y, 0, 1) == float(dim * 255 * 255)
+
+
+@pytest.mark.parametrize("dim", [8, 50, 96])
+def test_distance_f16_widened(dim):
+    rng = np.random.default_rng(dim)
+    x = rng.standard_normal((40, dim)).astype(np.float16)
+    a = rng.integers(0, 40, 200)
+    b = rng.integers(0, 40, 200)
+    got = O.distances(x, a, b).astype(np.float64)
+    exact = ((x[a].astype(np.float64) - x[b].astype(np.float64)) ** 2).sum(1)
+    assert np.all(np.abs(got - exact) <= (dim + 3) * 2.0 ** -24 * exact + 1e-30)
+
+
+# ---------------------------------------------------------------- medoid
+
+def test_medoid_matches_fp64_bruteforce():
+    rng = np.random.default_rng(5)
+    N, dim = 600, 24
+    x = rng.standard_normal((N, dim)).astype(np.float32)
+    m, scores, cands = O.medoid(x)
+    nc, ns = min(1024, N), min(4096, N)
+    want_c = np.array([O.hash_u32((w * 9973 + 17) & M32) % N for w in range(nc)])
+    assert np.array_equal(cands, want_c)
+    samples = np.array([O.hash_u32((s * 10007 + 131) & M32) % N for s in range(ns)])
+    x64 = x.astype(np.float64)
+    ref = np.array([((x64[samples[samples != c]] - x64[c]) ** 2).sum() / ns for c in want_c])
+    assert np.allclose(scores, ref, rtol=1e-5)
+    best = ref.min()
+    assert ref[list(want_c).index(m)] <= best * (1 + 1e-5)
+
+
+# ---------------------------------------------------------------- init
+
+def test_init_graph_closed_form():
+    rng = np.random.default_rng(2)
+    N, dim, R, C = 300, 16, 12, 20
+    x = rng.standard_normal((N, dim)).astype(np.float32)
+    s = O.init_graph(x, R, C)
+    for v in range(N):
+        nb = [O.det_neighbor(v, k, N) for k in range(R)]
+        assert s.cur[v].tolist() == nb
+        assert s.work[v, :R].tolist() == nb and np.all(s.work[v, R:] == INV)
+        assert np.array_equal(s.wd[v, :R], O.distances(x, np.full(R, v), np.array(nb)))
+        assert np.all(s.wd[v, R:] == FMAX)
+    assert np.all(s.deg_cur == R) and np.all(s.deg_work == R)
+
+
+# ---------------------------------------------------------------- prune
+
+def random_work_state(x, R, C, seed):
+    rng = np.random.default_rng(seed)
+    N = x.shape[0]
+    s = O.State.empty(N, R, C)
+    ids = rng.integers(0, N, (N, C)).astype(np.uint32)
+    ids[rng.random((N, C)) < 0.08] = INV
+    selfm = rng.random((N, C)) < 0.03
+    ids[selfm] = np.broadcast_to(np.arange(N, dtype=np.uint32)[:, None], (N, C))[selfm]
+    dupm = rng.random((N, C - 1)) < 0.08
+    ids[:, 1:][dupm] = ids[:, :-1][dupm]
+    a = np.repeat(np.arange(N, dtype=np.uint32), C)
+    b = ids.ravel()
+    ok = b < N
+    d = np.full(N * C, FMAX, np.float32)
+    d[ok] = O.distances(x, a[ok], b[ok])
+    d = d.reshape(N, C)
+    d[rng.random((N, C)) < 0.02] = FMAX
+    s.work, s.wd = ids, d
+    s.deg_work = rng.integers(0, C + 1, N).astype(np.uint32)
+    return s
+
+
+def textbook_prune(x, node, ids, ds, R, alpha, min_degree):
+    """RobustPrune (DiskANN Alg. 2) over the candidate slots, selection by
+    (distance, slot); then the nearest-first fill of unused ids."""
+    N = x.shape[0]
+    V = [(float(d), i, int(v)) for i, (v, d) in enumerate(zip(ids, ds))
+         if v != INV and v < N and v != node and np.float32(d) < FMAX]
+    out = []
+    while V:
+        p = min(V)
+        out.append((p[2], p[0]))
+        if len(out) == R:
+            break
+        rest = []
+        for (d, i, v) in V:
+            if v == p[2]:
+                continue
+            dpv = O.distance(x, p[2], v)
+            if p[0] <= d and np.float32(alpha) * np.float32(dpv) <= np.float32(d):
+                continue
+            rest.append((d, i, v))
+        V = rest
+    chosen = {v for v, _ in out}
+    fill = sorted((float(d), i, int(v)) for i, (v, d) in enumerate(zip(ids, ds))
+                  if v != INV and v < N and v != node and np.float32(d) < FMAX)
+    for d, i, v in fill:
+        if len(out) >= min(min_degree, R):
+            break
+        if v in chosen:
+            continue
+        chosen.add(v)
+        out.append((v, d))
+    return out
+
+
+@pytest.mark.parametrize("alpha,min_degree", [(1.0, 0), (1.2, 0), (1.2, 16), (1.5, 64)])
+def test_prune_matches_textbook(alpha, min_degree):
+    rng = np.random.default_rng(9)
+    N, dim, R, C = 200, 12, 16, 40
+    x = rng.standard_normal((N, dim)).astype(np.float32)
+    s0 = random_work_state(x, R, C, seed=4)
+    s = O.prune(x, s0, min_degree, alpha)
+    for v in range(N):
+        deg = min(int(s0.deg_work[v]), C)
+        want = textbook_prune(x, v, s0.work[v, :deg], s0.wd[v, :deg], R, alpha, min_degree)
+        k = int(s.deg_cur[v])
+        assert [int(i) for i in s.cur[v, :k]] == [w for w, _ in want]
+        assert np.all(s.cur[v, k:] == INV)
+        assert np.array_equal(s.wd[v, :k], np.array([d for _, d in want], np.float32))
+        assert s.deg_work[v] == k
+
+
+def test_prune_invariants():
+    rng = np.random.default_rng(1)
+    N, dim, R, C, alpha = 300, 16, 24, 60, 1.2
+    x = rng.standard_normal((N, dim)).astype(np.float32)
+    s0 = random_work_state(x, R, C, seed=8)
+    s = O.prune(x, s0, 0, alpha)
+    for v in range(N):
+        k = int(s.deg_cur[v])
+        out = [int(i) for i in s.cur[v, :k]]
+        assert len(set(out)) == k and v not in out and all(i < N for i in out)
+        d = s.wd[v, :k]
+        assert np.all(np.diff(d) >= 0)  # selection order is nearest first
+        for i in range(k):  # no selected node occludes a later one
+            for j in range(i + 1, k):
+                assert alpha * O.distance(x, out[i], out[j]) > d[j]
+
+
+# ---------------------------------------------------------------- reverse
+
+def test_reverse_csr_is_transpose_with_ascending_sources():
+    rng = np.random.default_rng(3)
+    N, dim, R, C = 400, 8, 10, 24
+    x = rng.standard_normal((N, dim)).astype(np.float32)
+    s0 = random_work_state(x, R, C, seed=5)
+    _, off, ids = O.reverse_merge(x, s0)
+    want = {}
+    for src in range(N):
+        for i in range(min(int(s0.deg_work[src]), R)):
+            t = int(s0.work[src, i])
+            if t != INV and t < N and t != src:
+                want.setdefault(t, []).append(src)
+    for t in range(N):
+        seg = ids[off[t]:off[t + 1]].tolist()
+        assert seg == sorted(want.get(t, []))
+
+
+def textbook_merge(x, t, row, drow, deg, srcs, C):
+    row, drow = list(row), list(drow)
+    for s in srcs:
+        if s == t or s in row[:deg]:
+            continue
+        d = O.distance(x, t, s)
+        if deg < C:
+            row[deg], drow[deg] = s, d
+            deg += 1
+            continue
+        w = int(np.argmax(np.array(drow, np.float32)))  # first index of the max
+        if np.float32(d) < np.float32(drow[w]):
+            row[w], drow[w] = s, d
+    return row, drow, deg
+
+
+def test_reverse_merge_matches_textbook():
+    rng = np.random.default_rng(6)
+    N, dim, R, C = 300, 8, 12, 20
+    x = rng.standard_normal((N, dim)).astype(np.float32)
+    s0 = random_work_state(x, R, C, seed=7)
+    s, off, ids = O.reverse_merge(x, s0)
+    for t in range(N):
+        row, drow, deg = textbook_merge(x, t, s0.work[t].tolist(), s0.wd[t].tolist(),
+                                        min(int(s0.deg_work[t]), C), ids[off[t]:off[t + 1]].tolist(), C)
+        assert s.work[t].tolist() == row
+        assert np.array_equal(s.wd[t], np.array(drow, np.float32))
+        assert int(s.deg_work[t]) == deg
+
+
+# ---------------------------------------------------------------- search
+
+def test_search_invariants():
+    rng = np.random.default_rng(11)
+    N, dim, R, L, C = 800, 16, 16, 40, 32
+    x = rng.standard_normal((N, dim)).astype(np.float32)
+    s0 = O.init_graph(x, R, C)
+    m, _, _ = O.medoid(x)
+    s = O.search(x, s0, L, 24, 1.0, m)
+    for v in range(N):
+        k = int(s.deg_work[v])
+        assert k <= C
+        row = [int(i) for i in s.work[v, :k] if i != INV]
+        assert v not in row
+        # The hashed init may repeat a neighbour; the work row starts as a copy
+        # of the current row, and the online insert never adds a duplicate.
+        cur = [int(i) for i in s0.cur[v]]
+        for i in set(row):
+            assert row.count(i) == 1 or row.count(i) <= cur.count(i)
+        assert np.array_equal(s.wd[v, :k][s.work[v, :k] != INV],
+                              O.distances(x, np.full(len(row), v), np.array(row, np.uint32)))
+        assert np.all(s.work[v, k:] == INV)
+
+
+def test_build_recall_and_cpu_vamana():
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((3000, 32)).astype(np.float32)
+    x /= np.linalg.norm(x, axis=1, keepdims=True)
+    q = rng.standard_normal((200, 32)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=1, keepdims=True)
+    gt, _ = O.bruteforce_knn(x, q, 10)
+    g, deg, m = O.vnew2_build(x, 24, 48, 32, 32)
+    assert np.all(deg <= 24) and m < 3000
+    r1 = O.recall_at_k(O.beam_search(x, g, deg, m, q, 10, 64), gt)
+    g2, deg2, st = O.cpu_vamana_build(x, 24, 48, 1.2)
+    r2 = O.recall_at_k(O.beam_search(x, g2, deg2, st, q, 10, 64), gt)
+    assert r1 > 0.9 and r2 > 0.9
+
+
+def test_bruteforce_knn_exact():
+    rng = np.random.default_rng(13)
+    x = rng.standard_normal((500, 10)).astype(np.float32)
+    q = rng.standard_normal((20, 10)).astype(np.float32)
+    ids, d = O.bruteforce_knn(x, q, 5)
+    full = ((q[:, None, :].astype(np.float64) - x[None].astype(np.float64)) ** 2).sum(2)
+    assert np.array_equal(ids, np.argsort(full, axis=1, kind="stable")[:, :5])
+
+
+def test_build_rejects_bad_parameters():
+    x = np.zeros((10, 4), np.float32)
+    with pytest.raises(ValueError):
+        O.vnew2_build(x, 8, 10, 4, 4)  # C < R
+    with pytest.raises(ValueError):
+        O.vnew2_build(x, 0, 10, 8, 4)
