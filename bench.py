@@ -76,6 +76,8 @@ def main() -> int:
     ap.add_argument("--recall-queries", type=int, default=1000)
     ap.add_argument("--cpu-sample", type=int, default=50_000, help="0 disables the CPU baseline")
     ap.add_argument("--profile", default="QUALITY")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="run one device copy of this size first (HBM counter calibration)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -103,6 +105,15 @@ def main() -> int:
         D.vamana_build_resident(base_t.data_ptr(), dcode, n, cfg["dim"], cfg["R"], cfg["L"], cfg["C"],
                                 cfg["STEPS"], graph_t.data_ptr(), deg_t.data_ptr())
 
+    if args.copy_calibration_mib > 0:
+        nbytes = args.copy_calibration_mib << 20
+        src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: {nbytes} bytes read + {nbytes} bytes written")
+        del src, dst
     for i in range(args.warmup):
         step()
         log(f"warmup {i + 1}/{args.warmup} done")
@@ -175,6 +186,8 @@ def main() -> int:
                                                      "prune_ms", "total_ms")},
         "counters": {k: kp[k] for k in ("search_dist", "insert_dist", "expansions", "vis_skips", "merge_dist",
                                         "prune_dist", "reverse_edges")},
+        "search_cycles": ({k: kp[k] for k in ("cyc_select", "cyc_insert", "cyc_dist", "cyc_pool", "cyc_seed",
+                                              "cyc_total")} if kp["cyc_total"] else None),
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

@@ -15,7 +15,9 @@ from dataclasses import dataclass
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libdance_hip.so")
+# DANCE_HIP_LIB points at another build of the same library (e.g. one compiled
+# with DANCE_SEARCH_TIMING=1); default is the in-tree build.
+LIB_PATH = os.environ.get("DANCE_HIP_LIB", os.path.join(HERE, "libdance_hip.so"))
 
 DTYPE_F32, DTYPE_U8, DTYPE_F16 = 0, 1, 2
 INVALID = 0xFFFFFFFF
@@ -57,6 +59,8 @@ class DanceKernelProfile(C.Structure):
         ("reverse_edges", C.c_uint64), ("touched_rows", C.c_uint64),
         ("search_bytes", C.c_double), ("merge_bytes", C.c_double), ("prune_bytes", C.c_double),
         ("reverse_bytes", C.c_double),
+        ("cyc_select", C.c_uint64), ("cyc_insert", C.c_uint64), ("cyc_dist", C.c_uint64),
+        ("cyc_pool", C.c_uint64), ("cyc_seed", C.c_uint64), ("cyc_total", C.c_uint64),
     ]
 
 

@@ -357,6 +357,8 @@ struct State {
 static uint32_t round64(uint32_t x) { return (x + 63u) / 64u * 64u; }
 
 static uint32_t wave_grid(uint32_t n) { return (n + kWavesPerBlock - 1) / kWavesPerBlock; }
+// Grid for kernels that remap workgroups across XCDs (xcd_block): a multiple of 8.
+static uint32_t xcd_grid(uint32_t n) { return (wave_grid(n) + 7u) / 8u * 8u; }
 
 static int launch_medoid(const Rows& rows, hipStream_t s, float* d_scores, uint32_t* d_cands, uint32_t nc,
                          uint32_t ns) {
@@ -380,11 +382,11 @@ static int launch_init(const Rows& rows, GraphBufs g, hipStream_t s) {
 }
 
 static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t steps, float alpha, uint32_t start,
-                         VCounters* ctr, hipStream_t s) {
+                         const uint32_t* order, VCounters* ctr, hipStream_t s) {
   const int cpl = pick_cpl(rows.rs.nch);
   const uint32_t Cp = round64(g.C);
   const size_t lds = (size_t)kWavesPerBlock * search_lds_words(Cp) * 4;
-  SearchArgs a{rows.rs, g, L, steps, start, alpha, nullptr, ctr};
+  SearchArgs a{rows.rs, g, L, steps, start, alpha, order, ctr};
   if (L > 256) {
     std::fprintf(stderr, "[dance_hip] L=%u exceeds the supported maximum 256\n", L);
     return -1;
@@ -392,22 +394,22 @@ static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t ste
   return with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
     constexpr int DT = decltype(dt)::value, CPL = decltype(c)::value;
     if (L <= 128)
-      hipLaunchKernelGGL((k_search<DT, CPL, 2>), dim3(wave_grid(g.N)), dim3(kBlock), lds, s, a, Cp);
+      hipLaunchKernelGGL((k_search<DT, CPL, 2>), dim3(xcd_grid(g.N)), dim3(kBlock), lds, s, a, Cp);
     else
-      hipLaunchKernelGGL((k_search<DT, CPL, 4>), dim3(wave_grid(g.N)), dim3(kBlock), lds, s, a, Cp);
+      hipLaunchKernelGGL((k_search<DT, CPL, 4>), dim3(xcd_grid(g.N)), dim3(kBlock), lds, s, a, Cp);
     DHIP(hipGetLastError());
     return 0;
   });
 }
 
-static int launch_prune(const Rows& rows, GraphBufs g, uint32_t min_degree, float alpha, VCounters* ctr,
-                        hipStream_t s) {
+static int launch_prune(const Rows& rows, GraphBufs g, uint32_t min_degree, float alpha, const uint32_t* order,
+                        VCounters* ctr, hipStream_t s) {
   const int cpl = pick_cpl(rows.rs.nch);
   const uint32_t Cp = round64(g.C), Rp = round64(g.R);
   const size_t lds = (size_t)kWavesPerBlock * prune_lds_words(Cp, Rp) * 4;
-  PruneArgs a{rows.rs, g, min_degree, alpha, nullptr, ctr};
+  PruneArgs a{rows.rs, g, min_degree, alpha, order, ctr};
   return with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
-    hipLaunchKernelGGL((k_prune<decltype(dt)::value, decltype(c)::value>), dim3(wave_grid(g.N)), dim3(kBlock), lds,
+    hipLaunchKernelGGL((k_prune<decltype(dt)::value, decltype(c)::value>), dim3(xcd_grid(g.N)), dim3(kBlock), lds,
                        s, a, Cp, Rp);
     DHIP(hipGetLastError());
     return 0;
@@ -415,7 +417,7 @@ static int launch_prune(const Rows& rows, GraphBufs g, uint32_t min_degree, floa
 }
 
 struct ReverseWs {
-  DevBuf keys[2], vals[2], offs;
+  DevBuf keys[2], vals[2], offs, order;
   SortWorkspace sort;
   ScanWorkspace scan;
   int alloc(uint32_t N, uint32_t R) {
@@ -449,17 +451,57 @@ static int build_reverse_csr(GraphBufs g, ReverseWs& ws, hipStream_t s, const ui
 }
 
 static int launch_merge(const Rows& rows, GraphBufs g, const uint32_t* offs, const uint32_t* srcs,
-                        const Profile& prof, VCounters* ctr, hipStream_t s) {
+                        const Profile& prof, const uint32_t* order, VCounters* ctr, hipStream_t s) {
   const int cpl = pick_cpl(rows.rs.nch);
   const uint32_t Cp = round64(g.C);
   const size_t lds = (size_t)kWavesPerBlock * merge_lds_words(Cp) * 4;
-  MergeArgs a{rows.rs, g, offs, srcs, prof.heavy_threshold, prof.heavy_sample, nullptr, ctr};
+  MergeArgs a{rows.rs, g, offs, srcs, prof.heavy_threshold, prof.heavy_sample, order, ctr};
   return with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
-    hipLaunchKernelGGL((k_merge<decltype(dt)::value, decltype(c)::value>), dim3(wave_grid(g.N)), dim3(kBlock), lds,
+    hipLaunchKernelGGL((k_merge<decltype(dt)::value, decltype(c)::value>), dim3(xcd_grid(g.N)), dim3(kBlock), lds,
                        s, a, Cp);
     DHIP(hipGetLastError());
     return 0;
   });
+}
+
+// Locality schedule (see k_cells): order[] = vertices sorted by nearest pivot.
+// Pivots are K evenly spaced rows. K comes from DANCE_LOCALITY_CELLS (default
+// 512; 0 disables the schedule). Uses the reverse-sort buffers as scratch.
+static uint32_t locality_cells() {
+  const char* e = std::getenv("DANCE_LOCALITY_CELLS");
+  if (e && e[0]) return (uint32_t)std::strtoul(e, nullptr, 10);
+  return 512;
+}
+
+static int build_schedule(const Rows& rows, ReverseWs& ws, hipStream_t s, const uint32_t** order_out) {
+  const uint32_t N = rows.N;
+  const uint32_t K = std::min(locality_cells(), N);
+  *order_out = nullptr;
+  if (K < 2) return 0;
+  std::vector<uint32_t> piv(K);
+  for (uint32_t k = 0; k < K; ++k) piv[k] = (uint32_t)(((uint64_t)k * N) / K);
+  DevBuf dpiv;
+  DCHECK(dpiv.alloc(K * 4));
+  DHIP(hipMemcpyAsync(dpiv.p, piv.data(), K * 4, hipMemcpyHostToDevice, s));
+  const int cpl = pick_cpl(rows.rs.nch);
+  uint32_t* kb[2] = {ws.keys[0].as<uint32_t>(), ws.keys[1].as<uint32_t>()};
+  uint32_t* vb[2] = {ws.vals[0].as<uint32_t>(), ws.vals[1].as<uint32_t>()};
+  DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
+    const uint32_t waves = (N + 7) / 8;
+    hipLaunchKernelGGL((k_cells<decltype(dt)::value, decltype(c)::value>), dim3(wave_grid(waves)), dim3(kBlock), 0,
+                       s, rows.rs, N, dpiv.as<uint32_t>(), K, kb[0], vb[0]);
+    DHIP(hipGetLastError());
+    return 0;
+  }));
+  int which = 0;
+  DCHECK(radix_sort_pairs(kb, vb, N, bit_length(K - 1), ws.sort, s, &which));
+  // Keep the order in the offsets-sized scratch that is free until the first
+  // reverse step: copy into its own buffer owned by the workspace.
+  DCHECK(ws.order.alloc((size_t)N * 4));
+  DHIP(hipMemcpyAsync(ws.order.p, vb[which], (size_t)N * 4, hipMemcpyDeviceToDevice, s));
+  DHIP(hipStreamSynchronize(s));
+  *order_out = ws.order.as<uint32_t>();
+  return 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -555,6 +597,8 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   if (stats) stats->medoid_seconds = now_sec() - t_med;
 
   DCHECK(launch_init(rows, g, s));
+  const uint32_t* order = nullptr;
+  DCHECK(build_schedule(rows, rws, s, &order));
   DHIP(hipEventRecord(e_init, s));
 
   struct IterEv {
@@ -576,15 +620,15 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     if (verbose())
       std::printf("[gpu_vamana_build] iteration %u / %u, alpha=%.3f\n", it + 1, kIters, (double)alpha);
     DHIP(hipEventRecord(iev[it].s0, s));
-    DCHECK(launch_search(rows, g, L, steps, alpha, start, ctr, s));
+    DCHECK(launch_search(rows, g, L, steps, alpha, start, order, ctr, s));
     DHIP(hipEventRecord(iev[it].s1, s));
     const uint32_t* srcs = nullptr;
     DCHECK(build_reverse_csr(g, rws, s, &srcs));
     DHIP(hipEventRecord(iev[it].r1, s));
-    DCHECK(launch_merge(rows, g, rws.offs.as<uint32_t>(), srcs, prof, ctr, s));
+    DCHECK(launch_merge(rows, g, rws.offs.as<uint32_t>(), srcs, prof, order, ctr, s));
     DHIP(hipEventRecord(iev[it].m1, s));
     const uint32_t md = (it + 1 == kIters) ? kFinalMinDegree : 0u;
-    DCHECK(launch_prune(rows, g, md, alpha, ctr, s));
+    DCHECK(launch_prune(rows, g, md, alpha, order, ctr, s));
     DHIP(hipEventRecord(iev[it].p1, s));
   }
   DHIP(hipStreamSynchronize(s));
@@ -612,6 +656,12 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   p.prune_dist = hc_ctr.prune_dist;
   p.reverse_edges = hc_ctr.reverse_edges;
   p.touched_rows = hc_ctr.touched_rows;
+  p.cyc_select = hc_ctr.cyc_select;
+  p.cyc_insert = hc_ctr.cyc_insert;
+  p.cyc_dist = hc_ctr.cyc_dist;
+  p.cyc_pool = hc_ctr.cyc_pool;
+  p.cyc_seed = hc_ctr.cyc_seed;
+  p.cyc_total = hc_ctr.cyc_total;
   const double V = rows.vbytes();
   p.search_bytes = (double)(p.search_dist + p.insert_dist) * V + (double)p.expansions * (4.0 * R + 4.0) +
                    (double)kIters * N * (V + 4.0 * R + 4.0 + 16.0 * C);
@@ -975,7 +1025,7 @@ int dance_stage_search(const void* h_data, int dtype, uint32_t N, uint32_t dim, 
   StageCtx cx;
   DCHECK(cx.open(h_data, dtype, N, dim));
   DCHECK(upload_state(cx.st, N, R, C, cur, deg_cur, work, deg_work, wd, cx.s));
-  DCHECK(launch_search(cx.rows, cx.st.g(), L, steps, alpha, start, nullptr, cx.s));
+  DCHECK(launch_search(cx.rows, cx.st.g(), L, steps, alpha, start, nullptr, nullptr, cx.s));
   return download_state(cx.st, cur, deg_cur, work, deg_work, wd, cx.s);
 }
 
@@ -997,7 +1047,7 @@ int dance_stage_reverse_merge(const void* h_data, int dtype, uint32_t N, uint32_
   if (offsets) std::memcpy(offsets, off.data(), off.size() * 4);
   if (ids) DCHECK(down(ids, srcs, (size_t)off[N] * 4, cx.s));
   Profile prof{"stage", false, heavy_threshold, heavy_sample};
-  DCHECK(launch_merge(cx.rows, g, rws.offs.as<uint32_t>(), srcs, prof, nullptr, cx.s));
+  DCHECK(launch_merge(cx.rows, g, rws.offs.as<uint32_t>(), srcs, prof, nullptr, nullptr, cx.s));
   return download_state(cx.st, nullptr, nullptr, work, deg_work, wd, cx.s);
 }
 
@@ -1008,7 +1058,7 @@ int dance_stage_prune(const void* h_data, int dtype, uint32_t N, uint32_t dim, u
   StageCtx cx;
   DCHECK(cx.open(h_data, dtype, N, dim));
   DCHECK(upload_state(cx.st, N, R, C, nullptr, nullptr, work, deg_work, wd, cx.s));
-  DCHECK(launch_prune(cx.rows, cx.st.g(), min_degree, alpha, nullptr, cx.s));
+  DCHECK(launch_prune(cx.rows, cx.st.g(), min_degree, alpha, nullptr, nullptr, cx.s));
   return download_state(cx.st, cur, deg_cur, work, deg_work, wd, cx.s);
 }
 

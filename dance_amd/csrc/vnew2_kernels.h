@@ -16,7 +16,21 @@
 
 #include "wave.h"
 
+// Opt-in per-phase cycle counters of the search kernel (the analogue of the
+// reference's ENABLE_SEARCH_PRUNE_TIMING, vnew2.cu:100-102). Off by default.
+#ifndef DANCE_SEARCH_TIMING
+#define DANCE_SEARCH_TIMING 0
+#endif
+
 namespace dance {
+
+__device__ __forceinline__ uint64_t dclock() {
+#if DANCE_SEARCH_TIMING
+  return __builtin_amdgcn_s_memtime();
+#else
+  return 0;
+#endif
+}
 
 constexpr uint32_t kVisBits = 10;
 constexpr uint32_t kVis = 1u << kVisBits;  // visited cache slots per wave
@@ -34,7 +48,9 @@ struct VCounters {
   unsigned long long prune_dist;    // prune pair distances
   unsigned long long reverse_edges; // reverse proposals
   unsigned long long touched_rows;  // targets with at least one reverse edge
-  unsigned long long pad[6];
+  // DANCE_SEARCH_TIMING: cycles in select / online insert / candidate
+  // distances / ordered pool inserts / seeding, summed over waves.
+  unsigned long long cyc_select, cyc_insert, cyc_dist, cyc_pool, cyc_seed, cyc_total;
 };
 
 struct GraphBufs {
@@ -232,19 +248,31 @@ struct SearchArgs {
   VCounters* ctr;
 };
 
-// Per-wave LDS words of the search kernel.
-__host__ __device__ constexpr uint32_t search_lds_words(uint32_t Cp) { return kVis + 4u * Cp + 128u; }
+// Per-wave LDS words of the search kernel: visited cache, work row (ids,
+// dists), candidate batch (ids, dists), occlusion list, victim list (slots,
+// keys, ranked slots).
+__host__ __device__ constexpr uint32_t search_lds_words(uint32_t Cp) { return kVis + 6u * Cp + 128u; }
+
+// Workgroup -> logical block. Workgroups are dispatched round-robin over the 8
+// XCDs; this mapping hands XCD k the contiguous logical range
+// [k*per, (k+1)*per) so each XCD's L2 walks one region of the processing
+// order. nb_pad is the launched grid size, a multiple of 8.
+__device__ __forceinline__ uint32_t xcd_block(uint32_t b, uint32_t nb_pad) {
+  const uint32_t per = nb_pad >> 3;
+  return (b & 7u) * per + (b >> 3);
+}
 
 template <int DT, int CPL, int PS>
 struct SearchWave {
   const SearchArgs& a;
   uint32_t node, lane, grp, sub, Cp;
-  uint32_t *vis, *wid, *lst, *lsa, *lsb;
-  float *wdd, *lsd;
+  uint32_t *vis, *wid, *lst, *lsa, *lsb, *lsr;
+  float *wdd, *lsd, *lsk;
   uint4 av[CPL];
   RegPool<PS> P;
   uint32_t wdeg;
   uint32_t n_search, n_insert, n_skip, n_mut, n_try;
+  uint64_t c_select = 0, c_insert = 0, c_dist = 0, c_pool = 0;
 
   __device__ SearchWave(const SearchArgs& args, uint32_t node_, uint32_t* base, uint32_t Cp_)
       : a(args), node(node_), Cp(Cp_) {
@@ -258,6 +286,8 @@ struct SearchWave {
     lsd = reinterpret_cast<float*>(lst + 64);
     lsa = reinterpret_cast<uint32_t*>(lsd + 64);
     lsb = lsa + Cp;
+    lsk = reinterpret_cast<float*>(lsb + Cp);
+    lsr = reinterpret_cast<uint32_t*>(lsk + Cp);
     n_search = n_insert = n_skip = n_mut = n_try = 0;
   }
 
@@ -275,12 +305,16 @@ struct SearchWave {
     if (n == 0) return;
     if (need) lst[mbcnt64(m)] = c;
     wave_sync();
+    const uint64_t t0 = dclock();
+    const bool full = P.size >= P.L && P.max_pos >= 0;
     batch_dist<DT, CPL>(a.rs, av, lst, lsd, n, grp, sub);
     n_search += n;
+    const uint64_t t1 = dclock();
+    c_dist += t1 - t0;
     const uint32_t ck = lane < n ? lst[lane] : DANCE_INV;
     const float dk = lane < n ? lsd[lane] : FLT_MAX;
     bool keep = lane < n;
-    if (P.size >= P.L && P.max_pos >= 0) keep = keep && dk < P.max_d;
+    if (full) keep = keep && dk < P.max_d;
     uint64_t km = wballot(keep);
     while (km) {
       const int k = ffs64(km);
@@ -289,6 +323,7 @@ struct SearchWave {
     }
     if (need) vis[slot] = c;
     wave_sync();
+    c_pool += dclock() - t1;
   }
 
   // dynamic_robust_insert_C_warp (vnew2.cu:759-877) on the LDS work row.
@@ -315,7 +350,11 @@ struct SearchWave {
       const bool cb = v && dpy > dpx;
       const uint64_t ma = wballot(ca), mb = wballot(cb);
       if (ca) lsa[nA + mbcnt64(ma)] = i;
-      if (cb) lsb[nB + mbcnt64(mb)] = i;
+      if (cb) {
+        const uint32_t k = nB + mbcnt64(mb);
+        lsb[k] = i;
+        lsk[k] = dpy;
+      }
       nA += popc64(ma);
       nB += popc64(mb);
       if (v && dpy > wl) {
@@ -324,20 +363,19 @@ struct SearchWave {
       }
     }
     wave_sync();
-    // Occlusion: exists y with d_py <= d_px and alpha * d(y, x) <= d_px.
+    // Occlusion: exists y with d_py <= d_px and alpha * d(y, x) <= d_px. The
+    // answer does not depend on the order, so stop at the first pass of 8 that
+    // finds an occluder.
     bool occluded = false;
-    for (uint32_t p = 0; p < nA && !occluded; p += 16) {
-      const uint32_t k0 = p + grp, k1 = p + 8 + grp;
-      const bool a0 = k0 < nA, a1 = k1 < nA;
-      const uint32_t y0 = a0 ? wid[lsa[k0]] : 0u, y1 = a1 ? wid[lsa[k1]] : 0u;
-      uint4 b0[CPL], b1[CPL];
+    for (uint32_t p = 0; p < nA && !occluded; p += 8) {
+      const uint32_t k0 = p + grp;
+      const bool a0 = k0 < nA;
+      const uint32_t y0 = a0 ? wid[lsa[k0]] : 0u;
+      uint4 b0[CPL];
       load_row<CPL>(a.rs, y0, a0, sub, b0);
-      load_row<CPL>(a.rs, y1, a1, sub, b1);
       const float d0 = octet_finish<DT, CPL>(xv, b0);
-      const float d1 = octet_finish<DT, CPL>(xv, b1);
-      n_insert += min(16u, nA - p);
-      const bool o = sub == 0 && ((a0 && a.alpha * d0 <= dpx) || (a1 && a.alpha * d1 <= dpx));
-      occluded = wballot(o) != 0;
+      n_insert += min(8u, nA - p);
+      occluded = wballot(sub == 0 && a0 && a.alpha * d0 <= dpx) != 0;
     }
     if (occluded) return;
     // Worst valid entry (largest d_py, lowest slot).
@@ -348,46 +386,35 @@ struct SearchWave {
       wpos = (int)wave_min_u((wp >= 0 && fkey(wl) == WK) ? (uint32_t)wp : 0xFFFFFFFFu);
       wdist = __int_as_float(WK);
     }
-    // Victim: largest d_py among y with d_py > d_px and alpha * d(x, y) <= d_py.
-    int vk = INT_MIN;
-    uint32_t vs = 0xFFFFFFFFu;
-    for (uint32_t p = 0; p < nB; p += 16) {
-      const uint32_t k0 = p + grp, k1 = p + 8 + grp;
-      const bool a0 = k0 < nB, a1 = k1 < nB;
-      const uint32_t s0 = a0 ? lsb[k0] : 0u, s1 = a1 ? lsb[k1] : 0u;
-      const uint32_t y0 = a0 ? wid[s0] : 0u, y1 = a1 ? wid[s1] : 0u;
-      uint4 b0[CPL], b1[CPL];
-      load_row<CPL>(a.rs, y0, a0, sub, b0);
-      load_row<CPL>(a.rs, y1, a1, sub, b1);
-      const float d0 = octet_finish<DT, CPL>(xv, b0);
-      const float d1 = octet_finish<DT, CPL>(xv, b1);
-      n_insert += min(16u, nB - p);
-      if (sub == 0) {
-        if (a0) {
-          const float dpy = wdd[s0];
-          if (a.alpha * d0 <= dpy && dpy == dpy) {
-            const int key = fkey(dpy);
-            if (key > vk || (key == vk && s0 < vs)) {
-              vk = key;
-              vs = s0;
-            }
-          }
+    // Victim: the largest d_py (lowest slot on ties) among y with d_py > d_px
+    // and alpha * d(x, y) <= d_py. Rank the candidates by (d_py desc, slot asc)
+    // and take the first that qualifies, so only a prefix is gathered.
+    int vpos = -1;
+    if (nB > 0) {
+      for (uint32_t k = lane; k < nB; k += 64) {
+        const float dk = lsk[k];
+        const uint32_t sk = lsb[k];
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < nB; ++j) {
+          const float dj = lsk[j];
+          rank += (dj > dk || (dj == dk && lsb[j] < sk)) ? 1u : 0u;
         }
-        if (a1) {
-          const float dpy = wdd[s1];
-          if (a.alpha * d1 <= dpy && dpy == dpy) {
-            const int key = fkey(dpy);
-            if (key > vk || (key == vk && s1 < vs)) {
-              vk = key;
-              vs = s1;
-            }
-          }
-        }
+        lsr[rank] = sk;
+      }
+      wave_sync();
+      for (uint32_t p = 0; p < nB && vpos < 0; p += 8) {
+        const uint32_t k0 = p + grp;
+        const bool a0 = k0 < nB;
+        const uint32_t s0 = a0 ? lsr[k0] : 0u;
+        const uint32_t y0 = a0 ? wid[s0] : 0u;
+        uint4 b0[CPL];
+        load_row<CPL>(a.rs, y0, a0, sub, b0);
+        const float d0 = octet_finish<DT, CPL>(xv, b0);
+        n_insert += min(8u, nB - p);
+        const uint64_t hit = wballot(sub == 0 && a0 && a.alpha * d0 <= wdd[s0]);
+        if (hit) vpos = (int)lsr[p + ((uint32_t)ffs64(hit) >> 3)];
       }
     }
-    const int VK = wave_max_i(vk);
-    int vpos = -1;
-    if (VK != INT_MIN) vpos = (int)wave_min_u(vk == VK ? vs : 0xFFFFFFFFu);
     if (vpos >= 0) {
       if (lane == 0) {
         wid[vpos] = x;
@@ -412,6 +439,7 @@ struct SearchWave {
   }
 
   __device__ void run() {
+    const uint64_t t_run = dclock();
     const GraphBufs& g = a.g;
     const uint32_t N = g.N, R = g.R, C = g.C;
     for (uint32_t i = lane; i < kVis; i += 64) vis[i] = DANCE_INV;
@@ -456,7 +484,10 @@ struct SearchWave {
     process_batch(lane < 8 ? d_det_neighbor(node, lane + 1024u, N) : DANCE_INV);
     const uint32_t max_steps = min(a.steps, a.L);
     uint32_t n_exp = 0;
+    const uint64_t t_seed = dclock() - t_run;
+    (void)t_seed;
     for (uint32_t step = 0; step < max_steps; ++step) {
+      const uint64_t ts0 = dclock();
       const int pos = P.select();
       if (pos < 0) break;
       const uint32_t x = P.get_id(pos);
@@ -468,7 +499,10 @@ struct SearchWave {
       const uint32_t degx = min(g.deg_cur[x], R);
       const size_t xb = (size_t)x * R;
       const uint32_t c0 = lane < degx ? g.cur[xb + lane] : DANCE_INV;
+      const uint64_t ts1 = dclock();
+      c_select += ts1 - ts0;
       robust_insert(x, dx);
+      c_insert += dclock() - ts1;
       process_batch(c0);
       for (uint32_t b = 64; b < degx; b += 64) {
         const uint32_t pidx = b + lane;
@@ -489,6 +523,14 @@ struct SearchWave {
         atomicAdd(&a.ctr->vis_skips, (unsigned long long)n_skip);
         atomicAdd(&a.ctr->insert_mut, (unsigned long long)n_mut);
         atomicAdd(&a.ctr->insert_try, (unsigned long long)n_try);
+#if DANCE_SEARCH_TIMING
+        atomicAdd(&a.ctr->cyc_select, (unsigned long long)c_select);
+        atomicAdd(&a.ctr->cyc_insert, (unsigned long long)c_insert);
+        atomicAdd(&a.ctr->cyc_dist, (unsigned long long)c_dist);
+        atomicAdd(&a.ctr->cyc_pool, (unsigned long long)c_pool);
+        atomicAdd(&a.ctr->cyc_seed, (unsigned long long)t_seed);
+        atomicAdd(&a.ctr->cyc_total, (unsigned long long)(dclock() - t_run));
+#endif
       }
     }
   }
@@ -499,7 +541,7 @@ template <int DT, int CPL, int PS>
 __global__ __launch_bounds__(kBlock) void k_search(SearchArgs a, uint32_t Cp) {
   extern __shared__ uint32_t smem[];
   const uint32_t w = threadIdx.x >> 6;
-  const uint32_t gw = blockIdx.x * kWavesPerBlock + w;
+  const uint32_t gw = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + w;
   if (gw >= a.g.N) return;
   const uint32_t node = a.order ? a.order[gw] : gw;
   SearchWave<DT, CPL, PS> sw(a, node, smem + w * search_lds_words(Cp), Cp);
@@ -527,7 +569,7 @@ template <int DT, int CPL>
 __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint32_t Rp) {
   extern __shared__ uint32_t smem[];
   const uint32_t w = threadIdx.x >> 6;
-  const uint32_t gw = blockIdx.x * kWavesPerBlock + w;
+  const uint32_t gw = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + w;
   const GraphBufs& g = a.g;
   if (gw >= g.N) return;
   const uint32_t node = a.order ? a.order[gw] : gw;
@@ -690,7 +732,7 @@ template <int DT, int CPL>
 __global__ __launch_bounds__(kBlock) void k_merge(MergeArgs a, uint32_t Cp) {
   extern __shared__ uint32_t smem[];
   const uint32_t w = threadIdx.x >> 6;
-  const uint32_t gw = blockIdx.x * kWavesPerBlock + w;
+  const uint32_t gw = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + w;
   const GraphBufs& g = a.g;
   if (gw >= g.N) return;
   const uint32_t t = a.order ? a.order[gw] : gw;
@@ -890,6 +932,41 @@ __global__ __launch_bounds__(kBlock) void k_init(RowSet rs, GraphBufs g) {
     const uint32_t deg = N > 1 ? R : 0u;
     g.deg_cur[node] = deg;
     g.deg_work[node] = deg;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Locality schedule: each vertex's nearest of K pivot rows (one octet per
+// vertex, eight vertices per wave). Vertices sorted by cell make the waves in
+// flight work on neighbouring vertices, whose searches, candidate rows and
+// reverse sources overlap in L2 and the MALL. The schedule only changes the
+// order in which independent vertices are processed, never a result.
+// ---------------------------------------------------------------------------
+template <int DT, int CPL>
+__global__ __launch_bounds__(kBlock) void k_cells(RowSet rs, uint32_t N, const uint32_t* __restrict__ pivots,
+                                                  uint32_t K, uint32_t* __restrict__ cell,
+                                                  uint32_t* __restrict__ vid) {
+  const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;
+  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t v = (blockIdx.x * kWavesPerBlock + w) * 8 + grp;
+  if ((blockIdx.x * kWavesPerBlock + w) * 8 >= N) return;
+  const bool act = v < N;
+  uint4 xv[CPL];
+  load_row<CPL>(rs, act ? v : 0u, act, sub, xv);
+  float best = FLT_MAX;
+  uint32_t bi = 0;
+  for (uint32_t k = 0; k < K; ++k) {
+    uint4 pv[CPL];
+    load_row<CPL>(rs, pivots[k], true, sub, pv);
+    const float d = octet_finish<DT, CPL>(xv, pv);
+    if (d < best) {
+      best = d;
+      bi = k;
+    }
+  }
+  if (act && sub == 0) {
+    cell[v] = bi;
+    vid[v] = v;
   }
 }
 

@@ -7,8 +7,9 @@
 //
 // Canonical arithmetic (shared bit for bit with the CPU oracle):
 //   fp32 / fp16 (widened exactly to fp32): p = fmaf(t, t, p), t = a - b, in
-//   ascending element order within the lane's chunks; then the xor-4/2/1 lane
-//   butterfly ((p0+p4)+(p2+p6)) + ((p1+p5)+(p3+p7)).
+//   ascending element order within the lane's chunks; then the DPP tree
+//   half-row mirror (lane j + lane 7-j), quad swap 2, quad swap 1:
+//   ((p0+p7)+(p2+p5)) + ((p1+p6)+(p3+p4)); every lane of the octet holds it.
 //   uint8: exact integer sum of (a-b)^2, converted to fp32 once.
 // The value is symmetric in (a, b): a-b and b-a differ only in sign.
 #pragma once
@@ -52,20 +53,39 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// DPP controls (gfx9 encoding).
+constexpr int kDppQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <- lane 7-i within 8
+constexpr int kDppRowMirror = 0x140;   // lane i <- lane 15-i within 16
+constexpr int kDppBcast15 = 0x142;     // lane 15 of each row -> next row
+constexpr int kDppBcast31 = 0x143;     // lane 31 -> rows 2 and 3
+
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ int dpp(int old, int v) {
+  return __builtin_amdgcn_update_dpp(old, v, CTRL, ROWS, 0xF, false);
+}
+
+// Wave-wide reductions with DPP; max/min are exact, so the tree shape does not
+// matter. The full result lands in lane 63 and is read back as a scalar.
+template <typename Op>
+__device__ __forceinline__ int wave_reduce_i(int v, int ident, Op op) {
+  v = op(v, dpp<kDppQuadXor1>(ident, v));
+  v = op(v, dpp<kDppQuadXor2>(ident, v));
+  v = op(v, dpp<kDppHalfMirror>(ident, v));
+  v = op(v, dpp<kDppRowMirror>(ident, v));
+  v = op(v, dpp<kDppBcast15, 0xA>(ident, v));
+  v = op(v, dpp<kDppBcast31, 0xC>(ident, v));
+  return __builtin_amdgcn_readlane(v, 63);
+}
 __device__ __forceinline__ int wave_max_i(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
-  return uni_i(v);
+  return wave_reduce_i(v, INT_MIN, [](int a, int b) { return max(a, b); });
 }
 __device__ __forceinline__ int wave_min_i(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
-  return uni_i(v);
+  return wave_reduce_i(v, INT_MAX, [](int a, int b) { return min(a, b); });
 }
 __device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o));
-  return uni_u(v);
+  return (uint32_t)wave_reduce_i((int)v, -1, [](int a, int b) { return (int)min((uint32_t)a, (uint32_t)b); });
 }
 
 // Reference hashes: vnew2.cu:169-191.
@@ -165,22 +185,26 @@ __device__ __forceinline__ int octet_partial_u8(const uint4 (&a)[CPL], const uin
   return (int)(sq - 2u * cr);
 }
 
+// Canonical octet combination of per-lane partial sums (see the header).
+__device__ __forceinline__ float octet_combine(float p) {
+  p += __int_as_float(dpp<kDppHalfMirror>(0, __float_as_int(p)));
+  p += __int_as_float(dpp<kDppQuadXor2>(0, __float_as_int(p)));
+  p += __int_as_float(dpp<kDppQuadXor1>(0, __float_as_int(p)));
+  return p;
+}
+
 // Full distance of a pair held by an octet; every lane of the octet returns it.
 // Must be called by all 64 lanes (the butterfly crosses lanes).
 template <int DT, int CPL>
 __device__ __forceinline__ float octet_finish(const uint4 (&a)[CPL], const uint4 (&b)[CPL]) {
   if constexpr (DT == DANCE_U8) {
     int p = octet_partial_u8<CPL>(a, b);
-    p += __shfl_xor(p, 4);
-    p += __shfl_xor(p, 2);
-    p += __shfl_xor(p, 1);
+    p += dpp<kDppHalfMirror>(0, p);
+    p += dpp<kDppQuadXor2>(0, p);
+    p += dpp<kDppQuadXor1>(0, p);
     return (float)(uint32_t)p;
   } else {
-    float p = octet_partial_f<DT, CPL>(a, b);
-    p += __shfl_xor(p, 4);
-    p += __shfl_xor(p, 2);
-    p += __shfl_xor(p, 1);
-    return p;
+    return octet_combine(octet_partial_f<DT, CPL>(a, b));
   }
 }
 

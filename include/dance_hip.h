@@ -29,6 +29,8 @@ typedef struct DanceKernelProfile {
     uint64_t search_dist, insert_dist, expansions, vis_skips;
     uint64_t merge_dist, prune_dist, reverse_edges, touched_rows;
     double search_bytes, merge_bytes, prune_bytes, reverse_bytes;
+    /* Search-kernel phase cycles (zero unless built with DANCE_SEARCH_TIMING=1). */
+    uint64_t cyc_select, cyc_insert, cyc_dist, cyc_pool, cyc_seed, cyc_total;
 } DanceKernelProfile;
 
 /* Full standard (vnew2) build with the vectors already resident in device

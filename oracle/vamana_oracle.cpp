@@ -65,9 +65,10 @@ inline uint32_t det_neighbor(uint32_t node, uint32_t k, uint32_t N) {
 // Sub-lane j in [0,8) owns chunks j, j+8, j+16, ... and walks its elements in
 // ascending order. fp32 and fp16 (widened exactly to fp32) accumulate
 // p_j = fmaf(t, t, p_j) with t = a_e - b_e rounded to fp32; the eight partials
-// are combined as ((p0+p4)+(p2+p6)) + ((p1+p5)+(p3+p7)), the xor-4/2/1 lane
-// butterfly of the HIP kernels. uint8 sums (a-b)^2 exactly in integers, like
-// the reference's dp4a form xx+yy-2xy (vnew2.cu:268-290), and converts once.
+// are combined as ((p0+p7)+(p2+p5)) + ((p1+p6)+(p3+p4)), the DPP tree of the
+// HIP kernels (half-row mirror, then quad swaps by 2 and by 1). uint8 sums
+// (a-b)^2 exactly in integers, like the reference's dp4a form xx+yy-2xy
+// (vnew2.cu:268-290), and converts once.
 // ---------------------------------------------------------------------------
 inline float half_to_float(uint16_t h) {
   uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
@@ -95,7 +96,7 @@ inline float half_to_float(uint16_t h) {
 }
 
 inline float combine8(const float p[8]) {
-  return ((p[0] + p[4]) + (p[2] + p[6])) + ((p[1] + p[5]) + (p[3] + p[7]));
+  return ((p[0] + p[7]) + (p[2] + p[5])) + ((p[1] + p[6]) + (p[3] + p[4]));
 }
 
 float dist_f32(const float* a, const float* b, uint32_t dim) {
