@@ -173,3 +173,44 @@ def test_sort_pairs_and_scan():
         x = rng.integers(0, 100, n).astype(np.uint32)
         ex = np.concatenate([[0], np.cumsum(x, dtype=np.uint64)[:-1]]).astype(np.uint32)
         assert np.array_equal(D.stage_scan(x), ex)
+
+
+def test_fast_small_profile_fp16_storage():
+    """FAST_SMALL stores float input as fp16 (round to nearest even) and builds
+    on it; the graph equals the oracle's build on the same fp16 rows."""
+    data = make_data("f32", 3000, 96, seed=23)
+    try:
+        D.set_profile("FAST_SMALL")
+        res = D.vamana_build(data, 32, 64, 48, 32)
+    finally:
+        D.set_profile("QUALITY")
+    og, od, om = O.vnew2_build(data.astype(np.float16), 32, 64, 48, 32)
+    assert res.medoid == om
+    assert np.array_equal(res.degree, od)
+    assert np.array_equal(res.graph, og)
+
+
+def test_build_device_handoff():
+    """gpu_vamana_vnew2_build_device_float keeps data/graph/degree on the device
+    and hands ownership to the caller (hipFree)."""
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    hip.hipFree.argtypes = [C.c_void_p]
+    data = make_data("f32", 2000, 96, seed=29)
+    N, R = 2000, 32
+    dd, dg, ddeg = C.c_void_p(), C.c_void_p(), C.c_void_p()
+    rc = D.lib().gpu_vamana_vnew2_build_device_float(data.ctypes.data, N, 96, R, 64, 48, 32, C.byref(dd),
+                                                     C.byref(dg), C.byref(ddeg))
+    assert rc == 0 and dd.value and dg.value and ddeg.value
+    back = np.empty_like(data)
+    graph = np.empty((N, R), np.uint32)
+    deg = np.empty(N, np.uint32)
+    assert hip.hipMemcpy(back.ctypes.data, dd, back.nbytes, 2) == 0
+    assert hip.hipMemcpy(graph.ctypes.data, dg, graph.nbytes, 2) == 0
+    assert hip.hipMemcpy(deg.ctypes.data, ddeg, deg.nbytes, 2) == 0
+    for p in (dd, dg, ddeg):
+        assert hip.hipFree(p) == 0
+    assert np.array_equal(back, data)
+    want = D.vamana_build(data, R, 64, 48, 32)
+    assert np.array_equal(graph, want.graph) and np.array_equal(deg, want.degree)
