@@ -1,7 +1,8 @@
 """dance_amd: MI355X-native (gfx950) GPU Vamana graph construction.
 
-Host-side Python mirror of the reference's builder interface
-(/root/reference/include/gpu_vamana_builder.h). All device work runs in
+Host-side Python mirror of the reference's builder interfaces
+(/root/reference/include/gpu_vamana_builder.h, gpu_vamana_filtered.h; the
+filtered build's helpers live in dance_amd.filtered). All device work runs in
 libdance_hip.so (hand-written HIP kernels); this module only marshals numpy
 arrays and device pointers across the C ABI. There is no CPU fallback: if the
 library is missing, every entry point raises.
@@ -64,6 +65,54 @@ class DanceKernelProfile(C.Structure):
     ]
 
 
+_FILTERED_STATS_FIELDS = (
+    [(n, C.c_double) for n in (
+        "gpu_build_seconds", "label_h2d_seconds", "graph_build_seconds", "diagnostics_seconds", "d2h_seconds",
+        "peak_gpu_mem_gb", "backbone_seconds", "task_generation_seconds", "filtered_search_seconds",
+        "ordinary_search_seconds", "merge_seconds", "forward_prune_seconds", "csr_reverse_seconds",
+        "reverse_prune_seconds", "compaction_seconds")]
+    + [(n, C.c_uint64) for n in (
+        "filtered_search_distance_count", "unfiltered_search_distance_count", "label_check_count",
+        "label_reject_count", "filtered_candidate_count", "unfiltered_candidate_count", "merged_candidate_count",
+        "active_rows", "original_neighbor_count", "filtered_seed_count", "filtered_visited_count",
+        "filtered_visited_reserved_count", "filtered_top_reserved_count", "bridge_reserved_count",
+        "unfiltered_reserved_count", "filtered_reserved_count", "label_occlusion_blocked_count",
+        "geometry_occluded_count", "candidate_rejected_by_label_count", "refill_count",
+        "filtered_prune_reject_count", "universal_label_pass_count", "final_prune_rows", "reverse_edges",
+        "reverse_touched_rows", "filtered_reverse_edges", "filtered_reverse_touched_rows",
+        "filtered_reverse_candidates_kept", "filtered_reverse_pruned_rows")]
+    + [(n, C.c_double) for n in (
+        "avg_common_label_out_degree", "common_label_degree_before_avg", "common_label_degree_after_avg",
+        "active_rows_frac")]
+    + [(n, C.c_uint32) for n in (
+        "low_common_label_degree_count", "low_common_before", "low_common_after", "out_degree_min",
+        "out_degree_max")]
+    + [("out_degree_avg", C.c_double)]
+    + [(n, C.c_uint32) for n in (
+        "common_label_degree_min", "common_label_degree_max", "invalid_neighbor_count", "self_loop_count")]
+    + [("prune_output_degree_avg", C.c_double)]
+    + [(n, C.c_uint32) for n in ("filtered_seed_source", "semantic_stage", "semantic_complete")]
+)
+
+
+class GPUFilteredVamanaStats(C.Structure):
+    """Layout of GPUFilteredVamanaStats (reference include/gpu_vamana_filtered.h:11-77)."""
+
+    _fields_ = _FILTERED_STATS_FIELDS
+
+
+class DanceFilteredProfile(C.Structure):
+    _fields_ = (
+        [(n, C.c_double) for n in ("backbone_ms", "task_search_ms", "row_ms", "reverse_ms", "csr_ms",
+                                   "diagnostics_ms", "total_ms")]
+        + [("rounds", C.c_uint32), ("vector_bytes", C.c_uint32)]
+        + [(n, C.c_uint64) for n in ("task_dist", "union_dist", "work_dist", "prune_dist", "csr_dist",
+                                     "csr_prune_dist", "merged_candidates", "quota_dropped", "reverse_edges",
+                                     "touched_rows", "csr_candidates", "long_lists", "out_edges",
+                                     "common_edges")]
+    )
+
+
 def struct_dict(s: C.Structure) -> dict:
     return {name: getattr(s, name) for name, _ in s._fields_}
 
@@ -81,6 +130,8 @@ EXPORTS = [
     "dance_stage_distances", "dance_stage_medoid", "dance_stage_init", "dance_stage_search",
     "dance_stage_reverse_merge", "dance_stage_prune", "dance_stage_sort_pairs", "dance_stage_scan",
     "dance_synth_f32", "dance_synth_u8",
+    "gpu_vamana_filtered_build_uint8", "gpu_vamana_filtered_build_float", "gpu_vamana_filtered_get_last_stats",
+    "dance_filtered_build", "dance_filtered_build_resident", "dance_get_last_filtered_profile",
 ]
 
 _LIB = None
@@ -137,6 +188,21 @@ def lib() -> C.CDLL:
         L.dance_synth_f32.restype = i32
         L.dance_synth_u8.argtypes = [C.c_uint64, u32, u32, u32, u32, f32, C.POINTER(C.c_uint8)]
         L.dance_synth_u8.restype = i32
+        labels_args = [_u32p, _u32p, u32, _u32p, u32, u32, u32]
+        for name in ("gpu_vamana_filtered_build_uint8", "gpu_vamana_filtered_build_float"):
+            getattr(L, name).argtypes = ([vp, u32, u32, u32, u32, u32, u32, u32, f32] + labels_args
+                                         + [_u32p, _u32p, u32, _u32p, _u32p])
+            getattr(L, name).restype = i32
+        L.gpu_vamana_filtered_get_last_stats.argtypes = [C.POINTER(GPUFilteredVamanaStats)]
+        L.gpu_vamana_filtered_get_last_stats.restype = None
+        L.dance_filtered_build.argtypes = ([vp, i32, u32, u32, u32, u32, u32, u32, u32, f32] + labels_args
+                                           + [u32, _u32p, _u32p])
+        L.dance_filtered_build.restype = i32
+        L.dance_filtered_build_resident.argtypes = ([vp, i32, u32, u32, u32, u32, u32, u32, u32, f32] + labels_args
+                                                    + [vp, vp])
+        L.dance_filtered_build_resident.restype = i32
+        L.dance_get_last_filtered_profile.argtypes = [C.POINTER(DanceFilteredProfile)]
+        L.dance_get_last_filtered_profile.restype = None
         _LIB = L
     return _LIB
 

@@ -1,0 +1,515 @@
+// Host orchestration of the label-filtered build and the C ABI of
+// include/gpu_vamana_filtered.h (+ the dance_filtered_* extensions of
+// include/dance_hip.h).
+//
+// Schedule (gpu_vamana_filtered_build_impl, /root/reference/src/gpu_vamana_filtered.cu:6511-7067,
+// canonical_round0_from_host_backbone_typed, :5663-6483):
+//   labels + postings upload -> random backbone -> task rows ->
+//   3 x (task search -> row kernel (union search, merge, quota, work
+//        distances, forward prune) -> reverse count / scan / fill ->
+//        exact CSR prune) -> diagnostics -> download.
+//
+// Device layout (row-major):
+//   rows      N x stride16 x 16 B    fp16 (float input) or u8 vectors
+//   ga, gb    N x R u32              graph (round input) / forward graph
+//   da, db    N u32                  degrees
+//   tids, td  T x keep               task results (T = total labels)
+//   roff      N+1 u32                reverse CSR offsets; rids <= N*R sources
+//   boff      N+1 u32                scratch offsets of lists > 256 entries
+//   bd, brem  per long-list entry    distances / removed flags
+// Each round reads ga and writes gb (forward), then writes ga (repaired).
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstddef>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "../../include/dance_hip.h"
+#include "../../include/gpu_vamana_filtered.h"
+#include "filtered_kernels.h"
+#include "host_common.h"
+
+static_assert(sizeof(GPUFilteredVamanaStats) == 456, "GPUFilteredVamanaStats layout");
+static_assert(offsetof(GPUFilteredVamanaStats, filtered_search_distance_count) == 120, "layout");
+static_assert(offsetof(GPUFilteredVamanaStats, avg_common_label_out_degree) == 352, "layout");
+static_assert(offsetof(GPUFilteredVamanaStats, out_degree_avg) == 408, "layout");
+static_assert(offsetof(GPUFilteredVamanaStats, prune_output_degree_avg) == 432, "layout");
+static_assert(offsetof(GPUFilteredVamanaStats, semantic_complete) == 448, "layout");
+
+namespace dance {
+namespace {
+
+using namespace filt;
+
+constexpr uint32_t kRounds = 3;         // configured_rounds (:5707)
+constexpr uint32_t kBackboneSeed = 42;  // (:6987)
+constexpr uint32_t kBackboneDegree = 16;
+constexpr uint32_t kStageLabelSync = 6;  // GPU_FILTERED_STAGE_LABEL_SYNC (:65)
+
+std::mutex g_fmu;
+GPUFilteredVamanaStats g_fstats{};
+DanceFilteredProfile g_fprof{};
+
+struct FParams {
+  uint32_t N, dim, R, L, filtered_L, C, STEPS;
+  float alpha;
+  uint32_t total, num_labels, universal, global_start, rounds;
+};
+
+const char* kTag = "[gpu_vamana_filtered]";
+
+// Parameter and label checks of gpu_vamana_filtered_build_impl (:6558-6568),
+// plus offsets consistency (the reference reads out of bounds otherwise).
+int validate(const FParams& p, const uint32_t* off, const uint32_t* lab, const uint32_t* starts) {
+  if (!off || !lab || !starts) {
+    std::fprintf(stderr, "%s null input pointer.\n", kTag);
+    return -1;
+  }
+  if (p.N == 0 || p.dim == 0 || p.R == 0 || p.L == 0 || p.C < p.R) {
+    std::fprintf(stderr, "%s invalid parameters N=%u dim=%u R=%u L=%u C=%u\n", kTag, p.N, p.dim, p.R, p.L, p.C);
+    return -1;
+  }
+  if (p.rounds > kRounds) {
+    std::fprintf(stderr, "%s rounds=%u exceeds %u\n", kTag, p.rounds, kRounds);
+    return -1;
+  }
+  if (off[0] != 0 || off[p.N] != p.total) {
+    std::fprintf(stderr, "%s label offsets must start at 0 and end at total_label_count=%u\n", kTag, p.total);
+    return -1;
+  }
+  for (uint32_t i = 0; i < p.N; ++i)
+    if (off[i + 1] < off[i]) {
+      std::fprintf(stderr, "%s label offsets decrease at point %u\n", kTag, i);
+      return -1;
+    }
+  // The reverse CSR needs 2R entries per point of the work capacity (:5839-5846).
+  if ((uint64_t)p.N * std::min(p.C, kMaxWorkC) < (uint64_t)2 * p.N * p.R) {
+    std::fprintf(stderr, "%s GPU work capacity cannot hold exact reverse CSR\n", kTag);
+    return 1;
+  }
+  return 0;
+}
+
+struct FState {
+  DevBuf off, lab, lpo, lpts, starts, task_rows;
+  DevBuf ga, gb, da, db, tids, td;
+  DevBuf roff, cursor, rids, boff, bd, brem;
+  DevBuf ctr, d32, d64;
+  size_t big_cap = 0;
+};
+
+struct FEvents {
+  std::vector<hipEvent_t> ev;
+  ~FEvents() {
+    for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+  }
+  hipEvent_t mark(hipStream_t s) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    ev.push_back(e);
+    (void)hipEventRecord(e, s);
+    return e;
+  }
+};
+
+float ms_between(hipEvent_t a, hipEvent_t b) {
+  float ms = 0.f;
+  if (a && b && hipEventElapsedTime(&ms, a, b) == hipSuccess) return ms;
+  return 0.f;
+}
+
+uint32_t grid_xcd(uint64_t waves) { return (uint32_t)(((waves + kWaves - 1) / kWaves + 7) / 8 * 8); }
+uint32_t grid_thr(uint64_t n) { return (uint32_t)((n + 255) / 256); }
+
+void peak_mem(double& peak) {
+  size_t fr = 0, tot = 0;
+  if (hipMemGetInfo(&fr, &tot) == hipSuccess) peak = std::max(peak, (double)(tot - fr) / (1024.0 * 1024.0 * 1024.0));
+}
+
+// Runs the build on resident rows; on success st.ga / st.da hold the graph.
+int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, const uint32_t* h_lab,
+                 const uint32_t* h_starts, hipStream_t s, FState& st, GPUFilteredVamanaStats& gs,
+                 DanceFilteredProfile& kp) {
+  const uint32_t N = p.N, R = p.R, T = p.total;
+  const uint32_t work_C = std::min(p.C, kMaxWorkC);
+  const int cpl = pick_cpl(rows.rs.nch);
+  if (cpl < 0) {
+    std::fprintf(stderr, "%s dim=%u is beyond the supported row width\n", kTag, p.dim);
+    return -1;
+  }
+  if ((uint64_t)N * R > 0xFFFFFFFFull) {
+    std::fprintf(stderr, "%s N*R=%llu exceeds 2^32 edges\n", kTag, (unsigned long long)N * R);
+    return -1;
+  }
+  const uint32_t per_label_pool = std::min(p.filtered_L, 32u), per_label_keep = std::min(per_label_pool, 8u);
+  const uint32_t ordinary_keep = std::min(R, p.L), ordinary_pool = std::min(64u, p.filtered_L);
+
+  // Label -> points postings, ascending rows (:5768-5800).
+  const uint32_t nl = std::max(1u, p.num_labels);
+  const double tl = now_sec();
+  std::vector<uint32_t> lpo((size_t)nl + 1, 0);
+  for (uint32_t i = 0; i < T; ++i)
+    if (h_lab[i] < p.num_labels) ++lpo[(size_t)h_lab[i] + 1];
+  for (uint32_t l = 0; l < p.num_labels; ++l) lpo[l + 1] += lpo[l];
+  std::vector<uint32_t> lpts(std::max<size_t>(1, lpo[p.num_labels]), DANCE_INV);
+  {
+    std::vector<uint32_t> cur(lpo.begin(), lpo.end());
+    for (uint32_t r = 0; r < N; ++r)
+      for (uint32_t i = h_off[r]; i < h_off[r + 1]; ++i)
+        if (h_lab[i] < p.num_labels) lpts[cur[h_lab[i]]++] = r;
+  }
+  DCHECK(st.off.alloc((size_t)(N + 1) * 4));
+  DCHECK(st.lab.alloc((size_t)std::max(1u, T) * 4));
+  DCHECK(st.lpo.alloc(lpo.size() * 4));
+  DCHECK(st.lpts.alloc(lpts.size() * 4));
+  DCHECK(st.starts.alloc((size_t)nl * 4));
+  DCHECK(st.task_rows.alloc((size_t)std::max(1u, T) * 4));
+  DHIP(hipMemcpyAsync(st.off.p, h_off, (size_t)(N + 1) * 4, hipMemcpyHostToDevice, s));
+  if (T) DHIP(hipMemcpyAsync(st.lab.p, h_lab, (size_t)T * 4, hipMemcpyHostToDevice, s));
+  DHIP(hipMemcpyAsync(st.lpo.p, lpo.data(), lpo.size() * 4, hipMemcpyHostToDevice, s));
+  DHIP(hipMemcpyAsync(st.lpts.p, lpts.data(), lpts.size() * 4, hipMemcpyHostToDevice, s));
+  DHIP(hipMemcpyAsync(st.starts.p, h_starts, (size_t)nl * 4, hipMemcpyHostToDevice, s));
+  DHIP(hipStreamSynchronize(s));
+  gs.label_h2d_seconds = now_sec() - tl;
+
+  const size_t NR = (size_t)N * R;
+  DCHECK(st.ga.alloc(NR * 4));
+  DCHECK(st.gb.alloc(NR * 4));
+  DCHECK(st.da.alloc((size_t)N * 4));
+  DCHECK(st.db.alloc((size_t)N * 4));
+  DCHECK(st.tids.alloc((size_t)std::max(1u, T) * std::max(1u, per_label_keep) * 4));
+  DCHECK(st.td.alloc((size_t)std::max(1u, T) * std::max(1u, per_label_keep) * 4));
+  DCHECK(st.roff.alloc((size_t)(N + 1) * 4));
+  DCHECK(st.cursor.alloc((size_t)N * 4));
+  DCHECK(st.rids.alloc(std::max<size_t>(1, NR) * 4));
+  DCHECK(st.boff.alloc((size_t)(N + 1) * 4));
+  DCHECK(st.ctr.alloc(kNumCounters * 8));
+  DCHECK(st.d32.alloc(8 * 4));
+  DCHECK(st.d64.alloc(8 * 8));
+  DHIP(hipMemsetAsync(st.ctr.p, 0, kNumCounters * 8, s));
+  unsigned long long* ctr = st.ctr.as<unsigned long long>();
+  ScanWorkspace scan;
+
+  Labels Ld{st.off.as<uint32_t>(), st.lab.as<uint32_t>(), st.lpo.as<uint32_t>(), st.lpts.as<uint32_t>(),
+            st.starts.as<uint32_t>(), p.num_labels, p.universal};
+  uint32_t* ga = st.ga.as<uint32_t>();
+  uint32_t* gb = st.gb.as<uint32_t>();
+  uint32_t* da = st.da.as<uint32_t>();
+  uint32_t* db = st.db.as<uint32_t>();
+  uint32_t* roff = st.roff.as<uint32_t>();
+  uint32_t* boff = st.boff.as<uint32_t>();
+
+  FEvents E;
+  hipEvent_t e0 = E.mark(s);
+  hipLaunchKernelGGL(k_random_graph, dim3(grid_thr(N)), dim3(256), 0, s, N, R,
+                     std::min(std::min(kBackboneDegree, R), N - 1), kBackboneSeed, ga, da);
+  DHIP(hipGetLastError());
+  hipEvent_t e1 = E.mark(s);
+  hipLaunchKernelGGL(k_task_rows, dim3(grid_thr(N)), dim3(256), 0, s, N, Ld.off, st.task_rows.as<uint32_t>());
+  DHIP(hipGetLastError());
+  hipEvent_t e2 = E.mark(s);
+  kp.backbone_ms = ms_between(e0, e1);
+  double task_ms = 0, row_ms = 0, rev_ms = 0, csr_ms = 0;
+  const size_t search_lds = (size_t)kWaves * kSearchLds * 4;
+  const size_t csr_lds = (size_t)kWaves * kCsrLds * 4;
+  uint64_t reverse_edges = 0;
+
+  for (uint32_t round = 0; round < p.rounds; ++round) {
+    const Graph Ga{N, R, ga, da};
+    hipEvent_t r0 = E.mark(s);
+    if (T > 0) {
+      DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
+        hipLaunchKernelGGL((k_task_search<decltype(dt)::value, decltype(c)::value>), dim3(grid_xcd(T)),
+                           dim3(kBlock), search_lds, s, rows.rs, Ga, Ld, st.task_rows.as<const uint32_t>(), T,
+                           per_label_pool, per_label_keep, p.STEPS, st.tids.as<uint32_t>(), st.td.as<float>(), ctr);
+        DHIP(hipGetLastError());
+        return 0;
+      }));
+    }
+    hipEvent_t r1 = E.mark(s);
+    RowArgs A{ordinary_pool, ordinary_keep, p.STEPS, p.global_start, work_C, per_label_keep, p.alpha,
+              st.tids.as<const uint32_t>(), st.td.as<const float>(), gb, db, ctr};
+    DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
+      hipLaunchKernelGGL((k_row<decltype(dt)::value, decltype(c)::value>), dim3(grid_xcd(N)), dim3(kBlock),
+                         search_lds, s, rows.rs, Ga, Ld, A);
+      DHIP(hipGetLastError());
+      return 0;
+    }));
+    hipEvent_t r2 = E.mark(s);
+    // exact reverse CSR of the forward graph
+    DHIP(hipMemsetAsync(roff, 0, (size_t)(N + 1) * 4, s));
+    hipLaunchKernelGGL(k_rev_count, dim3(grid_thr(N)), dim3(256), 0, s, N, R, gb, db, roff);
+    DHIP(hipGetLastError());
+    DCHECK(scan_exclusive(roff, (size_t)N + 1, scan, s));
+    DHIP(hipMemsetAsync(st.cursor.p, 0, (size_t)N * 4, s));
+    hipLaunchKernelGGL(k_rev_fill, dim3(grid_thr(N)), dim3(256), 0, s, N, R, gb, db, roff,
+                       st.cursor.as<uint32_t>(), st.rids.as<uint32_t>());
+    DHIP(hipGetLastError());
+    hipLaunchKernelGGL(k_big_sizes, dim3(grid_thr((uint64_t)N + 1)), dim3(256), 0, s, N, R, db, roff, boff);
+    DHIP(hipGetLastError());
+    DCHECK(scan_exclusive(boff, (size_t)N + 1, scan, s));
+    uint32_t tails[2] = {0, 0};
+    DHIP(hipMemcpyAsync(&tails[0], roff + N, 4, hipMemcpyDeviceToHost, s));
+    DHIP(hipMemcpyAsync(&tails[1], boff + N, 4, hipMemcpyDeviceToHost, s));
+    DHIP(hipStreamSynchronize(s));
+    reverse_edges += tails[0];
+    if (tails[1] > st.big_cap) {
+      DCHECK(st.bd.alloc((size_t)tails[1] * 4));
+      DCHECK(st.brem.alloc((size_t)tails[1]));
+      st.big_cap = tails[1];
+    }
+    hipEvent_t r3 = E.mark(s);
+    const Graph Gb{N, R, gb, db};
+    CsrArgs Cs{p.alpha, roff, st.rids.as<const uint32_t>(), boff, st.bd.as<float>(), st.brem.as<uint8_t>(),
+               ga, da, ctr};
+    DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
+      hipLaunchKernelGGL((k_csr<decltype(dt)::value, decltype(c)::value>), dim3(grid_xcd(N)), dim3(kBlock), csr_lds,
+                         s, rows.rs, Gb, Ld, Cs);
+      DHIP(hipGetLastError());
+      return 0;
+    }));
+    hipEvent_t r4 = E.mark(s);
+    DHIP(hipEventSynchronize(r4));
+    task_ms += ms_between(r0, r1);
+    row_ms += ms_between(r1, r2);
+    rev_ms += ms_between(r2, r3);
+    csr_ms += ms_between(r3, r4);
+    peak_mem(gs.peak_gpu_mem_gb);
+  }
+  if (p.rounds == 0) DHIP(hipStreamSynchronize(s));
+
+  // diagnostics of the final graph
+  hipEvent_t g0 = E.mark(s);
+  const uint32_t init32[8] = {0, 0, 0, 0xFFFFFFFFu, 0, 0xFFFFFFFFu, 0, 0};
+  DHIP(hipMemcpyAsync(st.d32.p, init32, sizeof(init32), hipMemcpyHostToDevice, s));
+  DHIP(hipMemsetAsync(st.d64.p, 0, 8 * 8, s));
+  hipLaunchKernelGGL(k_diagnostics, dim3(grid_thr(N)), dim3(256), 0, s, Graph{N, R, ga, da}, Ld,
+                     st.d32.as<uint32_t>(), st.d64.as<unsigned long long>());
+  DHIP(hipGetLastError());
+  hipEvent_t g1 = E.mark(s);
+  uint32_t h32[8];
+  unsigned long long h64[8], hc[kNumCounters];
+  DHIP(hipMemcpyAsync(h32, st.d32.p, sizeof(h32), hipMemcpyDeviceToHost, s));
+  DHIP(hipMemcpyAsync(h64, st.d64.p, sizeof(h64), hipMemcpyDeviceToHost, s));
+  DHIP(hipMemcpyAsync(hc, st.ctr.p, sizeof(hc), hipMemcpyDeviceToHost, s));
+  DHIP(hipStreamSynchronize(s));
+
+  // Published stats follow the reference's release path (:8648-8718): search
+  // counters are reported as zero there and the candidate counts are the
+  // final edge counts; the device counters go to DanceFilteredProfile.
+  gs.backbone_seconds = kp.backbone_ms * 1e-3;
+  gs.graph_build_seconds = gs.backbone_seconds;
+  gs.task_generation_seconds = ms_between(e1, e2) * 1e-3;
+  gs.filtered_search_seconds = task_ms * 1e-3;
+  gs.ordinary_search_seconds = row_ms * 1e-3;
+  gs.csr_reverse_seconds = rev_ms * 1e-3;
+  gs.reverse_prune_seconds = csr_ms * 1e-3;
+  gs.diagnostics_seconds = ms_between(g0, g1) * 1e-3;
+  gs.invalid_neighbor_count = h32[0];
+  gs.self_loop_count = h32[1];
+  gs.low_common_label_degree_count = h32[2];
+  gs.out_degree_min = h32[3];
+  gs.out_degree_max = h32[4];
+  gs.common_label_degree_min = h32[5];
+  gs.common_label_degree_max = h32[6];
+  gs.out_degree_avg = (double)h64[0] / N;
+  gs.avg_common_label_out_degree = (double)h64[1] / N;
+  gs.label_check_count = h64[2];
+  gs.label_reject_count = h64[3];
+  gs.universal_label_pass_count = h64[4];
+  gs.filtered_candidate_count = h64[1];
+  gs.unfiltered_candidate_count = h64[0];
+  gs.merged_candidate_count = h64[0];
+  gs.final_prune_rows = N;
+  gs.semantic_stage = kStageLabelSync;
+  gs.semantic_complete = 1;
+  peak_mem(gs.peak_gpu_mem_gb);
+
+  kp.rounds = p.rounds;
+  kp.vector_bytes = rows.vbytes();
+  kp.task_search_ms = task_ms;
+  kp.row_ms = row_ms;
+  kp.reverse_ms = rev_ms;
+  kp.csr_ms = csr_ms;
+  kp.diagnostics_ms = ms_between(g0, g1);
+  kp.total_ms = ms_between(e0, g1);
+  kp.task_dist = hc[kTaskDist];
+  kp.union_dist = hc[kUnionDist];
+  kp.work_dist = hc[kWorkDist];
+  kp.prune_dist = hc[kPruneDist];
+  kp.csr_dist = hc[kCsrDist];
+  kp.csr_prune_dist = hc[kCsrPruneDist];
+  kp.merged_candidates = hc[kMergedCands];
+  kp.quota_dropped = hc[kQuotaDropped];
+  kp.reverse_edges = reverse_edges;
+  kp.touched_rows = hc[kTouchedRows];
+  kp.csr_candidates = hc[kCsrCandidates];
+  kp.long_lists = hc[kBigRows];
+  kp.out_edges = h64[0];
+  kp.common_edges = h64[1];
+  if (verbose())
+    std::printf("%s N=%u dim=%u R=%u L=%u FilteredL=%u C=%u labels=%u total=%u rounds=%u total_ms=%.3f\n", kTag, N,
+                p.dim, R, p.L, p.filtered_L, p.C, p.num_labels, T, p.rounds, kp.total_ms);
+  return 0;
+}
+
+struct StreamGuard {
+  hipStream_t s = nullptr;
+  ~StreamGuard() {
+    if (s) (void)hipStreamDestroy(s);
+  }
+};
+
+// Host-input build. src_dtype: DANCE_F32 (searched as fp16), DANCE_U8 or
+// DANCE_F16 (host fp16 rows, used by tests).
+int filtered_host(const void* h_data, int src_dtype, const FParams& p, const uint32_t* off, const uint32_t* lab,
+                  const uint32_t* starts, uint32_t* h_graph, uint32_t* h_degree) {
+  std::lock_guard<std::mutex> lk(g_fmu);
+  g_fstats = GPUFilteredVamanaStats{};
+  g_fprof = DanceFilteredProfile{};
+  const double t0 = now_sec();
+  if (!h_data || !h_graph || !h_degree) {
+    std::fprintf(stderr, "%s null input pointer.\n", kTag);
+    return -1;
+  }
+  if (const int rc = validate(p, off, lab, starts)) return rc;
+  StreamGuard sg;
+  DHIP(hipStreamCreate(&sg.s));
+  hipStream_t s = sg.s;
+  const int store = src_dtype == DANCE_U8 ? DANCE_U8 : DANCE_F16;
+  Rows rows;
+  DCHECK(setup_rows(rows, h_data, false, src_dtype, store, p.N, p.dim, s));
+  DHIP(hipStreamSynchronize(s));
+  GPUFilteredVamanaStats gs{};
+  DanceFilteredProfile kp{};
+  FState st;
+  const int rc = run_filtered(rows, p, off, lab, starts, s, st, gs, kp);
+  if (rc != 0) return rc;
+  const double td = now_sec();
+  DHIP(hipMemcpy(h_graph, st.ga.p, (size_t)p.N * p.R * 4, hipMemcpyDeviceToHost));
+  DHIP(hipMemcpy(h_degree, st.da.p, (size_t)p.N * 4, hipMemcpyDeviceToHost));
+  gs.d2h_seconds = now_sec() - td;
+  gs.gpu_build_seconds = now_sec() - t0;
+  g_fstats = gs;
+  g_fprof = kp;
+  return 0;
+}
+
+FParams make_params(uint32_t N, uint32_t dim, uint32_t R, uint32_t L, uint32_t filtered_L, uint32_t C,
+                    uint32_t STEPS, float alpha, uint32_t total, uint32_t num_labels, uint32_t universal,
+                    uint32_t global_start, uint32_t rounds) {
+  return FParams{N, dim, R, L, filtered_L, C, STEPS, alpha, total, num_labels, universal, global_start, rounds};
+}
+
+}  // namespace
+}  // namespace dance
+
+using namespace dance;
+
+extern "C" {
+
+int gpu_vamana_filtered_build_uint8(const uint8_t* h_data, uint32_t num_points, uint32_t dim, uint32_t R, uint32_t L,
+                                    uint32_t filtered_L, uint32_t C, uint32_t STEPS, float alpha,
+                                    const uint32_t* point_label_offsets, const uint32_t* point_labels,
+                                    uint32_t total_label_count, const uint32_t* label_to_start_id,
+                                    uint32_t num_labels, uint32_t universal_label_id, uint32_t global_start_id,
+                                    const uint32_t* query_anchor_offsets, const uint32_t* query_anchor_ids,
+                                    uint32_t query_anchor_count, uint32_t* h_graph, uint32_t* h_degree) {
+  (void)query_anchor_offsets;
+  (void)query_anchor_ids;
+  (void)query_anchor_count;
+  return filtered_host(h_data, DANCE_U8,
+                       make_params(num_points, dim, R, L, filtered_L, C, STEPS, alpha, total_label_count, num_labels,
+                                   universal_label_id, global_start_id, kRounds),
+                       point_label_offsets, point_labels, label_to_start_id, h_graph, h_degree);
+}
+
+int gpu_vamana_filtered_build_float(const float* h_data, uint32_t num_points, uint32_t dim, uint32_t R, uint32_t L,
+                                    uint32_t filtered_L, uint32_t C, uint32_t STEPS, float alpha,
+                                    const uint32_t* point_label_offsets, const uint32_t* point_labels,
+                                    uint32_t total_label_count, const uint32_t* label_to_start_id,
+                                    uint32_t num_labels, uint32_t universal_label_id, uint32_t global_start_id,
+                                    const uint32_t* query_anchor_offsets, const uint32_t* query_anchor_ids,
+                                    uint32_t query_anchor_count, uint32_t* h_graph, uint32_t* h_degree) {
+  (void)query_anchor_offsets;
+  (void)query_anchor_ids;
+  (void)query_anchor_count;
+  return filtered_host(h_data, DANCE_F32,
+                       make_params(num_points, dim, R, L, filtered_L, C, STEPS, alpha, total_label_count, num_labels,
+                                   universal_label_id, global_start_id, kRounds),
+                       point_label_offsets, point_labels, label_to_start_id, h_graph, h_degree);
+}
+
+void gpu_vamana_filtered_get_last_stats(GPUFilteredVamanaStats* stats) {
+  if (!stats) return;
+  std::lock_guard<std::mutex> lk(g_fmu);
+  *stats = g_fstats;
+}
+
+int dance_filtered_build(const void* h_data, int dtype, uint32_t num_points, uint32_t dim, uint32_t R, uint32_t L,
+                         uint32_t filtered_L, uint32_t C, uint32_t STEPS, float alpha,
+                         const uint32_t* point_label_offsets, const uint32_t* point_labels,
+                         uint32_t total_label_count, const uint32_t* label_to_start_id, uint32_t num_labels,
+                         uint32_t universal_label_id, uint32_t global_start_id, uint32_t rounds, uint32_t* h_graph,
+                         uint32_t* h_degree) {
+  if (dtype != DANCE_F32 && dtype != DANCE_U8 && dtype != DANCE_F16) {
+    std::fprintf(stderr, "[gpu_vamana_filtered] unsupported dtype %d\n", dtype);
+    return -1;
+  }
+  return filtered_host(h_data, dtype,
+                       make_params(num_points, dim, R, L, filtered_L, C, STEPS, alpha, total_label_count, num_labels,
+                                   universal_label_id, global_start_id, rounds),
+                       point_label_offsets, point_labels, label_to_start_id, h_graph, h_degree);
+}
+
+int dance_filtered_build_resident(const void* d_data, int dtype, uint32_t num_points, uint32_t dim, uint32_t R,
+                                  uint32_t L, uint32_t filtered_L, uint32_t C, uint32_t STEPS, float alpha,
+                                  const uint32_t* point_label_offsets, const uint32_t* point_labels,
+                                  uint32_t total_label_count, const uint32_t* label_to_start_id,
+                                  uint32_t num_labels, uint32_t universal_label_id, uint32_t global_start_id,
+                                  uint32_t* d_graph, uint32_t* d_degree) {
+  std::lock_guard<std::mutex> lk(g_fmu);
+  g_fstats = GPUFilteredVamanaStats{};
+  g_fprof = DanceFilteredProfile{};
+  const double t0 = now_sec();
+  if (!d_data || !d_graph || !d_degree) {
+    std::fprintf(stderr, "[gpu_vamana_filtered] null input pointer.\n");
+    return -1;
+  }
+  if (dtype != DANCE_F32 && dtype != DANCE_U8 && dtype != DANCE_F16) {
+    std::fprintf(stderr, "[gpu_vamana_filtered] unsupported dtype %d\n", dtype);
+    return -1;
+  }
+  const FParams p = make_params(num_points, dim, R, L, filtered_L, C, STEPS, alpha, total_label_count, num_labels,
+                                universal_label_id, global_start_id, kRounds);
+  if (const int rc = validate(p, point_label_offsets, point_labels, label_to_start_id)) return rc;
+  StreamGuard sg;
+  DHIP(hipStreamCreate(&sg.s));
+  hipStream_t s = sg.s;
+  Rows rows;
+  DCHECK(setup_rows(rows, d_data, true, dtype, dtype == DANCE_U8 ? DANCE_U8 : DANCE_F16, p.N, p.dim, s));
+  GPUFilteredVamanaStats gs{};
+  DanceFilteredProfile kp{};
+  FState st;
+  const int rc = run_filtered(rows, p, point_label_offsets, point_labels, label_to_start_id, s, st, gs, kp);
+  if (rc != 0) return rc;
+  DHIP(hipMemcpyAsync(d_graph, st.ga.p, (size_t)p.N * p.R * 4, hipMemcpyDeviceToDevice, s));
+  DHIP(hipMemcpyAsync(d_degree, st.da.p, (size_t)p.N * 4, hipMemcpyDeviceToDevice, s));
+  DHIP(hipStreamSynchronize(s));
+  gs.gpu_build_seconds = now_sec() - t0;
+  g_fstats = gs;
+  g_fprof = kp;
+  return 0;
+}
+
+void dance_get_last_filtered_profile(DanceFilteredProfile* profile) {
+  if (!profile) return;
+  std::lock_guard<std::mutex> lk(g_fmu);
+  *profile = g_fprof;
+}
+
+}  // extern "C"

@@ -1,0 +1,916 @@
+// Device kernels of the label-filtered Vamana build ("canonical_v2" release
+// path of /root/reference/src/gpu_vamana_filtered.cu) for gfx950.
+//
+// Work decomposition (one wave64 each):
+//   k_task_search   one (row, label) task: exact-label search, pool <= 32
+//   k_row           one row: union-label search (pool <= 64) -> merge of the
+//                   row's task results, old neighbours and union results ->
+//                   label-quota compaction -> missing distances ->
+//                   FilteredRobustPrune into the forward graph
+//   k_csr           one row of the exact reverse CSR: forward row plus new
+//                   reverse sources -> distances -> FilteredRobustPrune
+// Candidate pools live in VGPRs (slot s = lane s); merged lists of <= 128
+// entries live in two VGPRs per lane (entry i = lane i % 64, slot i / 64).
+// Distances use the octet scheme of wave.h (canonical, bit-exact with the
+// CPU oracle).
+//
+// The visited cache of the searches is a forgetful direct-mapped table in
+// LDS. It is transparent: a repeated candidate has the same distance, so a
+// duplicate insert into the canonical pool is a no-op, and once the pool is
+// full its worst (distance, id) only falls, so a candidate rejected or evicted
+// earlier is rejected again. Label filters are deterministic and every
+// unfiltered insertion (entry points, posting seeds) precedes the filtered
+// traversal, so skipping a cached id never changes the pool.
+#pragma once
+
+#include "wave.h"
+
+namespace dance {
+namespace filt {
+
+constexpr uint32_t kVisBits = 10;
+constexpr uint32_t kVis = 1u << kVisBits;
+constexpr uint32_t kWaves = 4;
+constexpr uint32_t kBlock = 64 * kWaves;
+constexpr uint32_t kMaxWorkC = 128;
+constexpr uint32_t kCsrSlots = 4;  // CSR candidate lists up to 256 entries stay in VGPRs
+constexpr uint32_t kCsrRegMax = 64u * kCsrSlots;
+constexpr uint32_t kRandomAttempts = 1u << 20;
+// LDS words per wave: visited cache + one distance batch (ids, distances).
+constexpr uint32_t kSearchLds = kVis + 128u;
+// LDS words per wave of k_csr: forward row + one distance batch.
+constexpr uint32_t kCsrLds = 64u + 128u;
+
+// Device counters (u64 each).
+enum : uint32_t {
+  kTaskDist = 0,
+  kUnionDist,
+  kWorkDist,
+  kPruneDist,
+  kCsrDist,
+  kCsrPruneDist,
+  kMergedCands,
+  kQuotaDropped,
+  kTouchedRows,
+  kCsrCandidates,
+  kBigRows,
+  kNumCounters
+};
+
+struct Labels {
+  const uint32_t* off;     // N+1: point -> label list offsets
+  const uint32_t* lab;     // label ids per point (sorted, unique)
+  const uint32_t* lpo;     // num_labels+1: label -> posting offsets
+  const uint32_t* lpts;    // postings (points per label, ascending)
+  const uint32_t* starts;  // num_labels: label entry points
+  uint32_t num_labels, universal;
+};
+
+struct Graph {
+  uint32_t N, R;
+  const uint32_t* g;  // N x R
+  const uint32_t* d;  // N
+};
+
+// point_has_exact_label_device (gpu_vamana_filtered.cu:557-573)
+__device__ __forceinline__ bool has_exact(const Labels& L, uint32_t p, uint32_t label) {
+  const uint32_t e = L.off[p + 1];
+  for (uint32_t i = L.off[p]; i < e; ++i) {
+    const uint32_t v = L.lab[i];
+    if (v == label) return true;
+    if (v > label) break;
+  }
+  return false;
+}
+
+// has_common_label_device (gpu_vamana_filtered.cu:495-528); DANCE_INV as the
+// universal label disables the universal rule.
+__device__ __forceinline__ bool has_common(const Labels& L, uint32_t a, uint32_t b, uint32_t universal) {
+  uint32_t i = L.off[a], j = L.off[b];
+  const uint32_t ie = L.off[a + 1], je = L.off[b + 1];
+  while (i < ie && j < je) {
+    const uint32_t x = L.lab[i], y = L.lab[j];
+    if (x == universal || y == universal || x == y) return true;
+    if (x < y)
+      ++i;
+    else
+      ++j;
+  }
+  return false;
+}
+
+// Union-search compatibility (gpu_vamana_filtered.cu:4561-4566): cand carries
+// one of the row's labels exactly.
+__device__ __forceinline__ bool compatible(const Labels& L, uint32_t row, uint32_t cand) {
+  const uint32_t e = L.off[row + 1];
+  for (uint32_t p = L.off[row]; p < e; ++p)
+    if (has_exact(L, cand, L.lab[p])) return true;
+  return false;
+}
+
+// filtered_selected_covers_common_labels (include/filtered_label_coverage.cuh:7-44):
+// every label shared by target and cand is also a label of selected.
+__device__ __forceinline__ bool covers(const Labels& L, uint32_t target, uint32_t selected, uint32_t cand) {
+  uint32_t ti = L.off[target], ci = L.off[cand];
+  const uint32_t te = L.off[target + 1], ce = L.off[cand + 1];
+  while (ti < te && ci < ce) {
+    const uint32_t tl = L.lab[ti], cl = L.lab[ci];
+    if (tl < cl) {
+      ++ti;
+    } else if (cl < tl) {
+      ++ci;
+    } else {
+      if (!has_exact(L, selected, tl)) return false;
+      ++ti;
+      ++ci;
+    }
+  }
+  return true;
+}
+
+// ---------------------------------------------------------------------------
+// Canonical pool (gpu_vamana_filtered.cu:4156-4263): no early reject; the
+// worst entry is the largest (distance, id); selection takes the smallest
+// unexpanded (distance, id) with distance <= FLT_MAX.
+// ---------------------------------------------------------------------------
+struct CanonPool {
+  uint32_t id;
+  float d;
+  uint32_t ex;
+  uint32_t count, cap;
+  int wpos;
+  float wd;
+  uint32_t wid;
+
+  __device__ __forceinline__ void init(uint32_t c) {
+    id = DANCE_INV;
+    d = FLT_MAX;
+    ex = 0;
+    count = 0;
+    cap = c;
+    wpos = -1;
+    wd = -FLT_MAX;
+    wid = 0;
+  }
+  __device__ __forceinline__ void recompute_worst(uint32_t lane) {
+    const bool v = lane < count && d == d;
+    const int M = wave_max_i(v ? fkey(d) : INT_MIN);
+    if (M == INT_MIN) {
+      wpos = -1;
+      wd = -FLT_MAX;
+      wid = 0;
+      return;
+    }
+    const bool tie = v && fkey(d) == M;
+    const uint32_t W = wave_max_u(tie ? id : 0u);
+    wpos = ffs64(wballot(tie && id == W));
+    wd = __int_as_float(M);
+    wid = W;
+  }
+  __device__ __forceinline__ void insert(uint32_t nid, float nd, uint32_t lane) {
+    const uint64_t dm = wballot(lane < count && id == nid);
+    bool changed = false;
+    if (dm) {
+      const int p = ffs64(dm);
+      if (nd < rdlane_f(d, p)) {
+        if ((int)lane == p) {
+          d = nd;
+          ex = 0;
+        }
+        changed = true;
+      }
+    } else if (count < cap) {
+      if (lane == count) {
+        id = nid;
+        d = nd;
+        ex = 0;
+      }
+      ++count;
+      changed = true;
+    } else if (wpos >= 0 && (nd < wd || (nd == wd && nid < wid))) {
+      if ((int)lane == wpos) {
+        id = nid;
+        d = nd;
+        ex = 0;
+      }
+      changed = true;
+    }
+    if (changed) recompute_worst(lane);
+  }
+  // True when (nd, nid) is certainly rejected: the pool is full and the pair
+  // is not below the worst entry (which only falls while the pool is full).
+  __device__ __forceinline__ bool full_reject(float nd, uint32_t nid) const {
+    return count >= cap && wpos >= 0 && !(nd < wd || (nd == wd && nid < wid));
+  }
+  __device__ __forceinline__ int select(uint32_t lane) const {
+    const bool c = lane < count && ex == 0 && d <= FLT_MAX;
+    const int M = wave_min_i(c ? fkey(d) : INT_MAX);
+    if (M == INT_MAX) return -1;
+    const bool tie = c && fkey(d) == M;
+    const uint32_t I = wave_min_u(tie ? id : DANCE_INV);
+    return ffs64(wballot(tie && id == I));
+  }
+};
+
+// Search skeleton shared by the task search and the union search.
+template <int DT, int CPL>
+struct FSearch {
+  RowSet rs;
+  uint32_t N, row, lane, grp, sub;
+  uint32_t* vis;
+  uint32_t* lst;
+  float* lsd;
+  uint4 av[CPL];
+  CanonPool P;
+  uint32_t ndist;
+
+  __device__ __forceinline__ void init(const RowSet& rs_, uint32_t N_, uint32_t row_, uint32_t* lds, uint32_t cap) {
+    rs = rs_;
+    N = N_;
+    row = row_;
+    lane = lane_id();
+    grp = lane >> 3;
+    sub = lane & 7u;
+    vis = lds;
+    lst = lds + kVis;
+    lsd = reinterpret_cast<float*>(lds + kVis + 64);
+    ndist = 0;
+    for (uint32_t i = lane; i < kVis; i += 64) vis[i] = DANCE_INV;
+    load_row<CPL>(rs, row, true, sub, av);
+    P.init(cap);
+    wave_sync();
+  }
+
+  // One batch of up to 64 candidates in insertion order (lane order; DANCE_INV
+  // = no candidate). accept() is the label filter of the current phase.
+  template <typename F>
+  __device__ __forceinline__ void batch(uint32_t c, F&& accept) {
+    const bool v = c < N && c != row;
+    const uint32_t slot = (c * 0x9E3779B1u) >> (32 - kVisBits);
+    const bool seen = v && vis[slot] == c;
+    const bool need = v && !seen && accept(c);
+    const uint64_t m = wballot(need);
+    if (m) {
+      const uint32_t n = popc64(m);
+      if (need) lst[mbcnt64(m)] = c;
+      wave_sync();
+      batch_dist<DT, CPL>(rs, av, lst, lsd, n, grp, sub);
+      ndist += n;
+      const uint32_t ck = lane < n ? lst[lane] : DANCE_INV;
+      const float dk = lane < n ? lsd[lane] : FLT_MAX;
+      uint64_t km = wballot(lane < n && !P.full_reject(dk, ck));
+      while (km) {
+        const int k = ffs64(km);
+        km &= km - 1;
+        P.insert(rdlane_u(ck, k), rdlane_f(dk, k), lane);
+      }
+    }
+    if (v && !seen) vis[slot] = c;
+    wave_sync();
+  }
+
+  template <typename F>
+  __device__ __forceinline__ void neighbours(const Graph& G, uint32_t u, F&& accept) {
+    const uint32_t deg = min(G.d[u], G.R);
+    const size_t b = (size_t)u * G.R;
+    for (uint32_t j = 0; j < deg; j += 64) batch(j + lane < deg ? G.g[b + j + lane] : DANCE_INV, accept);
+  }
+
+  template <typename F>
+  __device__ __forceinline__ void expand(const Graph& G, uint32_t steps, F&& accept) {
+    for (uint32_t step = 0; step < steps; ++step) {
+      const int pos = P.select(lane);
+      if (pos < 0) break;
+      if ((int)lane == pos) P.ex = 1;
+      neighbours(G, rdlane_u(P.id, pos), accept);
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// FilteredRobustPrune (canonical_exact_prune / canonical_exact_prune_csr,
+// gpu_vamana_filtered.cu:4876-4994, 5130-5230) over a list held in VGPRs:
+// entry e*64+lane is (id[e], d[e]); bit e of `rem` marks it removed or absent.
+// Repeatedly selects the smallest (distance, id, index) and removes every
+// remaining candidate c with covers(row, sel, c), D(sel, c) > 0 and
+// alpha * D(sel, c) <= d(c). Lane k < R receives the k-th selected id.
+// ---------------------------------------------------------------------------
+template <int DT, int CPL, int E>
+__device__ __forceinline__ uint32_t prune_regs(const RowSet& rs, const Labels& L, uint32_t row, uint32_t R,
+                                               float alpha, const uint32_t (&id)[E], const float (&d)[E],
+                                               uint32_t rem, uint32_t* lst, float* lsd, uint32_t lane,
+                                               uint32_t& outv, uint32_t& ndist) {
+  const uint32_t grp = lane >> 3, sub = lane & 7u;
+  uint32_t sel = 0;
+  outv = DANCE_INV;
+  while (sel < R) {
+    int bk = INT_MAX;
+    uint32_t bid = DANCE_INV, bix = DANCE_INV;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      if (!((rem >> e) & 1u) && d[e] <= FLT_MAX) {
+        const int k = fkey(d[e]);
+        if (k < bk || (k == bk && id[e] < bid)) {
+          bk = k;
+          bid = id[e];
+          bix = (uint32_t)e * 64u + lane;
+        }
+      }
+    }
+    const int M = wave_min_i(bk);
+    if (M == INT_MAX) break;
+    const uint32_t I = wave_min_u(bk == M ? bid : DANCE_INV);
+    const uint32_t X = wave_min_u(bk == M && bid == I ? bix : DANCE_INV);
+    if (lane == sel) outv = I;
+    if (lane == (X & 63u)) rem |= 1u << (X >> 6);
+    ++sel;
+    uint4 bv[CPL];
+    load_row<CPL>(rs, I, true, sub, bv);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const bool need = !((rem >> e) & 1u) && covers(L, row, I, id[e]);
+      const uint64_t m = wballot(need);
+      if (m) {
+        const uint32_t n = popc64(m), pos = mbcnt64(m);
+        if (need) lst[pos] = id[e];
+        wave_sync();
+        batch_dist<DT, CPL>(rs, bv, lst, lsd, n, grp, sub);
+        ndist += n;
+        if (need) {
+          const float pd = lsd[pos];
+          if (pd > 0.0f && alpha * pd <= d[e]) rem |= 1u << e;
+        }
+        wave_sync();
+      }
+    }
+  }
+  return sel;
+}
+
+// The same prune over a long list in global memory: entry i belongs to lane
+// i % 64, which alone reads and writes its removed flag and distance.
+// ids(i) yields the candidate id of entry i.
+template <int DT, int CPL, typename Ids>
+__device__ __forceinline__ uint32_t prune_mem(const RowSet& rs, const Labels& L, uint32_t row, uint32_t R,
+                                              float alpha, uint32_t n, Ids&& ids, const float* d, uint8_t* rem,
+                                              uint32_t* lst, float* lsd, uint32_t lane, uint32_t& outv,
+                                              uint32_t& ndist) {
+  const uint32_t grp = lane >> 3, sub = lane & 7u;
+  uint32_t sel = 0;
+  outv = DANCE_INV;
+  while (sel < R) {
+    int bk = INT_MAX;
+    uint32_t bid = DANCE_INV, bix = DANCE_INV;
+    for (uint32_t i = lane; i < n; i += 64) {
+      if (rem[i] || !(d[i] <= FLT_MAX)) continue;
+      const int k = fkey(d[i]);
+      const uint32_t c = ids(i);
+      if (k < bk || (k == bk && c < bid)) {
+        bk = k;
+        bid = c;
+        bix = i;
+      }
+    }
+    const int M = wave_min_i(bk);
+    if (M == INT_MAX) break;
+    const uint32_t I = wave_min_u(bk == M ? bid : DANCE_INV);
+    const uint32_t X = wave_min_u(bk == M && bid == I ? bix : DANCE_INV);
+    if (lane == sel) outv = I;
+    if (lane == (X & 63u)) rem[X] = 1;
+    ++sel;
+    uint4 bv[CPL];
+    load_row<CPL>(rs, I, true, sub, bv);
+    for (uint32_t b = 0; b < n; b += 64) {
+      const uint32_t i = b + lane;
+      const uint32_t c = i < n ? ids(i) : DANCE_INV;
+      const bool need = i < n && !rem[i] && covers(L, row, I, c);
+      const uint64_t m = wballot(need);
+      if (!m) continue;
+      const uint32_t cnt = popc64(m), pos = mbcnt64(m);
+      if (need) lst[pos] = c;
+      wave_sync();
+      batch_dist<DT, CPL>(rs, bv, lst, lsd, cnt, grp, sub);
+      ndist += cnt;
+      if (need) {
+        const float pd = lsd[pos];
+        if (pd > 0.0f && alpha * pd <= d[i]) rem[i] = 1;
+      }
+      wave_sync();
+    }
+  }
+  return sel;
+}
+
+// ---------------------------------------------------------------------------
+// Kernels.
+// ---------------------------------------------------------------------------
+
+// filtered_deterministic_random_graph_kernel (gpu_vamana_filtered.cu:716-744):
+// `target` distinct non-self neighbours from a hash stream. The attempt bound
+// only guarantees termination; it is far above what any input needs.
+static __global__ void k_random_graph(uint32_t N, uint32_t R, uint32_t target, uint32_t seed, uint32_t* g,
+                                      uint32_t* deg) {
+  const uint32_t row = blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= N) return;
+  uint32_t* out = g + (size_t)row * R;
+  uint32_t n = 0;
+  for (uint32_t attempt = 0; n < target && attempt < kRandomAttempts; ++attempt) {
+    const uint32_t c = d_hash_u32(row * 0x9e3779b1u ^ seed * 0x85ebca6bu ^ attempt * 0xc2b2ae35u) % N;
+    if (c == row) continue;
+    bool dup = false;
+    for (uint32_t i = 0; i < n && !dup; ++i) dup = out[i] == c;
+    if (!dup) out[n++] = c;
+  }
+  for (uint32_t i = n; i < R; ++i) out[i] = DANCE_INV;
+  deg[row] = n;
+}
+
+// canonical_make_task_rows: task p (a position in the label array) -> its row.
+static __global__ void k_task_rows(uint32_t N, const uint32_t* off, uint32_t* task_rows) {
+  const uint32_t row = blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= N) return;
+  for (uint32_t p = off[row]; p < off[row + 1]; ++p) task_rows[p] = row;
+}
+
+// canonical_filtered_task_search (gpu_vamana_filtered.cu:4265-4426) with the
+// posting anchor off: label entry point and <= 16 posting seeds (unfiltered),
+// then the exact-label traversal; the first `keep` pool slots are the output.
+template <int DT, int CPL>
+__global__ __launch_bounds__(kBlock) void k_task_search(RowSet rs, Graph G, Labels L, const uint32_t* task_rows,
+                                                        uint32_t tasks, uint32_t cap, uint32_t keep,
+                                                        uint32_t steps, uint32_t* out_ids, float* out_d,
+                                                        unsigned long long* ctr) {
+  extern __shared__ uint32_t smem[];
+  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t t = xcd_block(blockIdx.x, gridDim.x) * kWaves + w;
+  if (t >= tasks) return;
+  const uint32_t lane = lane_id();
+  const uint32_t row = task_rows[t], label = L.lab[t];
+  const uint32_t N = G.N;
+  const size_t ob = (size_t)t * keep;
+  if (row >= N || label >= L.num_labels || label == L.universal) {
+    if (lane < keep) {
+      out_ids[ob + lane] = DANCE_INV;
+      out_d[ob + lane] = FLT_MAX;
+    }
+    return;
+  }
+  FSearch<DT, CPL> S;
+  S.init(rs, N, row, smem + w * kSearchLds, cap);
+  auto any = [](uint32_t) { return true; };
+  auto exact = [&](uint32_t c) { return has_exact(L, c, label); };
+  S.batch(lane == 0 ? L.starts[label] : DANCE_INV, any);
+  const uint32_t pb = L.lpo[label], pc = L.lpo[label + 1] - pb;
+  const uint32_t sc = min(16u, pc);
+  S.batch(lane < sc ? L.lpts[pb + d_hash_u32(row + lane * 7919u + label * 17u) % pc] : DANCE_INV, any);
+  S.neighbours(G, row, exact);
+  S.expand(G, steps, exact);
+  if (lane < keep) {
+    const bool h = lane < S.P.count;
+    out_ids[ob + lane] = h ? S.P.id : DANCE_INV;
+    out_d[ob + lane] = h ? S.P.d : FLT_MAX;
+  }
+  if (ctr && lane == 0) atomicAdd(ctr + kTaskDist, (unsigned long long)S.ndist);
+}
+
+struct RowArgs {
+  uint32_t ocap, okeep, steps, global_start, C, tkeep;
+  float alpha;
+  const uint32_t* task_ids;
+  const float* task_d;
+  uint32_t* gout;  // N x R forward graph
+  uint32_t* dout;  // N
+  unsigned long long* ctr;
+};
+
+// Merged candidate list of one row: entry i in lane i % 64, slot i / 64.
+struct MList {
+  uint32_t id0, id1;
+  float d0, d1;
+  uint32_t count;
+  // canonical_merge_one_warp (gpu_vamana_filtered.cu:4672-4701): skip invalid,
+  // self and overflow; a duplicate keeps the smaller distance; else append.
+  __device__ __forceinline__ void merge_one(uint32_t c, float dist, uint32_t row, uint32_t N, uint32_t C,
+                                            uint32_t lane) {
+    if (c >= N || c == row || count >= C) return;
+    const uint64_t m0 = wballot(lane < count && id0 == c);
+    const uint64_t m1 = count > 64 ? wballot(lane + 64 < count && id1 == c) : 0ull;
+    if (m0 | m1) {
+      if (m0) {
+        if ((int)lane == ffs64(m0) && dist < d0) d0 = dist;
+      } else {
+        if ((int)lane == ffs64(m1) && dist < d1) d1 = dist;
+      }
+      return;
+    }
+    if (lane == (count & 63u)) {
+      if (count < 64) {
+        id0 = c;
+        d0 = dist;
+      } else {
+        id1 = c;
+        d1 = dist;
+      }
+    }
+    ++count;
+  }
+  // Runs merge_one over the lanes set in `m`, in lane order.
+  __device__ __forceinline__ void merge_lanes(uint64_t m, uint32_t c, float dist, uint32_t row, uint32_t N,
+                                              uint32_t C, uint32_t lane) {
+    while (m && count < C) {
+      const int k = ffs64(m);
+      m &= m - 1;
+      merge_one(rdlane_u(c, k), rdlane_f(dist, k), row, N, C, lane);
+    }
+  }
+};
+
+// One row of a canonical round: canonical_ordinary_search restricted to
+// compatible candidates (gpu_vamana_filtered.cu:4529-4670),
+// canonical_merge_candidates with the label quota (:4703-4842),
+// canonical_compute_work_distances (:4844-4871) and canonical_exact_prune
+// (:4876-4994) fused; the merged list never leaves the wave.
+template <int DT, int CPL>
+__global__ __launch_bounds__(kBlock) void k_row(RowSet rs, Graph G, Labels L, RowArgs A) {
+  extern __shared__ uint32_t smem[];
+  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t row = xcd_block(blockIdx.x, gridDim.x) * kWaves + w;
+  const uint32_t N = G.N, R = G.R;
+  if (row >= N) return;
+  const uint32_t lane = lane_id();
+  uint32_t* lds = smem + w * kSearchLds;
+  const uint32_t lb = L.off[row], le = L.off[row + 1];
+
+  // 1. union-label search: label entry points and posting seeds unfiltered,
+  //    then the global start and the traversal restricted to compatible ids
+  FSearch<DT, CPL> S;
+  S.init(rs, N, row, lds, A.ocap);
+  auto any = [](uint32_t) { return true; };
+  auto compat = [&](uint32_t c) { return compatible(L, row, c); };
+  for (uint32_t p = lb; p < le; ++p) {
+    const uint32_t label = L.lab[p];
+    if (label >= L.num_labels) continue;
+    S.batch(lane == 0 ? L.starts[label] : DANCE_INV, any);
+    const uint32_t pb = L.lpo[label], pc = L.lpo[label + 1] - pb;
+    const uint32_t sc = min(64u, pc);
+    S.batch(lane < sc ? L.lpts[pb + d_hash_u32(row + lane * 7919u + label * 17u) % pc] : DANCE_INV, any);
+  }
+  S.batch(lane == 0 ? A.global_start : DANCE_INV, compat);
+  S.neighbours(G, row, compat);
+  S.expand(G, A.steps, compat);
+  const bool oh = lane < A.okeep && lane < S.P.count;
+  const uint32_t o_id = oh ? S.P.id : DANCE_INV;
+  const float o_d = oh ? S.P.d : FLT_MAX;
+  uint32_t ndist_prune = 0, ndist_work = 0;
+  const uint32_t ndist_union = S.ndist;
+
+  // 2. merge: task results, old label-sharing neighbours, union results
+  MList M;
+  M.id0 = M.id1 = DANCE_INV;
+  M.d0 = M.d1 = FLT_MAX;
+  M.count = 0;
+  const uint32_t C = A.C;
+  {
+    const size_t tb = (size_t)lb * A.tkeep, te = (size_t)le * A.tkeep;
+    for (size_t b = tb; b < te && M.count < C; b += 64) {
+      const bool in = b + lane < te;
+      const uint32_t c = in ? A.task_ids[b + lane] : DANCE_INV;
+      const float dd = in ? A.task_d[b + lane] : FLT_MAX;
+      M.merge_lanes(wballot(c < N && c != row), c, dd, row, N, C, lane);
+    }
+    const uint32_t deg = min(G.d[row], R);
+    const uint32_t c = lane < deg ? G.g[(size_t)row * R + lane] : DANCE_INV;
+    const bool ok = c < N && c != row && has_common(L, row, c, DANCE_INV);
+    M.merge_lanes(wballot(ok), c, FLT_MAX, row, N, C, lane);
+    M.merge_lanes(wballot(o_id < N && o_id != row), o_id, o_d, row, N, C, lane);
+  }
+
+  // 3. label quota for rows with 1..16 labels: each candidate is assigned to
+  //    its row label of smallest (cardinality, label id) that still has room;
+  //    candidates with no such label are dropped; the order is kept.
+  const uint32_t lc = le - lb;
+  uint32_t count = M.count;
+  if (lc >= 1 && lc <= 16) {
+    uint32_t* rl = lds;        // row labels [16]
+    uint32_t* rk = lds + 16;   // rank of row label q
+    uint32_t* sid = lds + 64;  // compaction staging [128]
+    float* sd = reinterpret_cast<float*>(lds + 192);
+    const uint32_t myl = lane < lc ? L.lab[lb + lane] : DANCE_INV;
+    const uint32_t myc = lane < lc ? (myl < L.num_labels ? L.lpo[myl + 1] - L.lpo[myl] : 0u) : DANCE_INV;
+    // rank by (cardinality, label, position): equal to the reference's
+    // first-minimum choice among the eligible labels
+    uint32_t rank = 0;
+    for (uint32_t q = 0; q < lc; ++q) {
+      const uint32_t ql = rdlane_u(myl, q), qc = rdlane_u(myc, q);
+      rank += (qc < myc || (qc == myc && (ql < myl || (ql == myl && q < lane)))) ? 1u : 0u;
+    }
+    if (lane < lc) {
+      rl[lane] = myl;
+      rk[lane] = rank;
+    }
+    wave_sync();
+    uint32_t quota = (R + lc - 1) / lc;
+    if (quota < A.tkeep) quota = A.tkeep;
+    auto elig = [&](uint32_t c, bool valid) -> uint32_t {
+      uint32_t bits = 0;
+      if (valid)
+        for (uint32_t q = 0; q < lc; ++q)
+          if (has_exact(L, c, rl[q])) bits |= 1u << rk[q];
+      return bits;
+    };
+    const uint32_t e0 = elig(M.id0, lane < count), e1 = elig(M.id1, lane + 64 < count);
+    uint64_t cnt_lo = 0, cnt_hi = 0;  // 8-bit counters per rank (quota <= 64)
+    uint32_t full = 0;
+    uint64_t k0 = 0, k1 = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+      const uint32_t e = rdlane_u(i < 64 ? e0 : e1, (int)(i & 63u)) & ~full;
+      if (!e) continue;
+      const uint32_t r = (uint32_t)__builtin_ctz(e);
+      uint32_t v;
+      if (r < 8) {
+        cnt_lo += 1ull << (8 * r);
+        v = (uint32_t)(cnt_lo >> (8 * r)) & 255u;
+      } else {
+        cnt_hi += 1ull << (8 * (r - 8));
+        v = (uint32_t)(cnt_hi >> (8 * (r - 8))) & 255u;
+      }
+      if (v >= quota) full |= 1u << r;
+      if (i < 64)
+        k0 |= 1ull << i;
+      else
+        k1 |= 1ull << (i - 64);
+    }
+    const uint32_t kept = popc64(k0) + popc64(k1);
+    if ((k0 >> lane) & 1ull) {
+      sid[mbcnt64(k0)] = M.id0;
+      sd[mbcnt64(k0)] = M.d0;
+    }
+    if ((k1 >> lane) & 1ull) {
+      sid[popc64(k0) + mbcnt64(k1)] = M.id1;
+      sd[popc64(k0) + mbcnt64(k1)] = M.d1;
+    }
+    wave_sync();
+    M.id0 = lane < kept ? sid[lane] : DANCE_INV;
+    M.d0 = lane < kept ? sd[lane] : FLT_MAX;
+    M.id1 = lane + 64 < kept ? sid[lane + 64] : DANCE_INV;
+    M.d1 = lane + 64 < kept ? sd[lane + 64] : FLT_MAX;
+    wave_sync();
+    if (A.ctr && lane == 0) atomicAdd(A.ctr + kQuotaDropped, (unsigned long long)(count - kept));
+    count = kept;
+  }
+
+  // 4. distances of entries merged without one
+  uint32_t* lst = lds + kVis;
+  float* lsd = reinterpret_cast<float*>(lds + kVis + 64);
+  uint32_t id[2] = {M.id0, M.id1};
+  float d[2] = {M.d0, M.d1};
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const bool need = (uint32_t)e * 64u + lane < count && d[e] == FLT_MAX;
+    const uint64_t m = wballot(need);
+    if (m) {
+      const uint32_t n = popc64(m), pos = mbcnt64(m);
+      if (need) lst[pos] = id[e];
+      wave_sync();
+      batch_dist<DT, CPL>(rs, S.av, lst, lsd, n, S.grp, S.sub);
+      ndist_work += n;
+      if (need) d[e] = lsd[pos];
+      wave_sync();
+    }
+  }
+
+  // 5. FilteredRobustPrune into the forward graph
+  uint32_t rem = 0;
+  if (lane >= count) rem |= 1u;
+  if (lane + 64 >= count) rem |= 2u;
+  uint32_t outv;
+  const uint32_t sel = prune_regs<DT, CPL, 2>(rs, L, row, R, A.alpha, id, d, rem, lst, lsd, lane, outv, ndist_prune);
+  if (lane < R) A.gout[(size_t)row * R + lane] = lane < sel ? outv : DANCE_INV;
+  if (lane == 0) {
+    A.dout[row] = sel;
+    if (A.ctr) {
+      atomicAdd(A.ctr + kUnionDist, (unsigned long long)ndist_union);
+      atomicAdd(A.ctr + kWorkDist, (unsigned long long)ndist_work);
+      atomicAdd(A.ctr + kPruneDist, (unsigned long long)ndist_prune);
+      atomicAdd(A.ctr + kMergedCands, (unsigned long long)count);
+    }
+  }
+}
+
+// canonical_reverse_count (gpu_vamana_filtered.cu:4996-5016): in-degree per
+// target of the forward graph.
+static __global__ void k_rev_count(uint32_t N, uint32_t R, const uint32_t* g, const uint32_t* deg,
+                                   uint32_t* indeg) {
+  const uint32_t row = blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= N) return;
+  const uint32_t n = min(deg[row], R);
+  for (uint32_t i = 0; i < n; ++i) {
+    const uint32_t t = g[(size_t)row * R + i];
+    if (t < N && t != row) atomicAdd(indeg + t, 1u);
+  }
+}
+
+// canonical_reverse_fill (gpu_vamana_filtered.cu:5018-5034): sources grouped
+// by target, in arbitrary order within a target (the prune's result does not
+// depend on it: live candidate ids are unique).
+static __global__ void k_rev_fill(uint32_t N, uint32_t R, const uint32_t* g, const uint32_t* deg,
+                                  const uint32_t* roff, uint32_t* cursor, uint32_t* rids) {
+  const uint32_t row = blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= N) return;
+  const uint32_t n = min(deg[row], R);
+  for (uint32_t i = 0; i < n; ++i) {
+    const uint32_t t = g[(size_t)row * R + i];
+    if (t < N && t != row) rids[roff[t] + atomicAdd(cursor + t, 1u)] = row;
+  }
+}
+
+// Sizes of the candidate lists that exceed the VGPR capacity (they get
+// global scratch); N+1 entries, the last one 0, ready for an exclusive scan.
+static __global__ void k_big_sizes(uint32_t N, uint32_t R, const uint32_t* deg, const uint32_t* roff,
+                                   uint32_t* big) {
+  const uint32_t row = blockIdx.x * blockDim.x + threadIdx.x;
+  if (row > N) return;
+  if (row == N) {
+    big[N] = 0;
+    return;
+  }
+  const uint32_t in = roff[row + 1] - roff[row];
+  const uint32_t ub = min(deg[row], R) + in;
+  big[row] = (in > 0 && ub > kCsrRegMax) ? ub : 0u;
+}
+
+struct CsrArgs {
+  float alpha;
+  const uint32_t* roff;  // N+1 reverse offsets
+  const uint32_t* rids;  // reverse sources
+  const uint32_t* boff;  // N+1 scratch offsets of long lists
+  float* bd;
+  uint8_t* brem;
+  uint32_t* gout;
+  uint32_t* dout;
+  unsigned long long* ctr;
+};
+
+// canonical_reverse_candidate_count/fill, canonical_csr_candidate_distances
+// and canonical_exact_prune_csr (gpu_vamana_filtered.cu:5036-5230) for one
+// row. The candidate list is the forward row followed by the reverse sources
+// not already in it; entry i is the i-th of that concatenation (duplicates
+// are marked removed instead of compacted away, so live ids stay unique and
+// the selection is unchanged). Rows without reverse sources keep their row.
+template <int DT, int CPL>
+__global__ __launch_bounds__(kBlock) void k_csr(RowSet rs, Graph G, Labels L, CsrArgs A) {
+  extern __shared__ uint32_t smem[];
+  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t row = xcd_block(blockIdx.x, gridDim.x) * kWaves + w;
+  const uint32_t N = G.N, R = G.R;
+  if (row >= N) return;
+  const uint32_t lane = lane_id();
+  const size_t gb = (size_t)row * R;
+  const uint32_t s0 = A.roff[row], s1 = A.roff[row + 1];
+  if (s0 == s1) {
+    if (lane < R) A.gout[gb + lane] = G.g[gb + lane];
+    if (lane == 0) A.dout[row] = G.d[row];
+    return;
+  }
+  uint32_t* fw = smem + w * kCsrLds;
+  uint32_t* lst = fw + 64;
+  float* lsd = reinterpret_cast<float*>(fw + 128);
+  const uint32_t deg = min(G.d[row], R);
+  fw[lane] = lane < deg ? G.g[gb + lane] : DANCE_INV;
+  wave_sync();
+  const uint32_t grp = lane >> 3, sub = lane & 7u;
+  uint4 av[CPL];
+  load_row<CPL>(rs, row, true, sub, av);
+  const uint32_t n = deg + (s1 - s0);
+  const uint32_t* rids = A.rids + s0;
+  auto id_at = [&](uint32_t i) -> uint32_t { return i < deg ? fw[i] : rids[i - deg]; };
+  auto live = [&](uint32_t i, uint32_t c) -> bool {
+    if (i < deg) return true;
+    if (c >= N || c == row) return false;
+    for (uint32_t j = 0; j < deg; ++j)
+      if (fw[j] == c) return false;
+    return true;
+  };
+  uint32_t nd = 0, npd = 0, nlive = 0, outv, sel;
+  if (n <= kCsrRegMax) {
+    uint32_t id[kCsrSlots];
+    float d[kCsrSlots];
+    uint32_t rem = 0;
+#pragma unroll
+    for (int e = 0; e < (int)kCsrSlots; ++e) {
+      const uint32_t i = (uint32_t)e * 64u + lane;
+      const uint32_t c = i < n ? id_at(i) : DANCE_INV;
+      const bool ok = i < n && live(i, c);
+      id[e] = c;
+      d[e] = FLT_MAX;
+      if (!ok) rem |= 1u << e;
+      const uint64_t m = wballot(ok);
+      if (m) {
+        const uint32_t cnt = popc64(m), pos = mbcnt64(m);
+        if (ok) lst[pos] = c;
+        wave_sync();
+        batch_dist<DT, CPL>(rs, av, lst, lsd, cnt, grp, sub);
+        nd += cnt;
+        nlive += cnt;
+        if (ok) d[e] = lsd[pos];
+        wave_sync();
+      }
+    }
+    sel = prune_regs<DT, CPL, (int)kCsrSlots>(rs, L, row, R, A.alpha, id, d, rem, lst, lsd, lane, outv, npd);
+  } else {
+    const uint32_t base = A.boff[row];
+    float* bd = A.bd + base;
+    uint8_t* brem = A.brem + base;
+    for (uint32_t b = 0; b < n; b += 64) {
+      const uint32_t i = b + lane;
+      const uint32_t c = i < n ? id_at(i) : DANCE_INV;
+      const bool ok = i < n && live(i, c);
+      if (i < n) {
+        brem[i] = ok ? 0 : 1;
+        bd[i] = FLT_MAX;
+      }
+      const uint64_t m = wballot(ok);
+      if (!m) continue;
+      const uint32_t cnt = popc64(m), pos = mbcnt64(m);
+      if (ok) lst[pos] = c;
+      wave_sync();
+      batch_dist<DT, CPL>(rs, av, lst, lsd, cnt, grp, sub);
+      nd += cnt;
+      nlive += cnt;
+      if (ok) bd[i] = lsd[pos];
+      wave_sync();
+    }
+    sel = prune_mem<DT, CPL>(rs, L, row, R, A.alpha, n, id_at, bd, brem, lst, lsd, lane, outv, npd);
+  }
+  if (lane < R) A.gout[gb + lane] = lane < sel ? outv : DANCE_INV;
+  if (lane == 0) {
+    A.dout[row] = sel;
+    if (A.ctr) {
+      atomicAdd(A.ctr + kCsrDist, (unsigned long long)nd);
+      atomicAdd(A.ctr + kCsrPruneDist, (unsigned long long)npd);
+      atomicAdd(A.ctr + kTouchedRows, 1ull);
+      atomicAdd(A.ctr + kCsrCandidates, (unsigned long long)nlive);
+      if (n > kCsrRegMax) atomicAdd(A.ctr + kBigRows, 1ull);
+    }
+  }
+}
+
+// filtered_graph_diagnostics_kernel (gpu_vamana_filtered.cu:2716-2774).
+// u32 slots: invalid, self, low_common, deg_min, deg_max, common_min,
+// common_max; u64 slots: out_edges, common_edges, label_checks,
+// label_rejects, universal_passes.
+static __global__ void k_diagnostics(Graph G, Labels L, uint32_t* d32, unsigned long long* d64) {
+  const uint32_t row = blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= G.N) return;
+  const uint32_t deg = G.d[row];
+  uint32_t invalid = 0, self = 0, common = 0, checks = 0, uni = 0;
+  const uint32_t n = min(deg, G.R);
+  for (uint32_t j = 0; j < n; ++j) {
+    const uint32_t nb = G.g[(size_t)row * G.R + j];
+    if (nb >= G.N) {
+      ++invalid;
+      continue;
+    }
+    if (nb == row) {
+      ++self;
+      continue;
+    }
+    ++checks;
+    // has_common with the universal rule, noting universal passes
+    uint32_t i = L.off[row], k = L.off[nb];
+    const uint32_t ie = L.off[row + 1], ke = L.off[nb + 1];
+    while (i < ie && k < ke) {
+      const uint32_t x = L.lab[i], y = L.lab[k];
+      if (x == L.universal || y == L.universal) {
+        ++uni;
+        ++common;
+        break;
+      }
+      if (x == y) {
+        ++common;
+        break;
+      }
+      if (x < y)
+        ++i;
+      else
+        ++k;
+    }
+  }
+  if (invalid) atomicAdd(d32 + 0, invalid);
+  if (self) atomicAdd(d32 + 1, self);
+  if (common < 2) atomicAdd(d32 + 2, 1u);
+  atomicMin(d32 + 3, deg);
+  atomicMax(d32 + 4, deg);
+  atomicMin(d32 + 5, common);
+  atomicMax(d32 + 6, common);
+  atomicAdd(d64 + 0, (unsigned long long)deg);
+  atomicAdd(d64 + 1, (unsigned long long)common);
+  if (checks) {
+    atomicAdd(d64 + 2, (unsigned long long)checks);
+    atomicAdd(d64 + 3, (unsigned long long)(checks - common));
+  }
+  if (uni) atomicAdd(d64 + 4, (unsigned long long)uni);
+}
+
+}  // namespace filt
+}  // namespace dance

@@ -30,7 +30,7 @@ __device__ __forceinline__ uint32_t block_inclusive_scan(uint32_t v, uint32_t* w
 }
 
 // Pass 1: per-tile exclusive scan in place; tile totals to `partial`.
-__global__ __launch_bounds__(kScanThreads) void k_scan_tile(uint32_t* __restrict__ d, size_t n,
+static __global__ __launch_bounds__(kScanThreads) void k_scan_tile(uint32_t* __restrict__ d, size_t n,
                                                             uint32_t* __restrict__ partial) {
   __shared__ uint32_t wsum[4];
   const size_t base = (size_t)blockIdx.x * kScanTile + (size_t)threadIdx.x * kScanItems;
@@ -55,7 +55,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_tile(uint32_t* __restrict
 }
 
 // Pass 3: add the scanned tile offsets.
-__global__ __launch_bounds__(kScanThreads) void k_scan_add(uint32_t* __restrict__ d, size_t n,
+static __global__ __launch_bounds__(kScanThreads) void k_scan_add(uint32_t* __restrict__ d, size_t n,
                                                            const uint32_t* __restrict__ partial) {
   const uint32_t add = partial[blockIdx.x];
   const size_t base = (size_t)blockIdx.x * kScanTile;
@@ -74,7 +74,7 @@ constexpr uint32_t kRadixThreads = 256;
 constexpr uint32_t kRadixItems = 16;
 constexpr uint32_t kRadixTile = kRadixThreads * kRadixItems;  // 4096
 
-__global__ __launch_bounds__(kRadixThreads) void k_radix_hist(const uint32_t* __restrict__ keys, size_t n,
+static __global__ __launch_bounds__(kRadixThreads) void k_radix_hist(const uint32_t* __restrict__ keys, size_t n,
                                                               uint32_t shift, uint32_t num_tiles,
                                                               uint32_t* __restrict__ hist) {
   __shared__ uint32_t h[256];
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(kRadixThreads) void k_radix_hist(const uint32_t* __
   hist[(size_t)threadIdx.x * num_tiles + blockIdx.x] = h[threadIdx.x];
 }
 
-__global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(const uint32_t* __restrict__ keys,
+static __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(const uint32_t* __restrict__ keys,
                                                                  const uint32_t* __restrict__ vals, size_t n,
                                                                  uint32_t shift, uint32_t num_tiles,
                                                                  const uint32_t* __restrict__ hist_scanned,

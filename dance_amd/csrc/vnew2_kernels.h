@@ -66,28 +66,6 @@ __device__ __forceinline__ bool valid_for(uint32_t id, uint32_t N, uint32_t node
   return id != DANCE_INV && id < N && id != node;
 }
 
-// Distances from a cached vector `av` to up to 64 ids lst[0..n) -> lsd[0..n).
-// Two passes of 8 octets are kept in flight. Returns after lsd is visible.
-template <int DT, int CPL>
-__device__ __forceinline__ void batch_dist(const RowSet& rs, const uint4 (&av)[CPL], const uint32_t* lst,
-                                           float* lsd, uint32_t n, uint32_t grp, uint32_t sub) {
-  for (uint32_t p = 0; p < n; p += 16) {
-    const uint32_t k0 = p + grp, k1 = p + 8 + grp;
-    const bool a0 = k0 < n, a1 = k1 < n;
-    const uint32_t id0 = a0 ? lst[k0] : 0u, id1 = a1 ? lst[k1] : 0u;
-    uint4 b0[CPL], b1[CPL];
-    load_row<CPL>(rs, id0, a0, sub, b0);
-    load_row<CPL>(rs, id1, a1, sub, b1);
-    const float d0 = octet_finish<DT, CPL>(av, b0);
-    const float d1 = octet_finish<DT, CPL>(av, b1);
-    if (sub == 0) {
-      if (a0) lsd[k0] = d0;
-      if (a1) lsd[k1] = d1;
-    }
-  }
-  wave_sync();
-}
-
 // ---------------------------------------------------------------------------
 // Register-resident bounded top-L pool (vnew2.cu:520-734).
 // ---------------------------------------------------------------------------
@@ -252,15 +230,6 @@ struct SearchArgs {
 // dists), candidate batch (ids, dists), occlusion list, victim list (slots,
 // keys, ranked slots).
 __host__ __device__ constexpr uint32_t search_lds_words(uint32_t Cp) { return kVis + 6u * Cp + 128u; }
-
-// Workgroup -> logical block. Workgroups are dispatched round-robin over the 8
-// XCDs; this mapping hands XCD k the contiguous logical range
-// [k*per, (k+1)*per) so each XCD's L2 walks one region of the processing
-// order. nb_pad is the launched grid size, a multiple of 8.
-__device__ __forceinline__ uint32_t xcd_block(uint32_t b, uint32_t nb_pad) {
-  const uint32_t per = nb_pad >> 3;
-  return (b & 7u) * per + (b >> 3);
-}
 
 template <int DT, int CPL, int PS>
 struct SearchWave {
@@ -702,7 +671,7 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
 // in ascending source order. k_merge is reverse_merge_csr_kernel
 // (vnew2.cu:1722-1814) over those canonical segments.
 // ---------------------------------------------------------------------------
-__global__ void k_rev_keys(const uint32_t* __restrict__ work, const uint32_t* __restrict__ deg_work, uint32_t N,
+static __global__ void k_rev_keys(const uint32_t* __restrict__ work, const uint32_t* __restrict__ deg_work, uint32_t N,
                            uint32_t R, uint32_t C, uint32_t* __restrict__ keys, uint32_t* __restrict__ vals,
                            uint32_t* __restrict__ indeg) {
   const size_t j = (size_t)blockIdx.x * blockDim.x + threadIdx.x;

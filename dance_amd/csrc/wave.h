@@ -84,8 +84,20 @@ __device__ __forceinline__ int wave_max_i(int v) {
 __device__ __forceinline__ int wave_min_i(int v) {
   return wave_reduce_i(v, INT_MAX, [](int a, int b) { return min(a, b); });
 }
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+  return (uint32_t)wave_reduce_i((int)v, 0, [](int a, int b) { return (int)max((uint32_t)a, (uint32_t)b); });
+}
 __device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
   return (uint32_t)wave_reduce_i((int)v, -1, [](int a, int b) { return (int)min((uint32_t)a, (uint32_t)b); });
+}
+
+// Workgroup -> logical block. Workgroups are dispatched round-robin over the 8
+// XCDs; this mapping hands XCD k the contiguous logical range
+// [k*per, (k+1)*per) so each XCD's L2 walks one region of the processing
+// order. nb_pad is the launched grid size, a multiple of 8.
+__device__ __forceinline__ uint32_t xcd_block(uint32_t b, uint32_t nb_pad) {
+  const uint32_t per = nb_pad >> 3;
+  return (b & 7u) * per + (b >> 3);
 }
 
 // Reference hashes: vnew2.cu:169-191.
@@ -211,3 +223,27 @@ __device__ __forceinline__ float octet_finish(const uint4 (&a)[CPL], const uint4
 // Float ordering keys for wave reductions over non-negative distances.
 // NaN never wins, matching the reference's strict float comparisons.
 __device__ __forceinline__ int fkey(float d) { return __float_as_int(d); }
+
+// Distances from a cached vector `av` to up to 64 ids lst[0..n) -> lsd[0..n).
+// Two passes of 8 octets are kept in flight. Returns after lsd is visible.
+template <int DT, int CPL>
+__device__ __forceinline__ void batch_dist(const RowSet& rs, const uint4 (&av)[CPL], const uint32_t* lst,
+                                           float* lsd, uint32_t n, uint32_t grp, uint32_t sub) {
+  for (uint32_t p = 0; p < n; p += 16) {
+    const uint32_t k0 = p + grp, k1 = p + 8 + grp;
+    const bool a0 = k0 < n, a1 = k1 < n;
+    const uint32_t id0 = a0 ? lst[k0] : 0u, id1 = a1 ? lst[k1] : 0u;
+    uint4 b0[CPL], b1[CPL];
+    load_row<CPL>(rs, id0, a0, sub, b0);
+    load_row<CPL>(rs, id1, a1, sub, b1);
+    const float d0 = octet_finish<DT, CPL>(av, b0);
+    const float d1 = octet_finish<DT, CPL>(av, b1);
+    if (sub == 0) {
+      if (a0) lsd[k0] = d0;
+      if (a1) lsd[k1] = d1;
+    }
+  }
+  wave_sync();
+}
+
+

@@ -1,0 +1,187 @@
+"""Label-filtered GPU Vamana build: Python side of include/gpu_vamana_filtered.h.
+
+Mirrors the reference's filtered builder interface
+(/root/reference/include/gpu_vamana_filtered.h:79-123) and the host glue
+DiskANN runs before calling it (label CSR canonicalisation, label entry
+points, global start; reference integrations/dance-diskann-78256bba.patch:20245-20540).
+All graph work runs in libdance_hip.so; this module marshals arrays.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import (DTYPE_F16, DTYPE_F32, DTYPE_U8, INVALID, DanceFilteredProfile, GPUFilteredVamanaStats, _check,
+               _p, dtype_code, lib, struct_dict)
+
+# Defaults of the reference's release path and of DiskANN's build parameters.
+ROUNDS = 3
+DISKANN_MAXC = 750
+
+
+@dataclass
+class LabelSet:
+    """Per-point label lists in CSR form, sorted ascending without repeats."""
+    offsets: np.ndarray  # N+1 uint32
+    labels: np.ndarray   # total uint32
+    num_labels: int
+
+    @property
+    def n(self) -> int:
+        return self.offsets.shape[0] - 1
+
+    def row(self, i: int) -> np.ndarray:
+        return self.labels[self.offsets[i]:self.offsets[i + 1]]
+
+    def postings(self) -> tuple[np.ndarray, np.ndarray]:
+        """label -> points CSR (points ascending), labels >= num_labels skipped."""
+        rows = np.repeat(np.arange(self.n, dtype=np.uint32), np.diff(self.offsets).astype(np.int64))
+        keep = self.labels < self.num_labels
+        lab, rows = self.labels[keep], rows[keep]
+        order = np.argsort(lab, kind="stable")
+        counts = np.bincount(lab, minlength=self.num_labels)
+        off = np.zeros(self.num_labels + 1, np.uint32)
+        off[1:] = np.cumsum(counts)
+        return off, rows[order].astype(np.uint32)
+
+
+def canonical_labels(rows: list, num_labels: int | None = None) -> LabelSet:
+    """Sorted-unique label CSR from per-point label lists (reference
+    patch:20269-20286 canonicalises DiskANN's label lists the same way)."""
+    offs = np.zeros(len(rows) + 1, np.uint32)
+    flat = []
+    for i, r in enumerate(rows):
+        u = sorted(set(int(x) for x in r))
+        flat.extend(u)
+        offs[i + 1] = offs[i] + len(u)
+    labels = np.asarray(flat, np.uint32)
+    nl = num_labels if num_labels is not None else (int(labels.max()) + 1 if labels.size else 0)
+    return LabelSet(offs, labels, nl)
+
+
+def synth_labels(n: int, vocab: int, min_per: int = 1, max_per: int = 8, zipf_s: float = 1.0,
+                 seed: int = 42) -> LabelSet:
+    """Seeded multi-label workload: a uniform count in [min_per, max_per] per
+    point, labels drawn Zipf(zipf_s) over `vocab` ids (rank r has weight
+    1/(r+1)^s), duplicates within a point removed."""
+    rng = np.random.default_rng(seed)
+    w = 1.0 / np.power(np.arange(1, vocab + 1, dtype=np.float64), zipf_s)
+    cdf = np.cumsum(w / w.sum())
+    counts = rng.integers(min_per, max_per + 1, n)
+    draws = np.searchsorted(cdf, rng.random(int(counts.sum())), side="right").astype(np.int64)
+    draws = np.minimum(draws, vocab - 1)
+    rows_of = np.repeat(np.arange(n, dtype=np.int64), counts)
+    key = np.unique(rows_of * vocab + draws)  # sorted, unique per row
+    rows_u = key // vocab
+    labs = (key % vocab).astype(np.uint32)
+    offs = np.zeros(n + 1, np.uint32)
+    offs[1:] = np.cumsum(np.bincount(rows_u, minlength=n))
+    return LabelSet(offs, labs, vocab)
+
+
+def label_starts(data: np.ndarray, ls: LabelSet) -> np.ndarray:
+    """Entry point per label: the point of the label nearest (squared L2, fp64)
+    to the label's centroid; INVALID for labels without points. DiskANN picks
+    label entry points with its own sampler (upstream, not part of the
+    reference); any in-label point is a valid entry for the builder."""
+    off, pts = ls.postings()
+    x = np.asarray(data, np.float64)
+    starts = np.full(max(1, ls.num_labels), INVALID, np.uint32)
+    lab_of = np.repeat(np.arange(ls.num_labels), np.diff(off).astype(np.int64))
+    if pts.size == 0:
+        return starts
+    sums = np.zeros((ls.num_labels, x.shape[1]))
+    np.add.at(sums, lab_of, x[pts])
+    cnt = np.diff(off).astype(np.float64)
+    cent = sums / np.maximum(cnt, 1)[:, None]
+    d = ((x[pts] - cent[lab_of]) ** 2).sum(1)
+    for l in np.nonzero(cnt)[0]:
+        seg = slice(off[l], off[l + 1])
+        j = int(np.argmin(d[seg]))
+        starts[l] = pts[off[l] + j]
+    return starts
+
+
+def global_start(data: np.ndarray) -> int:
+    """Point nearest to the centroid (DiskANN calculate_entry_point analogue)."""
+    x = np.asarray(data, np.float64)
+    return int(np.argmin(((x - x.mean(0)) ** 2).sum(1)))
+
+
+@dataclass
+class FilteredResult:
+    graph: np.ndarray   # N x R uint32, INVALID-padded rows
+    degree: np.ndarray  # N uint32
+    stats: dict
+    profile: dict
+
+
+def last_stats() -> dict:
+    s = GPUFilteredVamanaStats()
+    lib().gpu_vamana_filtered_get_last_stats(C.byref(s))
+    return struct_dict(s)
+
+
+def last_profile() -> dict:
+    p = DanceFilteredProfile()
+    lib().dance_get_last_filtered_profile(C.byref(p))
+    return struct_dict(p)
+
+
+def build_rc(data, ls: LabelSet, starts, R: int, L: int, filtered_L: int, C_: int = DISKANN_MAXC,
+             STEPS: int = 64, alpha: float = 1.2, universal: int = INVALID, gstart: int = INVALID,
+             rounds: int = ROUNDS, graph=None, degree=None, total: int | None = None) -> int:
+    """Calls the C ABI and returns its code (no exception). data: uint8 /
+    float32 host rows (reference entry points) or float16 (extension entry,
+    rows searched as given); rounds != 3 also uses the extension entry."""
+    N = ls.n if data is None else data.shape[0]
+    dim = 0 if data is None else data.shape[1]
+    graph = np.empty((N, R), np.uint32) if graph is None else graph
+    degree = np.empty(N, np.uint32) if degree is None else degree
+    starts = np.ascontiguousarray(starts, np.uint32)
+    total = int(ls.labels.shape[0]) if total is None else total
+    dptr = None if data is None else data.ctypes.data
+    lab_args = (_p(ls.offsets, C.c_uint32), _p(ls.labels, C.c_uint32), total, _p(starts, C.c_uint32),
+                ls.num_labels, universal, gstart)
+    L_ = lib()
+    code = DTYPE_U8 if data is None else dtype_code(data)
+    if rounds == ROUNDS and code in (DTYPE_U8, DTYPE_F32):
+        fn = L_.gpu_vamana_filtered_build_uint8 if code == DTYPE_U8 else L_.gpu_vamana_filtered_build_float
+        return fn(dptr, N, dim, R, L, filtered_L, C_, STEPS, alpha, *lab_args, None, None, 0,
+                  _p(graph, C.c_uint32), _p(degree, C.c_uint32))
+    return L_.dance_filtered_build(dptr, code, N, dim, R, L, filtered_L, C_, STEPS, alpha, *lab_args, rounds,
+                                   _p(graph, C.c_uint32), _p(degree, C.c_uint32))
+
+
+def filtered_build(data: np.ndarray, ls: LabelSet, starts: np.ndarray | None = None, R: int = 64, L: int = 100,
+                   filtered_L: int = 100, C_: int = DISKANN_MAXC, STEPS: int = 64, alpha: float = 1.2,
+                   universal: int = INVALID, gstart: int | None = None, rounds: int = ROUNDS) -> FilteredResult:
+    """gpu_vamana_filtered_build_{uint8,float} on host rows."""
+    data = np.ascontiguousarray(data)
+    if data.ndim != 2 or data.shape[0] != ls.n:
+        raise ValueError("data must be N x dim with one label row per point")
+    starts = label_starts(data, ls) if starts is None else starts
+    gstart = global_start(data) if gstart is None else gstart
+    graph = np.empty((data.shape[0], R), np.uint32)
+    degree = np.empty(data.shape[0], np.uint32)
+    _check(build_rc(data, ls, starts, R, L, filtered_L, C_, STEPS, alpha, universal, gstart, rounds, graph,
+                    degree), "gpu_vamana_filtered_build")
+    return FilteredResult(graph, degree, last_stats(), last_profile())
+
+
+def filtered_build_resident(d_data: int, dtype: int, N: int, dim: int, ls: LabelSet, starts: np.ndarray, R: int,
+                            L: int, filtered_L: int, C_: int, STEPS: int, alpha: float, universal: int,
+                            gstart: int, d_graph: int, d_degree: int) -> None:
+    """dance_filtered_build_resident on device pointers (torch data_ptr())."""
+    starts = np.ascontiguousarray(starts, np.uint32)
+    _check(lib().dance_filtered_build_resident(
+        d_data, dtype, N, dim, R, L, filtered_L, C_, STEPS, alpha, _p(ls.offsets, C.c_uint32),
+        _p(ls.labels, C.c_uint32), int(ls.labels.shape[0]), _p(starts, C.c_uint32), ls.num_labels, universal,
+        gstart, d_graph, d_degree), "dance_filtered_build_resident")
+
+
+__all__ = ["LabelSet", "canonical_labels", "synth_labels", "label_starts", "global_start", "FilteredResult",
+           "filtered_build", "filtered_build_resident", "build_rc", "last_stats", "last_profile", "ROUNDS",
+           "DISKANN_MAXC", "DTYPE_F16", "DTYPE_F32", "DTYPE_U8"]

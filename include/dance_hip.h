@@ -52,6 +52,43 @@ void dance_get_last_kernel_profile(DanceKernelProfile *profile);
 int dance_set_profile(const char *name);
 const char *dance_get_profile(void);
 
+/* ---- label-filtered build (gpu_vamana_filtered.h) extensions ---- */
+
+/* Per-kernel timings (HIP events) and device-counted work of the last
+ * filtered build. row_ms covers the fused union search, merge, label quota,
+ * work distances and forward prune; csr_ms the exact reverse-CSR prune. */
+typedef struct DanceFilteredProfile {
+    double backbone_ms, task_search_ms, row_ms, reverse_ms, csr_ms, diagnostics_ms, total_ms;
+    uint32_t rounds;
+    uint32_t vector_bytes;
+    uint64_t task_dist, union_dist, work_dist, prune_dist, csr_dist, csr_prune_dist;
+    uint64_t merged_candidates, quota_dropped, reverse_edges, touched_rows, csr_candidates, long_lists;
+    uint64_t out_edges, common_edges;
+} DanceFilteredProfile;
+
+/* The filtered build of gpu_vamana_filtered_build_{uint8,float} (reference:
+ * src/gpu_vamana_filtered.cu:6511-7067) with the element type as a parameter
+ * (DANCE_DTYPE_F32: searched as fp16; DANCE_DTYPE_U8; DANCE_DTYPE_F16: host
+ * fp16 rows) and the number of canonical rounds (0..3; 3 is the reference,
+ * 0 returns the random backbone). Used by the parity tests. */
+int dance_filtered_build(const void *h_data, int dtype, uint32_t num_points, uint32_t dim, uint32_t R, uint32_t L,
+                         uint32_t filtered_L, uint32_t C, uint32_t STEPS, float alpha,
+                         const uint32_t *point_label_offsets, const uint32_t *point_labels,
+                         uint32_t total_label_count, const uint32_t *label_to_start_id, uint32_t num_labels,
+                         uint32_t universal_label_id, uint32_t global_start_id, uint32_t rounds, uint32_t *h_graph,
+                         uint32_t *h_degree);
+
+/* Filtered build with the vectors resident in device memory (labels stay on
+ * the host, as in the reference ABI) and device outputs; used by the bench. */
+int dance_filtered_build_resident(const void *d_data, int dtype, uint32_t num_points, uint32_t dim, uint32_t R,
+                                  uint32_t L, uint32_t filtered_L, uint32_t C, uint32_t STEPS, float alpha,
+                                  const uint32_t *point_label_offsets, const uint32_t *point_labels,
+                                  uint32_t total_label_count, const uint32_t *label_to_start_id,
+                                  uint32_t num_labels, uint32_t universal_label_id, uint32_t global_start_id,
+                                  uint32_t *d_graph, uint32_t *d_degree);
+
+void dance_get_last_filtered_profile(DanceFilteredProfile *profile);
+
 /* ---- stage hooks (host buffers), used by the parity tests ---- */
 
 /* Canonical squared-L2 distances d(a[i], b[i]) (reference distance family,

@@ -25,6 +25,21 @@ Parity status of each oracle function (how it is pinned; see tests/test_oracle.p
                           brute-force ground truth.
   cpu_vamana_build        baseline only (DiskANN restated; parity unpinned:
                           upstream DiskANN is not available offline).
+  filtered_random_graph   pinned: distinct non-self ids, degree min(16, R, N-1),
+                          first entry = closed-form hash draw.
+  filtered_prune          pinned: equals a greedy in (distance, id) order that
+                          keeps a candidate iff no kept one occludes it, with
+                          label coverage as Python set inclusion; with one
+                          shared label it is textbook RobustPrune without fill.
+  filtered_merge          pinned: ordered min-distance dedupe (Python dict) when
+                          no quota applies; single-label rows keep the first
+                          quota candidates carrying the label.
+  filtered_build          pinned by the stages above plus build invariants
+                          (no self / duplicate / invalid edge, degree <= R,
+                          label-compatible edges) and recall on labelled
+                          queries; task and union search semantics are pinned
+                          by source reading and by the independent GPU
+                          implementation only (parity unpinned beyond that).
 """
 from __future__ import annotations
 
@@ -85,6 +100,17 @@ def lib() -> C.CDLL:
         L.oracle_beam_search.restype = u64
         L.oracle_bruteforce_knn.argtypes = [vp, i32, u32, u32, vp, u32, u32, _u32p, _f32p]
         L.oracle_bruteforce_knn.restype = None
+        L.oracle_filtered_random_graph.argtypes = [u32, u32, u32, u32, _u32p, _u32p]
+        L.oracle_filtered_random_graph.restype = None
+        L.oracle_filtered_build.argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, u32, f32, _u32p, _u32p, u32,
+                                            _u32p, u32, u32, u32, u32, _u32p, _u32p, C.POINTER(u64)]
+        L.oracle_filtered_build.restype = i32
+        L.oracle_filtered_prune.argtypes = [vp, i32, u32, u32, u32, f32, _u32p, _u32p, u32, _u32p, _f32p, u32,
+                                            _u32p]
+        L.oracle_filtered_prune.restype = u32
+        L.oracle_filtered_merge.argtypes = [u32, u32, u32, u32, _u32p, _u32p, u32, u32, _u32p, _u32p, u32,
+                                            _u32p, _f32p, _u32p, _f32p, u32, _u32p, _f32p]
+        L.oracle_filtered_merge.restype = u32
         L.oracle_num_threads.argtypes = []
         L.oracle_num_threads.restype = i32
         _LIB = L
@@ -242,3 +268,68 @@ def recall_at_k(found: np.ndarray, gt: np.ndarray, k: int = 10) -> float:
 
 def num_threads() -> int:
     return int(lib().oracle_num_threads())
+
+
+# ------------------------------------------------------------ filtered build
+
+def filtered_random_graph(N: int, R: int, initial_degree: int = 16, seed: int = 42):
+    g = np.empty((N, R), np.uint32)
+    d = np.empty(N, np.uint32)
+    lib().oracle_filtered_random_graph(N, R, initial_degree, seed, _p(g), _p(d))
+    return g, d
+
+
+def filtered_build(data: np.ndarray, offsets: np.ndarray, labels: np.ndarray, starts: np.ndarray,
+                   num_labels: int, R: int = 64, L: int = 100, filtered_L: int = 100, C_: int = 750,
+                   STEPS: int = 64, alpha: float = 1.2, universal: int = INVALID, global_start: int = INVALID,
+                   rounds: int = 3):
+    """canonical_v2 filtered build. Float32 rows are searched as fp16 (the
+    reference converts float input, src/gpu_vamana_filtered.cu:6497-6503).
+    Returns (rc, graph, degree, diag[12])."""
+    if data.dtype == np.float32:
+        data = data.astype(np.float16)
+    data = np.ascontiguousarray(data)
+    N, dim = data.shape
+    g = np.empty((N, R), np.uint32)
+    d = np.empty(N, np.uint32)
+    diag = np.zeros(12, np.uint64)
+    offsets = np.ascontiguousarray(offsets, np.uint32)
+    labels = np.ascontiguousarray(labels, np.uint32)
+    starts = np.ascontiguousarray(starts, np.uint32)
+    rc = lib().oracle_filtered_build(data.ctypes.data, _dt(data), N, dim, R, L, filtered_L, C_, STEPS, alpha,
+                                     _p(offsets), _p(labels), int(labels.shape[0]), _p(starts), num_labels,
+                                     universal, global_start, rounds, _p(g), _p(d),
+                                     diag.ctypes.data_as(C.POINTER(C.c_uint64)))
+    return rc, g, d, diag
+
+
+def filtered_prune(data: np.ndarray, offsets: np.ndarray, labels: np.ndarray, row: int, ids: np.ndarray,
+                   ds: np.ndarray, R: int, alpha: float) -> np.ndarray:
+    data = np.ascontiguousarray(data)
+    ids = np.ascontiguousarray(ids, np.uint32)
+    ds = np.ascontiguousarray(ds, np.float32)
+    out = np.empty(R, np.uint32)
+    n = lib().oracle_filtered_prune(data.ctypes.data, _dt(data), data.shape[0], data.shape[1], R, alpha,
+                                    _p(np.ascontiguousarray(offsets, np.uint32)),
+                                    _p(np.ascontiguousarray(labels, np.uint32)), row, _p(ids), _p(ds, C.c_float),
+                                    ids.shape[0], _p(out))
+    return out[:n]
+
+
+def filtered_merge(N: int, R: int, C_: int, keep: int, offsets, labels, num_labels: int, graph, degree, row: int,
+                   task_ids, task_d, ord_ids, ord_d):
+    offsets = np.ascontiguousarray(offsets, np.uint32)
+    labels = np.ascontiguousarray(labels, np.uint32)
+    graph = np.ascontiguousarray(graph, np.uint32)
+    degree = np.ascontiguousarray(degree, np.uint32)
+    task_ids = np.ascontiguousarray(task_ids, np.uint32)
+    task_d = np.ascontiguousarray(task_d, np.float32)
+    ord_ids = np.ascontiguousarray(ord_ids, np.uint32)
+    ord_d = np.ascontiguousarray(ord_d, np.float32)
+    out_i = np.empty(C_, np.uint32)
+    out_d = np.empty(C_, np.float32)
+    n = lib().oracle_filtered_merge(N, R, C_, keep, _p(offsets), _p(labels), int(labels.shape[0]), num_labels,
+                                    _p(graph), _p(degree), row, _p(task_ids), _p(task_d, C.c_float),
+                                    _p(ord_ids), _p(ord_d, C.c_float), ord_ids.shape[0], _p(out_i),
+                                    _p(out_d, C.c_float))
+    return out_i[:n], out_d[:n]

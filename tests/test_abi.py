@@ -16,7 +16,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def header_functions():
     names = set()
-    for h in ("gpu_vamana_builder.h", "dance_hip.h"):
+    for h in ("gpu_vamana_builder.h", "gpu_vamana_filtered.h", "dance_hip.h"):
         text = open(os.path.join(ROOT, "include", h)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         for m in re.finditer(r"\b([a-z_0-9]+)\s*\(", text):
@@ -43,6 +43,15 @@ def test_stats_struct_layout():
     assert D.GPUVamanaStats.distance_computations.offset == 56
     assert D.GPUVamanaStats.reverse_csr_seconds.offset == 104
     assert D.GPUVamanaStats.selective_active_nodes.offset == 112
+    # GPUFilteredVamanaStats: 15 doubles, 29 u64, 4 doubles, u32 x5, double,
+    # u32 x4, double, u32 x3 (reference include/gpu_vamana_filtered.h:11-77)
+    F = D.GPUFilteredVamanaStats
+    assert C.sizeof(F) == 456
+    assert F.filtered_search_distance_count.offset == 120
+    assert F.avg_common_label_out_degree.offset == 352
+    assert F.out_degree_avg.offset == 408
+    assert F.prune_output_degree_avg.offset == 432
+    assert F.semantic_complete.offset == 448
 
 
 def test_parameter_errors_return_minus_one():
@@ -61,6 +70,29 @@ def test_parameter_errors_return_minus_one():
     assert lib.gpu_vamana_vnew2_build_float(x.ctypes.data, 16, 8, 8, 16, 8, 8, None, dp) == -1
     assert lib.dance_vamana_build_resident(None, 0, 16, 8, 8, 16, 8, 8, None, None) == -1
     assert lib.dance_set_profile(b"NOPE") == -1
+
+
+def test_filtered_parameter_errors():
+    """Filtered ABI: -1 for null pointers, zero sizes, C < R and malformed
+    label offsets; 1 when min(C, 128) < 2R (reference
+    src/gpu_vamana_filtered.cu:6558-6568, 5839-5846). All are decided before
+    any device call."""
+    from dance_amd import filtered as F
+    x = np.zeros((16, 8), np.uint8)
+    xf = np.zeros((16, 8), np.float32)
+    ls = F.LabelSet(np.arange(17, dtype=np.uint32), np.zeros(16, np.uint32), 1)
+    st = np.zeros(1, np.uint32)
+    assert F.build_rc(None, ls, st, 8, 16, 16, 64) == -1                 # null data
+    assert F.build_rc(x, ls, st, 8, 16, 16, 4) == -1                     # C < R
+    assert F.build_rc(x, ls, st, 0, 16, 16, 64) == -1                    # R = 0
+    assert F.build_rc(x, ls, st, 8, 0, 16, 64) == -1                     # L = 0
+    assert F.build_rc(x[:, :0].copy(), ls, st, 8, 16, 16, 64) == -1      # dim = 0
+    assert F.build_rc(x, ls, st, 8, 16, 16, 64, total=15) == -1          # offsets[N] != total
+    bad = F.LabelSet(np.r_[np.arange(9), np.arange(7, 15)].astype(np.uint32), np.zeros(16, np.uint32), 1)
+    assert F.build_rc(x, bad, st, 8, 16, 16, 64, total=14) == -1         # offsets decrease
+    assert F.build_rc(x, ls, st, 40, 16, 16, 64) == 1                    # min(C,128) < 2R
+    assert F.build_rc(xf, ls, st, 70, 16, 16, 750) == 1                  # 128 < 140
+    assert F.build_rc(x, ls, st, 8, 16, 16, 64, rounds=4) == -1          # extension: rounds <= 3
 
 
 def test_profiles():

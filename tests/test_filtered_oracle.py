@@ -1,0 +1,205 @@
+"""Pins the CPU oracle of the filtered build (oracle/filtered_oracle.cpp) with
+checks that do not restate its code: closed forms, an independent greedy
+formulation of FilteredRobustPrune, dictionary-based merges, special cases
+that reduce to textbook RobustPrune, and build invariants. CPU only."""
+import numpy as np
+import pytest
+
+from dance_amd import INVALID
+from dance_amd import filtered as F
+from oracle import oracle as O
+
+FMAX = np.float32(np.finfo(np.float32).max)
+
+
+def sqdist(x, a, b):
+    d = x[a].astype(np.float64) - x[b].astype(np.float64)
+    return float((d * d).sum())
+
+
+def test_random_backbone_closed_form():
+    for N, R in [(1, 8), (2, 8), (17, 32), (500, 32), (3000, 8)]:
+        g, d = O.filtered_random_graph(N, R)
+        target = min(16, R, N - 1)
+        assert (d == target).all()
+        for row in range(0, N, max(1, N // 50)):
+            nb = g[row, :target]
+            assert len(set(nb.tolist())) == target and row not in nb and (nb < N).all()
+            assert (g[row, target:] == INVALID).all()
+            if target == 0:
+                continue
+            # first entry: the first hash draw (attempt 0, 1, ...) that is not the row
+            a = 0
+            while True:
+                h = O.hash_u32(((row * 0x9E3779B1) ^ (42 * 0x85EBCA6B) ^ (a * 0xC2B2AE35)) & 0xFFFFFFFF) % N
+                if h != row:
+                    break
+                a += 1
+            assert nb[0] == h
+
+
+def labels_of(ls, i):
+    return set(ls.row(i).tolist())
+
+
+def greedy_prune(x, ls, row, ids, ds, R, alpha):
+    """FilteredRobustPrune as a single pass in (distance, id) order: a
+    candidate is kept iff no already-kept p occludes it, where p occludes c
+    iff (F_row & F_c) <= F_p, d(p,c) > 0 and alpha * d(p,c) <= d(row,c)."""
+    order = sorted(range(len(ids)), key=lambda i: (ds[i], ids[i], i))
+    kept = []
+    fr = labels_of(ls, row)
+    for i in order:
+        if len(kept) == R:
+            break
+        c = int(ids[i])
+        occluded = False
+        for p in kept:
+            if (fr & labels_of(ls, c)) <= labels_of(ls, p):
+                pd = np.float32(O.distance(x, p, c))
+                if pd > 0 and np.float32(alpha) * pd <= ds[i]:
+                    occluded = True
+                    break
+        if not occluded:
+            kept.append(c)
+    return kept
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+@pytest.mark.parametrize("vocab", [1, 4, 12])
+def test_filtered_prune_matches_greedy(seed, vocab):
+    rng = np.random.default_rng(seed)
+    n = 400
+    x = rng.integers(0, 256, (n, 16), dtype=np.uint8)
+    x[7] = x[3]  # a zero-distance pair (pd > 0 rule)
+    ls = F.synth_labels(n, vocab, 1, min(3, vocab), 1.0, seed=seed)
+    for row in (0, 3, 11, 250):
+        ids = rng.choice(np.setdiff1d(np.arange(n), [row]), 120, replace=False).astype(np.uint32)
+        if row == 3:
+            ids[0] = 7
+        ds = np.array([O.distance(x, row, int(c)) for c in ids], np.float32)
+        for R, alpha in [(32, 1.2), (16, 1.0), (120, 1.2)]:
+            got = O.filtered_prune(x, ls.offsets, ls.labels, row, ids, ds, R, alpha).tolist()
+            assert got == greedy_prune(x, ls, row, ids, ds, R, alpha)
+
+
+def test_single_label_prune_is_textbook_robust_prune():
+    """With one label everywhere the coverage test always passes: the result is
+    DiskANN's RobustPrune (Alg. 2) without the degree fill, computed on exact
+    fp64 distances of integer vectors (exact in fp32 at this size)."""
+    rng = np.random.default_rng(4)
+    x = rng.integers(0, 256, (300, 12), dtype=np.uint8)
+    ls = F.canonical_labels([[5]] * 300, 8)
+    ids = np.arange(1, 300, dtype=np.uint32)
+    ds = np.array([sqdist(x, 0, int(c)) for c in ids], np.float32)
+    cand = {int(c): float(d) for c, d in zip(ids, ds)}
+    out = []
+    while cand and len(out) < 24:
+        p = min(cand, key=lambda c: (cand[c], c))
+        out.append(p)
+        del cand[p]
+        for c in list(cand):
+            pd = sqdist(x, p, c)
+            if pd > 0 and np.float32(1.2) * np.float32(pd) <= np.float32(cand[c]):
+                del cand[c]
+    got = O.filtered_prune(x, ls.offsets, ls.labels, 0, ids, ds, 24, 1.2).tolist()
+    assert got == out
+
+
+def dict_merge(row, N, C_, streams):
+    """Insertion-ordered dict: a repeat keeps the smaller distance; once C_
+    entries are held every further candidate is ignored, repeats included
+    (reference canonical_merge_one_warp, gpu_vamana_filtered.cu:4677-4678)."""
+    out = {}
+    for c, d in streams:
+        if c >= N or c == row or len(out) >= C_:
+            continue
+        out[c] = min(out.get(c, d), d)
+    return list(out.keys()), list(out.values())
+
+
+def merge_inputs(rng, N, R, ls, row, keep, nord):
+    T = ls.labels.shape[0]
+    tids = rng.integers(0, N + 3, (T, keep)).astype(np.uint32)  # includes invalid ids
+    tids[rng.random((T, keep)) < 0.2] = INVALID
+    td = rng.random((T, keep)).astype(np.float32)
+    graph = rng.integers(0, N, (N, R)).astype(np.uint32)
+    deg = rng.integers(0, R + 1, N).astype(np.uint32)
+    oid = rng.integers(0, N, nord).astype(np.uint32)
+    od = rng.random(nord).astype(np.float32)
+    return tids, td, graph, deg, oid, od
+
+
+def test_merge_without_quota_is_ordered_min_dedupe():
+    """Rows with 0 or more than 16 labels: tasks, label-sharing old neighbours
+    (distance FLT_MAX), union results; first position kept, minimum distance."""
+    rng = np.random.default_rng(7)
+    N, R, keep = 60, 8, 4
+    rows = [list(rng.choice(20, rng.integers(1, 4), replace=False)) for _ in range(N)]
+    rows[5] = []
+    rows[9] = list(range(18))
+    ls = F.canonical_labels(rows, 20)
+    for row, C_ in [(5, 128), (9, 128), (9, 10)]:
+        tids, td, graph, deg, oid, od = merge_inputs(rng, N, R, ls, row, keep, 8)
+        got_i, got_d = O.filtered_merge(N, R, C_, keep, ls.offsets, ls.labels, 20, graph, deg, row, tids, td, oid, od)
+        streams = []
+        for p in range(ls.offsets[row], ls.offsets[row + 1]):
+            streams += [(int(tids[p, i]), float(td[p, i])) for i in range(keep)]
+        fr = labels_of(ls, row)
+        for i in range(min(int(deg[row]), R)):
+            c = int(graph[row, i])
+            if c < N and c != row and fr & labels_of(ls, c):
+                streams.append((c, float(FMAX)))
+        streams += [(int(c), float(d)) for c, d in zip(oid, od)]
+        want_i, want_d = dict_merge(row, N, C_, streams)
+        assert got_i.tolist() == want_i
+        assert np.array_equal(got_d, np.array(want_d, np.float32))
+
+
+def test_merge_single_label_quota():
+    """One row label: quota = max(R, keep); the kept list is the first quota
+    merged candidates that carry the row's label, in merged order."""
+    rng = np.random.default_rng(8)
+    N, R, keep = 300, 16, 8
+    rows = [[int(rng.integers(0, 3))] for _ in range(N)]
+    rows[1] = [2]
+    ls = F.canonical_labels(rows, 3)
+    tids, td, graph, deg, oid, od = merge_inputs(rng, N, R, ls, 1, keep, 64)
+    got_i, _ = O.filtered_merge(N, R, 128, keep, ls.offsets, ls.labels, 3, graph, deg, 1, tids, td, oid, od)
+    streams = [(int(tids[0 + ls.offsets[1], i]), 0.0) for i in range(keep)]
+    for i in range(min(int(deg[1]), R)):
+        c = int(graph[1, i])
+        if c < N and c != 1 and rows[c][0] == 2:
+            streams.append((c, 0.0))
+    streams += [(int(c), 0.0) for c in oid]
+    merged, _ = dict_merge(1, N, 128, streams)
+    want = [c for c in merged if rows[c][0] == 2][:max(R, keep)]
+    assert got_i.tolist() == want
+
+
+def test_build_invariants_and_determinism():
+    rng = np.random.default_rng(3)
+    N = 2000
+    x = rng.integers(0, 256, (N, 32), dtype=np.uint8)
+    ls = F.synth_labels(N, 30, 1, 4, 1.0, seed=4)
+    st, gs = F.label_starts(x, ls), F.global_start(x)
+    rc, g, d, diag = O.filtered_build(x, ls.offsets, ls.labels, st, 30, 32, 64, 64, 750, 32, 1.2, INVALID, gs)
+    assert rc == 0
+    assert diag[0] == 0 and diag[1] == 0            # invalid, self
+    assert diag[10] == 0                              # every edge shares a label with its row
+    assert diag[7] == d.sum() and d.max() <= 32
+    for row in range(N):
+        nb = g[row, :d[row]]
+        assert len(set(nb.tolist())) == d[row]
+        assert (g[row, d[row]:] == INVALID).all()
+    rc2, g2, d2, _ = O.filtered_build(x, ls.offsets, ls.labels, st, 30, 32, 64, 64, 750, 32, 1.2, INVALID, gs)
+    assert np.array_equal(g, g2) and np.array_equal(d, d2)
+
+
+def test_build_parameter_errors():
+    x = np.zeros((10, 4), np.uint8)
+    ls = F.canonical_labels([[0]] * 10, 1)
+    st = np.zeros(1, np.uint32)
+    assert O.filtered_build(x, ls.offsets, ls.labels, st, 1, R=8, C_=4)[0] == -1
+    assert O.filtered_build(x, ls.offsets, ls.labels, st, 1, R=70, C_=750)[0] == 1
+    assert O.filtered_build(x, ls.offsets, ls.labels, st, 1, R=8, C_=64, rounds=4)[0] == -1

@@ -1,0 +1,133 @@
+"""GPU parity of the label-filtered build ("canonical_v2",
+/root/reference/src/gpu_vamana_filtered.cu:5663-6483) against the CPU oracle:
+identical seeded inputs, identical graphs (ids, order, degrees) and identical
+diagnostics, after 0 (random backbone), 1 and 3 rounds."""
+import numpy as np
+import pytest
+
+from dance_amd import INVALID
+from dance_amd import filtered as F
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def make_case(kind, n, dim, vocab, max_per, seed, hub=False):
+    rng = np.random.default_rng(seed)
+    if kind == "u8":
+        x = rng.integers(0, 256, (n, dim), dtype=np.uint8)
+    else:
+        centers = rng.standard_normal((16, dim)).astype(np.float32)
+        x = centers[rng.integers(0, 16, n)] + 0.4 * rng.standard_normal((n, dim)).astype(np.float32)
+        x /= np.linalg.norm(x, axis=1, keepdims=True)
+        if kind == "f16":
+            x = x.astype(np.float16)
+    ls = F.synth_labels(n, vocab, 1, max_per, 1.0, seed=seed + 1)
+    if hub:
+        # a point at the origin carrying the ten most frequent labels is the
+        # nearest neighbour of every unit vector: its reverse list is long
+        x[0] = 0
+        rows = [list(range(10))] + [list(ls.row(i)) for i in range(1, n)]
+        ls = F.canonical_labels(rows, vocab)
+    return x, ls
+
+
+def oracle_rows(x):
+    return x.astype(np.float16) if x.dtype == np.float32 else x
+
+
+def run_both(x, ls, starts, gstart, R, L, FL, C_, steps, alpha=1.2, universal=INVALID, rounds=3):
+    res_rc = F.build_rc(x, ls, starts, R, L, FL, C_, steps, alpha, universal, gstart, rounds,
+                        graph=(g := np.empty((x.shape[0], R), np.uint32)), degree=(d := np.empty(x.shape[0], np.uint32)))
+    orc, og, od, diag = O.filtered_build(oracle_rows(x), ls.offsets, ls.labels, starts, ls.num_labels, R, L, FL, C_,
+                                         steps, alpha, universal, gstart, rounds)
+    return res_rc, g, d, orc, og, od, diag
+
+
+def assert_same(x, ls, starts, gstart, R, L, FL, C_, steps, **kw):
+    rc, g, d, orc, og, od, diag = run_both(x, ls, starts, gstart, R, L, FL, C_, steps, **kw)
+    assert rc == orc == 0
+    assert np.array_equal(d, od), f"degree differs at rows {np.nonzero(d != od)[0][:8]}"
+    bad = np.nonzero((g != og).any(1))[0]
+    assert bad.size == 0, f"rows differ: {bad[:8]} gpu={g[bad[0]][:d[bad[0]]]} oracle={og[bad[0]][:od[bad[0]]]}"
+    st = F.last_stats()
+    assert st["invalid_neighbor_count"] == diag[0] and st["self_loop_count"] == diag[1]
+    assert st["low_common_label_degree_count"] == diag[2]
+    assert (st["out_degree_min"], st["out_degree_max"]) == (diag[3], diag[4])
+    assert (st["common_label_degree_min"], st["common_label_degree_max"]) == (diag[5], diag[6])
+    assert st["unfiltered_candidate_count"] == diag[7] and st["filtered_candidate_count"] == diag[8]
+    assert (st["label_check_count"], st["label_reject_count"], st["universal_label_pass_count"]) == tuple(diag[9:12])
+    assert st["semantic_stage"] == 6 and st["semantic_complete"] == 1
+    return g, d, diag
+
+
+@pytest.mark.parametrize("rounds", [0, 1, 3])
+@pytest.mark.parametrize("kind", ["u8", "f32"])
+def test_filtered_rounds_identical(kind, rounds):
+    x, ls = make_case(kind, 3000, 64 if kind == "u8" else 96, 40, 4, seed=11)
+    starts, gs = F.label_starts(x, ls), F.global_start(x)
+    g, d, diag = assert_same(x, ls, starts, gs, 32, 64, 64, 750, 32, rounds=rounds)
+    if rounds == 0:
+        assert (d == 16).all()
+    else:
+        assert diag[0] == 0 and diag[1] == 0
+
+
+def test_filtered_fp16_rows_extension_entry():
+    x, ls = make_case("f16", 2500, 96, 30, 3, seed=5)
+    starts, gs = F.label_starts(x, ls), F.global_start(x)
+    assert_same(x, ls, starts, gs, 24, 48, 48, 64, 24, rounds=2)
+
+
+@pytest.mark.parametrize("FL,C_,R,L", [(20, 64, 32, 64), (100, 750, 64, 100), (8, 128, 16, 12)])
+def test_filtered_pool_and_capacity_edges(FL, C_, R, L):
+    """Pools below 32/64 (filtered_L), work capacity exactly 2R, L < R."""
+    x, ls = make_case("u8", 2000, 64, 25, 5, seed=FL + C_)
+    starts, gs = F.label_starts(x, ls), F.global_start(x)
+    assert_same(x, ls, starts, gs, R, L, FL, C_, 24)
+
+
+def test_filtered_universal_label_and_missing_starts():
+    """Universal label (never a task; matches everything in diagnostics),
+    labels >= num_labels (no postings), unlabelled rows, invalid starts and
+    an invalid global start."""
+    x, ls = make_case("u8", 2500, 64, 30, 4, seed=9)
+    rows = [list(ls.row(i)) for i in range(2500)]
+    for i in range(0, 2500, 7):
+        rows[i] = rows[i] + [0]          # label 0 = universal on every 7th row
+    for i in range(3, 2500, 11):
+        rows[i] = []                     # unlabelled
+    for i in range(5, 2500, 13):
+        rows[i] = rows[i] + [31, 33]     # beyond num_labels = 30
+    ls = F.canonical_labels(rows, 30)
+    starts = F.label_starts(x, ls)
+    starts[[2, 5, 17]] = INVALID
+    starts[4] = 10 ** 6                  # out of range: skipped like INVALID
+    assert_same(x, ls, starts, INVALID, 32, 64, 64, 750, 32, universal=0)
+    assert_same(x, ls, starts, F.global_start(x), 32, 64, 64, 750, 32, universal=0, rounds=1)
+
+
+def test_filtered_hub_long_reverse_lists():
+    """A hub with in-degree far above 256 takes the global-memory prune path."""
+    x, ls = make_case("f32", 3000, 64, 40, 3, seed=21, hub=True)
+    starts, gs = F.label_starts(x, ls), F.global_start(x)
+    g, d, _ = assert_same(x, ls, starts, gs, 32, 64, 64, 750, 32, rounds=1)
+    assert F.last_profile()["long_lists"] > 0
+
+
+@pytest.mark.parametrize("n", [1, 2, 17, 50])
+def test_filtered_tiny(n):
+    x, ls = make_case("u8", n, 32, 5, 3, seed=n)
+    starts, gs = F.label_starts(x, ls), F.global_start(x)
+    assert_same(x, ls, starts, gs, 16, 32, 32, 64, 16)
+
+
+def test_filtered_abi_float_entry_matches_extension():
+    """gpu_vamana_filtered_build_float (reference entry) == fp16 search of the
+    rounded rows through the extension entry."""
+    x, ls = make_case("f32", 2000, 96, 30, 3, seed=3)
+    starts, gs = F.label_starts(x, ls), F.global_start(x)
+    a = F.filtered_build(x, ls, starts, 32, 64, 64, 750, 32, 1.2, INVALID, gs)
+    b = F.filtered_build(x.astype(np.float16), ls, starts, 32, 64, 64, 750, 32, 1.2, INVALID, gs)
+    assert np.array_equal(a.graph, b.graph) and np.array_equal(a.degree, b.degree)
+    assert a.profile["rounds"] == 3 and a.stats["gpu_build_seconds"] > 0
