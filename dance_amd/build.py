@@ -29,7 +29,7 @@ HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-pthread", "-Wall", "-Wextra", "-Wn
 
 HIP_SOURCES = ["vnew2_build.hip", "filtered_build.hip"]
 HOST_SOURCES = ["synth.cpp"]
-APP_SOURCES = ["gpu_vamana_memory_index.cpp"]
+APP_SOURCES = ["gpu_vamana_memory_index.cpp", "gpu_stitched_vamana_index.cpp"]
 
 
 def _run(cmd: list[str]) -> None:

@@ -1,0 +1,147 @@
+"""gpu_stitched_vamana_index (reference apps/utils/gpu_stitched_vamana_index.cpp):
+label-file and argument errors (CPU), and on the GPU the stitched graph equals
+the per-label standard builds remapped to global ids, with the five sidecars."""
+import json
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import dance_amd as D
+from dance_amd import formats
+from oracle import oracle as O
+
+APP = os.path.join(os.path.dirname(D.__file__), "gpu_stitched_vamana_index")
+
+
+def run_app(*args):
+    return subprocess.run([APP, *args], capture_output=True, text=True, timeout=300)
+
+
+def write_case(tmp_path, x, rows):
+    p = str(tmp_path / "x.bin")
+    formats.write_bin(p, x)
+    lp = str(tmp_path / "labels.txt")
+    with open(lp, "w") as f:
+        f.write("".join(r + "\n" for r in rows))
+    return p, lp
+
+
+def base_args(p, lp, prefix, kind="uint8"):
+    return ["--data_type", kind, "--data_path", p, "--label_file", lp, "--index_path_prefix", prefix]
+
+
+@pytest.mark.parametrize("rows,msg", [
+    (["a", "", "b"], "empty label row is not supported"),
+    (["a", "a,,b", "b"], "empty label token is not supported"),
+    (["a", "U", "b"], "does not support universal-label rows"),
+    (["a", "b"], "number of label rows does not match data points"),
+])
+def test_label_file_errors(tmp_path, rows, msg):
+    x = np.zeros((3, 4), np.uint8)
+    p, lp = write_case(tmp_path, x, rows)
+    r = run_app(*base_args(p, lp, str(tmp_path / "i")), "--universal_label", "U")
+    assert r.returncode == 1 and msg in r.stderr
+
+
+def test_argument_errors(tmp_path):
+    r = run_app("--data_type", "uint8")
+    assert r.returncode == 1 and "'--data_path' is required" in r.stderr
+    r = run_app("--data_type=int8", "--data_path=x", "--label_file=y", "--index_path_prefix=z")
+    assert r.returncode == 2 and "supports uint8 and float" in r.stderr
+    r = run_app("--data_type", "uint8", "--data_path", "/nonexistent", "--label_file", "y",
+                "--index_path_prefix", "z")
+    assert r.returncode == 1 and "failed to open data file" in r.stderr
+    r = run_app("--bogus", "1")
+    assert r.returncode == 1 and "unrecognised option" in r.stderr
+    r = run_app("--help")
+    assert r.returncode == 0 and "--Rstitched" in r.stdout
+
+
+def expected_stitched(x, rows, Rs, Ls, Rout, C_, steps, builder):
+    """Per label (ids 1.. by first appearance): build on the label's points,
+    remap local -> global, cap Rout per label, drop invalid / self / repeats."""
+    names, points = [], []
+    for pid, r in enumerate(rows):
+        seen = []
+        for tok in r.replace(" ", "").split(","):
+            if tok not in seen:
+                seen.append(tok)
+        for tok in seen:
+            if tok not in names:
+                names.append(tok)
+                points.append([])
+            points[names.index(tok)].append(pid)
+    graph = [[] for _ in rows]
+    medoids = []
+    for ids in points:
+        ids = np.asarray(ids)
+        g, d, med = builder(x[ids])
+        medoids.append(int(ids[med if med < len(ids) else 0]))
+        for i in range(len(ids)):
+            row = graph[ids[i]]
+            for j in range(min(int(d[i]), Rout)):
+                nb = int(g[i, j])
+                if nb >= len(ids) or ids[nb] == ids[i]:
+                    continue
+                if int(ids[nb]) not in row:
+                    row.append(int(ids[nb]))
+    return names, graph, medoids
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", ["uint8", "float"])
+def test_stitched_equals_per_label_builds(tmp_path, kind):
+    rng = np.random.default_rng(5)
+    n = 3000
+    if kind == "uint8":
+        x = rng.integers(0, 256, (n, 64), dtype=np.uint8)
+    else:
+        x = rng.standard_normal((n, 48)).astype(np.float32)
+    lab = rng.integers(0, 6, n)
+    lab[:40] = 6  # a small label
+    rows = [f"L{v}" for v in lab]
+    p, lp = write_case(tmp_path, x, rows)
+    prefix = str(tmp_path / "idx")
+    tj = str(tmp_path / "t.json")
+    r = run_app(*base_args(p, lp, prefix, kind), "--Rsmall", "24", "--Lsmall", "48", "--Rstitched", "32",
+                "--C", "40", "--steps", "24", "--timing_json", tj)
+    assert r.returncode == 0, r.stderr
+
+    def oracle_build(xl):
+        g, d, m = O.vnew2_build(xl, 24, 48, 40, 24)
+        return g, d, m
+    names, want, medoids = expected_stitched(x, rows, 24, 48, 32, 40, 24, oracle_build)
+    adj, max_deg, start, frozen = formats.read_graph(prefix)
+    assert start == 0 and frozen == 0 and len(adj) == n
+    for v in range(n):
+        assert adj[v].tolist() == want[v], v
+    assert max_deg == max(len(r) for r in want)
+    # sidecars
+    assert open(prefix + ".data", "rb").read() == open(p, "rb").read()
+    ids = {nm: i + 1 for i, nm in enumerate(names)}
+    lines = open(prefix + "_labels.txt").read().splitlines()
+    assert lines == [str(ids[r]) for r in rows]
+    assert open(prefix + "_label_formatted.txt").read().splitlines() == lines
+    assert open(prefix + "_labels_map.txt").read().splitlines() == [f"{nm}\t{i + 1}" for i, nm in enumerate(names)]
+    assert open(prefix + "_labels_to_medoids.txt").read().splitlines() == [
+        f"{i + 1}, {m}" for i, m in enumerate(medoids)]
+    t = json.load(open(tj))
+    assert t["num_labels"] == len(names) and t["total_label_memberships"] == n
+    assert t["output_edges"] == sum(len(r) for r in want)
+
+
+@pytest.mark.gpu
+def test_stitched_multi_label_needs_global_prune(tmp_path):
+    rng = np.random.default_rng(6)
+    x = rng.integers(0, 256, (600, 32), dtype=np.uint8)
+    rows = ["a,b" if i % 3 == 0 else ("a" if i % 2 else "b") for i in range(600)]
+    p, lp = write_case(tmp_path, x, rows)
+    prefix = str(tmp_path / "idx")
+    r = run_app(*base_args(p, lp, prefix), "--Rsmall", "16", "--Lsmall", "32", "--Rstitched", "16", "--C", "32",
+                "--steps", "16")
+    assert r.returncode == 3 and "prune_all_neighbors" in r.stderr
+    assert os.path.exists(prefix + "_full")
+    adj, *_ = formats.read_graph(prefix + "_full")
+    assert max(len(a) for a in adj) > 16  # two labels contribute up to Rstitched each
