@@ -4,11 +4,15 @@ A step is one full build (medoid, init, 4 x (search + online insert, reverse
 merge, prune)) of the configured synthetic workload, with the vectors already
 resident in HBM. value = vertices/s = N / seconds per build.
 
-Prints ONE JSON line. Also reports recall@10 of the built graph (beam search
-against exact ground truth on a query subset), the HBM roofline of the
+Prints ONE JSON line. Also reports recall@10 of the built graph (GPU
+best-first search against exact ground truth on a query subset), the HBM roofline of the
 dominant kernel (search + online insert; algorithmic bytes counted on device,
 duration from HIP events on the build stream) and the CPU baseline (the CPU
 oracle of the same algorithm on a bounded sample, on this host's cores).
+
+--config c5f / c5s measure the label-filtered and stitched builds on the c5
+workload (recall of label-filtered search against per-label exact ground
+truth); the default run is the c3 standard build.
 """
 from __future__ import annotations
 
@@ -29,7 +33,13 @@ WORKLOADS = {
     "c2": "c2: 1M x 96 fp32 256-center Gaussian mixture sigma 0.3 L2-normalized, seed 42; R64 L100 C80 STEPS64 alpha1.2",
     "c3": "c3: 10M x 96 fp32 256-center Gaussian mixture sigma 0.3 L2-normalized, seed 42; R64 L100 C80 STEPS64 alpha1.2",
     "c4": "c4: 10M x 128 uint8 clip(round(64+24z)) 1024-center mixture, seed 42; R64 L100 C80 STEPS64 alpha1.2",
+    "c5f": ("c5 filtered: 1M x 192 uint8 (c4 generator at 192 dims), 1-8 distinct labels/row Zipf(1.0) over 20k, "
+            "GPU-FilteredVamana canonical_v2 R64 L=FL=100 alpha1.2 C750 (work C 128) STEPS64, 3 rounds"),
+    "c5s": ("c5 stitched: the c5 vectors, 100 partitioned labels (one per row, uniform), StitchedVamana "
+            "Rsmall32 Lsmall100 Rstitched64 C96 steps64"),
 }
+C5 = dict(n=1_000_000, dim=192, centers=1024, sigma=0.3, nq=10_000, vocab=20_000, min_labels=1, max_labels=8,
+          R=64, L=100, FL=100, C=750, STEPS=64, alpha=1.2, parts=100, Rsmall=32, Lsmall=100, Rstitched=64, Cs=96)
 METRIC = "Vamana build seconds + vertices/sec at 10M×96 fp32 R64/L100; recall@10"
 
 
@@ -66,6 +76,192 @@ def ground_truth(base_t, base_np: np.ndarray, queries: np.ndarray, k: int = 10, 
     return out
 
 
+def label_starts_gpu(torch, base_t, ls):
+    """Per label: the member nearest (fp64) to the label centroid, ties to the
+    smaller id; INVALID for empty labels. Also the global start (nearest to
+    the centroid of all points)."""
+    from dance_amd import INVALID
+    dev = base_t.device
+    off, pts = ls.postings()
+    nl = ls.num_labels
+    cnt = np.diff(off).astype(np.int64)
+    lab_of = torch.from_numpy(np.repeat(np.arange(nl), cnt)).to(dev)
+    P = torch.from_numpy(pts.astype(np.int64)).to(dev)
+    dim = base_t.shape[1]
+    sums = torch.zeros((nl, dim), dtype=torch.float64, device=dev)
+    step = 1 << 20
+    for s0 in range(0, P.shape[0], step):
+        sums.index_add_(0, lab_of[s0:s0 + step], base_t[P[s0:s0 + step]].double())
+    cent = sums / torch.from_numpy(np.maximum(cnt, 1)).to(dev).double()[:, None]
+    d = torch.empty(P.shape[0], dtype=torch.float64, device=dev)
+    for s0 in range(0, P.shape[0], step):
+        diff = base_t[P[s0:s0 + step]].double() - cent[lab_of[s0:s0 + step]]
+        d[s0:s0 + step] = (diff * diff).sum(1)
+    o1 = torch.sort(d, stable=True).indices
+    o2 = torch.sort(lab_of[o1], stable=True).indices
+    best = P[o1[o2]].cpu().numpy()
+    starts = np.full(max(1, nl), INVALID, np.uint32)
+    nz = np.nonzero(cnt)[0]
+    starts[nz] = best[off[nz]]
+    mean = base_t.double().mean(0)
+    gd = ((base_t.double() - mean) ** 2).sum(1)
+    gstart = int(torch.nonzero(gd == gd.min())[0, 0])
+    return starts, gstart
+
+
+def label_ground_truth(torch, base_t, ls, queries, qlabels, k=10):
+    """Exact top-k among the points carrying each query's label (uint8 rows:
+    integer distances, exact in the fp32 Gram form), ties to the smaller id;
+    INVALID pads labels with fewer than k points."""
+    from dance_amd import INVALID
+    dev = base_t.device
+    off, pts = ls.postings()
+    out = np.full((queries.shape[0], k), INVALID, np.uint32)
+    xf = base_t.float()
+    xn = (xf * xf).sum(1)
+    for l in np.unique(qlabels):
+        qi = np.nonzero(qlabels == l)[0]
+        rows = torch.from_numpy(pts[off[l]:off[l + 1]].astype(np.int64)).to(dev)
+        if rows.numel() == 0:
+            continue
+        q = torch.from_numpy(queries[qi].astype(np.float32)).to(dev)
+        d = (xn[rows][None, :] + (q * q).sum(1)[:, None] - 2.0 * (q @ xf[rows].T)).round().long()
+        key = d * (1 << 21) + rows[None, :]
+        kk = min(k, rows.numel())
+        top = torch.topk(key, kk, dim=1, largest=False).values
+        out[qi, :kk] = (top % (1 << 21)).cpu().numpy().astype(np.uint32)
+    return out
+
+
+def run_c5(args, mode) -> int:
+    import torch
+    import dance_amd as D
+    from dance_amd import INVALID
+    from dance_amd import filtered as F
+
+    c = C5
+    n = args.n or c["n"]
+    t0 = time.time()
+    base = D.synth_u8(42, 0, n, c["dim"], c["centers"], c["sigma"])
+    queries = D.synth_u8(42, 1, c["nq"], c["dim"], c["centers"], c["sigma"])
+    dev = torch.device("cuda:0")
+    base_t = torch.from_numpy(base).to(dev)
+    if mode == "c5f":
+        ls = F.synth_labels(n, c["vocab"], c["min_labels"], c["max_labels"], 1.0, seed=42)
+        qlab = F.zipf_labels(c["nq"], c["vocab"], 1.0, seed=43)
+    else:
+        part = np.random.default_rng(44).integers(0, c["parts"], n)
+        ls = F.LabelSet(np.arange(n + 1, dtype=np.uint32), part.astype(np.uint32), c["parts"])
+        qlab = np.random.default_rng(45).integers(0, c["parts"], c["nq"]).astype(np.uint32)
+    starts, gstart = label_starts_gpu(torch, base_t, ls)
+    log(f"generated {mode} N={n} labels={ls.labels.shape[0]} in {time.time() - t0:.1f}s")
+    R = c["R"] if mode == "c5f" else c["Rsmall"]
+    graph_t = torch.empty((n, c["R"]), dtype=torch.int32, device=dev)
+    deg_t = torch.empty((n,), dtype=torch.int32, device=dev)
+    stitched = {}
+
+    def step_filtered():
+        F.filtered_build_resident(base_t.data_ptr(), D.DTYPE_U8, n, c["dim"], ls, starts, c["R"], c["L"], c["FL"],
+                                  c["C"], c["STEPS"], c["alpha"], INVALID, gstart, graph_t.data_ptr(),
+                                  deg_t.data_ptr())
+
+    off, pts = ls.postings()
+    parts = [torch.from_numpy(pts[off[l]:off[l + 1]].astype(np.int64)).to(dev) for l in range(ls.num_labels)]
+
+    def step_stitched():
+        # per label: gather the label's rows, standard build (Rsmall), remap
+        # local -> global on the device (rows are partitioned: one label each)
+        t_build = 0.0
+        medoids = np.zeros(ls.num_labels, np.uint32)
+        graph_t.fill_(-1)
+        deg_t.zero_()
+        for l, ids in enumerate(parts):
+            m = ids.numel()
+            if m == 0:
+                continue
+            xl = base_t[ids].contiguous()
+            gl = torch.empty((m, c["Rsmall"]), dtype=torch.int32, device=dev)
+            dl = torch.empty((m,), dtype=torch.int32, device=dev)
+            tb = time.perf_counter()
+            D.vamana_build_resident(xl.data_ptr(), D.DTYPE_U8, m, c["dim"], c["Rsmall"], c["Lsmall"], c["Cs"],
+                                    c["STEPS"], gl.data_ptr(), dl.data_ptr())
+            t_build += time.perf_counter() - tb
+            medoids[l] = int(ids[int(D.lib().gpu_vamana_vnew2_get_last_medoid())])
+            k = min(c["Rsmall"], c["Rstitched"])
+            loc = gl[:, :k].long()
+            ok = (loc >= 0) & (loc < m) & (torch.arange(k, device=dev)[None, :] < dl[:, None].long())
+            glob = torch.where(ok, ids[loc.clamp(0, m - 1)], torch.full_like(loc, -1))
+            # valid entries first, order kept (stable sort on the invalid flag)
+            order = torch.sort((~ok).to(torch.int8), dim=1, stable=True).indices
+            rows = torch.gather(glob, 1, order).to(torch.int32)
+            graph_t[ids, :k] = rows
+            deg_t[ids] = ok.sum(1).to(torch.int32)
+        stitched["gpu_build_sum_s"] = round(t_build, 3)
+        stitched["medoids"] = medoids
+
+    step = step_filtered if mode == "c5f" else step_stitched
+    for i in range(args.warmup):
+        step()
+        log(f"warmup {i + 1}/{args.warmup} done")
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for i in range(args.steps):
+        step()
+        log(f"step {i + 1}/{args.steps} done")
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    ms_per_step = elapsed * 1000.0 / args.steps
+    value = n / (ms_per_step / 1000.0)
+
+    # recall@10 of label-filtered search against exact per-label ground truth
+    nq = min(args.recall_queries, c["nq"])
+    recall = {}
+    qs = queries[:nq]
+    ql = qlab[:nq]
+    if nq > 0:
+        t1 = time.time()
+        gt = label_ground_truth(torch, base_t, ls, qs, ql)
+        ent = starts[ql] if mode == "c5f" else stitched["medoids"][ql]
+        for Ls in (10, 20, 50, 100, 200):
+            found, _ = D.search_resident(base_t.data_ptr(), D.DTYPE_U8, n, c["dim"], graph_t.data_ptr(),
+                                         deg_t.data_ptr(), c["R"], ent, qs, 10, Ls, ls.offsets, ls.labels, ql)
+            recall[f"L{Ls}"] = round(D.recall_at_k(found, gt, 10), 4)
+        log(f"recall {recall} ({time.time() - t1:.1f}s)")
+
+    line = {"metric": ("filtered" if mode == "c5f" else "stitched") + " Vamana build vertices/sec (1M x 192 uint8)",
+            "value": round(value, 1), "unit": "vertices/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms_per_step, 2), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "u8", "data": "synthetic",
+            "config": {"workload": WORKLOADS[mode] + (f" (N overridden to {n})" if args.n else ""), "N": n},
+            "build_seconds": round(ms_per_step / 1000.0, 3), "recall@10": recall}
+    if mode == "c5f":
+        kp = F.last_profile()
+        st = F.last_stats()
+        V = c["dim"]
+        kernels = {"k_task_search": (kp["task_search_ms"], kp["task_dist"] * V),
+                   "k_row": (kp["row_ms"], (kp["union_dist"] + kp["work_dist"] + kp["prune_dist"]) * V),
+                   "k_csr": (kp["csr_ms"], (kp["csr_dist"] + kp["csr_prune_dist"]) * V)}
+        name = max(kernels, key=lambda k: kernels[k][0])
+        ms, by = kernels[name]
+        achieved = by / (ms * 1e-3) / 1e9 if ms > 0 else 0.0  # bytes and time summed over the rounds
+        line["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
+                            "avg_launch_ms": round(ms / kp["rounds"], 3),
+                            "algorithmic_bytes_per_launch": by / kp["rounds"]}
+        line["stage_ms"] = {k: round(kp[k], 2) for k in ("backbone_ms", "task_search_ms", "row_ms", "reverse_ms",
+                                                        "csr_ms", "diagnostics_ms", "total_ms")}
+        line["counters"] = {k: kp[k] for k in ("task_dist", "union_dist", "work_dist", "prune_dist", "csr_dist",
+                                               "csr_prune_dist", "merged_candidates", "quota_dropped",
+                                               "reverse_edges", "touched_rows", "long_lists")}
+        line["diagnostics"] = {k: st[k] for k in ("invalid_neighbor_count", "self_loop_count", "out_degree_min",
+                                                  "out_degree_max", "out_degree_avg", "avg_common_label_out_degree",
+                                                  "low_common_label_degree_count")}
+    else:
+        line["stitched"] = {"gpu_build_sum_s": stitched["gpu_build_sum_s"], "labels": ls.num_labels}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -84,6 +280,9 @@ def main() -> int:
         print("bench.py: this build targets one GPU; multi-GPU sharding is design-only "
               "(see DESIGN.md), so --gpus must be 1.", file=sys.stderr)
         return 2
+
+    if args.config in ("c5f", "c5s"):
+        return run_c5(args, args.config)
 
     import torch
     import dance_amd as D
@@ -145,23 +344,23 @@ def main() -> int:
         with open(traffic_file) as f:
             roofline["traffic"] = json.load(f).get("search_hbm_bytes_per_launch")
 
-    # Recall@10 on a query subset.
-    from oracle import oracle as O
+    # Recall@10 on a query subset: GPU best-first search over the resident
+    # graph (dance_search_resident) against exact ground truth.
     nq = min(args.recall_queries, queries.shape[0])
     recall = {}
     if nq > 0:
         t0 = time.time()
         gt = ground_truth(base_t, base, queries[:nq])
-        graph = graph_t.cpu().numpy().view(np.uint32)
-        deg = deg_t.cpu().numpy().view(np.uint32)
         medoid = int(D.lib().gpu_vamana_vnew2_get_last_medoid())
         for Ls in (10, 20, 50, 100, 200):
-            found = O.beam_search(base, graph, deg, medoid, queries[:nq], 10, Ls)
-            recall[f"L{Ls}"] = round(O.recall_at_k(found, gt, 10), 4)
+            found, _ = D.search_resident(base_t.data_ptr(), dcode, n, cfg["dim"], graph_t.data_ptr(),
+                                         deg_t.data_ptr(), cfg["R"], medoid, queries[:nq], 10, Ls)
+            recall[f"L{Ls}"] = round(D.recall_at_k(found, gt, 10), 4)
         log(f"recall {recall} ({time.time() - t0:.1f}s)")
 
     cpu = None
     if args.cpu_sample > 0:
+        from oracle import oracle as O  # the CPU baseline leg only
         m = min(args.cpu_sample, n)
         sample = np.ascontiguousarray(base[:m])
         t0 = time.perf_counter()

@@ -113,6 +113,11 @@ class DanceFilteredProfile(C.Structure):
     )
 
 
+class DanceSearchStats(C.Structure):
+    _fields_ = [("kernel_ms", C.c_double), ("distances", C.c_uint64), ("expansions", C.c_uint64),
+                ("capped_queries", C.c_uint64)]
+
+
 def struct_dict(s: C.Structure) -> dict:
     return {name: getattr(s, name) for name, _ in s._fields_}
 
@@ -132,6 +137,7 @@ EXPORTS = [
     "dance_synth_f32", "dance_synth_u8",
     "gpu_vamana_filtered_build_uint8", "gpu_vamana_filtered_build_float", "gpu_vamana_filtered_get_last_stats",
     "dance_filtered_build", "dance_filtered_build_resident", "dance_get_last_filtered_profile",
+    "dance_search", "dance_search_resident", "dance_get_last_search_stats",
 ]
 
 _LIB = None
@@ -203,6 +209,12 @@ def lib() -> C.CDLL:
         L.dance_filtered_build_resident.restype = i32
         L.dance_get_last_filtered_profile.argtypes = [C.POINTER(DanceFilteredProfile)]
         L.dance_get_last_filtered_profile.restype = None
+        search_args = [vp, i32, u32, u32, vp, vp, u32, _u32p, u32, vp, u32, u32, u32, vp, vp, vp, _u32p, _f32p]
+        for name in ("dance_search", "dance_search_resident"):
+            getattr(L, name).argtypes = search_args
+            getattr(L, name).restype = i32
+        L.dance_get_last_search_stats.argtypes = [C.POINTER(DanceSearchStats)]
+        L.dance_get_last_search_stats.restype = None
         _LIB = L
     return _LIB
 
@@ -395,6 +407,66 @@ def stage_scan(x: np.ndarray) -> np.ndarray:
     out = np.empty_like(x)
     _check(lib().dance_stage_scan(_p(x, C.c_uint32), x.shape[0], _p(out, C.c_uint32)), "dance_stage_scan")
     return out
+
+
+# ------------------------------------------------------------- query search
+
+def _opt_ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def search(data: np.ndarray, graph: np.ndarray, degree: np.ndarray, starts, queries: np.ndarray, k: int, L: int,
+           label_offsets=None, labels=None, query_labels=None):
+    """dance_search: best-first search of host queries over a built graph on
+    host arrays. starts: int (shared entry point) or one per query; the label
+    arrays (all or none) restrict the search to points carrying the query's
+    label. Returns (ids, dists), each nq x k."""
+    data = np.ascontiguousarray(data)
+    graph = np.ascontiguousarray(graph, np.uint32)
+    degree = np.ascontiguousarray(degree, np.uint32)
+    return _search(lib().dance_search, data.ctypes.data, dtype_code(data), data.shape[0], data.shape[1],
+                   graph.ctypes.data, degree.ctypes.data, graph.shape[1], starts, queries, k, L, label_offsets,
+                   labels, query_labels)
+
+
+def search_resident(d_data: int, dtype: int, N: int, dim: int, d_graph: int, d_degree: int, R: int, starts,
+                    queries: np.ndarray, k: int, L: int, label_offsets=None, labels=None, query_labels=None):
+    """dance_search_resident: as search() with base rows, graph and degrees
+    given as device pointers (e.g. torch data_ptr())."""
+    return _search(lib().dance_search_resident, d_data, dtype, N, dim, d_graph, d_degree, R, starts, queries, k, L,
+                   label_offsets, labels, query_labels)
+
+
+def _search(fn, data_p, dtype, N, dim, graph_p, degree_p, R, starts, queries, k, L, label_offsets, labels,
+            query_labels):
+    queries = np.ascontiguousarray(queries)
+    starts = np.atleast_1d(np.asarray(starts, np.uint32))
+    nq = queries.shape[0]
+    ids = np.empty((nq, k), np.uint32)
+    dists = np.empty((nq, k), np.float32)
+    opt = [None if a is None else np.ascontiguousarray(a, np.uint32) for a in (label_offsets, labels, query_labels)]
+    ptrs = [_opt_ptr(a) for a in opt]
+    rc = fn(data_p, dtype, N, dim, graph_p, degree_p, R, _p(starts, C.c_uint32), starts.shape[0], queries.ctypes.data,
+            nq, k, L, *ptrs, _p(ids, C.c_uint32), _p(dists, C.c_float))
+    _check(rc, "dance_search")
+    return ids, dists
+
+
+def last_search_stats() -> dict:
+    s = DanceSearchStats()
+    lib().dance_get_last_search_stats(C.byref(s))
+    return struct_dict(s)
+
+
+def recall_at_k(found: np.ndarray, gt: np.ndarray, k: int = 10) -> float:
+    """Mean |found[:k] & gt[:k]| / k over queries (gt rows may hold INVALID
+    padding when fewer than k points qualify; those slots are not counted)."""
+    hits, total = 0, 0
+    for f, g in zip(found, gt):
+        g = [x for x in g[:k] if x != INVALID]
+        total += len(g)
+        hits += len(set(f[:k].tolist()) & set(g))
+    return hits / max(1, total)
 
 
 # ------------------------------------------------------------------ workloads

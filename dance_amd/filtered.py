@@ -64,21 +64,37 @@ def canonical_labels(rows: list, num_labels: int | None = None) -> LabelSet:
 def synth_labels(n: int, vocab: int, min_per: int = 1, max_per: int = 8, zipf_s: float = 1.0,
                  seed: int = 42) -> LabelSet:
     """Seeded multi-label workload: a uniform count in [min_per, max_per] per
-    point, labels drawn Zipf(zipf_s) over `vocab` ids (rank r has weight
-    1/(r+1)^s), duplicates within a point removed."""
+    point, that many distinct labels drawn Zipf(zipf_s) over `vocab` ids
+    (rank r has weight 1/(r+1)^s) without replacement within a point."""
+    if max_per > vocab:
+        raise ValueError("max_per exceeds the vocabulary")
     rng = np.random.default_rng(seed)
     w = 1.0 / np.power(np.arange(1, vocab + 1, dtype=np.float64), zipf_s)
     cdf = np.cumsum(w / w.sum())
-    counts = rng.integers(min_per, max_per + 1, n)
-    draws = np.searchsorted(cdf, rng.random(int(counts.sum())), side="right").astype(np.int64)
-    draws = np.minimum(draws, vocab - 1)
-    rows_of = np.repeat(np.arange(n, dtype=np.int64), counts)
-    key = np.unique(rows_of * vocab + draws)  # sorted, unique per row
-    rows_u = key // vocab
-    labs = (key % vocab).astype(np.uint32)
+    want = rng.integers(min_per, max_per + 1, n).astype(np.int64)
+    keys = np.empty(0, np.int64)
+    have = np.zeros(n, np.int64)
+    while True:
+        short = np.nonzero(have < want)[0]
+        if short.size == 0:
+            break
+        need = want[short] - have[short]
+        rows = np.repeat(short, need)
+        draws = np.minimum(np.searchsorted(cdf, rng.random(rows.size), side="right"), vocab - 1)
+        # each short row draws its deficit; repeats collapse and are redrawn
+        keys = np.unique(np.concatenate([keys, rows * vocab + draws]))
+        have = np.bincount(keys // vocab, minlength=n)
     offs = np.zeros(n + 1, np.uint32)
-    offs[1:] = np.cumsum(np.bincount(rows_u, minlength=n))
-    return LabelSet(offs, labs, vocab)
+    offs[1:] = np.cumsum(have)
+    return LabelSet(offs, (keys % vocab).astype(np.uint32), vocab)
+
+
+def zipf_labels(count: int, vocab: int, zipf_s: float = 1.0, seed: int = 43) -> np.ndarray:
+    """One label per query, Zipf(zipf_s) over vocab ids."""
+    rng = np.random.default_rng(seed)
+    w = 1.0 / np.power(np.arange(1, vocab + 1, dtype=np.float64), zipf_s)
+    cdf = np.cumsum(w / w.sum())
+    return np.minimum(np.searchsorted(cdf, rng.random(count), side="right"), vocab - 1).astype(np.uint32)
 
 
 def label_starts(data: np.ndarray, ls: LabelSet) -> np.ndarray:
@@ -182,6 +198,6 @@ def filtered_build_resident(d_data: int, dtype: int, N: int, dim: int, ls: Label
         gstart, d_graph, d_degree), "dance_filtered_build_resident")
 
 
-__all__ = ["LabelSet", "canonical_labels", "synth_labels", "label_starts", "global_start", "FilteredResult",
+__all__ = ["LabelSet", "canonical_labels", "synth_labels", "zipf_labels", "label_starts", "global_start", "FilteredResult",
            "filtered_build", "filtered_build_resident", "build_rc", "last_stats", "last_profile", "ROUNDS",
            "DISKANN_MAXC", "DTYPE_F16", "DTYPE_F32", "DTYPE_U8"]

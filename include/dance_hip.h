@@ -89,6 +89,40 @@ int dance_filtered_build_resident(const void *d_data, int dtype, uint32_t num_po
 
 void dance_get_last_filtered_profile(DanceFilteredProfile *profile);
 
+/* ---- query search over a built graph ---- */
+
+/* Kernel time (HIP events) and device counters of the last search. */
+typedef struct DanceSearchStats {
+    double kernel_ms;
+    uint64_t distances, expansions, capped_queries;
+} DanceSearchStats;
+
+/* Best-first search of num_queries query rows (host, same dtype and dim as
+ * the base) over a graph (N x R rows, degree per row): DiskANN
+ * search_memory_index semantics (reference counterpart; filtered start points
+ * integrations/dance-diskann-78256bba.patch:20583-20600): a candidate list of
+ * the L smallest (distance, id) seen, the closest unexpanded candidate is
+ * expanded until none is left; returns the k best ids and canonical squared
+ * distances per query in order (0xFFFFFFFF / FLT_MAX past the end). starts
+ * holds 1 shared or num_queries entry points. With point_label_offsets /
+ * point_labels / query_labels (all or none), only points carrying the query's
+ * label are visited besides the start. 1 <= k <= 64, k <= L <= 256.
+ * Expansions are capped at 16 L + 1024 per query (capped_queries counts hits). */
+int dance_search(const void *h_data, int dtype, uint32_t num_points, uint32_t dim, const uint32_t *h_graph,
+                 const uint32_t *h_degree, uint32_t R, const uint32_t *starts, uint32_t num_starts,
+                 const void *h_queries, uint32_t num_queries, uint32_t k, uint32_t L,
+                 const uint32_t *point_label_offsets, const uint32_t *point_labels, const uint32_t *query_labels,
+                 uint32_t *ids_out, float *dists_out);
+
+/* Same with the base rows, graph and degrees resident in device memory. */
+int dance_search_resident(const void *d_data, int dtype, uint32_t num_points, uint32_t dim, const uint32_t *d_graph,
+                          const uint32_t *d_degree, uint32_t R, const uint32_t *starts, uint32_t num_starts,
+                          const void *h_queries, uint32_t num_queries, uint32_t k, uint32_t L,
+                          const uint32_t *point_label_offsets, const uint32_t *point_labels,
+                          const uint32_t *query_labels, uint32_t *ids_out, float *dists_out);
+
+void dance_get_last_search_stats(DanceSearchStats *stats);
+
 /* ---- stage hooks (host buffers), used by the parity tests ---- */
 
 /* Canonical squared-L2 distances d(a[i], b[i]) (reference distance family,

@@ -25,6 +25,9 @@ Parity status of each oracle function (how it is pinned; see tests/test_oracle.p
                           brute-force ground truth.
   cpu_vamana_build        baseline only (DiskANN restated; parity unpinned:
                           upstream DiskANN is not available offline).
+  query_search            pinned: exact top-k on a complete graph; equal to the
+                          independently written beam_search on integer data
+                          (exact distances).
   filtered_random_graph   pinned: distinct non-self ids, degree min(16, R, N-1),
                           first entry = closed-form hash draw.
   filtered_prune          pinned: equals a greedy in (distance, id) order that
@@ -111,6 +114,9 @@ def lib() -> C.CDLL:
         L.oracle_filtered_merge.argtypes = [u32, u32, u32, u32, _u32p, _u32p, u32, u32, _u32p, _u32p, u32,
                                             _u32p, _f32p, _u32p, _f32p, u32, _u32p, _f32p]
         L.oracle_filtered_merge.restype = u32
+        L.oracle_query_search.argtypes = [vp, i32, u32, u32, _u32p, _u32p, u32, _u32p, u32, vp, u32, u32, u32,
+                                          vp, vp, vp, _u32p, _f32p]
+        L.oracle_query_search.restype = u64
         L.oracle_num_threads.argtypes = []
         L.oracle_num_threads.restype = i32
         _LIB = L
@@ -333,3 +339,22 @@ def filtered_merge(N: int, R: int, C_: int, keep: int, offsets, labels, num_labe
                                     _p(ord_ids), _p(ord_d, C.c_float), ord_ids.shape[0], _p(out_i),
                                     _p(out_d, C.c_float))
     return out_i[:n], out_d[:n]
+
+
+def query_search(data, graph, degree, starts, queries, k, L, label_offsets=None, labels=None, query_labels=None):
+    """Canonical-distance best-first search (DiskANN search semantics);
+    returns (ids, dists, distance count)."""
+    data = np.ascontiguousarray(data)
+    queries = np.ascontiguousarray(queries)
+    graph = np.ascontiguousarray(graph, np.uint32)
+    degree = np.ascontiguousarray(degree, np.uint32)
+    starts = np.atleast_1d(np.asarray(starts, np.uint32))
+    nq = queries.shape[0]
+    ids = np.empty((nq, k), np.uint32)
+    dd = np.empty((nq, k), np.float32)
+    opt = [None if a is None else np.ascontiguousarray(a, np.uint32) for a in (label_offsets, labels, query_labels)]
+    ptrs = [None if a is None else a.ctypes.data for a in opt]
+    n = lib().oracle_query_search(data.ctypes.data, _dt(data), data.shape[0], data.shape[1], _p(graph), _p(degree),
+                                  graph.shape[1], _p(starts), starts.shape[0], queries.ctypes.data, nq, k, L, *ptrs,
+                                  _p(ids), _p(dd, C.c_float))
+    return ids, dd, int(n)

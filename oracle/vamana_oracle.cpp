@@ -623,6 +623,15 @@ extern "C" {
 uint32_t oracle_hash_u32(uint32_t x) { return hash_u32(x); }
 uint32_t oracle_det_neighbor(uint32_t node, uint32_t k, uint32_t N) { return det_neighbor(node, k, N); }
 
+// Canonical distance of two rows given by pointer (a query row and a base row).
+float oracle_distance_rows(const void* a, const void* b, int dtype, uint32_t dim) {
+  switch (dtype) {
+    case DT_F32: return dist_f32((const float*)a, (const float*)b, dim);
+    case DT_U8: return dist_u8((const uint8_t*)a, (const uint8_t*)b, dim);
+    default: return dist_f16((const uint16_t*)a, (const uint16_t*)b, dim);
+  }
+}
+
 float oracle_distance(const void* data, int dtype, uint32_t dim, uint32_t a, uint32_t b) {
   Data D{data, dtype, 0xFFFFFFFFu, dim};
   return D(a, b);
