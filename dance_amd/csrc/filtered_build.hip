@@ -81,11 +81,18 @@ int validate(const FParams& p, const uint32_t* off, const uint32_t* lab, const u
     std::fprintf(stderr, "%s label offsets must start at 0 and end at total_label_count=%u\n", kTag, p.total);
     return -1;
   }
-  for (uint32_t i = 0; i < p.N; ++i)
+  for (uint32_t i = 0; i < p.N; ++i) {
     if (off[i + 1] < off[i]) {
       std::fprintf(stderr, "%s label offsets decrease at point %u\n", kTag, i);
       return -1;
     }
+    // sorted unique labels per point (DiskANN canonicalises them, patch:20269-20286)
+    for (uint32_t j = off[i] + 1; j < off[i + 1]; ++j)
+      if (lab[j] <= lab[j - 1]) {
+        std::fprintf(stderr, "%s labels of point %u are not sorted and unique\n", kTag, i);
+        return -1;
+      }
+  }
   // The reverse CSR needs 2R entries per point of the work capacity (:5839-5846).
   if ((uint64_t)p.N * std::min(p.C, kMaxWorkC) < (uint64_t)2 * p.N * p.R) {
     std::fprintf(stderr, "%s GPU work capacity cannot hold exact reverse CSR\n", kTag);
@@ -97,7 +104,7 @@ int validate(const FParams& p, const uint32_t* off, const uint32_t* lab, const u
 struct FState {
   DevBuf off, lab, lpo, lpts, starts, task_rows;
   DevBuf ga, gb, da, db, tids, td;
-  DevBuf roff, cursor, rids, boff, bd, brem;
+  DevBuf roff, cursor, rids, boff, bd, brem, bmask;
   DevBuf ctr, d32, d64;
   size_t big_cap = 0;
 };
@@ -260,12 +267,13 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
     if (tails[1] > st.big_cap) {
       DCHECK(st.bd.alloc((size_t)tails[1] * 4));
       DCHECK(st.brem.alloc((size_t)tails[1]));
+      DCHECK(st.bmask.alloc((size_t)tails[1] * 4));
       st.big_cap = tails[1];
     }
     hipEvent_t r3 = E.mark(s);
     const Graph Gb{N, R, gb, db};
     CsrArgs Cs{p.alpha, roff, st.rids.as<const uint32_t>(), boff, st.bd.as<float>(), st.brem.as<uint8_t>(),
-               ga, da, ctr};
+               st.bmask.as<uint32_t>(), ga, da, ctr};
     DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
       hipLaunchKernelGGL((k_csr<decltype(dt)::value, decltype(c)::value>), dim3(grid_xcd(N)), dim3(kBlock), csr_lds,
                          s, rows.rs, Gb, Ld, Cs);

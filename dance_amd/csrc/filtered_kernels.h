@@ -128,6 +128,30 @@ __device__ __forceinline__ bool covers(const Labels& L, uint32_t target, uint32_
   return true;
 }
 
+// Bit q is set when c carries the row's q-th label (rows with <= 32 labels).
+// For sorted unique label lists covers(row, s, c) == !(mask(c) & ~mask(s)):
+// the labels shared by row and c are exactly the set bits of mask(c).
+__device__ __forceinline__ uint32_t row_mask(const Labels& L, uint32_t row, uint32_t c) {
+  uint32_t i = L.off[row], j = L.off[c], bits = 0, q = 0;
+  const uint32_t ie = L.off[row + 1], je = L.off[c + 1];
+  while (i < ie && j < je) {
+    const uint32_t x = L.lab[i], y = L.lab[j];
+    if (x == y) {
+      bits |= 1u << q;
+      ++i;
+      ++q;
+      ++j;
+    } else if (x < y) {
+      ++i;
+      ++q;
+    } else {
+      ++j;
+    }
+  }
+  return bits;
+}
+constexpr uint32_t kMaskLabels = 32;
+
 // ---------------------------------------------------------------------------
 // Canonical pool (gpu_vamana_filtered.cu:4156-4263): no early reject; the
 // worst entry is the largest (distance, id); selection takes the smallest
@@ -301,6 +325,10 @@ __device__ __forceinline__ uint32_t prune_regs(const RowSet& rs, const Labels& L
                                                uint32_t rem, uint32_t* lst, float* lsd, uint32_t lane,
                                                uint32_t& outv, uint32_t& ndist) {
   const uint32_t grp = lane >> 3, sub = lane & 7u;
+  const bool use_mask = L.off[row + 1] - L.off[row] <= kMaskLabels;
+  uint32_t msk[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) msk[e] = (use_mask && !((rem >> e) & 1u)) ? row_mask(L, row, id[e]) : 0u;
   uint32_t sel = 0;
   outv = DANCE_INV;
   while (sel < R) {
@@ -321,6 +349,11 @@ __device__ __forceinline__ uint32_t prune_regs(const RowSet& rs, const Labels& L
     if (M == INT_MAX) break;
     const uint32_t I = wave_min_u(bk == M ? bid : DANCE_INV);
     const uint32_t X = wave_min_u(bk == M && bid == I ? bix : DANCE_INV);
+    uint32_t mv = msk[0];
+#pragma unroll
+    for (int e = 1; e < E; ++e)
+      if ((uint32_t)e == (X >> 6)) mv = msk[e];
+    const uint32_t msel = rdlane_u(mv, (int)(X & 63u));
     if (lane == sel) outv = I;
     if (lane == (X & 63u)) rem |= 1u << (X >> 6);
     ++sel;
@@ -328,7 +361,8 @@ __device__ __forceinline__ uint32_t prune_regs(const RowSet& rs, const Labels& L
     load_row<CPL>(rs, I, true, sub, bv);
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      const bool need = !((rem >> e) & 1u) && covers(L, row, I, id[e]);
+      const bool live = !((rem >> e) & 1u);
+      const bool need = live && (use_mask ? (msk[e] & ~msel) == 0u : covers(L, row, I, id[e]));
       const uint64_t m = wballot(need);
       if (m) {
         const uint32_t n = popc64(m), pos = mbcnt64(m);
@@ -353,9 +387,12 @@ __device__ __forceinline__ uint32_t prune_regs(const RowSet& rs, const Labels& L
 template <int DT, int CPL, typename Ids>
 __device__ __forceinline__ uint32_t prune_mem(const RowSet& rs, const Labels& L, uint32_t row, uint32_t R,
                                               float alpha, uint32_t n, Ids&& ids, const float* d, uint8_t* rem,
-                                              uint32_t* lst, float* lsd, uint32_t lane, uint32_t& outv,
-                                              uint32_t& ndist) {
+                                              uint32_t* msk, uint32_t* lst, float* lsd, uint32_t lane,
+                                              uint32_t& outv, uint32_t& ndist) {
   const uint32_t grp = lane >> 3, sub = lane & 7u;
+  const bool use_mask = L.off[row + 1] - L.off[row] <= kMaskLabels;
+  if (use_mask)
+    for (uint32_t i = lane; i < n; i += 64) msk[i] = rem[i] ? 0u : row_mask(L, row, ids(i));
   uint32_t sel = 0;
   outv = DANCE_INV;
   while (sel < R) {
@@ -375,15 +412,18 @@ __device__ __forceinline__ uint32_t prune_mem(const RowSet& rs, const Labels& L,
     if (M == INT_MAX) break;
     const uint32_t I = wave_min_u(bk == M ? bid : DANCE_INV);
     const uint32_t X = wave_min_u(bk == M && bid == I ? bix : DANCE_INV);
+    const bool own = lane == (X & 63u);
+    const uint32_t msel = use_mask ? rdlane_u(own ? msk[X] : 0u, (int)(X & 63u)) : 0u;
     if (lane == sel) outv = I;
-    if (lane == (X & 63u)) rem[X] = 1;
+    if (own) rem[X] = 1;
     ++sel;
     uint4 bv[CPL];
     load_row<CPL>(rs, I, true, sub, bv);
     for (uint32_t b = 0; b < n; b += 64) {
       const uint32_t i = b + lane;
-      const uint32_t c = i < n ? ids(i) : DANCE_INV;
-      const bool need = i < n && !rem[i] && covers(L, row, I, c);
+      const bool live = i < n && !rem[i];
+      const uint32_t c = live ? ids(i) : DANCE_INV;
+      const bool need = live && (use_mask ? (msk[i] & ~msel) == 0u : covers(L, row, I, c));
       const uint64_t m = wballot(need);
       if (!m) continue;
       const uint32_t cnt = popc64(m), pos = mbcnt64(m);
@@ -746,6 +786,7 @@ struct CsrArgs {
   const uint32_t* boff;  // N+1 scratch offsets of long lists
   float* bd;
   uint8_t* brem;
+  uint32_t* bmask;
   uint32_t* gout;
   uint32_t* dout;
   unsigned long long* ctr;
@@ -821,6 +862,7 @@ __global__ __launch_bounds__(kBlock) void k_csr(RowSet rs, Graph G, Labels L, Cs
     const uint32_t base = A.boff[row];
     float* bd = A.bd + base;
     uint8_t* brem = A.brem + base;
+    uint32_t* bmask = A.bmask + base;
     for (uint32_t b = 0; b < n; b += 64) {
       const uint32_t i = b + lane;
       const uint32_t c = i < n ? id_at(i) : DANCE_INV;
@@ -840,7 +882,7 @@ __global__ __launch_bounds__(kBlock) void k_csr(RowSet rs, Graph G, Labels L, Cs
       if (ok) bd[i] = lsd[pos];
       wave_sync();
     }
-    sel = prune_mem<DT, CPL>(rs, L, row, R, A.alpha, n, id_at, bd, brem, lst, lsd, lane, outv, npd);
+    sel = prune_mem<DT, CPL>(rs, L, row, R, A.alpha, n, id_at, bd, brem, bmask, lst, lsd, lane, outv, npd);
   }
   if (lane < R) A.gout[gb + lane] = lane < sel ? outv : DANCE_INV;
   if (lane == 0) {

@@ -21,7 +21,8 @@
  * the reference's release path.
  *
  * Returns 0 on success; -1 on null pointers, invalid sizes (num_points, dim,
- * R or L zero, C < R), malformed label offsets or a runtime error; 1 when the
+ * R or L zero, C < R), malformed label offsets, labels of a point that are
+ * not strictly ascending, or a runtime error; 1 when the
  * GPU work capacity min(C, 128) per point cannot hold the exact reverse CSR
  * (min(C, 128) < 2 * R), as the reference does. Messages go to stderr.
  * Caller owns h_graph (num_points * R, rows padded with 0xFFFFFFFF) and

@@ -90,6 +90,10 @@ def test_filtered_parameter_errors():
     assert F.build_rc(x, ls, st, 8, 16, 16, 64, total=15) == -1          # offsets[N] != total
     bad = F.LabelSet(np.r_[np.arange(9), np.arange(7, 15)].astype(np.uint32), np.zeros(16, np.uint32), 1)
     assert F.build_rc(x, bad, st, 8, 16, 16, 64, total=14) == -1         # offsets decrease
+    # point 0 carries labels [3, 1] (not ascending), points 1..15 label 0
+    unsorted = F.LabelSet(np.r_[0, np.arange(2, 18)].astype(np.uint32), np.r_[3, 1, np.zeros(15)].astype(np.uint32), 4)
+    assert unsorted.offsets.shape[0] == 17 and unsorted.offsets[-1] == unsorted.labels.shape[0]
+    assert F.build_rc(x, unsorted, np.zeros(4, np.uint32), 8, 16, 16, 64) == -1  # labels not ascending
     assert F.build_rc(x, ls, st, 40, 16, 16, 64) == 1                    # min(C,128) < 2R
     assert F.build_rc(xf, ls, st, 70, 16, 16, 750) == 1                  # 128 < 140
     assert F.build_rc(x, ls, st, 8, 16, 16, 64, rounds=4) == -1          # extension: rounds <= 3
