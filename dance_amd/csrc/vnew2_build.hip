@@ -18,7 +18,7 @@
 // build; V = bytes of one vector row, counted on device by each wave):
 //   search: (search_dist + insert_dist) * V + expansions * (4R + 4)
 //           + N * (V + 4R + 4 + 16C)            (own vector, cur row, work row r/w)
-//   merge : merge_dist * V + reverse_edges * 4 + touched_rows * (V + 16C + 8)
+//   merge : merge_dist * 4 (snapshot distance) + reverse_edges * 4 + touched_rows * (16C + 8)
 //   prune : prune_dist * V + (selected rows) * V + N * 24C
 //   reverse (keys + sort): N*R*(4*3) + passes * N*R * 20
 
@@ -178,7 +178,7 @@ static int launch_prune(const Rows& rows, GraphBufs g, uint32_t min_degree, floa
 }
 
 struct ReverseWs {
-  DevBuf keys[2], vals[2], offs, order;
+  DevBuf keys[2], vals[2], offs, order, snap;
   SortWorkspace sort;
   ScanWorkspace scan;
   int alloc(uint32_t N, uint32_t R) {
@@ -187,19 +187,21 @@ struct ReverseWs {
       DCHECK(keys[i].alloc(std::max<size_t>(items, 1) * 4));
       DCHECK(vals[i].alloc(std::max<size_t>(items, 1) * 4));
     }
+    DCHECK(snap.alloc(std::max<size_t>(items, 1) * 4));
     DCHECK(offs.alloc(((size_t)N + 1) * 4));
     return 0;
   }
 };
 
 // Reverse CSR in canonical (ascending source) order. Returns the sorted
-// source array through *srcs_out.
+// forward slots (s*R + i) through *srcs_out; ws.snap holds their distances.
 static int build_reverse_csr(GraphBufs g, ReverseWs& ws, hipStream_t s, const uint32_t** srcs_out) {
   const size_t items = (size_t)g.N * g.R;
   DHIP(hipMemsetAsync(ws.offs.p, 0, ((size_t)g.N + 1) * 4, s));
   if (items > 0) {
-    hipLaunchKernelGGL(k_rev_keys, dim3((uint32_t)((items + 255) / 256)), dim3(256), 0, s, g.work, g.deg_work, g.N,
-                       g.R, g.C, ws.keys[0].as<uint32_t>(), ws.vals[0].as<uint32_t>(), ws.offs.as<uint32_t>());
+    hipLaunchKernelGGL(k_rev_keys, dim3((uint32_t)((items + 255) / 256)), dim3(256), 0, s, g.work, g.deg_work, g.wd,
+                       g.N, g.R, g.C, ws.keys[0].as<uint32_t>(), ws.vals[0].as<uint32_t>(), ws.snap.as<float>(),
+                       ws.offs.as<uint32_t>());
     DHIP(hipGetLastError());
   }
   DCHECK(scan_exclusive(ws.offs.as<uint32_t>(), (size_t)g.N + 1, ws.scan, s));
@@ -211,15 +213,23 @@ static int build_reverse_csr(GraphBufs g, ReverseWs& ws, hipStream_t s, const ui
   return 0;
 }
 
-static int launch_merge(const Rows& rows, GraphBufs g, const uint32_t* offs, const uint32_t* srcs,
+static int launch_merge(const Rows& rows, GraphBufs g, const uint32_t* offs, const uint32_t* srcs, const float* snap,
                         const Profile& prof, const uint32_t* order, VCounters* ctr, hipStream_t s) {
   const int cpl = pick_cpl(rows.rs.nch);
   const uint32_t Cp = round64(g.C);
-  const size_t lds = (size_t)kWavesPerBlock * merge_lds_words(Cp) * 4;
-  MergeArgs a{rows.rs, g, offs, srcs, prof.heavy_threshold, prof.heavy_sample, order, ctr};
+  MergeArgs a{rows.rs, g, offs, srcs, snap, prof.heavy_threshold, prof.heavy_sample, order, ctr};
   return with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
-    hipLaunchKernelGGL((k_merge<decltype(dt)::value, decltype(c)::value>), dim3(xcd_grid(g.N)), dim3(kBlock), lds,
-                       s, a, Cp);
+    constexpr int DT = decltype(dt)::value, CPL = decltype(c)::value;
+    const size_t rl = (size_t)kWavesPerBlock * merge_reg_lds_words() * 4;
+    if (g.C <= 64)
+      hipLaunchKernelGGL((k_merge_reg<DT, CPL, 1>), dim3(xcd_grid(g.N)), dim3(kBlock), rl, s, a);
+    else if (g.C <= 128)
+      hipLaunchKernelGGL((k_merge_reg<DT, CPL, 2>), dim3(xcd_grid(g.N)), dim3(kBlock), rl, s, a);
+    else if (g.C <= 256)
+      hipLaunchKernelGGL((k_merge_reg<DT, CPL, 4>), dim3(xcd_grid(g.N)), dim3(kBlock), rl, s, a);
+    else
+      hipLaunchKernelGGL((k_merge<DT, CPL>), dim3(xcd_grid(g.N)), dim3(kBlock),
+                         (size_t)kWavesPerBlock * merge_lds_words(Cp) * 4, s, a, Cp);
     DHIP(hipGetLastError());
     return 0;
   });
@@ -386,7 +396,7 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     const uint32_t* srcs = nullptr;
     DCHECK(build_reverse_csr(g, rws, s, &srcs));
     DHIP(hipEventRecord(iev[it].r1, s));
-    DCHECK(launch_merge(rows, g, rws.offs.as<uint32_t>(), srcs, prof, order, ctr, s));
+    DCHECK(launch_merge(rows, g, rws.offs.as<uint32_t>(), srcs, rws.snap.as<float>(), prof, order, ctr, s));
     DHIP(hipEventRecord(iev[it].m1, s));
     const uint32_t md = (it + 1 == kIters) ? kFinalMinDegree : 0u;
     DCHECK(launch_prune(rows, g, md, alpha, order, ctr, s));
@@ -426,19 +436,19 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   const double V = rows.vbytes();
   p.search_bytes = (double)(p.search_dist + p.insert_dist) * V + (double)p.expansions * (4.0 * R + 4.0) +
                    (double)kIters * N * (V + 4.0 * R + 4.0 + 16.0 * C);
-  p.merge_bytes = (double)p.merge_dist * V + (double)p.reverse_edges * 4.0 +
-                  (double)p.touched_rows * (V + 16.0 * C + 8.0);
+  p.merge_bytes = (double)p.merge_dist * 4.0 + (double)p.reverse_edges * 4.0 +
+                  (double)p.touched_rows * (16.0 * C + 8.0);
   p.prune_bytes = (double)p.prune_dist * V + (double)kIters * N * (24.0 * C);
   const double items = (double)N * R;
   const double passes = (bit_length(N) + 7) / 8;
-  p.reverse_bytes = (double)kIters * (items * 12.0 + passes * items * 20.0);
+  p.reverse_bytes = (double)kIters * (items * 16.0 + passes * items * 20.0);
   if (kp) *kp = p;
   if (stats) {
     stats->search_online_insert_seconds = p.search_ms * 1e-3;
     stats->reverse_seconds = (p.reverse_ms + p.merge_ms) * 1e-3;
     stats->reverse_csr_seconds = p.reverse_ms * 1e-3;
     stats->final_prune_seconds = p.prune_ms * 1e-3;
-    stats->distance_computations = p.search_dist + p.insert_dist + p.merge_dist + p.prune_dist;
+    stats->distance_computations = p.search_dist + p.insert_dist + p.prune_dist;
     stats->online_insert_attempts = hc_ctr.insert_try;
     stats->online_insert_mutations = hc_ctr.insert_mut;
     stats->reverse_proposals = p.reverse_edges;
@@ -806,9 +816,13 @@ int dance_stage_reverse_merge(const void* h_data, int dtype, uint32_t N, uint32_
   DCHECK(down(off.data(), rws.offs.p, ((size_t)N + 1) * 4, cx.s));
   DHIP(hipStreamSynchronize(cx.s));
   if (offsets) std::memcpy(offsets, off.data(), off.size() * 4);
-  if (ids) DCHECK(down(ids, srcs, (size_t)off[N] * 4, cx.s));
+  if (ids) {
+    DCHECK(down(ids, srcs, (size_t)off[N] * 4, cx.s));
+    DHIP(hipStreamSynchronize(cx.s));
+    for (uint32_t e = 0; e < off[N]; ++e) ids[e] /= R;  // forward slot -> source
+  }
   Profile prof{"stage", false, heavy_threshold, heavy_sample};
-  DCHECK(launch_merge(cx.rows, g, rws.offs.as<uint32_t>(), srcs, prof, nullptr, nullptr, cx.s));
+  DCHECK(launch_merge(cx.rows, g, rws.offs.as<uint32_t>(), srcs, rws.snap.as<float>(), prof, nullptr, nullptr, cx.s));
   return download_state(cx.st, nullptr, nullptr, work, deg_work, wd, cx.s);
 }
 

@@ -44,7 +44,7 @@ struct VCounters {
   unsigned long long vis_skips;     // candidates skipped by the visited cache
   unsigned long long insert_mut;    // online-insert mutations of the work row
   unsigned long long insert_try;    // online-insert attempts
-  unsigned long long merge_dist;    // reverse-merge distances
+  unsigned long long merge_dist;    // reverse-merge candidates (distance from the slot snapshot)
   unsigned long long prune_dist;    // prune pair distances
   unsigned long long reverse_edges; // reverse proposals
   unsigned long long touched_rows;  // targets with at least one reverse edge
@@ -666,22 +666,31 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
 }
 
 // ---------------------------------------------------------------------------
-// Reverse edges. k_rev_keys emits one (target, source) item per forward slot
-// in source order; a stable LSD radix sort by target then yields every segment
-// in ascending source order. k_merge is reverse_merge_csr_kernel
-// (vnew2.cu:1722-1814) over those canonical segments.
+// Reverse edges. k_rev_keys emits one (target, slot) item per forward slot j =
+// s*R + i in source order and snapshots that slot's stored distance; a stable
+// LSD radix sort by target then yields every segment in ascending source
+// order. k_merge is reverse_merge_csr_kernel (vnew2.cu:1722-1814) over those
+// canonical segments. The reference recomputes d(t, s) for each reverse
+// candidate; here it is read from the snapshot of s's forward entry, which
+// holds d(s, t): every writer of a work row stores the canonical distance of
+// the row's vertex to the entry (init, search, online insert, merge, prune
+// keep them), and the canonical distance is bitwise symmetric (a-b and b-a
+// differ only in sign). The snapshot is taken before any merge writes rows.
 // ---------------------------------------------------------------------------
-static __global__ void k_rev_keys(const uint32_t* __restrict__ work, const uint32_t* __restrict__ deg_work, uint32_t N,
-                           uint32_t R, uint32_t C, uint32_t* __restrict__ keys, uint32_t* __restrict__ vals,
-                           uint32_t* __restrict__ indeg) {
+static __global__ void k_rev_keys(const uint32_t* __restrict__ work, const uint32_t* __restrict__ deg_work,
+                                  const float* __restrict__ wd, uint32_t N, uint32_t R, uint32_t C,
+                                  uint32_t* __restrict__ keys, uint32_t* __restrict__ vals,
+                                  float* __restrict__ snap, uint32_t* __restrict__ indeg) {
   const size_t j = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= (size_t)N * R) return;
   const uint32_t s = (uint32_t)(j / R), i = (uint32_t)(j % R);
   const uint32_t deg = min(deg_work[s], R);
-  const uint32_t t = i < deg ? work[(size_t)s * C + i] : DANCE_INV;
+  const size_t wi = (size_t)s * C + i;
+  const uint32_t t = i < deg ? work[wi] : DANCE_INV;
   const bool v = t != DANCE_INV && t < N && t != s;
   keys[j] = v ? t : N;
-  vals[j] = s;
+  vals[j] = (uint32_t)j;
+  snap[j] = v ? wd[wi] : FLT_MAX;
   if (v) atomicAdd(&indeg[t], 1u);
 }
 
@@ -689,7 +698,8 @@ struct MergeArgs {
   RowSet rs;
   GraphBufs g;
   const uint32_t* offsets;  // N+1
-  const uint32_t* srcs;     // sorted sources
+  const uint32_t* srcs;     // sorted forward slots s*R + i
+  const float* snap;        // distance of forward slot j
   uint32_t heavy_threshold, heavy_sample;
   const uint32_t* order;
   VCounters* ctr;
@@ -705,8 +715,8 @@ __global__ __launch_bounds__(kBlock) void k_merge(MergeArgs a, uint32_t Cp) {
   const GraphBufs& g = a.g;
   if (gw >= g.N) return;
   const uint32_t t = a.order ? a.order[gw] : gw;
-  const uint32_t N = g.N, C = g.C;
-  const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;
+  const uint32_t N = g.N, C = g.C, R = g.R;
+  const uint32_t lane = lane_id();
   uint32_t* wid = smem + w * merge_lds_words(Cp);
   float* wdd = reinterpret_cast<float*>(wid + Cp);
   uint32_t* lst = wid + 2 * Cp;
@@ -725,20 +735,19 @@ __global__ __launch_bounds__(kBlock) void k_merge(MergeArgs a, uint32_t Cp) {
     wid[i] = i < C ? g.work[wb + i] : DANCE_INV;
     wdd[i] = i < C ? g.wd[wb + i] : -FLT_MAX;
   }
-  uint4 tv[CPL];
-  load_row<CPL>(a.rs, t, true, sub, tv);
   wave_sync();
   bool worst_ok = false;
   int wpos = -1;
   float wdist = -FLT_MAX;
-  uint32_t ndist = 0;
+  uint32_t ncand = 0;
   for (uint32_t b = 0; b < count; b += 64) {
     const uint32_t k = b + lane;
-    uint32_t src = DANCE_INV;
+    uint32_t src = DANCE_INV, slot = 0;
     if (k < count) {
       const uint32_t idx =
           count < indeg ? begin + (uint32_t)(((unsigned long long)k * indeg) / count) : begin + k;
-      src = a.srcs[idx];
+      slot = a.srcs[idx];
+      src = slot / R;
     }
     const bool v = valid_for(src, N, t);
     bool inrow = false;
@@ -747,12 +756,15 @@ __global__ __launch_bounds__(kBlock) void k_merge(MergeArgs a, uint32_t Cp) {
     const uint64_t m = wballot(need);
     const uint32_t n = popc64(m);
     if (n == 0) continue;
-    if (need) lst[mbcnt64(m)] = src;
+    if (need) {
+      lst[mbcnt64(m)] = src;
+      lsd[mbcnt64(m)] = a.snap[slot];
+    }
     wave_sync();
-    batch_dist<DT, CPL>(a.rs, tv, lst, lsd, n, grp, sub);
-    ndist += n;
+    ncand += n;
     const uint32_t ck = lane < n ? lst[lane] : DANCE_INV;
     const float dk = lane < n ? lsd[lane] : FLT_MAX;
+    wave_sync();
     for (uint32_t kk = 0; kk < n; ++kk) {
       const uint32_t s = rdlane_u(ck, (int)kk);
       const float ds = rdlane_f(dk, (int)kk);
@@ -806,7 +818,164 @@ __global__ __launch_bounds__(kBlock) void k_merge(MergeArgs a, uint32_t Cp) {
   if (lane == 0) {
     g.deg_work[t] = deg;
     if (a.ctr) {
-      atomicAdd(&a.ctr->merge_dist, (unsigned long long)ndist);
+      atomicAdd(&a.ctr->merge_dist, (unsigned long long)ncand);
+      atomicAdd(&a.ctr->reverse_edges, (unsigned long long)indeg);
+      atomicAdd(&a.ctr->touched_rows, 1ull);
+    }
+  }
+}
+
+// Register-resident variant of k_merge for C <= 64*MS: the work row lives in
+// MS VGPRs per lane (entry i = lane i % 64, slot i / 64), so membership tests
+// are ballots and the worst-slot search is one wave reduction. Same decisions
+// as k_merge (reverse_merge_csr_kernel, vnew2.cu:1722-1814): per candidate in
+// source order, skip if present, append while deg < C, else replace the
+// largest distance (lowest slot on ties) when strictly closer.
+template <int MS>
+struct MergeRow {
+  uint32_t id[MS];
+  float d[MS];
+  __device__ __forceinline__ uint32_t id_at(uint32_t i) const {
+    uint32_t v = id[0];
+#pragma unroll
+    for (int s = 1; s < MS; ++s)
+      if ((i >> 6) == (uint32_t)s) v = id[s];
+    return rdlane_u(v, (int)(i & 63u));
+  }
+  __device__ __forceinline__ bool contains(uint32_t x, uint32_t deg, uint32_t lane) const {
+    uint64_t m = 0;
+#pragma unroll
+    for (int s = 0; s < MS; ++s) m |= wballot((uint32_t)s * 64u + lane < deg && id[s] == x);
+    return m != 0;
+  }
+  __device__ __forceinline__ void set(uint32_t i, uint32_t x, float dist, uint32_t lane) {
+    if (lane == (i & 63u)) {
+#pragma unroll
+      for (int s = 0; s < MS; ++s)
+        if ((i >> 6) == (uint32_t)s) {
+          id[s] = x;
+          d[s] = dist;
+        }
+    }
+  }
+  // Largest non-NaN distance over [0, C) and its lowest slot; -1 when none
+  // exceeds -FLT_MAX.
+  __device__ __forceinline__ int worst(uint32_t C, uint32_t lane, float* wdist) const {
+    int best = INT_MIN;
+    uint32_t bi = 0xFFFFFFFFu;
+#pragma unroll
+    for (int s = 0; s < MS; ++s) {
+      const uint32_t i = (uint32_t)s * 64u + lane;
+      if (i < C && d[s] == d[s]) {
+        const int k = fkey(d[s]);
+        if (k > best) {
+          best = k;
+          bi = i;
+        }
+      }
+    }
+    const int M = wave_max_i(best);
+    *wdist = -FLT_MAX;
+    if (M == INT_MIN || !(__int_as_float(M) > -FLT_MAX)) return -1;
+    *wdist = __int_as_float(M);
+    return (int)wave_min_u(best == M ? bi : 0xFFFFFFFFu);
+  }
+};
+
+__host__ __device__ constexpr uint32_t merge_reg_lds_words() { return 128u; }
+
+template <int DT, int CPL, int MS>
+__global__ __launch_bounds__(kBlock) void k_merge_reg(MergeArgs a) {
+  extern __shared__ uint32_t smem[];
+  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t gw = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + w;
+  const GraphBufs& g = a.g;
+  if (gw >= g.N) return;
+  const uint32_t t = a.order ? a.order[gw] : gw;
+  const uint32_t N = g.N, C = g.C, R = g.R;
+  const uint32_t lane = lane_id();
+  uint32_t* lst = smem + w * merge_reg_lds_words();
+  float* lsd = reinterpret_cast<float*>(lst + 64);
+  const uint32_t begin = a.offsets[t], end = a.offsets[t + 1];
+  const uint32_t indeg = end - begin;
+  if (indeg == 0) return;
+  uint32_t count = indeg;
+  if (a.heavy_threshold != 0 && indeg > a.heavy_threshold) {
+    count = min(a.heavy_sample, indeg);
+    if (count == 0) count = 1;
+  }
+  const size_t wb = (size_t)t * C;
+  uint32_t deg = min(g.deg_work[t], C);
+  MergeRow<MS> row;
+#pragma unroll
+  for (int s = 0; s < MS; ++s) {
+    const uint32_t i = (uint32_t)s * 64u + lane;
+    row.id[s] = i < C ? g.work[wb + i] : DANCE_INV;
+    row.d[s] = i < C ? g.wd[wb + i] : -FLT_MAX;
+  }
+  bool worst_ok = false;
+  int wpos = -1;
+  float wdist = -FLT_MAX;
+  uint32_t ncand = 0;
+  for (uint32_t b = 0; b < count; b += 64) {
+    const uint32_t k = b + lane;
+    uint32_t src = DANCE_INV, slot = 0;
+    if (k < count) {
+      const uint32_t idx =
+          count < indeg ? begin + (uint32_t)(((unsigned long long)k * indeg) / count) : begin + k;
+      slot = a.srcs[idx];
+      src = slot / R;
+    }
+    const bool v = valid_for(src, N, t);
+    bool inrow = false;
+    if (wballot(v))
+      for (uint32_t j = 0; j < deg; ++j) inrow |= row.id_at(j) == src;
+    const bool need = v && !inrow;
+    const uint64_t m = wballot(need);
+    const uint32_t n = popc64(m);
+    if (n == 0) continue;
+    if (need) {
+      lst[mbcnt64(m)] = src;
+      lsd[mbcnt64(m)] = a.snap[slot];
+    }
+    wave_sync();
+    ncand += n;
+    const uint32_t ck = lane < n ? lst[lane] : DANCE_INV;
+    const float dk = lane < n ? lsd[lane] : FLT_MAX;
+    wave_sync();
+    for (uint32_t kk = 0; kk < n; ++kk) {
+      const uint32_t s = rdlane_u(ck, (int)kk);
+      const float ds = rdlane_f(dk, (int)kk);
+      if (deg == C && worst_ok && !(wpos >= 0 && ds < wdist)) continue;  // rejected either way
+      if (row.contains(s, deg, lane)) continue;
+      if (deg < C) {
+        row.set(deg, s, ds, lane);
+        ++deg;
+        worst_ok = false;
+        continue;
+      }
+      if (!worst_ok) {
+        wpos = row.worst(C, lane, &wdist);
+        worst_ok = true;
+      }
+      if (wpos >= 0 && ds < wdist) {
+        row.set((uint32_t)wpos, s, ds, lane);
+        worst_ok = false;
+      }
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < MS; ++s) {
+    const uint32_t i = (uint32_t)s * 64u + lane;
+    if (i < C) {
+      g.work[wb + i] = row.id[s];
+      g.wd[wb + i] = row.d[s];
+    }
+  }
+  if (lane == 0) {
+    g.deg_work[t] = deg;
+    if (a.ctr) {
+      atomicAdd(&a.ctr->merge_dist, (unsigned long long)ncand);
       atomicAdd(&a.ctr->reverse_edges, (unsigned long long)indeg);
       atomicAdd(&a.ctr->touched_rows, 1ull);
     }

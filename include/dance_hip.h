@@ -147,7 +147,10 @@ int dance_stage_search(const void *h_data, int dtype, uint32_t num_points, uint3
 
 /* Reverse CSR + merge (reverse_count/fill_csr_kernel + reverse_merge_csr_kernel,
  * src/gpu_vamana_vnew2.cu:1604-1661, 1722-1814). offsets (N+1) and ids (N*R)
- * receive the canonical CSR when non-null. */
+ * receive the canonical CSR when non-null. Precondition, as in every work row
+ * the build produces: the stored distance of each valid entry among the first
+ * R is the canonical distance of the row's vertex to it (the merge reads it
+ * instead of recomputing the symmetric distance). */
 int dance_stage_reverse_merge(const void *h_data, int dtype, uint32_t num_points, uint32_t dim, uint32_t R,
                               uint32_t C, uint32_t *work, uint32_t *deg_work, float *wd, uint32_t heavy_threshold,
                               uint32_t heavy_sample, uint32_t *offsets, uint32_t *ids);
