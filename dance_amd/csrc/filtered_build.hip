@@ -194,10 +194,10 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   DCHECK(st.cursor.alloc((size_t)N * 4));
   DCHECK(st.rids.alloc(std::max<size_t>(1, NR) * 4));
   DCHECK(st.boff.alloc((size_t)(N + 1) * 4));
-  DCHECK(st.ctr.alloc(kNumCounters * 8));
+  DCHECK(st.ctr.alloc((size_t)kCtrStripes * kNumCounters * 8));
   DCHECK(st.d32.alloc(8 * 4));
   DCHECK(st.d64.alloc(8 * 8));
-  DHIP(hipMemsetAsync(st.ctr.p, 0, kNumCounters * 8, s));
+  DHIP(hipMemsetAsync(st.ctr.p, 0, (size_t)kCtrStripes * kNumCounters * 8, s));
   unsigned long long* ctr = st.ctr.as<unsigned long long>();
   ScanWorkspace scan;
 
@@ -300,11 +300,13 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   DHIP(hipGetLastError());
   hipEvent_t g1 = E.mark(s);
   uint32_t h32[8];
-  unsigned long long h64[8], hc[kNumCounters];
+  unsigned long long h64[8], hc[kNumCounters] = {};
+  std::vector<unsigned long long> stripes((size_t)kCtrStripes * kNumCounters);
   DHIP(hipMemcpyAsync(h32, st.d32.p, sizeof(h32), hipMemcpyDeviceToHost, s));
   DHIP(hipMemcpyAsync(h64, st.d64.p, sizeof(h64), hipMemcpyDeviceToHost, s));
-  DHIP(hipMemcpyAsync(hc, st.ctr.p, sizeof(hc), hipMemcpyDeviceToHost, s));
+  DHIP(hipMemcpyAsync(stripes.data(), st.ctr.p, stripes.size() * 8, hipMemcpyDeviceToHost, s));
   DHIP(hipStreamSynchronize(s));
+  for (size_t i = 0; i < stripes.size(); ++i) hc[i % kNumCounters] += stripes[i];
 
   // Published stats follow the reference's release path (:8648-8718): search
   // counters are reported as zero there and the candidate counts are the

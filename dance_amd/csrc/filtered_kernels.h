@@ -56,6 +56,12 @@ enum : uint32_t {
   kBigRows,
   kNumCounters
 };
+// Counters are striped over kCtrStripes copies (by workgroup) so that per-wave
+// atomics do not serialise on one address; the host sums the stripes.
+constexpr uint32_t kCtrStripes = 64;
+__device__ __forceinline__ unsigned long long* ctr_at(unsigned long long* base, uint32_t idx) {
+  return base + (size_t)(blockIdx.x & (kCtrStripes - 1u)) * kNumCounters + idx;
+}
 
 struct Labels {
   const uint32_t* off;     // N+1: point -> label list offsets
@@ -510,7 +516,7 @@ __global__ __launch_bounds__(kBlock) void k_task_search(RowSet rs, Graph G, Labe
     out_ids[ob + lane] = h ? S.P.id : DANCE_INV;
     out_d[ob + lane] = h ? S.P.d : FLT_MAX;
   }
-  if (ctr && lane == 0) atomicAdd(ctr + kTaskDist, (unsigned long long)S.ndist);
+  if (ctr && lane == 0) atomicAdd(ctr_at(ctr, kTaskDist), (unsigned long long)S.ndist);
 }
 
 struct RowArgs {
@@ -695,7 +701,7 @@ __global__ __launch_bounds__(kBlock) void k_row(RowSet rs, Graph G, Labels L, Ro
     M.id1 = lane + 64 < kept ? sid[lane + 64] : DANCE_INV;
     M.d1 = lane + 64 < kept ? sd[lane + 64] : FLT_MAX;
     wave_sync();
-    if (A.ctr && lane == 0) atomicAdd(A.ctr + kQuotaDropped, (unsigned long long)(count - kept));
+    if (A.ctr && lane == 0) atomicAdd(ctr_at(A.ctr, kQuotaDropped), (unsigned long long)(count - kept));
     count = kept;
   }
 
@@ -729,10 +735,10 @@ __global__ __launch_bounds__(kBlock) void k_row(RowSet rs, Graph G, Labels L, Ro
   if (lane == 0) {
     A.dout[row] = sel;
     if (A.ctr) {
-      atomicAdd(A.ctr + kUnionDist, (unsigned long long)ndist_union);
-      atomicAdd(A.ctr + kWorkDist, (unsigned long long)ndist_work);
-      atomicAdd(A.ctr + kPruneDist, (unsigned long long)ndist_prune);
-      atomicAdd(A.ctr + kMergedCands, (unsigned long long)count);
+      atomicAdd(ctr_at(A.ctr, kUnionDist), (unsigned long long)ndist_union);
+      atomicAdd(ctr_at(A.ctr, kWorkDist), (unsigned long long)ndist_work);
+      atomicAdd(ctr_at(A.ctr, kPruneDist), (unsigned long long)ndist_prune);
+      atomicAdd(ctr_at(A.ctr, kMergedCands), (unsigned long long)count);
     }
   }
 }
@@ -888,11 +894,11 @@ __global__ __launch_bounds__(kBlock) void k_csr(RowSet rs, Graph G, Labels L, Cs
   if (lane == 0) {
     A.dout[row] = sel;
     if (A.ctr) {
-      atomicAdd(A.ctr + kCsrDist, (unsigned long long)nd);
-      atomicAdd(A.ctr + kCsrPruneDist, (unsigned long long)npd);
-      atomicAdd(A.ctr + kTouchedRows, 1ull);
-      atomicAdd(A.ctr + kCsrCandidates, (unsigned long long)nlive);
-      if (n > kCsrRegMax) atomicAdd(A.ctr + kBigRows, 1ull);
+      atomicAdd(ctr_at(A.ctr, kCsrDist), (unsigned long long)nd);
+      atomicAdd(ctr_at(A.ctr, kCsrPruneDist), (unsigned long long)npd);
+      atomicAdd(ctr_at(A.ctr, kTouchedRows), 1ull);
+      atomicAdd(ctr_at(A.ctr, kCsrCandidates), (unsigned long long)nlive);
+      if (n > kCsrRegMax) atomicAdd(ctr_at(A.ctr, kBigRows), 1ull);
     }
   }
 }
@@ -903,10 +909,10 @@ __global__ __launch_bounds__(kBlock) void k_csr(RowSet rs, Graph G, Labels L, Cs
 // label_rejects, universal_passes.
 static __global__ void k_diagnostics(Graph G, Labels L, uint32_t* d32, unsigned long long* d64) {
   const uint32_t row = blockIdx.x * blockDim.x + threadIdx.x;
-  if (row >= G.N) return;
-  const uint32_t deg = G.d[row];
+  const bool in = row < G.N;
+  const uint32_t deg = in ? G.d[row] : 0u;
   uint32_t invalid = 0, self = 0, common = 0, checks = 0, uni = 0;
-  const uint32_t n = min(deg, G.R);
+  const uint32_t n = in ? min(deg, G.R) : 0u;
   for (uint32_t j = 0; j < n; ++j) {
     const uint32_t nb = G.g[(size_t)row * G.R + j];
     if (nb >= G.N) {
@@ -938,20 +944,32 @@ static __global__ void k_diagnostics(Graph G, Labels L, uint32_t* d32, unsigned 
         ++k;
     }
   }
-  if (invalid) atomicAdd(d32 + 0, invalid);
-  if (self) atomicAdd(d32 + 1, self);
-  if (common < 2) atomicAdd(d32 + 2, 1u);
-  atomicMin(d32 + 3, deg);
-  atomicMax(d32 + 4, deg);
-  atomicMin(d32 + 5, common);
-  atomicMax(d32 + 6, common);
-  atomicAdd(d64 + 0, (unsigned long long)deg);
-  atomicAdd(d64 + 1, (unsigned long long)common);
-  if (checks) {
-    atomicAdd(d64 + 2, (unsigned long long)checks);
-    atomicAdd(d64 + 3, (unsigned long long)(checks - common));
+  // one atomic per wave and counter (wave sums fit in 32 bits: <= 64 * R)
+  auto add = [](int a, int b) { return a + b; };
+  const uint32_t s_invalid = (uint32_t)wave_reduce_i((int)invalid, 0, add);
+  const uint32_t s_self = (uint32_t)wave_reduce_i((int)self, 0, add);
+  const uint32_t s_low = (uint32_t)wave_reduce_i(in && common < 2 ? 1 : 0, 0, add);
+  const uint32_t s_deg = (uint32_t)wave_reduce_i((int)deg, 0, add);
+  const uint32_t s_common = (uint32_t)wave_reduce_i((int)common, 0, add);
+  const uint32_t s_checks = (uint32_t)wave_reduce_i((int)checks, 0, add);
+  const uint32_t s_uni = (uint32_t)wave_reduce_i((int)uni, 0, add);
+  const uint32_t mn_deg = wave_min_u(in ? deg : 0xFFFFFFFFu), mx_deg = wave_max_u(deg);
+  const uint32_t mn_com = wave_min_u(in ? common : 0xFFFFFFFFu), mx_com = wave_max_u(common);
+  const bool any_row = wballot(in) != 0ull;
+  if (lane_id() == 0 && any_row) {
+    if (s_invalid) atomicAdd(d32 + 0, s_invalid);
+    if (s_self) atomicAdd(d32 + 1, s_self);
+    if (s_low) atomicAdd(d32 + 2, s_low);
+    atomicMin(d32 + 3, mn_deg);
+    atomicMax(d32 + 4, mx_deg);
+    atomicMin(d32 + 5, mn_com);
+    atomicMax(d32 + 6, mx_com);
+    atomicAdd(d64 + 0, (unsigned long long)s_deg);
+    atomicAdd(d64 + 1, (unsigned long long)s_common);
+    atomicAdd(d64 + 2, (unsigned long long)s_checks);
+    atomicAdd(d64 + 3, (unsigned long long)(s_checks - s_common));
+    if (s_uni) atomicAdd(d64 + 4, (unsigned long long)s_uni);
   }
-  if (uni) atomicAdd(d64 + 4, (unsigned long long)uni);
 }
 
 }  // namespace filt

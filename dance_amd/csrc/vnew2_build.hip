@@ -336,8 +336,8 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   ReverseWs rws;
   DCHECK(rws.alloc(N, R));
   DevBuf ctr_buf, scores, cands;
-  DCHECK(ctr_buf.alloc(sizeof(VCounters)));
-  DHIP(hipMemsetAsync(ctr_buf.p, 0, sizeof(VCounters), s));
+  DCHECK(ctr_buf.alloc(sizeof(VCounters) * kCtrStripes));
+  DHIP(hipMemsetAsync(ctr_buf.p, 0, sizeof(VCounters) * kCtrStripes, s));
   VCounters* ctr = ctr_buf.as<VCounters>();
   GraphBufs g = st.g();
   StageEvents E;
@@ -406,7 +406,17 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   DHIP(hipGetLastError());
 
   VCounters hc_ctr{};
-  DHIP(hipMemcpy(&hc_ctr, ctr_buf.p, sizeof(VCounters), hipMemcpyDeviceToHost));
+  {
+    std::vector<VCounters> stripes(kCtrStripes);
+    DHIP(hipMemcpy(stripes.data(), ctr_buf.p, sizeof(VCounters) * kCtrStripes, hipMemcpyDeviceToHost));
+    static_assert(sizeof(VCounters) % sizeof(unsigned long long) == 0, "VCounters holds u64 fields only");
+    const size_t nf = sizeof(VCounters) / sizeof(unsigned long long);
+    auto* dst = reinterpret_cast<unsigned long long*>(&hc_ctr);
+    for (const VCounters& st : stripes) {
+      const auto* src = reinterpret_cast<const unsigned long long*>(&st);
+      for (size_t f = 0; f < nf; ++f) dst[f] += src[f];
+    }
+  }
   DanceKernelProfile p{};
   p.iterations = kIters;
   p.vector_bytes = rows.vbytes();

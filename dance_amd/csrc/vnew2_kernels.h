@@ -53,6 +53,15 @@ struct VCounters {
   unsigned long long cyc_select, cyc_insert, cyc_dist, cyc_pool, cyc_seed, cyc_total;
 };
 
+// Counters are striped over kCtrStripes copies (by workgroup) so that the
+// per-wave atomics of millions of waves do not serialise on one address; the
+// host sums the stripes.
+constexpr uint32_t kCtrStripes = 64;
+__device__ __forceinline__ VCounters* ctr_stripe(VCounters* base) {
+  return base + (blockIdx.x & (kCtrStripes - 1u));
+}
+
+
 struct GraphBufs {
   uint32_t N, R, C;
   uint32_t* cur;       // N x R
@@ -486,19 +495,19 @@ struct SearchWave {
     if (a.ctr) {
       const uint64_t m = wballot(true);
       if (lane == (uint32_t)ffs64(m)) {
-        atomicAdd(&a.ctr->search_dist, (unsigned long long)n_search);
-        atomicAdd(&a.ctr->insert_dist, (unsigned long long)n_insert);
-        atomicAdd(&a.ctr->expansions, (unsigned long long)n_exp);
-        atomicAdd(&a.ctr->vis_skips, (unsigned long long)n_skip);
-        atomicAdd(&a.ctr->insert_mut, (unsigned long long)n_mut);
-        atomicAdd(&a.ctr->insert_try, (unsigned long long)n_try);
+        atomicAdd(&ctr_stripe(a.ctr)->search_dist, (unsigned long long)n_search);
+        atomicAdd(&ctr_stripe(a.ctr)->insert_dist, (unsigned long long)n_insert);
+        atomicAdd(&ctr_stripe(a.ctr)->expansions, (unsigned long long)n_exp);
+        atomicAdd(&ctr_stripe(a.ctr)->vis_skips, (unsigned long long)n_skip);
+        atomicAdd(&ctr_stripe(a.ctr)->insert_mut, (unsigned long long)n_mut);
+        atomicAdd(&ctr_stripe(a.ctr)->insert_try, (unsigned long long)n_try);
 #if DANCE_SEARCH_TIMING
-        atomicAdd(&a.ctr->cyc_select, (unsigned long long)c_select);
-        atomicAdd(&a.ctr->cyc_insert, (unsigned long long)c_insert);
-        atomicAdd(&a.ctr->cyc_dist, (unsigned long long)c_dist);
-        atomicAdd(&a.ctr->cyc_pool, (unsigned long long)c_pool);
-        atomicAdd(&a.ctr->cyc_seed, (unsigned long long)t_seed);
-        atomicAdd(&a.ctr->cyc_total, (unsigned long long)(dclock() - t_run));
+        atomicAdd(&ctr_stripe(a.ctr)->cyc_select, (unsigned long long)c_select);
+        atomicAdd(&ctr_stripe(a.ctr)->cyc_insert, (unsigned long long)c_insert);
+        atomicAdd(&ctr_stripe(a.ctr)->cyc_dist, (unsigned long long)c_dist);
+        atomicAdd(&ctr_stripe(a.ctr)->cyc_pool, (unsigned long long)c_pool);
+        atomicAdd(&ctr_stripe(a.ctr)->cyc_seed, (unsigned long long)t_seed);
+        atomicAdd(&ctr_stripe(a.ctr)->cyc_total, (unsigned long long)(dclock() - t_run));
 #endif
       }
     }
@@ -662,7 +671,7 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
     g.deg_work[node] = oc;
     g.deg_cur[node] = oc;
   }
-  if (a.ctr && lane == 0) atomicAdd(&a.ctr->prune_dist, (unsigned long long)npair);
+  if (a.ctr && lane == 0) atomicAdd(&ctr_stripe(a.ctr)->prune_dist, (unsigned long long)npair);
 }
 
 // ---------------------------------------------------------------------------
@@ -818,9 +827,9 @@ __global__ __launch_bounds__(kBlock) void k_merge(MergeArgs a, uint32_t Cp) {
   if (lane == 0) {
     g.deg_work[t] = deg;
     if (a.ctr) {
-      atomicAdd(&a.ctr->merge_dist, (unsigned long long)ncand);
-      atomicAdd(&a.ctr->reverse_edges, (unsigned long long)indeg);
-      atomicAdd(&a.ctr->touched_rows, 1ull);
+      atomicAdd(&ctr_stripe(a.ctr)->merge_dist, (unsigned long long)ncand);
+      atomicAdd(&ctr_stripe(a.ctr)->reverse_edges, (unsigned long long)indeg);
+      atomicAdd(&ctr_stripe(a.ctr)->touched_rows, 1ull);
     }
   }
 }
@@ -975,9 +984,9 @@ __global__ __launch_bounds__(kBlock) void k_merge_reg(MergeArgs a) {
   if (lane == 0) {
     g.deg_work[t] = deg;
     if (a.ctr) {
-      atomicAdd(&a.ctr->merge_dist, (unsigned long long)ncand);
-      atomicAdd(&a.ctr->reverse_edges, (unsigned long long)indeg);
-      atomicAdd(&a.ctr->touched_rows, 1ull);
+      atomicAdd(&ctr_stripe(a.ctr)->merge_dist, (unsigned long long)ncand);
+      atomicAdd(&ctr_stripe(a.ctr)->reverse_edges, (unsigned long long)indeg);
+      atomicAdd(&ctr_stripe(a.ctr)->touched_rows, 1ull);
     }
   }
 }
