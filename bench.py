@@ -88,10 +88,23 @@ def label_starts_gpu(torch, base_t, ls):
     lab_of = torch.from_numpy(np.repeat(np.arange(nl), cnt)).to(dev)
     P = torch.from_numpy(pts.astype(np.int64)).to(dev)
     dim = base_t.shape[1]
-    sums = torch.zeros((nl, dim), dtype=torch.float64, device=dev)
+    # per-label sums from prefix sums over the label-grouped memberships
+    # (no atomics); fp64 prefix sums of uint8 rows are exact integers
+    ends = np.cumsum(cnt) - 1
+    at_end = torch.zeros((max(1, P.shape[0]), dim), dtype=torch.float64, device=dev)
+    carry = torch.zeros(dim, dtype=torch.float64, device=dev)
     step = 1 << 20
     for s0 in range(0, P.shape[0], step):
-        sums.index_add_(0, lab_of[s0:s0 + step], base_t[P[s0:s0 + step]].double())
+        cs = torch.cumsum(base_t[P[s0:s0 + step]].double(), 0) + carry
+        at_end[s0:s0 + cs.shape[0]] = cs
+        carry = cs[-1]
+    nz = cnt > 0
+    sums = torch.zeros((nl, dim), dtype=torch.float64, device=dev)
+    e_t = torch.from_numpy(ends[nz]).to(dev)
+    b_t = torch.from_numpy((ends - cnt)[nz]).to(dev)
+    hi = at_end[e_t]
+    lo = torch.where((b_t >= 0)[:, None], at_end[b_t.clamp(min=0)], torch.zeros_like(hi))
+    sums[torch.from_numpy(np.nonzero(nz)[0]).to(dev)] = hi - lo
     cent = sums / torch.from_numpy(np.maximum(cnt, 1)).to(dev).double()[:, None]
     d = torch.empty(P.shape[0], dtype=torch.float64, device=dev)
     for s0 in range(0, P.shape[0], step):
@@ -165,8 +178,10 @@ def run_c5(args, mode) -> int:
                                   c["C"], c["STEPS"], c["alpha"], INVALID, gstart, graph_t.data_ptr(),
                                   deg_t.data_ptr())
 
-    off, pts = ls.postings()
-    parts = [torch.from_numpy(pts[off[l]:off[l + 1]].astype(np.int64)).to(dev) for l in range(ls.num_labels)]
+    parts = []
+    if mode == "c5s":
+        off, pts = ls.postings()
+        parts = [torch.from_numpy(pts[off[l]:off[l + 1]].astype(np.int64)).to(dev) for l in range(ls.num_labels)]
 
     def step_stitched():
         # per label: gather the label's rows, standard build (Rsmall), remap
