@@ -236,16 +236,15 @@ struct SearchArgs {
 };
 
 // Per-wave LDS words of the search kernel: visited cache, work row (ids,
-// dists), candidate batch (ids, dists), occlusion list, victim list (slots,
-// keys, ranked slots).
-__host__ __device__ constexpr uint32_t search_lds_words(uint32_t Cp) { return kVis + 6u * Cp + 128u; }
+// dists), candidate batch (ids, dists), occlusion list, work-row order.
+__host__ __device__ constexpr uint32_t search_lds_words(uint32_t Cp) { return kVis + 4u * Cp + 128u; }
 
 template <int DT, int CPL, int PS>
 struct SearchWave {
   const SearchArgs& a;
   uint32_t node, lane, grp, sub, Cp;
-  uint32_t *vis, *wid, *lst, *lsa, *lsb, *lsr;
-  float *wdd, *lsd, *lsk;
+  uint32_t *vis, *wid, *lst, *lsa, *ord;
+  float *wdd, *lsd;
   uint4 av[CPL];
   RegPool<PS> P;
   uint32_t wdeg;
@@ -263,9 +262,7 @@ struct SearchWave {
     lst = reinterpret_cast<uint32_t*>(wdd + Cp);
     lsd = reinterpret_cast<float*>(lst + 64);
     lsa = reinterpret_cast<uint32_t*>(lsd + 64);
-    lsb = lsa + Cp;
-    lsk = reinterpret_cast<float*>(lsb + Cp);
-    lsr = reinterpret_cast<uint32_t*>(lsk + Cp);
+    ord = lsa + Cp;
     n_search = n_insert = n_skip = n_mut = n_try = 0;
   }
 
@@ -304,6 +301,78 @@ struct SearchWave {
     c_pool += dclock() - t1;
   }
 
+  // Work-row order: ord[r] is the slot of rank r over [0, wdeg), ascending by
+  // (usable, distance, slot descending), where unusable entries (invalid id
+  // or NaN distance) rank lowest. Reading it from the top gives the usable
+  // entries by (distance descending, slot ascending): the worst entry first,
+  // then the victim candidates in the order the online insert tries them.
+  __device__ __forceinline__ bool usable(uint32_t j) const {
+    return valid_for(wid[j], a.g.N, node) && wdd[j] == wdd[j];
+  }
+  // Whether slot j orders before a usable entry (d, s).
+  __device__ __forceinline__ bool before(uint32_t j, float d, uint32_t s) const {
+    if (!usable(j)) return true;
+    const float dj = wdd[j];
+    return dj < d || (dj == d && j > s);
+  }
+  __device__ __forceinline__ void ord_init() {
+    for (uint32_t i = lane; i < wdeg; i += 64) {
+      const bool ui = usable(i);
+      const float di = wdd[i];
+      uint32_t r = 0;
+      for (uint32_t j = 0; j < wdeg; ++j) {
+        if (j == i) continue;
+        const bool uj = usable(j);
+        r += ui ? (!uj || wdd[j] < di || (wdd[j] == di && j > i)) : (!uj && j > i);
+      }
+      ord[r] = i;
+    }
+    wave_sync();
+  }
+  // Slot s now holds a usable entry of distance d; deg is the row length
+  // after the change (s == deg - 1 and fresh when appended).
+  __device__ __forceinline__ void ord_update(uint32_t s, float d, bool appended, uint32_t deg) {
+    uint32_t rnew = 0;
+    for (uint32_t b = 0; b < deg; b += 64) {
+      const uint32_t j = b + lane;
+      rnew += popc64(wballot(j < deg && j != s && before(j, d, s)));
+    }
+    uint32_t rold = deg - 1;
+    if (!appended) {
+      uint64_t m = 0;
+      uint32_t base = 0;
+      for (uint32_t b = 0; b < deg && !m; b += 64) {
+        m = wballot(b + lane < deg && ord[b + lane] == s);
+        base = b;
+      }
+      rold = base + (uint32_t)ffs64(m);
+    }
+    // ranks between rnew and rold move one step toward rold; rnew receives s.
+    // Chunks of 64 are read before they are written and walk away from the
+    // ranks they read, so every rank is read before it is overwritten.
+    if (rnew < rold) {
+      for (int top = (int)rold; top > (int)rnew; top -= 64) {
+        const int i = top - (int)lane;
+        const bool ok = i > (int)rnew;
+        const uint32_t v = ok ? ord[i - 1] : 0u;
+        wave_sync();
+        if (ok) ord[i] = v;
+        wave_sync();
+      }
+    } else if (rnew > rold) {
+      for (uint32_t bot = rold; bot < rnew; bot += 64) {
+        const uint32_t i = bot + lane;
+        const bool ok = i < rnew;
+        const uint32_t v = ok ? ord[i + 1] : 0u;
+        wave_sync();
+        if (ok) ord[i] = v;
+        wave_sync();
+      }
+    }
+    if (lane == 0) ord[rnew] = s;
+    wave_sync();
+  }
+
   // dynamic_robust_insert_C_warp (vnew2.cu:759-877) on the LDS work row.
   __device__ __forceinline__ void robust_insert(uint32_t x, float dpx) {
     const uint32_t N = a.g.N, C = a.g.C;
@@ -316,8 +385,6 @@ struct SearchWave {
     uint4 xv[CPL];
     load_row<CPL>(a.rs, x, true, sub, xv);
     uint32_t nA = 0, nB = 0;
-    float wl = -FLT_MAX;
-    int wp = -1;
     for (uint32_t b = 0; b < wdeg; b += 64) {
       const uint32_t i = b + lane;
       const bool in = i < wdeg;
@@ -325,20 +392,10 @@ struct SearchWave {
       const float dpy = in ? wdd[i] : 0.0f;
       const bool v = in && valid_for(y, N, node);
       const bool ca = v && dpy <= dpx;
-      const bool cb = v && dpy > dpx;
-      const uint64_t ma = wballot(ca), mb = wballot(cb);
+      const uint64_t ma = wballot(ca);
       if (ca) lsa[nA + mbcnt64(ma)] = i;
-      if (cb) {
-        const uint32_t k = nB + mbcnt64(mb);
-        lsb[k] = i;
-        lsk[k] = dpy;
-      }
       nA += popc64(ma);
-      nB += popc64(mb);
-      if (v && dpy > wl) {
-        wl = dpy;
-        wp = (int)i;
-      }
+      nB += popc64(wballot(v && dpy > dpx));
     }
     wave_sync();
     // Occlusion: exists y with d_py <= d_px and alpha * d(y, x) <= d_px. The
@@ -356,64 +413,53 @@ struct SearchWave {
       occluded = wballot(sub == 0 && a0 && a.alpha * d0 <= dpx) != 0;
     }
     if (occluded) return;
-    // Worst valid entry (largest d_py, lowest slot).
-    const int WK = wave_max_i(wp >= 0 ? fkey(wl) : INT_MIN);
+    // Worst usable entry (largest d_py, lowest slot): the top of the order.
     int wpos = -1;
     float wdist = -FLT_MAX;
-    if (WK != INT_MIN) {
-      wpos = (int)wave_min_u((wp >= 0 && fkey(wl) == WK) ? (uint32_t)wp : 0xFFFFFFFFu);
-      wdist = __int_as_float(WK);
+    if (wdeg > 0) {
+      const uint32_t top = ord[wdeg - 1];
+      if (usable(top)) {
+        wpos = (int)top;
+        wdist = wdd[top];
+      }
     }
     // Victim: the largest d_py (lowest slot on ties) among y with d_py > d_px
-    // and alpha * d(x, y) <= d_py. Rank the candidates by (d_py desc, slot asc)
-    // and take the first that qualifies, so only a prefix is gathered.
+    // and alpha * d(x, y) <= d_py. The nB candidates are the top nB ranks of
+    // the order, already in that sequence, so only a prefix is gathered.
     int vpos = -1;
-    if (nB > 0) {
-      for (uint32_t k = lane; k < nB; k += 64) {
-        const float dk = lsk[k];
-        const uint32_t sk = lsb[k];
-        uint32_t rank = 0;
-        for (uint32_t j = 0; j < nB; ++j) {
-          const float dj = lsk[j];
-          rank += (dj > dk || (dj == dk && lsb[j] < sk)) ? 1u : 0u;
-        }
-        lsr[rank] = sk;
-      }
-      wave_sync();
-      for (uint32_t p = 0; p < nB && vpos < 0; p += 8) {
-        const uint32_t k0 = p + grp;
-        const bool a0 = k0 < nB;
-        const uint32_t s0 = a0 ? lsr[k0] : 0u;
-        const uint32_t y0 = a0 ? wid[s0] : 0u;
-        uint4 b0[CPL];
-        load_row<CPL>(a.rs, y0, a0, sub, b0);
-        const float d0 = octet_finish<DT, CPL>(xv, b0);
-        n_insert += min(8u, nB - p);
-        const uint64_t hit = wballot(sub == 0 && a0 && a.alpha * d0 <= wdd[s0]);
-        if (hit) vpos = (int)lsr[p + ((uint32_t)ffs64(hit) >> 3)];
-      }
+    for (uint32_t p = 0; p < nB && vpos < 0; p += 8) {
+      const uint32_t k0 = p + grp;
+      const bool a0 = k0 < nB;
+      const uint32_t s0 = a0 ? ord[wdeg - 1u - k0] : 0u;
+      const uint32_t y0 = a0 ? wid[s0] : 0u;
+      uint4 b0[CPL];
+      load_row<CPL>(a.rs, y0, a0, sub, b0);
+      const float d0 = octet_finish<DT, CPL>(xv, b0);
+      n_insert += min(8u, nB - p);
+      const uint64_t hit = wballot(sub == 0 && a0 && a.alpha * d0 <= wdd[s0]);
+      if (hit) vpos = (int)ord[wdeg - 1u - (p + ((uint32_t)ffs64(hit) >> 3))];
     }
+    int mslot = -1;
+    bool appended = false;
     if (vpos >= 0) {
-      if (lane == 0) {
-        wid[vpos] = x;
-        wdd[vpos] = dpx;
-      }
-      n_mut++;
+      mslot = vpos;
     } else if (wdeg < C) {
-      if (lane == 0) {
-        wid[wdeg] = x;
-        wdd[wdeg] = dpx;
-      }
-      wdeg++;
-      n_mut++;
+      mslot = (int)wdeg;
+      appended = true;
     } else if (wpos >= 0 && dpx < wdist) {
-      if (lane == 0) {
-        wid[wpos] = x;
-        wdd[wpos] = dpx;
-      }
-      n_mut++;
+      mslot = wpos;
     }
-    wave_sync();
+    if (mslot >= 0) {
+      wave_sync();
+      if (lane == 0) {
+        wid[mslot] = x;
+        wdd[mslot] = dpx;
+      }
+      if (appended) wdeg++;
+      n_mut++;
+      wave_sync();
+      ord_update((uint32_t)mslot, dpx, appended, wdeg);
+    }
   }
 
   __device__ void run() {
@@ -441,6 +487,7 @@ struct SearchWave {
     wdeg = deg_self;
     P.init(a.L);
     wave_sync();
+    ord_init();
     // Entry point (vnew2.cu:1223-1244).
     process_batch(lane == 0 && a.start < N && a.start != node ? a.start : DANCE_INV);
     // Own neighbours with stored distances (vnew2.cu:1246-1278).
