@@ -62,6 +62,7 @@ class DanceKernelProfile(C.Structure):
         ("reverse_bytes", C.c_double),
         ("cyc_select", C.c_uint64), ("cyc_insert", C.c_uint64), ("cyc_dist", C.c_uint64),
         ("cyc_pool", C.c_uint64), ("cyc_seed", C.c_uint64), ("cyc_total", C.c_uint64),
+        ("bound_checks", C.c_uint64), ("bound_skips", C.c_uint64),
     ]
 
 
@@ -132,7 +133,7 @@ EXPORTS = [
     "gpu_vamana_vnew2_get_last_medoid", "gpu_vamana_vnew2_get_last_stats",
     "dance_vamana_build_resident", "dance_get_last_kernel_profile",
     "dance_set_profile", "dance_get_profile",
-    "dance_stage_distances", "dance_stage_medoid", "dance_stage_init", "dance_stage_search",
+    "dance_stage_distances", "dance_stage_qbound", "dance_stage_medoid", "dance_stage_init", "dance_stage_search",
     "dance_stage_reverse_merge", "dance_stage_prune", "dance_stage_sort_pairs", "dance_stage_scan",
     "dance_synth_f32", "dance_synth_u8",
     "gpu_vamana_filtered_build_uint8", "gpu_vamana_filtered_build_float", "gpu_vamana_filtered_get_last_stats",
@@ -176,6 +177,7 @@ def lib() -> C.CDLL:
         L.dance_get_profile.argtypes = []
         L.dance_get_profile.restype = C.c_char_p
         L.dance_stage_distances.argtypes = [vp, i32, u32, u32, _u32p, _u32p, C.c_uint64, _f32p]
+        L.dance_stage_qbound.argtypes = [vp, i32, u32, u32, _u32p, _u32p, _f32p, C.c_uint64, _u32p]
         L.dance_stage_medoid.argtypes = [vp, i32, u32, u32, _f32p, _u32p, _u32p]
         L.dance_stage_init.argtypes = [vp, i32, u32, u32, u32, u32, _u32p, _u32p, _u32p, _u32p, _f32p]
         L.dance_stage_search.argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, f32, u32,
@@ -186,7 +188,7 @@ def lib() -> C.CDLL:
                                         _u32p, _u32p]
         L.dance_stage_sort_pairs.argtypes = [_u32p, _u32p, C.c_uint64, u32, _u32p, _u32p]
         L.dance_stage_scan.argtypes = [_u32p, C.c_uint64, _u32p]
-        for name in ("dance_stage_distances", "dance_stage_medoid", "dance_stage_init",
+        for name in ("dance_stage_distances", "dance_stage_qbound", "dance_stage_medoid", "dance_stage_init",
                      "dance_stage_search", "dance_stage_reverse_merge", "dance_stage_prune",
                      "dance_stage_sort_pairs", "dance_stage_scan"):
             getattr(L, name).restype = i32
@@ -310,6 +312,19 @@ def stage_distances(data: np.ndarray, a: np.ndarray, b: np.ndarray) -> np.ndarra
     _check(lib().dance_stage_distances(data.ctypes.data, dtype_code(data), data.shape[0], data.shape[1],
                                        _p(a, C.c_uint32), _p(b, C.c_uint32), a.shape[0],
                                        _p(out, C.c_float)), "dance_stage_distances")
+    return out
+
+
+def stage_qbound(data: np.ndarray, a: np.ndarray, b: np.ndarray, T: np.ndarray) -> np.ndarray:
+    """Flags of the search's quantized bound: 1 where it proves dist(a, b) >= T."""
+    data = np.ascontiguousarray(data)
+    a = np.ascontiguousarray(a, dtype=np.uint32)
+    b = np.ascontiguousarray(b, dtype=np.uint32)
+    T = np.ascontiguousarray(T, dtype=np.float32)
+    out = np.empty(a.shape[0], dtype=np.uint32)
+    _check(lib().dance_stage_qbound(data.ctypes.data, dtype_code(data), data.shape[0], data.shape[1],
+                                    _p(a, C.c_uint32), _p(b, C.c_uint32), _p(T, C.c_float), a.shape[0],
+                                    _p(out, C.c_uint32)), "dance_stage_qbound")
     return out
 
 

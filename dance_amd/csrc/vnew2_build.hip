@@ -12,12 +12,15 @@
 //   work   N x C   u32 + wd N x C f32   candidate rows with distances
 //   keys/vals 2 x 2 x N*R u32     reverse-edge radix sort double buffers
 //   offs   N+1 u32                reverse CSR offsets
+//   qrows  N x 128 B              int8 codes + header for the distance lower
+//                                 bound (fp32/fp16 rows of <= 112 dims)
 // All kernels run on one stream; stages are timed with HIP events.
 //
 // Algorithmic bytes reported for the roofline (per kernel, summed over the
 // build; V = bytes of one vector row, counted on device by each wave):
 //   search: (search_dist + insert_dist) * V + expansions * (4R + 4)
 //           + N * (V + 4R + 4 + 16C)            (own vector, cur row, work row r/w)
+//           + bound_checks * 128                (quantized rows, when the bound is on)
 //   merge : merge_dist * 4 (snapshot distance) + reverse_edges * 4 + touched_rows * (16C + 8)
 //   prune : prune_dist * V + (selected rows) * V + N * 24C
 //   reverse (keys + sort): N*R*(4*3) + passes * N*R * 20
@@ -142,12 +145,45 @@ static int launch_init(const Rows& rows, GraphBufs g, hipStream_t s) {
   });
 }
 
+// Quantized lower bound (qbound.h). DANCE_QBOUND=0 turns it off; otherwise
+// the build uses it in the iterations whose bit is set in DANCE_QBOUND_ITERS
+// (default kQBoundIters). Results are identical either way.
+constexpr uint32_t kQBoundIters = 0x1u;  // first iteration: random graph, HBM-bound
+static bool qbound_enabled() {
+  const char* e = std::getenv("DANCE_QBOUND");
+  return !(e && e[0] == '0');
+}
+static uint32_t qbound_iters() {
+  const char* e = std::getenv("DANCE_QBOUND_ITERS");
+  if (e && e[0]) return (uint32_t)std::strtoul(e, nullptr, 0);
+  return kQBoundIters;
+}
+
+// Builds the code rows for `rows` into buf; returns a disabled set when the
+// row type or width has no bound.
+static int build_qbound(const Rows& rows, DevBuf& buf, hipStream_t s, QBoundSet* out) {
+  *out = QBoundSet{nullptr, 0.0f};
+  if (!qbound_enabled() || rows.dtype == DANCE_U8 || rows.dim > kQMaxDim || rows.N == 0) return 0;
+  const int cpl = pick_cpl(rows.rs.nch);
+  if (cpl < 0) return 0;
+  DCHECK(buf.alloc((size_t)rows.N * kQChunks * 16));
+  const uint32_t grid = (rows.N + 255) / 256;
+  if (rows.dtype == DANCE_F32)
+    hipLaunchKernelGGL(k_quantize<DANCE_F32>, dim3(grid), dim3(256), 0, s, rows.rs, rows.N, rows.dim, buf.as<uint4>());
+  else
+    hipLaunchKernelGGL(k_quantize<DANCE_F16>, dim3(grid), dim3(256), 0, s, rows.rs, rows.N, rows.dim, buf.as<uint4>());
+  DHIP(hipGetLastError());
+  const double lane_terms = (double)cpl * (16.0 / elem_bytes(rows.dtype));
+  *out = QBoundSet{buf.as<uint4>(), (float)(2.0 * (lane_terms + 8.0) * 0x1p-24)};
+  return 0;
+}
+
 static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t steps, float alpha, uint32_t start,
-                         const uint32_t* order, VCounters* ctr, hipStream_t s) {
+                         const uint32_t* order, VCounters* ctr, const QBoundSet& qb, hipStream_t s) {
   const int cpl = pick_cpl(rows.rs.nch);
   const uint32_t Cp = round64(g.C);
   const size_t lds = (size_t)kWavesPerBlock * search_lds_words(Cp) * 4;
-  SearchArgs a{rows.rs, g, L, steps, start, alpha, order, ctr};
+  SearchArgs a{rows.rs, g, L, steps, start, alpha, order, ctr, qb};
   if (L > 256) {
     std::fprintf(stderr, "[dance_hip] L=%u exceeds the supported maximum 256\n", L);
     return -1;
@@ -370,6 +406,10 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   DCHECK(launch_init(rows, g, s));
   const uint32_t* order = nullptr;
   DCHECK(build_schedule(rows, rws, s, &order));
+  DevBuf qbuf;
+  QBoundSet qb{};
+  DCHECK(build_qbound(rows, qbuf, s, &qb));
+  const uint32_t q_iters = qbound_iters();
   DHIP(hipEventRecord(e_init, s));
 
   struct IterEv {
@@ -391,7 +431,8 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     if (verbose())
       std::printf("[gpu_vamana_build] iteration %u / %u, alpha=%.3f\n", it + 1, kIters, (double)alpha);
     DHIP(hipEventRecord(iev[it].s0, s));
-    DCHECK(launch_search(rows, g, L, steps, alpha, start, order, ctr, s));
+    const QBoundSet qb_it = ((q_iters >> it) & 1u) ? qb : QBoundSet{nullptr, 0.0f};
+    DCHECK(launch_search(rows, g, L, steps, alpha, start, order, ctr, qb_it, s));
     DHIP(hipEventRecord(iev[it].s1, s));
     const uint32_t* srcs = nullptr;
     DCHECK(build_reverse_csr(g, rws, s, &srcs));
@@ -443,9 +484,11 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   p.cyc_pool = hc_ctr.cyc_pool;
   p.cyc_seed = hc_ctr.cyc_seed;
   p.cyc_total = hc_ctr.cyc_total;
+  p.bound_checks = hc_ctr.bound_checks;
+  p.bound_skips = hc_ctr.bound_skips;
   const double V = rows.vbytes();
   p.search_bytes = (double)(p.search_dist + p.insert_dist) * V + (double)p.expansions * (4.0 * R + 4.0) +
-                   (double)kIters * N * (V + 4.0 * R + 4.0 + 16.0 * C);
+                   (double)kIters * N * (V + 4.0 * R + 4.0 + 16.0 * C) + (double)p.bound_checks * (kQChunks * 16.0);
   p.merge_bytes = (double)p.merge_dist * 4.0 + (double)p.reverse_edges * 4.0 +
                   (double)p.touched_rows * (16.0 * C + 8.0);
   p.prune_bytes = (double)p.prune_dist * V + (double)kIters * N * (24.0 * C);
@@ -596,6 +639,32 @@ __global__ __launch_bounds__(kBlock) void k_pair_dist(RowSet rs, const uint32_t*
     load_row<CPL>(rs, act ? b[k] : 0u, act, sub, vb);
     const float d = octet_finish<DT, CPL>(va, vb);
     if (act && sub == 0) out[k] = d;
+  }
+}
+
+// The search's bound test on explicit pairs: flag[k] = 1 when the quantized
+// bound proves dist(a[k], b[k]) >= T[k] (the querying row is a[k]).
+__global__ __launch_bounds__(kBlock) void k_qbound_pairs(QBoundSet qb, const uint32_t* __restrict__ a,
+                                                         const uint32_t* __restrict__ b,
+                                                         const float* __restrict__ T, uint64_t n,
+                                                         uint32_t* __restrict__ flag) {
+  const uint32_t w = threadIdx.x >> 6;
+  const uint64_t base = ((uint64_t)blockIdx.x * kWavesPerBlock + w) * 64;
+  if (base >= n) return;
+  const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;
+  for (uint32_t p = 0; p < 64; p += 8) {
+    const uint64_t k = base + p + grp;
+    const bool act = k < n;
+    // the querying row differs per octet here, so its header is read per lane
+    const uint4* qa = qb.rows + (size_t)(act ? a[k] : 0u) * kQChunks;
+    const uint4 h = qa[0];
+    const QSelf me{qa, __uint_as_float(h.x), __uint_as_float(h.y), __uint_as_float(h.z)};
+    const float t = ((act ? T[k] : 0.0f) + 1e-30f) * (1.0f + qb.kappa2);
+    const float sT = (__builtin_sqrtf(t) + me.r) * (1.0f + kQSlack);
+    const uint4 code = qa[sub];
+    const uint4 bc = q_load(qb, act ? b[k] : 0u, act, sub);
+    const bool rej = q_proves_reject(me, code, sT, bc, act, sub);
+    if (act && sub == 0) flag[k] = rej ? 1u : 0u;
   }
 }
 
@@ -760,6 +829,42 @@ int dance_stage_distances(const void* h_data, int dtype, uint32_t N, uint32_t di
   return 0;
 }
 
+int dance_stage_qbound(const void* h_data, int dtype, uint32_t N, uint32_t dim, const uint32_t* a, const uint32_t* b,
+                       const float* T, uint64_t n, uint32_t* flags) {
+  if (!h_data || !a || !b || !T || !flags || N == 0 || dim == 0) return -1;
+  for (uint64_t i = 0; i < n; ++i)
+    if (a[i] >= N || b[i] >= N) {
+      std::fprintf(stderr, "[dance_hip] bound index out of range\n");
+      return -1;
+    }
+  StageCtx cx;
+  DCHECK(cx.open(h_data, dtype, N, dim));
+  DevBuf qbuf, da, db, dt, dout;
+  QBoundSet qb{};
+  DCHECK(build_qbound(cx.rows, qbuf, cx.s, &qb));
+  if (!qb.rows) {
+    std::fprintf(stderr, "[dance_hip] no distance bound for this row type / width (or DANCE_QBOUND=0)\n");
+    return -1;
+  }
+  const uint64_t m = std::max<uint64_t>(n, 1);
+  DCHECK(da.alloc(m * 4));
+  DCHECK(db.alloc(m * 4));
+  DCHECK(dt.alloc(m * 4));
+  DCHECK(dout.alloc(m * 4));
+  DCHECK(up(da.p, a, n * 4, cx.s));
+  DCHECK(up(db.p, b, n * 4, cx.s));
+  DCHECK(up(dt.p, T, n * 4, cx.s));
+  const uint64_t waves = (n + 63) / 64;
+  if (waves) {
+    hipLaunchKernelGGL(k_qbound_pairs, dim3((uint32_t)((waves + kWavesPerBlock - 1) / kWavesPerBlock)), dim3(kBlock),
+                       0, cx.s, qb, da.as<uint32_t>(), db.as<uint32_t>(), dt.as<float>(), n, dout.as<uint32_t>());
+    DHIP(hipGetLastError());
+  }
+  DCHECK(down(flags, dout.p, n * 4, cx.s));
+  DHIP(hipStreamSynchronize(cx.s));
+  return 0;
+}
+
 int dance_stage_medoid(const void* h_data, int dtype, uint32_t N, uint32_t dim, float* scores, uint32_t* cands,
                        uint32_t* medoid) {
   if (!h_data || N == 0 || dim == 0) return -1;
@@ -806,7 +911,10 @@ int dance_stage_search(const void* h_data, int dtype, uint32_t N, uint32_t dim, 
   StageCtx cx;
   DCHECK(cx.open(h_data, dtype, N, dim));
   DCHECK(upload_state(cx.st, N, R, C, cur, deg_cur, work, deg_work, wd, cx.s));
-  DCHECK(launch_search(cx.rows, cx.st.g(), L, steps, alpha, start, nullptr, nullptr, cx.s));
+  DevBuf qbuf;
+  QBoundSet qb{};
+  DCHECK(build_qbound(cx.rows, qbuf, cx.s, &qb));
+  DCHECK(launch_search(cx.rows, cx.st.g(), L, steps, alpha, start, nullptr, nullptr, qb, cx.s));
   return download_state(cx.st, cur, deg_cur, work, deg_work, wd, cx.s);
 }
 

@@ -14,6 +14,7 @@
 // and distances are a deterministic function of the id).
 #pragma once
 
+#include "qbound.h"
 #include "wave.h"
 
 // Opt-in per-phase cycle counters of the search kernel (the analogue of the
@@ -36,6 +37,7 @@ constexpr uint32_t kVisBits = 10;
 constexpr uint32_t kVis = 1u << kVisBits;  // visited cache slots per wave
 constexpr uint32_t kWavesPerBlock = 4;
 constexpr uint32_t kBlock = 64 * kWavesPerBlock;
+constexpr uint32_t kQInFlight = 4;  // bound-filter passes whose loads are in flight together
 
 struct VCounters {
   unsigned long long search_dist;   // distances computed for pool candidates
@@ -51,6 +53,8 @@ struct VCounters {
   // DANCE_SEARCH_TIMING: cycles in select / online insert / candidate
   // distances / ordered pool inserts / seeding, summed over waves.
   unsigned long long cyc_select, cyc_insert, cyc_dist, cyc_pool, cyc_seed, cyc_total;
+  unsigned long long bound_checks;  // candidates tested with the quantized lower bound
+  unsigned long long bound_skips;   // candidates whose exact distance the bound made unnecessary
 };
 
 // Counters are striped over kCtrStripes copies (by workgroup) so that the
@@ -233,6 +237,7 @@ struct SearchArgs {
   float alpha;
   const uint32_t* order;  // optional processing order (vertex = order[wave])
   VCounters* ctr;
+  QBoundSet qb;  // quantized lower bound (qb.rows == nullptr: exact distances only)
 };
 
 // Per-wave LDS words of the search kernel: visited cache, work row (ids,
@@ -247,8 +252,9 @@ struct SearchWave {
   float *wdd, *lsd;
   uint4 av[CPL];
   RegPool<PS> P;
+  QSelf qme;
   uint32_t wdeg;
-  uint32_t n_search, n_insert, n_skip, n_mut, n_try;
+  uint32_t n_search, n_insert, n_skip, n_mut, n_try, n_bchk, n_bskip;
   uint64_t c_select = 0, c_insert = 0, c_dist = 0, c_pool = 0;
 
   __device__ SearchWave(const SearchArgs& args, uint32_t node_, uint32_t* base, uint32_t Cp_)
@@ -263,7 +269,40 @@ struct SearchWave {
     lsd = reinterpret_cast<float*>(lst + 64);
     lsa = reinterpret_cast<uint32_t*>(lsd + 64);
     ord = lsa + Cp;
-    n_search = n_insert = n_skip = n_mut = n_try = 0;
+    n_search = n_insert = n_skip = n_mut = n_try = n_bchk = n_bskip = 0;
+  }
+
+  // Drops from lst[0..n) the candidates whose distance the quantized bound
+  // proves >= the pool threshold (they would be rejected unseen); keeps the
+  // others in order and returns their count.
+  __device__ __forceinline__ uint32_t bound_filter(uint32_t n) {
+    const float sT = q_threshold(a.qb, qme, P.max_d);
+    const uint4 code = qme.row[sub];
+    uint64_t keep = 0;
+    for (uint32_t p = 0; p < n; p += 8 * kQInFlight) {
+      uint4 b[kQInFlight];
+#pragma unroll
+      for (uint32_t u = 0; u < kQInFlight; ++u) {
+        const uint32_t k = p + 8 * u + grp;
+        b[u] = q_load(a.qb, k < n ? lst[k] : 0u, k < n, sub);
+      }
+      bool rej[kQInFlight];
+#pragma unroll
+      for (uint32_t u = 0; u < kQInFlight; ++u)
+        rej[u] = q_proves_reject(qme, code, sT, b[u], p + 8 * u + grp < n, sub);
+#pragma unroll
+      for (uint32_t u = 0; u < kQInFlight; ++u)
+        keep |= (uint64_t)octet_bits(wballot(sub == 0 && p + 8 * u + grp < n && !rej[u])) << (p + 8 * u);
+    }    const uint32_t nk = popc64(keep);
+    n_bchk += n;
+    n_bskip += n - nk;
+    if (nk < n) {
+      const uint32_t ck = lane < n ? lst[lane] : 0u;
+      wave_sync();
+      if ((keep >> lane) & 1ull) lst[mbcnt64(keep)] = ck;
+      wave_sync();
+    }
+    return nk;
   }
 
   // Handles one batch of <= 64 candidates given in insertion order (one per
@@ -282,13 +321,14 @@ struct SearchWave {
     wave_sync();
     const uint64_t t0 = dclock();
     const bool full = P.size >= P.L && P.max_pos >= 0;
-    batch_dist<DT, CPL>(a.rs, av, lst, lsd, n, grp, sub);
-    n_search += n;
+    const uint32_t nx = (full && a.qb.rows) ? bound_filter(n) : n;
+    if (nx) batch_dist<DT, CPL>(a.rs, av, lst, lsd, nx, grp, sub);
+    n_search += nx;
     const uint64_t t1 = dclock();
     c_dist += t1 - t0;
-    const uint32_t ck = lane < n ? lst[lane] : DANCE_INV;
-    const float dk = lane < n ? lsd[lane] : FLT_MAX;
-    bool keep = lane < n;
+    const uint32_t ck = lane < nx ? lst[lane] : DANCE_INV;
+    const float dk = lane < nx ? lsd[lane] : FLT_MAX;
+    bool keep = lane < nx;
     if (full) keep = keep && dk < P.max_d;
     uint64_t km = wballot(keep);
     while (km) {
@@ -468,6 +508,7 @@ struct SearchWave {
     const uint32_t N = g.N, R = g.R, C = g.C;
     for (uint32_t i = lane; i < kVis; i += 64) vis[i] = DANCE_INV;
     load_row<CPL>(a.rs, node, true, sub, av);
+    if (a.qb.rows) q_load_self(a.qb, node, qme);
     // Work row := current row with its stored distances (vnew2.cu:1186-1212).
     const uint32_t deg_self = min(g.deg_cur[node], R);
     const size_t cb = (size_t)node * R, wb = (size_t)node * C;
@@ -548,6 +589,10 @@ struct SearchWave {
         atomicAdd(&ctr_stripe(a.ctr)->vis_skips, (unsigned long long)n_skip);
         atomicAdd(&ctr_stripe(a.ctr)->insert_mut, (unsigned long long)n_mut);
         atomicAdd(&ctr_stripe(a.ctr)->insert_try, (unsigned long long)n_try);
+        if (a.qb.rows) {
+          atomicAdd(&ctr_stripe(a.ctr)->bound_checks, (unsigned long long)n_bchk);
+          atomicAdd(&ctr_stripe(a.ctr)->bound_skips, (unsigned long long)n_bskip);
+        }
 #if DANCE_SEARCH_TIMING
         atomicAdd(&ctr_stripe(a.ctr)->cyc_select, (unsigned long long)c_select);
         atomicAdd(&ctr_stripe(a.ctr)->cyc_insert, (unsigned long long)c_insert);
@@ -561,9 +606,15 @@ struct SearchWave {
   }
 };
 
+// Waves per SIMD the register allocator must leave room for: 5 for the
+// narrow-row, L <= 128 variants (the common case; the allocator would
+// otherwise settle at 4 by a few registers), no constraint elsewhere.
+template <int CPL, int PS>
+constexpr int kSearchMinWaves = (CPL <= 3 && PS == 2) ? 5 : 1;
+
 // search_prune_kernel_shared (vnew2.cu:1119-1439).
 template <int DT, int CPL, int PS>
-__global__ __launch_bounds__(kBlock) void k_search(SearchArgs a, uint32_t Cp) {
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kSearchMinWaves<CPL, PS>))) void k_search(SearchArgs a, uint32_t Cp) {
   extern __shared__ uint32_t smem[];
   const uint32_t w = threadIdx.x >> 6;
   const uint32_t gw = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + w;

@@ -31,6 +31,11 @@ typedef struct DanceKernelProfile {
     double search_bytes, merge_bytes, prune_bytes, reverse_bytes;
     /* Search-kernel phase cycles (zero unless built with DANCE_SEARCH_TIMING=1). */
     uint64_t cyc_select, cyc_insert, cyc_dist, cyc_pool, cyc_seed, cyc_total;
+    /* Quantized lower bound of the search (fp32/fp16 rows of <= 112 dims):
+     * candidates tested, and those whose exact distance it made unnecessary
+     * (proved >= the pool threshold). DANCE_QBOUND=0 disables the bound;
+     * DANCE_QBOUND_ITERS selects the iterations (bit i = iteration i). */
+    uint64_t bound_checks, bound_skips;
 } DanceKernelProfile;
 
 /* Full standard (vnew2) build with the vectors already resident in device
@@ -129,6 +134,12 @@ void dance_get_last_search_stats(DanceSearchStats *stats);
  * src/gpu_vamana_vnew2.cu:215-423). */
 int dance_stage_distances(const void *h_data, int dtype, uint32_t num_points, uint32_t dim, const uint32_t *a,
                           const uint32_t *b, uint64_t n, float *out);
+
+/* The search's quantized distance bound on explicit pairs (no counterpart in
+ * the reference; it only skips work): flags[i] = 1 when the bound proves
+ * dist(a[i], b[i]) >= T[i]. fp32/fp16 rows of <= 112 dims; -1 otherwise. */
+int dance_stage_qbound(const void *h_data, int dtype, uint32_t num_points, uint32_t dim, const uint32_t *a,
+                       const uint32_t *b, const float *T, uint64_t n, uint32_t *flags);
 
 /* medoid_score_kernel_warp + host top-1 (src/gpu_vamana_vnew2.cu:1032-1064, 2359-2479).
  * scores/cands: min(1024, N) entries. */

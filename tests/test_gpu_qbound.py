@@ -1,0 +1,163 @@
+"""The search's quantized distance bound (dance_amd/csrc/qbound.h).
+
+The bound may only flag a pair when the canonical distance is >= the
+threshold; it is probed right at the threshold (T = d and the next float
+above d) on adversarial rows: exact and one-ulp duplicates, tiny, huge,
+zero and integer-valued rows, non-finite rows. Builds and searches with the
+bound off, on in the first iteration (default) and on in every iteration
+must give the oracle's graph bit for bit.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import dance_amd as D
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+FMAX = np.finfo(np.float32).max
+
+
+def adversarial(n, dim, seed, dtype=np.float32, huge=True):
+    """huge=False keeps every value finite in fp16."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((n, dim))
+    x /= np.linalg.norm(x, axis=1, keepdims=True)
+    x = x.astype(np.float32)
+    x[10:20] = x[0]                                   # exact duplicates
+    x[20:40] = x[1]
+    x[20:40, 0] = np.nextafter(x[20:40, 0], np.float32(np.inf))  # one ulp apart
+    x[40:50] *= np.float32(1e-20)                     # scale below the coded range
+    x[50:60] *= np.float32(1e9 if huge else 300.0)    # large but coded
+    x[60:70] *= np.float32(1e17 if huge else 3e4)     # scale above the coded range (fp32)
+    x[70:80] = 0.0                                    # zero rows
+    x[80:90] = rng.integers(-3, 4, (10, dim))         # exact small integers
+    x[90:100] = x[91] + np.float32(1e-7) * rng.standard_normal((10, dim)).astype(np.float32)
+    return x.astype(dtype)
+
+
+def pairs(n, m, seed):
+    rng = np.random.default_rng(seed)
+    a = rng.integers(0, n, m).astype(np.uint32)
+    b = rng.integers(0, n, m).astype(np.uint32)
+    special = np.arange(0, 100, dtype=np.uint32)  # every adversarial row against its neighbours
+    a = np.concatenate([a, special, special, np.zeros(100, np.uint32)])
+    b = np.concatenate([b, (special + 1) % n, (special + 7) % n, special])
+    return a, b
+
+
+def check_sound(x, a, b):
+    d = D.stage_distances(x, a, b)
+    above = np.nextafter(d, np.float32(np.inf))
+    flagged_any = 0
+    for T in (d, above, d * np.float32(1 + 1e-6), d * np.float32(0.999), d * np.float32(0.5),
+              np.zeros_like(d), np.full_like(d, FMAX), np.full_like(d, 1e-38)):
+        T = np.ascontiguousarray(T, np.float32)
+        f = D.stage_qbound(x, a, b, T).astype(bool)
+        bad = f & ~(d >= T)
+        assert not bad.any(), f"bound flagged dist < T at {np.nonzero(bad)[0][:5]}: d={d[bad][:3]} T={T[bad][:3]}"
+        flagged_any += int(f.sum())
+    assert not D.stage_qbound(x, a, b, above).any()  # no pair has dist >= next float above it
+    return flagged_any
+
+
+@pytest.mark.parametrize("dim", [96, 112, 20, 1, 7])
+def test_bound_is_sound_f32(dim):
+    x = adversarial(4000, dim, seed=dim)
+    a, b = pairs(4000, 20000, seed=dim + 1)
+    assert check_sound(x, a, b) > 0
+
+
+def test_bound_is_sound_f16():
+    x = adversarial(3000, 96, seed=5, dtype=np.float16, huge=False)
+    a, b = pairs(3000, 20000, seed=6)
+    assert check_sound(x, a, b) > 0
+
+
+def test_bound_never_flags_non_finite_rows():
+    x = adversarial(500, 96, seed=8)
+    x[100] = np.inf
+    x[101, 3] = np.nan
+    x[102, 5] = -np.inf
+    a = np.repeat(np.arange(100, 103, dtype=np.uint32), 500)
+    b = np.tile(np.arange(500, dtype=np.uint32), 3)
+    for aa, bb in ((a, b), (b, a)):
+        f = D.stage_qbound(x, aa, bb, np.zeros(aa.shape[0], np.float32))
+        assert not f.any()
+
+
+def test_bound_is_strong_on_far_pairs():
+    """Far below the distance the bound proves almost every pair (the
+    property the search relies on for its speed, not for its results)."""
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((3000, 96)).astype(np.float32)
+    x /= np.linalg.norm(x, axis=1, keepdims=True)
+    a, b = pairs(3000, 20000, seed=12)
+    keep = a != b
+    a, b = a[keep], b[keep]
+    d = D.stage_distances(x, a, b)
+    f = D.stage_qbound(x, a, b, d * np.float32(0.9))
+    assert f.mean() > 0.95
+
+
+def test_bound_rejects_unsupported_rows():
+    with pytest.raises(D.BuildError):
+        D.stage_qbound(np.zeros((10, 8), np.uint8), np.zeros(1, np.uint32), np.zeros(1, np.uint32),
+                       np.zeros(1, np.float32))
+    with pytest.raises(D.BuildError):  # 113 dims do not fit one code row
+        D.stage_qbound(np.ones((10, 113), np.float32), np.zeros(1, np.uint32), np.zeros(1, np.uint32),
+                       np.zeros(1, np.float32))
+
+
+class _env:
+    def __init__(self, **kv):
+        self.kv = kv
+
+    def __enter__(self):
+        self.old = {k: os.environ.get(k) for k in self.kv}
+        os.environ.update({k: str(v) for k, v in self.kv.items()})
+
+    def __exit__(self, *exc):
+        for k, v in self.old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+def test_search_stage_on_adversarial_rows():
+    x = adversarial(3000, 96, seed=21)
+    R, L, C, steps = 32, 64, 48, 48
+    s0 = O.init_graph(x, R, C)
+    start, _, _ = O.medoid(x)
+    from test_gpu_parity import assert_state_equal, to_dance
+    want = O.search(x, s0, L, steps, 1.2, start)
+    for env in ({}, {"DANCE_QBOUND": "0"}):
+        with _env(**env):
+            g = D.stage_search(x, to_dance(s0), L, steps, 1.2, start)
+        assert_state_equal(g, want, ("work", "deg_work", "wd"))
+
+
+@pytest.mark.parametrize("profile", ["QUALITY", "FAST_SMALL"])
+def test_build_identical_with_bound_off_first_and_every_iteration(profile):
+    """QUALITY builds on fp32 rows, FAST_SMALL on the same input stored as fp16."""
+    x = adversarial(4000, 96, seed=31, huge=profile == "QUALITY")
+    ox = x if profile == "QUALITY" else x.astype(np.float16)
+    og, od, om = O.vnew2_build(ox, 32, 64, 48, 32)
+    seen = {}
+    try:
+        D.set_profile(profile)
+        for name, env in (("off", {"DANCE_QBOUND": "0"}), ("first", {}), ("all", {"DANCE_QBOUND_ITERS": "15"})):
+            with _env(**env):
+                res = D.vamana_build(x, 32, 64, 48, 32)
+            assert res.medoid == om, name
+            assert np.array_equal(res.degree, od), name
+            assert np.array_equal(res.graph, og), name
+            seen[name] = (res.kernel_profile["bound_checks"], res.kernel_profile["bound_skips"])
+    finally:
+        D.set_profile("QUALITY")
+    assert seen["off"] == (0, 0)
+    assert seen["first"][0] > 0 and seen["first"][1] > 0
+    assert seen["all"][0] > seen["first"][0]
