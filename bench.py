@@ -400,7 +400,8 @@ def main() -> int:
         "stage_ms": {k: round(kp[k], 2) for k in ("medoid_ms", "init_ms", "search_ms", "reverse_ms", "merge_ms",
                                                      "prune_ms", "total_ms")},
         "counters": {k: kp[k] for k in ("search_dist", "insert_dist", "expansions", "vis_skips", "merge_dist",
-                                        "prune_dist", "reverse_edges", "bound_checks", "bound_skips")},
+                                        "prune_dist", "reverse_edges", "bound_checks", "bound_skips",
+                                        "prune_bound_checks", "prune_bound_skips")},
         "search_cycles": ({k: kp[k] for k in ("cyc_select", "cyc_insert", "cyc_dist", "cyc_pool", "cyc_seed",
                                               "cyc_total")} if kp["cyc_total"] else None),
         "roofline": roofline,

@@ -63,6 +63,7 @@ class DanceKernelProfile(C.Structure):
         ("cyc_select", C.c_uint64), ("cyc_insert", C.c_uint64), ("cyc_dist", C.c_uint64),
         ("cyc_pool", C.c_uint64), ("cyc_seed", C.c_uint64), ("cyc_total", C.c_uint64),
         ("bound_checks", C.c_uint64), ("bound_skips", C.c_uint64),
+        ("prune_bound_checks", C.c_uint64), ("prune_bound_skips", C.c_uint64),
     ]
 
 

@@ -22,7 +22,7 @@
 //           + N * (V + 4R + 4 + 16C)            (own vector, cur row, work row r/w)
 //           + bound_checks * 128                (quantized rows, when the bound is on)
 //   merge : merge_dist * 4 (snapshot distance) + reverse_edges * 4 + touched_rows * (16C + 8)
-//   prune : prune_dist * V + (selected rows) * V + N * 24C
+//   prune : prune_dist * V + (selected rows) * V + N * 24C + prune_bound_checks * 128
 //   reverse (keys + sort): N*R*(4*3) + passes * N*R * 20
 
 #include <hip/hip_runtime.h>
@@ -149,15 +149,20 @@ static int launch_init(const Rows& rows, GraphBufs g, hipStream_t s) {
 // the build uses it in the iterations whose bit is set in DANCE_QBOUND_ITERS
 // (default kQBoundIters). Results are identical either way.
 constexpr uint32_t kQBoundIters = 0x1u;  // first iteration: random graph, HBM-bound
+// The prune uses it in the iterations of DANCE_QBOUND_PRUNE_ITERS (default
+// kQBoundPruneIters).
+constexpr uint32_t kQBoundPruneIters = 0x9u;  // first and last (alpha) iterations
 static bool qbound_enabled() {
   const char* e = std::getenv("DANCE_QBOUND");
   return !(e && e[0] == '0');
 }
-static uint32_t qbound_iters() {
-  const char* e = std::getenv("DANCE_QBOUND_ITERS");
+static uint32_t env_mask(const char* name, uint32_t def) {
+  const char* e = std::getenv(name);
   if (e && e[0]) return (uint32_t)std::strtoul(e, nullptr, 0);
-  return kQBoundIters;
+  return def;
 }
+static uint32_t qbound_iters() { return env_mask("DANCE_QBOUND_ITERS", kQBoundIters); }
+static uint32_t qbound_prune_iters() { return env_mask("DANCE_QBOUND_PRUNE_ITERS", kQBoundPruneIters); }
 
 // Builds the code rows for `rows` into buf; returns a disabled set when the
 // row type or width has no bound.
@@ -200,11 +205,11 @@ static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t ste
 }
 
 static int launch_prune(const Rows& rows, GraphBufs g, uint32_t min_degree, float alpha, const uint32_t* order,
-                        VCounters* ctr, hipStream_t s) {
+                        VCounters* ctr, const QBoundSet& qb, hipStream_t s) {
   const int cpl = pick_cpl(rows.rs.nch);
   const uint32_t Cp = round64(g.C), Rp = round64(g.R);
   const size_t lds = (size_t)kWavesPerBlock * prune_lds_words(Cp, Rp) * 4;
-  PruneArgs a{rows.rs, g, min_degree, alpha, order, ctr};
+  PruneArgs a{rows.rs, g, min_degree, alpha, order, ctr, qb};
   return with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
     hipLaunchKernelGGL((k_prune<decltype(dt)::value, decltype(c)::value>), dim3(xcd_grid(g.N)), dim3(kBlock), lds,
                        s, a, Cp, Rp);
@@ -409,7 +414,7 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   DevBuf qbuf;
   QBoundSet qb{};
   DCHECK(build_qbound(rows, qbuf, s, &qb));
-  const uint32_t q_iters = qbound_iters();
+  const uint32_t q_iters = qbound_iters(), q_prune_iters = qbound_prune_iters();
   DHIP(hipEventRecord(e_init, s));
 
   struct IterEv {
@@ -440,7 +445,8 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     DCHECK(launch_merge(rows, g, rws.offs.as<uint32_t>(), srcs, rws.snap.as<float>(), prof, order, ctr, s));
     DHIP(hipEventRecord(iev[it].m1, s));
     const uint32_t md = (it + 1 == kIters) ? kFinalMinDegree : 0u;
-    DCHECK(launch_prune(rows, g, md, alpha, order, ctr, s));
+    const QBoundSet qp_it = ((q_prune_iters >> it) & 1u) ? qb : QBoundSet{nullptr, 0.0f};
+    DCHECK(launch_prune(rows, g, md, alpha, order, ctr, qp_it, s));
     DHIP(hipEventRecord(iev[it].p1, s));
   }
   DHIP(hipStreamSynchronize(s));
@@ -486,12 +492,15 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   p.cyc_total = hc_ctr.cyc_total;
   p.bound_checks = hc_ctr.bound_checks;
   p.bound_skips = hc_ctr.bound_skips;
+  p.prune_bound_checks = hc_ctr.prune_bound_checks;
+  p.prune_bound_skips = hc_ctr.prune_bound_skips;
   const double V = rows.vbytes();
   p.search_bytes = (double)(p.search_dist + p.insert_dist) * V + (double)p.expansions * (4.0 * R + 4.0) +
                    (double)kIters * N * (V + 4.0 * R + 4.0 + 16.0 * C) + (double)p.bound_checks * (kQChunks * 16.0);
   p.merge_bytes = (double)p.merge_dist * 4.0 + (double)p.reverse_edges * 4.0 +
                   (double)p.touched_rows * (16.0 * C + 8.0);
-  p.prune_bytes = (double)p.prune_dist * V + (double)kIters * N * (24.0 * C);
+  p.prune_bytes = (double)p.prune_dist * V + (double)kIters * N * (24.0 * C) +
+                  (double)p.prune_bound_checks * (kQChunks * 16.0);
   const double items = (double)N * R;
   const double passes = (bit_length(N) + 7) / 8;
   p.reverse_bytes = (double)kIters * (items * 16.0 + passes * items * 20.0);
@@ -951,7 +960,10 @@ int dance_stage_prune(const void* h_data, int dtype, uint32_t N, uint32_t dim, u
   StageCtx cx;
   DCHECK(cx.open(h_data, dtype, N, dim));
   DCHECK(upload_state(cx.st, N, R, C, nullptr, nullptr, work, deg_work, wd, cx.s));
-  DCHECK(launch_prune(cx.rows, cx.st.g(), min_degree, alpha, nullptr, nullptr, cx.s));
+  DevBuf qbuf;
+  QBoundSet qb{};
+  DCHECK(build_qbound(cx.rows, qbuf, cx.s, &qb));
+  DCHECK(launch_prune(cx.rows, cx.st.g(), min_degree, alpha, nullptr, nullptr, qb, cx.s));
   return download_state(cx.st, cur, deg_cur, work, deg_work, wd, cx.s);
 }
 

@@ -55,6 +55,7 @@ struct VCounters {
   unsigned long long cyc_select, cyc_insert, cyc_dist, cyc_pool, cyc_seed, cyc_total;
   unsigned long long bound_checks;  // candidates tested with the quantized lower bound
   unsigned long long bound_skips;   // candidates whose exact distance the bound made unnecessary
+  unsigned long long prune_bound_checks, prune_bound_skips;  // the same for prune pairs
 };
 
 // Counters are striped over kCtrStripes copies (by workgroup) so that the
@@ -81,12 +82,29 @@ __device__ __forceinline__ bool valid_for(uint32_t id, uint32_t N, uint32_t node
 
 // ---------------------------------------------------------------------------
 // Register-resident bounded top-L pool (vnew2.cu:520-734).
+//
+// Slot p = r*64 + lane lives in register r of that lane. Besides the id, each
+// slot keeps two ordering keys so that the max and the selection are one
+// wave reduction each, with no per-slot validity tests:
+//   mkey: the distance bits (an order-preserving int for non-negative floats)
+//         of a valid entry with a non-NaN distance, INT_MIN otherwise; the
+//         largest mkey, lowest slot, is the pool's worst entry.
+//   skey: mkey of an entry that can still be expanded (not expanded,
+//         distance < FLT_MAX), INT_MAX otherwise; the smallest skey, lowest
+//         slot, is the next entry to expand.
+// Distances are non-negative (squared L2), so mkey also stores the distance
+// itself; NaN entries (mkey INT_MIN) are never read back as distances.
 // ---------------------------------------------------------------------------
+constexpr int kSelLimit = 0x7F7FFFFF;  // bits of FLT_MAX: keys below it are selectable
+
+__device__ __forceinline__ int pool_mkey(float d) { return d == d ? __float_as_int(d) : INT_MIN; }
+__device__ __forceinline__ int pool_skey(int mk) { return mk != INT_MIN && mk < kSelLimit ? mk : INT_MAX; }
+
 template <int PS>
 struct RegPool {
   uint32_t id[PS];
-  float d[PS];
-  uint32_t expbits;  // bit r: slot r*64+lane expanded
+  int mkey[PS];
+  int skey[PS];
   uint32_t size;
   int max_pos;
   float max_d;
@@ -96,9 +114,9 @@ struct RegPool {
 #pragma unroll
     for (int r = 0; r < PS; ++r) {
       id[r] = DANCE_INV;
-      d[r] = FLT_MAX;
+      mkey[r] = INT_MIN;
+      skey[r] = INT_MAX;
     }
-    expbits = 0u;
     size = 0u;
     max_pos = -1;
     max_d = -FLT_MAX;
@@ -112,44 +130,49 @@ struct RegPool {
       if (r == (pos >> 6)) v = id[r];
     return rdlane_u(v, pos & 63);
   }
+  // Distance of a valid slot (NaN for a NaN entry).
   __device__ __forceinline__ float get_d(int pos) const {
-    float v = FLT_MAX;
+    int v = INT_MIN;
 #pragma unroll
     for (int r = 0; r < PS; ++r)
-      if (r == (pos >> 6)) v = d[r];
-    return rdlane_f(v, pos & 63);
+      if (r == (pos >> 6)) v = mkey[r];
+    const int k = __builtin_amdgcn_readlane(v, pos & 63);
+    return k == INT_MIN ? __builtin_nanf("") : __int_as_float(k);
   }
+  // Slot updates are select instructions on every lane (no divergent
+  // branch, so no register copies at the merge).
   __device__ __forceinline__ void set_slot(int pos, uint32_t nid, float nd, uint32_t lane) {
-    if ((int)lane == (pos & 63)) {
+    const int mk = pool_mkey(nd), sk = pool_skey(mk);
+    const bool hit = (int)lane == (pos & 63);
 #pragma unroll
-      for (int r = 0; r < PS; ++r)
-        if (r == (pos >> 6)) {
-          id[r] = nid;
-          d[r] = nd;
-        }
-      expbits &= ~(1u << (pos >> 6));
+    for (int r = 0; r < PS; ++r) {
+      const bool h = hit && r == (pos >> 6);
+      id[r] = h ? nid : id[r];
+      mkey[r] = h ? mk : mkey[r];
+      skey[r] = h ? sk : skey[r];
     }
   }
   __device__ __forceinline__ void set_d(int pos, float nd, uint32_t lane) {
-    if ((int)lane == (pos & 63)) {
+    const int mk = pool_mkey(nd), sk = pool_skey(mk);
+    const bool hit = (int)lane == (pos & 63);
 #pragma unroll
-      for (int r = 0; r < PS; ++r)
-        if (r == (pos >> 6)) d[r] = nd;
-      expbits &= ~(1u << (pos >> 6));
+    for (int r = 0; r < PS; ++r) {
+      const bool h = hit && r == (pos >> 6);
+      mkey[r] = h ? mk : mkey[r];
+      skey[r] = h ? sk : skey[r];
     }
   }
   __device__ __forceinline__ void set_expanded(int pos, uint32_t lane) {
-    if ((int)lane == (pos & 63)) expbits |= 1u << (pos >> 6);
+    const bool hit = (int)lane == (pos & 63);
+#pragma unroll
+    for (int r = 0; r < PS; ++r) skey[r] = (hit && r == (pos >> 6)) ? INT_MAX : skey[r];
   }
 
   // recompute_max_pos_size_warp: largest distance, lowest slot on ties.
   __device__ __forceinline__ void recompute_max() {
-    int best = INT_MIN;
+    int best = mkey[0];
 #pragma unroll
-    for (int r = 0; r < PS; ++r) {
-      const bool v = id[r] != DANCE_INV && d[r] == d[r];
-      best = max(best, v ? fkey(d[r]) : INT_MIN);
-    }
+    for (int r = 1; r < PS; ++r) best = max(best, mkey[r]);
     const int M = wave_max_i(best);
     if (M == INT_MIN) {
       max_pos = -1;
@@ -160,7 +183,7 @@ struct RegPool {
 #pragma unroll
     for (int r = 0; r < PS; ++r) {
       if (pos < 0) {
-        const uint64_t m = wballot(id[r] != DANCE_INV && d[r] == d[r] && fkey(d[r]) == M);
+        const uint64_t m = wballot(mkey[r] == M);
         if (m) pos = r * 64 + ffs64(m);
       }
     }
@@ -207,20 +230,16 @@ struct RegPool {
   // select_next_unexpanded_size_warp: smallest distance among unexpanded
   // entries with distance < FLT_MAX, lowest slot on ties; -1 if none.
   __device__ __forceinline__ int select() const {
-    int best = INT_MAX;
+    int best = skey[0];
 #pragma unroll
-    for (int r = 0; r < PS; ++r) {
-      const bool c = id[r] != DANCE_INV && ((expbits >> r) & 1u) == 0u && d[r] < FLT_MAX;
-      best = min(best, c ? fkey(d[r]) : INT_MAX);
-    }
+    for (int r = 1; r < PS; ++r) best = min(best, skey[r]);
     const int M = wave_min_i(best);
     if (M == INT_MAX) return -1;
     int pos = -1;
 #pragma unroll
     for (int r = 0; r < PS; ++r) {
       if (pos < 0) {
-        const bool c = id[r] != DANCE_INV && ((expbits >> r) & 1u) == 0u && d[r] < FLT_MAX;
-        const uint64_t m = wballot(c && fkey(d[r]) == M);
+        const uint64_t m = wballot(skey[r] == M);
         if (m) pos = r * 64 + ffs64(m);
       }
     }
@@ -635,9 +654,22 @@ struct PruneArgs {
   float alpha;
   const uint32_t* order;
   VCounters* ctr;
+  QBoundSet qb;  // quantized lower bound (qb.rows == nullptr: exact distances only)
 };
 
-__host__ __device__ constexpr uint32_t prune_lds_words(uint32_t Cp, uint32_t Rp) { return 4u * Cp + 2u * Rp; }
+__host__ __device__ constexpr uint32_t prune_lds_words(uint32_t Cp, uint32_t Rp) { return 5u * Cp + 2u * Rp; }
+
+// Threshold of the prune's bound for a candidate at stored distance sd: a
+// pair distance d >= T gives fl(alpha * d) >= fl(alpha * T) > sd, so the
+// candidate survives. Returns sqrt((T + 1e-30)(1 + kappa2)) rounded up, the
+// per-candidate part of q_threshold; +inf (never skipped) for sd < 1e-30 or
+// non-finite sd, where the relative slack would not cover rounding.
+__device__ __forceinline__ float prune_bound_root(const QBoundSet& qb, float sd, float alpha) {
+  if (!(sd >= 1e-30f) || !(sd <= FLT_MAX)) return __builtin_inff();
+  const float T = sd / alpha * (1.0f + 0x1p-20f);
+  const float t = (T + 1e-30f) * (1.0f + qb.kappa2);
+  return __builtin_sqrtf(t) * (1.0f + kQSlack);
+}
 
 constexpr uint32_t PR_REMOVED = 1u, PR_INOUT = 2u;
 
@@ -657,8 +689,10 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
   uint32_t* lst = sid + 3 * Cp;
   uint32_t* oid = sid + 4 * Cp;
   float* od = reinterpret_cast<float*>(oid + Rp);
+  float* sroot = od + Rp;  // prune_bound_root of each candidate
   const size_t wb = (size_t)node * C, cb = (size_t)node * R;
   const uint32_t deg = min(g.deg_work[node], C);
+  const bool qon = a.qb.rows != nullptr;
   for (uint32_t i = lane; i < Cp; i += 64) {
     uint32_t id = DANCE_INV;
     float dist = FLT_MAX;
@@ -674,9 +708,10 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
     sid[i] = id;
     sd[i] = dist;
     fl[i] = f;
+    if (qon) sroot[i] = prune_bound_root(a.qb, dist, a.alpha);
   }
   wave_sync();
-  uint32_t oc = 0, npair = 0;
+  uint32_t oc = 0, npair = 0, nbchk = 0, nbskip = 0;
   for (uint32_t round = 0; round < R; ++round) {
     int best = INT_MAX;
     for (uint32_t i = lane; i < Cp; i += 64) {
@@ -713,6 +748,46 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
     }
     wave_sync();
     if (nq == 0) continue;
+    if (qon) {
+      // Drop the candidates whose pair distance the bound proves large
+      // enough to keep them; their exact distance cannot remove them.
+      const uint4* qs = a.qb.rows + (size_t)sel * kQChunks;
+      const uint4 code = qs[sub];
+      const QSelf me{qs, __uint_as_float(uni_u(rdlane_u(code.x, 0))), __uint_as_float(uni_u(rdlane_u(code.y, 0))),
+                     __uint_as_float(uni_u(rdlane_u(code.z, 0)))};
+      uint32_t nk = 0;
+      for (uint32_t base = 0; base < nq; base += 64) {  // lst holds up to C entries
+        const uint32_t nb = min(64u, nq - base);
+        uint64_t keep = 0;
+        for (uint32_t p = 0; p < nb; p += 8 * kQInFlight) {
+          uint4 b[kQInFlight];
+          uint32_t si[kQInFlight];
+#pragma unroll
+          for (uint32_t u = 0; u < kQInFlight; ++u) {
+            const uint32_t k = p + 8 * u + grp;
+            si[u] = k < nb ? lst[base + k] : 0u;
+            b[u] = q_load(a.qb, k < nb ? sid[si[u]] : 0u, k < nb, sub);
+          }
+#pragma unroll
+          for (uint32_t u = 0; u < kQInFlight; ++u) {
+            const uint32_t k = p + 8 * u + grp;
+            const float sT = (sroot[si[u]] + me.r) * (1.0f + kQSlack);
+            const bool prove = q_proves_reject(me, code, sT, b[u], k < nb, sub);
+            keep |= (uint64_t)octet_bits(wballot(sub == 0 && k < nb && !prove)) << (p + 8 * u);
+          }
+        }
+        // compact in place: writes land at or below the entries just read
+        const uint32_t v = lane < nb ? lst[base + lane] : 0u;
+        wave_sync();
+        if ((keep >> lane) & 1ull) lst[nk + mbcnt64(keep)] = v;
+        wave_sync();
+        nk += popc64(keep);
+      }
+      nbchk += nq;
+      nbskip += nq - nk;
+      nq = nk;
+      if (nq == 0) continue;
+    }
     uint4 sv[CPL];
     load_row<CPL>(a.rs, sel, true, sub, sv);
     for (uint32_t p = 0; p < nq; p += 16) {
@@ -769,7 +844,13 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
     g.deg_work[node] = oc;
     g.deg_cur[node] = oc;
   }
-  if (a.ctr && lane == 0) atomicAdd(&ctr_stripe(a.ctr)->prune_dist, (unsigned long long)npair);
+  if (a.ctr && lane == 0) {
+    atomicAdd(&ctr_stripe(a.ctr)->prune_dist, (unsigned long long)npair);
+    if (qon) {
+      atomicAdd(&ctr_stripe(a.ctr)->prune_bound_checks, (unsigned long long)nbchk);
+      atomicAdd(&ctr_stripe(a.ctr)->prune_bound_skips, (unsigned long long)nbskip);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------

@@ -36,6 +36,10 @@ typedef struct DanceKernelProfile {
      * (proved >= the pool threshold). DANCE_QBOUND=0 disables the bound;
      * DANCE_QBOUND_ITERS selects the iterations (bit i = iteration i). */
     uint64_t bound_checks, bound_skips;
+    /* The same bound in RobustPrune: pairs tested, and pairs it proved far
+     * enough that the candidate survives (DANCE_QBOUND_PRUNE_ITERS selects
+     * the iterations). */
+    uint64_t prune_bound_checks, prune_bound_skips;
 } DanceKernelProfile;
 
 /* Full standard (vnew2) build with the vectors already resident in device

@@ -140,6 +140,21 @@ def test_search_stage_on_adversarial_rows():
         assert_state_equal(g, want, ("work", "deg_work", "wd"))
 
 
+@pytest.mark.parametrize("alpha", [1.0, 1.2, 2.0])
+@pytest.mark.parametrize("C", [80, 150])
+def test_prune_stage_on_adversarial_rows(alpha, C):
+    """Candidate lists longer than one wave (C = 150) and both min-degree modes."""
+    from test_gpu_parity import assert_state_equal, random_work_state, to_dance
+    x = adversarial(2500, 96, seed=41)
+    s0 = random_work_state(x, 32, C, seed=43)
+    for md in (0, 32):
+        want = O.prune(x, s0, md, alpha)
+        for env in ({}, {"DANCE_QBOUND": "0"}):
+            with _env(**env):
+                g = D.stage_prune(x, to_dance(s0), md, alpha)
+            assert_state_equal(g, want)
+
+
 @pytest.mark.parametrize("profile", ["QUALITY", "FAST_SMALL"])
 def test_build_identical_with_bound_off_first_and_every_iteration(profile):
     """QUALITY builds on fp32 rows, FAST_SMALL on the same input stored as fp16."""
@@ -149,15 +164,19 @@ def test_build_identical_with_bound_off_first_and_every_iteration(profile):
     seen = {}
     try:
         D.set_profile(profile)
-        for name, env in (("off", {"DANCE_QBOUND": "0"}), ("first", {}), ("all", {"DANCE_QBOUND_ITERS": "15"})):
+        for name, env in (("off", {"DANCE_QBOUND": "0"}), ("first", {}),
+                          ("all", {"DANCE_QBOUND_ITERS": "15", "DANCE_QBOUND_PRUNE_ITERS": "15"}),
+                          ("prune_none", {"DANCE_QBOUND_PRUNE_ITERS": "0"})):
             with _env(**env):
                 res = D.vamana_build(x, 32, 64, 48, 32)
             assert res.medoid == om, name
             assert np.array_equal(res.degree, od), name
             assert np.array_equal(res.graph, og), name
-            seen[name] = (res.kernel_profile["bound_checks"], res.kernel_profile["bound_skips"])
+            kp = res.kernel_profile
+            seen[name] = (kp["bound_checks"], kp["bound_skips"], kp["prune_bound_checks"], kp["prune_bound_skips"])
     finally:
         D.set_profile("QUALITY")
-    assert seen["off"] == (0, 0)
-    assert seen["first"][0] > 0 and seen["first"][1] > 0
+    assert seen["off"] == (0, 0, 0, 0)
+    assert seen["first"][0] > 0 and seen["first"][1] > 0 and seen["first"][3] > 0
     assert seen["all"][0] > seen["first"][0]
+    assert seen["prune_none"][2:] == (0, 0)
