@@ -187,12 +187,18 @@ struct RegPool {
         if (m) pos = r * 64 + ffs64(m);
       }
     }
-    max_pos = pos;
-    max_d = __int_as_float(M);
+    // wave-uniform: keep the loop-carried pool state in scalar registers
+    max_pos = uni_i(pos);
+    max_d = uni_f(__int_as_float(M));
   }
 
   // insert_top_l_state_warp with ENABLE_TOPL_EARLY_REJECT=1. `nid`/`nd` are uniform.
   __device__ __forceinline__ void insert(uint32_t nid, float nd, uint32_t lane) {
+    // The pool state is wave-uniform; reading it through readfirstlane makes
+    // every branch below a scalar branch (no exec-masked regions).
+    size = uni_u(size);
+    max_pos = uni_i(max_pos);
+    max_d = uni_f(max_d);
     if (nid == DANCE_INV) return;
     if (size >= L && max_pos >= 0 && nd >= max_d) return;
     int same = -1;
@@ -214,10 +220,10 @@ struct RegPool {
     if (size < L) {
       const int pos = (int)size;
       set_slot(pos, nid, nd, lane);
-      size++;
+      size = uni_u(size + 1u);
       if (max_pos < 0 || nd > max_d) {
-        max_pos = pos;
-        max_d = nd;
+        max_pos = uni_i(pos);
+        max_d = uni_f(nd);
       }
       return;
     }
@@ -225,6 +231,31 @@ struct RegPool {
       set_slot(max_pos, nid, nd, lane);
       recompute_max();
     }
+  }
+
+  // insert() for a pool with size >= L and max_pos >= 0 (which every path
+  // below preserves) and a valid candidate id.
+  __device__ __forceinline__ void insert_full(uint32_t nid, float nd, uint32_t lane) {
+    max_pos = uni_i(max_pos);
+    max_d = uni_f(max_d);
+    if (!(nd < max_d)) return;  // a NaN distance changes nothing in insert() either
+    int same = -1;
+#pragma unroll
+    for (int r = 0; r < PS; ++r) {
+      if (same < 0) {
+        const uint64_t m = wballot(id[r] == nid);
+        if (m) same = r * 64 + ffs64(m);
+      }
+    }
+    if (same >= 0) {
+      if (nd < get_d(same)) {
+        set_d(same, nd, lane);
+        if (same == max_pos) recompute_max();
+      }
+      return;
+    }
+    set_slot(max_pos, nid, nd, lane);
+    recompute_max();
   }
 
   // select_next_unexpanded_size_warp: smallest distance among unexpanded
@@ -350,10 +381,21 @@ struct SearchWave {
     bool keep = lane < nx;
     if (full) keep = keep && dk < P.max_d;
     uint64_t km = wballot(keep);
-    while (km) {
-      const int k = ffs64(km);
-      km &= km - 1;
-      P.insert(rdlane_u(ck, k), rdlane_f(dk, k), lane);
+    if (full) {
+      // A pool that starts the batch full stays full with a valid worst
+      // entry, so insert() reduces to: reject unless below the worst,
+      // refresh a duplicate, else replace the worst slot.
+      while (km) {
+        const int k = ffs64(km);
+        km &= km - 1;
+        P.insert_full(rdlane_u(ck, k), rdlane_f(dk, k), lane);
+      }
+    } else {
+      while (km) {
+        const int k = ffs64(km);
+        km &= km - 1;
+        P.insert(rdlane_u(ck, k), rdlane_f(dk, k), lane);
+      }
     }
     if (need) vis[slot] = c;
     wave_sync();

@@ -225,11 +225,13 @@ __device__ __forceinline__ float octet_finish(const uint4 (&a)[CPL], const uint4
 __device__ __forceinline__ int fkey(float d) { return __float_as_int(d); }
 
 // Distances from a cached vector `av` to up to 64 ids lst[0..n) -> lsd[0..n).
-// Two passes of 8 octets are kept in flight. Returns after lsd is visible.
+// Two passes of 8 octets are kept in flight (one for a last group of <= 8).
+// Returns after lsd is visible.
 template <int DT, int CPL>
 __device__ __forceinline__ void batch_dist(const RowSet& rs, const uint4 (&av)[CPL], const uint32_t* lst,
                                            float* lsd, uint32_t n, uint32_t grp, uint32_t sub) {
-  for (uint32_t p = 0; p < n; p += 16) {
+  uint32_t p = 0;
+  for (; p + 8 < n; p += 16) {
     const uint32_t k0 = p + grp, k1 = p + 8 + grp;
     const bool a0 = k0 < n, a1 = k1 < n;
     const uint32_t id0 = a0 ? lst[k0] : 0u, id1 = a1 ? lst[k1] : 0u;
@@ -242,6 +244,14 @@ __device__ __forceinline__ void batch_dist(const RowSet& rs, const uint4 (&av)[C
       if (a0) lsd[k0] = d0;
       if (a1) lsd[k1] = d1;
     }
+  }
+  if (p < n) {  // a last group of at most 8: one pass
+    const uint32_t k0 = p + grp;
+    const bool a0 = k0 < n;
+    uint4 b0[CPL];
+    load_row<CPL>(rs, a0 ? lst[k0] : 0u, a0, sub, b0);
+    const float d0 = octet_finish<DT, CPL>(av, b0);
+    if (sub == 0 && a0) lsd[k0] = d0;
   }
   wave_sync();
 }
