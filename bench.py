@@ -267,7 +267,7 @@ def run_c5(args, mode) -> int:
                                                         "csr_ms", "diagnostics_ms", "total_ms")}
         line["counters"] = {k: kp[k] for k in ("task_dist", "union_dist", "work_dist", "prune_dist", "csr_dist",
                                                "csr_prune_dist", "merged_candidates", "quota_dropped",
-                                               "reverse_edges", "touched_rows", "long_lists")}
+                                               "reverse_edges", "touched_rows", "long_lists", "long_fallbacks")}
         line["diagnostics"] = {k: st[k] for k in ("invalid_neighbor_count", "self_loop_count", "out_degree_min",
                                                   "out_degree_max", "out_degree_avg", "avg_common_label_out_degree",
                                                   "low_common_label_degree_count")}

@@ -111,7 +111,7 @@ class DanceFilteredProfile(C.Structure):
         + [(n, C.c_uint64) for n in ("task_dist", "union_dist", "work_dist", "prune_dist", "csr_dist",
                                      "csr_prune_dist", "merged_candidates", "quota_dropped", "reverse_edges",
                                      "touched_rows", "csr_candidates", "long_lists", "out_edges",
-                                     "common_edges")]
+                                     "common_edges", "long_fallbacks")]
     )
 
 

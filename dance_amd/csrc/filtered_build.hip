@@ -359,6 +359,7 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   kp.touched_rows = hc[kTouchedRows];
   kp.csr_candidates = hc[kCsrCandidates];
   kp.long_lists = hc[kBigRows];
+  kp.long_fallbacks = hc[kBigFallback];
   kp.out_edges = h64[0];
   kp.common_edges = h64[1];
   if (verbose())

@@ -38,8 +38,12 @@ constexpr uint32_t kCsrRegMax = 64u * kCsrSlots;
 constexpr uint32_t kRandomAttempts = 1u << 20;
 // LDS words per wave: visited cache + one distance batch (ids, distances).
 constexpr uint32_t kSearchLds = kVis + 128u;
-// LDS words per wave of k_csr: forward row + one distance batch.
-constexpr uint32_t kCsrLds = 64u + 128u;
+// Long lists are pruned on their kCsrPrefix smallest candidates first.
+constexpr uint32_t kCsrPrefix = kCsrRegMax;
+// LDS words per wave of k_csr: forward row + one distance batch + the
+// prefix staging area (ids, distances; its first 256 words double as the
+// radix-select histogram).
+constexpr uint32_t kCsrLds = 64u + 128u + 2u * kCsrPrefix;
 
 // Device counters (u64 each).
 enum : uint32_t {
@@ -54,6 +58,7 @@ enum : uint32_t {
   kTouchedRows,
   kCsrCandidates,
   kBigRows,
+  kBigFallback,
   kNumCounters
 };
 // Counters are striped over kCtrStripes copies (by workgroup) so that per-wave
@@ -447,6 +452,139 @@ __device__ __forceinline__ uint32_t prune_mem(const RowSet& rs, const Labels& L,
   return sel;
 }
 
+// Selection key of a live entry: distance bits (order-preserving for
+// non-negative floats), then id. Entries that can never be selected
+// (distance NaN or above FLT_MAX) get the largest key.
+__device__ __forceinline__ uint64_t prune_key(float d, uint32_t id) {
+  return d <= FLT_MAX ? (((uint64_t)(uint32_t)fkey(d) << 32) | id) : ~0ull;
+}
+
+// Inclusive prefix sum over the wave.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, uint32_t lane) {
+#pragma unroll
+  for (uint32_t o = 1; o < 64; o <<= 1) {
+    const uint32_t u = (uint32_t)__shfl_up((int)v, (int)o, 64);
+    if (lane >= o) v += u;
+  }
+  return v;
+}
+
+// FilteredRobustPrune of a long list (prune_mem's contract) that first runs
+// on the kCsrPrefix entries with the smallest keys. Each round selects the
+// smallest live key, so while the prefix still has a selectable entry every
+// selection and every removal decision equals the full prune's; when the
+// prefix runs out before R selections and entries outside it remain, the
+// full prune_mem runs instead (counted in kBigFallback). Keys are unique
+// (live ids are unique), so the prefix is an exact radix select on the
+// 64-bit key, 8 bits per pass.
+template <int DT, int CPL, typename Ids>
+__device__ __forceinline__ uint32_t prune_long(const RowSet& rs, const Labels& L, uint32_t row, uint32_t R,
+                                               float alpha, uint32_t n, Ids&& ids, const float* d, uint8_t* rem,
+                                               uint32_t* msk, uint32_t* lst, float* lsd, uint32_t* stage,
+                                               uint32_t lane, uint32_t& outv, uint32_t& ndist, bool& fallback) {
+  fallback = false;
+  auto key_at = [&](uint32_t i) -> uint64_t { return rem[i] ? ~0ull : prune_key(d[i], ids(i)); };
+  uint32_t total = 0;
+  for (uint32_t b = 0; b < n; b += 64) {
+    const uint32_t i = b + lane;
+    total += popc64(wballot(i < n && key_at(i) != ~0ull));
+  }
+  // Radix select: after the loop, the prefix is every key whose top
+  // (64 - shift) bits are <= pre (the kCsrPrefix smallest, or all).
+  uint64_t pre = ~0ull;
+  int shift = 0;
+  if (total > kCsrPrefix) {
+    uint32_t need = kCsrPrefix;
+    uint64_t acc = 0;
+    shift = 64;
+    uint32_t* hist = stage;
+    while (true) {
+      shift -= 8;
+      for (uint32_t j = lane; j < 256; j += 64) hist[j] = 0u;
+      wave_sync();
+      for (uint32_t b = 0; b < n; b += 64) {
+        const uint32_t i = b + lane;
+        const uint64_t k = i < n ? key_at(i) : ~0ull;
+        const bool match = k != ~0ull && (shift == 56 || (k >> (shift + 8)) == acc);
+        if (match) atomicAdd(&hist[(uint32_t)(k >> shift) & 255u], 1u);
+      }
+      wave_sync();
+      uint32_t c[4], sum = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        c[j] = hist[lane * 4 + j];
+        sum += c[j];
+      }
+      const uint32_t incl = wave_incl_scan(sum, lane);
+      uint32_t before = incl - sum;
+      uint32_t digit = 0, below = 0, cnt = 0;
+      bool found = false;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool cross = !found && before < need && before + c[j] >= need;
+        if (cross) {
+          digit = lane * 4 + j;
+          below = before;
+          cnt = c[j];
+          found = true;
+        }
+        before += c[j];
+      }
+      const uint64_t fm = wballot(found);
+      if (!fm) {  // cannot happen with unique keys; stay exact regardless
+        fallback = true;
+        return prune_mem<DT, CPL>(rs, L, row, R, alpha, n, ids, d, rem, msk, lst, lsd, lane, outv, ndist);
+      }
+      const int fl = ffs64(fm);
+      digit = rdlane_u(digit, fl);
+      below = rdlane_u(below, fl);
+      cnt = rdlane_u(cnt, fl);
+      wave_sync();
+      need -= below;
+      acc = (acc << 8) | digit;
+      if (cnt == need || shift == 0) break;
+    }
+    pre = acc;
+  }
+  // Stage the prefix (ids, distances) in LDS, then one entry per slot.
+  uint32_t* sid = stage;
+  float* sdd = reinterpret_cast<float*>(stage + kCsrPrefix);
+  uint32_t np = 0;
+  for (uint32_t b = 0; b < n; b += 64) {
+    const uint32_t i = b + lane;
+    const uint64_t k = i < n ? key_at(i) : ~0ull;
+    const bool in = k != ~0ull && (shift == 64 ? true : (k >> shift) <= pre);
+    const uint64_t m = wballot(in);
+    const uint32_t p = np + mbcnt64(m);
+    if (in && p < kCsrPrefix) {
+      sid[p] = (uint32_t)k;
+      sdd[p] = d[i];
+    }
+    np += popc64(m);
+  }
+  wave_sync();
+  if (np > kCsrPrefix) {  // only with repeated keys, which live lists do not have
+    fallback = true;
+    return prune_mem<DT, CPL>(rs, L, row, R, alpha, n, ids, d, rem, msk, lst, lsd, lane, outv, ndist);
+  }
+  uint32_t pid[kCsrSlots];
+  float pdist[kCsrSlots];
+  uint32_t prem = 0;
+#pragma unroll
+  for (int e = 0; e < (int)kCsrSlots; ++e) {
+    const uint32_t p = (uint32_t)e * 64u + lane;
+    pid[e] = p < np ? sid[p] : DANCE_INV;
+    pdist[e] = p < np ? sdd[p] : FLT_MAX;
+    if (p >= np) prem |= 1u << e;
+  }
+  wave_sync();
+  const uint32_t sel = prune_regs<DT, CPL, (int)kCsrSlots>(rs, L, row, R, alpha, pid, pdist, prem, lst, lsd, lane,
+                                                            outv, ndist);
+  if (sel >= R || total <= np) return sel;
+  fallback = true;
+  return prune_mem<DT, CPL>(rs, L, row, R, alpha, n, ids, d, rem, msk, lst, lsd, lane, outv, ndist);
+}
+
 // ---------------------------------------------------------------------------
 // Kernels.
 // ---------------------------------------------------------------------------
@@ -822,6 +960,7 @@ __global__ __launch_bounds__(kBlock) void k_csr(RowSet rs, Graph G, Labels L, Cs
   uint32_t* fw = smem + w * kCsrLds;
   uint32_t* lst = fw + 64;
   float* lsd = reinterpret_cast<float*>(fw + 128);
+  uint32_t* stage = fw + 192;
   const uint32_t deg = min(G.d[row], R);
   fw[lane] = lane < deg ? G.g[gb + lane] : DANCE_INV;
   wave_sync();
@@ -839,6 +978,7 @@ __global__ __launch_bounds__(kBlock) void k_csr(RowSet rs, Graph G, Labels L, Cs
     return true;
   };
   uint32_t nd = 0, npd = 0, nlive = 0, outv, sel;
+  bool fell_back = false;
   if (n <= kCsrRegMax) {
     uint32_t id[kCsrSlots];
     float d[kCsrSlots];
@@ -888,7 +1028,8 @@ __global__ __launch_bounds__(kBlock) void k_csr(RowSet rs, Graph G, Labels L, Cs
       if (ok) bd[i] = lsd[pos];
       wave_sync();
     }
-    sel = prune_mem<DT, CPL>(rs, L, row, R, A.alpha, n, id_at, bd, brem, bmask, lst, lsd, lane, outv, npd);
+    sel = prune_long<DT, CPL>(rs, L, row, R, A.alpha, n, id_at, bd, brem, bmask, lst, lsd, stage, lane, outv, npd,
+                              fell_back);
   }
   if (lane < R) A.gout[gb + lane] = lane < sel ? outv : DANCE_INV;
   if (lane == 0) {
@@ -899,6 +1040,7 @@ __global__ __launch_bounds__(kBlock) void k_csr(RowSet rs, Graph G, Labels L, Cs
       atomicAdd(ctr_at(A.ctr, kTouchedRows), 1ull);
       atomicAdd(ctr_at(A.ctr, kCsrCandidates), (unsigned long long)nlive);
       if (n > kCsrRegMax) atomicAdd(ctr_at(A.ctr, kBigRows), 1ull);
+      if (fell_back) atomicAdd(ctr_at(A.ctr, kBigFallback), 1ull);
     }
   }
 }

@@ -73,6 +73,8 @@ typedef struct DanceFilteredProfile {
     uint64_t task_dist, union_dist, work_dist, prune_dist, csr_dist, csr_prune_dist;
     uint64_t merged_candidates, quota_dropped, reverse_edges, touched_rows, csr_candidates, long_lists;
     uint64_t out_edges, common_edges;
+    /* long CSR lists whose prune needed more than their 256 smallest candidates */
+    uint64_t long_fallbacks;
 } DanceFilteredProfile;
 
 /* The filtered build of gpu_vamana_filtered_build_{uint8,float} (reference:
