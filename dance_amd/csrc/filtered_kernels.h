@@ -625,7 +625,7 @@ __global__ __launch_bounds__(kBlock) void k_task_search(RowSet rs, Graph G, Labe
                                                         uint32_t steps, uint32_t* out_ids, float* out_d,
                                                         unsigned long long* ctr) {
   extern __shared__ uint32_t smem[];
-  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t w = wave_index();
   const uint32_t t = xcd_block(blockIdx.x, gridDim.x) * kWaves + w;
   if (t >= tasks) return;
   const uint32_t lane = lane_id();
@@ -717,7 +717,7 @@ struct MList {
 template <int DT, int CPL>
 __global__ __launch_bounds__(kBlock) void k_row(RowSet rs, Graph G, Labels L, RowArgs A) {
   extern __shared__ uint32_t smem[];
-  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t w = wave_index();
   const uint32_t row = xcd_block(blockIdx.x, gridDim.x) * kWaves + w;
   const uint32_t N = G.N, R = G.R;
   if (row >= N) return;
@@ -945,7 +945,7 @@ struct CsrArgs {
 template <int DT, int CPL>
 __global__ __launch_bounds__(kBlock) void k_csr(RowSet rs, Graph G, Labels L, CsrArgs A) {
   extern __shared__ uint32_t smem[];
-  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t w = wave_index();
   const uint32_t row = xcd_block(blockIdx.x, gridDim.x) * kWaves + w;
   const uint32_t N = G.N, R = G.R;
   if (row >= N) return;

@@ -15,7 +15,7 @@ constexpr uint32_t kScanTile = kScanThreads * kScanItems;  // 4096
 
 // Inclusive scan across the 256 threads of a block (4 waves).
 __device__ __forceinline__ uint32_t block_inclusive_scan(uint32_t v, uint32_t* wsum) {
-  const uint32_t lane = lane_id(), w = threadIdx.x >> 6;
+  const uint32_t lane = lane_id(), w = wave_index();
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
     const uint32_t u = (uint32_t)__shfl_up((int)v, o);
@@ -97,7 +97,7 @@ static __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(const ui
                                                                  uint32_t* __restrict__ ovals) {
   __shared__ uint32_t wcnt[4][256];
   __shared__ uint32_t gbase[256];
-  const uint32_t lane = lane_id(), w = threadIdx.x >> 6;
+  const uint32_t lane = lane_id(), w = wave_index();
   for (uint32_t i = threadIdx.x; i < 4 * 256; i += kRadixThreads) (&wcnt[0][0])[i] = 0u;
   gbase[threadIdx.x] = hist_scanned[(size_t)threadIdx.x * num_tiles + blockIdx.x];
   __syncthreads();

@@ -169,7 +169,7 @@ __device__ __forceinline__ bool q_has_label(const QArgs& a, uint32_t p, uint32_t
 template <int DT, int CPL, int PS>
 __global__ __launch_bounds__(kBlock) void k_query(RowSet base, RowSet qrows, QArgs a) {
   extern __shared__ uint32_t smem[];
-  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t w = wave_index();
   const uint32_t q = blockIdx.x * kWaves + w;
   if (q >= a.nq) return;
   const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;

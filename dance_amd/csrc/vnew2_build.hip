@@ -636,7 +636,7 @@ template <int DT, int CPL>
 __global__ __launch_bounds__(kBlock) void k_pair_dist(RowSet rs, const uint32_t* __restrict__ a,
                                                       const uint32_t* __restrict__ b, uint64_t n,
                                                       float* __restrict__ out) {
-  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t w = wave_index();
   const uint64_t base = ((uint64_t)blockIdx.x * kWavesPerBlock + w) * 64;
   if (base >= n) return;
   const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;
@@ -657,7 +657,7 @@ __global__ __launch_bounds__(kBlock) void k_qbound_pairs(QBoundSet qb, const uin
                                                          const uint32_t* __restrict__ b,
                                                          const float* __restrict__ T, uint64_t n,
                                                          uint32_t* __restrict__ flag) {
-  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t w = wave_index();
   const uint64_t base = ((uint64_t)blockIdx.x * kWavesPerBlock + w) * 64;
   if (base >= n) return;
   const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;

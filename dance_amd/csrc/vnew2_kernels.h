@@ -677,7 +677,7 @@ constexpr int kSearchMinWaves = (CPL <= 3 && PS == 2) ? 5 : 1;
 template <int DT, int CPL, int PS>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kSearchMinWaves<CPL, PS>))) void k_search(SearchArgs a, uint32_t Cp) {
   extern __shared__ uint32_t smem[];
-  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t w = wave_index();
   const uint32_t gw = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + w;
   if (gw >= a.g.N) return;
   const uint32_t node = a.order ? a.order[gw] : gw;
@@ -718,7 +718,7 @@ constexpr uint32_t PR_REMOVED = 1u, PR_INOUT = 2u;
 template <int DT, int CPL>
 __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint32_t Rp) {
   extern __shared__ uint32_t smem[];
-  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t w = wave_index();
   const uint32_t gw = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + w;
   const GraphBufs& g = a.g;
   if (gw >= g.N) return;
@@ -940,7 +940,7 @@ __host__ __device__ constexpr uint32_t merge_lds_words(uint32_t Cp) { return 2u 
 template <int DT, int CPL>
 __global__ __launch_bounds__(kBlock) void k_merge(MergeArgs a, uint32_t Cp) {
   extern __shared__ uint32_t smem[];
-  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t w = wave_index();
   const uint32_t gw = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + w;
   const GraphBufs& g = a.g;
   if (gw >= g.N) return;
@@ -1117,7 +1117,7 @@ __host__ __device__ constexpr uint32_t merge_reg_lds_words() { return 128u; }
 template <int DT, int CPL, int MS>
 __global__ __launch_bounds__(kBlock) void k_merge_reg(MergeArgs a) {
   extern __shared__ uint32_t smem[];
-  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t w = wave_index();
   const uint32_t gw = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + w;
   const GraphBufs& g = a.g;
   if (gw >= g.N) return;
@@ -1220,7 +1220,7 @@ template <int DT, int CPL>
 __global__ __launch_bounds__(kBlock) void k_medoid(RowSet rs, uint32_t N, uint32_t nc, uint32_t ns,
                                                    float* scores, uint32_t* cands) {
   __shared__ float buf[kWavesPerBlock][512];
-  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t w = wave_index();
   const uint32_t cw = blockIdx.x * kWavesPerBlock + w;
   if (cw >= nc) return;
   const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;
@@ -1266,7 +1266,7 @@ template <int DT, int CPL>
 __global__ __launch_bounds__(kBlock) void k_init(RowSet rs, GraphBufs g) {
   __shared__ uint32_t lstb[kWavesPerBlock][64];
   __shared__ float lsdb[kWavesPerBlock][64];
-  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t w = wave_index();
   const uint32_t node = blockIdx.x * kWavesPerBlock + w;
   const uint32_t N = g.N, R = g.R, C = g.C;
   if (node >= N) return;
@@ -1315,7 +1315,7 @@ __global__ __launch_bounds__(kBlock) void k_cells(RowSet rs, uint32_t N, const u
                                                   uint32_t K, uint32_t* __restrict__ cell,
                                                   uint32_t* __restrict__ vid) {
   const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;
-  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t w = wave_index();
   const uint32_t v = (blockIdx.x * kWavesPerBlock + w) * 8 + grp;
   if ((blockIdx.x * kWavesPerBlock + w) * 8 >= N) return;
   const bool act = v < N;

@@ -45,6 +45,10 @@ __device__ __forceinline__ float rdlane_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
+// Index of this wave in its workgroup, as a scalar: everything derived from it
+// (LDS bases, vertex ids, row addresses) then lives in SGPRs.
+__device__ __forceinline__ uint32_t wave_index() { return uni_u(threadIdx.x >> 6); }
+
 // Orders LDS traffic between lanes of one wave (the wave runs in lockstep;
 // this keeps the compiler from reordering and drains outstanding LDS ops).
 __device__ __forceinline__ void wave_sync() {
