@@ -140,6 +140,7 @@ EXPORTS = [
     "gpu_vamana_filtered_build_uint8", "gpu_vamana_filtered_build_float", "gpu_vamana_filtered_get_last_stats",
     "dance_filtered_build", "dance_filtered_build_resident", "dance_get_last_filtered_profile",
     "dance_search", "dance_search_resident", "dance_get_last_search_stats",
+    "dance_merge_shards", "dance_merge_get_last_stats",
 ]
 
 _LIB = None

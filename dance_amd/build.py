@@ -27,7 +27,7 @@ HIP_FLAGS = [
 ]
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-pthread", "-Wall", "-Wextra", "-Wno-unused-parameter"]
 
-HIP_SOURCES = ["vnew2_build.hip", "filtered_build.hip", "query_search.hip"]
+HIP_SOURCES = ["vnew2_build.hip", "filtered_build.hip", "query_search.hip", "merge_shards.hip"]
 HOST_SOURCES = ["synth.cpp"]
 APP_SOURCES = ["gpu_vamana_memory_index.cpp", "gpu_stitched_vamana_index.cpp"]
 

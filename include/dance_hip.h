@@ -134,6 +134,30 @@ int dance_search_resident(const void *d_data, int dtype, uint32_t num_points, ui
 
 void dance_get_last_search_stats(DanceSearchStats *stats);
 
+/* ---- shard-graph merge (gpu_merge.h) ---- */
+
+/* Counters and timings of the last merge_shards_gpu / dance_merge_shards call.
+ * unique_edges counts distinct (source, target) pairs after self loops are
+ * dropped; output_edges those kept under max_degree; long_segments the sources
+ * whose edge list exceeded one wave's LDS sort and took the radix-sort path;
+ * device_ms is HIP-event time of the device passes (expand, scan, rank, pack). */
+typedef struct DanceMergeStats {
+    uint64_t nnodes, replicated_nodes, input_edges, self_loops, unique_edges, output_edges;
+    uint32_t min_degree, max_degree;
+    uint64_t buckets, long_segments;
+    uint32_t resident_shards, reserved0;
+    double read_seconds, device_ms, write_seconds, total_seconds;
+} DanceMergeStats;
+
+/* C-ABI form of diskann::merge_shards_gpu (include/gpu_merge.h; reference
+ * include/gpu_merge.h:8-12): the same files, arguments and return codes, with
+ * C strings in place of std::string. */
+int dance_merge_shards(const char *vamana_prefix, const char *vamana_suffix, const char *idmaps_prefix,
+                       const char *idmaps_suffix, uint64_t nshards, uint32_t max_degree, const char *output_vamana,
+                       const char *medoids_file);
+
+void dance_merge_get_last_stats(DanceMergeStats *stats);
+
 /* ---- stage hooks (host buffers), used by the parity tests ---- */
 
 /* Canonical squared-L2 distances d(a[i], b[i]) (reference distance family,

@@ -25,6 +25,10 @@ Parity status of each oracle function (how it is pinned; see tests/test_oracle.p
                           brute-force ground truth.
   cpu_vamana_build        baseline only (DiskANN restated; parity unpinned:
                           upstream DiskANN is not available offline).
+  merge_shards            pinned: mix64 by its closed-form inverse; the merge by
+                          an independent Python restatement (sets, sorted())
+                          on random shard sets, plus invariants; error codes
+                          on malformed inputs (tests/test_merge_oracle.py).
   query_search            pinned: exact top-k on a complete graph; equal to the
                           independently written beam_search on integer data
                           (exact distances).
@@ -117,6 +121,12 @@ def lib() -> C.CDLL:
         L.oracle_query_search.argtypes = [vp, i32, u32, u32, _u32p, _u32p, u32, _u32p, u32, vp, u32, u32, u32,
                                           vp, vp, vp, _u32p, _f32p]
         L.oracle_query_search.restype = u64
+        L.oracle_mix64.argtypes = [u64]
+        L.oracle_mix64.restype = u64
+        L.oracle_edge_hash.argtypes = [u32, u32, u64]
+        L.oracle_edge_hash.restype = u32
+        L.oracle_merge_shards.argtypes = [C.c_char_p] * 4 + [u64, u32] + [C.c_char_p] * 2 + [u64, C.POINTER(u64)]
+        L.oracle_merge_shards.restype = i32
         L.oracle_num_threads.argtypes = []
         L.oracle_num_threads.restype = i32
         _LIB = L
@@ -358,3 +368,24 @@ def query_search(data, graph, degree, starts, queries, k, L, label_offsets=None,
                                   graph.shape[1], _p(starts), starts.shape[0], queries.ctypes.data, nq, k, L, *ptrs,
                                   _p(ids), _p(dd, C.c_float))
     return ids, dd, int(n)
+
+
+MERGE_DEFAULT_SEED = 0x9E3779B97F4A7C15
+
+
+def mix64(x: int) -> int:
+    return int(lib().oracle_mix64(x))
+
+
+def edge_hash(src: int, dst: int, seed: int = MERGE_DEFAULT_SEED) -> int:
+    return int(lib().oracle_edge_hash(src, dst, seed))
+
+
+def merge_shards(vamana_prefix: str, vamana_suffix: str, idmaps_prefix: str, idmaps_suffix: str, nshards: int,
+                 max_degree: int, output_vamana: str, medoids_file: str, seed: int = MERGE_DEFAULT_SEED):
+    """CPU restatement of diskann::merge_shards_gpu; returns (rc, {self_loops, unique_edges, output_edges})."""
+    cnt = (C.c_uint64 * 3)()
+    rc = lib().oracle_merge_shards(vamana_prefix.encode(), vamana_suffix.encode(), idmaps_prefix.encode(),
+                                   idmaps_suffix.encode(), nshards, max_degree, output_vamana.encode(),
+                                   medoids_file.encode(), seed, cnt)
+    return int(rc), {"self_loops": int(cnt[0]), "unique_edges": int(cnt[1]), "output_edges": int(cnt[2])}

@@ -38,6 +38,37 @@ def test_library_exports_every_declared_symbol():
         getattr(lib, n)
 
 
+def test_merge_cpp_symbol_exported():
+    """include/gpu_merge.h declares diskann::merge_shards_gpu with std::string
+    arguments (reference include/gpu_merge.h:8-12): the C++ symbol is exported."""
+    out = subprocess.run(["nm", "-DC", "--defined-only", D.LIB_PATH], capture_output=True, text=True).stdout
+    sym = [l for l in out.splitlines() if " T " in l and "diskann::merge_shards_gpu(" in l]
+    assert len(sym) == 1, sym
+    assert sym[0].count("std::__cxx11::basic_string") == 6 and "unsigned long, unsigned int" in sym[0]
+    from dance_amd.merge import DanceMergeStats
+    assert C.sizeof(DanceMergeStats) == 112 and DanceMergeStats.total_seconds.offset == 104
+
+
+def test_merge_missing_inputs_before_device(tmp_path):
+    """merge_shards_gpu validates id maps and headers before any device call."""
+    from dance_amd import merge as M
+    pre = (str(tmp_path / "s_"), ".index", str(tmp_path / "m_"), ".bin")
+    assert M.merge_shards(*pre, 2, 8, str(tmp_path / "o"), str(tmp_path / "med")) == -2
+    M.write_idmap(str(tmp_path / "m_0.bin"), [0, 1])
+    M.write_idmap(str(tmp_path / "m_1.bin"), [1, 2])
+    assert M.merge_shards(*pre, 2, 8, str(tmp_path / "o"), str(tmp_path / "med")) == -3
+    M.write_shard(str(tmp_path / "s_0.index"), [[1], [0]], 5)
+    M.write_shard(str(tmp_path / "s_1.index"), [[1], [0]], 0)
+    assert M.merge_shards(*pre, 2, 8, str(tmp_path / "o"), str(tmp_path / "med")) == -4
+    M.write_shard(str(tmp_path / "s_0.index"), [[1], [0]], 0, frozen=1)
+    assert M.merge_shards(*pre, 2, 8, str(tmp_path / "o"), str(tmp_path / "med")) == -3
+    M.write_shard(str(tmp_path / "s_0.index"), [[1], [0]], 0)
+    raw = open(str(tmp_path / "s_1.index"), "rb").read()
+    open(str(tmp_path / "s_1.index"), "wb").write(raw[:-4])
+    assert M.merge_shards(*pre, 2, 8, str(tmp_path / "o"), str(tmp_path / "med")) == -6
+    assert not os.path.exists(str(tmp_path / "o"))
+
+
 def test_stats_struct_layout():
     assert C.sizeof(D.GPUVamanaStats) == 120
     assert D.GPUVamanaStats.distance_computations.offset == 56
