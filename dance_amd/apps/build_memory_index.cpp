@@ -1,0 +1,379 @@
+// build_memory_index --gpu_filtered: builds a label-filtered DiskANN in-memory
+// index with the GPU-FilteredVamana builder (libdance_hip.so).
+//
+// Drop-in for the DANCE-patched DiskANN app (reference:
+// integrations/dance-diskann-78256bba.patch:120-160 for the option, and
+// :20243-20530 for the GPU branch of Index::build_filtered_index). Only the
+// --gpu_filtered path is provided; without it the app exits with an error,
+// because DiskANN's CPU build is not part of this library.
+//
+//   --data_type uint8|float --dist_fn l2 --data_path <bin>
+//   --index_path_prefix PATH --label_file <txt> [--universal_label NAME]
+//   [--max_degree|-R 64] [--Lbuild|-L 100] [--FilteredLbuild 0] [--alpha 1.2]
+//   [--num_threads|-T N] [--label_type uint] [--build_PQ_bytes 0] --gpu_filtered
+//
+// Steps:
+//   1. labels: one row per point, comma-separated names; names are numbered
+//      1, 2, ... in order of first appearance, the universal label is 0
+//      (DiskANN convert_labels_string_to_int, upstream); rows become sorted
+//      unique id lists (the canonical CSR, patch:20269-20286);
+//   2. entry points: global start = the point nearest to the centroid of all
+//      points; label start = the carrier of the label nearest to the centroid
+//      of its carriers (squared L2 in fp64, ties to the lower id);
+//   3. gpu_vamana_filtered_build_{uint8,float} with R = max(max_degree, 64),
+//      L = Lbuild, filtered_L = FilteredLbuild or Lbuild, C = 750 (DiskANN's
+//      default max occlusion size), STEPS = min(64, L) or
+//      DISKANN_GPU_FILTERED_STEPS (patch:20372-20398);
+//   4. install: per row drop invalid / self / repeated ids, an empty row of a
+//      multi-point index gets (i + 1) mod N (patch:20506-20521);
+//   5. save: <prefix> (graph: u64 file bytes, u32 max degree, u32 start,
+//      u64 frozen 0, rows), <prefix>.data, <prefix>_labels.txt,
+//      <prefix>_label_formatted.txt, <prefix>_labels_map.txt,
+//      <prefix>_labels_to_medoids.txt and, with a universal label,
+//      <prefix>_universal_label.txt.
+// max_degree < 64 needs the reference's GPU publish prune from the internal
+// degree 64 down to max_degree, which this library does not provide: the
+// app then exits with an error. Exit status: 0 ok, 255 (-1) on any error.
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <iostream>
+#include <limits>
+#include <sstream>
+#include <stdexcept>
+#include <string>
+#include <type_traits>
+#include <unordered_map>
+#include <vector>
+
+#include "gpu_vamana_filtered.h"
+
+namespace {
+
+constexpr uint32_t kInvalid = 0xFFFFFFFFu;
+constexpr uint32_t kMinInternalDegree = 64;  // patch:20367-20370
+constexpr uint32_t kDefaultMaxC = 750;       // DiskANN IndexWriteParameters default
+
+double now_sec() {
+  return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+struct Options {
+  std::string data_type, dist_fn = "l2", data_path, prefix, label_file, universal_label, label_type = "uint";
+  uint32_t R = 64, L = 100, Lf = 0, threads = 0, pq_bytes = 0;
+  float alpha = 1.2f;
+  bool gpu_filtered = false, use_opq = false;
+};
+
+uint32_t to_u32(const std::string& v, const std::string& k) {
+  if (v.empty() || v.find_first_not_of("0123456789") != std::string::npos)
+    throw std::runtime_error(k + " must be an unsigned integer");
+  const unsigned long long x = std::stoull(v);
+  if (x > std::numeric_limits<uint32_t>::max()) throw std::runtime_error(k + " is out of range");
+  return (uint32_t)x;
+}
+
+Options parse(int argc, char** argv) {
+  Options o;
+  for (int i = 1; i < argc; ++i) {
+    const std::string k = argv[i];
+    if (k == "--gpu_filtered") {
+      o.gpu_filtered = true;
+      continue;
+    }
+    if (k == "--use_opq") {
+      o.use_opq = true;
+      continue;
+    }
+    if (i + 1 >= argc) throw std::runtime_error("missing value for " + k);
+    const std::string v = argv[++i];
+    if (k == "--data_type") o.data_type = v;
+    else if (k == "--dist_fn") o.dist_fn = v;
+    else if (k == "--data_path") o.data_path = v;
+    else if (k == "--index_path_prefix") o.prefix = v;
+    else if (k == "--label_file") o.label_file = v;
+    else if (k == "--universal_label") o.universal_label = v;
+    else if (k == "--label_type") o.label_type = v;
+    else if (k == "--max_degree" || k == "-R") o.R = to_u32(v, k);
+    else if (k == "--Lbuild" || k == "-L") o.L = to_u32(v, k);
+    else if (k == "--FilteredLbuild" || k == "-Lf") o.Lf = to_u32(v, k);
+    else if (k == "--num_threads" || k == "-T") o.threads = to_u32(v, k);
+    else if (k == "--build_PQ_bytes") o.pq_bytes = to_u32(v, k);
+    else if (k == "--alpha") {
+      char* end = nullptr;
+      o.alpha = std::strtof(v.c_str(), &end);
+      if (!end || *end || !(o.alpha > 0.0f)) throw std::runtime_error("--alpha must be a positive number");
+    } else
+      throw std::runtime_error("unknown argument: " + k);
+  }
+  if (o.data_type.empty() || o.data_path.empty() || o.prefix.empty())
+    throw std::runtime_error("--data_type, --data_path and --index_path_prefix are required");
+  if (!o.gpu_filtered)
+    throw std::runtime_error("only the --gpu_filtered build is provided (DiskANN's CPU build is not part of this library)");
+  if (o.data_type != "float" && o.data_type != "uint8")
+    throw std::runtime_error("--gpu_filtered supports only float and uint8 data");
+  if (o.label_file.empty()) throw std::runtime_error("--gpu_filtered requires --label_file");
+  if (o.dist_fn != "l2") throw std::runtime_error("--gpu_filtered builds with --dist_fn l2 only");
+  if (o.label_type != "uint") throw std::runtime_error("--gpu_filtered supports --label_type uint only");
+  if (o.pq_bytes != 0 || o.use_opq)
+    throw std::runtime_error("[GPU filtered] first version supports only static memory indices without tags or PQ build");
+  if (o.R == 0 || o.L == 0) throw std::runtime_error("--max_degree and --Lbuild must be positive");
+  if (o.R < kMinInternalDegree)
+    throw std::runtime_error("--max_degree below 64 needs the GPU publish prune from the internal degree 64, "
+                             "which this build does not provide");
+  return o;
+}
+
+template <typename T>
+std::vector<T> read_matrix(const std::string& path, uint32_t& n, uint32_t& dim) {
+  std::ifstream in(path, std::ios::binary);
+  if (!in) throw std::runtime_error("failed to open " + path);
+  uint32_t hdr[2] = {0, 0};
+  in.read(reinterpret_cast<char*>(hdr), 8);
+  if (!in) throw std::runtime_error("failed to read the matrix header of " + path);
+  n = hdr[0];
+  dim = hdr[1];
+  in.seekg(0, std::ios::end);
+  const uint64_t bytes = (uint64_t)in.tellg();
+  if (n == 0 || dim == 0 || bytes != 8 + (uint64_t)n * dim * sizeof(T))
+    throw std::runtime_error("matrix header of " + path + " does not match its size");
+  std::vector<T> v((size_t)n * dim);
+  in.seekg(8);
+  in.read(reinterpret_cast<char*>(v.data()), (std::streamsize)(v.size() * sizeof(T)));
+  if (!in) throw std::runtime_error("failed to read " + path);
+  return v;
+}
+
+struct Labels {
+  std::vector<std::string> names;             // id -> name (id 0 = universal when set)
+  std::vector<std::vector<uint32_t>> tokens;  // per row, ids in file order (with repeats)
+  std::vector<uint32_t> offsets, ids;         // canonical CSR: sorted unique per row
+  uint32_t universal = kInvalid;
+};
+
+Labels read_labels(const Options& o, uint32_t n) {
+  std::ifstream in(o.label_file);
+  if (!in) throw std::runtime_error("failed to open label file: " + o.label_file);
+  Labels lb;
+  std::unordered_map<std::string, uint32_t> id_of;
+  if (!o.universal_label.empty()) {
+    id_of.emplace(o.universal_label, 0u);
+    lb.names.push_back(o.universal_label);
+    lb.universal = 0;
+  } else {
+    lb.names.push_back("");  // id 0 unused without a universal label
+  }
+  std::string line;
+  while (std::getline(in, line)) {
+    line.erase(std::remove(line.begin(), line.end(), '\r'), line.end());
+    if (line.empty()) throw std::runtime_error("label row " + std::to_string(lb.tokens.size()) + " is empty");
+    std::vector<uint32_t> row;
+    std::stringstream ss(line);
+    std::string tok;
+    while (std::getline(ss, tok, ',')) {
+      if (tok.empty()) throw std::runtime_error("empty label token in row " + std::to_string(lb.tokens.size()));
+      auto it = id_of.find(tok);
+      if (it == id_of.end()) {
+        it = id_of.emplace(tok, (uint32_t)lb.names.size()).first;
+        lb.names.push_back(tok);
+      }
+      row.push_back(it->second);
+    }
+    if (line.back() == ',') throw std::runtime_error("empty label token in row " + std::to_string(lb.tokens.size()));
+    lb.tokens.push_back(std::move(row));
+  }
+  if (lb.tokens.size() != n)
+    throw std::runtime_error("label file has " + std::to_string(lb.tokens.size()) + " rows for " +
+                             std::to_string(n) + " points");
+  lb.offsets.assign(n + 1, 0);
+  for (uint32_t i = 0; i < n; ++i) {
+    std::vector<uint32_t> r = lb.tokens[i];
+    std::sort(r.begin(), r.end());
+    r.erase(std::unique(r.begin(), r.end()), r.end());
+    lb.offsets[i] = (uint32_t)lb.ids.size();
+    lb.ids.insert(lb.ids.end(), r.begin(), r.end());
+  }
+  lb.offsets[n] = (uint32_t)lb.ids.size();
+  return lb;
+}
+
+// Index of the row nearest (fp64 squared L2, ties to the lower id) to the
+// centroid of the listed rows.
+template <typename T>
+uint32_t nearest_to_centroid(const std::vector<T>& x, uint32_t dim, const uint32_t* rows, size_t count,
+                             std::vector<double>& cent) {
+  cent.assign(dim, 0.0);
+  for (size_t i = 0; i < count; ++i) {
+    const T* v = x.data() + (size_t)rows[i] * dim;
+    for (uint32_t d = 0; d < dim; ++d) cent[d] += (double)v[d];
+  }
+  for (uint32_t d = 0; d < dim; ++d) cent[d] /= (double)count;
+  uint32_t best = kInvalid;
+  double best_d = std::numeric_limits<double>::infinity();
+  for (size_t i = 0; i < count; ++i) {
+    const T* v = x.data() + (size_t)rows[i] * dim;
+    double s = 0.0;
+    for (uint32_t d = 0; d < dim; ++d) {
+      const double t = (double)v[d] - cent[d];
+      s += t * t;
+    }
+    if (s < best_d || (s == best_d && rows[i] < best)) {
+      best_d = s;
+      best = rows[i];
+    }
+  }
+  return best;
+}
+
+template <typename T>
+void entry_points(const std::vector<T>& x, uint32_t n, uint32_t dim, const Labels& lb, uint32_t& global_start,
+                  std::vector<uint32_t>& label_start) {
+  std::vector<uint32_t> all(n);
+  for (uint32_t i = 0; i < n; ++i) all[i] = i;
+  std::vector<double> cent;
+  global_start = nearest_to_centroid(x, dim, all.data(), n, cent);
+  const uint32_t num_labels = (uint32_t)lb.names.size();
+  std::vector<uint32_t> loff(num_labels + 1, 0), pts(lb.ids.size());
+  for (uint32_t l : lb.ids) ++loff[l + 1];
+  for (uint32_t l = 0; l < num_labels; ++l) loff[l + 1] += loff[l];
+  std::vector<uint32_t> cur(loff.begin(), loff.end() - 1);
+  for (uint32_t i = 0; i < n; ++i)
+    for (uint32_t p = lb.offsets[i]; p < lb.offsets[i + 1]; ++p) pts[cur[lb.ids[p]]++] = i;
+  label_start.assign(num_labels, kInvalid);
+#pragma omp parallel for schedule(dynamic, 16)
+  for (uint32_t l = 0; l < num_labels; ++l) {
+    const size_t c = loff[l + 1] - loff[l];
+    if (c == 0) continue;
+    std::vector<double> cl;
+    label_start[l] = nearest_to_centroid(x, dim, pts.data() + loff[l], c, cl);
+  }
+}
+
+void write_text(const std::string& path, const std::string& body) {
+  std::ofstream f(path);
+  if (!f) throw std::runtime_error("failed to write " + path);
+  f << body;
+  if (!f) throw std::runtime_error("failed to write " + path);
+}
+
+template <typename T>
+int run(const Options& o) {
+  const double t0 = now_sec();
+  uint32_t n = 0, dim = 0;
+  std::vector<T> x = read_matrix<T>(o.data_path, n, dim);
+  Labels lb = read_labels(o, n);
+  uint32_t global_start = 0;
+  std::vector<uint32_t> starts;
+  entry_points(x, n, dim, lb, global_start, starts);
+  const double t_prep = now_sec();
+
+  const uint32_t R = o.R, L = o.L, Lf = o.Lf == 0 ? o.L : o.Lf;
+  const char* steps_env = std::getenv("DISKANN_GPU_FILTERED_STEPS");
+  const uint32_t steps = steps_env ? (uint32_t)std::max(1, std::atoi(steps_env)) : std::min<uint32_t>(64, L);
+  std::cout << "[GPU filtered] requested_R=" << R << " internal_R=" << R << " publish_backend=direct" << std::endl;
+  std::cout << "[GPU filtered] N=" << n << " dim=" << dim << " labels=" << lb.names.size() - (lb.universal == 0 ? 1 : 0)
+            << " label_slots=" << lb.ids.size() << " global_start=" << global_start << " L=" << L
+            << " filtered_L=" << Lf << " C=" << kDefaultMaxC << " steps=" << steps << " alpha=" << o.alpha
+            << std::endl;
+  std::vector<uint32_t> graph((size_t)n * R, kInvalid), degree(n, 0);
+  int rc;
+  if (std::is_same<T, uint8_t>::value)
+    rc = gpu_vamana_filtered_build_uint8(reinterpret_cast<const uint8_t*>(x.data()), n, dim, R, L, Lf, kDefaultMaxC,
+                                         steps, o.alpha, lb.offsets.data(), lb.ids.data(), (uint32_t)lb.ids.size(),
+                                         starts.data(), (uint32_t)starts.size(), lb.universal, global_start, nullptr,
+                                         nullptr, 0, graph.data(), degree.data());
+  else
+    rc = gpu_vamana_filtered_build_float(reinterpret_cast<const float*>(x.data()), n, dim, R, L, Lf, kDefaultMaxC,
+                                         steps, o.alpha, lb.offsets.data(), lb.ids.data(), (uint32_t)lb.ids.size(),
+                                         starts.data(), (uint32_t)starts.size(), lb.universal, global_start, nullptr,
+                                         nullptr, 0, graph.data(), degree.data());
+  if (rc != 0) throw std::runtime_error("[GPU filtered] gpu_vamana_filtered_build failed with code " + std::to_string(rc));
+  GPUFilteredVamanaStats st;
+  gpu_vamana_filtered_get_last_stats(&st);
+  std::cout << "[GPU filtered] stats semantic_complete=" << st.semantic_complete
+            << " gpu_build_seconds=" << st.gpu_build_seconds << " peak_gpu_mem_gb=" << st.peak_gpu_mem_gb
+            << " avg_common_label_out_degree=" << st.avg_common_label_out_degree
+            << " label_reject_count=" << st.label_reject_count
+            << " invalid_neighbor_count=" << st.invalid_neighbor_count
+            << " self_loop_count=" << st.self_loop_count << std::endl;
+  const double t_build = now_sec();
+
+  // Install (patch:20506-20521) and save.
+  std::string body;
+  body.reserve((size_t)n * 4 * (R + 1));
+  uint32_t max_deg = 0;
+  uint64_t edges = 0;
+  std::vector<uint32_t> row;
+  for (uint32_t i = 0; i < n; ++i) {
+    row.clear();
+    for (uint32_t j = 0; j < degree[i] && j < R; ++j) {
+      const uint32_t nb = graph[(size_t)i * R + j];
+      if (nb != kInvalid && nb < n && nb != i && std::find(row.begin(), row.end(), nb) == row.end())
+        row.push_back(nb);
+    }
+    if (row.empty() && n > 1) row.push_back((i + 1) % n);
+    const uint32_t k = (uint32_t)row.size();
+    body.append(reinterpret_cast<const char*>(&k), 4);
+    body.append(reinterpret_cast<const char*>(row.data()), 4ull * k);
+    max_deg = std::max(max_deg, k);
+    edges += k;
+  }
+  {
+    std::ofstream g(o.prefix, std::ios::binary);
+    if (!g) throw std::runtime_error("failed to write " + o.prefix);
+    const uint64_t size = 24 + body.size(), frozen = 0;
+    g.write(reinterpret_cast<const char*>(&size), 8);
+    g.write(reinterpret_cast<const char*>(&max_deg), 4);
+    g.write(reinterpret_cast<const char*>(&global_start), 4);
+    g.write(reinterpret_cast<const char*>(&frozen), 8);
+    g.write(body.data(), (std::streamsize)body.size());
+    if (!g) throw std::runtime_error("failed to write " + o.prefix);
+  }
+  {
+    std::ofstream d(o.prefix + ".data", std::ios::binary);
+    const uint32_t hdr[2] = {n, dim};
+    d.write(reinterpret_cast<const char*>(hdr), 8);
+    d.write(reinterpret_cast<const char*>(x.data()), (std::streamsize)(x.size() * sizeof(T)));
+    if (!d) throw std::runtime_error("failed to write " + o.prefix + ".data");
+  }
+  std::ostringstream labels, formatted, map, medoids;
+  for (uint32_t i = 0; i < n; ++i) {
+    for (uint32_t p = lb.offsets[i]; p < lb.offsets[i + 1]; ++p) labels << (p > lb.offsets[i] ? "," : "") << lb.ids[p];
+    labels << "\n";
+    for (size_t j = 0; j < lb.tokens[i].size(); ++j) formatted << (j ? "," : "") << lb.tokens[i][j];
+    formatted << "\n";
+  }
+  for (uint32_t l = lb.universal == 0 ? 0 : 1; l < lb.names.size(); ++l) map << lb.names[l] << "\t" << l << "\n";
+  for (uint32_t l = 0; l < starts.size(); ++l)
+    if (starts[l] != kInvalid) medoids << l << ", " << starts[l] << "\n";
+  write_text(o.prefix + "_labels.txt", labels.str());
+  write_text(o.prefix + "_label_formatted.txt", formatted.str());
+  write_text(o.prefix + "_labels_map.txt", map.str());
+  write_text(o.prefix + "_labels_to_medoids.txt", medoids.str());
+  if (lb.universal == 0) write_text(o.prefix + "_universal_label.txt", "0\n");
+  const double t_end = now_sec();
+  std::cout << "[GPU filtered] graph installed: edges=" << edges << " max_degree=" << max_deg
+            << " prepare_seconds=" << t_prep - t0 << " build_seconds=" << t_build - t_prep
+            << " save_seconds=" << t_end - t_build << " total_seconds=" << t_end - t0 << std::endl;
+  return 0;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  try {
+    const Options o = parse(argc, argv);
+    std::cout << "Starting index build with R: " << o.R << "  Lbuild: " << o.L << "  alpha: " << o.alpha
+              << "  #threads: " << o.threads << std::endl;
+    return o.data_type == "uint8" ? run<uint8_t>(o) : run<float>(o);
+  } catch (const std::exception& e) {
+    std::cerr << "Index build failed: " << e.what() << std::endl;
+    return -1;
+  }
+}

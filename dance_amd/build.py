@@ -29,7 +29,7 @@ HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-pthread", "-Wall", "-Wextra", "-Wn
 
 HIP_SOURCES = ["vnew2_build.hip", "filtered_build.hip", "query_search.hip", "merge_shards.hip"]
 HOST_SOURCES = ["synth.cpp"]
-APP_SOURCES = ["gpu_vamana_memory_index.cpp", "gpu_stitched_vamana_index.cpp"]
+APP_SOURCES = ["gpu_vamana_memory_index.cpp", "gpu_stitched_vamana_index.cpp", "build_memory_index.cpp"]
 
 
 def _run(cmd: list[str]) -> None:
@@ -60,7 +60,7 @@ def build(jobs: int | None = None) -> str:
         path = os.path.join(APPS, src)
         if os.path.exists(path):
             exe = os.path.join(HERE, os.path.splitext(src)[0])
-            _run(["g++", *HOST_FLAGS, f"-I{os.path.join(ROOT, 'include')}", path, "-o", exe,
+            _run(["g++", *HOST_FLAGS, "-fopenmp", f"-I{os.path.join(ROOT, 'include')}", path, "-o", exe,
                   f"-L{HERE}", "-ldance_hip", f"-Wl,-rpath,{HERE}", "-Wl,-rpath,$ORIGIN",
                   "-L/opt/rocm/lib", "-lamdhip64"])
     return LIB

@@ -1,0 +1,158 @@
+"""build_memory_index --gpu_filtered (reference: the DANCE-patched DiskANN app,
+integrations/dance-diskann-78256bba.patch:120-160, GPU branch :20243-20530).
+
+CPU: option and label-file errors, all decided before any device call.
+GPU: the written graph equals the CPU oracle's filtered build fed the same
+label CSR, entry points and parameters, after the reference's install rule;
+label ids, entry points and every sidecar are checked against independent
+Python restatements."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import dance_amd as D
+from dance_amd import filtered as F
+from dance_amd import formats
+from oracle import oracle as O
+
+APP = os.path.join(os.path.dirname(D.__file__), "build_memory_index")
+INV = 0xFFFFFFFF
+
+
+def run_app(*args, env=None):
+    return subprocess.run([APP, *args], capture_output=True, text=True, timeout=600, env=env)
+
+
+def make_case(tmp_path, kind="uint8", n=600, dim=16, vocab=12, universal_every=0, seed=3):
+    rng = np.random.default_rng(seed)
+    if kind == "uint8":
+        x = rng.integers(0, 256, size=(n, dim), dtype=np.uint8)
+    else:
+        x = rng.standard_normal((n, dim)).astype(np.float32)
+    rows = []
+    for i in range(n):
+        k = int(rng.integers(1, 4))
+        toks = [f"tag{int(t)}" for t in rng.integers(0, vocab, size=k)]
+        if universal_every and i % universal_every == 0:
+            toks.append("ANY")
+        rows.append(toks)
+    dp = str(tmp_path / "base.bin")
+    formats.write_bin(dp, x)
+    lp = str(tmp_path / "labels.txt")
+    with open(lp, "w") as f:
+        f.write("".join(",".join(r) + "\n" for r in rows))
+    return x, rows, dp, lp
+
+
+def base_args(dp, lp, prefix, kind="uint8"):
+    return ["--data_type", kind, "--dist_fn", "l2", "--data_path", dp, "--index_path_prefix", prefix,
+            "--label_file", lp, "--max_degree", "64", "--Lbuild", "100", "--alpha", "1.2", "--gpu_filtered"]
+
+
+@pytest.mark.parametrize("edit,msg", [
+    (lambda a: [x for x in a if x != "--gpu_filtered"], "only the --gpu_filtered build"),
+    (lambda a: a[:1] + ["int8"] + a[2:], "supports only float and uint8"),
+    (lambda a: a[:3] + ["mips"] + a[4:], "--dist_fn l2 only"),
+    (lambda a: a + ["--max_degree", "32"], "below 64"),
+    (lambda a: a + ["--build_PQ_bytes", "8"], "without tags or PQ"),
+    (lambda a: a + ["--bogus", "1"], "unknown argument"),
+])
+def test_option_errors(tmp_path, edit, msg):
+    _, _, dp, lp = make_case(tmp_path, n=20)
+    r = run_app(*edit(base_args(dp, lp, str(tmp_path / "idx"))))
+    assert r.returncode == 255 and msg in r.stderr, r.stderr
+
+
+@pytest.mark.parametrize("content,msg", [
+    ("a\n" * 19, "19 rows for 20 points"),
+    ("a\n" * 10 + "\n" + "a\n" * 9, "is empty"),
+    ("a\n" * 10 + "a,,b\n" + "a\n" * 9, "empty label token"),
+    ("a\n" * 10 + "a,\n" + "a\n" * 9, "empty label token"),
+])
+def test_label_file_errors(tmp_path, content, msg):
+    _, _, dp, lp = make_case(tmp_path, n=20)
+    with open(lp, "w") as f:
+        f.write(content)
+    r = run_app(*base_args(dp, lp, str(tmp_path / "idx")))
+    assert r.returncode == 255 and msg in r.stderr, r.stderr
+    assert not os.path.exists(str(tmp_path / "idx"))
+
+
+def expected_ids(rows, universal=None):
+    """Label numbering: universal 0, others 1.. by first appearance."""
+    ids = {} if universal is None else {universal: 0}
+    nxt = 1
+    per_row = []
+    for r in rows:
+        out = []
+        for t in r:
+            if t not in ids:
+                ids[t] = nxt
+                nxt += 1
+            out.append(ids[t])
+        per_row.append(out)
+    return ids, per_row
+
+
+def centroid_start(x, carriers):
+    v = x[carriers].astype(np.float64)
+    d = ((v - v.mean(0)) ** 2).sum(1)
+    return int(carriers[int(np.argmin(d))])  # carriers ascending: argmin takes the lower id on ties
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind,universal_every", [("uint8", 0), ("float", 0), ("uint8", 7)])
+def test_app_matches_oracle(tmp_path, kind, universal_every):
+    x, rows, dp, lp = make_case(tmp_path, kind=kind, universal_every=universal_every)
+    prefix = str(tmp_path / "idx")
+    args = base_args(dp, lp, prefix, kind) + (["--universal_label", "ANY"] if universal_every else [])
+    r = run_app(*args)
+    assert r.returncode == 0, r.stdout + r.stderr
+    n = x.shape[0]
+    ids, per_row = expected_ids(rows, "ANY" if universal_every else None)
+    # sidecars
+    with open(prefix + "_labels_map.txt") as f:
+        got_map = dict((a, int(b)) for a, b in (l.rstrip("\n").split("\t") for l in f))
+    assert got_map == ids
+    with open(prefix + "_label_formatted.txt") as f:
+        assert [list(map(int, l.split(","))) for l in f.read().splitlines()] == per_row
+    canon = [sorted(set(r)) for r in per_row]
+    with open(prefix + "_labels.txt") as f:
+        assert [list(map(int, l.split(","))) for l in f.read().splitlines()] == canon
+    assert os.path.exists(prefix + "_universal_label.txt") == bool(universal_every)
+    data = formats.read_bin(prefix + ".data", np.uint8 if kind == "uint8" else np.float32)
+    assert np.array_equal(data, x)
+    # entry points
+    num_labels = max(ids.values()) + 1
+    starts = np.full(num_labels, INV, np.uint32)
+    with open(prefix + "_labels_to_medoids.txt") as f:
+        for l in f:
+            a, b = l.split(",")
+            starts[int(a)] = int(b)
+    for lab in range(num_labels):
+        carriers = np.array([i for i in range(n) if lab in canon[i]], np.int64)
+        assert (starts[lab] == INV) == (carriers.size == 0)
+        if carriers.size:
+            assert starts[lab] == centroid_start(x, carriers)
+    adj, max_deg, start, frozen = formats.read_graph(prefix)
+    assert start == centroid_start(x, np.arange(n)) and frozen == 0
+    # graph vs the oracle's build with the same inputs, then the install rule
+    ls = F.canonical_labels(canon, num_labels)
+    rc, g, deg, _ = O.filtered_build(x, ls.offsets, ls.labels, starts, num_labels, R=64, L=100, filtered_L=100,
+                                     C_=750, STEPS=64, alpha=1.2, universal=0 if universal_every else INV,
+                                     global_start=start)
+    assert rc == 0
+    want = []
+    for i in range(n):
+        row = []
+        for j in range(min(int(deg[i]), 64)):
+            v = int(g[i, j])
+            if v != INV and v < n and v != i and v not in row:
+                row.append(v)
+        if not row and n > 1:
+            row.append((i + 1) % n)
+        want.append(row)
+    assert [list(map(int, a)) for a in adj] == want
+    assert max_deg == max(len(w) for w in want)
