@@ -140,10 +140,39 @@ EXPORTS = [
     "gpu_vamana_filtered_build_uint8", "gpu_vamana_filtered_build_float", "gpu_vamana_filtered_get_last_stats",
     "dance_filtered_build", "dance_filtered_build_resident", "dance_get_last_filtered_profile",
     "dance_search", "dance_search_resident", "dance_get_last_search_stats",
-    "dance_merge_shards", "dance_merge_get_last_stats",
+    "dance_merge_shards", "dance_merge_get_last_stats", "dance_struct_sizes",
 ]
 
+class DanceMergeStats(C.Structure):
+    _fields_ = [
+        ("nnodes", C.c_uint64), ("replicated_nodes", C.c_uint64), ("input_edges", C.c_uint64),
+        ("self_loops", C.c_uint64), ("unique_edges", C.c_uint64), ("output_edges", C.c_uint64),
+        ("min_degree", C.c_uint32), ("max_degree", C.c_uint32),
+        ("buckets", C.c_uint64), ("long_segments", C.c_uint64),
+        ("resident_shards", C.c_uint32), ("reserved0", C.c_uint32),
+        ("read_seconds", C.c_double), ("device_ms", C.c_double), ("write_seconds", C.c_double),
+        ("total_seconds", C.c_double),
+    ]
+
+
+
 _LIB = None
+
+
+def _check_struct_sizes(L) -> None:
+    """The library writes these structs into memory this module allocates:
+    a layout mismatch (a library built from other headers) must fail here,
+    before it can overrun a buffer."""
+    mine = [GPUVamanaStats, DanceKernelProfile, GPUFilteredVamanaStats, DanceFilteredProfile, DanceSearchStats,
+            DanceMergeStats]
+    L.dance_struct_sizes.argtypes = [C.POINTER(C.c_uint64), C.c_uint32]
+    L.dance_struct_sizes.restype = C.c_uint32
+    got = (C.c_uint64 * len(mine))()
+    L.dance_struct_sizes(got, len(mine))
+    for cls, size in zip(mine, got):
+        if C.sizeof(cls) != size:
+            raise RuntimeError(f"{LIB_PATH}: {cls.__name__} is {size} bytes in the library and {C.sizeof(cls)} "
+                               "here; rebuild the library (python -m dance_amd.build)")
 
 
 def lib() -> C.CDLL:
@@ -154,6 +183,7 @@ def lib() -> C.CDLL:
             raise RuntimeError(f"{LIB_PATH} is missing: run `python -m dance_amd.build` "
                                "(or __graft_entry__.build()) first")
         L = C.CDLL(LIB_PATH)
+        _check_struct_sizes(L)
         u32, f32, vp, i32 = C.c_uint32, C.c_float, C.c_void_p, C.c_int
         build_args = [vp, u32, u32, u32, u32, u32, u32, _u32p, _u32p]
         for name in ("gpu_vamana_build", "gpu_vamana_build_float", "gpu_vamana_vnew2_build",

@@ -145,6 +145,18 @@ __device__ __forceinline__ bool q_proves_reject(const QSelf& me, const uint4& co
   return active && q >= w * w * (1.0f + kQSlack);
 }
 
+// Threshold of the prune's bound for a candidate at stored distance sd: a
+// pair distance d >= T gives fl(alpha * d) >= fl(alpha * T) > sd, so the
+// candidate survives. Returns sqrt((T + 1e-30)(1 + kappa2)) rounded up, the
+// per-candidate part of q_threshold; +inf (never skipped) for sd < 1e-30 or
+// non-finite sd, where the relative slack would not cover rounding.
+__device__ __forceinline__ float prune_bound_root(const QBoundSet& qb, float sd, float alpha) {
+  if (!(sd >= 1e-30f) || !(sd <= FLT_MAX)) return __builtin_inff();
+  const float T = sd / alpha * (1.0f + 0x1p-20f);
+  const float t = (T + 1e-30f) * (1.0f + qb.kappa2);
+  return __builtin_sqrtf(t) * (1.0f + kQSlack);
+}
+
 // Bits 0, 8, ..., 56 of a ballot -> bits 0..7.
 __device__ __forceinline__ uint32_t octet_bits(uint64_t m) {
   return (uint32_t)(((m & 0x0101010101010101ull) * 0x0102040810204080ull) >> 56);

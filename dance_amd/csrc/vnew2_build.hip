@@ -42,6 +42,7 @@
 
 #include "../../include/dance_hip.h"
 #include "../../include/gpu_vamana_builder.h"
+#include "../../include/gpu_vamana_filtered.h"
 #include "host_common.h"
 #include "vnew2_kernels.h"
 
@@ -195,10 +196,22 @@ static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t ste
   }
   return with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
     constexpr int DT = decltype(dt)::value, CPL = decltype(c)::value;
+    // Bounded variants exist only where build_qbound can produce code rows.
+    constexpr bool kHasQB = DT != DANCE_U8 && CPL <= 4;
+    if constexpr (kHasQB) {
+      if (qb.rows) {
+        if (L <= 128)
+          hipLaunchKernelGGL((k_search<DT, CPL, 2, true>), dim3(xcd_grid(g.N)), dim3(kBlock), lds, s, a, Cp);
+        else
+          hipLaunchKernelGGL((k_search<DT, CPL, 4, true>), dim3(xcd_grid(g.N)), dim3(kBlock), lds, s, a, Cp);
+        DHIP(hipGetLastError());
+        return 0;
+      }
+    }
     if (L <= 128)
-      hipLaunchKernelGGL((k_search<DT, CPL, 2>), dim3(xcd_grid(g.N)), dim3(kBlock), lds, s, a, Cp);
+      hipLaunchKernelGGL((k_search<DT, CPL, 2, false>), dim3(xcd_grid(g.N)), dim3(kBlock), lds, s, a, Cp);
     else
-      hipLaunchKernelGGL((k_search<DT, CPL, 4>), dim3(xcd_grid(g.N)), dim3(kBlock), lds, s, a, Cp);
+      hipLaunchKernelGGL((k_search<DT, CPL, 4, false>), dim3(xcd_grid(g.N)), dim3(kBlock), lds, s, a, Cp);
     DHIP(hipGetLastError());
     return 0;
   });
@@ -729,6 +742,13 @@ int gpu_vamana_vnew2_build_device_float(const float* h_data, uint32_t N, uint32_
   int r = build_host<float>(h_data, DANCE_F32, N, dim, R, L, C, STEPS, nullptr, nullptr, &dd, d_graph, d_degree);
   if (r == 0) *d_data = static_cast<float*>(dd);
   return r;
+}
+
+uint32_t dance_struct_sizes(uint64_t* sizes, uint32_t count) {
+  const uint64_t all[6] = {sizeof(GPUVamanaStats),   sizeof(DanceKernelProfile), sizeof(GPUFilteredVamanaStats),
+                           sizeof(DanceFilteredProfile), sizeof(DanceSearchStats), sizeof(DanceMergeStats)};
+  for (uint32_t i = 0; sizes && i < count && i < 6; ++i) sizes[i] = all[i];
+  return 6;
 }
 
 uint32_t gpu_vamana_vnew2_get_last_medoid(void) { return g_last_medoid; }

@@ -33,7 +33,10 @@ __device__ __forceinline__ uint64_t dclock() {
 #endif
 }
 
-constexpr uint32_t kVisBits = 10;
+#ifndef DANCE_VIS_BITS
+#define DANCE_VIS_BITS 10
+#endif
+constexpr uint32_t kVisBits = DANCE_VIS_BITS;
 constexpr uint32_t kVis = 1u << kVisBits;  // visited cache slots per wave
 constexpr uint32_t kWavesPerBlock = 4;
 constexpr uint32_t kBlock = 64 * kWavesPerBlock;
@@ -294,7 +297,10 @@ struct SearchArgs {
 // dists), candidate batch (ids, dists), occlusion list, work-row order.
 __host__ __device__ constexpr uint32_t search_lds_words(uint32_t Cp) { return kVis + 4u * Cp + 128u; }
 
-template <int DT, int CPL, int PS>
+// QB compiles the quantized-bound path in (the launcher picks QB = true only
+// when the bound is on for the launch); QB = false kernels carry no bound code
+// and keep their register budget for the exact path.
+template <int DT, int CPL, int PS, bool QB>
 struct SearchWave {
   const SearchArgs& a;
   uint32_t node, lane, grp, sub, Cp;
@@ -371,7 +377,7 @@ struct SearchWave {
     wave_sync();
     const uint64_t t0 = dclock();
     const bool full = P.size >= P.L && P.max_pos >= 0;
-    const uint32_t nx = (full && a.qb.rows) ? bound_filter(n) : n;
+    const uint32_t nx = (QB && full && a.qb.rows) ? bound_filter(n) : n;
     if (nx) batch_dist<DT, CPL>(a.rs, av, lst, lsd, nx, grp, sub);
     n_search += nx;
     const uint64_t t1 = dclock();
@@ -569,7 +575,7 @@ struct SearchWave {
     const uint32_t N = g.N, R = g.R, C = g.C;
     for (uint32_t i = lane; i < kVis; i += 64) vis[i] = DANCE_INV;
     load_row<CPL>(a.rs, node, true, sub, av);
-    if (a.qb.rows) q_load_self(a.qb, node, qme);
+    if (QB && a.qb.rows) q_load_self(a.qb, node, qme);
     // Work row := current row with its stored distances (vnew2.cu:1186-1212).
     const uint32_t deg_self = min(g.deg_cur[node], R);
     const size_t cb = (size_t)node * R, wb = (size_t)node * C;
@@ -650,7 +656,7 @@ struct SearchWave {
         atomicAdd(&ctr_stripe(a.ctr)->vis_skips, (unsigned long long)n_skip);
         atomicAdd(&ctr_stripe(a.ctr)->insert_mut, (unsigned long long)n_mut);
         atomicAdd(&ctr_stripe(a.ctr)->insert_try, (unsigned long long)n_try);
-        if (a.qb.rows) {
+        if (QB && a.qb.rows) {
           atomicAdd(&ctr_stripe(a.ctr)->bound_checks, (unsigned long long)n_bchk);
           atomicAdd(&ctr_stripe(a.ctr)->bound_skips, (unsigned long long)n_bskip);
         }
@@ -667,21 +673,29 @@ struct SearchWave {
   }
 };
 
-// Waves per SIMD the register allocator must leave room for: 5 for the
-// narrow-row, L <= 128 variants (the common case; the allocator would
-// otherwise settle at 4 by a few registers), no constraint elsewhere.
-template <int CPL, int PS>
-constexpr int kSearchMinWaves = (CPL <= 3 && PS == 2) ? 5 : 1;
+// Waves per SIMD the register allocator must leave room for, for the
+// narrow-row, L <= 128 variants (the common case): DANCE_SEARCH_WAVES_QB
+// (default 5) with the bound compiled in (the allocator would otherwise
+// settle at 4 by a few registers), and DANCE_SEARCH_WAVES (default 6, the
+// LDS limit of 4-wave blocks) without it. No constraint elsewhere.
+#ifndef DANCE_SEARCH_WAVES
+#define DANCE_SEARCH_WAVES 6
+#endif
+#ifndef DANCE_SEARCH_WAVES_QB
+#define DANCE_SEARCH_WAVES_QB 5
+#endif
+template <int CPL, int PS, bool QB>
+constexpr int kSearchMinWaves = (CPL <= 3 && PS == 2) ? (QB ? DANCE_SEARCH_WAVES_QB : DANCE_SEARCH_WAVES) : 1;
 
 // search_prune_kernel_shared (vnew2.cu:1119-1439).
-template <int DT, int CPL, int PS>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kSearchMinWaves<CPL, PS>))) void k_search(SearchArgs a, uint32_t Cp) {
+template <int DT, int CPL, int PS, bool QB>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kSearchMinWaves<CPL, PS, QB>))) void k_search(SearchArgs a, uint32_t Cp) {
   extern __shared__ uint32_t smem[];
   const uint32_t w = wave_index();
   const uint32_t gw = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + w;
   if (gw >= a.g.N) return;
   const uint32_t node = a.order ? a.order[gw] : gw;
-  SearchWave<DT, CPL, PS> sw(a, node, smem + w * search_lds_words(Cp), Cp);
+  SearchWave<DT, CPL, PS, QB> sw(a, node, smem + w * search_lds_words(Cp), Cp);
   sw.run();
 }
 
@@ -700,18 +714,6 @@ struct PruneArgs {
 };
 
 __host__ __device__ constexpr uint32_t prune_lds_words(uint32_t Cp, uint32_t Rp) { return 5u * Cp + 2u * Rp; }
-
-// Threshold of the prune's bound for a candidate at stored distance sd: a
-// pair distance d >= T gives fl(alpha * d) >= fl(alpha * T) > sd, so the
-// candidate survives. Returns sqrt((T + 1e-30)(1 + kappa2)) rounded up, the
-// per-candidate part of q_threshold; +inf (never skipped) for sd < 1e-30 or
-// non-finite sd, where the relative slack would not cover rounding.
-__device__ __forceinline__ float prune_bound_root(const QBoundSet& qb, float sd, float alpha) {
-  if (!(sd >= 1e-30f) || !(sd <= FLT_MAX)) return __builtin_inff();
-  const float T = sd / alpha * (1.0f + 0x1p-20f);
-  const float t = (T + 1e-30f) * (1.0f + qb.kappa2);
-  return __builtin_sqrtf(t) * (1.0f + kQSlack);
-}
 
 constexpr uint32_t PR_REMOVED = 1u, PR_INOUT = 2u;
 

@@ -13,19 +13,8 @@ import struct
 
 import numpy as np
 
+from . import DanceMergeStats
 from . import lib as _lib
-
-
-class DanceMergeStats(C.Structure):
-    _fields_ = [
-        ("nnodes", C.c_uint64), ("replicated_nodes", C.c_uint64), ("input_edges", C.c_uint64),
-        ("self_loops", C.c_uint64), ("unique_edges", C.c_uint64), ("output_edges", C.c_uint64),
-        ("min_degree", C.c_uint32), ("max_degree", C.c_uint32),
-        ("buckets", C.c_uint64), ("long_segments", C.c_uint64),
-        ("resident_shards", C.c_uint32), ("reserved0", C.c_uint32),
-        ("read_seconds", C.c_double), ("device_ms", C.c_double), ("write_seconds", C.c_double),
-        ("total_seconds", C.c_double),
-    ]
 
 
 def _bind():

@@ -158,6 +158,13 @@ int dance_merge_shards(const char *vamana_prefix, const char *vamana_suffix, con
 
 void dance_merge_get_last_stats(DanceMergeStats *stats);
 
+/* Sizes in bytes of the structs this library fills, in the order
+ * GPUVamanaStats, DanceKernelProfile, GPUFilteredVamanaStats,
+ * DanceFilteredProfile, DanceSearchStats, DanceMergeStats; writes
+ * min(count, 6) entries and returns 6. Bindings compare them with their own
+ * layouts before any call that writes a struct. */
+uint32_t dance_struct_sizes(uint64_t *sizes, uint32_t count);
+
 /* ---- stage hooks (host buffers), used by the parity tests ---- */
 
 /* Canonical squared-L2 distances d(a[i], b[i]) (reference distance family,
