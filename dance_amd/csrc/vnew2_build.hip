@@ -289,16 +289,18 @@ static int launch_merge(const Rows& rows, GraphBufs g, const uint32_t* offs, con
   });
 }
 
-// Locality schedule (see k_cells): order[] = vertices sorted by nearest pivot.
-// Pivots are K evenly spaced rows. K comes from DANCE_LOCALITY_CELLS (default
-// 512; 0 disables the schedule). Uses the reverse-sort buffers as scratch.
+// Locality schedule (see k_cells_q / k_cells): order[] = vertices sorted by
+// nearest pivot. Pivots are K evenly spaced rows. K comes from
+// DANCE_LOCALITY_CELLS (default 1024, the fastest c3 build of 256..4096; 0
+// disables the schedule). Uses the reverse-sort buffers as scratch.
 static uint32_t locality_cells() {
   const char* e = std::getenv("DANCE_LOCALITY_CELLS");
   if (e && e[0]) return (uint32_t)std::strtoul(e, nullptr, 10);
-  return 512;
+  return 1024;
 }
 
-static int build_schedule(const Rows& rows, ReverseWs& ws, hipStream_t s, const uint32_t** order_out) {
+static int build_schedule(const Rows& rows, const QBoundSet& qb, ReverseWs& ws, hipStream_t s,
+                          const uint32_t** order_out) {
   const uint32_t N = rows.N;
   const uint32_t K = std::min(locality_cells(), N);
   *order_out = nullptr;
@@ -311,13 +313,24 @@ static int build_schedule(const Rows& rows, ReverseWs& ws, hipStream_t s, const 
   const int cpl = pick_cpl(rows.rs.nch);
   uint32_t* kb[2] = {ws.keys[0].as<uint32_t>(), ws.keys[1].as<uint32_t>()};
   uint32_t* vb[2] = {ws.vals[0].as<uint32_t>(), ws.vals[1].as<uint32_t>()};
-  DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
-    const uint32_t waves = (N + 7) / 8;
-    hipLaunchKernelGGL((k_cells<decltype(dt)::value, decltype(c)::value>), dim3(wave_grid(waves)), dim3(kBlock), 0,
-                       s, rows.rs, N, dpiv.as<uint32_t>(), K, kb[0], vb[0]);
+  if (qb.rows) {
+    // integer-code pivot search on the quantized rows
+    hipLaunchKernelGGL(k_cells_q<false>, dim3((N + 255) / 256), dim3(256), 0, s, qb.rows, kQChunks, kQChunks, N,
+                       dpiv.as<uint32_t>(), K, kb[0], vb[0]);
     DHIP(hipGetLastError());
-    return 0;
-  }));
+  } else if (rows.dtype == DANCE_U8 && rows.rs.nch <= 8) {
+    hipLaunchKernelGGL(k_cells_q<true>, dim3((N + 255) / 256), dim3(256), 0, s, rows.rs.rows, rows.rs.stride16,
+                       rows.rs.nch, N, dpiv.as<uint32_t>(), K, kb[0], vb[0]);
+    DHIP(hipGetLastError());
+  } else {
+    DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
+      const uint32_t waves = (N + 7) / 8;
+      hipLaunchKernelGGL((k_cells<decltype(dt)::value, decltype(c)::value>), dim3(wave_grid(waves)), dim3(kBlock), 0,
+                         s, rows.rs, N, dpiv.as<uint32_t>(), K, kb[0], vb[0]);
+      DHIP(hipGetLastError());
+      return 0;
+    }));
+  }
   int which = 0;
   DCHECK(radix_sort_pairs(kb, vb, N, bit_length(K - 1), ws.sort, s, &which));
   // Keep the order in the offsets-sized scratch that is free until the first
@@ -422,11 +435,11 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   if (stats) stats->medoid_seconds = now_sec() - t_med;
 
   DCHECK(launch_init(rows, g, s));
-  const uint32_t* order = nullptr;
-  DCHECK(build_schedule(rows, rws, s, &order));
   DevBuf qbuf;
   QBoundSet qb{};
   DCHECK(build_qbound(rows, qbuf, s, &qb));
+  const uint32_t* order = nullptr;
+  DCHECK(build_schedule(rows, qb, rws, s, &order));
   const uint32_t q_iters = qbound_iters(), q_prune_iters = qbound_prune_iters();
   DHIP(hipEventRecord(e_init, s));
 

@@ -1340,4 +1340,110 @@ __global__ __launch_bounds__(kBlock) void k_cells(RowSet rs, uint32_t N, const u
   }
 }
 
+
+// Approximate nearest pivot for the locality schedule, from integer codes:
+// one thread per vertex, pivot codes staged in LDS 64 at a time. U8 = false
+// reads the quantized rows (header {s, r, a} + 7 chunks of int8 codes;
+// distance ~ a_x + a_p - 2 s_x s_p <q_x, q_p>); U8 = true reads uint8 rows of
+// at most 8 chunks (exact squared distance from unsigned dot products). Only
+// the processing order depends on the result, never the graph.
+template <bool U8>
+__global__ __launch_bounds__(256) void k_cells_q(const uint4* __restrict__ rows, uint32_t stride16, uint32_t nch,
+                                                 uint32_t N, const uint32_t* __restrict__ pivots, uint32_t K,
+                                                 uint32_t* __restrict__ cell, uint32_t* __restrict__ vid) {
+  constexpr uint32_t NC = U8 ? 8u : 7u;  // code chunks per row
+  constexpr uint32_t OFF = U8 ? 0u : 1u;  // q-rows keep their header in chunk 0
+  __shared__ uint4 pc[64][NC];
+  __shared__ float pn[64], psc[64];
+  const uint32_t v = blockIdx.x * 256u + threadIdx.x;
+  const bool act = v < N;
+  const uint32_t have = U8 ? nch : 8u;
+  uint4 xc[NC];
+  float sx = 1.0f, ax = 0.0f;
+  {
+    const uint4* r = rows + (size_t)(act ? v : 0u) * stride16;
+#pragma unroll
+    for (uint32_t c = 0; c < NC; ++c) xc[c] = (act && OFF + c < have) ? r[OFF + c] : make_uint4(0u, 0u, 0u, 0u);
+    if constexpr (U8) {
+      uint32_t n2 = 0;
+#pragma unroll
+      for (uint32_t c = 0; c < NC; ++c) {
+        n2 = __builtin_amdgcn_udot4(xc[c].x, xc[c].x, n2, false);
+        n2 = __builtin_amdgcn_udot4(xc[c].y, xc[c].y, n2, false);
+        n2 = __builtin_amdgcn_udot4(xc[c].z, xc[c].z, n2, false);
+        n2 = __builtin_amdgcn_udot4(xc[c].w, xc[c].w, n2, false);
+      }
+      ax = (float)n2;
+    } else if (act) {
+      const uint4 h = r[0];
+      sx = __uint_as_float(h.x);
+      ax = __uint_as_float(h.z);
+    }
+  }
+  float best = FLT_MAX;
+  uint32_t bi = 0;
+  for (uint32_t k0 = 0; k0 < K; k0 += 64) {
+    const uint32_t np = min(64u, K - k0);
+    __syncthreads();
+    if (threadIdx.x < np) {
+      const uint4* r = rows + (size_t)pivots[k0 + threadIdx.x] * stride16;
+      uint32_t n2 = 0;
+#pragma unroll
+      for (uint32_t c = 0; c < NC; ++c) {
+        const uint4 w = OFF + c < have ? r[OFF + c] : make_uint4(0u, 0u, 0u, 0u);
+        pc[threadIdx.x][c] = w;
+        if constexpr (U8) {
+          n2 = __builtin_amdgcn_udot4(w.x, w.x, n2, false);
+          n2 = __builtin_amdgcn_udot4(w.y, w.y, n2, false);
+          n2 = __builtin_amdgcn_udot4(w.z, w.z, n2, false);
+          n2 = __builtin_amdgcn_udot4(w.w, w.w, n2, false);
+        }
+      }
+      if constexpr (U8) {
+        pn[threadIdx.x] = (float)n2;
+        psc[threadIdx.x] = 1.0f;
+      } else {
+        const uint4 h = r[0];
+        pn[threadIdx.x] = __uint_as_float(h.z);
+        psc[threadIdx.x] = __uint_as_float(h.x);
+      }
+    }
+    __syncthreads();
+    for (uint32_t p = 0; p < np; ++p) {
+      float d;
+      if constexpr (U8) {
+        uint32_t dot = 0;
+#pragma unroll
+        for (uint32_t c = 0; c < NC; ++c) {
+          const uint4 w = pc[p][c];
+          dot = __builtin_amdgcn_udot4(xc[c].x, w.x, dot, false);
+          dot = __builtin_amdgcn_udot4(xc[c].y, w.y, dot, false);
+          dot = __builtin_amdgcn_udot4(xc[c].z, w.z, dot, false);
+          dot = __builtin_amdgcn_udot4(xc[c].w, w.w, dot, false);
+        }
+        d = ax + pn[p] - 2.0f * (float)dot;
+      } else {
+        int dot = 0;
+#pragma unroll
+        for (uint32_t c = 0; c < NC; ++c) {
+          const uint4 w = pc[p][c];
+          dot = __builtin_amdgcn_sdot4((int)xc[c].x, (int)w.x, dot, false);
+          dot = __builtin_amdgcn_sdot4((int)xc[c].y, (int)w.y, dot, false);
+          dot = __builtin_amdgcn_sdot4((int)xc[c].z, (int)w.z, dot, false);
+          dot = __builtin_amdgcn_sdot4((int)xc[c].w, (int)w.w, dot, false);
+        }
+        d = ax + pn[p] - 2.0f * sx * psc[p] * (float)dot;
+      }
+      if (d < best) {
+        best = d;
+        bi = k0 + p;
+      }
+    }
+  }
+  if (act) {
+    cell[v] = bi;
+    vid[v] = v;
+  }
+}
+
 }  // namespace dance
