@@ -110,6 +110,19 @@ def test_prune_bitexact(kind, alpha, min_degree):
     assert_state_equal(g, s)
 
 
+@pytest.mark.parametrize("kind", ["f32", "f16"])
+@pytest.mark.parametrize("R,C", [(64, 200), (64, 64), (72, 100), (8, 256)])
+def test_prune_shapes_bitexact(kind, R, C):
+    """Wider and narrower rows than the build configurations (R up to 72, C up
+    to 256, C = R), with the bound on for f32 / f16."""
+    data = make_data(kind, 1500, 96, seed=4)
+    s0 = random_work_state(data, R, C, seed=12)
+    for alpha, md in ((1.0, 0), (1.2, 64)):
+        g = D.stage_prune(data, to_dance(s0), md, alpha)
+        s = O.prune(data, s0, md, alpha)
+        assert_state_equal(g, s)
+
+
 @pytest.mark.parametrize("kind", ["f32", "u8"])
 @pytest.mark.parametrize("heavy", [(0, 0), (8, 12)])
 def test_reverse_merge_bitexact(kind, heavy):
