@@ -21,7 +21,7 @@
 //   search: (search_dist + insert_dist) * V + expansions * (4R + 4)
 //           + N * (V + 4R + 4 + 16C)            (own vector, cur row, work row r/w)
 //           + bound_checks * 128                (quantized rows, when the bound is on)
-//   merge : merge_dist * 4 (snapshot distance) + reverse_edges * 4 + touched_rows * (16C + 8)
+//   merge : merge_dist * 4 (snapshot distances read) + reverse_edges * 4 + touched_rows * (16C + 8)
 //   prune : prune_dist * V + (selected rows) * V + N * 24C + prune_bound_checks * 128
 //   reverse (keys + sort): N*R*(4*3) + passes * N*R * 20
 
@@ -274,13 +274,12 @@ static int launch_merge(const Rows& rows, GraphBufs g, const uint32_t* offs, con
   MergeArgs a{rows.rs, g, offs, srcs, snap, prof.heavy_threshold, prof.heavy_sample, order, ctr};
   return with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
     constexpr int DT = decltype(dt)::value, CPL = decltype(c)::value;
-    const size_t rl = (size_t)kWavesPerBlock * merge_reg_lds_words() * 4;
     if (g.C <= 64)
-      hipLaunchKernelGGL((k_merge_reg<DT, CPL, 1>), dim3(xcd_grid(g.N)), dim3(kBlock), rl, s, a);
+      hipLaunchKernelGGL((k_merge_reg<DT, CPL, 1>), dim3(xcd_grid(g.N)), dim3(kBlock), 0, s, a);
     else if (g.C <= 128)
-      hipLaunchKernelGGL((k_merge_reg<DT, CPL, 2>), dim3(xcd_grid(g.N)), dim3(kBlock), rl, s, a);
+      hipLaunchKernelGGL((k_merge_reg<DT, CPL, 2>), dim3(xcd_grid(g.N)), dim3(kBlock), 0, s, a);
     else if (g.C <= 256)
-      hipLaunchKernelGGL((k_merge_reg<DT, CPL, 4>), dim3(xcd_grid(g.N)), dim3(kBlock), rl, s, a);
+      hipLaunchKernelGGL((k_merge_reg<DT, CPL, 4>), dim3(xcd_grid(g.N)), dim3(kBlock), 0, s, a);
     else
       hipLaunchKernelGGL((k_merge<DT, CPL>), dim3(xcd_grid(g.N)), dim3(kBlock),
                          (size_t)kWavesPerBlock * merge_lds_words(Cp) * 4, s, a, Cp);

@@ -1114,11 +1114,8 @@ struct MergeRow {
   }
 };
 
-__host__ __device__ constexpr uint32_t merge_reg_lds_words() { return 128u; }
-
 template <int DT, int CPL, int MS>
 __global__ __launch_bounds__(kBlock) void k_merge_reg(MergeArgs a) {
-  extern __shared__ uint32_t smem[];
   const uint32_t w = wave_index();
   const uint32_t gw = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + w;
   const GraphBufs& g = a.g;
@@ -1126,8 +1123,6 @@ __global__ __launch_bounds__(kBlock) void k_merge_reg(MergeArgs a) {
   const uint32_t t = a.order ? a.order[gw] : gw;
   const uint32_t N = g.N, C = g.C, R = g.R;
   const uint32_t lane = lane_id();
-  uint32_t* lst = smem + w * merge_reg_lds_words();
-  float* lsd = reinterpret_cast<float*>(lst + 64);
   const uint32_t begin = a.offsets[t], end = a.offsets[t + 1];
   const uint32_t indeg = end - begin;
   if (indeg == 0) return;
@@ -1159,25 +1154,21 @@ __global__ __launch_bounds__(kBlock) void k_merge_reg(MergeArgs a) {
       src = slot / R;
     }
     const bool v = valid_for(src, N, t);
-    bool inrow = false;
-    if (wballot(v))
-      for (uint32_t j = 0; j < deg; ++j) inrow |= row.id_at(j) == src;
-    const bool need = v && !inrow;
-    const uint64_t m = wballot(need);
-    const uint32_t n = popc64(m);
-    if (n == 0) continue;
-    if (need) {
-      lst[mbcnt64(m)] = src;
-      lsd[mbcnt64(m)] = a.snap[slot];
+    const float dsv = v ? a.snap[slot] : FLT_MAX;
+    ncand += popc64(wballot(v));
+    // Once the row is full its worst only decreases, so a source that does
+    // not beat the batch-start worst is rejected at its turn as well: the
+    // batch walks only the others (hub targets reject most of their list).
+    if (deg == C && !worst_ok) {
+      wpos = row.worst(C, lane, &wdist);
+      worst_ok = true;
     }
-    wave_sync();
-    ncand += n;
-    const uint32_t ck = lane < n ? lst[lane] : DANCE_INV;
-    const float dk = lane < n ? lsd[lane] : FLT_MAX;
-    wave_sync();
-    for (uint32_t kk = 0; kk < n; ++kk) {
-      const uint32_t s = rdlane_u(ck, (int)kk);
-      const float ds = rdlane_f(dk, (int)kk);
+    uint64_t m = wballot(v && (deg < C || (wpos >= 0 && dsv < wdist)));
+    while (m) {
+      const int kk = ffs64(m);
+      m &= m - 1;
+      const uint32_t s = rdlane_u(src, kk);
+      const float ds = rdlane_f(dsv, kk);
       if (deg == C && worst_ok && !(wpos >= 0 && ds < wdist)) continue;  // rejected either way
       if (row.contains(s, deg, lane)) continue;
       if (deg < C) {
