@@ -35,65 +35,101 @@ struct QBoundSet {
   float kappa2;       // 2 (n_lane + 8) 2^-24 for the row type and width
 };
 
-// One thread per row: codes, scale, radius. Reads `dim` elements of the row.
+// One octet per row (8 rows per wave): lane sub owns code words sub, sub+8,
+// sub+16, sub+24 (word w = dimensions 4w..4w+3), so every load and store of
+// an octet covers contiguous bytes. Computes codes, scale and radius from the
+// first `dim` elements of the row.
 template <int DT>
-__global__ void k_quantize(RowSet rs, uint32_t N, uint32_t dim, uint4* __restrict__ out) {
-  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= N) return;
-  const uint4* row = rs.rows + (size_t)i * rs.stride16;
-  auto elem = [&](uint32_t d) -> float {
+__global__ __launch_bounds__(256) void k_quantize(RowSet rs, uint32_t N, uint32_t dim, uint4* __restrict__ out) {
+  constexpr uint32_t kWords = (kQChunks - 1) * 4;  // 28 code words
+  constexpr uint32_t kEB = DT == DANCE_F32 ? 4u : 2u;  // element bytes
+  const uint32_t lane = threadIdx.x & 63u, sub = lane & 7u;
+  const uint32_t row = (blockIdx.x * 256u + threadIdx.x) >> 3;
+  const bool act = row < N;
+  const uint8_t* rb = reinterpret_cast<const uint8_t*>(rs.rows + (size_t)(act ? row : 0u) * rs.stride16);
+  const uint32_t row_bytes = rs.stride16 * 16u;
+  float v[4][4];
+#pragma unroll
+  for (uint32_t k = 0; k < 4; ++k) {
+    const uint32_t w = sub + 8u * k;
+    const bool in = act && w < kWords && 4u * w < dim && (4u * w + 4u) * kEB <= row_bytes;
     if constexpr (DT == DANCE_F32) {
-      const uint32_t* w = reinterpret_cast<const uint32_t*>(row);
-      return __uint_as_float(w[d]);
+      const uint4 c = in ? *reinterpret_cast<const uint4*>(rb + 16u * w) : make_uint4(0u, 0u, 0u, 0u);
+      v[k][0] = __uint_as_float(c.x);
+      v[k][1] = __uint_as_float(c.y);
+      v[k][2] = __uint_as_float(c.z);
+      v[k][3] = __uint_as_float(c.w);
     } else {
-      const uint16_t* h = reinterpret_cast<const uint16_t*>(row);
-      return (float)__builtin_bit_cast(_Float16, h[d]);
+      const uint2 c = in ? *reinterpret_cast<const uint2*>(rb + 8u * w) : make_uint2(0u, 0u);
+      v[k][0] = (float)__builtin_bit_cast(_Float16, (uint16_t)(c.x & 0xFFFFu));
+      v[k][1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(c.x >> 16));
+      v[k][2] = (float)__builtin_bit_cast(_Float16, (uint16_t)(c.y & 0xFFFFu));
+      v[k][3] = (float)__builtin_bit_cast(_Float16, (uint16_t)(c.y >> 16));
     }
-  };
-  float mx = 0.0f;
-  bool finite = true;
-  for (uint32_t d = 0; d < dim; ++d) {
-    const float v = elem(d);
-    finite = finite && __builtin_isfinite(v);
-    mx = fmaxf(mx, fabsf(v));
+#pragma unroll
+    for (uint32_t e = 0; e < 4; ++e)
+      if (4u * w + e >= dim) v[k][e] = 0.0f;  // padding inside a word
   }
+  float mx = 0.0f;
+  int fin = 1;
+#pragma unroll
+  for (uint32_t k = 0; k < 4; ++k)
+#pragma unroll
+    for (uint32_t e = 0; e < 4; ++e) {
+      fin &= __builtin_isfinite(v[k][e]) ? 1 : 0;
+      mx = fmaxf(mx, fabsf(v[k][e]));
+    }
+  // octet reductions (every lane of the octet ends with the result)
+  mx = fmaxf(mx, __int_as_float(dpp<kDppQuadXor1>(0, __float_as_int(mx))));
+  mx = fmaxf(mx, __int_as_float(dpp<kDppQuadXor2>(0, __float_as_int(mx))));
+  mx = fmaxf(mx, __int_as_float(dpp<kDppHalfMirror>(0, __float_as_int(mx))));
+  fin &= dpp<kDppQuadXor1>(1, fin);
+  fin &= dpp<kDppQuadXor2>(1, fin);
+  fin &= dpp<kDppHalfMirror>(1, fin);
   float s = mx / 127.0f;
   // all-zero rows are exact with s = 0; other scales must stay in range
-  const bool usable = finite && (mx == 0.0f || (s >= 0x1p-60f && s <= 0x1p50f));
+  const bool usable = fin && (mx == 0.0f || (s >= 0x1p-60f && s <= 0x1p50f));
   if (!usable || mx == 0.0f) s = 0.0f;
-  int64_t A = 0;
+  int A = 0;
   double err = 0.0;
-  uint32_t words[(kQChunks - 1) * 4];
+  uint32_t words[4];
 #pragma unroll
-  for (uint32_t w = 0; w < (kQChunks - 1) * 4; ++w) {
+  for (uint32_t k = 0; k < 4; ++k) {
     uint32_t word = 0u;
 #pragma unroll
-    for (uint32_t b = 0; b < 4; ++b) {
-      const uint32_t d = 4u * w + b;
-      if (d < dim) {
-        const float v = elem(d);
-        int q = 0;
-        if (s > 0.0f) q = (int)fminf(127.0f, fmaxf(-127.0f, rintf(v / s)));
-        A += (int64_t)q * q;
-        const double e = (double)v - (double)s * (double)q;
-        err = fma(e, e, err);
-        word |= ((uint32_t)(q & 0xFF)) << (8u * b);
-      }
+    for (uint32_t e = 0; e < 4; ++e) {
+      int qv = 0;
+      if (s > 0.0f) qv = (int)fminf(127.0f, fmaxf(-127.0f, rintf(v[k][e] / s)));
+      A += qv * qv;
+      const double d = (double)v[k][e] - (double)s * (double)qv;
+      err = fma(d, d, err);
+      word |= ((uint32_t)(qv & 0xFF)) << (8u * e);
     }
-    words[w] = word;
+    words[k] = word;
   }
-  float r = __builtin_inff();
-  if (usable) {
-    const double rd = sqrt(err) * (1.0 + 0x1p-40);
-    r = (float)rd;
-    if ((double)r < rd) r = __uint_as_float(__float_as_uint(r) + 1u);  // r >= 0: next float up
-  }
-  const float a = (float)((double)s * (double)s * (double)A);
-  uint4* o = out + (size_t)i * kQChunks;
-  o[0] = make_uint4(__float_as_uint(s), __float_as_uint(r), __float_as_uint(a), 0u);
+  A += dpp<kDppQuadXor1>(0, A);
+  A += dpp<kDppQuadXor2>(0, A);
+  A += dpp<kDppHalfMirror>(0, A);
+  err += __shfl_xor(err, 1);
+  err += __shfl_xor(err, 2);
+  err += __shfl_xor(err, 4);
+  if (!act) return;
+  uint32_t* o = reinterpret_cast<uint32_t*>(out + (size_t)row * kQChunks);
 #pragma unroll
-  for (uint32_t c = 1; c < kQChunks; ++c)
-    o[c] = make_uint4(words[4 * (c - 1)], words[4 * (c - 1) + 1], words[4 * (c - 1) + 2], words[4 * (c - 1) + 3]);
+  for (uint32_t k = 0; k < 4; ++k) {
+    const uint32_t w = sub + 8u * k;
+    if (w < kWords) o[4u + w] = words[k];
+  }
+  if (sub == 0) {
+    float r = __builtin_inff();
+    if (usable) {
+      const double rd = sqrt(err) * (1.0 + 0x1p-40);
+      r = (float)rd;
+      if ((double)r < rd) r = __uint_as_float(__float_as_uint(r) + 1u);  // r >= 0: next float up
+    }
+    const float a = (float)((double)s * (double)s * (double)A);
+    reinterpret_cast<uint4*>(o)[0] = make_uint4(__float_as_uint(s), __float_as_uint(r), __float_as_uint(a), 0u);
+  }
 }
 
 // The querying row's header (scalars) and code row address.

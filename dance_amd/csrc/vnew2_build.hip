@@ -173,7 +173,7 @@ static int build_qbound(const Rows& rows, DevBuf& buf, hipStream_t s, QBoundSet*
   const int cpl = pick_cpl(rows.rs.nch);
   if (cpl < 0) return 0;
   DCHECK(buf.alloc((size_t)rows.N * kQChunks * 16));
-  const uint32_t grid = (rows.N + 255) / 256;
+  const uint32_t grid = (uint32_t)(((uint64_t)rows.N * 8 + 255) / 256);  // one octet per row
   if (rows.dtype == DANCE_F32)
     hipLaunchKernelGGL(k_quantize<DANCE_F32>, dim3(grid), dim3(256), 0, s, rows.rs, rows.N, rows.dim, buf.as<uint4>());
   else
