@@ -89,6 +89,10 @@ static __global__ __launch_bounds__(kRadixThreads) void k_radix_hist(const uint3
   hist[(size_t)threadIdx.x * num_tiles + blockIdx.x] = h[threadIdx.x];
 }
 
+// Scatter of one pass: items get the same output positions as a direct
+// scatter (digit base of the tile + rank among the tile's items of that digit,
+// in input order), but the tile is first reordered by digit in LDS so that
+// consecutive threads write consecutive addresses of a digit's run.
 static __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(const uint32_t* __restrict__ keys,
                                                                  const uint32_t* __restrict__ vals, size_t n,
                                                                  uint32_t shift, uint32_t num_tiles,
@@ -97,11 +101,16 @@ static __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(const ui
                                                                  uint32_t* __restrict__ ovals) {
   __shared__ uint32_t wcnt[4][256];
   __shared__ uint32_t gbase[256];
+  __shared__ uint32_t toff[256];
+  __shared__ uint32_t wsum[4];
+  __shared__ uint32_t skey[kRadixTile];
+  __shared__ uint32_t sval[kRadixTile];
   const uint32_t lane = lane_id(), w = wave_index();
   for (uint32_t i = threadIdx.x; i < 4 * 256; i += kRadixThreads) (&wcnt[0][0])[i] = 0u;
   gbase[threadIdx.x] = hist_scanned[(size_t)threadIdx.x * num_tiles + blockIdx.x];
   __syncthreads();
-  const size_t base = (size_t)blockIdx.x * kRadixTile + (size_t)w * (64 * kRadixItems);
+  const size_t tile0 = (size_t)blockIdx.x * kRadixTile;
+  const size_t base = tile0 + (size_t)w * (64 * kRadixItems);
   uint32_t kk[kRadixItems], vv[kRadixItems], rk[kRadixItems];
   const uint64_t lt = (1ull << lane) - 1ull;
 #pragma unroll
@@ -135,6 +144,8 @@ static __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(const ui
       wcnt[q][dgt] = run;
       run += c;
     }
+    // offset of this digit's run inside the tile
+    toff[dgt] = block_inclusive_scan(run, wsum) - run;
   }
   __syncthreads();
 #pragma unroll
@@ -142,10 +153,19 @@ static __global__ __launch_bounds__(kRadixThreads) void k_radix_scatter(const ui
     const size_t i = base + (size_t)r * 64 + lane;
     if (i < n) {
       const uint32_t dig = (kk[r] >> shift) & 255u;
-      const size_t pos = (size_t)gbase[dig] + wcnt[w][dig] + rk[r];
-      okeys[pos] = kk[r];
-      ovals[pos] = vv[r];
+      const uint32_t li = toff[dig] + wcnt[w][dig] + rk[r];
+      skey[li] = kk[r];
+      sval[li] = vv[r];
     }
+  }
+  __syncthreads();
+  const uint32_t cnt = (uint32_t)min((size_t)kRadixTile, n - tile0);
+  for (uint32_t i = threadIdx.x; i < cnt; i += kRadixThreads) {
+    const uint32_t key = skey[i];
+    const uint32_t dig = (key >> shift) & 255u;
+    const size_t pos = (size_t)gbase[dig] + (i - toff[dig]);
+    okeys[pos] = key;
+    ovals[pos] = sval[i];
   }
 }
 

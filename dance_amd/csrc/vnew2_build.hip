@@ -251,18 +251,18 @@ struct ReverseWs {
 // forward slots (s*R + i) through *srcs_out; ws.snap holds their distances.
 static int build_reverse_csr(GraphBufs g, ReverseWs& ws, hipStream_t s, const uint32_t** srcs_out) {
   const size_t items = (size_t)g.N * g.R;
-  DHIP(hipMemsetAsync(ws.offs.p, 0, ((size_t)g.N + 1) * 4, s));
   if (items > 0) {
     hipLaunchKernelGGL(k_rev_keys, dim3((uint32_t)((items + 255) / 256)), dim3(256), 0, s, g.work, g.deg_work, g.wd,
-                       g.N, g.R, g.C, ws.keys[0].as<uint32_t>(), ws.vals[0].as<uint32_t>(), ws.snap.as<float>(),
-                       ws.offs.as<uint32_t>());
+                       g.N, g.R, g.C, ws.keys[0].as<uint32_t>(), ws.vals[0].as<uint32_t>(), ws.snap.as<float>());
     DHIP(hipGetLastError());
   }
-  DCHECK(scan_exclusive(ws.offs.as<uint32_t>(), (size_t)g.N + 1, ws.scan, s));
   uint32_t* kb[2] = {ws.keys[0].as<uint32_t>(), ws.keys[1].as<uint32_t>()};
   uint32_t* vb[2] = {ws.vals[0].as<uint32_t>(), ws.vals[1].as<uint32_t>()};
   int which = 0;
   DCHECK(radix_sort_pairs(kb, vb, items, bit_length(g.N), ws.sort, s, &which));
+  hipLaunchKernelGGL(k_seg_offsets, dim3((uint32_t)((items + 1 + 255) / 256)), dim3(256), 0, s, kb[which], items, g.N,
+                     ws.offs.as<uint32_t>());
+  DHIP(hipGetLastError());
   *srcs_out = vb[which];
   return 0;
 }

@@ -912,7 +912,7 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
 static __global__ void k_rev_keys(const uint32_t* __restrict__ work, const uint32_t* __restrict__ deg_work,
                                   const float* __restrict__ wd, uint32_t N, uint32_t R, uint32_t C,
                                   uint32_t* __restrict__ keys, uint32_t* __restrict__ vals,
-                                  float* __restrict__ snap, uint32_t* __restrict__ indeg) {
+                                  float* __restrict__ snap) {
   const size_t j = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= (size_t)N * R) return;
   const uint32_t s = (uint32_t)(j / R), i = (uint32_t)(j % R);
@@ -923,7 +923,18 @@ static __global__ void k_rev_keys(const uint32_t* __restrict__ work, const uint3
   keys[j] = v ? t : N;
   vals[j] = (uint32_t)j;
   snap[j] = v ? wd[wi] : FLT_MAX;
-  if (v) atomicAdd(&indeg[t], 1u);
+}
+
+// CSR offsets from the sorted keys (invalid items carry key N and sort last):
+// offs[t] = first index whose key is >= t, for t in [0, N]. Item i fills the
+// targets after its predecessor's key up to its own; i = n closes the range.
+static __global__ void k_seg_offsets(const uint32_t* __restrict__ keys, size_t n, uint32_t N,
+                                     uint32_t* __restrict__ offs) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i > n) return;
+  const uint32_t lo = i == 0 ? 0u : keys[i - 1] + 1u;
+  const uint32_t hi = i == n ? N : min(keys[i], N);
+  for (uint32_t t = lo; t <= hi && t <= N; ++t) offs[t] = (uint32_t)i;
 }
 
 struct MergeArgs {
