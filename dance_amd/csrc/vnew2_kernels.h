@@ -294,8 +294,8 @@ struct SearchArgs {
 };
 
 // Per-wave LDS words of the search kernel: visited cache, work row (ids,
-// dists), candidate batch (ids, dists), occlusion list, work-row order.
-__host__ __device__ constexpr uint32_t search_lds_words(uint32_t Cp) { return kVis + 4u * Cp + 128u; }
+// dists), candidate batch (ids, dists), work-row order.
+__host__ __device__ constexpr uint32_t search_lds_words(uint32_t Cp) { return kVis + 3u * Cp + 128u; }
 
 // QB compiles the quantized-bound path in (the launcher picks QB = true only
 // when the bound is on for the launch); QB = false kernels carry no bound code
@@ -304,7 +304,7 @@ template <int DT, int CPL, int PS, bool QB>
 struct SearchWave {
   const SearchArgs& a;
   uint32_t node, lane, grp, sub, Cp;
-  uint32_t *vis, *wid, *lst, *lsa, *ord;
+  uint32_t *vis, *wid, *lst, *ord;
   float *wdd, *lsd;
   uint4 av[CPL];
   RegPool<PS> P;
@@ -323,8 +323,7 @@ struct SearchWave {
     wdd = reinterpret_cast<float*>(wid + Cp);
     lst = reinterpret_cast<uint32_t*>(wdd + Cp);
     lsd = reinterpret_cast<float*>(lst + 64);
-    lsa = reinterpret_cast<uint32_t*>(lsd + 64);
-    ord = lsa + Cp;
+    ord = reinterpret_cast<uint32_t*>(lsd + 64);
     n_search = n_insert = n_skip = n_mut = n_try = n_bchk = n_bskip = 0;
   }
 
@@ -491,28 +490,27 @@ struct SearchWave {
     }
     uint4 xv[CPL];
     load_row<CPL>(a.rs, x, true, sub, xv);
-    uint32_t nA = 0, nB = 0;
+    uint32_t nA = 0, nB = 0, nU = 0;
     for (uint32_t b = 0; b < wdeg; b += 64) {
       const uint32_t i = b + lane;
       const bool in = i < wdeg;
       const uint32_t y = in ? wid[i] : DANCE_INV;
       const float dpy = in ? wdd[i] : 0.0f;
       const bool v = in && valid_for(y, N, node);
-      const bool ca = v && dpy <= dpx;
-      const uint64_t ma = wballot(ca);
-      if (ca) lsa[nA + mbcnt64(ma)] = i;
-      nA += popc64(ma);
+      nA += popc64(wballot(v && dpy <= dpx));
       nB += popc64(wballot(v && dpy > dpx));
+      nU += popc64(wballot(in && !(v && dpy == dpy)));
     }
-    wave_sync();
     // Occlusion: exists y with d_py <= d_px and alpha * d(y, x) <= d_px. The
-    // answer does not depend on the order, so stop at the first pass of 8 that
-    // finds an occluder.
+    // answer does not depend on the order; the candidates are the order's
+    // ranks [nU, nU + nA) (usable entries with d_py <= d_px, nearest to the
+    // vertex first), and the test stops at the first pass of 8 that finds an
+    // occluder.
     bool occluded = false;
     for (uint32_t p = 0; p < nA && !occluded; p += 8) {
       const uint32_t k0 = p + grp;
       const bool a0 = k0 < nA;
-      const uint32_t y0 = a0 ? wid[lsa[k0]] : 0u;
+      const uint32_t y0 = a0 ? wid[ord[nU + k0]] : 0u;
       uint4 b0[CPL];
       load_row<CPL>(a.rs, y0, a0, sub, b0);
       const float d0 = octet_finish<DT, CPL>(xv, b0);
