@@ -102,7 +102,7 @@ int validate(const FParams& p, const uint32_t* off, const uint32_t* lab, const u
 }
 
 struct FState {
-  DevBuf off, lab, lpo, lpts, starts, task_rows;
+  DevBuf off, lab, lab8, lpo, lpts, starts, task_rows;
   DevBuf ga, gb, da, db, tids, td;
   DevBuf roff, cursor, rids, boff, bd, brem, bmask;
   DevBuf ctr, d32, d64;
@@ -201,8 +201,17 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   unsigned long long* ctr = st.ctr.as<unsigned long long>();
   ScanWorkspace scan;
 
+  // Fixed-width label rows for membership tests (DANCE_FILTERED_LAB8=0: list walks only).
+  const char* l8e = std::getenv("DANCE_FILTERED_LAB8");
+  const bool use_lab8 = !(l8e && l8e[0] == '0');
+  if (use_lab8) {
+    DCHECK(st.lab8.alloc((size_t)N * 32));
+    hipLaunchKernelGGL(k_lab8, dim3(grid_thr(N)), dim3(256), 0, s, N, st.off.as<uint32_t>(), st.lab.as<uint32_t>(),
+                       st.lab8.as<uint4>());
+    DHIP(hipGetLastError());
+  }
   Labels Ld{st.off.as<uint32_t>(), st.lab.as<uint32_t>(), st.lpo.as<uint32_t>(), st.lpts.as<uint32_t>(),
-            st.starts.as<uint32_t>(), p.num_labels, p.universal};
+            st.starts.as<uint32_t>(), p.num_labels, p.universal, use_lab8 ? st.lab8.as<const uint4>() : nullptr};
   uint32_t* ga = st.ga.as<uint32_t>();
   uint32_t* gb = st.gb.as<uint32_t>();
   uint32_t* da = st.da.as<uint32_t>();

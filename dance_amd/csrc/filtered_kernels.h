@@ -75,7 +75,45 @@ struct Labels {
   const uint32_t* lpts;    // postings (points per label, ascending)
   const uint32_t* starts;  // num_labels: label entry points
   uint32_t num_labels, universal;
+  // Per point, its first 8 labels padded with DANCE_INV (two uint4), or the
+  // marker {DANCE_INV, 0, ...} for points whose list the table cannot hold
+  // (more than 8 labels, or the label DANCE_INV): membership tests then read
+  // one 32-byte row instead of walking the list. nullptr: list walks only.
+  const uint4* lab8;
 };
+
+// Builds Labels::lab8 (one thread per point).
+static __global__ void k_lab8(uint32_t N, const uint32_t* __restrict__ off, const uint32_t* __restrict__ lab,
+                              uint4* __restrict__ lab8) {
+  const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= N) return;
+  const uint32_t b = off[p], n = off[p + 1] - b;
+  uint32_t v[8];
+  bool fits = n <= 8;
+#pragma unroll
+  for (uint32_t i = 0; i < 8; ++i) {
+    v[i] = (fits && i < n) ? lab[b + i] : DANCE_INV;
+    if (fits && i < n && v[i] == DANCE_INV) fits = false;
+  }
+  if (!fits) {
+    v[0] = DANCE_INV;
+    v[1] = 0u;
+  }
+  lab8[2 * (size_t)p] = make_uint4(v[0], v[1], v[2], v[3]);
+  lab8[2 * (size_t)p + 1] = make_uint4(v[4], v[5], v[6], v[7]);
+}
+
+// Point p's table row; false when p's list must be walked instead.
+__device__ __forceinline__ bool lab8_row(const Labels& L, uint32_t p, uint4& a, uint4& b) {
+  if (!L.lab8) return false;
+  a = L.lab8[2 * (size_t)p];
+  b = L.lab8[2 * (size_t)p + 1];
+  return !(a.x == DANCE_INV && a.y == 0u);
+}
+__device__ __forceinline__ bool lab8_has(const uint4& a, const uint4& b, uint32_t label) {
+  return label != DANCE_INV && (a.x == label || a.y == label || a.z == label || a.w == label || b.x == label ||
+                                b.y == label || b.z == label || b.w == label);
+}
 
 struct Graph {
   uint32_t N, R;
@@ -85,6 +123,8 @@ struct Graph {
 
 // point_has_exact_label_device (gpu_vamana_filtered.cu:557-573)
 __device__ __forceinline__ bool has_exact(const Labels& L, uint32_t p, uint32_t label) {
+  uint4 a, b;
+  if (label != DANCE_INV && lab8_row(L, p, a, b)) return lab8_has(a, b, label);
   const uint32_t e = L.off[p + 1];
   for (uint32_t i = L.off[p]; i < e; ++i) {
     const uint32_t v = L.lab[i];
@@ -114,6 +154,12 @@ __device__ __forceinline__ bool has_common(const Labels& L, uint32_t a, uint32_t
 // one of the row's labels exactly.
 __device__ __forceinline__ bool compatible(const Labels& L, uint32_t row, uint32_t cand) {
   const uint32_t e = L.off[row + 1];
+  uint4 a, b;
+  if (lab8_row(L, cand, a, b)) {
+    for (uint32_t p = L.off[row]; p < e; ++p)
+      if (lab8_has(a, b, L.lab[p])) return true;
+    return false;
+  }
   for (uint32_t p = L.off[row]; p < e; ++p)
     if (has_exact(L, cand, L.lab[p])) return true;
   return false;
@@ -143,6 +189,14 @@ __device__ __forceinline__ bool covers(const Labels& L, uint32_t target, uint32_
 // For sorted unique label lists covers(row, s, c) == !(mask(c) & ~mask(s)):
 // the labels shared by row and c are exactly the set bits of mask(c).
 __device__ __forceinline__ uint32_t row_mask(const Labels& L, uint32_t row, uint32_t c) {
+  uint4 a, b;
+  if (lab8_row(L, c, a, b)) {
+    uint32_t bits = 0;
+    const uint32_t rb = L.off[row], re = L.off[row + 1];
+    for (uint32_t q = 0; rb + q < re; ++q)
+      if (lab8_has(a, b, L.lab[rb + q])) bits |= 1u << q;
+    return bits;
+  }
   uint32_t i = L.off[row], j = L.off[c], bits = 0, q = 0;
   const uint32_t ie = L.off[row + 1], je = L.off[c + 1];
   while (i < ie && j < je) {

@@ -107,6 +107,22 @@ def test_filtered_universal_label_and_missing_starts():
     assert_same(x, ls, starts, F.global_start(x), 32, 64, 64, 750, 32, universal=0, rounds=1)
 
 
+def test_filtered_wide_label_rows():
+    """Rows with 9-12 labels and rows carrying the label 0xFFFFFFFF mixed with
+    ordinary rows: membership tests read the fixed-width label table where a
+    point's list fits it and walk the list otherwise."""
+    x, ls = make_case("u8", 2500, 64, 40, 4, seed=21)
+    rng = np.random.default_rng(22)
+    rows = [list(ls.row(i)) for i in range(2500)]
+    for i in range(0, 2500, 5):
+        rows[i] = sorted(set(rows[i]) | set(int(v) for v in rng.choice(40, int(rng.integers(9, 13)), replace=False)))
+    for i in range(3, 2500, 17):
+        rows[i] = rows[i] + [0xFFFFFFFF]
+    ls = F.canonical_labels(rows, 40)
+    starts = F.label_starts(x, ls)
+    assert_same(x, ls, starts, F.global_start(x), 32, 64, 64, 750, 32)
+
+
 def test_filtered_hub_long_reverse_lists():
     """A hub with in-degree far above 256 takes the global-memory prune path."""
     x, ls = make_case("f32", 3000, 64, 40, 3, seed=21, hub=True)
