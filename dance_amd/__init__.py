@@ -112,6 +112,9 @@ class DanceFilteredProfile(C.Structure):
                                      "csr_prune_dist", "merged_candidates", "quota_dropped", "reverse_edges",
                                      "touched_rows", "csr_candidates", "long_lists", "out_edges",
                                      "common_edges", "long_fallbacks")]
+        + [("publish_ms", C.c_double)]
+        + [(n, C.c_uint64) for n in ("publish_dist", "publish_touched", "publish_long_entries")]
+        + [("publish_degree", C.c_uint32), ("reserved0", C.c_uint32)]
     )
 
 

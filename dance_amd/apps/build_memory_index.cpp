@@ -20,10 +20,14 @@
 //   2. entry points: global start = the point nearest to the centroid of all
 //      points; label start = the carrier of the label nearest to the centroid
 //      of its carriers (squared L2 in fp64, ties to the lower id);
-//   3. gpu_vamana_filtered_build_{uint8,float} with R = max(max_degree, 64),
-//      L = Lbuild, filtered_L = FilteredLbuild or Lbuild, C = 750 (DiskANN's
-//      default max occlusion size), STEPS = min(64, L) or
-//      DISKANN_GPU_FILTERED_STEPS (patch:20372-20398);
+//   3. gpu_vamana_filtered_build_{uint8,float} with the internal degree
+//      R_b = max(max_degree, 64) (or max(max_degree,
+//      DISKANN_GPU_FILTERED_INTERNAL_DEGREE)), L = Lbuild, filtered_L =
+//      FilteredLbuild or Lbuild, C = 750 (DiskANN's default max occlusion
+//      size), STEPS = min(64, L) or DISKANN_GPU_FILTERED_STEPS; when R_b
+//      exceeds max_degree the library's publish step prunes the graph to
+//      max_degree (DISKANN_GPU_FILTERED_PUBLISH_DEGREE is set to max_degree,
+//      and unset otherwise) (patch:20368-20398);
 //   4. install: per row drop invalid / self / repeated ids, an empty row of a
 //      multi-point index gets (i + 1) mod N (patch:20506-20521);
 //   5. save: <prefix> (graph: u64 file bytes, u32 max degree, u32 start,
@@ -31,9 +35,10 @@
 //      <prefix>_label_formatted.txt, <prefix>_labels_map.txt,
 //      <prefix>_labels_to_medoids.txt and, with a universal label,
 //      <prefix>_universal_label.txt.
-// max_degree < 64 needs the reference's GPU publish prune from the internal
-// degree 64 down to max_degree, which this library does not provide: the
-// app then exits with an error. Exit status: 0 ok, 255 (-1) on any error.
+// DISKANN_GPU_FILTERED_GPU_PUBLISH=0 with R_b above max_degree asks for
+// DiskANN's CPU prune and reverse repair instead of the publish step
+// (patch:20527-20537); that CPU code is not part of this library, so the app
+// then exits with an error. Exit status: 0 ok, 255 (-1) on any error.
 
 #include <algorithm>
 #include <chrono>
@@ -124,9 +129,6 @@ Options parse(int argc, char** argv) {
   if (o.pq_bytes != 0 || o.use_opq)
     throw std::runtime_error("[GPU filtered] first version supports only static memory indices without tags or PQ build");
   if (o.R == 0 || o.L == 0) throw std::runtime_error("--max_degree and --Lbuild must be positive");
-  if (o.R < kMinInternalDegree)
-    throw std::runtime_error("--max_degree below 64 needs the GPU publish prune from the internal degree 64, "
-                             "which this build does not provide");
   return o;
 }
 
@@ -262,9 +264,31 @@ void write_text(const std::string& path, const std::string& body) {
   if (!f) throw std::runtime_error("failed to write " + path);
 }
 
+// Internal degree and publish choice (patch:20368-20384); sets or clears
+// DISKANN_GPU_FILTERED_PUBLISH_DEGREE for the library.
+void publish_plan(uint32_t R, uint32_t& builder_R, bool& gpu_publish) {
+  builder_R = std::max(R, kMinInternalDegree);
+  const char* internal_env = std::getenv("DISKANN_GPU_FILTERED_INTERNAL_DEGREE");
+  if (internal_env && std::atoi(internal_env) > 0) builder_R = std::max(R, (uint32_t)std::atoi(internal_env));
+  const char* publish_env = std::getenv("DISKANN_GPU_FILTERED_GPU_PUBLISH");
+  gpu_publish = builder_R > R && (!publish_env || std::atoi(publish_env) != 0);
+  if (builder_R > R && !gpu_publish)
+    throw std::runtime_error("[GPU filtered] DISKANN_GPU_FILTERED_GPU_PUBLISH=0 with internal degree " +
+                             std::to_string(builder_R) + " above --max_degree " + std::to_string(R) +
+                             " needs DiskANN's CPU prune, which this build does not provide");
+  if (gpu_publish)
+    setenv("DISKANN_GPU_FILTERED_PUBLISH_DEGREE", std::to_string(R).c_str(), 1);
+  else
+    unsetenv("DISKANN_GPU_FILTERED_PUBLISH_DEGREE");
+}
+
 template <typename T>
 int run(const Options& o) {
   const double t0 = now_sec();
+  uint32_t builder_R = 0;
+  bool gpu_publish = false;
+  publish_plan(o.R, builder_R, gpu_publish);
+  const uint32_t R = gpu_publish ? o.R : builder_R;  // row width of the returned graph
   uint32_t n = 0, dim = 0;
   std::vector<T> x = read_matrix<T>(o.data_path, n, dim);
   Labels lb = read_labels(o, n);
@@ -273,23 +297,26 @@ int run(const Options& o) {
   entry_points(x, n, dim, lb, global_start, starts);
   const double t_prep = now_sec();
 
-  const uint32_t R = o.R, L = o.L, Lf = o.Lf == 0 ? o.L : o.Lf;
+  const uint32_t L = o.L, Lf = o.Lf == 0 ? o.L : o.Lf;
   const char* steps_env = std::getenv("DISKANN_GPU_FILTERED_STEPS");
   const uint32_t steps = steps_env ? (uint32_t)std::max(1, std::atoi(steps_env)) : std::min<uint32_t>(64, L);
-  std::cout << "[GPU filtered] requested_R=" << R << " internal_R=" << R << " publish_backend=direct" << std::endl;
+  std::cout << "[GPU filtered] requested_R=" << o.R << " internal_R=" << builder_R
+            << " publish_backend=" << (gpu_publish ? "gpu_warp_exact_csr" : "direct") << std::endl;
   std::cout << "[GPU filtered] N=" << n << " dim=" << dim << " labels=" << lb.names.size() - (lb.universal == 0 ? 1 : 0)
             << " label_slots=" << lb.ids.size() << " global_start=" << global_start << " L=" << L
             << " filtered_L=" << Lf << " C=" << kDefaultMaxC << " steps=" << steps << " alpha=" << o.alpha
             << std::endl;
-  std::vector<uint32_t> graph((size_t)n * R, kInvalid), degree(n, 0);
+  std::vector<uint32_t> graph((size_t)n * builder_R, kInvalid), degree(n, 0);
   int rc;
   if (std::is_same<T, uint8_t>::value)
-    rc = gpu_vamana_filtered_build_uint8(reinterpret_cast<const uint8_t*>(x.data()), n, dim, R, L, Lf, kDefaultMaxC,
+    rc = gpu_vamana_filtered_build_uint8(reinterpret_cast<const uint8_t*>(x.data()), n, dim, builder_R, L, Lf,
+                                         kDefaultMaxC,
                                          steps, o.alpha, lb.offsets.data(), lb.ids.data(), (uint32_t)lb.ids.size(),
                                          starts.data(), (uint32_t)starts.size(), lb.universal, global_start, nullptr,
                                          nullptr, 0, graph.data(), degree.data());
   else
-    rc = gpu_vamana_filtered_build_float(reinterpret_cast<const float*>(x.data()), n, dim, R, L, Lf, kDefaultMaxC,
+    rc = gpu_vamana_filtered_build_float(reinterpret_cast<const float*>(x.data()), n, dim, builder_R, L, Lf,
+                                         kDefaultMaxC,
                                          steps, o.alpha, lb.offsets.data(), lb.ids.data(), (uint32_t)lb.ids.size(),
                                          starts.data(), (uint32_t)starts.size(), lb.universal, global_start, nullptr,
                                          nullptr, 0, graph.data(), degree.data());

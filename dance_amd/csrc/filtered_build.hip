@@ -7,7 +7,9 @@
 //   labels + postings upload -> random backbone -> task rows ->
 //   3 x (task search -> row kernel (union search, merge, quota, work
 //        distances, forward prune) -> reverse count / scan / fill ->
-//        exact CSR prune) -> diagnostics -> download.
+//        exact CSR prune) -> [publish: shortlist + prune to PR, reverse
+//        CSR, shortlist + prune of the touched rows] -> diagnostics ->
+//        download.
 //
 // Device layout (row-major):
 //   rows      N x stride16 x 16 B    fp16 (float input) or u8 vectors
@@ -18,12 +20,16 @@
 //   boff      N+1 u32                scratch offsets of lists > 256 entries
 //   bd, brem  per long-list entry    distances / removed flags
 // Each round reads ga and writes gb (forward), then writes ga (repaired).
+// The publish step (DISKANN_GPU_FILTERED_PUBLISH_DEGREE = PR below R) writes
+// its N x PR graph into gb / db; rows of more than 256 candidates use
+// boff / bmask (ids) / bd / brem (states) as scratch.
 
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cstddef>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <vector>
@@ -107,7 +113,29 @@ struct FState {
   DevBuf roff, cursor, rids, boff, bd, brem, bmask;
   DevBuf ctr, d32, d64;
   size_t big_cap = 0;
+  // the output graph: ga / da, or gb / db after the publish step
+  uint32_t out_R = 0;
+  void* out_g = nullptr;
+  void* out_d = nullptr;
 };
+
+// DISKANN_GPU_FILTERED_PUBLISH_DEGREE (gpu_vamana_filtered.cu:6328-6331): a
+// positive value caps the published degree at min(R, value).
+uint32_t publish_degree(uint32_t R) {
+  const char* e = std::getenv("DISKANN_GPU_FILTERED_PUBLISH_DEGREE");
+  const int v = e ? std::atoi(e) : 0;
+  return v > 0 ? std::min(R, (uint32_t)v) : R;
+}
+
+// Makes the long-list scratch hold `need` entries.
+int ensure_big(FState& st, size_t need) {
+  if (need <= st.big_cap) return 0;
+  DCHECK(st.bd.alloc(need * 4));
+  DCHECK(st.brem.alloc(need));
+  DCHECK(st.bmask.alloc(need * 4));
+  st.big_cap = need;
+  return 0;
+}
 
 struct FEvents {
   std::vector<hipEvent_t> ev;
@@ -273,12 +301,7 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
     DHIP(hipMemcpyAsync(&tails[1], boff + N, 4, hipMemcpyDeviceToHost, s));
     DHIP(hipStreamSynchronize(s));
     reverse_edges += tails[0];
-    if (tails[1] > st.big_cap) {
-      DCHECK(st.bd.alloc((size_t)tails[1] * 4));
-      DCHECK(st.brem.alloc((size_t)tails[1]));
-      DCHECK(st.bmask.alloc((size_t)tails[1] * 4));
-      st.big_cap = tails[1];
-    }
+    DCHECK(ensure_big(st, tails[1]));
     hipEvent_t r3 = E.mark(s);
     const Graph Gb{N, R, gb, db};
     CsrArgs Cs{p.alpha, roff, st.rids.as<const uint32_t>(), boff, st.bd.as<float>(), st.brem.as<uint8_t>(),
@@ -299,12 +322,64 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   }
   if (p.rounds == 0) DHIP(hipStreamSynchronize(s));
 
+  // publish step (gpu_vamana_filtered.cu:6328-6432)
+  const uint32_t PR = publish_degree(R);
+  st.out_R = R;
+  st.out_g = ga;
+  st.out_d = da;
+  uint32_t pub_tail = 0;
+  double pub_ms = 0;
+  if (PR < R) {
+    const size_t pub_lds = (size_t)kWaves * kPubLds * 4;
+    hipEvent_t p0 = E.mark(s);
+    PubArgs P{p.alpha, PR, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, gb, db, ctr};
+    DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
+      hipLaunchKernelGGL((k_publish<decltype(dt)::value, decltype(c)::value, false>), dim3(grid_xcd(N)),
+                         dim3(kBlock), pub_lds, s, rows.rs, Graph{N, R, ga, da}, Ld, P);
+      DHIP(hipGetLastError());
+      return 0;
+    }));
+    DHIP(hipMemsetAsync(roff, 0, (size_t)(N + 1) * 4, s));
+    hipLaunchKernelGGL(k_rev_count, dim3(grid_thr(N)), dim3(256), 0, s, N, PR, gb, db, roff);
+    DHIP(hipGetLastError());
+    DCHECK(scan_exclusive(roff, (size_t)N + 1, scan, s));
+    DHIP(hipMemsetAsync(st.cursor.p, 0, (size_t)N * 4, s));
+    hipLaunchKernelGGL(k_rev_fill, dim3(grid_thr(N)), dim3(256), 0, s, N, PR, gb, db, roff,
+                       st.cursor.as<uint32_t>(), st.rids.as<uint32_t>());
+    DHIP(hipGetLastError());
+    hipLaunchKernelGGL(k_big_sizes, dim3(grid_thr((uint64_t)N + 1)), dim3(256), 0, s, N, PR, db, roff, boff);
+    DHIP(hipGetLastError());
+    DCHECK(scan_exclusive(boff, (size_t)N + 1, scan, s));
+    uint32_t tails[2] = {0, 0};
+    DHIP(hipMemcpyAsync(&tails[0], roff + N, 4, hipMemcpyDeviceToHost, s));
+    DHIP(hipMemcpyAsync(&tails[1], boff + N, 4, hipMemcpyDeviceToHost, s));
+    DHIP(hipStreamSynchronize(s));
+    pub_tail = tails[1];
+    DCHECK(ensure_big(st, tails[1]));
+    P = PubArgs{p.alpha, PR, roff, st.rids.as<const uint32_t>(), boff, st.bmask.as<uint32_t>(), st.bd.as<float>(),
+                st.brem.as<uint8_t>(), gb, db, ctr};
+    DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
+      hipLaunchKernelGGL((k_publish<decltype(dt)::value, decltype(c)::value, true>), dim3(grid_xcd(N)),
+                         dim3(kBlock), pub_lds, s, rows.rs, Graph{N, PR, gb, db}, Ld, P);
+      DHIP(hipGetLastError());
+      return 0;
+    }));
+    hipEvent_t p1 = E.mark(s);
+    DHIP(hipEventSynchronize(p1));
+    pub_ms = ms_between(p0, p1);
+    st.out_R = PR;
+    st.out_g = gb;
+    st.out_d = db;
+    peak_mem(gs.peak_gpu_mem_gb);
+  }
+
   // diagnostics of the final graph
   hipEvent_t g0 = E.mark(s);
   const uint32_t init32[8] = {0, 0, 0, 0xFFFFFFFFu, 0, 0xFFFFFFFFu, 0, 0};
   DHIP(hipMemcpyAsync(st.d32.p, init32, sizeof(init32), hipMemcpyHostToDevice, s));
   DHIP(hipMemsetAsync(st.d64.p, 0, 8 * 8, s));
-  hipLaunchKernelGGL(k_diagnostics, dim3(grid_thr(N)), dim3(256), 0, s, Graph{N, R, ga, da}, Ld,
+  hipLaunchKernelGGL(k_diagnostics, dim3(grid_thr(N)), dim3(256), 0, s,
+                     Graph{N, st.out_R, static_cast<const uint32_t*>(st.out_g), static_cast<const uint32_t*>(st.out_d)}, Ld,
                      st.d32.as<uint32_t>(), st.d64.as<unsigned long long>());
   DHIP(hipGetLastError());
   hipEvent_t g1 = E.mark(s);
@@ -369,6 +444,11 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   kp.csr_candidates = hc[kCsrCandidates];
   kp.long_lists = hc[kBigRows];
   kp.long_fallbacks = hc[kBigFallback];
+  kp.publish_ms = pub_ms;
+  kp.publish_dist = hc[kPubDist];
+  kp.publish_touched = hc[kPubTouched];
+  kp.publish_long_entries = pub_tail;
+  kp.publish_degree = st.out_R;
   kp.out_edges = h64[0];
   kp.common_edges = h64[1];
   if (verbose())
@@ -410,8 +490,8 @@ int filtered_host(const void* h_data, int src_dtype, const FParams& p, const uin
   const int rc = run_filtered(rows, p, off, lab, starts, s, st, gs, kp);
   if (rc != 0) return rc;
   const double td = now_sec();
-  DHIP(hipMemcpy(h_graph, st.ga.p, (size_t)p.N * p.R * 4, hipMemcpyDeviceToHost));
-  DHIP(hipMemcpy(h_degree, st.da.p, (size_t)p.N * 4, hipMemcpyDeviceToHost));
+  DHIP(hipMemcpy(h_graph, st.out_g, (size_t)p.N * st.out_R * 4, hipMemcpyDeviceToHost));
+  DHIP(hipMemcpy(h_degree, st.out_d, (size_t)p.N * 4, hipMemcpyDeviceToHost));
   gs.d2h_seconds = now_sec() - td;
   gs.gpu_build_seconds = now_sec() - t0;
   g_fstats = gs;
@@ -517,8 +597,8 @@ int dance_filtered_build_resident(const void* d_data, int dtype, uint32_t num_po
   FState st;
   const int rc = run_filtered(rows, p, point_label_offsets, point_labels, label_to_start_id, s, st, gs, kp);
   if (rc != 0) return rc;
-  DHIP(hipMemcpyAsync(d_graph, st.ga.p, (size_t)p.N * p.R * 4, hipMemcpyDeviceToDevice, s));
-  DHIP(hipMemcpyAsync(d_degree, st.da.p, (size_t)p.N * 4, hipMemcpyDeviceToDevice, s));
+  DHIP(hipMemcpyAsync(d_graph, st.out_g, (size_t)p.N * st.out_R * 4, hipMemcpyDeviceToDevice, s));
+  DHIP(hipMemcpyAsync(d_degree, st.out_d, (size_t)p.N * 4, hipMemcpyDeviceToDevice, s));
   DHIP(hipStreamSynchronize(s));
   gs.gpu_build_seconds = now_sec() - t0;
   g_fstats = gs;

@@ -59,6 +59,8 @@ enum : uint32_t {
   kCsrCandidates,
   kBigRows,
   kBigFallback,
+  kPubDist,
+  kPubTouched,
   kNumCounters
 };
 // Counters are striped over kCtrStripes copies (by workgroup) so that per-wave
@@ -1095,6 +1097,208 @@ __global__ __launch_bounds__(kBlock) void k_csr(RowSet rs, Graph G, Labels L, Cs
       atomicAdd(ctr_at(A.ctr, kCsrCandidates), (unsigned long long)nlive);
       if (n > kCsrRegMax) atomicAdd(ctr_at(A.ctr, kBigRows), 1ull);
       if (fell_back) atomicAdd(ctr_at(A.ctr, kBigFallback), 1ull);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Publish step for a published degree PR below the build degree
+// (gpu_vamana_filtered.cu:6328-6432).
+// ---------------------------------------------------------------------------
+constexpr uint32_t kPubLocal = kCsrRegMax;  // candidate lists up to this length stay in LDS
+// LDS words per wave of k_publish: forward row, one distance batch, then the
+// local candidate ids, distances and state bytes.
+constexpr uint32_t kPubLds = 64u + 128u + 2u * kPubLocal + kPubLocal / 4u;
+
+// canonical_rare_label_shortlist_warp (gpu_vamana_filtered.cu:5285-5406)
+// over n candidates (cid, cd) with state bytes cst; entry i belongs to lane
+// i % 64, which alone reads and writes cst[i]. For each row label that is not
+// universal, is below num_labels and has at most PR*PR points: up to quota =
+// max(1, PR / |labels(row)|) picks of the smallest (distance, id, position)
+// carrier not yet picked for that label, each output unless an earlier label
+// already output it. Then the smallest candidates not yet output fill up to
+// PR. Only ids != DANCE_INV with distance <= FLT_MAX are picked. Lane k <
+// count receives the k-th output. State bits: 1 output, 2 picked for the
+// current label, 4 carries the current label.
+__device__ uint32_t rare_shortlist(const Labels& L, uint32_t N, uint32_t row, uint32_t PR, uint32_t n,
+                                   const uint32_t* cid, const float* cd, uint8_t* cst, uint32_t lane, uint32_t& oid,
+                                   float& od) {
+  // smallest pickable (distance, id, position) with (state & mask) == want;
+  // returns its position (DANCE_INV: none), id and distance
+  auto pick = [&](uint32_t mask, uint32_t want, uint32_t& I, float& D) -> uint32_t {
+    int bk = INT_MAX;
+    uint32_t bid = DANCE_INV, bpos = DANCE_INV;
+    for (uint32_t i = lane; i < n; i += 64) {
+      if ((cst[i] & mask) != want) continue;
+      const uint32_t c = cid[i];
+      const float d = cd[i];
+      if (c == DANCE_INV || !(d <= FLT_MAX)) continue;
+      const int k = fkey(d);
+      if (k < bk || (k == bk && c < bid)) {  // positions ascend per lane: ties keep the first
+        bk = k;
+        bid = c;
+        bpos = i;
+      }
+    }
+    const int M = wave_min_i(bk);
+    if (M == INT_MAX) return DANCE_INV;
+    I = wave_min_u(bk == M ? bid : DANCE_INV);
+    D = __int_as_float(M);
+    return wave_min_u(bk == M && bid == I ? bpos : DANCE_INV);
+  };
+  for (uint32_t i = lane; i < n; i += 64) cst[i] = 0;
+  uint32_t count = 0;
+  oid = DANCE_INV;
+  od = FLT_MAX;
+  const uint32_t l0 = L.off[row], l1 = L.off[row + 1], nl = l1 - l0;
+  const uint32_t quota = nl ? max(1u, PR / nl) : 0u;
+  const uint64_t risk = (uint64_t)PR * PR;
+  for (uint32_t lp = l0; lp < l1 && count < PR; ++lp) {
+    const uint32_t label = L.lab[lp];
+    if (label == L.universal || label >= L.num_labels || (uint64_t)(L.lpo[label + 1] - L.lpo[label]) > risk) continue;
+    for (uint32_t i = lane; i < n; i += 64) {
+      const uint32_t c = cid[i];
+      const bool car = c < N && has_exact(L, c, label);
+      cst[i] = (uint8_t)((cst[i] & 1u) | (car ? 4u : 0u));
+    }
+    for (uint32_t k = 0; k < quota && count < PR; ++k) {
+      uint32_t I;
+      float D;
+      const uint32_t X = pick(6u, 4u, I, D);
+      if (X == DANCE_INV) break;
+      uint32_t was = 0;
+      if (lane == (X & 63u)) {
+        was = cst[X] & 1u;
+        cst[X] |= 3u;
+      }
+      if (!rdlane_u(was, (int)(X & 63u))) {
+        if (lane == count) {
+          oid = I;
+          od = D;
+        }
+        ++count;
+      }
+    }
+  }
+  while (count < PR) {
+    uint32_t I;
+    float D;
+    const uint32_t X = pick(1u, 0u, I, D);
+    if (X == DANCE_INV) break;
+    if (lane == (X & 63u)) cst[X] |= 1u;
+    if (lane == count) {
+      oid = I;
+      od = D;
+    }
+    ++count;
+  }
+  return count;
+}
+
+struct PubArgs {
+  float alpha;
+  uint32_t PR;
+  const uint32_t* roff;  // reverse pass: N+1 reverse offsets of the forward pass's graph
+  const uint32_t* rids;  // reverse pass: reverse sources
+  const uint32_t* boff;  // reverse pass: N+1 scratch offsets of lists longer than kPubLocal
+  uint32_t* bid;
+  float* bd;
+  uint8_t* bst;
+  uint32_t* gout;  // N x PR
+  uint32_t* dout;  // N
+  unsigned long long* ctr;
+};
+
+// One row of the publish step, one wave per row.
+// Forward pass (REV = false; canonical_fixed_rare_shortlist :5408-5431 +
+// canonical_exact_prune): candidates are the row of G (build degree R <= 64),
+// distanced, shortlisted to PR and pruned to PR into gout.
+// Reverse pass (REV = true; canonical_reverse_candidate_count/fill,
+// canonical_csr_candidate_distances, canonical_csr_rare_shortlist
+// :5036-5106, :5433-5450 + canonical_exact_prune): rows with reverse sources
+// in the forward pass's graph G (stride PR) take their forward row followed by
+// the sources not in it (not the row itself), every distance recomputed, and
+// are shortlisted and pruned again, in place (gout == G.g: each wave reads
+// only its own row, before writing it). Rows without sources keep their row.
+// Sources that duplicate the forward row stay in the list as DANCE_INV
+// entries, never picked: the relative order of the others, which alone
+// breaks ties, is that of the reference's compacted list.
+template <int DT, int CPL, bool REV>
+__global__ __launch_bounds__(kBlock) void k_publish(RowSet rs, Graph G, Labels L, PubArgs A) {
+  extern __shared__ uint32_t smem[];
+  const uint32_t w = wave_index();
+  const uint32_t row = xcd_block(blockIdx.x, gridDim.x) * kWaves + w;
+  const uint32_t N = G.N;
+  if (row >= N) return;
+  const uint32_t lane = lane_id();
+  uint32_t s0 = 0, s1 = 0;
+  if constexpr (REV) {
+    s0 = A.roff[row];
+    s1 = A.roff[row + 1];
+    if (s0 == s1) return;
+  }
+  uint32_t* fw = smem + w * kPubLds;
+  uint32_t* lst = fw + 64;
+  float* lsd = reinterpret_cast<float*>(fw + 128);
+  uint32_t* cid = fw + 192;
+  float* cdist = reinterpret_cast<float*>(cid + kPubLocal);
+  uint8_t* cst = reinterpret_cast<uint8_t*>(cid + 2u * kPubLocal);
+  const uint32_t deg = min(G.d[row], G.R);  // G.R <= 64
+  fw[lane] = lane < deg ? G.g[(size_t)row * G.R + lane] : DANCE_INV;
+  wave_sync();
+  const uint32_t n = deg + (s1 - s0);
+  if (n > kPubLocal) {  // reverse pass only: deg <= 64
+    const uint32_t b = A.boff[row];
+    cid = A.bid + b;
+    cdist = A.bd + b;
+    cst = A.bst + b;
+  }
+  const uint32_t grp = lane >> 3, sub = lane & 7u;
+  uint4 av[CPL];
+  load_row<CPL>(rs, row, true, sub, av);
+  uint32_t nd = 0;
+  for (uint32_t b = 0; b < n; b += 64) {
+    const uint32_t i = b + lane;
+    uint32_t c = DANCE_INV;
+    if (i < deg) {
+      c = fw[i];
+    } else if (i < n) {
+      c = A.rids[s0 + (i - deg)];
+      bool dup = c >= N || c == row;
+      for (uint32_t j = 0; !dup && j < deg; ++j) dup = fw[j] == c;
+      if (dup) c = DANCE_INV;
+    }
+    const bool ok = i < n && c < N;  // ids outside the graph get no distance and are never picked
+    float dist = __builtin_inff();
+    const uint64_t m = wballot(ok);
+    if (m) {
+      const uint32_t cnt = popc64(m), pos = mbcnt64(m);
+      if (ok) lst[pos] = c;
+      wave_sync();
+      batch_dist<DT, CPL>(rs, av, lst, lsd, cnt, grp, sub);
+      nd += cnt;
+      if (ok) dist = lsd[pos];
+      wave_sync();
+    }
+    if (i < n) {
+      cid[i] = c;
+      cdist[i] = dist;
+    }
+  }
+  uint32_t oid;
+  float od;
+  const uint32_t cnt = rare_shortlist(L, N, row, A.PR, n, cid, cdist, cst, lane, oid, od);
+  const uint32_t id1[1] = {oid};
+  const float d1[1] = {od};
+  uint32_t outv, npd = 0;
+  const uint32_t sel =
+      prune_regs<DT, CPL, 1>(rs, L, row, A.PR, A.alpha, id1, d1, lane < cnt ? 0u : 1u, lst, lsd, lane, outv, npd);
+  if (lane < A.PR) A.gout[(size_t)row * A.PR + lane] = lane < sel ? outv : DANCE_INV;
+  if (lane == 0) {
+    A.dout[row] = sel;
+    if (A.ctr) {
+      atomicAdd(ctr_at(A.ctr, kPubDist), (unsigned long long)(nd + npd));
+      if (REV) atomicAdd(ctr_at(A.ctr, kPubTouched), 1ull);
     }
   }
 }

@@ -174,7 +174,9 @@ def build_rc(data, ls: LabelSet, starts, R: int, L: int, filtered_L: int, C_: in
 def filtered_build(data: np.ndarray, ls: LabelSet, starts: np.ndarray | None = None, R: int = 64, L: int = 100,
                    filtered_L: int = 100, C_: int = DISKANN_MAXC, STEPS: int = 64, alpha: float = 1.2,
                    universal: int = INVALID, gstart: int | None = None, rounds: int = ROUNDS) -> FilteredResult:
-    """gpu_vamana_filtered_build_{uint8,float} on host rows."""
+    """gpu_vamana_filtered_build_{uint8,float} on host rows. With
+    DISKANN_GPU_FILTERED_PUBLISH_DEGREE set to PR in (0, R) the graph has PR
+    columns (the publish step)."""
     data = np.ascontiguousarray(data)
     if data.ndim != 2 or data.shape[0] != ls.n:
         raise ValueError("data must be N x dim with one label row per point")
@@ -184,7 +186,11 @@ def filtered_build(data: np.ndarray, ls: LabelSet, starts: np.ndarray | None = N
     degree = np.empty(data.shape[0], np.uint32)
     _check(build_rc(data, ls, starts, R, L, filtered_L, C_, STEPS, alpha, universal, gstart, rounds, graph,
                     degree), "gpu_vamana_filtered_build")
-    return FilteredResult(graph, degree, last_stats(), last_profile())
+    prof = last_profile()
+    PR = int(prof["publish_degree"])  # below R after the publish step (DISKANN_GPU_FILTERED_PUBLISH_DEGREE)
+    if PR < R:
+        graph = np.ascontiguousarray(graph.ravel()[:data.shape[0] * PR].reshape(data.shape[0], PR))
+    return FilteredResult(graph, degree, last_stats(), prof)
 
 
 def filtered_build_resident(d_data: int, dtype: int, N: int, dim: int, ls: LabelSet, starts: np.ndarray, R: int,

@@ -75,6 +75,12 @@ typedef struct DanceFilteredProfile {
     uint64_t out_edges, common_edges;
     /* long CSR lists whose prune needed more than their 256 smallest candidates */
     uint64_t long_fallbacks;
+    /* publish step (DISKANN_GPU_FILTERED_PUBLISH_DEGREE below R): kernel time,
+     * distances, rows rebuilt from reverse sources, scratch entries of lists
+     * over 256 candidates; publish_degree is the output graph's row width */
+    double publish_ms;
+    uint64_t publish_dist, publish_touched, publish_long_entries;
+    uint32_t publish_degree, reserved0;
 } DanceFilteredProfile;
 
 /* The filtered build of gpu_vamana_filtered_build_{uint8,float} (reference:

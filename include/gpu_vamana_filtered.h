@@ -25,8 +25,12 @@
  * not strictly ascending, or a runtime error; 1 when the
  * GPU work capacity min(C, 128) per point cannot hold the exact reverse CSR
  * (min(C, 128) < 2 * R), as the reference does. Messages go to stderr.
- * Caller owns h_graph (num_points * R, rows padded with 0xFFFFFFFF) and
- * h_degree (num_points). Builds are synchronous and serialized; the last
+ * Caller owns h_graph (num_points * PR, rows padded with 0xFFFFFFFF) and
+ * h_degree (num_points). PR is R, or min(R, v) when the environment variable
+ * DISKANN_GPU_FILTERED_PUBLISH_DEGREE holds v > 0 (atoi): below R the built
+ * graph is shortlisted and pruned to PR per row, then rows with reverse
+ * edges are rebuilt from their row plus those sources and pruned again (the
+ * publish step, reference gpu_vamana_filtered.cu:6328-6432). Builds are synchronous and serialized; the last
  * stats are a process global, as in the reference. */
 #ifndef DANCE_GPU_VAMANA_FILTERED_H
 #define DANCE_GPU_VAMANA_FILTERED_H

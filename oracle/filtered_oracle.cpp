@@ -294,11 +294,11 @@ uint32_t merge_row(const Ctx& c, const uint32_t* ga, const uint32_t* da, uint32_
 // canonical_exact_prune / canonical_exact_prune_csr (:4876-4994, :5130-5230):
 // FilteredRobustPrune, selection by (distance, id, position).
 uint32_t filtered_prune(const Ctx& c, uint32_t row, const uint32_t* ids, const float* ds, uint32_t n, float alpha,
-                        uint32_t* out) {
+                        uint32_t* out, uint32_t R) {
   std::vector<uint8_t> removed(n, 0);
   uint32_t sel = 0;
-  for (uint32_t i = 0; i < c.R; ++i) out[i] = INV;
-  while (sel < c.R) {
+  for (uint32_t i = 0; i < R; ++i) out[i] = INV;
+  while (sel < R) {
     float bd = FLT_MAX;
     uint32_t bid = 0xFFFFFFFFu, bi = 0xFFFFFFFFu;
     for (uint32_t i = 0; i < n; ++i) {
@@ -316,6 +316,104 @@ uint32_t filtered_prune(const Ctx& c, uint32_t row, const uint32_t* ids, const f
     }
   }
   return sel;
+}
+
+// canonical_rare_label_shortlist_warp (:5291-5406): keeps at most R of the
+// n candidates. For each row label (CSR order) that is not universal, is
+// below num_labels and has at most R*R points, up to quota = max(1, R / |F_row|)
+// picks of the smallest (distance, id, position) carrying the label, each
+// pick output unless an earlier label already output it; then the smallest
+// remaining candidates fill up to R. Only ids != INV with distance <=
+// FLT_MAX are picked.
+uint32_t rare_shortlist(const Ctx& c, uint32_t row, uint32_t R, const uint32_t* ids, const float* ds, uint32_t n,
+                        uint32_t* out_ids, float* out_ds) {
+  std::vector<uint8_t> state(n, 0);  // bit 1: output, bit 2: picked for the current label
+  uint32_t count = 0;
+  const uint32_t nl = c.off[row + 1] - c.off[row];
+  const uint32_t quota = nl ? std::max(1u, R / nl) : 0u;
+  const uint64_t risk = (uint64_t)R * R;
+  auto better = [&](uint32_t i, uint32_t best) {
+    if (best == INV) return true;
+    return ds[i] < ds[best] || (ds[i] == ds[best] && (ids[i] < ids[best] || (ids[i] == ids[best] && i < best)));
+  };
+  auto pickable = [&](uint32_t i) { return ids[i] != INV && ds[i] <= FLT_MAX; };
+  for (uint32_t lp = c.off[row]; lp < c.off[row + 1] && count < R; ++lp) {
+    const uint32_t label = c.lab[lp];
+    if (label == c.universal || label >= c.num_labels || (uint64_t)(c.lpo[label + 1] - c.lpo[label]) > risk) continue;
+    for (uint32_t i = 0; i < n; ++i) state[i] &= 1;
+    for (uint32_t k = 0; k < quota && count < R; ++k) {
+      uint32_t best = INV;
+      for (uint32_t i = 0; i < n; ++i)
+        if (!(state[i] & 2) && pickable(i) && has_exact(c, ids[i], label) && better(i, best)) best = i;
+      if (best == INV) break;
+      state[best] |= 2;
+      if (!(state[best] & 1)) {
+        state[best] |= 1;
+        out_ids[count] = ids[best];
+        out_ds[count] = ds[best];
+        ++count;
+      }
+    }
+  }
+  while (count < R) {
+    uint32_t best = INV;
+    for (uint32_t i = 0; i < n; ++i)
+      if (!(state[i] & 1) && pickable(i) && better(i, best)) best = i;
+    if (best == INV) break;
+    state[best] |= 1;
+    out_ids[count] = ids[best];
+    out_ds[count] = ds[best];
+    ++count;
+  }
+  return count;
+}
+
+// The publish step for a published degree PR below the build degree R
+// (gpu_vamana_filtered.cu:6328-6432): every row's R-row is distanced,
+// shortlisted and pruned to PR (canonical_fixed_rare_shortlist :5408-5431 +
+// canonical_exact_prune); then rows with reverse edges in that graph are
+// rebuilt from their forward row plus new reverse sources, shortlisted and
+// pruned to PR again (canonical_reverse_* + canonical_csr_rare_shortlist
+// :5433-5450 + canonical_exact_prune).
+void publish(const Ctx& c, const std::vector<uint32_t>& ga, const std::vector<uint32_t>& da, uint32_t R,
+             uint32_t PR, float alpha, std::vector<uint32_t>& pg, std::vector<uint32_t>& pd) {
+  const uint32_t N = c.N;
+  pg.assign((size_t)N * PR, INV);
+  pd.assign(N, 0);
+#pragma omp parallel for schedule(dynamic, 64)
+  for (int64_t r = 0; r < (int64_t)N; ++r) {
+    const uint32_t row = (uint32_t)r, deg = std::min(da[row], R);
+    std::vector<uint32_t> ids(ga.begin() + (size_t)row * R, ga.begin() + (size_t)row * R + deg), sid(PR);
+    std::vector<float> ds(deg), sd(PR);
+    for (uint32_t i = 0; i < deg; ++i) ds[i] = ids[i] < N ? c.D(row, ids[i]) : INFINITY;  // never picked
+    const uint32_t n = rare_shortlist(c, row, PR, ids.data(), ds.data(), deg, sid.data(), sd.data());
+    pd[row] = filtered_prune(c, row, sid.data(), sd.data(), n, alpha, &pg[(size_t)row * PR], PR);
+  }
+  std::vector<std::vector<uint32_t>> rev(N);
+  for (uint32_t row = 0; row < N; ++row)
+    for (uint32_t i = 0; i < std::min(pd[row], PR); ++i) {
+      const uint32_t dst = pg[(size_t)row * PR + i];
+      if (dst < N && dst != row) rev[dst].push_back(row);
+    }
+  std::vector<uint32_t> gnew(pg), dnew(pd);
+#pragma omp parallel for schedule(dynamic, 64)
+  for (int64_t r = 0; r < (int64_t)N; ++r) {
+    const uint32_t row = (uint32_t)r;
+    if (rev[row].empty()) continue;
+    const uint32_t deg = std::min(pd[row], PR);
+    std::vector<uint32_t> ids(pg.begin() + (size_t)row * PR, pg.begin() + (size_t)row * PR + deg), sid(PR);
+    for (uint32_t s : rev[row]) {
+      bool dup = s >= N || s == row;
+      for (uint32_t i = 0; !dup && i < deg; ++i) dup = pg[(size_t)row * PR + i] == s;
+      if (!dup) ids.push_back(s);
+    }
+    std::vector<float> ds(ids.size()), sd(PR);
+    for (size_t i = 0; i < ids.size(); ++i) ds[i] = ids[i] < N ? c.D(row, ids[i]) : INFINITY;
+    const uint32_t n = rare_shortlist(c, row, PR, ids.data(), ds.data(), (uint32_t)ids.size(), sid.data(), sd.data());
+    dnew[row] = filtered_prune(c, row, sid.data(), sd.data(), n, alpha, &gnew[(size_t)row * PR], PR);
+  }
+  pg.swap(gnew);
+  pd.swap(dnew);
 }
 
 // Context with the label -> points postings (ascending rows), as the
@@ -373,7 +471,7 @@ int oracle_filtered_build(const void* data, int dtype, uint32_t N, uint32_t dim,
                           uint32_t filtered_L, uint32_t C, uint32_t STEPS, float alpha, const uint32_t* offsets,
                           const uint32_t* labels, uint32_t total_labels, const uint32_t* label_starts,
                           uint32_t num_labels, uint32_t universal_label, uint32_t global_start, uint32_t rounds,
-                          uint32_t* graph_out, uint32_t* degree_out, uint64_t* diag) {
+                          uint32_t publish_R, uint32_t* graph_out, uint32_t* degree_out, uint64_t* diag) {
   if (!data || !graph_out || !degree_out || !offsets || !labels || !label_starts) return -1;
   if (N == 0 || dim == 0 || R == 0 || L == 0 || C < R || rounds > 3) return -1;
   const uint32_t work_C = std::min(C, 128u);
@@ -407,7 +505,7 @@ int oracle_filtered_build(const void* data, int dtype, uint32_t N, uint32_t dim,
                             td.data(), w, dd);
       for (uint32_t i = 0; i < wdeg[row]; ++i)  // canonical_compute_work_distances (:4844-4871)
         if (dd[i] == FLT_MAX) dd[i] = c.D(row, w[i]);
-      db[row] = filtered_prune(c, row, w, dd, wdeg[row], alpha, &gb[(size_t)row * R]);
+      db[row] = filtered_prune(c, row, w, dd, wdeg[row], alpha, &gb[(size_t)row * R], R);
     }
     // Exact CSR reverse (:4996-5128) + CSR prune (:5130-5230).
     std::vector<std::vector<uint32_t>> rev(N);
@@ -430,10 +528,18 @@ int oracle_filtered_build(const void* data, int dtype, uint32_t N, uint32_t dim,
       }
       std::vector<float> ds(ids.size());
       for (size_t i = 0; i < ids.size(); ++i) ds[i] = c.D(row, ids[i]);
-      dnew[row] = filtered_prune(c, row, ids.data(), ds.data(), (uint32_t)ids.size(), alpha, &gnew[(size_t)row * R]);
+      dnew[row] = filtered_prune(c, row, ids.data(), ds.data(), (uint32_t)ids.size(), alpha, &gnew[(size_t)row * R],
+                                 R);
     }
     ga.swap(gnew);
     da.swap(dnew);
+  }
+  if (publish_R > 0 && publish_R < R) {
+    std::vector<uint32_t> pg, pd;
+    publish(c, ga, da, R, publish_R, alpha, pg, pd);
+    ga.swap(pg);
+    da.swap(pd);
+    R = publish_R;
   }
   std::memcpy(graph_out, ga.data(), ga.size() * 4);
   std::memcpy(degree_out, da.data(), da.size() * 4);
@@ -471,13 +577,23 @@ int oracle_filtered_build(const void* data, int dtype, uint32_t N, uint32_t dim,
   return 0;
 }
 
+// Pinning hook (tests only): one rare-label shortlist of an explicit list.
+uint32_t oracle_filtered_shortlist(uint32_t N, uint32_t R, const uint32_t* offsets, const uint32_t* labels,
+                                   uint32_t total_labels, uint32_t num_labels, uint32_t universal, uint32_t row,
+                                   const uint32_t* ids, const float* ds, uint32_t n, uint32_t* out_ids,
+                                   float* out_ds) {
+  std::vector<uint32_t> starts(std::max(1u, num_labels), INV);
+  Ctx c = make_ctx(nullptr, 1, N, 1, R, offsets, labels, total_labels, starts.data(), num_labels, universal);
+  return rare_shortlist(c, row, R, ids, ds, n, out_ids, out_ds);
+}
+
 // Pinning hooks (tests only): one FilteredRobustPrune of an explicit list,
 // and one merge + label quota of explicit task / old-neighbour / union inputs.
 uint32_t oracle_filtered_prune(const void* data, int dtype, uint32_t N, uint32_t dim, uint32_t R, float alpha,
                                const uint32_t* offsets, const uint32_t* labels, uint32_t row, const uint32_t* ids,
                                const float* ds, uint32_t n, uint32_t* out) {
   Ctx c{data, dtype, N, dim, R, offsets, labels, 0, INV, nullptr, {}, {}};
-  return filtered_prune(c, row, ids, ds, n, alpha, out);
+  return filtered_prune(c, row, ids, ds, n, alpha, out, R);
 }
 
 uint32_t oracle_filtered_merge(uint32_t N, uint32_t R, uint32_t C, uint32_t per_label_keep, const uint32_t* offsets,

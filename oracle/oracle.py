@@ -110,7 +110,7 @@ def lib() -> C.CDLL:
         L.oracle_filtered_random_graph.argtypes = [u32, u32, u32, u32, _u32p, _u32p]
         L.oracle_filtered_random_graph.restype = None
         L.oracle_filtered_build.argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, u32, f32, _u32p, _u32p, u32,
-                                            _u32p, u32, u32, u32, u32, _u32p, _u32p, C.POINTER(u64)]
+                                            _u32p, u32, u32, u32, u32, u32, _u32p, _u32p, C.POINTER(u64)]
         L.oracle_filtered_build.restype = i32
         L.oracle_filtered_prune.argtypes = [vp, i32, u32, u32, u32, f32, _u32p, _u32p, u32, _u32p, _f32p, u32,
                                             _u32p]
@@ -121,6 +121,9 @@ def lib() -> C.CDLL:
         L.oracle_query_search.argtypes = [vp, i32, u32, u32, _u32p, _u32p, u32, _u32p, u32, vp, u32, u32, u32,
                                           vp, vp, vp, _u32p, _f32p]
         L.oracle_query_search.restype = u64
+        L.oracle_filtered_shortlist.argtypes = [u32, u32, _u32p, _u32p, u32, u32, u32, u32, _u32p, _f32p, u32,
+                                                _u32p, _f32p]
+        L.oracle_filtered_shortlist.restype = u32
         L.oracle_mix64.argtypes = [u64]
         L.oracle_mix64.restype = u64
         L.oracle_edge_hash.argtypes = [u32, u32, u64]
@@ -298,10 +301,11 @@ def filtered_random_graph(N: int, R: int, initial_degree: int = 16, seed: int = 
 def filtered_build(data: np.ndarray, offsets: np.ndarray, labels: np.ndarray, starts: np.ndarray,
                    num_labels: int, R: int = 64, L: int = 100, filtered_L: int = 100, C_: int = 750,
                    STEPS: int = 64, alpha: float = 1.2, universal: int = INVALID, global_start: int = INVALID,
-                   rounds: int = 3):
+                   rounds: int = 3, publish_R: int = 0):
     """canonical_v2 filtered build. Float32 rows are searched as fp16 (the
     reference converts float input, src/gpu_vamana_filtered.cu:6497-6503).
-    Returns (rc, graph, degree, diag[12])."""
+    With 0 < publish_R < R the publish step prunes the graph to publish_R
+    (the graph then has publish_R columns). Returns (rc, graph, degree, diag[12])."""
     if data.dtype == np.float32:
         data = data.astype(np.float16)
     data = np.ascontiguousarray(data)
@@ -314,8 +318,10 @@ def filtered_build(data: np.ndarray, offsets: np.ndarray, labels: np.ndarray, st
     starts = np.ascontiguousarray(starts, np.uint32)
     rc = lib().oracle_filtered_build(data.ctypes.data, _dt(data), N, dim, R, L, filtered_L, C_, STEPS, alpha,
                                      _p(offsets), _p(labels), int(labels.shape[0]), _p(starts), num_labels,
-                                     universal, global_start, rounds, _p(g), _p(d),
+                                     universal, global_start, rounds, publish_R, _p(g), _p(d),
                                      diag.ctypes.data_as(C.POINTER(C.c_uint64)))
+    if 0 < publish_R < R:
+        g = np.ascontiguousarray(g.ravel()[:N * publish_R].reshape(N, publish_R))
     return rc, g, d, diag
 
 
@@ -389,3 +395,17 @@ def merge_shards(vamana_prefix: str, vamana_suffix: str, idmaps_prefix: str, idm
                                    idmaps_suffix.encode(), nshards, max_degree, output_vamana.encode(),
                                    medoids_file.encode(), seed, cnt)
     return int(rc), {"self_loops": int(cnt[0]), "unique_edges": int(cnt[1]), "output_edges": int(cnt[2])}
+
+
+def filtered_shortlist(offsets, labels, num_labels: int, universal: int, R: int, row: int, ids, ds):
+    """One rare-label shortlist (the publish step's candidate choice); returns (ids, dists)."""
+    offsets = np.ascontiguousarray(offsets, np.uint32)
+    labels = np.ascontiguousarray(labels, np.uint32)
+    ids = np.ascontiguousarray(ids, np.uint32)
+    ds = np.ascontiguousarray(ds, np.float32)
+    oi = np.empty(max(R, 1), np.uint32)
+    od = np.empty(max(R, 1), np.float32)
+    n = lib().oracle_filtered_shortlist(offsets.shape[0] - 1, R, _p(offsets), _p(labels), int(labels.shape[0]),
+                                        num_labels, universal, row, _p(ids), _p(ds, C.c_float), int(ids.shape[0]),
+                                        _p(oi), _p(od, C.c_float))
+    return oi[:n], od[:n]

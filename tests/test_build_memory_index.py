@@ -55,7 +55,6 @@ def base_args(dp, lp, prefix, kind="uint8"):
     (lambda a: [x for x in a if x != "--gpu_filtered"], "only the --gpu_filtered build"),
     (lambda a: a[:1] + ["int8"] + a[2:], "supports only float and uint8"),
     (lambda a: a[:3] + ["mips"] + a[4:], "--dist_fn l2 only"),
-    (lambda a: a + ["--max_degree", "32"], "below 64"),
     (lambda a: a + ["--build_PQ_bytes", "8"], "without tags or PQ"),
     (lambda a: a + ["--bogus", "1"], "unknown argument"),
 ])
@@ -77,6 +76,16 @@ def test_label_file_errors(tmp_path, content, msg):
         f.write(content)
     r = run_app(*base_args(dp, lp, str(tmp_path / "idx")))
     assert r.returncode == 255 and msg in r.stderr, r.stderr
+    assert not os.path.exists(str(tmp_path / "idx"))
+
+
+def test_cpu_publish_request_is_an_error(tmp_path):
+    # DISKANN_GPU_FILTERED_GPU_PUBLISH=0 below the internal degree asks for
+    # DiskANN's CPU prune (patch:20527-20537), which is not part of this build
+    _, _, dp, lp = make_case(tmp_path, n=20)
+    env = dict(os.environ, DISKANN_GPU_FILTERED_GPU_PUBLISH="0")
+    r = run_app(*base_args(dp, lp, str(tmp_path / "idx")), "--max_degree", "32", env=env)
+    assert r.returncode == 255 and "CPU prune" in r.stderr, r.stderr
     assert not os.path.exists(str(tmp_path / "idx"))
 
 
@@ -103,13 +112,19 @@ def centroid_start(x, carriers):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("kind,universal_every", [("uint8", 0), ("float", 0), ("uint8", 7)])
-def test_app_matches_oracle(tmp_path, kind, universal_every):
+@pytest.mark.parametrize("kind,universal_every,R", [("uint8", 0, 64), ("float", 0, 64), ("uint8", 7, 64),
+                                                    ("uint8", 0, 32), ("float", 7, 12)])
+def test_app_matches_oracle(tmp_path, kind, universal_every, R):
+    # R below 64: built at internal degree 64, published at R by the GPU
+    # publish step (patch:20368-20384, gpu_vamana_filtered.cu:6328-6432)
     x, rows, dp, lp = make_case(tmp_path, kind=kind, universal_every=universal_every)
     prefix = str(tmp_path / "idx")
     args = base_args(dp, lp, prefix, kind) + (["--universal_label", "ANY"] if universal_every else [])
-    r = run_app(*args)
+    env = {k: v for k, v in os.environ.items() if not k.startswith("DISKANN_GPU_FILTERED_")}
+    r = run_app(*args, "--max_degree", str(R), env=env)
     assert r.returncode == 0, r.stdout + r.stderr
+    assert f"requested_R={R} internal_R=64" in r.stdout
+    assert ("publish_backend=gpu_warp_exact_csr" in r.stdout) == (R < 64)
     n = x.shape[0]
     ids, per_row = expected_ids(rows, "ANY" if universal_every else None)
     # sidecars
@@ -142,12 +157,12 @@ def test_app_matches_oracle(tmp_path, kind, universal_every):
     ls = F.canonical_labels(canon, num_labels)
     rc, g, deg, _ = O.filtered_build(x, ls.offsets, ls.labels, starts, num_labels, R=64, L=100, filtered_L=100,
                                      C_=750, STEPS=64, alpha=1.2, universal=0 if universal_every else INV,
-                                     global_start=start)
-    assert rc == 0
+                                     global_start=start, publish_R=R if R < 64 else 0)
+    assert rc == 0 and g.shape == (n, R)
     want = []
     for i in range(n):
         row = []
-        for j in range(min(int(deg[i]), 64)):
+        for j in range(min(int(deg[i]), R)):
             v = int(g[i, j])
             if v != INV and v < n and v != i and v not in row:
                 row.append(v)

@@ -203,3 +203,103 @@ def test_build_parameter_errors():
     assert O.filtered_build(x, ls.offsets, ls.labels, st, 1, R=8, C_=4)[0] == -1
     assert O.filtered_build(x, ls.offsets, ls.labels, st, 1, R=70, C_=750)[0] == 1
     assert O.filtered_build(x, ls.offsets, ls.labels, st, 1, R=8, C_=64, rounds=4)[0] == -1
+
+
+def shortlist_by_sorting(row_labels, labels_of, label_size, universal, num_labels, R, ids, ds):
+    """The rare-label shortlist restated with sorted lists: per eligible row
+    label, its quota smallest (distance, id, position) carriers in order, each
+    output once; then the smallest remaining fill up to R."""
+    cand = [(float(d), int(i), p) for p, (i, d) in enumerate(zip(ids, ds)) if i != INVALID and d <= FMAX]
+    out, taken = [], set()
+    quota = max(1, R // len(row_labels)) if row_labels else 0
+    for label in row_labels:
+        if label == universal or label >= num_labels or label_size[label] > R * R:
+            continue
+        for d, i, p in sorted(x for x in cand if label in labels_of(x[1]))[:quota]:
+            if len(out) >= R:
+                break
+            if p not in taken:
+                taken.add(p)
+                out.append((i, d))
+    for d, i, p in sorted(cand):
+        if len(out) >= R:
+            break
+        if p not in taken:
+            taken.add(p)
+            out.append((i, d))
+    return out
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_rare_shortlist_matches_sorted_restatement(seed):
+    rng = np.random.default_rng(seed)
+    N, vocab = 60, 10
+    rows = [sorted(set(int(v) for v in rng.choice(vocab + 2, int(rng.integers(0, 5)), replace=False)))
+            for _ in range(N)]
+    offs = np.zeros(N + 1, np.uint32)
+    offs[1:] = np.cumsum([len(r) for r in rows])
+    labs = np.array([v for r in rows for v in r], np.uint32)
+    universal = int(rng.integers(0, vocab)) if seed % 3 == 0 else INVALID
+    size = {l: sum(l in r for r in rows) for l in range(vocab + 2)}
+    R = int(rng.integers(2, 12))
+    row = int(rng.integers(0, N))
+    n = int(rng.integers(0, 40))
+    ids = rng.integers(0, N, n).astype(np.uint32)
+    ids[rng.random(n) < 0.1] = INVALID
+    for k in range(1, n):  # repeated ids: each position is taken at most once
+        if rng.random() < 0.1:
+            ids[k] = ids[k - 1]
+    ds = rng.integers(0, 6, n).astype(np.float32)  # many ties
+    ds[rng.random(n) < 0.05] = FMAX
+    got_i, got_d = O.filtered_shortlist(offs, labs, vocab, universal, R, row, ids, ds)
+    want = shortlist_by_sorting(rows[row], lambda i: rows[i], size, universal, vocab, R, ids, ds)
+    assert list(zip(got_i.tolist(), got_d.tolist())) == [(i, d) for i, d in want]
+
+
+def publish_by_composition(x, ls, universal, g, d, R, PR, alpha):
+    """The publish step restated from its two pinned parts (the shortlist and
+    FilteredRobustPrune): every row's R-row distanced, shortlisted and pruned
+    to PR; then rows with reverse edges in that graph rebuilt from their row
+    plus the new sources (not the row itself), distanced again, shortlisted
+    and pruned to PR."""
+    N = x.shape[0]
+
+    def one(row, ids):
+        ids = np.asarray(ids, np.uint32)
+        ds = np.array([O.distance(x, row, int(c)) for c in ids], np.float32)
+        si, sd = O.filtered_shortlist(ls.offsets, ls.labels, ls.num_labels, universal, PR, row, ids, ds)
+        return O.filtered_prune(x, ls.offsets, ls.labels, row, si, sd, PR, alpha).tolist()
+
+    fwd = [one(row, g[row, :min(int(d[row]), R)]) for row in range(N)]
+    rev = [[] for _ in range(N)]
+    for row in range(N):
+        for c in fwd[row]:
+            if c < N and c != row:
+                rev[c].append(row)
+    out = [one(row, fwd[row] + [s for s in rev[row] if s not in fwd[row] and s != row]) if rev[row] else fwd[row]
+           for row in range(N)]
+    pg = np.full((N, PR), INVALID, np.uint32)
+    for row, r in enumerate(out):
+        pg[row, :len(r)] = r
+    return pg, np.array([len(r) for r in out], np.uint32)
+
+
+@pytest.mark.parametrize("PR,universal", [(6, INVALID), (20, 0), (31, INVALID)])
+def test_publish_matches_composition(PR, universal):
+    rng = np.random.default_rng(PR)
+    N, R = 400, 32
+    x = rng.integers(0, 256, (N, 16), dtype=np.uint8)
+    ls = F.synth_labels(N, 12, 1, 4, 1.0, seed=PR + 1)
+    st, gs = F.label_starts(x, ls), F.global_start(x)
+    args = (x, ls.offsets, ls.labels, st, 12, R, 48, 48, 750, 32, 1.2, universal, gs)
+    rc, g, d, _ = O.filtered_build(*args)
+    assert rc == 0
+    rc, pg, pd, diag = O.filtered_build(*args, publish_R=PR)
+    assert rc == 0 and pg.shape == (N, PR)
+    want_g, want_d = publish_by_composition(x, ls, universal, g, d, R, PR, 1.2)
+    assert np.array_equal(pd, want_d)
+    assert np.array_equal(pg, want_g)
+    assert diag[7] == pd.sum() and pd.max() <= PR
+    # at or above R the publish step does nothing
+    rc, g2, d2, _ = O.filtered_build(*args, publish_R=R)
+    assert rc == 0 and np.array_equal(g2, g) and np.array_equal(d2, d)

@@ -36,11 +36,14 @@ def oracle_rows(x):
     return x.astype(np.float16) if x.dtype == np.float32 else x
 
 
-def run_both(x, ls, starts, gstart, R, L, FL, C_, steps, alpha=1.2, universal=INVALID, rounds=3):
+def run_both(x, ls, starts, gstart, R, L, FL, C_, steps, alpha=1.2, universal=INVALID, rounds=3, publish_R=0):
+    """publish_R: the DISKANN_GPU_FILTERED_PUBLISH_DEGREE the caller set (0: none)."""
     res_rc = F.build_rc(x, ls, starts, R, L, FL, C_, steps, alpha, universal, gstart, rounds,
                         graph=(g := np.empty((x.shape[0], R), np.uint32)), degree=(d := np.empty(x.shape[0], np.uint32)))
+    if 0 < publish_R < R:
+        g = g.ravel()[:x.shape[0] * publish_R].reshape(x.shape[0], publish_R)
     orc, og, od, diag = O.filtered_build(oracle_rows(x), ls.offsets, ls.labels, starts, ls.num_labels, R, L, FL, C_,
-                                         steps, alpha, universal, gstart, rounds)
+                                         steps, alpha, universal, gstart, rounds, publish_R)
     return res_rc, g, d, orc, og, od, diag
 
 
@@ -176,3 +179,34 @@ def test_filtered_abi_float_entry_matches_extension():
     b = F.filtered_build(x.astype(np.float16), ls, starts, 32, 64, 64, 750, 32, 1.2, INVALID, gs)
     assert np.array_equal(a.graph, b.graph) and np.array_equal(a.degree, b.degree)
     assert a.profile["rounds"] == 3 and a.stats["gpu_build_seconds"] > 0
+
+
+@pytest.mark.parametrize("kind,PR,hub,rounds", [("u8", 8, False, 3), ("f32", 24, True, 3), ("u8", 40, False, 3),
+                                                ("f32", 63, True, 3), ("u8", 16, False, 0)])
+def test_filtered_publish_degree(monkeypatch, kind, PR, hub, rounds):
+    # DISKANN_GPU_FILTERED_PUBLISH_DEGREE below R: the publish step
+    # (gpu_vamana_filtered.cu:6328-6432) against the oracle's
+    monkeypatch.setenv("DISKANN_GPU_FILTERED_PUBLISH_DEGREE", str(PR))
+    x, ls = make_case(kind, 3000, 64 if kind == "u8" else 96, 40, 4, seed=17, hub=hub)
+    starts, gs = F.label_starts(x, ls), F.global_start(x)
+    g, d, diag = assert_same(x, ls, starts, gs, 64, 100, 100, 750, 64, rounds=rounds, publish_R=PR)
+    assert g.shape == (3000, PR) and d.max() <= PR
+    p = F.last_profile()
+    assert p["publish_degree"] == PR and p["publish_touched"] > 0 and p["publish_ms"] > 0
+    if hub:  # the hub (in-degree > 1000 after the forward pass) takes global scratch
+        assert p["publish_long_entries"] > 1000
+    res = F.filtered_build(x, ls, starts, R=64, L=100, filtered_L=100, STEPS=64, gstart=gs, rounds=rounds)
+    assert res.graph.shape == (3000, PR) and np.array_equal(res.graph, g)
+
+
+@pytest.mark.parametrize("value", ["64", "500", "0", "-3", "abc"])
+def test_filtered_publish_degree_inactive(monkeypatch, value):
+    # values at or above R, and non-positive ones, publish the build graph as is
+    x, ls = make_case("u8", 1500, 32, 20, 3, seed=23)
+    starts, gs = F.label_starts(x, ls), F.global_start(x)
+    monkeypatch.delenv("DISKANN_GPU_FILTERED_PUBLISH_DEGREE", raising=False)
+    base = F.filtered_build(x, ls, starts, R=64, L=64, filtered_L=64, STEPS=32, gstart=gs)
+    monkeypatch.setenv("DISKANN_GPU_FILTERED_PUBLISH_DEGREE", value)
+    res = F.filtered_build(x, ls, starts, R=64, L=64, filtered_L=64, STEPS=32, gstart=gs)
+    assert res.profile["publish_degree"] == 64 and res.profile["publish_touched"] == 0
+    assert np.array_equal(res.graph, base.graph) and np.array_equal(res.degree, base.degree)
