@@ -237,9 +237,12 @@ def run_c5(args, mode) -> int:
         t1 = time.time()
         gt = label_ground_truth(torch, base_t, ls, qs, ql)
         ent = starts[ql] if mode == "c5f" else stitched["medoids"][ql]
+        # row width of the built graph: R, or the published degree when
+        # DISKANN_GPU_FILTERED_PUBLISH_DEGREE ran the publish step
+        Rg = int(F.last_profile()["publish_degree"]) if mode == "c5f" else c["R"]
         for Ls in (10, 20, 50, 100, 200):
             found, _ = D.search_resident(base_t.data_ptr(), D.DTYPE_U8, n, c["dim"], graph_t.data_ptr(),
-                                         deg_t.data_ptr(), c["R"], ent, qs, 10, Ls, ls.offsets, ls.labels, ql)
+                                         deg_t.data_ptr(), Rg, ent, qs, 10, Ls, ls.offsets, ls.labels, ql)
             recall[f"L{Ls}"] = round(D.recall_at_k(found, gt, 10), 4)
         log(f"recall {recall} ({time.time() - t1:.1f}s)")
 
@@ -264,10 +267,11 @@ def run_c5(args, mode) -> int:
                             "avg_launch_ms": round(ms / kp["rounds"], 3),
                             "algorithmic_bytes_per_launch": by / kp["rounds"]}
         line["stage_ms"] = {k: round(kp[k], 2) for k in ("backbone_ms", "task_search_ms", "row_ms", "reverse_ms",
-                                                        "csr_ms", "diagnostics_ms", "total_ms")}
+                                                        "csr_ms", "publish_ms", "diagnostics_ms", "total_ms")}
+        line["config"]["published_degree"] = kp["publish_degree"]
         line["counters"] = {k: kp[k] for k in ("task_dist", "union_dist", "work_dist", "prune_dist", "csr_dist",
                                                "csr_prune_dist", "merged_candidates", "quota_dropped",
-                                               "reverse_edges", "touched_rows", "long_lists", "long_fallbacks")}
+                                               "reverse_edges", "touched_rows", "long_lists", "long_max_candidates")}
         line["diagnostics"] = {k: st[k] for k in ("invalid_neighbor_count", "self_loop_count", "out_degree_min",
                                                   "out_degree_max", "out_degree_avg", "avg_common_label_out_degree",
                                                   "low_common_label_degree_count")}
@@ -293,8 +297,8 @@ def main() -> int:
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build targets one GPU; multi-GPU sharding is design-only "
-              "(see DESIGN.md), so --gpus must be 1.", file=sys.stderr)
+        print("bench.py: this build targets one GPU; sharding over several GPUs is a design only, "
+              "so --gpus must be 1.", file=sys.stderr)
         return 2
 
     if args.config in ("c5f", "c5s"):

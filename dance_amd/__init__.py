@@ -111,7 +111,7 @@ class DanceFilteredProfile(C.Structure):
         + [(n, C.c_uint64) for n in ("task_dist", "union_dist", "work_dist", "prune_dist", "csr_dist",
                                      "csr_prune_dist", "merged_candidates", "quota_dropped", "reverse_edges",
                                      "touched_rows", "csr_candidates", "long_lists", "out_edges",
-                                     "common_edges", "long_fallbacks")]
+                                     "common_edges", "long_max_candidates")]
         + [("publish_ms", C.c_double)]
         + [(n, C.c_uint64) for n in ("publish_dist", "publish_touched", "publish_long_entries")]
         + [("publish_degree", C.c_uint32), ("reserved0", C.c_uint32)]
@@ -535,8 +535,9 @@ def synth_u8(seed: int, stream: int, n: int, dim: int, centers: int, sigma: floa
     return out
 
 
-# BASELINE.json configs (synthetic generators of SURVEY 8(d)); stream 0 =
-# base vectors, stream 1 = queries.
+# The benchmark configurations (seeded synthetic generators: i.i.d. or
+# Gaussian-mixture rows, L2-normalised for float); stream 0 = base vectors,
+# stream 1 = queries.
 CONFIGS = {
     "c1": dict(kind="f32", n=100_000, dim=96, centers=0, sigma=1.0, nq=1_000, R=64, L=100, C=80, STEPS=64),
     "c2": dict(kind="f32", n=1_000_000, dim=96, centers=256, sigma=0.3, nq=10_000, R=64, L=100, C=80, STEPS=64),

@@ -7,7 +7,7 @@
 //   labels + postings upload -> random backbone -> task rows ->
 //   3 x (task search -> row kernel (union search, merge, quota, work
 //        distances, forward prune) -> reverse count / scan / fill ->
-//        exact CSR prune) -> [publish: shortlist + prune to PR, reverse
+//        exact CSR prune: k_csr for lists <= 256, k_csr_long above) -> [publish: shortlist + prune to PR, reverse
 //        CSR, shortlist + prune of the touched rows] -> diagnostics ->
 //        download.
 //
@@ -18,7 +18,8 @@
 //   tids, td  T x keep               task results (T = total labels)
 //   roff      N+1 u32                reverse CSR offsets; rids <= N*R sources
 //   boff      N+1 u32                scratch offsets of lists > 256 entries
-//   bd, brem  per long-list entry    distances / removed flags
+//   bd, brem, bmask  per long-list entry   distances / removed flags / label masks
+//   lrows     <= N u32               rows with long lists (k_csr_long, one workgroup each)
 // Each round reads ga and writes gb (forward), then writes ga (repaired).
 // The publish step (DISKANN_GPU_FILTERED_PUBLISH_DEGREE = PR below R) writes
 // its N x PR graph into gb / db; rows of more than 256 candidates use
@@ -110,7 +111,7 @@ int validate(const FParams& p, const uint32_t* off, const uint32_t* lab, const u
 struct FState {
   DevBuf off, lab, lab8, lpo, lpts, starts, task_rows;
   DevBuf ga, gb, da, db, tids, td;
-  DevBuf roff, cursor, rids, boff, bd, brem, bmask;
+  DevBuf roff, cursor, rids, boff, bd, brem, bmask, lrows, lcount;
   DevBuf ctr, d32, d64;
   size_t big_cap = 0;
   // the output graph: ga / da, or gb / db after the publish step
@@ -222,6 +223,8 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   DCHECK(st.cursor.alloc((size_t)N * 4));
   DCHECK(st.rids.alloc(std::max<size_t>(1, NR) * 4));
   DCHECK(st.boff.alloc((size_t)(N + 1) * 4));
+  DCHECK(st.lrows.alloc((size_t)N * 4));
+  DCHECK(st.lcount.alloc(4));
   DCHECK(st.ctr.alloc((size_t)kCtrStripes * kNumCounters * 8));
   DCHECK(st.d32.alloc(8 * 4));
   DCHECK(st.d64.alloc(8 * 8));
@@ -296,9 +299,14 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
     hipLaunchKernelGGL(k_big_sizes, dim3(grid_thr((uint64_t)N + 1)), dim3(256), 0, s, N, R, db, roff, boff);
     DHIP(hipGetLastError());
     DCHECK(scan_exclusive(boff, (size_t)N + 1, scan, s));
-    uint32_t tails[2] = {0, 0};
+    DHIP(hipMemsetAsync(st.lcount.p, 0, 4, s));
+    hipLaunchKernelGGL(k_long_rows, dim3(grid_thr(N)), dim3(256), 0, s, N, boff, st.lrows.as<uint32_t>(),
+                       st.lcount.as<uint32_t>());
+    DHIP(hipGetLastError());
+    uint32_t tails[3] = {0, 0, 0};
     DHIP(hipMemcpyAsync(&tails[0], roff + N, 4, hipMemcpyDeviceToHost, s));
     DHIP(hipMemcpyAsync(&tails[1], boff + N, 4, hipMemcpyDeviceToHost, s));
+    DHIP(hipMemcpyAsync(&tails[2], st.lcount.p, 4, hipMemcpyDeviceToHost, s));
     DHIP(hipStreamSynchronize(s));
     reverse_edges += tails[0];
     DCHECK(ensure_big(st, tails[1]));
@@ -310,6 +318,11 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
       hipLaunchKernelGGL((k_csr<decltype(dt)::value, decltype(c)::value>), dim3(grid_xcd(N)), dim3(kBlock), csr_lds,
                          s, rows.rs, Gb, Ld, Cs);
       DHIP(hipGetLastError());
+      if (tails[2] > 0) {
+        hipLaunchKernelGGL((k_csr_long<decltype(dt)::value, decltype(c)::value>), dim3(tails[2]), dim3(kLongBlock), 0,
+                           s, rows.rs, Gb, Ld, Cs, st.lrows.as<const uint32_t>());
+        DHIP(hipGetLastError());
+      }
       return 0;
     }));
     hipEvent_t r4 = E.mark(s);
@@ -390,7 +403,10 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   DHIP(hipMemcpyAsync(h64, st.d64.p, sizeof(h64), hipMemcpyDeviceToHost, s));
   DHIP(hipMemcpyAsync(stripes.data(), st.ctr.p, stripes.size() * 8, hipMemcpyDeviceToHost, s));
   DHIP(hipStreamSynchronize(s));
-  for (size_t i = 0; i < stripes.size(); ++i) hc[i % kNumCounters] += stripes[i];
+  for (size_t i = 0; i < stripes.size(); ++i) {
+    const size_t k = i % kNumCounters;
+    hc[k] = k == kBigMax ? std::max(hc[k], stripes[i]) : hc[k] + stripes[i];
+  }
 
   // Published stats follow the reference's release path (:8648-8718): search
   // counters are reported as zero there and the candidate counts are the
@@ -443,7 +459,7 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   kp.touched_rows = hc[kTouchedRows];
   kp.csr_candidates = hc[kCsrCandidates];
   kp.long_lists = hc[kBigRows];
-  kp.long_fallbacks = hc[kBigFallback];
+  kp.long_max_candidates = hc[kBigMax];
   kp.publish_ms = pub_ms;
   kp.publish_dist = hc[kPubDist];
   kp.publish_touched = hc[kPubTouched];

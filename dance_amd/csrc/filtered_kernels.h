@@ -38,12 +38,12 @@ constexpr uint32_t kCsrRegMax = 64u * kCsrSlots;
 constexpr uint32_t kRandomAttempts = 1u << 20;
 // LDS words per wave: visited cache + one distance batch (ids, distances).
 constexpr uint32_t kSearchLds = kVis + 128u;
-// Long lists are pruned on their kCsrPrefix smallest candidates first.
-constexpr uint32_t kCsrPrefix = kCsrRegMax;
-// LDS words per wave of k_csr: forward row + one distance batch + the
-// prefix staging area (ids, distances; its first 256 words double as the
-// radix-select histogram).
-constexpr uint32_t kCsrLds = 64u + 128u + 2u * kCsrPrefix;
+// LDS words per wave of k_csr: forward row + one distance batch.
+constexpr uint32_t kCsrLds = 64u + 128u;
+// Candidate lists longer than kCsrRegMax are pruned by k_csr_long, one
+// workgroup of kLongWaves waves per row.
+constexpr uint32_t kLongWaves = 16;
+constexpr uint32_t kLongBlock = 64u * kLongWaves;
 
 // Device counters (u64 each).
 enum : uint32_t {
@@ -58,7 +58,7 @@ enum : uint32_t {
   kTouchedRows,
   kCsrCandidates,
   kBigRows,
-  kBigFallback,
+  kBigMax,
   kPubDist,
   kPubTouched,
   kNumCounters
@@ -448,198 +448,6 @@ __device__ __forceinline__ uint32_t prune_regs(const RowSet& rs, const Labels& L
   return sel;
 }
 
-// The same prune over a long list in global memory: entry i belongs to lane
-// i % 64, which alone reads and writes its removed flag and distance.
-// ids(i) yields the candidate id of entry i.
-template <int DT, int CPL, typename Ids>
-__device__ __forceinline__ uint32_t prune_mem(const RowSet& rs, const Labels& L, uint32_t row, uint32_t R,
-                                              float alpha, uint32_t n, Ids&& ids, const float* d, uint8_t* rem,
-                                              uint32_t* msk, uint32_t* lst, float* lsd, uint32_t lane,
-                                              uint32_t& outv, uint32_t& ndist) {
-  const uint32_t grp = lane >> 3, sub = lane & 7u;
-  const bool use_mask = L.off[row + 1] - L.off[row] <= kMaskLabels;
-  if (use_mask)
-    for (uint32_t i = lane; i < n; i += 64) msk[i] = rem[i] ? 0u : row_mask(L, row, ids(i));
-  uint32_t sel = 0;
-  outv = DANCE_INV;
-  while (sel < R) {
-    int bk = INT_MAX;
-    uint32_t bid = DANCE_INV, bix = DANCE_INV;
-    for (uint32_t i = lane; i < n; i += 64) {
-      if (rem[i] || !(d[i] <= FLT_MAX)) continue;
-      const int k = fkey(d[i]);
-      const uint32_t c = ids(i);
-      if (k < bk || (k == bk && c < bid)) {
-        bk = k;
-        bid = c;
-        bix = i;
-      }
-    }
-    const int M = wave_min_i(bk);
-    if (M == INT_MAX) break;
-    const uint32_t I = wave_min_u(bk == M ? bid : DANCE_INV);
-    const uint32_t X = wave_min_u(bk == M && bid == I ? bix : DANCE_INV);
-    const bool own = lane == (X & 63u);
-    const uint32_t msel = use_mask ? rdlane_u(own ? msk[X] : 0u, (int)(X & 63u)) : 0u;
-    if (lane == sel) outv = I;
-    if (own) rem[X] = 1;
-    ++sel;
-    uint4 bv[CPL];
-    load_row<CPL>(rs, I, true, sub, bv);
-    for (uint32_t b = 0; b < n; b += 64) {
-      const uint32_t i = b + lane;
-      const bool live = i < n && !rem[i];
-      const uint32_t c = live ? ids(i) : DANCE_INV;
-      const bool need = live && (use_mask ? (msk[i] & ~msel) == 0u : covers(L, row, I, c));
-      const uint64_t m = wballot(need);
-      if (!m) continue;
-      const uint32_t cnt = popc64(m), pos = mbcnt64(m);
-      if (need) lst[pos] = c;
-      wave_sync();
-      batch_dist<DT, CPL>(rs, bv, lst, lsd, cnt, grp, sub);
-      ndist += cnt;
-      if (need) {
-        const float pd = lsd[pos];
-        if (pd > 0.0f && alpha * pd <= d[i]) rem[i] = 1;
-      }
-      wave_sync();
-    }
-  }
-  return sel;
-}
-
-// Selection key of a live entry: distance bits (order-preserving for
-// non-negative floats), then id. Entries that can never be selected
-// (distance NaN or above FLT_MAX) get the largest key.
-__device__ __forceinline__ uint64_t prune_key(float d, uint32_t id) {
-  return d <= FLT_MAX ? (((uint64_t)(uint32_t)fkey(d) << 32) | id) : ~0ull;
-}
-
-// Inclusive prefix sum over the wave.
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, uint32_t lane) {
-#pragma unroll
-  for (uint32_t o = 1; o < 64; o <<= 1) {
-    const uint32_t u = (uint32_t)__shfl_up((int)v, (int)o, 64);
-    if (lane >= o) v += u;
-  }
-  return v;
-}
-
-// FilteredRobustPrune of a long list (prune_mem's contract) that first runs
-// on the kCsrPrefix entries with the smallest keys. Each round selects the
-// smallest live key, so while the prefix still has a selectable entry every
-// selection and every removal decision equals the full prune's; when the
-// prefix runs out before R selections and entries outside it remain, the
-// full prune_mem runs instead (counted in kBigFallback). Keys are unique
-// (live ids are unique), so the prefix is an exact radix select on the
-// 64-bit key, 8 bits per pass.
-template <int DT, int CPL, typename Ids>
-__device__ __forceinline__ uint32_t prune_long(const RowSet& rs, const Labels& L, uint32_t row, uint32_t R,
-                                               float alpha, uint32_t n, Ids&& ids, const float* d, uint8_t* rem,
-                                               uint32_t* msk, uint32_t* lst, float* lsd, uint32_t* stage,
-                                               uint32_t lane, uint32_t& outv, uint32_t& ndist, bool& fallback) {
-  fallback = false;
-  auto key_at = [&](uint32_t i) -> uint64_t { return rem[i] ? ~0ull : prune_key(d[i], ids(i)); };
-  uint32_t total = 0;
-  for (uint32_t b = 0; b < n; b += 64) {
-    const uint32_t i = b + lane;
-    total += popc64(wballot(i < n && key_at(i) != ~0ull));
-  }
-  // Radix select: after the loop, the prefix is every key whose top
-  // (64 - shift) bits are <= pre (the kCsrPrefix smallest, or all).
-  uint64_t pre = ~0ull;
-  int shift = 0;
-  if (total > kCsrPrefix) {
-    uint32_t need = kCsrPrefix;
-    uint64_t acc = 0;
-    shift = 64;
-    uint32_t* hist = stage;
-    while (true) {
-      shift -= 8;
-      for (uint32_t j = lane; j < 256; j += 64) hist[j] = 0u;
-      wave_sync();
-      for (uint32_t b = 0; b < n; b += 64) {
-        const uint32_t i = b + lane;
-        const uint64_t k = i < n ? key_at(i) : ~0ull;
-        const bool match = k != ~0ull && (shift == 56 || (k >> (shift + 8)) == acc);
-        if (match) atomicAdd(&hist[(uint32_t)(k >> shift) & 255u], 1u);
-      }
-      wave_sync();
-      uint32_t c[4], sum = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        c[j] = hist[lane * 4 + j];
-        sum += c[j];
-      }
-      const uint32_t incl = wave_incl_scan(sum, lane);
-      uint32_t before = incl - sum;
-      uint32_t digit = 0, below = 0, cnt = 0;
-      bool found = false;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bool cross = !found && before < need && before + c[j] >= need;
-        if (cross) {
-          digit = lane * 4 + j;
-          below = before;
-          cnt = c[j];
-          found = true;
-        }
-        before += c[j];
-      }
-      const uint64_t fm = wballot(found);
-      if (!fm) {  // cannot happen with unique keys; stay exact regardless
-        fallback = true;
-        return prune_mem<DT, CPL>(rs, L, row, R, alpha, n, ids, d, rem, msk, lst, lsd, lane, outv, ndist);
-      }
-      const int fl = ffs64(fm);
-      digit = rdlane_u(digit, fl);
-      below = rdlane_u(below, fl);
-      cnt = rdlane_u(cnt, fl);
-      wave_sync();
-      need -= below;
-      acc = (acc << 8) | digit;
-      if (cnt == need || shift == 0) break;
-    }
-    pre = acc;
-  }
-  // Stage the prefix (ids, distances) in LDS, then one entry per slot.
-  uint32_t* sid = stage;
-  float* sdd = reinterpret_cast<float*>(stage + kCsrPrefix);
-  uint32_t np = 0;
-  for (uint32_t b = 0; b < n; b += 64) {
-    const uint32_t i = b + lane;
-    const uint64_t k = i < n ? key_at(i) : ~0ull;
-    const bool in = k != ~0ull && (shift == 64 ? true : (k >> shift) <= pre);
-    const uint64_t m = wballot(in);
-    const uint32_t p = np + mbcnt64(m);
-    if (in && p < kCsrPrefix) {
-      sid[p] = (uint32_t)k;
-      sdd[p] = d[i];
-    }
-    np += popc64(m);
-  }
-  wave_sync();
-  if (np > kCsrPrefix) {  // only with repeated keys, which live lists do not have
-    fallback = true;
-    return prune_mem<DT, CPL>(rs, L, row, R, alpha, n, ids, d, rem, msk, lst, lsd, lane, outv, ndist);
-  }
-  uint32_t pid[kCsrSlots];
-  float pdist[kCsrSlots];
-  uint32_t prem = 0;
-#pragma unroll
-  for (int e = 0; e < (int)kCsrSlots; ++e) {
-    const uint32_t p = (uint32_t)e * 64u + lane;
-    pid[e] = p < np ? sid[p] : DANCE_INV;
-    pdist[e] = p < np ? sdd[p] : FLT_MAX;
-    if (p >= np) prem |= 1u << e;
-  }
-  wave_sync();
-  const uint32_t sel = prune_regs<DT, CPL, (int)kCsrSlots>(rs, L, row, R, alpha, pid, pdist, prem, lst, lsd, lane,
-                                                            outv, ndist);
-  if (sel >= R || total <= np) return sel;
-  fallback = true;
-  return prune_mem<DT, CPL>(rs, L, row, R, alpha, n, ids, d, rem, msk, lst, lsd, lane, outv, ndist);
-}
 
 // ---------------------------------------------------------------------------
 // Kernels.
@@ -997,7 +805,8 @@ struct CsrArgs {
 // row. The candidate list is the forward row followed by the reverse sources
 // not already in it; entry i is the i-th of that concatenation (duplicates
 // are marked removed instead of compacted away, so live ids stay unique and
-// the selection is unchanged). Rows without reverse sources keep their row.
+// the selection is unchanged). Rows without reverse sources keep their row;
+// rows of more than kCsrRegMax candidates are left to k_csr_long.
 template <int DT, int CPL>
 __global__ __launch_bounds__(kBlock) void k_csr(RowSet rs, Graph G, Labels L, CsrArgs A) {
   extern __shared__ uint32_t smem[];
@@ -1013,80 +822,50 @@ __global__ __launch_bounds__(kBlock) void k_csr(RowSet rs, Graph G, Labels L, Cs
     if (lane == 0) A.dout[row] = G.d[row];
     return;
   }
+  const uint32_t deg = min(G.d[row], R);
+  const uint32_t n = deg + (s1 - s0);
+  if (n > kCsrRegMax) return;
   uint32_t* fw = smem + w * kCsrLds;
   uint32_t* lst = fw + 64;
   float* lsd = reinterpret_cast<float*>(fw + 128);
-  uint32_t* stage = fw + 192;
-  const uint32_t deg = min(G.d[row], R);
   fw[lane] = lane < deg ? G.g[gb + lane] : DANCE_INV;
   wave_sync();
   const uint32_t grp = lane >> 3, sub = lane & 7u;
   uint4 av[CPL];
   load_row<CPL>(rs, row, true, sub, av);
-  const uint32_t n = deg + (s1 - s0);
   const uint32_t* rids = A.rids + s0;
-  auto id_at = [&](uint32_t i) -> uint32_t { return i < deg ? fw[i] : rids[i - deg]; };
-  auto live = [&](uint32_t i, uint32_t c) -> bool {
-    if (i < deg) return true;
-    if (c >= N || c == row) return false;
-    for (uint32_t j = 0; j < deg; ++j)
-      if (fw[j] == c) return false;
-    return true;
-  };
-  uint32_t nd = 0, npd = 0, nlive = 0, outv, sel;
-  bool fell_back = false;
-  if (n <= kCsrRegMax) {
-    uint32_t id[kCsrSlots];
-    float d[kCsrSlots];
-    uint32_t rem = 0;
+  uint32_t nd = 0, npd = 0, outv;
+  uint32_t id[kCsrSlots];
+  float d[kCsrSlots];
+  uint32_t rem = 0;
 #pragma unroll
-    for (int e = 0; e < (int)kCsrSlots; ++e) {
-      const uint32_t i = (uint32_t)e * 64u + lane;
-      const uint32_t c = i < n ? id_at(i) : DANCE_INV;
-      const bool ok = i < n && live(i, c);
-      id[e] = c;
-      d[e] = FLT_MAX;
-      if (!ok) rem |= 1u << e;
-      const uint64_t m = wballot(ok);
-      if (m) {
-        const uint32_t cnt = popc64(m), pos = mbcnt64(m);
-        if (ok) lst[pos] = c;
-        wave_sync();
-        batch_dist<DT, CPL>(rs, av, lst, lsd, cnt, grp, sub);
-        nd += cnt;
-        nlive += cnt;
-        if (ok) d[e] = lsd[pos];
-        wave_sync();
-      }
+  for (int e = 0; e < (int)kCsrSlots; ++e) {
+    const uint32_t i = (uint32_t)e * 64u + lane;
+    uint32_t c = DANCE_INV;
+    bool ok = false;
+    if (i < deg) {
+      c = fw[i];
+      ok = true;
+    } else if (i < n) {
+      c = rids[i - deg];
+      ok = c < N && c != row;
+      for (uint32_t j = 0; ok && j < deg; ++j) ok = fw[j] != c;
     }
-    sel = prune_regs<DT, CPL, (int)kCsrSlots>(rs, L, row, R, A.alpha, id, d, rem, lst, lsd, lane, outv, npd);
-  } else {
-    const uint32_t base = A.boff[row];
-    float* bd = A.bd + base;
-    uint8_t* brem = A.brem + base;
-    uint32_t* bmask = A.bmask + base;
-    for (uint32_t b = 0; b < n; b += 64) {
-      const uint32_t i = b + lane;
-      const uint32_t c = i < n ? id_at(i) : DANCE_INV;
-      const bool ok = i < n && live(i, c);
-      if (i < n) {
-        brem[i] = ok ? 0 : 1;
-        bd[i] = FLT_MAX;
-      }
-      const uint64_t m = wballot(ok);
-      if (!m) continue;
+    id[e] = c;
+    d[e] = FLT_MAX;
+    if (!ok) rem |= 1u << e;
+    const uint64_t m = wballot(ok);
+    if (m) {
       const uint32_t cnt = popc64(m), pos = mbcnt64(m);
       if (ok) lst[pos] = c;
       wave_sync();
       batch_dist<DT, CPL>(rs, av, lst, lsd, cnt, grp, sub);
       nd += cnt;
-      nlive += cnt;
-      if (ok) bd[i] = lsd[pos];
+      if (ok) d[e] = lsd[pos];
       wave_sync();
     }
-    sel = prune_long<DT, CPL>(rs, L, row, R, A.alpha, n, id_at, bd, brem, bmask, lst, lsd, stage, lane, outv, npd,
-                              fell_back);
   }
+  const uint32_t sel = prune_regs<DT, CPL, (int)kCsrSlots>(rs, L, row, R, A.alpha, id, d, rem, lst, lsd, lane, outv, npd);
   if (lane < R) A.gout[gb + lane] = lane < sel ? outv : DANCE_INV;
   if (lane == 0) {
     A.dout[row] = sel;
@@ -1094,9 +873,159 @@ __global__ __launch_bounds__(kBlock) void k_csr(RowSet rs, Graph G, Labels L, Cs
       atomicAdd(ctr_at(A.ctr, kCsrDist), (unsigned long long)nd);
       atomicAdd(ctr_at(A.ctr, kCsrPruneDist), (unsigned long long)npd);
       atomicAdd(ctr_at(A.ctr, kTouchedRows), 1ull);
-      atomicAdd(ctr_at(A.ctr, kCsrCandidates), (unsigned long long)nlive);
-      if (n > kCsrRegMax) atomicAdd(ctr_at(A.ctr, kBigRows), 1ull);
-      if (fell_back) atomicAdd(ctr_at(A.ctr, kBigFallback), 1ull);
+      atomicAdd(ctr_at(A.ctr, kCsrCandidates), (unsigned long long)nd);
+    }
+  }
+}
+
+// Rows whose candidate list is longer than kCsrRegMax (k_big_sizes gave them
+// scratch); the order of the list does not matter.
+static __global__ void k_long_rows(uint32_t N, const uint32_t* boff, uint32_t* list, uint32_t* count) {
+  const uint32_t row = blockIdx.x * blockDim.x + threadIdx.x;
+  if (row < N && boff[row + 1] > boff[row]) list[atomicAdd(count, 1u)] = row;
+}
+
+// k_csr for one long row per workgroup: the candidate list (same entries as
+// k_csr) is distanced by all kLongWaves waves into the row's scratch (bd
+// distances, brem removed flags, bmask row-label masks), then
+// FilteredRobustPrune runs over it: each selection is the smallest live
+// (distance, id, index), reduced over the waves through LDS, and every wave
+// applies the occlusion rule to its own entries. Entry i belongs to wave
+// (i / 64) % kLongWaves, lane i % 64, which alone writes its scratch after
+// the distance pass.
+template <int DT, int CPL>
+__global__ __launch_bounds__(kLongBlock) void k_csr_long(RowSet rs, Graph G, Labels L, CsrArgs A,
+                                                          const uint32_t* rows) {
+  __shared__ uint32_t fw[64];
+  __shared__ uint32_t wl[kLongWaves][64];
+  __shared__ float wd[kLongWaves][64];
+  __shared__ int rk[kLongWaves];
+  __shared__ uint32_t ri[kLongWaves], rx[kLongWaves];
+  __shared__ uint32_t out[64];
+  const uint32_t row = rows[blockIdx.x];
+  const uint32_t w = wave_index(), lane = lane_id();
+  const uint32_t grp = lane >> 3, sub = lane & 7u;
+  const uint32_t N = G.N, R = G.R;
+  const size_t gb = (size_t)row * R;
+  const uint32_t s0 = A.roff[row], s1 = A.roff[row + 1];
+  const uint32_t deg = min(G.d[row], R);
+  const uint32_t n = deg + (s1 - s0);
+  if (w == 0) fw[lane] = lane < deg ? G.g[gb + lane] : DANCE_INV;
+  __syncthreads();
+  const uint32_t base = A.boff[row];
+  float* bd = A.bd + base;
+  uint8_t* brem = A.brem + base;
+  uint32_t* bmask = A.bmask + base;
+  const uint32_t* rids = A.rids + s0;
+  uint32_t* lst = wl[w];
+  float* lsd = wd[w];
+  auto id_at = [&](uint32_t i) -> uint32_t { return i < deg ? fw[i] : rids[i - deg]; };
+  const bool use_mask = L.off[row + 1] - L.off[row] <= kMaskLabels;
+  constexpr uint32_t kStride = 64u * kLongWaves;
+  uint32_t nd = 0, npd = 0;
+  {
+    uint4 av[CPL];
+    load_row<CPL>(rs, row, true, sub, av);
+    for (uint32_t b = w * 64u; b < n; b += kStride) {
+      const uint32_t i = b + lane;
+      uint32_t c = DANCE_INV;
+      bool ok = false;
+      if (i < deg) {
+        c = fw[i];
+        ok = true;
+      } else if (i < n) {
+        c = rids[i - deg];
+        ok = c < N && c != row;
+        for (uint32_t j = 0; ok && j < deg; ++j) ok = fw[j] != c;
+      }
+      float dist = FLT_MAX;
+      const uint64_t m = wballot(ok);
+      if (m) {
+        const uint32_t cnt = popc64(m), pos = mbcnt64(m);
+        if (ok) lst[pos] = c;
+        wave_sync();
+        batch_dist<DT, CPL>(rs, av, lst, lsd, cnt, grp, sub);
+        nd += cnt;
+        if (ok) dist = lsd[pos];
+        wave_sync();
+      }
+      if (i < n) {
+        brem[i] = ok ? 0 : 1;
+        bd[i] = dist;
+        bmask[i] = ok && use_mask ? row_mask(L, row, c) : 0u;
+      }
+    }
+  }
+  uint32_t sel = 0;
+  while (sel < R) {
+    int bk = INT_MAX;
+    uint32_t bid = DANCE_INV, bix = DANCE_INV;
+    for (uint32_t b = w * 64u; b < n; b += kStride) {
+      const uint32_t i = b + lane;
+      if (i >= n || brem[i] || !(bd[i] <= FLT_MAX)) continue;
+      const int k = fkey(bd[i]);
+      const uint32_t c = id_at(i);
+      if (k < bk || (k == bk && c < bid)) {  // entries ascend per lane: ties keep the first
+        bk = k;
+        bid = c;
+        bix = i;
+      }
+    }
+    const int M = wave_min_i(bk);
+    const uint32_t I = wave_min_u(bk == M ? bid : DANCE_INV);
+    const uint32_t X = wave_min_u(bk == M && bid == I ? bix : DANCE_INV);
+    if (lane == 0) {
+      rk[w] = M;
+      ri[w] = I;
+      rx[w] = X;
+    }
+    __syncthreads();
+    const int mk = lane < kLongWaves ? rk[lane] : INT_MAX;
+    const uint32_t mi = lane < kLongWaves ? ri[lane] : DANCE_INV;
+    const uint32_t mx = lane < kLongWaves ? rx[lane] : DANCE_INV;
+    __syncthreads();  // rk / ri / rx are rewritten by the next selection
+    const int GM = wave_min_i(mk);
+    if (GM == INT_MAX) break;
+    const uint32_t GI = wave_min_u(mk == GM ? mi : DANCE_INV);
+    const uint32_t GX = wave_min_u(mk == GM && mi == GI ? mx : DANCE_INV);
+    const uint32_t msel = use_mask ? bmask[GX] : 0u;
+    if (w == 0 && lane == 0) out[sel] = GI;
+    if (w == ((GX >> 6) % kLongWaves) && lane == (GX & 63u)) brem[GX] = 1;
+    ++sel;
+    uint4 bv[CPL];
+    load_row<CPL>(rs, GI, true, sub, bv);
+    for (uint32_t b = w * 64u; b < n; b += kStride) {
+      const uint32_t i = b + lane;
+      const bool live = i < n && !brem[i];
+      const uint32_t c = live ? id_at(i) : DANCE_INV;
+      const bool need = live && (use_mask ? (bmask[i] & ~msel) == 0u : covers(L, row, GI, c));
+      const uint64_t m = wballot(need);
+      if (!m) continue;
+      const uint32_t cnt = popc64(m), pos = mbcnt64(m);
+      if (need) lst[pos] = c;
+      wave_sync();
+      batch_dist<DT, CPL>(rs, bv, lst, lsd, cnt, grp, sub);
+      npd += cnt;
+      if (need) {
+        const float pd = lsd[pos];
+        if (pd > 0.0f && A.alpha * pd <= bd[i]) brem[i] = 1;
+      }
+      wave_sync();
+    }
+  }
+  __syncthreads();
+  if (w == 0) {
+    if (lane < R) A.gout[gb + lane] = lane < sel ? out[lane] : DANCE_INV;
+    if (lane == 0) A.dout[row] = sel;
+  }
+  if (A.ctr && lane == 0) {
+    atomicAdd(ctr_at(A.ctr, kCsrDist), (unsigned long long)nd);
+    atomicAdd(ctr_at(A.ctr, kCsrPruneDist), (unsigned long long)npd);
+    atomicAdd(ctr_at(A.ctr, kCsrCandidates), (unsigned long long)nd);
+    if (w == 0) {
+      atomicAdd(ctr_at(A.ctr, kTouchedRows), 1ull);
+      atomicAdd(ctr_at(A.ctr, kBigRows), 1ull);
+      atomicMax(ctr_at(A.ctr, kBigMax), (unsigned long long)n);
     }
   }
 }

@@ -73,8 +73,8 @@ typedef struct DanceFilteredProfile {
     uint64_t task_dist, union_dist, work_dist, prune_dist, csr_dist, csr_prune_dist;
     uint64_t merged_candidates, quota_dropped, reverse_edges, touched_rows, csr_candidates, long_lists;
     uint64_t out_edges, common_edges;
-    /* long CSR lists whose prune needed more than their 256 smallest candidates */
-    uint64_t long_fallbacks;
+    /* largest CSR candidate list of a row (long lists: over 256 candidates) */
+    uint64_t long_max_candidates;
     /* publish step (DISKANN_GPU_FILTERED_PUBLISH_DEGREE below R): kernel time,
      * distances, rows rebuilt from reverse sources, scratch entries of lists
      * over 256 candidates; publish_degree is the output graph's row width */

@@ -135,23 +135,23 @@ def test_filtered_hub_long_reverse_lists():
 
 
 @pytest.mark.parametrize("alpha", [0.5, 1.2, 3.0])
-def test_filtered_hub_prefix_prune(alpha):
-    """Long lists are pruned on their 256 smallest candidates first; alpha 0.5
-    occludes so much that the prefix runs out and the full prune runs. A block
-    of identical vectors gives tied distances and zero pair distances."""
+def test_filtered_hub_long_prune(alpha):
+    """Long lists are pruned by one workgroup per row (selection reduced over
+    the waves); alpha 0.5 occludes so much that selections reach deep into
+    the list. A block of identical vectors gives tied distances and zero pair
+    distances."""
     x, ls = make_case("f32", 3000, 64, 40, 3, seed=25, hub=True)
     x[100:400] = x[100]
     starts, gs = F.label_starts(x, ls), F.global_start(x)
     assert_same(x, ls, starts, gs, 32, 64, 64, 750, 32, alpha=alpha, rounds=1)
     p = F.last_profile()
-    assert p["long_lists"] > 0
-    assert p["long_fallbacks"] < p["long_lists"]
+    assert p["long_lists"] > 0 and p["long_max_candidates"] > 256
 
 
-def test_filtered_hub_prefix_exhausted():
+def test_filtered_hub_deep_selection():
     """One shared label makes every pair coverable, so alpha 0.5 occludes
-    about half the sphere per selection: the hub's 256-entry prefix runs out
-    before R selections and the full prune takes over."""
+    about half the sphere per selection: the hub's selections run past its
+    256 nearest candidates."""
     rng = np.random.default_rng(27)
     x = rng.standard_normal((3000, 64)).astype(np.float32)
     x /= np.linalg.norm(x, axis=1, keepdims=True)
@@ -160,7 +160,8 @@ def test_filtered_hub_prefix_exhausted():
     starts, gs = F.label_starts(x, ls), F.global_start(x)
     assert_same(x, ls, starts, gs, 32, 64, 64, 750, 32, alpha=0.5, rounds=1)
     p = F.last_profile()
-    assert p["long_lists"] > 0 and p["long_fallbacks"] > 0
+    assert p["long_lists"] > 0
+    assert p["long_max_candidates"] > 2048  # the hub's entries wrap around the workgroup's 16 waves
 
 
 @pytest.mark.parametrize("n", [1, 2, 17, 50])
