@@ -144,6 +144,7 @@ EXPORTS = [
     "dance_filtered_build", "dance_filtered_build_resident", "dance_get_last_filtered_profile",
     "dance_search", "dance_search_resident", "dance_get_last_search_stats",
     "dance_merge_shards", "dance_merge_get_last_stats", "dance_struct_sizes",
+    "dance_partition_assign",
 ]
 
 class DanceMergeStats(C.Structure):

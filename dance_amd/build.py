@@ -27,9 +27,10 @@ HIP_FLAGS = [
 ]
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-pthread", "-Wall", "-Wextra", "-Wno-unused-parameter"]
 
-HIP_SOURCES = ["vnew2_build.hip", "filtered_build.hip", "query_search.hip", "merge_shards.hip"]
+HIP_SOURCES = ["vnew2_build.hip", "filtered_build.hip", "query_search.hip", "merge_shards.hip", "partition.hip"]
 HOST_SOURCES = ["synth.cpp"]
-APP_SOURCES = ["gpu_vamana_memory_index.cpp", "gpu_stitched_vamana_index.cpp", "build_memory_index.cpp"]
+APP_SOURCES = ["gpu_vamana_memory_index.cpp", "gpu_stitched_vamana_index.cpp", "build_memory_index.cpp",
+               "build_sharded_index.cpp"]
 
 
 def _run(cmd: list[str]) -> None:

@@ -236,9 +236,23 @@ inline int setup_rows(Rows& out, const void* src, bool src_on_device, int src_dt
   }
   DCHECK(out.owned.alloc(stride * N));
   if (src_dtype == store_dtype) {
-    if (stride != row_bytes) DHIP(hipMemsetAsync(out.owned.p, 0, stride * N, s));
-    DHIP(hipMemcpy2DAsync(out.owned.p, stride, src, row_bytes, row_bytes, N,
+    if (stride == row_bytes) {
+      DHIP(hipMemcpyAsync(out.owned.p, src, row_bytes * N,
                           src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, s));
+    } else {
+      // Pitched copies from pageable host memory go row by row (6 s for
+      // 250 MB measured): upload contiguously, then pad on the device.
+      DevBuf tmp;
+      const void* dsrc = src;
+      if (!src_on_device) {
+        DCHECK(tmp.alloc(row_bytes * N));
+        DHIP(hipMemcpyAsync(tmp.p, src, row_bytes * N, hipMemcpyHostToDevice, s));
+        dsrc = tmp.p;
+      }
+      DHIP(hipMemsetAsync(out.owned.p, 0, stride * N, s));
+      DHIP(hipMemcpy2DAsync(out.owned.p, stride, dsrc, row_bytes, row_bytes, N, hipMemcpyDeviceToDevice, s));
+      DHIP(hipStreamSynchronize(s));  // tmp is freed on return
+    }
   } else {
     // fp32 input stored as fp16 (FAST_SMALL): upload, convert on device.
     DevBuf tmp;

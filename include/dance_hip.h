@@ -164,6 +164,19 @@ int dance_merge_shards(const char *vamana_prefix, const char *vamana_suffix, con
 
 void dance_merge_get_last_stats(DanceMergeStats *stats);
 
+/* Shard assignment of the sharded build (DiskANN's
+ * shard_data_into_clusters_only_ids and its k-means assignment step, upstream
+ * partition.cpp, called from build_merged_vamana_index,
+ * integrations/dance-diskann-78256bba.patch:1212-1260): for each of
+ * num_points host rows (dtype DANCE_DTYPE_F32 or DANCE_DTYPE_U8, dim <= 255)
+ * the k_base (1..min(8, num_centers)) nearest of num_centers fp32 centers,
+ * nearest first, into h_assign (num_points x k_base). Distances are squared
+ * L2 accumulated in fp64 in dimension order (fma per dimension); ties go to
+ * the lower center index; a point whose distances are all NaN gets
+ * 0xFFFFFFFF. Returns 0, or -1 on invalid arguments or a HIP error. */
+int dance_partition_assign(const void *h_data, int dtype, uint64_t num_points, uint32_t dim, const float *h_centers,
+                           uint32_t num_centers, uint32_t k_base, uint32_t *h_assign);
+
 /* Sizes in bytes of the structs this library fills, in the order
  * GPUVamanaStats, DanceKernelProfile, GPUFilteredVamanaStats,
  * DanceFilteredProfile, DanceSearchStats, DanceMergeStats; writes

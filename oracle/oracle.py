@@ -130,6 +130,8 @@ def lib() -> C.CDLL:
         L.oracle_edge_hash.restype = u32
         L.oracle_merge_shards.argtypes = [C.c_char_p] * 4 + [u64, u32] + [C.c_char_p] * 2 + [u64, C.POINTER(u64)]
         L.oracle_merge_shards.restype = i32
+        L.oracle_partition_assign.argtypes = [vp, i32, u64, u32, C.POINTER(C.c_float), u32, u32, C.POINTER(u32)]
+        L.oracle_partition_assign.restype = None
         L.oracle_num_threads.argtypes = []
         L.oracle_num_threads.restype = i32
         _LIB = L
@@ -409,3 +411,14 @@ def filtered_shortlist(offsets, labels, num_labels: int, universal: int, R: int,
                                         num_labels, universal, row, _p(ids), _p(ds, C.c_float), int(ids.shape[0]),
                                         _p(oi), _p(od, C.c_float))
     return oi[:n], od[:n]
+
+
+def partition_assign(data: np.ndarray, centers: np.ndarray, k_base: int) -> np.ndarray:
+    """Each row's k_base nearest centers (fp64 squared L2 in dimension order,
+    ties to the lower center); returns N x k_base uint32."""
+    data = np.ascontiguousarray(data)
+    centers = np.ascontiguousarray(centers, np.float32)
+    out = np.empty((data.shape[0], k_base), np.uint32)
+    lib().oracle_partition_assign(data.ctypes.data, 0 if data.dtype == np.float32 else 1, data.shape[0],
+                                  data.shape[1], _p(centers, C.c_float), centers.shape[0], k_base, _p(out))
+    return out
