@@ -111,7 +111,7 @@ int validate(const FParams& p, const uint32_t* off, const uint32_t* lab, const u
 struct FState {
   DevBuf off, lab, lab8, lpo, lpts, starts, task_rows;
   DevBuf ga, gb, da, db, tids, td;
-  DevBuf roff, cursor, rids, boff, bd, brem, bmask, lrows, lcount;
+  DevBuf roff, cursor, rids, boff, bd, brem, bmask, lrows, lsort, lcount;
   DevBuf ctr, d32, d64;
   size_t big_cap = 0;
   // the output graph: ga / da, or gb / db after the publish step
@@ -224,6 +224,7 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   DCHECK(st.rids.alloc(std::max<size_t>(1, NR) * 4));
   DCHECK(st.boff.alloc((size_t)(N + 1) * 4));
   DCHECK(st.lrows.alloc((size_t)N * 4));
+  DCHECK(st.lsort.alloc((size_t)N * 12));  // keys (2 buffers) + a second value buffer
   DCHECK(st.lcount.alloc(4));
   DCHECK(st.ctr.alloc((size_t)kCtrStripes * kNumCounters * 8));
   DCHECK(st.d32.alloc(8 * 4));
@@ -231,6 +232,7 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   DHIP(hipMemsetAsync(st.ctr.p, 0, (size_t)kCtrStripes * kNumCounters * 8, s));
   unsigned long long* ctr = st.ctr.as<unsigned long long>();
   ScanWorkspace scan;
+  SortWorkspace sort_ws;
 
   // Fixed-width label rows for membership tests (DANCE_FILTERED_LAB8=0: list walks only).
   const char* l8e = std::getenv("DANCE_FILTERED_LAB8");
@@ -300,7 +302,9 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
     DHIP(hipGetLastError());
     DCHECK(scan_exclusive(boff, (size_t)N + 1, scan, s));
     DHIP(hipMemsetAsync(st.lcount.p, 0, 4, s));
-    hipLaunchKernelGGL(k_long_rows, dim3(grid_thr(N)), dim3(256), 0, s, N, boff, st.lrows.as<uint32_t>(),
+    uint32_t* lkeys[2] = {st.lsort.as<uint32_t>(), st.lsort.as<uint32_t>() + N};
+    uint32_t* lvals[2] = {st.lrows.as<uint32_t>(), st.lsort.as<uint32_t>() + 2 * (size_t)N};
+    hipLaunchKernelGGL(k_long_rows, dim3(grid_thr(N)), dim3(256), 0, s, N, boff, lvals[0], lkeys[0],
                        st.lcount.as<uint32_t>());
     DHIP(hipGetLastError());
     uint32_t tails[3] = {0, 0, 0};
@@ -310,6 +314,8 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
     DHIP(hipStreamSynchronize(s));
     reverse_edges += tails[0];
     DCHECK(ensure_big(st, tails[1]));
+    int lr = 0;  // long rows, longest first
+    if (tails[2] > 1) DCHECK(radix_sort_pairs(lkeys, lvals, tails[2], 32, sort_ws, s, &lr));
     hipEvent_t r3 = E.mark(s);
     const Graph Gb{N, R, gb, db};
     CsrArgs Cs{p.alpha, roff, st.rids.as<const uint32_t>(), boff, st.bd.as<float>(), st.brem.as<uint8_t>(),
@@ -320,7 +326,7 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
       DHIP(hipGetLastError());
       if (tails[2] > 0) {
         hipLaunchKernelGGL((k_csr_long<decltype(dt)::value, decltype(c)::value>), dim3(tails[2]), dim3(kLongBlock), 0,
-                           s, rows.rs, Gb, Ld, Cs, st.lrows.as<const uint32_t>());
+                           s, rows.rs, Gb, Ld, Cs, lvals[lr]);
         DHIP(hipGetLastError());
       }
       return 0;

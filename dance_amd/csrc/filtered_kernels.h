@@ -879,10 +879,14 @@ __global__ __launch_bounds__(kBlock) void k_csr(RowSet rs, Graph G, Labels L, Cs
 }
 
 // Rows whose candidate list is longer than kCsrRegMax (k_big_sizes gave them
-// scratch); the order of the list does not matter.
-static __global__ void k_long_rows(uint32_t N, const uint32_t* boff, uint32_t* list, uint32_t* count) {
+// scratch), with the sort key ~length, so that an ascending sort puts the
+// longest lists (the slowest workgroups) first.
+static __global__ void k_long_rows(uint32_t N, const uint32_t* boff, uint32_t* list, uint32_t* key, uint32_t* count) {
   const uint32_t row = blockIdx.x * blockDim.x + threadIdx.x;
-  if (row < N && boff[row + 1] > boff[row]) list[atomicAdd(count, 1u)] = row;
+  if (row >= N || boff[row + 1] == boff[row]) return;
+  const uint32_t pos = atomicAdd(count, 1u);
+  list[pos] = row;
+  key[pos] = ~(boff[row + 1] - boff[row]);
 }
 
 // k_csr for one long row per workgroup: the candidate list (same entries as
@@ -956,21 +960,25 @@ __global__ __launch_bounds__(kLongBlock) void k_csr_long(RowSet rs, Graph G, Lab
       }
     }
   }
+  // Each lane tracks the smallest live (distance, id, index) of its own
+  // entries; entries ascend per lane, so ties keep the first.
+  int bk = INT_MAX;
+  uint32_t bid = DANCE_INV, bix = DANCE_INV;
+  auto consider = [&](float d, uint32_t c, uint32_t i) {
+    if (!(d <= FLT_MAX)) return;
+    const int k = fkey(d);
+    if (k < bk || (k == bk && c < bid)) {
+      bk = k;
+      bid = c;
+      bix = i;
+    }
+  };
+  for (uint32_t b = w * 64u; b < n; b += kStride) {
+    const uint32_t i = b + lane;
+    if (i < n && !brem[i]) consider(bd[i], id_at(i), i);
+  }
   uint32_t sel = 0;
   while (sel < R) {
-    int bk = INT_MAX;
-    uint32_t bid = DANCE_INV, bix = DANCE_INV;
-    for (uint32_t b = w * 64u; b < n; b += kStride) {
-      const uint32_t i = b + lane;
-      if (i >= n || brem[i] || !(bd[i] <= FLT_MAX)) continue;
-      const int k = fkey(bd[i]);
-      const uint32_t c = id_at(i);
-      if (k < bk || (k == bk && c < bid)) {  // entries ascend per lane: ties keep the first
-        bk = k;
-        bid = c;
-        bix = i;
-      }
-    }
     const int M = wave_min_i(bk);
     const uint32_t I = wave_min_u(bk == M ? bid : DANCE_INV);
     const uint32_t X = wave_min_u(bk == M && bid == I ? bix : DANCE_INV);
@@ -991,26 +999,35 @@ __global__ __launch_bounds__(kLongBlock) void k_csr_long(RowSet rs, Graph G, Lab
     const uint32_t msel = use_mask ? bmask[GX] : 0u;
     if (w == 0 && lane == 0) out[sel] = GI;
     if (w == ((GX >> 6) % kLongWaves) && lane == (GX & 63u)) brem[GX] = 1;
-    ++sel;
+    if (++sel == R) break;  // removals after the last selection change nothing
+    // one pass per selection: the occlusion rule on this lane's entries,
+    // then the survivors' minimum for the next selection
     uint4 bv[CPL];
     load_row<CPL>(rs, GI, true, sub, bv);
+    bk = INT_MAX;
+    bid = bix = DANCE_INV;
     for (uint32_t b = w * 64u; b < n; b += kStride) {
       const uint32_t i = b + lane;
-      const bool live = i < n && !brem[i];
+      bool live = i < n && !brem[i];
       const uint32_t c = live ? id_at(i) : DANCE_INV;
       const bool need = live && (use_mask ? (bmask[i] & ~msel) == 0u : covers(L, row, GI, c));
       const uint64_t m = wballot(need);
-      if (!m) continue;
-      const uint32_t cnt = popc64(m), pos = mbcnt64(m);
-      if (need) lst[pos] = c;
-      wave_sync();
-      batch_dist<DT, CPL>(rs, bv, lst, lsd, cnt, grp, sub);
-      npd += cnt;
-      if (need) {
-        const float pd = lsd[pos];
-        if (pd > 0.0f && A.alpha * pd <= bd[i]) brem[i] = 1;
+      if (m) {
+        const uint32_t cnt = popc64(m), pos = mbcnt64(m);
+        if (need) lst[pos] = c;
+        wave_sync();
+        batch_dist<DT, CPL>(rs, bv, lst, lsd, cnt, grp, sub);
+        npd += cnt;
+        if (need) {
+          const float pd = lsd[pos];
+          if (pd > 0.0f && A.alpha * pd <= bd[i]) {
+            brem[i] = 1;
+            live = false;
+          }
+        }
+        wave_sync();
       }
-      wave_sync();
+      if (live) consider(bd[i], c, i);
     }
   }
   __syncthreads();

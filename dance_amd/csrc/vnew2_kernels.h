@@ -348,7 +348,8 @@ struct SearchWave {
 #pragma unroll
       for (uint32_t u = 0; u < kQInFlight; ++u)
         keep |= (uint64_t)octet_bits(wballot(sub == 0 && p + 8 * u + grp < n && !rej[u])) << (p + 8 * u);
-    }    const uint32_t nk = popc64(keep);
+    }
+    const uint32_t nk = popc64(keep);
     n_bchk += n;
     n_bskip += n - nk;
     if (nk < n) {
