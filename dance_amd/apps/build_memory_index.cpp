@@ -28,7 +28,9 @@
 //      exceeds max_degree the library's publish step prunes the graph to
 //      max_degree (DISKANN_GPU_FILTERED_PUBLISH_DEGREE is set to max_degree,
 //      and unset otherwise) (patch:20368-20398);
-//   4. install: per row drop invalid / self / repeated ids, an empty row of a
+//   4. with DISKANN_GPU_FILTERED_RESELECT_LABEL_STARTS=common_degree, label
+//      starts are reselected from the raw graph (patch:20447-20504);
+//      install: per row drop invalid / self / repeated ids, an empty row of a
 //      multi-point index gets (i + 1) mod N (patch:20506-20521);
 //   5. save: <prefix> (graph: u64 file bytes, u32 max degree, u32 start,
 //      u64 frozen 0, rows), <prefix>.data, <prefix>_labels.txt,
@@ -330,6 +332,45 @@ int run(const Options& o) {
             << " invalid_neighbor_count=" << st.invalid_neighbor_count
             << " self_loop_count=" << st.self_loop_count << std::endl;
   const double t_build = now_sec();
+
+  // DISKANN_GPU_FILTERED_RESELECT_LABEL_STARTS=common_degree (patch:20447-20504):
+  // each label's start becomes the carrier with the most neighbours carrying
+  // the label (or the universal label) in the raw graph, then the larger raw
+  // degree, then the lower id. Labels without a carrier keep their start.
+  const char* reselect = std::getenv("DISKANN_GPU_FILTERED_RESELECT_LABEL_STARTS");
+  if (reselect && std::string(reselect) == "common_degree") {
+    auto has = [&](uint32_t p, uint32_t label) {
+      return std::binary_search(lb.ids.begin() + lb.offsets[p], lb.ids.begin() + lb.offsets[p + 1], label);
+    };
+    const size_t nl = starts.size();
+    std::vector<uint32_t> best(nl, kInvalid), best_common(nl, 0), best_out(nl, 0);
+    for (uint32_t node = 0; node < n; ++node)
+      for (uint32_t q = lb.offsets[node]; q < lb.offsets[node + 1]; ++q) {
+        const uint32_t label = lb.ids[q];
+        if (label == lb.universal || label >= nl) continue;
+        uint32_t common = 0;
+        for (uint32_t j = 0; j < degree[node] && j < R; ++j) {
+          const uint32_t nb = graph[(size_t)node * R + j];
+          if (nb < n && nb != node && (has(nb, label) || (lb.universal != kInvalid && has(nb, lb.universal))))
+            ++common;
+        }
+        if (best[label] == kInvalid || common > best_common[label] ||
+            (common == best_common[label] && degree[node] > best_out[label])) {
+          best[label] = node;
+          best_common[label] = common;
+          best_out[label] = degree[node];
+        }
+      }
+    uint32_t reselected = 0, changed = 0;
+    for (size_t l = 0; l < nl; ++l)
+      if (best[l] != kInvalid) {
+        ++reselected;
+        changed += starts[l] != best[l];
+        starts[l] = best[l];
+      }
+    std::cout << "[GPU filtered] reselected label starts mode=common_degree labels=" << reselected
+              << " changed=" << changed << std::endl;
+  }
 
   // Install (patch:20506-20521) and save.
   std::string body;

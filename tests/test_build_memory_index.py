@@ -171,3 +171,56 @@ def test_app_matches_oracle(tmp_path, kind, universal_every, R):
         want.append(row)
     assert [list(map(int, a)) for a in adj] == want
     assert max_deg == max(len(w) for w in want)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind,universal_every,R", [("uint8", 0, 64), ("uint8", 7, 32)])
+def test_reselected_label_starts(tmp_path, kind, universal_every, R):
+    # DISKANN_GPU_FILTERED_RESELECT_LABEL_STARTS=common_degree (patch:20447-20504):
+    # per label, the carrier with the most raw-graph neighbours carrying the
+    # label or the universal label, then the larger raw degree, then the lower id
+    x, rows, dp, lp = make_case(tmp_path, kind=kind, universal_every=universal_every, seed=9)
+    prefix = str(tmp_path / "idx")
+    args = base_args(dp, lp, prefix, kind) + (["--universal_label", "ANY"] if universal_every else [])
+    env = {k: v for k, v in os.environ.items() if not k.startswith("DISKANN_GPU_FILTERED_")}
+    env["DISKANN_GPU_FILTERED_RESELECT_LABEL_STARTS"] = "common_degree"
+    r = run_app(*args, "--max_degree", str(R), env=env)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "reselected label starts mode=common_degree" in r.stdout
+    n = x.shape[0]
+    ids, per_row = expected_ids(rows, "ANY" if universal_every else None)
+    canon = [sorted(set(rw)) for rw in per_row]
+    num_labels = max(ids.values()) + 1
+    universal = 0 if universal_every else INV
+    starts = np.full(num_labels, INV, np.uint32)
+    for lab in range(num_labels):
+        carriers = np.array([i for i in range(n) if lab in canon[i]], np.int64)
+        if carriers.size:
+            starts[lab] = centroid_start(x, carriers)
+    _, _, start, _ = formats.read_graph(prefix)
+    ls = F.canonical_labels(canon, num_labels)
+    rc, g, deg, _ = O.filtered_build(x, ls.offsets, ls.labels, starts, num_labels, R=64, L=100, filtered_L=100,
+                                     C_=750, STEPS=64, alpha=1.2, universal=universal, global_start=start,
+                                     publish_R=R if R < 64 else 0)
+    assert rc == 0
+    sets = [set(c) for c in canon]
+    want = dict(enumerate(starts.tolist()))
+    best = {}
+    for node in range(n):
+        for lab in canon[node]:
+            if lab == universal:
+                continue
+            common = sum(1 for j in range(min(int(deg[node]), R))
+                         if int(g[node, j]) < n and int(g[node, j]) != node
+                         and (lab in sets[int(g[node, j])] or universal in sets[int(g[node, j])]))
+            b = best.get(lab)
+            if b is None or common > b[1] or (common == b[1] and int(deg[node]) > b[2]):
+                best[lab] = (node, common, int(deg[node]))
+    for lab, (node, _, _) in best.items():
+        want[lab] = node
+    got = {}
+    with open(prefix + "_labels_to_medoids.txt") as f:
+        for line in f:
+            a, b = line.split(",")
+            got[int(a)] = int(b)
+    assert got == {k: v for k, v in want.items() if v != INV}
