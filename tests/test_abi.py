@@ -103,6 +103,19 @@ def test_parameter_errors_return_minus_one():
     assert lib.dance_set_profile(b"NOPE") == -1
 
 
+def test_partition_assign_errors_before_device():
+    from dance_amd import partition as P
+    x = np.zeros((10, 8), np.float32)
+    c = np.zeros((4, 8), np.float32)
+    assert P.assign_rc(x, c, 0)[0] == -1            # k_base 0
+    assert P.assign_rc(x, c, 5)[0] == -1            # k_base > centers
+    assert P.assign_rc(x, np.zeros((20, 8), np.float32), 9)[0] == -1  # k_base > 8
+    assert P.assign_rc(np.zeros((10, 256), np.float32), np.zeros((4, 256), np.float32), 2)[0] == -1  # dim > 255
+    assert P.assign_rc(np.zeros((0, 8), np.float32), c, 2)[0] == 0  # no points: nothing to do
+    with pytest.raises(TypeError):
+        P.assign_rc(x.astype(np.float64), c, 1)
+
+
 def test_filtered_parameter_errors():
     """Filtered ABI: -1 for null pointers, zero sizes, C < R and malformed
     label offsets; 1 when min(C, 128) < 2R (reference
