@@ -238,27 +238,33 @@ struct RegPool {
 
   // insert() for a pool with size >= L and max_pos >= 0 (which every path
   // below preserves) and a valid candidate id.
+  // The slot registers are updated by selects on one straight path (no
+  // branch around them), so the compiler keeps them in place instead of
+  // copying them at every join; only the max recomputation is a (uniform)
+  // branch.
   __device__ __forceinline__ void insert_full(uint32_t nid, float nd, uint32_t lane) {
     max_pos = uni_i(max_pos);
     max_d = uni_f(max_d);
-    if (!(nd < max_d)) return;  // a NaN distance changes nothing in insert() either
     int same = -1;
 #pragma unroll
+    for (int r = PS - 1; r >= 0; --r) {
+      const uint64_t m = wballot(id[r] == nid);
+      same = m ? r * 64 + ffs64(m) : same;  // the lowest register wins
+    }
+    same = uni_i(same);
+    // a NaN distance changes nothing in insert() either
+    const bool write = nd < max_d && (same < 0 || nd < get_d(same));
+    const int pos = same >= 0 ? same : max_pos;
+    const int mk = pool_mkey(nd), sk = pool_skey(mk);
+    const bool hit = write && (int)lane == (pos & 63);
+#pragma unroll
     for (int r = 0; r < PS; ++r) {
-      if (same < 0) {
-        const uint64_t m = wballot(id[r] == nid);
-        if (m) same = r * 64 + ffs64(m);
-      }
+      const bool h = hit && r == (pos >> 6);
+      id[r] = h ? nid : id[r];  // a duplicate keeps its id
+      mkey[r] = h ? mk : mkey[r];
+      skey[r] = h ? sk : skey[r];
     }
-    if (same >= 0) {
-      if (nd < get_d(same)) {
-        set_d(same, nd, lane);
-        if (same == max_pos) recompute_max();
-      }
-      return;
-    }
-    set_slot(max_pos, nid, nd, lane);
-    recompute_max();
+    if (write && pos == max_pos) recompute_max();
   }
 
   // select_next_unexpanded_size_warp: smallest distance among unexpanded
