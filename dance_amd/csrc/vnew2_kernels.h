@@ -206,32 +206,33 @@ struct RegPool {
     if (size >= L && max_pos >= 0 && nd >= max_d) return;
     int same = -1;
 #pragma unroll
+    for (int r = PS - 1; r >= 0; --r) {
+      const uint64_t m = wballot(id[r] == nid);
+      same = m ? r * 64 + ffs64(m) : same;  // the lowest register wins
+    }
+    same = uni_i(same);
+    // One of: refresh a duplicate's distance, append, replace the worst.
+    // The slot registers change by selects on one path (see insert_full).
+    const bool refresh = same >= 0 && nd < get_d(same);
+    const bool append = same < 0 && size < L;
+    const bool replace = same < 0 && size >= L && max_pos >= 0 && nd < max_d;
+    const int pos = same >= 0 ? same : (append ? (int)size : max_pos);
+    const int mk = pool_mkey(nd), sk = pool_skey(mk);
+    const bool hit = (refresh || append || replace) && (int)lane == (pos & 63);
+#pragma unroll
     for (int r = 0; r < PS; ++r) {
-      if (same < 0) {
-        const uint64_t m = wballot(id[r] == nid);
-        if (m) same = r * 64 + ffs64(m);
-      }
+      const bool h = hit && r == (pos >> 6);
+      id[r] = h ? nid : id[r];  // a duplicate keeps its id
+      mkey[r] = h ? mk : mkey[r];
+      skey[r] = h ? sk : skey[r];
     }
-    if (same >= 0) {
-      const float cd = get_d(same);
-      if (nd < cd) {
-        set_d(same, nd, lane);
-        if (same == max_pos) recompute_max();
-      }
-      return;
-    }
-    if (size < L) {
-      const int pos = (int)size;
-      set_slot(pos, nid, nd, lane);
+    if (append) {
       size = uni_u(size + 1u);
       if (max_pos < 0 || nd > max_d) {
         max_pos = uni_i(pos);
         max_d = uni_f(nd);
       }
-      return;
-    }
-    if (max_pos >= 0 && nd < max_d) {
-      set_slot(max_pos, nid, nd, lane);
+    } else if (replace || (refresh && same == max_pos)) {
       recompute_max();
     }
   }
