@@ -763,19 +763,19 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
   wave_sync();
   uint32_t oc = 0, npair = 0, nbchk = 0, nbskip = 0;
   for (uint32_t round = 0; round < R; ++round) {
+    // smallest distance, lowest index on ties: each lane keeps its first
+    // entry of its smallest key (entries ascend per lane)
     int best = INT_MAX;
+    uint32_t cand = 0xFFFFFFFFu;
     for (uint32_t i = lane; i < Cp; i += 64) {
-      const bool ok = (fl[i] & PR_REMOVED) == 0u && sid[i] != DANCE_INV;
-      if (ok) best = min(best, fkey(sd[i]));
+      const int k = fkey(sd[i]);
+      const bool ok = (fl[i] & PR_REMOVED) == 0u && sid[i] != DANCE_INV && k < best;
+      best = ok ? k : best;
+      cand = ok ? i : cand;
     }
     const int M = wave_min_i(best);
     if (M == INT_MAX) break;
-    uint32_t cand = 0xFFFFFFFFu;
-    for (uint32_t i = lane; i < Cp; i += 64) {
-      const bool ok = (fl[i] & PR_REMOVED) == 0u && sid[i] != DANCE_INV && fkey(sd[i]) == M;
-      if (ok) cand = min(cand, i);
-    }
-    const uint32_t pos = wave_min_u(cand);
+    const uint32_t pos = wave_min_u(best == M ? cand : 0xFFFFFFFFu);
     const uint32_t sel = uni_u(sid[pos]);
     const float seld = uni_f(sd[pos]);
     if (lane == 0) {
