@@ -258,35 +258,22 @@ struct CanonPool {
     wd = __int_as_float(M);
     wid = W;
   }
+  // One of: refresh a duplicate's distance, append, replace the worst. The
+  // slot registers change by selects on one path, so the compiler does not
+  // copy them at branch joins; only the worst recomputation branches.
   __device__ __forceinline__ void insert(uint32_t nid, float nd, uint32_t lane) {
     const uint64_t dm = wballot(lane < count && id == nid);
-    bool changed = false;
-    if (dm) {
-      const int p = ffs64(dm);
-      if (nd < rdlane_f(d, p)) {
-        if ((int)lane == p) {
-          d = nd;
-          ex = 0;
-        }
-        changed = true;
-      }
-    } else if (count < cap) {
-      if (lane == count) {
-        id = nid;
-        d = nd;
-        ex = 0;
-      }
-      ++count;
-      changed = true;
-    } else if (wpos >= 0 && (nd < wd || (nd == wd && nid < wid))) {
-      if ((int)lane == wpos) {
-        id = nid;
-        d = nd;
-        ex = 0;
-      }
-      changed = true;
-    }
-    if (changed) recompute_worst(lane);
+    const int dup = dm ? ffs64(dm) : -1;
+    const bool refresh = dm != 0 && nd < rdlane_f(d, dup & 63);
+    const bool append = dm == 0 && count < cap;
+    const bool replace = dm == 0 && count >= cap && wpos >= 0 && (nd < wd || (nd == wd && nid < wid));
+    const int pos = dm ? dup : (append ? (int)count : wpos);
+    const bool hit = (refresh || append || replace) && (int)lane == pos;
+    id = hit ? nid : id;  // a duplicate keeps its id
+    d = hit ? nd : d;
+    ex = hit ? 0u : ex;
+    count += append ? 1u : 0u;
+    if (refresh || append || replace) recompute_worst(lane);
   }
   // True when (nd, nid) is certainly rejected: the pool is full and the pair
   // is not below the worst entry (which only falls while the pool is full).
