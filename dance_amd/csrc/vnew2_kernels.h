@@ -246,6 +246,7 @@ struct RegPool {
   __device__ __forceinline__ void insert_full(uint32_t nid, float nd, uint32_t lane) {
     max_pos = uni_i(max_pos);
     max_d = uni_f(max_d);
+    if (!(nd < max_d)) return;  // uniform; a NaN distance changes nothing either
     int same = -1;
 #pragma unroll
     for (int r = PS - 1; r >= 0; --r) {
@@ -253,8 +254,7 @@ struct RegPool {
       same = m ? r * 64 + ffs64(m) : same;  // the lowest register wins
     }
     same = uni_i(same);
-    // a NaN distance changes nothing in insert() either
-    const bool write = nd < max_d && (same < 0 || nd < get_d(same));
+    const bool write = same < 0 || nd < get_d(same);
     const int pos = same >= 0 ? same : max_pos;
     const int mk = pool_mkey(nd), sk = pool_skey(mk);
     const bool hit = write && (int)lane == (pos & 63);
