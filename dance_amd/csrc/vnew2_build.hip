@@ -363,6 +363,16 @@ static float elapsed_ms(hipEvent_t a, hipEvent_t b) {
   return 0.f;
 }
 
+// Rows wider than the widest compiled chunk group (16 chunks of 16 bytes per
+// lane of an octet) are rejected before any device call.
+static int check_width(uint32_t dim, int store) {
+  if (pick_cpl((uint32_t)(((uint64_t)dim * elem_bytes(store) + 15) / 16)) < 0) {
+    std::fprintf(stderr, "[gpu_vamana_build] dim=%u is beyond the supported row width\n", dim);
+    return -1;
+  }
+  return 0;
+}
+
 static int validate(uint32_t N, uint32_t dim, uint32_t R, uint32_t L, uint32_t C, uint32_t& STEPS) {
   if (N == 0 || dim == 0 || R == 0 || L == 0 || C == 0 || STEPS == 0) {
     std::fprintf(stderr, "[gpu_vamana_build] invalid parameters: N=%u dim=%u R=%u L=%u C=%u STEPS=%u\n", N, dim, R, L,
@@ -563,6 +573,7 @@ static int build_host(const HostT* h_data, int src_dtype, uint32_t N, uint32_t d
   DCHECK(validate(N, dim, R, L, C, STEPS));
   const Profile prof = kProfiles[profile_index_locked()];
   const int store = (src_dtype == DANCE_F32 && prof.fp16) ? DANCE_F16 : src_dtype;
+  DCHECK(check_width(dim, store));
   hipStream_t s = nullptr;
   DHIP(hipStreamCreate(&s));
   struct StreamGuard {
@@ -790,6 +801,7 @@ int dance_vamana_build_resident(const void* d_data, int dtype, uint32_t N, uint3
   const double t0 = now_sec();
   const Profile prof = kProfiles[profile_index_locked()];
   const int store = (dtype == DANCE_F32 && prof.fp16) ? DANCE_F16 : dtype;
+  DCHECK(check_width(dim, store));
   hipStream_t s = nullptr;
   DHIP(hipStreamCreate(&s));
   struct StreamGuard {

@@ -101,6 +101,11 @@ def test_parameter_errors_return_minus_one():
     assert lib.gpu_vamana_vnew2_build_float(x.ctypes.data, 16, 8, 8, 16, 8, 8, None, dp) == -1
     assert lib.dance_vamana_build_resident(None, 0, 16, 8, 8, 16, 8, 8, None, None) == -1
     assert lib.dance_set_profile(b"NOPE") == -1
+    # rows wider than 16 chunks of 16 bytes per lane are rejected before any device call
+    wide = np.zeros((16, 513), np.float32)
+    gw = np.zeros((16, 8), np.uint32)
+    assert lib.gpu_vamana_vnew2_build_float(wide.ctypes.data, 16, 513, 8, 16, 8, 8,
+                                            gw.ctypes.data_as(u32p), dp) == -1
 
 
 def test_partition_assign_errors_before_device():

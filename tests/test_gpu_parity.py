@@ -69,7 +69,9 @@ def assert_state_equal(g, s, fields=("cur", "deg_cur", "work", "deg_work", "wd")
 
 
 @pytest.mark.parametrize("kind,dim", [("f32", 96), ("f32", 100), ("f32", 7), ("u8", 128), ("u8", 192),
-                                      ("u8", 33), ("f16", 96), ("f16", 50)])
+                                      ("u8", 33), ("f16", 96), ("f16", 50),
+                                      # the widest rows of each type (16 chunks per lane)
+                                      ("f32", 512), ("u8", 2048), ("f16", 1024), ("f32", 260)])
 def test_distances_bitwise(kind, dim):
     data = make_data(kind, 3000, dim, seed=dim)
     rng = np.random.default_rng(1)
@@ -172,6 +174,18 @@ def test_end_to_end_graph_identical(kind, n, R, L, C, steps):
     data = make_data(kind, n, dim, seed=17)
     res = D.vamana_build(data, R, L, C, steps)
     og, od, om = O.vnew2_build(data, R, L, C, steps)
+    assert res.medoid == om
+    assert np.array_equal(res.degree, od)
+    assert np.array_equal(res.graph, og)
+
+
+@pytest.mark.parametrize("kind,dim", [("f32", 512), ("u8", 2048), ("f32", 200)])
+def test_end_to_end_wide_rows(kind, dim):
+    # the widest supported rows (16 chunks of 16 bytes per lane) and a width
+    # whose last chunk group is partial
+    data = make_data(kind, 1500, dim, seed=dim)
+    res = D.vamana_build(data, 32, 48, 40, 24)
+    og, od, om = O.vnew2_build(data, 32, 48, 40, 24)
     assert res.medoid == om
     assert np.array_equal(res.degree, od)
     assert np.array_equal(res.graph, og)
