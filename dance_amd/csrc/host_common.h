@@ -224,8 +224,13 @@ inline int setup_rows(Rows& out, const void* src, bool src_on_device, int src_dt
   out.N = N;
   out.dim = dim;
   const size_t row_bytes = (size_t)dim * elem_bytes(store_dtype);
-  const size_t stride = (row_bytes + 15) / 16 * 16;
-  const uint32_t nch = (uint32_t)(stride / 16);
+  // Rows are padded with zeros to the compiled chunk group (8 lanes x CPL
+  // chunks of 16 bytes), so every chunk slot of a row holds data and row
+  // loads need no per-chunk bounds test; zeros add nothing to a distance.
+  const uint32_t data_chunks = (uint32_t)((row_bytes + 15) / 16);
+  const int cpl = pick_cpl(data_chunks);
+  const uint32_t nch = cpl > 0 ? 8u * (uint32_t)cpl : data_chunks;
+  const size_t stride = (size_t)nch * 16;
   out.rs.stride16 = nch;
   out.rs.nch = nch;
   const size_t src_row_bytes = (size_t)dim * elem_bytes(src_dtype);

@@ -129,17 +129,20 @@ struct RowSet {
   uint32_t nch;       // chunks that hold data (ceil(dim * elem_bytes / 16))
 };
 
+// Chunks sub, sub + 8, ... of row `id`. Rows are padded with zeros to the
+// chunk group (nch == 8 CPL, see setup_rows), so every slot holds data. An
+// inactive lane loads nothing and v keeps whatever it held (callers pass
+// freshly declared arrays): `active` is the same on the 8 lanes of an octet,
+// so inactive values only reach the distances of inactive candidates, which
+// every caller discards. Leaving them unset spares the 4 zeroing moves per
+// chunk that a defined value costs in front of each masked load.
 template <int CPL>
 __device__ __forceinline__ void load_row(const RowSet& rs, uint32_t id, bool active, uint32_t sub,
                                          uint4 (&v)[CPL]) {
   const uint4* p = rs.rows + (size_t)id * rs.stride16;
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
-    const uint32_t cc = sub + 8u * (uint32_t)c;
-    if (active && cc < rs.nch)
-      v[c] = p[cc];
-    else
-      v[c] = make_uint4(0u, 0u, 0u, 0u);
+    if (active) v[c] = p[sub + 8u * (uint32_t)c];
   }
 }
 
