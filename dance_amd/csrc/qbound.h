@@ -153,9 +153,13 @@ __device__ __forceinline__ float q_threshold(const QBoundSet& qb, const QSelf& m
   return uni_f((__builtin_sqrtf(t) + me.r) * (1.0f + kQSlack));
 }
 
-// Chunk `sub` of the code row of candidate `id` (zero when inactive).
+// Chunk `sub` of the code row of candidate `id`. An inactive lane loads
+// nothing and the value is left unset (as in load_row): `active` is the same
+// on the 8 lanes of an octet and q_proves_reject returns false for it.
 __device__ __forceinline__ uint4 q_load(const QBoundSet& qb, uint32_t id, bool active, uint32_t sub) {
-  return active ? qb.rows[(size_t)id * kQChunks + sub] : make_uint4(0u, 0u, 0u, 0u);
+  uint4 b;
+  if (active) b = qb.rows[(size_t)id * kQChunks + sub];
+  return b;
 }
 
 // Octet test for a candidate: every lane of the octet holds one chunk `b` of
