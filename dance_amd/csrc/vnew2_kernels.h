@@ -389,8 +389,8 @@ struct SearchWave {
     n_search += nx;
     const uint64_t t1 = dclock();
     c_dist += t1 - t0;
-    const uint32_t ck = lane < nx ? lst[lane] : DANCE_INV;
-    const float dk = lane < nx ? lsd[lane] : FLT_MAX;
+    const uint32_t ck = lst[lane];  // read only where lane < nx (keep below)
+    const float dk = lsd[lane];
     bool keep = lane < nx;
     if (full) keep = keep && dk < P.max_d;
     uint64_t km = wballot(keep);

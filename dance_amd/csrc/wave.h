@@ -233,7 +233,8 @@ __device__ __forceinline__ int fkey(float d) { return __float_as_int(d); }
 
 // Distances from a cached vector `av` to up to 64 ids lst[0..n) -> lsd[0..n).
 // Two passes of 8 octets are kept in flight (one for a last group of <= 8).
-// Returns after lsd is visible.
+// lst holds 64 entries; every index read stays below 64. Returns after lsd
+// is visible.
 template <int DT, int CPL>
 __device__ __forceinline__ void batch_dist(const RowSet& rs, const uint4 (&av)[CPL], const uint32_t* lst,
                                            float* lsd, uint32_t n, uint32_t grp, uint32_t sub) {
@@ -241,7 +242,7 @@ __device__ __forceinline__ void batch_dist(const RowSet& rs, const uint4 (&av)[C
   for (; p + 8 < n; p += 16) {
     const uint32_t k0 = p + grp, k1 = p + 8 + grp;
     const bool a0 = k0 < n, a1 = k1 < n;
-    const uint32_t id0 = a0 ? lst[k0] : 0u, id1 = a1 ? lst[k1] : 0u;
+    const uint32_t id0 = lst[k0], id1 = lst[k1];  // k0, k1 < 64: in bounds; inactive ids are not loaded
     uint4 b0[CPL], b1[CPL];
     load_row<CPL>(rs, id0, a0, sub, b0);
     load_row<CPL>(rs, id1, a1, sub, b1);
@@ -256,7 +257,7 @@ __device__ __forceinline__ void batch_dist(const RowSet& rs, const uint4 (&av)[C
     const uint32_t k0 = p + grp;
     const bool a0 = k0 < n;
     uint4 b0[CPL];
-    load_row<CPL>(rs, a0 ? lst[k0] : 0u, a0, sub, b0);
+    load_row<CPL>(rs, lst[k0], a0, sub, b0);
     const float d0 = octet_finish<DT, CPL>(av, b0);
     if (sub == 0 && a0) lsd[k0] = d0;
   }
