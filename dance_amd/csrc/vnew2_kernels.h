@@ -346,7 +346,7 @@ struct SearchWave {
 #pragma unroll
       for (uint32_t u = 0; u < kQInFlight; ++u) {
         const uint32_t k = p + 8 * u + grp;
-        b[u] = q_load(a.qb, k < n ? lst[k] : 0u, k < n, sub);
+        b[u] = q_load(a.qb, lst[k], k < n, sub);  // k < 64 (p steps by 8 kQInFlight, which divides 64)
       }
       bool rej[kQInFlight];
 #pragma unroll
@@ -360,7 +360,7 @@ struct SearchWave {
     n_bchk += n;
     n_bskip += n - nk;
     if (nk < n) {
-      const uint32_t ck = lane < n ? lst[lane] : 0u;
+      const uint32_t ck = lst[lane];
       wave_sync();
       if ((keep >> lane) & 1ull) lst[mbcnt64(keep)] = ck;
       wave_sync();
