@@ -758,6 +758,7 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
     sid[i] = id;
     sd[i] = dist;
     fl[i] = f;
+    lst[i] = 0u;  // every entry a valid index, so lst reads need no guard
     if (qon) sroot[i] = prune_bound_root(a.qb, dist, a.alpha);
   }
   wave_sync();
@@ -815,8 +816,8 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
 #pragma unroll
           for (uint32_t u = 0; u < kQInFlight; ++u) {
             const uint32_t k = p + 8 * u + grp;
-            si[u] = k < nb ? lst[base + k] : 0u;
-            b[u] = q_load(a.qb, k < nb ? sid[si[u]] : 0u, k < nb, sub);
+            si[u] = lst[min(base + k, Cp - 1u)];
+            b[u] = q_load(a.qb, sid[si[u]], k < nb, sub);
           }
 #pragma unroll
           for (uint32_t u = 0; u < kQInFlight; ++u) {
@@ -843,10 +844,10 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
     for (uint32_t p = 0; p < nq; p += 16) {
       const uint32_t k0 = p + grp, k1 = p + 8 + grp;
       const bool a0 = k0 < nq, a1 = k1 < nq;
-      const uint32_t s0 = a0 ? lst[k0] : 0u, s1 = a1 ? lst[k1] : 0u;
+      const uint32_t s0 = lst[min(k0, Cp - 1u)], s1 = lst[min(k1, Cp - 1u)];
       uint4 b0[CPL], b1[CPL];
-      load_row<CPL>(a.rs, a0 ? sid[s0] : 0u, a0, sub, b0);
-      load_row<CPL>(a.rs, a1 ? sid[s1] : 0u, a1, sub, b1);
+      load_row<CPL>(a.rs, sid[s0], a0, sub, b0);
+      load_row<CPL>(a.rs, sid[s1], a1, sub, b1);
       const float d0 = octet_finish<DT, CPL>(sv, b0);
       const float d1 = octet_finish<DT, CPL>(sv, b1);
       if (sub == 0) {
