@@ -146,6 +146,22 @@ def label_ground_truth(torch, base_t, ls, queries, qlabels, k=10):
     return out
 
 
+def copy_calibration(torch, dev, mib):
+    """One device copy of known size before the build, so that a counter run
+    (FETCH_SIZE / WRITE_SIZE) can scale its readings by what the counters
+    report for the copy."""
+    if mib <= 0:
+        return
+    nbytes = mib << 20
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy calibration: {nbytes} bytes read + {nbytes} bytes written")
+    del src, dst
+
+
 def run_c5(args, mode) -> int:
     import torch
     import dance_amd as D
@@ -215,6 +231,7 @@ def run_c5(args, mode) -> int:
         stitched["medoids"] = medoids
 
     step = step_filtered if mode == "c5f" else step_stitched
+    copy_calibration(torch, dev, args.copy_calibration_mib)
     for i in range(args.warmup):
         step()
         log(f"warmup {i + 1}/{args.warmup} done")
@@ -266,6 +283,12 @@ def run_c5(args, mode) -> int:
                             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
                             "avg_launch_ms": round(ms / kp["rounds"], 3),
                             "algorithmic_bytes_per_launch": by / kp["rounds"]}
+        traffic_file = os.path.join(ROOT, "profiles", "traffic_c5f.json")
+        if os.path.exists(traffic_file) and args.n is None:
+            with open(traffic_file) as f:
+                tj = json.load(f)
+            if tj.get("kernel") == name:
+                line["roofline"]["traffic"] = tj.get("hbm_bytes_per_launch")
         line["stage_ms"] = {k: round(kp[k], 2) for k in ("backbone_ms", "task_search_ms", "row_ms", "reverse_ms",
                                                         "csr_ms", "publish_ms", "diagnostics_ms", "total_ms")}
         line["config"]["published_degree"] = kp["publish_degree"]
@@ -324,15 +347,7 @@ def main() -> int:
         D.vamana_build_resident(base_t.data_ptr(), dcode, n, cfg["dim"], cfg["R"], cfg["L"], cfg["C"],
                                 cfg["STEPS"], graph_t.data_ptr(), deg_t.data_ptr())
 
-    if args.copy_calibration_mib > 0:
-        nbytes = args.copy_calibration_mib << 20
-        src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        log(f"copy calibration: {nbytes} bytes read + {nbytes} bytes written")
-        del src, dst
+    copy_calibration(torch, dev, args.copy_calibration_mib)
     for i in range(args.warmup):
         step()
         log(f"warmup {i + 1}/{args.warmup} done")
