@@ -233,6 +233,7 @@ inline int setup_rows(Rows& out, const void* src, bool src_on_device, int src_dt
   const size_t stride = (size_t)nch * 16;
   out.rs.stride16 = nch;
   out.rs.nch = nch;
+  out.rs.tail16 = (store_dtype == DANCE_F16 && (dim & 1u)) ? (int32_t)((dim - 1u) / 2u) : -1;
   const size_t src_row_bytes = (size_t)dim * elem_bytes(src_dtype);
   if (src_dtype == store_dtype && src_on_device && stride == row_bytes &&
       (reinterpret_cast<uintptr_t>(src) & 15u) == 0) {

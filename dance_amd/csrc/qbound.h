@@ -11,10 +11,14 @@
 //
 // The canonical fp32 distance (fmaf per lane over n_lane non-negative terms,
 // then the three-level octet tree) satisfies dist >= D (1 - u)^(n_lane + 5)
-// - eta, with D the exact squared distance, u = 2^-24 and eta an underflow
-// slack, so D >= (T + 1e-30)(1 + kappa2), kappa2 = 2 (n_lane + 8) u, proves
-// dist >= T. That holds when Q >= (sqrt((T + 1e-30)(1 + kappa2)) + r_x +
-// r_y)^2. The test is evaluated in fp32 with explicit slack factors 2^-19,
+// - 1e-30, with D the exact squared distance, u = 2^-24 and 1e-30 an
+// underflow slack, so D >= (T + eta)(1 + kappa2), kappa2 = 2 (n_lane + 8) u,
+// eta = 1e-30, proves dist >= T. The fp16 distance rounds each difference and
+// square to binary16 (unit 2^-11): a term t^2 becomes at least
+// t^2 (1 - 3 2^-11) - 2^-24 (the absolute part covers the subnormal range),
+// so for fp16 rows kappa2 = 2 (3 2^-11 + (n_lane + 8) u) and
+// eta = 1e-30 + dim 2^-24. The test holds when Q >= (sqrt((T + eta)
+// (1 + kappa2)) + r_x + r_y)^2. The test is evaluated in fp32 with explicit slack factors 2^-19,
 // 32 times the accumulated rounding (|Q_computed - Q| <= 6 u (a_x + a_y),
 // since 2 s_x s_y |c| <= a_x + a_y). A candidate proved this way would be
 // rejected by the pool's threshold test, so skipping its exact distance
@@ -32,7 +36,8 @@ constexpr float kQSlack = 0x1p-19f;
 
 struct QBoundSet {
   const uint4* rows;  // N x kQChunks chunks; nullptr disables the bound
-  float kappa2;       // 2 (n_lane + 8) 2^-24 for the row type and width
+  float kappa2;       // relative rounding slack of the row type and width
+  float eta;          // absolute slack (underflow; binary16 subnormals)
 };
 
 // One octet per row (8 rows per wave): lane sub owns code words sub, sub+8,
@@ -147,9 +152,9 @@ __device__ __forceinline__ void q_load_self(const QBoundSet& qb, uint32_t id, QS
   me.a = __uint_as_float(uni_u(h.z));
 }
 
-// Upper bound of sqrt((T + 1e-30)(1 + kappa2)) + r_self (uniform).
+// Upper bound of sqrt((T + eta)(1 + kappa2)) + r_self (uniform).
 __device__ __forceinline__ float q_threshold(const QBoundSet& qb, const QSelf& me, float T) {
-  const float t = (T + 1e-30f) * (1.0f + qb.kappa2);
+  const float t = (T + qb.eta) * (1.0f + qb.kappa2);
   return uni_f((__builtin_sqrtf(t) + me.r) * (1.0f + kQSlack));
 }
 
@@ -187,13 +192,13 @@ __device__ __forceinline__ bool q_proves_reject(const QSelf& me, const uint4& co
 
 // Threshold of the prune's bound for a candidate at stored distance sd: a
 // pair distance d >= T gives fl(alpha * d) >= fl(alpha * T) > sd, so the
-// candidate survives. Returns sqrt((T + 1e-30)(1 + kappa2)) rounded up, the
+// candidate survives. Returns sqrt((T + eta)(1 + kappa2)) rounded up, the
 // per-candidate part of q_threshold; +inf (never skipped) for sd < 1e-30 or
 // non-finite sd, where the relative slack would not cover rounding.
 __device__ __forceinline__ float prune_bound_root(const QBoundSet& qb, float sd, float alpha) {
   if (!(sd >= 1e-30f) || !(sd <= FLT_MAX)) return __builtin_inff();
   const float T = sd / alpha * (1.0f + 0x1p-20f);
-  const float t = (T + 1e-30f) * (1.0f + qb.kappa2);
+  const float t = (T + qb.eta) * (1.0f + qb.kappa2);
   return __builtin_sqrtf(t) * (1.0f + kQSlack);
 }
 

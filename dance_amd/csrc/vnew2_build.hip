@@ -168,7 +168,7 @@ static uint32_t qbound_prune_iters() { return env_mask("DANCE_QBOUND_PRUNE_ITERS
 // Builds the code rows for `rows` into buf; returns a disabled set when the
 // row type or width has no bound.
 static int build_qbound(const Rows& rows, DevBuf& buf, hipStream_t s, QBoundSet* out) {
-  *out = QBoundSet{nullptr, 0.0f};
+  *out = QBoundSet{nullptr, 0.0f, 0.0f};
   if (!qbound_enabled() || rows.dtype == DANCE_U8 || rows.dim > kQMaxDim || rows.N == 0) return 0;
   const int cpl = pick_cpl(rows.rs.nch);
   if (cpl < 0) return 0;
@@ -180,7 +180,12 @@ static int build_qbound(const Rows& rows, DevBuf& buf, hipStream_t s, QBoundSet*
     hipLaunchKernelGGL(k_quantize<DANCE_F16>, dim3(grid), dim3(256), 0, s, rows.rs, rows.N, rows.dim, buf.as<uint4>());
   DHIP(hipGetLastError());
   const double lane_terms = (double)cpl * (16.0 / elem_bytes(rows.dtype));
-  *out = QBoundSet{buf.as<uint4>(), (float)(2.0 * (lane_terms + 8.0) * 0x1p-24)};
+  if (rows.dtype == DANCE_F32) {
+    *out = QBoundSet{buf.as<uint4>(), (float)(2.0 * (lane_terms + 8.0) * 0x1p-24), 1e-30f};
+  } else {  // binary16 differences and squares (see qbound.h)
+    *out = QBoundSet{buf.as<uint4>(), (float)(2.0 * (3.0 * 0x1p-11 + (lane_terms + 8.0) * 0x1p-24)),
+                     (float)(1e-30 + (double)rows.dim * 0x1p-24)};
+  }
   return 0;
 }
 
@@ -471,7 +476,7 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     if (verbose())
       std::printf("[gpu_vamana_build] iteration %u / %u, alpha=%.3f\n", it + 1, kIters, (double)alpha);
     DHIP(hipEventRecord(iev[it].s0, s));
-    const QBoundSet qb_it = ((q_iters >> it) & 1u) ? qb : QBoundSet{nullptr, 0.0f};
+    const QBoundSet qb_it = ((q_iters >> it) & 1u) ? qb : QBoundSet{nullptr, 0.0f, 0.0f};
     DCHECK(launch_search(rows, g, L, steps, alpha, start, order, ctr, qb_it, s));
     DHIP(hipEventRecord(iev[it].s1, s));
     const uint32_t* srcs = nullptr;
@@ -480,7 +485,7 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     DCHECK(launch_merge(rows, g, rws.offs.as<uint32_t>(), srcs, rws.snap.as<float>(), prof, order, ctr, s));
     DHIP(hipEventRecord(iev[it].m1, s));
     const uint32_t md = (it + 1 == kIters) ? kFinalMinDegree : 0u;
-    const QBoundSet qp_it = ((q_prune_iters >> it) & 1u) ? qb : QBoundSet{nullptr, 0.0f};
+    const QBoundSet qp_it = ((q_prune_iters >> it) & 1u) ? qb : QBoundSet{nullptr, 0.0f, 0.0f};
     DCHECK(launch_prune(rows, g, md, alpha, order, ctr, qp_it, s));
     DHIP(hipEventRecord(iev[it].p1, s));
   }
@@ -682,7 +687,7 @@ __global__ __launch_bounds__(kBlock) void k_pair_dist(RowSet rs, const uint32_t*
     uint4 va[CPL], vb[CPL];
     load_row<CPL>(rs, act ? a[k] : 0u, act, sub, va);
     load_row<CPL>(rs, act ? b[k] : 0u, act, sub, vb);
-    const float d = octet_finish<DT, CPL>(va, vb);
+    const float d = octet_finish<DT, CPL>(rs, sub, va, vb);
     if (act && sub == 0) out[k] = d;
   }
 }
@@ -704,7 +709,7 @@ __global__ __launch_bounds__(kBlock) void k_qbound_pairs(QBoundSet qb, const uin
     const uint4* qa = qb.rows + (size_t)(act ? a[k] : 0u) * kQChunks;
     const uint4 h = qa[0];
     const QSelf me{qa, __uint_as_float(h.x), __uint_as_float(h.y), __uint_as_float(h.z)};
-    const float t = ((act ? T[k] : 0.0f) + 1e-30f) * (1.0f + qb.kappa2);
+    const float t = ((act ? T[k] : 0.0f) + qb.eta) * (1.0f + qb.kappa2);
     const float sT = (__builtin_sqrtf(t) + me.r) * (1.0f + kQSlack);
     const uint4 code = qa[sub];
     const uint4 bc = q_load(qb, act ? b[k] : 0u, act, sub);

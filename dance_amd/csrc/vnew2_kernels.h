@@ -521,7 +521,7 @@ struct SearchWave {
       const uint32_t y0 = a0 ? wid[ord[nU + k0]] : 0u;
       uint4 b0[CPL];
       load_row<CPL>(a.rs, y0, a0, sub, b0);
-      const float d0 = octet_finish<DT, CPL>(xv, b0);
+      const float d0 = octet_finish<DT, CPL>(a.rs, sub, xv, b0);
       n_insert += min(8u, nA - p);
       occluded = wballot(sub == 0 && a0 && a.alpha * d0 <= dpx) != 0;
     }
@@ -547,7 +547,7 @@ struct SearchWave {
       const uint32_t y0 = a0 ? wid[s0] : 0u;
       uint4 b0[CPL];
       load_row<CPL>(a.rs, y0, a0, sub, b0);
-      const float d0 = octet_finish<DT, CPL>(xv, b0);
+      const float d0 = octet_finish<DT, CPL>(a.rs, sub, xv, b0);
       n_insert += min(8u, nB - p);
       const uint64_t hit = wballot(sub == 0 && a0 && a.alpha * d0 <= wdd[s0]);
       if (hit) vpos = (int)ord[wdeg - 1u - (p + ((uint32_t)ffs64(hit) >> 3))];
@@ -848,8 +848,8 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
       uint4 b0[CPL], b1[CPL];
       load_row<CPL>(a.rs, sid[s0], a0, sub, b0);
       load_row<CPL>(a.rs, sid[s1], a1, sub, b1);
-      const float d0 = octet_finish<DT, CPL>(sv, b0);
-      const float d1 = octet_finish<DT, CPL>(sv, b1);
+      const float d0 = octet_finish<DT, CPL>(a.rs, sub, sv, b0);
+      const float d1 = octet_finish<DT, CPL>(a.rs, sub, sv, b1);
       if (sub == 0) {
         if (a0 && a.alpha * d0 <= sd[s0]) fl[s0] |= PR_REMOVED;
         if (a1 && a.alpha * d1 <= sd[s1]) fl[s1] |= PR_REMOVED;
@@ -1249,8 +1249,8 @@ __global__ __launch_bounds__(kBlock) void k_medoid(RowSet rs, uint32_t N, uint32
       uint4 b0[CPL], b1[CPL];
       load_row<CPL>(rs, s0, a0, sub, b0);
       load_row<CPL>(rs, s1, a1, sub, b1);
-      const float d0 = octet_finish<DT, CPL>(cv, b0);
-      const float d1 = octet_finish<DT, CPL>(cv, b1);
+      const float d0 = octet_finish<DT, CPL>(rs, sub, cv, b0);
+      const float d1 = octet_finish<DT, CPL>(rs, sub, cv, b1);
       if (sub == 0) {
         if (a0) buf[w][k0] = d0;
         if (a1) buf[w][k1] = d1;
@@ -1337,7 +1337,7 @@ __global__ __launch_bounds__(kBlock) void k_cells(RowSet rs, uint32_t N, const u
   for (uint32_t k = 0; k < K; ++k) {
     uint4 pv[CPL];
     load_row<CPL>(rs, pivots[k], true, sub, pv);
-    const float d = octet_finish<DT, CPL>(xv, pv);
+    const float d = octet_finish<DT, CPL>(rs, sub, xv, pv);
     if (d < best) {
       best = d;
       bi = k;

@@ -6,12 +6,21 @@
 // and every 8-lane load instruction reads whole 128-byte lines.
 //
 // Canonical arithmetic (shared bit for bit with the CPU oracle):
-//   fp32 / fp16 (widened exactly to fp32): p = fmaf(t, t, p), t = a - b, in
-//   ascending element order within the lane's chunks; then the DPP tree
-//   half-row mirror (lane j + lane 7-j), quad swap 2, quad swap 1:
-//   ((p0+p7)+(p2+p5)) + ((p1+p6)+(p3+p4)); every lane of the octet holds it.
+//   fp32: p = fmaf(t, t, p), t = a - b, in ascending element order within the
+//   lane's chunks.
+//   fp16: the reference's element arithmetic (gpu_vamana_vnew2.cu:391-418,
+//   gpu_vamana_filtered.cu:4036-4047): per pair of elements (one 32-bit word)
+//   the difference and the square are binary16 operations (round to nearest
+//   even, overflow to inf), the two squares are widened and added in fp32,
+//   and that pair sum is added to p. For odd dim the last element is widened
+//   first and squared in fp32 (p = fmaf(t, t, p)), as the reference does.
+//   Words in ascending order within the lane's chunks.
+//   Then, for both, the DPP tree half-row mirror (lane j + lane 7-j), quad
+//   swap 2, quad swap 1: ((p0+p7)+(p2+p5)) + ((p1+p6)+(p3+p4)); every lane of
+//   the octet holds it.
 //   uint8: exact integer sum of (a-b)^2, converted to fp32 once.
-// The value is symmetric in (a, b): a-b and b-a differ only in sign.
+// The value is symmetric in (a, b): a-b and b-a differ only in sign, in
+// binary16 as in fp32.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -127,6 +136,8 @@ struct RowSet {
   const uint4* rows;  // device rows, each padded to stride16 16-byte chunks
   uint32_t stride16;  // chunks per row (row stride / 16 bytes)
   uint32_t nch;       // chunks that hold data (ceil(dim * elem_bytes / 16))
+  int32_t tail16;     // fp16 rows of odd dim: index of the 32-bit word holding
+                      // the last element (its upper half is padding); else -1
 };
 
 // Chunks sub, sub + 8, ... of row `id`. Rows are padded with zeros to the
@@ -151,32 +162,54 @@ __device__ __forceinline__ float fma_sq(float a, float b, float acc) {
   return __builtin_fmaf(t, t, acc);
 }
 
-__device__ __forceinline__ float h2f_lo(uint32_t w) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ half2_t as_half2(uint32_t w) { return __builtin_bit_cast(half2_t, w); }
+
+// One word of fp16 elements: binary16 difference and square, widened pair sum.
+__device__ __forceinline__ float h2_pair_sq(uint32_t a, uint32_t b) {
+  const half2_t t = as_half2(a) - as_half2(b);
+  const half2_t q = t * t;
+  return (float)q.x + (float)q.y;
 }
-__device__ __forceinline__ float h2f_hi(uint32_t w) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+
+// The odd-dim tail word: only the lower half holds data (the upper half is
+// padding, zero in every row); widened first, squared in fp32.
+__device__ __forceinline__ float h2_tail_fma(uint32_t a, uint32_t b, float acc) {
+  const float t = (float)as_half2(a).x - (float)as_half2(b).x;
+  return __builtin_fmaf(t, t, acc);
 }
 
 template <int DT, int CPL>
-__device__ __forceinline__ float octet_partial_f(const uint4 (&a)[CPL], const uint4 (&b)[CPL]) {
+__device__ __forceinline__ float octet_partial_f(const RowSet& rs, uint32_t sub, const uint4 (&a)[CPL],
+                                                 const uint4 (&b)[CPL]) {
   float acc = 0.0f;
+  if constexpr (DT == DANCE_F32) {
 #pragma unroll
-  for (int c = 0; c < CPL; ++c) {
-    if constexpr (DT == DANCE_F32) {
+    for (int c = 0; c < CPL; ++c) {
       acc = fma_sq(__uint_as_float(a[c].x), __uint_as_float(b[c].x), acc);
       acc = fma_sq(__uint_as_float(a[c].y), __uint_as_float(b[c].y), acc);
       acc = fma_sq(__uint_as_float(a[c].z), __uint_as_float(b[c].z), acc);
       acc = fma_sq(__uint_as_float(a[c].w), __uint_as_float(b[c].w), acc);
-    } else {
-      acc = fma_sq(h2f_lo(a[c].x), h2f_lo(b[c].x), acc);
-      acc = fma_sq(h2f_hi(a[c].x), h2f_hi(b[c].x), acc);
-      acc = fma_sq(h2f_lo(a[c].y), h2f_lo(b[c].y), acc);
-      acc = fma_sq(h2f_hi(a[c].y), h2f_hi(b[c].y), acc);
-      acc = fma_sq(h2f_lo(a[c].z), h2f_lo(b[c].z), acc);
-      acc = fma_sq(h2f_hi(a[c].z), h2f_hi(b[c].z), acc);
-      acc = fma_sq(h2f_lo(a[c].w), h2f_lo(b[c].w), acc);
-      acc = fma_sq(h2f_hi(a[c].w), h2f_hi(b[c].w), acc);
+    }
+  } else if (rs.tail16 < 0) {  // kernel argument: a uniform branch
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      acc += h2_pair_sq(a[c].x, b[c].x);
+      acc += h2_pair_sq(a[c].y, b[c].y);
+      acc += h2_pair_sq(a[c].z, b[c].z);
+      acc += h2_pair_sq(a[c].w, b[c].w);
+    }
+  } else {
+    // Word (c, w) of this lane is word 4*sub + 32*c + w of the row.
+    const int tl = rs.tail16 - 4 * (int)sub;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const uint32_t wa[4] = {a[c].x, a[c].y, a[c].z, a[c].w};
+      const uint32_t wb[4] = {b[c].x, b[c].y, b[c].z, b[c].w};
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        acc = tl == 32 * c + w ? h2_tail_fma(wa[w], wb[w], acc) : acc + h2_pair_sq(wa[w], wb[w]);
     }
   }
   return acc;
@@ -215,7 +248,8 @@ __device__ __forceinline__ float octet_combine(float p) {
 // Full distance of a pair held by an octet; every lane of the octet returns it.
 // Must be called by all 64 lanes (the butterfly crosses lanes).
 template <int DT, int CPL>
-__device__ __forceinline__ float octet_finish(const uint4 (&a)[CPL], const uint4 (&b)[CPL]) {
+__device__ __forceinline__ float octet_finish(const RowSet& rs, uint32_t sub, const uint4 (&a)[CPL],
+                                              const uint4 (&b)[CPL]) {
   if constexpr (DT == DANCE_U8) {
     int p = octet_partial_u8<CPL>(a, b);
     p += dpp<kDppHalfMirror>(0, p);
@@ -223,7 +257,7 @@ __device__ __forceinline__ float octet_finish(const uint4 (&a)[CPL], const uint4
     p += dpp<kDppQuadXor1>(0, p);
     return (float)(uint32_t)p;
   } else {
-    return octet_combine(octet_partial_f<DT, CPL>(a, b));
+    return octet_combine(octet_partial_f<DT, CPL>(rs, sub, a, b));
   }
 }
 
@@ -246,8 +280,8 @@ __device__ __forceinline__ void batch_dist(const RowSet& rs, const uint4 (&av)[C
     uint4 b0[CPL], b1[CPL];
     load_row<CPL>(rs, id0, a0, sub, b0);
     load_row<CPL>(rs, id1, a1, sub, b1);
-    const float d0 = octet_finish<DT, CPL>(av, b0);
-    const float d1 = octet_finish<DT, CPL>(av, b1);
+    const float d0 = octet_finish<DT, CPL>(rs, sub, av, b0);
+    const float d1 = octet_finish<DT, CPL>(rs, sub, av, b1);
     if (sub == 0) {
       if (a0) lsd[k0] = d0;
       if (a1) lsd[k1] = d1;
@@ -258,7 +292,7 @@ __device__ __forceinline__ void batch_dist(const RowSet& rs, const uint4 (&av)[C
     const bool a0 = k0 < n;
     uint4 b0[CPL];
     load_row<CPL>(rs, lst[k0], a0, sub, b0);
-    const float d0 = octet_finish<DT, CPL>(av, b0);
+    const float d0 = octet_finish<DT, CPL>(rs, sub, av, b0);
     if (sub == 0 && a0) lsd[k0] = d0;
   }
   wave_sync();

@@ -103,16 +103,22 @@ def label_starts(data: np.ndarray, ls: LabelSet) -> np.ndarray:
     label entry points with its own sampler (upstream, not part of the
     reference); any in-label point is a valid entry for the builder."""
     off, pts = ls.postings()
-    x = np.asarray(data, np.float64)
     starts = np.full(max(1, ls.num_labels), INVALID, np.uint32)
     lab_of = np.repeat(np.arange(ls.num_labels), np.diff(off).astype(np.int64))
     if pts.size == 0:
         return starts
-    sums = np.zeros((ls.num_labels, x.shape[1]))
-    np.add.at(sums, lab_of, x[pts])
+    dim = data.shape[1]
     cnt = np.diff(off).astype(np.float64)
+    # per-dimension label sums (fp64; exact for integer rows)
+    sums = np.empty((ls.num_labels, dim))
+    for j in range(dim):
+        sums[:, j] = np.bincount(lab_of, weights=data[pts, j].astype(np.float64), minlength=ls.num_labels)
     cent = sums / np.maximum(cnt, 1)[:, None]
-    d = ((x[pts] - cent[lab_of]) ** 2).sum(1)
+    d = np.empty(pts.size)
+    step = 1 << 18
+    for s0 in range(0, pts.size, step):
+        seg = slice(s0, s0 + step)
+        d[seg] = ((data[pts[seg]].astype(np.float64) - cent[lab_of[seg]]) ** 2).sum(1)
     for l in np.nonzero(cnt)[0]:
         seg = slice(off[l], off[l + 1])
         j = int(np.argmin(d[seg]))
@@ -122,8 +128,16 @@ def label_starts(data: np.ndarray, ls: LabelSet) -> np.ndarray:
 
 def global_start(data: np.ndarray) -> int:
     """Point nearest to the centroid (DiskANN calculate_entry_point analogue)."""
-    x = np.asarray(data, np.float64)
-    return int(np.argmin(((x - x.mean(0)) ** 2).sum(1)))
+    n = data.shape[0]
+    mean = np.zeros(data.shape[1])
+    step = 1 << 18
+    for s0 in range(0, n, step):
+        mean += data[s0:s0 + step].astype(np.float64).sum(0)
+    mean /= max(1, n)
+    d = np.empty(n)
+    for s0 in range(0, n, step):
+        d[s0:s0 + step] = ((data[s0:s0 + step].astype(np.float64) - mean) ** 2).sum(1)
+    return int(np.argmin(d))
 
 
 @dataclass

@@ -82,6 +82,10 @@ def lib() -> C.CDLL:
         L.oracle_hash_u32.restype = u32
         L.oracle_det_neighbor.argtypes = [u32, u32, u32]
         L.oracle_det_neighbor.restype = u32
+        L.oracle_half_round.argtypes = [C.c_double]
+        L.oracle_half_round.restype = C.c_uint16
+        L.oracle_half_sq_of_diff.argtypes = [C.c_uint16, C.c_uint16]
+        L.oracle_half_sq_of_diff.restype = f32
         L.oracle_distance.argtypes = [vp, i32, u32, u32, u32]
         L.oracle_distance.restype = f32
         L.oracle_distance_many.argtypes = [vp, i32, u32, _u32p, _u32p, u64, _f32p]
@@ -152,6 +156,16 @@ def hash_u32(x: int) -> int:
 
 def det_neighbor(node: int, k: int, N: int) -> int:
     return int(lib().oracle_det_neighbor(node, k, N))
+
+
+def half_round(x: float) -> int:
+    """binary16 bits of x rounded to nearest even (the oracle's helper)."""
+    return int(lib().oracle_half_round(float(x)))
+
+
+def half_sq_of_diff(a_bits: int, b_bits: int) -> float:
+    """binary16 (a - b)^2, widened (one element of the fp16 distance)."""
+    return float(np.float32(lib().oracle_half_sq_of_diff(a_bits, b_bits)))
 
 
 def distance(data: np.ndarray, a: int, b: int) -> float:

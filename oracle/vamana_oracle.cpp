@@ -63,12 +63,20 @@ inline uint32_t det_neighbor(uint32_t node, uint32_t k, uint32_t N) {
 //
 // The row is cut into 16-byte chunks (4 fp32, 8 fp16 or 16 uint8 elements).
 // Sub-lane j in [0,8) owns chunks j, j+8, j+16, ... and walks its elements in
-// ascending order. fp32 and fp16 (widened exactly to fp32) accumulate
-// p_j = fmaf(t, t, p_j) with t = a_e - b_e rounded to fp32; the eight partials
-// are combined as ((p0+p7)+(p2+p5)) + ((p1+p6)+(p3+p4)), the DPP tree of the
-// HIP kernels (half-row mirror, then quad swaps by 2 and by 1). uint8 sums
-// (a-b)^2 exactly in integers, like the reference's dp4a form xx+yy-2xy
-// (vnew2.cu:268-290), and converts once.
+// ascending order.
+//  * fp32 accumulates p_j = fmaf(t, t, p_j) with t = a_e - b_e rounded to fp32.
+//  * fp16 follows the reference's element arithmetic (vnew2.cu:391-418,
+//    filtered.cu:4036-4047): for each pair of elements (2e, 2e+1), the
+//    differences and squares are binary16 operations (__hsub2, __hmul2: round
+//    to nearest even, overflow to inf); the two squares are widened and added
+//    in fp32 and that pair sum is added to p_j. For odd dim the last element is
+//    widened first: t = float(a) - float(b), p_j = fmaf(t, t, p_j) (the
+//    reference's `sum += delta * delta` tail, :404-410).
+//  * The eight partials are combined as ((p0+p7)+(p2+p5)) + ((p1+p6)+(p3+p4)),
+//    the DPP tree of the HIP kernels (half-row mirror, then quad swaps by 2
+//    and by 1).
+//  * uint8 sums (a-b)^2 exactly in integers, like the reference's dp4a form
+//    xx+yy-2xy (vnew2.cu:268-290), and converts once.
 // ---------------------------------------------------------------------------
 inline float half_to_float(uint16_t h) {
   uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
@@ -117,6 +125,38 @@ float dist_f32(const float* a, const float* b, uint32_t dim) {
   return combine8(p);
 }
 
+// IEEE binary16 rounding (to nearest, ties to even) of a double. Every value
+// rounded here is exact in double (a difference or product of two binary16
+// values), so this is the single rounding of the binary16 operation.
+uint16_t half_round(double x) {
+  const uint16_t sign = std::signbit(x) ? 0x8000u : 0u;
+  if (std::isnan(x)) return (uint16_t)(sign | 0x7E00u);
+  const double ax = std::fabs(x);
+  if (ax >= 65520.0) return (uint16_t)(sign | 0x7C00u);  // max finite 65504; the tie 65520 goes to even (inf)
+  if (ax < 0x1p-14) {
+    // subnormal range: multiples of 2^-24; 1024 * 2^-24 is the smallest
+    // normal, whose encoding 0x0400 the integer already is
+    return (uint16_t)(sign | (uint16_t)std::nearbyint(ax * 0x1p24));
+  }
+  int e = 0;
+  std::frexp(ax, &e);  // ax in [2^(e-1), 2^e)
+  int E = e - 1;
+  double m = std::nearbyint(std::ldexp(ax, 10 - E));  // [1024, 2048]
+  if (m >= 2048.0) {
+    m = 1024.0;
+    ++E;
+  }
+  if (E > 15) return (uint16_t)(sign | 0x7C00u);
+  return (uint16_t)(sign | (uint16_t)((E + 15) << 10) | (uint16_t)((int)m - 1024));
+}
+
+// __hmul2(__hsub2(a, b), same) on one element, widened.
+inline float half_sq_of_diff(uint16_t a, uint16_t b) {
+  const uint16_t t = half_round((double)half_to_float(a) - (double)half_to_float(b));
+  const double tf = (double)half_to_float(t);
+  return half_to_float(half_round(tf * tf));
+}
+
 float dist_f16(const uint16_t* a, const uint16_t* b, uint32_t dim) {
   const uint32_t E = 8;
   const uint32_t nch = (dim + E - 1) / E;
@@ -125,9 +165,13 @@ float dist_f16(const uint16_t* a, const uint16_t* b, uint32_t dim) {
     float acc = 0.0f;
     for (uint32_t c = j; c < nch; c += 8) {
       const uint32_t e1 = std::min(c * E + E, dim);
-      for (uint32_t e = c * E; e < e1; ++e) {
-        float t = half_to_float(a[e]) - half_to_float(b[e]);
-        acc = fmaf(t, t, acc);
+      for (uint32_t e = c * E; e < e1; e += 2) {
+        if (e + 1 == dim) {  // odd dim: the last element alone, in fp32
+          const float t = half_to_float(a[e]) - half_to_float(b[e]);
+          acc = fmaf(t, t, acc);
+        } else {
+          acc = acc + (half_sq_of_diff(a[e], b[e]) + half_sq_of_diff(a[e + 1], b[e + 1]));
+        }
       }
     }
     p[j] = acc;
@@ -143,6 +187,13 @@ float dist_u8(const uint8_t* a, const uint8_t* b, uint32_t dim) {
   }
   return (float)(uint32_t)s;
 }
+
+}  // namespace
+
+extern "C" uint16_t oracle_half_round(double x) { return half_round(x); }
+extern "C" float oracle_half_sq_of_diff(uint16_t a, uint16_t b) { return half_sq_of_diff(a, b); }
+
+namespace {
 
 struct Data {
   const void* ptr;

@@ -69,7 +69,8 @@ def assert_state_equal(g, s, fields=("cur", "deg_cur", "work", "deg_work", "wd")
 
 
 @pytest.mark.parametrize("kind,dim", [("f32", 96), ("f32", 100), ("f32", 7), ("u8", 128), ("u8", 192),
-                                      ("u8", 33), ("f16", 96), ("f16", 50),
+                                      ("u8", 33), ("f16", 96), ("f16", 50), ("f16", 97), ("f16", 33),
+                                      ("f16", 1), ("f16", 255),
                                       # the widest rows of each type (16 chunks per lane)
                                       ("f32", 512), ("u8", 2048), ("f16", 1024), ("f32", 260)])
 def test_distances_bitwise(kind, dim):
@@ -79,6 +80,23 @@ def test_distances_bitwise(kind, dim):
     b = rng.integers(0, 3000, 20000).astype(np.uint32)
     g = D.stage_distances(data, a, b)
     o = O.distances(data, a, b)
+    assert np.array_equal(g.view(np.uint32), o.view(np.uint32))
+
+
+@pytest.mark.parametrize("dim", [96, 97, 8, 3])
+def test_distances_f16_binary16_edges(dim):
+    """fp16 rows whose binary16 differences round, go subnormal or overflow
+    the square to inf (|a - b| > 256), and odd tails squared in fp32."""
+    rng = np.random.default_rng(dim)
+    n = 512
+    x = (rng.standard_normal((n, dim)) * 10.0 ** rng.integers(-6, 3, (n, 1))).astype(np.float16)
+    x[::7, 0] = np.float16(300.0)
+    x[1::7, -1] = np.float16(-300.0)
+    a = rng.integers(0, n, 8000).astype(np.uint32)
+    b = rng.integers(0, n, 8000).astype(np.uint32)
+    g = D.stage_distances(x, a, b)
+    o = O.distances(x, a, b)
+    assert np.isinf(o).any() and np.isfinite(o).any()
     assert np.array_equal(g.view(np.uint32), o.view(np.uint32))
 
 

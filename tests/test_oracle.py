@@ -88,15 +88,94 @@ def test_distance_u8_exact(dim):
     assert O.distance(y, 0, 1) == float(dim * 255 * 255)
 
 
-@pytest.mark.parametrize("dim", [8, 50, 96])
-def test_distance_f16_widened(dim):
+def _np_half_sq(a16, b16):
+    """__hmul2(__hsub2(a, b), same) with numpy binary16 arithmetic, widened.
+    numpy evaluates float16 operations in float32 and rounds once to float16;
+    float32 carries 24 >= 2*11 + 2 bits, so that double rounding equals the
+    single binary16 rounding of the exact result."""
+    with np.errstate(over="ignore", invalid="ignore"):
+        t = (a16 - b16).astype(np.float16)
+        return (t * t).astype(np.float16).astype(np.float32)
+
+
+def test_half_round_matches_numpy():
+    rng = np.random.default_rng(11)
+    xs = np.concatenate([
+        rng.standard_normal(20000) * 10.0 ** rng.integers(-9, 6, 20000),
+        # ties at every binade and in the subnormal range, overflow boundary
+        (np.arange(1, 2048, dtype=np.float64) + 0.5) * 2.0 ** -24,
+        (1024 + np.arange(0, 1024) + 0.5) * 2.0 ** rng.integers(-24, 6, 1024),
+        [65504.0, 65519.99, 65520.0, 65536.0, 1e300, 2.0 ** -25, 2.0 ** -25 * 1.0001, 3 * 2.0 ** -26,
+         0.0, -0.0, np.inf, -np.inf],
+    ])
+    xs = np.concatenate([xs, -xs])
+    with np.errstate(over="ignore"):
+        want = xs.astype(np.float16).view(np.uint16)
+    got = np.array([O.half_round(float(x)) for x in xs], np.uint16)
+    assert np.array_equal(got, want), xs[got != want][:5]
+    assert O.half_round(float("nan")) & 0x7C00 == 0x7C00 and O.half_round(float("nan")) & 0x3FF
+
+
+def test_half_sq_of_diff_matches_numpy_binary16():
+    rng = np.random.default_rng(12)
+    a = (rng.standard_normal(30000) * 10.0 ** rng.integers(-6, 3, 30000)).astype(np.float16)
+    b = (rng.standard_normal(30000) * 10.0 ** rng.integers(-6, 3, 30000)).astype(np.float16)
+    # |a-b| above 256: the binary16 square overflows to inf (the widened fp32
+    # form would stay finite); subnormal differences; equal values
+    a = np.concatenate([a, np.float16([300.0, -200.0, 1.0, 6e-5, 0.5, 65504.0])])
+    b = np.concatenate([b, np.float16([0.0, 100.0, 1.0, 5.9e-5, 0.5 + 2 ** -11, -65504.0])])
+    want = _np_half_sq(a, b)
+    got = np.array([O.half_sq_of_diff(int(x), int(y)) for x, y in zip(a.view(np.uint16), b.view(np.uint16))],
+                   np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.isinf(got[-6]) and np.isinf(got[-5]) and np.isinf(got[-1])
+
+
+def test_distance_f16_small_dims_exact():
+    """dim 2: one pair, (float(sq0) + float(sq1)) exactly. dim 1: the odd
+    tail alone, widened first and squared in fp32."""
+    rng = np.random.default_rng(13)
+    x = (rng.standard_normal((200, 2)) * 4).astype(np.float16)
+    a = rng.integers(0, 200, 500)
+    b = rng.integers(0, 200, 500)
+    sq = _np_half_sq(x[a], x[b])
+    want = sq[:, 0] + sq[:, 1]
+    assert np.array_equal(O.distances(x, a, b).view(np.uint32), want.view(np.uint32))
+    x1 = np.ascontiguousarray(x[:, :1])
+    t = x1[a, 0].astype(np.float32) - x1[b, 0].astype(np.float32)
+    assert np.array_equal(O.distances(x1, a, b).view(np.uint32), (t * t).view(np.uint32))
+
+
+@pytest.mark.parametrize("dim", [8, 50, 96, 97, 33])
+def test_distance_f16_binary16_terms(dim):
+    """The fp16 distance sums the binary16 per-element squares (plus an fp32
+    square for an odd dim's last element): within the fp32 summation bound of
+    the fp64 sum of those terms, and far from the widened form where the
+    binary16 rounding of a difference moves it."""
     rng = np.random.default_rng(dim)
     x = rng.standard_normal((40, dim)).astype(np.float16)
     a = rng.integers(0, 40, 200)
     b = rng.integers(0, 40, 200)
     got = O.distances(x, a, b).astype(np.float64)
-    exact = ((x[a].astype(np.float64) - x[b].astype(np.float64)) ** 2).sum(1)
+    terms = _np_half_sq(x[a], x[b]).astype(np.float64)
+    if dim % 2:
+        t = x[a, -1].astype(np.float64) - x[b, -1].astype(np.float64)
+        terms[:, -1] = t * t
+    exact = terms.sum(1)
     assert np.all(np.abs(got - exact) <= (dim + 3) * 2.0 ** -24 * exact + 1e-30)
+    # symmetric bitwise, zero self-distance
+    assert np.array_equal(O.distances(x, a, b).view(np.uint32), O.distances(x, b, a).view(np.uint32))
+    assert np.all(O.distances(x, a, a) == 0.0)
+    # a row pair whose binary16 difference overflows its square: inf, where
+    # the widened form would give a finite value
+    y = np.zeros((2, dim), np.float16)
+    y[0, 0], y[1, 0] = 300.0, 0.0
+    assert np.isinf(O.distance(y, 0, 1))
+    if dim % 2:
+        # the odd tail is squared in fp32: finite
+        z = np.zeros((2, dim), np.float16)
+        z[0, -1] = 300.0
+        assert O.distance(z, 0, 1) == 90000.0
 
 
 # ---------------------------------------------------------------- medoid
