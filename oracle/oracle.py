@@ -86,6 +86,8 @@ def lib() -> C.CDLL:
         L.oracle_half_round.restype = C.c_uint16
         L.oracle_half_sq_of_diff.argtypes = [C.c_uint16, C.c_uint16]
         L.oracle_half_sq_of_diff.restype = f32
+        L.oracle_robust_insert.argtypes = [vp, i32, u32, u32, u32, u32, u32, f32, f32, _u32p, _f32p, _u32p]
+        L.oracle_robust_insert.restype = None
         L.oracle_distance.argtypes = [vp, i32, u32, u32, u32]
         L.oracle_distance.restype = f32
         L.oracle_distance_many.argtypes = [vp, i32, u32, _u32p, _u32p, u64, _f32p]
@@ -226,6 +228,17 @@ def search(data: np.ndarray, s: State, L: int, steps: int, alpha: float, start: 
     lib().oracle_search(data.ctypes.data, _dt(data), N, data.shape[1], R, L, s.work.shape[1], steps, alpha, start,
                         *s.ptrs())
     return s
+
+
+def robust_insert(data: np.ndarray, node: int, x: int, d_px: float, alpha: float, row, drow, deg: int):
+    """One online robust insert into a work row of capacity len(row); returns
+    (row, drow, deg) after it."""
+    row = np.ascontiguousarray(row, np.uint32).copy()
+    drow = np.ascontiguousarray(drow, np.float32).copy()
+    d = np.array([deg], np.uint32)
+    lib().oracle_robust_insert(data.ctypes.data, _dt(data), data.shape[0], data.shape[1], row.shape[0], node, x,
+                               d_px, alpha, _p(row), _p(drow, C.c_float), _p(d))
+    return row, drow, int(d[0])
 
 
 def reverse_merge(data: np.ndarray, s: State, heavy_threshold: int = 0, heavy_sample: int = 0):

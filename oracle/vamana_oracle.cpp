@@ -315,12 +315,10 @@ struct Graph {
 };
 
 // dynamic_robust_insert_C_warp, vnew2.cu:759-877 (ENABLE_FAST_ONLINE_REPLACE=0)
-void robust_insert(const Data& D, Graph& g, uint32_t node, uint32_t x, float d_px, float alpha) {
-  const uint32_t N = g.N, C = g.C;
+void robust_insert_row(const Data& D, uint32_t N, uint32_t C, uint32_t node, uint32_t x, float d_px, float alpha,
+                       uint32_t* row, float* drow, uint32_t& deg_io) {
   if (x == INV || x >= N || x == node) return;
-  uint32_t* row = g.work + (size_t)node * C;
-  float* drow = g.wd + (size_t)node * C;
-  uint32_t deg = std::min(g.deg_work[node], C);
+  uint32_t deg = std::min(deg_io, C);
   for (uint32_t i = 0; i < deg; ++i)
     if (row[i] == x) return;
   bool occluded = false;
@@ -360,11 +358,16 @@ void robust_insert(const Data& D, Graph& g, uint32_t node, uint32_t x, float d_p
   } else if (deg < C) {
     row[deg] = x;
     drow[deg] = d_px;
-    g.deg_work[node] = deg + 1;
+    deg_io = deg + 1;
   } else if (worst_pos >= 0 && d_px < worst_d) {
     row[worst_pos] = x;
     drow[worst_pos] = d_px;
   }
+}
+
+void robust_insert(const Data& D, Graph& g, uint32_t node, uint32_t x, float d_px, float alpha) {
+  robust_insert_row(D, g.N, g.C, node, x, d_px, alpha, g.work + (size_t)node * g.C, g.wd + (size_t)node * g.C,
+                    g.deg_work[node]);
 }
 
 // search_prune_kernel_shared, vnew2.cu:1119-1439 (one entry point,
@@ -722,6 +725,14 @@ uint64_t oracle_search(const void* data, int dtype, uint32_t N, uint32_t dim, ui
     total += nd;
   }
   return total;
+}
+
+// One online robust insert of x (distance d_px to node) into node's work
+// row (ids, dists, degree) of capacity C (vnew2.cu:759-877), for the tests.
+void oracle_robust_insert(const void* data, int dtype, uint32_t N, uint32_t dim, uint32_t C, uint32_t node,
+                          uint32_t x, float d_px, float alpha, uint32_t* row, float* drow, uint32_t* deg) {
+  Data D{data, dtype, N, dim};
+  robust_insert_row(D, N, C, node, x, d_px, alpha, row, drow, *deg);
 }
 
 // Reverse CSR + merge (vnew2.cu:2569-2611). offsets (N+1) and ids (<= N*R)

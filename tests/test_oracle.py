@@ -407,3 +407,152 @@ def test_build_rejects_bad_parameters():
         O.vnew2_build(x, 8, 10, 4, 4)  # C < R
     with pytest.raises(ValueError):
         O.vnew2_build(x, 0, 10, 8, 4)
+
+
+# ------------------------------------------------- online robust insert
+
+def restated_robust_insert(x, node, cand, d_px, alpha, row, drow, deg):
+    """The online insert of vnew2.cu:759-877, restated from the reference
+    source with Python lists: skip an invalid / self / present candidate;
+    drop it when a row member y with d_py <= d_px has alpha * d(y, x) <= d_px;
+    else overwrite the farthest member it alpha-dominates (d_py > d_px and
+    alpha * d(x, y) <= d_py; first slot on ties), else append while the row
+    has room, else overwrite the farthest member (first slot on ties) when
+    closer than it."""
+    N, C = x.shape[0], len(row)
+    row, drow = list(row), [np.float32(v) for v in drow]
+    deg = min(deg, C)
+    a, dpx = np.float32(alpha), np.float32(d_px)
+    if cand >= N or cand == node or cand in row[:deg]:
+        return row, drow, deg
+    members = [i for i in range(deg) if row[i] < N and row[i] != node]
+    for i in members:
+        if drow[i] <= dpx and a * np.float32(O.distance(x, row[i], cand)) <= dpx:
+            return row, drow, deg
+    finite = [i for i in members if drow[i] == drow[i]]
+    worst = None
+    if finite:
+        top = max(drow[i] for i in finite)
+        worst = min(i for i in finite if drow[i] == top)
+    dominated = [i for i in members if drow[i] > dpx and a * np.float32(O.distance(x, cand, row[i])) <= drow[i]]
+    if dominated:
+        top = max(drow[i] for i in dominated)
+        v = min(i for i in dominated if drow[i] == top)
+        row[v], drow[v] = cand, dpx
+    elif deg < C:
+        row[deg], drow[deg] = cand, dpx
+        deg += 1
+    elif worst is not None and dpx < drow[worst]:
+        row[worst], drow[worst] = cand, dpx
+    return row, drow, deg
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_robust_insert_matches_restatement(seed):
+    """Tiny rows of small-integer vectors, so exact ties are common: d_py ==
+    d_px, alpha * d == d_px (alpha 0.5 / 1 / 2 are exact), full rows,
+    invalid and self members, FLT_MAX and NaN stored distances, present,
+    invalid and self candidates."""
+    rng = np.random.default_rng(100 + seed)
+    N, dim = 24, 3
+    x = rng.integers(0, 3, (N, dim)).astype(np.uint8)
+    for trial in range(1500):
+        C = int(rng.integers(1, 7))
+        node = int(rng.integers(0, N))
+        row = rng.integers(0, N, C).astype(np.uint32)
+        row[rng.random(C) < 0.15] = INV
+        row[rng.random(C) < 0.1] = node
+        drow = np.array([O.distance(x, node, int(v)) if v < N else FMAX for v in row], np.float32)
+        drow[rng.random(C) < 0.1] = FMAX
+        drow[rng.random(C) < 0.05] = np.nan
+        deg = int(rng.integers(0, C + 1))
+        cand = int(rng.integers(0, N)) if rng.random() > 0.05 else INV
+        if rng.random() < 0.1 and deg:
+            cand = int(row[rng.integers(0, deg)])
+        d_px = O.distance(x, node, cand) if cand < N else FMAX
+        if rng.random() < 0.2 and deg:  # tie a stored distance
+            d_px = float(drow[rng.integers(0, deg)])
+        alpha = float(rng.choice([0.5, 1.0, 1.2, 2.0]))
+        got = O.robust_insert(x, node, cand, d_px, alpha, row, drow, deg)
+        want = restated_robust_insert(x, node, cand, d_px, alpha, row.tolist(), drow.tolist(), deg)
+        assert got[0].tolist() == want[0], (trial, node, cand, d_px, alpha, row, drow, deg)
+        assert np.array_equal(got[1].view(np.uint32), np.array(want[1], np.float32).view(np.uint32))
+        assert got[2] == want[2]
+
+
+# ------------------------------------------------- search (pool + steps)
+
+def textbook_best_first(x, node, cur, deg_cur, wd_row, start, L, steps):
+    """Best-first search with a beam of the L nearest candidates (DiskANN
+    Alg. 1; no slot layout): seeds are the start, the node's own neighbours at
+    their stored distances and the 8 hashed seeds h(node, 1024 + k); each step
+    expands the nearest unexpanded candidate, at most min(steps, L) steps.
+    Returns the expansion order. Valid for inputs with distinct distances."""
+    N = x.shape[0]
+    pool = {}
+
+    def offer(v, d):
+        if v >= N or v == node or v in pool:
+            return
+        if len(pool) < L:
+            pool[v] = [np.float32(d), False]
+            return
+        far = max(pool, key=lambda u: pool[u][0])
+        if np.float32(d) < pool[far][0]:
+            del pool[far]
+            pool[v] = [np.float32(d), False]
+
+    if start < N and start != node:
+        offer(start, O.distance(x, node, start))
+    for i in range(int(deg_cur[node])):
+        offer(int(cur[node, i]), wd_row[i])
+    for k in range(8):
+        s = O.det_neighbor(node, 1024 + k, N)
+        if s < N:
+            offer(s, O.distance(x, node, s))
+    order = []
+    for _ in range(min(steps, L)):
+        open_ = [u for u in pool if not pool[u][1]]
+        if not open_:
+            break
+        u = min(open_, key=lambda v: pool[v][0])
+        pool[u][1] = True
+        order.append(u)
+        for j in range(int(deg_cur[u])):
+            v = int(cur[u, j])
+            if v < N and v != node:
+                offer(v, O.distance(x, node, v))
+    return order
+
+
+@pytest.mark.parametrize("N,R,L,steps", [(60, 4, 80, 100), (120, 6, 24, 40), (200, 5, 16, 8), (90, 3, 10, 64),
+                                         (150, 8, 60, 20)])
+def test_search_expansion_order_matches_best_first(N, R, L, steps):
+    """With alpha huge nothing is occluded or replaced, so the online insert
+    appends every expanded node the row does not hold: the work row after the
+    search is the current row followed by the expansion order. Compared with
+    an independent best-first search, on random graphs (L >= N - 1: whole
+    graph explored; L < N: beam eviction; steps below and above L)."""
+    rng = np.random.default_rng(N * 7 + L)
+    x = rng.standard_normal((N, 12)).astype(np.float32)
+    C = R + min(steps, L) + 1
+    s0 = O.State.empty(N, R, C)
+    s0.cur = rng.integers(0, N, (N, R)).astype(np.uint32)
+    s0.cur[rng.random((N, R)) < 0.05] = INV
+    s0.deg_cur = rng.integers(1, R + 1, N).astype(np.uint32)
+    for v in range(N):
+        s0.cur[v, s0.deg_cur[v]:] = INV
+        for i in range(int(s0.deg_cur[v])):
+            u = int(s0.cur[v, i])
+            s0.wd[v, i] = O.distance(x, v, u) if u < N and u != v else FMAX
+    start = int(rng.integers(0, N))
+    s = O.search(x, s0, L, steps, 1e30, start)
+    for v in range(N):
+        order = textbook_best_first(x, v, s0.cur, s0.deg_cur, s0.wd[v], start, L, steps)
+        row = [int(u) if (u < N and u != v) else INV for u in s0.cur[v, :s0.deg_cur[v]]]
+        for u in order:
+            if u not in row:
+                row.append(u)
+        k = int(s.deg_work[v])
+        assert k == len(row), v
+        assert s.work[v, :k].tolist() == row, v
