@@ -186,6 +186,17 @@ def lib() -> C.CDLL:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} is missing: run `python -m dance_amd.build` "
                                "(or __graft_entry__.build()) first")
+        # PyTorch-ROCm ships its own HIP runtime (torch/lib/libamdhip64.so,
+        # requested by that unversioned name). If this library loaded the
+        # system runtime (libamdhip64.so.7) first, a later torch import would
+        # start a second HIP/HSA runtime in the process, which then finds no
+        # GPU. Loading torch first makes the library bind to torch's copy
+        # (same soname), so one runtime serves both and torch device pointers
+        # are valid here.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = C.CDLL(LIB_PATH)
         _check_struct_sizes(L)
         u32, f32, vp, i32 = C.c_uint32, C.c_float, C.c_void_p, C.c_int
