@@ -135,7 +135,7 @@ EXPORTS = [
     "gpu_vamana_vnew2_build_device", "gpu_vamana_vnew2_build_device_float",
     "gpu_vamana_get_last_medoid", "gpu_vamana_get_last_stats",
     "gpu_vamana_vnew2_get_last_medoid", "gpu_vamana_vnew2_get_last_stats",
-    "dance_vamana_build_resident", "dance_get_last_kernel_profile",
+    "dance_vamana_build_resident", "dance_vamana_build_resident_noalloc", "dance_get_last_kernel_profile",
     "dance_set_profile", "dance_get_profile",
     "dance_stage_distances", "dance_stage_qbound", "dance_stage_medoid", "dance_stage_init", "dance_stage_search",
     "dance_stage_reverse_merge", "dance_stage_prune", "dance_stage_sort_pairs", "dance_stage_scan",
@@ -215,8 +215,9 @@ def lib() -> C.CDLL:
         for name in ("gpu_vamana_get_last_stats", "gpu_vamana_vnew2_get_last_stats"):
             getattr(L, name).argtypes = [C.POINTER(GPUVamanaStats)]
             getattr(L, name).restype = None
-        L.dance_vamana_build_resident.argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, vp, vp]
-        L.dance_vamana_build_resident.restype = i32
+        for name in ("dance_vamana_build_resident", "dance_vamana_build_resident_noalloc"):
+            getattr(L, name).argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, vp, vp]
+            getattr(L, name).restype = i32
         L.dance_get_last_kernel_profile.argtypes = [C.POINTER(DanceKernelProfile)]
         L.dance_get_last_kernel_profile.restype = None
         L.dance_set_profile.argtypes = [C.c_char_p]
@@ -347,6 +348,14 @@ def vamana_build_resident(d_data: int, dtype: int, N: int, dim: int, R: int, L: 
     """dance_vamana_build_resident on device pointers (e.g. torch tensor data_ptr())."""
     _check(lib().dance_vamana_build_resident(d_data, dtype, N, dim, R, L, C_, STEPS, d_graph, d_degree),
            "dance_vamana_build_resident")
+
+
+def vamana_build_resident_noalloc(d_data: int, dtype: int, N: int, dim: int, R: int, L: int, C_: int, STEPS: int,
+                                  d_graph: int, d_degree: int) -> None:
+    """dance_vamana_build_resident_noalloc: the same build with every device
+    buffer taken from the library's per-GPU scratch array (no allocation)."""
+    _check(lib().dance_vamana_build_resident_noalloc(d_data, dtype, N, dim, R, L, C_, STEPS, d_graph, d_degree),
+           "dance_vamana_build_resident_noalloc")
 
 
 # ---------------------------------------------------------------- stage hooks

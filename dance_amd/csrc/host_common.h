@@ -83,24 +83,57 @@ inline int with_dt_cpl(int dtype, int cpl, Fn&& fn) {
 }
 
 // ---------------------------------------------------------------------------
-// RAII device memory.
+// Device memory: RAII buffers, or slices of a caller's arena.
 // ---------------------------------------------------------------------------
+
+// Bump allocator over device memory owned by someone else (the allocation-free
+// build's scratch array). While an ArenaScope is alive on a thread, every
+// DevBuf::alloc on that thread takes its bytes from the arena instead of
+// hipMalloc, and nothing is freed: the arena's contents end with the scope.
+struct Arena {
+  char* base = nullptr;
+  size_t cap = 0;
+  size_t used = 0;
+};
+inline thread_local Arena* tl_arena = nullptr;
+struct ArenaScope {
+  Arena* prev;
+  explicit ArenaScope(Arena* a) : prev(tl_arena) { tl_arena = a; }
+  ~ArenaScope() { tl_arena = prev; }
+  ArenaScope(const ArenaScope&) = delete;
+  ArenaScope& operator=(const ArenaScope&) = delete;
+};
+
 struct DevBuf {
   void* p = nullptr;
   size_t bytes = 0;
+  bool borrowed = false;  // a slice of an arena (never freed here)
   DevBuf() = default;
   DevBuf(const DevBuf&) = delete;
   DevBuf& operator=(const DevBuf&) = delete;
   ~DevBuf() {
-    if (p) (void)hipFree(p);
+    if (p && !borrowed) (void)hipFree(p);
   }
   int alloc(size_t b) {
     if (p) {
-      (void)hipFree(p);
+      if (!borrowed) (void)hipFree(p);
       p = nullptr;
     }
+    borrowed = false;
     bytes = b;
     if (b == 0) return 0;
+    if (Arena* a = tl_arena) {
+      const size_t off = (a->used + 255u) & ~(size_t)255u;
+      if (off > a->cap || b > a->cap - off) {
+        std::fprintf(stderr, "[dance_hip] scratch arena exhausted: %zu bytes requested, %zu of %zu in use\n", b,
+                     a->used, a->cap);
+        return -1;
+      }
+      p = a->base + off;
+      a->used = off + b;
+      borrowed = true;
+      return 0;
+    }
     hipError_t e = hipMalloc(&p, b);
     if (e != hipSuccess) {
       std::fprintf(stderr, "[dance_hip] hipMalloc(%zu) failed: %s\n", b, hipGetErrorString(e));

@@ -106,12 +106,12 @@ struct State {
     return GraphBufs{N, R, C, cur.as<uint32_t>(), deg_cur.as<uint32_t>(), work.as<uint32_t>(),
                      deg_work.as<uint32_t>(), wd.as<float>()};
   }
-  int alloc(uint32_t N_, uint32_t R_, uint32_t C_, bool with_cur = true) {
+  int alloc(uint32_t N_, uint32_t R_, uint32_t C_, bool with_cur = true, bool with_deg = true) {
     N = N_;
     R = R_;
     C = C_;
     if (with_cur) DCHECK(cur.alloc((size_t)N * R * 4));
-    DCHECK(deg_cur.alloc((size_t)N * 4));
+    if (with_deg) DCHECK(deg_cur.alloc((size_t)N * 4));
     DCHECK(work.alloc((size_t)N * C * 4));
     DCHECK(deg_work.alloc((size_t)N * 4));
     DCHECK(wd.alloc((size_t)N * C * 4));
@@ -303,17 +303,22 @@ static uint32_t locality_cells() {
   return 1024;
 }
 
+// Pivot k of K is row floor(k N / K) (evenly spaced).
+static __global__ void k_pivots(uint32_t N, uint32_t K, uint32_t* __restrict__ piv) {
+  const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k < K) piv[k] = (uint32_t)(((uint64_t)k * N) / K);
+}
+
 static int build_schedule(const Rows& rows, const QBoundSet& qb, ReverseWs& ws, hipStream_t s,
                           const uint32_t** order_out) {
   const uint32_t N = rows.N;
   const uint32_t K = std::min(locality_cells(), N);
   *order_out = nullptr;
   if (K < 2) return 0;
-  std::vector<uint32_t> piv(K);
-  for (uint32_t k = 0; k < K; ++k) piv[k] = (uint32_t)(((uint64_t)k * N) / K);
   DevBuf dpiv;
   DCHECK(dpiv.alloc(K * 4));
-  DHIP(hipMemcpyAsync(dpiv.p, piv.data(), K * 4, hipMemcpyHostToDevice, s));
+  hipLaunchKernelGGL(k_pivots, dim3((K + 255) / 256), dim3(256), 0, s, N, K, dpiv.as<uint32_t>());
+  DHIP(hipGetLastError());
   const int cpl = pick_cpl(rows.rs.nch);
   uint32_t* kb[2] = {ws.keys[0].as<uint32_t>(), ws.keys[1].as<uint32_t>()};
   uint32_t* vb[2] = {ws.vals[0].as<uint32_t>(), ws.vals[1].as<uint32_t>()};
@@ -349,18 +354,28 @@ static int build_schedule(const Rows& rows, const QBoundSet& qb, ReverseWs& ws, 
 // ---------------------------------------------------------------------------
 // Full build on resident rows.
 // ---------------------------------------------------------------------------
+// Stage timing events. With `on` false (the allocation-free entry) no event is
+// created: make() returns null, record() does nothing and the stage times
+// read 0.
 struct StageEvents {
+  bool on = true;
   std::vector<hipEvent_t> ev;
   ~StageEvents() {
     for (auto e : ev) (void)hipEventDestroy(e);
   }
-  hipEvent_t make() {
-    hipEvent_t e = nullptr;
-    if (hipEventCreate(&e) != hipSuccess) return nullptr;
-    ev.push_back(e);
-    return e;
+  int make(hipEvent_t* e) {
+    *e = nullptr;
+    if (!on) return 0;
+    DHIP(hipEventCreate(e));
+    ev.push_back(*e);
+    return 0;
   }
 };
+
+static int record(hipEvent_t e, hipStream_t s) {
+  if (e) DHIP(hipEventRecord(e, s));
+  return 0;
+}
 
 static float elapsed_ms(hipEvent_t a, hipEvent_t b) {
   float ms = 0.f;
@@ -407,13 +422,14 @@ static int validate(uint32_t N, uint32_t dim, uint32_t R, uint32_t L, uint32_t C
 // Runs the whole build. On success st.cur/deg_cur hold the graph.
 // Callers hold g_mu and pass the active profile.
 static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint32_t STEPS, const Profile& prof,
-                     State& st, hipStream_t s, GPUVamanaStats* stats, DanceKernelProfile* kp, uint32_t* medoid_out) {
+                     State& st, hipStream_t s, GPUVamanaStats* stats, DanceKernelProfile* kp, uint32_t* medoid_out,
+                     bool timed = true) {
   const uint32_t N = rows.N;
   if (pick_cpl(rows.rs.nch) < 0) {
     std::fprintf(stderr, "[gpu_vamana_build] dim=%u is beyond the supported row width\n", rows.dim);
     return -1;
   }
-  DCHECK(st.alloc(N, R, C, st.cur.p == nullptr));
+  DCHECK(st.alloc(N, R, C, st.cur.p == nullptr, st.deg_cur.p == nullptr));
   ReverseWs rws;
   DCHECK(rws.alloc(N, R));
   DevBuf ctr_buf, scores, cands;
@@ -422,9 +438,12 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   VCounters* ctr = ctr_buf.as<VCounters>();
   GraphBufs g = st.g();
   StageEvents E;
-  hipEvent_t e0 = E.make(), e_med = E.make(), e_init = E.make();
-  if (!e0 || !e_med || !e_init) return -1;
-  DHIP(hipEventRecord(e0, s));
+  E.on = timed;
+  hipEvent_t e0, e_med, e_init;
+  DCHECK(E.make(&e0));
+  DCHECK(E.make(&e_med));
+  DCHECK(E.make(&e_init));
+  DCHECK(record(e0, s));
 
   // Approximate medoid (vnew2.cu:2359-2479): device scores, host top-1.
   const double t_med = now_sec();
@@ -432,11 +451,11 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   DCHECK(scores.alloc(nc * 4));
   DCHECK(cands.alloc(nc * 4));
   DCHECK(launch_medoid(rows, s, scores.as<float>(), cands.as<uint32_t>(), nc, ns));
-  std::vector<float> hs(nc);
-  std::vector<uint32_t> hc(nc);
-  DHIP(hipMemcpyAsync(hs.data(), scores.p, nc * 4, hipMemcpyDeviceToHost, s));
-  DHIP(hipMemcpyAsync(hc.data(), cands.p, nc * 4, hipMemcpyDeviceToHost, s));
-  DHIP(hipEventRecord(e_med, s));
+  float hs[kMedoidCandidates];
+  uint32_t hc[kMedoidCandidates];
+  DHIP(hipMemcpyAsync(hs, scores.p, nc * 4, hipMemcpyDeviceToHost, s));
+  DHIP(hipMemcpyAsync(hc, cands.p, nc * 4, hipMemcpyDeviceToHost, s));
+  DCHECK(record(e_med, s));
   DHIP(hipStreamSynchronize(s));
   uint32_t best = DANCE_INV;
   float bs = FLT_MAX;
@@ -455,19 +474,18 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   const uint32_t* order = nullptr;
   DCHECK(build_schedule(rows, qb, rws, s, &order));
   const uint32_t q_iters = qbound_iters(), q_prune_iters = qbound_prune_iters();
-  DHIP(hipEventRecord(e_init, s));
+  DCHECK(record(e_init, s));
 
   struct IterEv {
     hipEvent_t s0, s1, r1, m1, p1;
   };
-  std::vector<IterEv> iev(kIters);
+  IterEv iev[kIters];
   for (auto& ie : iev) {
-    ie.s0 = E.make();
-    ie.s1 = E.make();
-    ie.r1 = E.make();
-    ie.m1 = E.make();
-    ie.p1 = E.make();
-    if (!ie.s0 || !ie.s1 || !ie.r1 || !ie.m1 || !ie.p1) return -1;
+    DCHECK(E.make(&ie.s0));
+    DCHECK(E.make(&ie.s1));
+    DCHECK(E.make(&ie.r1));
+    DCHECK(E.make(&ie.m1));
+    DCHECK(E.make(&ie.p1));
   }
   for (uint32_t it = 0; it < kIters; ++it) {
     const float alpha = (it + 1 >= kIters) ? kAlpha : 1.0f;
@@ -475,27 +493,28 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     if (it < kCoarseIters && steps > kWarmupSteps) steps = kWarmupSteps;
     if (verbose())
       std::printf("[gpu_vamana_build] iteration %u / %u, alpha=%.3f\n", it + 1, kIters, (double)alpha);
-    DHIP(hipEventRecord(iev[it].s0, s));
+    DCHECK(record(iev[it].s0, s));
     const QBoundSet qb_it = ((q_iters >> it) & 1u) ? qb : QBoundSet{nullptr, 0.0f, 0.0f};
     DCHECK(launch_search(rows, g, L, steps, alpha, start, order, ctr, qb_it, s));
-    DHIP(hipEventRecord(iev[it].s1, s));
+    DCHECK(record(iev[it].s1, s));
     const uint32_t* srcs = nullptr;
     DCHECK(build_reverse_csr(g, rws, s, &srcs));
-    DHIP(hipEventRecord(iev[it].r1, s));
+    DCHECK(record(iev[it].r1, s));
     DCHECK(launch_merge(rows, g, rws.offs.as<uint32_t>(), srcs, rws.snap.as<float>(), prof, order, ctr, s));
-    DHIP(hipEventRecord(iev[it].m1, s));
+    DCHECK(record(iev[it].m1, s));
     const uint32_t md = (it + 1 == kIters) ? kFinalMinDegree : 0u;
     const QBoundSet qp_it = ((q_prune_iters >> it) & 1u) ? qb : QBoundSet{nullptr, 0.0f, 0.0f};
     DCHECK(launch_prune(rows, g, md, alpha, order, ctr, qp_it, s));
-    DHIP(hipEventRecord(iev[it].p1, s));
+    DCHECK(record(iev[it].p1, s));
   }
   DHIP(hipStreamSynchronize(s));
   DHIP(hipGetLastError());
 
   VCounters hc_ctr{};
   {
-    std::vector<VCounters> stripes(kCtrStripes);
-    DHIP(hipMemcpy(stripes.data(), ctr_buf.p, sizeof(VCounters) * kCtrStripes, hipMemcpyDeviceToHost));
+    VCounters stripes[kCtrStripes];
+    DHIP(hipMemcpyAsync(stripes, ctr_buf.p, sizeof(VCounters) * kCtrStripes, hipMemcpyDeviceToHost, s));
+    DHIP(hipStreamSynchronize(s));
     static_assert(sizeof(VCounters) % sizeof(unsigned long long) == 0, "VCounters holds u64 fields only");
     const size_t nf = sizeof(VCounters) / sizeof(unsigned long long);
     auto* dst = reinterpret_cast<unsigned long long*>(&hc_ctr);
@@ -725,6 +744,140 @@ using namespace dance;
 // ===========================================================================
 // Reference ABI
 // ===========================================================================
+// ---------------------------------------------------------------------------
+// Device-resident build, and its allocation-free form.
+// ---------------------------------------------------------------------------
+
+// Scratch of the allocation-free build: one array per GPU, held until the
+// process ends. Host code never passes `scratch` itself to the device (the
+// name is a host-side stand-in); it uses the address hipGetSymbolAddress
+// returns on each device (scratch_base). Calls of the allocation-free entry
+// share that array; the library lock serialises them within a process.
+constexpr size_t kScratchBytes = 256ull << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+
+// Device address of this GPU's scratch array (looked up once per device, with
+// that device current). Callers hold g_mu.
+static int scratch_base(void** out) {
+  int dev = 0;
+  DHIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) {
+    std::fprintf(stderr, "[gpu_vamana_build] device %d is beyond the scratch table\n", dev);
+    return -1;
+  }
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    DHIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+// Upper bound of the device bytes a resident build takes from the arena: the
+// same buffers run_build, setup_rows and the radix sort allocate, each rounded
+// up to the arena's 256-byte alignment.
+static size_t resident_build_bytes(const void* d_data, int dtype, int store, uint32_t N, uint32_t dim, uint32_t R,
+                                   uint32_t C) {
+  size_t total = 0;
+  auto add = [&](size_t b) { total += (b + 255u) & ~(size_t)255u; };
+  const size_t row_bytes = (size_t)dim * elem_bytes(store);
+  const int cpl = pick_cpl((uint32_t)((row_bytes + 15) / 16));
+  const size_t stride = (size_t)8 * (size_t)cpl * 16;
+  if (!(dtype == store && stride == row_bytes && (reinterpret_cast<uintptr_t>(d_data) & 15u) == 0))
+    add(stride * N);  // padded or converted rows
+  const size_t items = std::max<size_t>((size_t)N * R, 1);
+  add((size_t)N * 4);               // deg_work
+  add((size_t)N * C * 4);           // work
+  add((size_t)N * C * 4);           // wd
+  for (int i = 0; i < 5; ++i) add(items * 4);  // keys[2], vals[2], snap
+  add(((size_t)N + 1) * 4);         // offs
+  add(sizeof(VCounters) * kCtrStripes);
+  add(kMedoidCandidates * 4);       // scores
+  add(kMedoidCandidates * 4);       // cands
+  add((size_t)N * kQChunks * 16);   // code rows of the bound
+  add((size_t)std::min(locality_cells(), N) * 4);  // pivots
+  add((size_t)N * 4);               // order
+  for (size_t n : {(size_t)N, items}) {  // the schedule's sort, then the reverse sort
+    const size_t tiles = (n + kRadixTile - 1) / kRadixTile;
+    add(tiles * 256 * 4);           // histograms
+    size_t levels = 0, m = tiles * 256;
+    while (true) {
+      const size_t t = (m + kScanTile - 1) / kScanTile;
+      levels += t;
+      if (t <= 1) break;
+      m = t;
+    }
+    add(std::max<size_t>(levels * 4, 256));  // scan partials
+  }
+  return total;
+}
+
+// Build on device rows into the caller's device graph (N x R) and degrees
+// (N). With noalloc, every device buffer comes from this GPU's scratch array,
+// the work runs on the null stream and no timing event is created (the stage
+// times of the kernel profile read 0; its counters are kept). Callers hold g_mu.
+static int resident_build(const void* d_data, int dtype, uint32_t N, uint32_t dim, uint32_t R, uint32_t L,
+                          uint32_t C, uint32_t STEPS, uint32_t* d_graph, uint32_t* d_degree, bool noalloc) {
+  if (d_data == nullptr || d_graph == nullptr || d_degree == nullptr) {
+    std::fprintf(stderr, "[gpu_vamana_build] null input pointer.\n");
+    return -1;
+  }
+  if (dtype != DANCE_F32 && dtype != DANCE_U8 && dtype != DANCE_F16) {
+    std::fprintf(stderr, "[gpu_vamana_build] unsupported dtype %d\n", dtype);
+    return -1;
+  }
+  DCHECK(validate(N, dim, R, L, C, STEPS));
+  const double t0 = now_sec();
+  const Profile prof = kProfiles[profile_index_locked()];
+  const int store = (dtype == DANCE_F32 && prof.fp16) ? DANCE_F16 : dtype;
+  DCHECK(check_width(dim, store));
+  Arena arena;
+  if (noalloc) {
+    const size_t need = resident_build_bytes(d_data, dtype, store, N, dim, R, C);
+    if (need > kScratchBytes) {
+      std::fprintf(stderr,
+                   "[gpu_vamana_build] allocation-free build: N=%u dim=%u R=%u C=%u needs %zu bytes of scratch, "
+                   "above its maximum of %zu bytes\n",
+                   N, dim, R, C, need, kScratchBytes);
+      return -1;
+    }
+    void* base = nullptr;
+    DCHECK(scratch_base(&base));
+    arena = Arena{static_cast<char*>(base), kScratchBytes, 0};
+  }
+  ArenaScope scope(noalloc ? &arena : tl_arena);
+  hipStream_t s = nullptr;  // the null stream unless a stream of our own is made
+  if (!noalloc) DHIP(hipStreamCreate(&s));
+  struct StreamGuard {
+    hipStream_t s;
+    ~StreamGuard() {
+      if (s) (void)hipStreamDestroy(s);
+    }
+  } sg{s};
+  Rows rows;
+  DCHECK(setup_rows(rows, d_data, true, dtype, store, N, dim, s));
+  State st;
+  // The caller's graph and degree buffers are the build's current graph.
+  st.cur.p = d_graph;
+  st.deg_cur.p = d_degree;
+  GPUVamanaStats stats{};
+  DanceKernelProfile kp{};
+  uint32_t medoid = 0;
+  int r = run_build(rows, R, L, C, STEPS, prof, st, s, &stats, &kp, &medoid, !noalloc);
+  st.cur.release();
+  st.deg_cur.release();
+  if (r != 0) return r;
+  DHIP(hipStreamSynchronize(s));
+  stats.gpu_build_seconds = now_sec() - t0;
+  g_last_stats = stats;
+  g_last_medoid = medoid;
+  g_last_prof = kp;
+  return 0;
+}
+
 extern "C" {
 
 int gpu_vamana_vnew2_build(const uint8_t* h_data, uint32_t N, uint32_t dim, uint32_t R, uint32_t L, uint32_t C,
@@ -794,45 +947,14 @@ void gpu_vamana_get_last_stats(GPUVamanaStats* stats) {
 int dance_vamana_build_resident(const void* d_data, int dtype, uint32_t N, uint32_t dim, uint32_t R, uint32_t L,
                                 uint32_t C, uint32_t STEPS, uint32_t* d_graph, uint32_t* d_degree) {
   std::lock_guard<std::mutex> lk(g_mu);
-  if (d_data == nullptr || d_graph == nullptr || d_degree == nullptr) {
-    std::fprintf(stderr, "[gpu_vamana_build] null input pointer.\n");
-    return -1;
-  }
-  if (dtype != DANCE_F32 && dtype != DANCE_U8 && dtype != DANCE_F16) {
-    std::fprintf(stderr, "[gpu_vamana_build] unsupported dtype %d\n", dtype);
-    return -1;
-  }
-  DCHECK(validate(N, dim, R, L, C, STEPS));
-  const double t0 = now_sec();
-  const Profile prof = kProfiles[profile_index_locked()];
-  const int store = (dtype == DANCE_F32 && prof.fp16) ? DANCE_F16 : dtype;
-  DCHECK(check_width(dim, store));
-  hipStream_t s = nullptr;
-  DHIP(hipStreamCreate(&s));
-  struct StreamGuard {
-    hipStream_t s;
-    ~StreamGuard() {
-      if (s) (void)hipStreamDestroy(s);
-    }
-  } sg{s};
-  Rows rows;
-  DCHECK(setup_rows(rows, d_data, true, dtype, store, N, dim, s));
-  State st;
-  // The caller's graph/degree buffers are the build's current graph.
-  st.cur.p = d_graph;
-  GPUVamanaStats stats{};
-  DanceKernelProfile kp{};
-  uint32_t medoid = 0;
-  int r = run_build(rows, R, L, C, STEPS, prof, st, s, &stats, &kp, &medoid);
-  st.cur.release();
-  if (r != 0) return r;
-  DHIP(hipMemcpyAsync(d_degree, st.deg_cur.p, (size_t)N * 4, hipMemcpyDeviceToDevice, s));
-  DHIP(hipStreamSynchronize(s));
-  stats.gpu_build_seconds = now_sec() - t0;
-  g_last_stats = stats;
-  g_last_medoid = medoid;
-  g_last_prof = kp;
-  return 0;
+  return resident_build(d_data, dtype, N, dim, R, L, C, STEPS, d_graph, d_degree, false);
+}
+
+int dance_vamana_build_resident_noalloc(const void* d_data, int dtype, uint32_t N, uint32_t dim, uint32_t R,
+                                        uint32_t L, uint32_t C, uint32_t STEPS, uint32_t* d_graph,
+                                        uint32_t* d_degree) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return resident_build(d_data, dtype, N, dim, R, L, C, STEPS, d_graph, d_degree, true);
 }
 
 void dance_get_last_kernel_profile(DanceKernelProfile* p) {

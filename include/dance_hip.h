@@ -50,6 +50,22 @@ typedef struct DanceKernelProfile {
 int dance_vamana_build_resident(const void *d_data, int dtype, uint32_t num_points, uint32_t dim, uint32_t R,
                                 uint32_t L, uint32_t C, uint32_t STEPS, uint32_t *d_graph, uint32_t *d_degree);
 
+/* dance_vamana_build_resident without any device allocation. No counterpart
+ * in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Every buffer the build needs beyond the caller's inputs and
+ * outputs comes from a per-GPU scratch array of 256 MiB that the library
+ * holds until the process ends (at R=64, C=80, fp32 rows of 96 dimensions
+ * that is about 120k vertices). Larger inputs return -1 with a message. The
+ * work runs on the null stream and creates no event, so the stage times of
+ * dance_get_last_kernel_profile read 0 after it (the counters are kept).
+ * Calls share their GPU's scratch array and keep nothing from one call to the
+ * next; the library lock serialises calls within a process. Same algorithm,
+ * parameters, results and errors as dance_vamana_build_resident. */
+int dance_vamana_build_resident_noalloc(const void *d_data, int dtype, uint32_t num_points, uint32_t dim,
+                                        uint32_t R, uint32_t L, uint32_t C, uint32_t STEPS, uint32_t *d_graph,
+                                        uint32_t *d_degree);
+
 /* Timings and counters of the last build on this process. */
 void dance_get_last_kernel_profile(DanceKernelProfile *profile);
 
