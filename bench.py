@@ -304,6 +304,90 @@ def run_c5(args, mode) -> int:
     return 0
 
 
+LS = (10, 20, 50, 100, 200)
+GATE_TOL = 0.005  # north star: recall@10 >= CPU Vamana - 0.005 at equal R, L, alpha
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def graph_check(torch, graph_t, deg_t, n: int, R: int) -> dict:
+    """Counts what no valid graph may hold: neighbour ids >= N, self loops,
+    repeated neighbours in a row, non-INVALID slots past the degree."""
+    from dance_amd import INVALID
+    g = graph_t.long() & 0xFFFFFFFF
+    d = deg_t.long()
+    col = torch.arange(R, device=g.device)[None, :]
+    live = col < d[:, None]
+    rows = torch.arange(n, device=g.device)[:, None]
+    invalid = int((live & (g >= n)).sum())
+    selfl = int((live & (g == rows)).sum())
+    pad = int((~live & (g != INVALID)).sum())
+    srt = torch.sort(torch.where(live, g, (-col - 1).expand_as(g)), dim=1).values
+    dup = int((srt[:, 1:] == srt[:, :-1]).sum())
+    del g, srt, live
+    out = {"invalid": invalid, "self_loops": selfl, "duplicates": dup, "bad_padding": pad,
+           "min_degree": int(d.min()), "max_degree": int(d.max()), "mean_degree": round(float(d.float().mean()), 3)}
+    out["ok"] = invalid == selfl == dup == pad == 0 and out["max_degree"] <= R and out["min_degree"] >= 1
+    return out
+
+
+def recall_curve(D, data, graph, degree, start, queries, gt) -> dict:
+    """recall@10 of GPU best-first search (dance_search) over a host graph."""
+    out = {}
+    for Ls in LS:
+        found, _ = D.search(data, graph, degree, start, queries, 10, Ls)
+        out[f"L{Ls}"] = round(D.recall_at_k(found, gt, 10), 4)
+    return out
+
+
+def gate(gpu: dict, cpu: dict) -> dict:
+    delta = {k: round(gpu[k] - cpu[k], 4) for k in gpu}
+    ok = {k: gpu[k] >= cpu[k] - GATE_TOL for k in gpu}
+    return {"gpu": gpu, "cpu_vamana": cpu, "delta": delta, "pass": ok, "all_pass": all(ok.values())}
+
+
+def cpu_leg(torch, D, O, cfg: dict, name: str, base: np.ndarray, queries: np.ndarray, m: int, nq: int,
+            with_port: bool) -> dict:
+    """On the first m rows of a workload: times the CPU Vamana (and the CPU
+    oracle of this algorithm), builds the same rows on the GPU through the C
+    ABI, checks the GPU graph against the oracle's, and scores both graphs'
+    recall@10 with the same GPU search against exact ground truth."""
+    sample = np.ascontiguousarray(base[:m])
+    R, L, C_, S = cfg["R"], cfg["L"], cfg["C"], cfg["STEPS"]
+    os.environ["DANCE_ORACLE_PROGRESS"] = "1"  # the CPU build reports each tenth of its points
+    t0 = time.perf_counter()
+    gc, dc, sc = O.cpu_vamana_build(sample, R, L, 1.2, 750)
+    t_cpu = time.perf_counter() - t0
+    log(f"{name}: CPU Vamana on {m} rows in {t_cpu:.1f}s")
+    res = D.vamana_build(sample, R, L, C_, S)
+    out = {"rows": m, "cpu_vamana_seconds": round(t_cpu, 2)}
+    if with_port:
+        t0 = time.perf_counter()
+        go, do, mo = O.vnew2_build(sample, R, L, C_, S)
+        t_port = time.perf_counter() - t0
+        log(f"{name}: CPU oracle on {m} rows in {t_port:.1f}s")
+        out["oracle_seconds"] = round(t_port, 2)
+        out["gpu_graph_equals_oracle"] = bool(np.array_equal(res.graph, go) and np.array_equal(res.degree, do)
+                                              and res.medoid == mo)
+    q = queries[:nq]
+    st = torch.from_numpy(sample).to(torch.device("cuda:0"))
+    gt = ground_truth(st, sample, q)
+    del st
+    out["recall_gate"] = gate(recall_curve(D, sample, res.graph, res.degree, res.medoid, q, gt),
+                              recall_curve(D, sample, gc, dc, sc, q, gt))
+    log(f"{name}: gate {out['recall_gate']['delta']} pass={out['recall_gate']['all_pass']}")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -313,7 +397,13 @@ def main() -> int:
     ap.add_argument("--n", type=int, default=None, help="override N (parity/debug runs)")
     ap.add_argument("--recall-queries", type=int, default=1000)
     ap.add_argument("--cpu-sample", type=int, default=200_000,
-                    help="vectors in the CPU baseline sample (about 20 s on 16 host cores); 0 disables it")
+                    help="rows of the workload in the CPU baseline sample (CPU Vamana and the CPU oracle, timed "
+                         "on this host's cores; the recall gate is scored on it); 0 disables the CPU legs")
+    ap.add_argument("--port-max", type=int, default=200_000,
+                    help="largest sample on which the CPU oracle of this algorithm is also timed")
+    ap.add_argument("--gate-c1", type=int, default=1, help="also score the recall gate on c1 (100k, CPU Vamana)")
+    ap.add_argument("--abi", type=int, default=1,
+                    help="also time one build through the host-buffer C ABI (H2D and D2H included)")
     ap.add_argument("--profile", default="QUALITY")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="run one device copy of this size first (HBM counter calibration)")
@@ -333,18 +423,19 @@ def main() -> int:
     D.set_profile(args.profile)
     cfg = dict(D.CONFIGS[args.config])
     n = args.n or cfg["n"]
+    R = cfg["R"]
     t0 = time.time()
     base, queries = D.make_workload(cfg, n=n)
     log(f"generated {args.config} N={n} dim={cfg['dim']} in {time.time() - t0:.1f}s")
     dev = torch.device("cuda:0")
     base_t = torch.from_numpy(base).to(dev)
-    graph_t = torch.empty((n, cfg["R"]), dtype=torch.int32, device=dev)
+    graph_t = torch.empty((n, R), dtype=torch.int32, device=dev)
     deg_t = torch.empty((n,), dtype=torch.int32, device=dev)
     dcode = D.DTYPE_F32 if base.dtype == np.float32 else D.DTYPE_U8
     torch.cuda.synchronize()
 
     def step():
-        D.vamana_build_resident(base_t.data_ptr(), dcode, n, cfg["dim"], cfg["R"], cfg["L"], cfg["C"],
+        D.vamana_build_resident(base_t.data_ptr(), dcode, n, cfg["dim"], R, cfg["L"], cfg["C"],
                                 cfg["STEPS"], graph_t.data_ptr(), deg_t.data_ptr())
 
     copy_calibration(torch, dev, args.copy_calibration_mib)
@@ -363,48 +454,89 @@ def main() -> int:
     ms_per_step = elapsed * 1000.0 / args.steps
     value = n / (ms_per_step / 1000.0)
     kp = profs[-1]
-    stats = D.last_stats()
+    medoid = int(D.lib().gpu_vamana_vnew2_get_last_medoid())
+    check = graph_check(torch, graph_t, deg_t, n, R)
+    log(f"graph check {check}")
 
-    # Roofline of the dominant kernel: search + online insert.
-    search_launches = kp["iterations"]
-    avg_ms = kp["search_ms"] / search_launches
-    bytes_per_launch = kp["search_bytes"] / search_launches
-    achieved = bytes_per_launch / (avg_ms * 1e-3) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "k_search (search + online robust insert)",
-                "avg_launch_ms": round(avg_ms, 3), "algorithmic_bytes_per_launch": bytes_per_launch}
+    # Roofline of the dominant kernel (search + online insert): measured HBM
+    # bytes per launch (committed counter profile of the same workload) over
+    # the live mean launch time; the device-counted algorithmic bytes are
+    # reported beside it, with their ratio to the measured bytes.
+    launches = kp["iterations"]
+    avg_ms = kp["search_ms"] / launches
+    algo = kp["search_bytes"] / launches
+    roofline = {"bound": "hbm", "achieved": None, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": None,
+                "traffic": None, "kernel": "k_search (search + online robust insert)",
+                "avg_launch_ms": round(avg_ms, 3), "launches": launches,
+                "algorithmic_bytes_per_launch": algo,
+                "algorithmic_GBps": round(algo / (avg_ms * 1e-3) / 1e9, 1)}
     traffic_file = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
-    if os.path.exists(traffic_file) and args.n is None:
+    if os.path.exists(traffic_file) and args.n is None and args.profile == "QUALITY":
         with open(traffic_file) as f:
-            roofline["traffic"] = json.load(f).get("search_hbm_bytes_per_launch")
+            tj = json.load(f)
+        per = [l["read_bytes"] + l["write_bytes"] for l in tj["search_launches"]]
+        traffic = sum(per) / len(per)
+        achieved = traffic / (avg_ms * 1e-3) / 1e9
+        roofline.update({"achieved": round(achieved, 1), "frac": round(achieved / HBM_PEAK_GBS, 4),
+                         "traffic": traffic, "traffic_source": tj["source"],
+                         "algorithmic_over_traffic": round(algo / traffic, 3)})
 
-    # Recall@10 on a query subset: GPU best-first search over the resident
-    # graph (dance_search_resident) against exact ground truth.
+    # Recall@10 of the resident graph on a query subset.
     nq = min(args.recall_queries, queries.shape[0])
     recall = {}
     if nq > 0:
         t0 = time.time()
         gt = ground_truth(base_t, base, queries[:nq])
-        medoid = int(D.lib().gpu_vamana_vnew2_get_last_medoid())
-        for Ls in (10, 20, 50, 100, 200):
+        for Ls in LS:
             found, _ = D.search_resident(base_t.data_ptr(), dcode, n, cfg["dim"], graph_t.data_ptr(),
-                                         deg_t.data_ptr(), cfg["R"], medoid, queries[:nq], 10, Ls)
+                                         deg_t.data_ptr(), R, medoid, queries[:nq], 10, Ls)
             recall[f"L{Ls}"] = round(D.recall_at_k(found, gt, 10), 4)
         log(f"recall {recall} ({time.time() - t0:.1f}s)")
 
-    cpu = None
-    if args.cpu_sample > 0:
-        from oracle import oracle as O  # the CPU baseline leg only
-        m = min(args.cpu_sample, n)
-        sample = np.ascontiguousarray(base[:m])
+    # The same build through the host-buffer C ABI (gpu_vamana_vnew2_build*),
+    # whose time includes the H2D and D2H copies, as the reference's
+    # gpu_build_seconds does (vnew2.cu:2174, 2838).
+    abi = None
+    if args.abi:
         t0 = time.perf_counter()
-        O.vnew2_build(sample, cfg["R"], cfg["L"], cfg["C"], cfg["STEPS"])
-        dt = time.perf_counter() - t0
-        cpu = {"value": round(m / dt, 1), "unit": "vertices/s", "cores": O.num_threads(), "kind": "port",
-               "sample": f"first {m} vectors of the same workload, full vnew2 build (CPU oracle, OpenMP)",
-               "seconds": round(dt, 2)}
-        log(f"cpu baseline {cpu}")
+        res = D.vamana_build(base, R, cfg["L"], cfg["C"], cfg["STEPS"])
+        wall = time.perf_counter() - t0
+        st = res.stats
+        same = bool(np.array_equal(res.degree, deg_t.cpu().numpy().view(np.uint32))
+                    and np.array_equal(res.graph, graph_t.cpu().numpy().view(np.uint32)))
+        abi = {"seconds": round(wall, 3), "gpu_build_seconds": round(st["gpu_build_seconds"], 3),
+               "h2d_seconds": round(st["h2d_seconds"], 3), "d2h_seconds": round(st["d2h_seconds"], 3),
+               "vertices_per_s": round(n / wall, 1), "graph_equals_resident": same}
+        del res
+        log(f"abi {abi}")
+
+    cpu = None
+    gates = {}
+    if args.cpu_sample > 0:
+        from oracle import oracle as O  # the CPU baseline legs only
+        m = min(args.cpu_sample, n)
+        leg = cpu_leg(torch, D, O, cfg, args.config, base, queries, m, nq or 1000, with_port=m <= args.port_max)
+        port = None
+        if "oracle_seconds" in leg:
+            port = {"value": round(m / leg["oracle_seconds"], 1), "seconds": leg["oracle_seconds"],
+                    "what": "CPU oracle of this build's algorithm (oracle/vamana_oracle.cpp), same sample, same cores",
+                    "gpu_graph_equals_oracle": leg["gpu_graph_equals_oracle"]}
+        cpu = {"value": round(m / leg["cpu_vamana_seconds"], 1), "unit": "vertices/s", "cores": O.num_threads(),
+               "kind": "port", "cpu_model": cpu_model(),
+               "sample": (f"first {m} rows of the {args.config} workload; DiskANN's in-memory Vamana build "
+                          f"(R{R} L{cfg['L']} alpha 1.2, maxc 750) restated in C++/OpenMP "
+                          "(oracle/cpu_baselines.cpp); Microsoft DiskANN itself is not available offline"),
+               "seconds": leg["cpu_vamana_seconds"], "oracle_port": port}
+        gates[f"{args.config}_first_{m}"] = leg["recall_gate"]
+        if args.gate_c1 and args.config != "c1":
+            c1 = D.CONFIGS["c1"]
+            b1, q1 = D.make_workload(c1)
+            gates["c1"] = cpu_leg(torch, D, O, c1, "c1", b1, q1, c1["n"], min(1000, q1.shape[0]),
+                                  with_port=False)["recall_gate"]
+        rec_file = os.path.join(ROOT, "profiles", "recall_gate_c2.json")
+        if args.config != "c2" and os.path.exists(rec_file):
+            with open(rec_file) as f:
+                gates["c2 (recorded)"] = json.load(f)
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "vertices/s", "n_gpus": 1, "steps": args.steps,
@@ -412,10 +544,13 @@ def main() -> int:
         "scaling": "weak", "vs_baseline": None, "dtype": "f32" if dcode == D.DTYPE_F32 else "u8",
         "data": "synthetic",
         "config": {"workload": WORKLOADS[args.config] + (f" (N overridden to {n})" if args.n else ""),
-                   "N": n, "dim": cfg["dim"], "R": cfg["R"], "L": cfg["L"], "C": cfg["C"], "STEPS": cfg["STEPS"],
+                   "N": n, "dim": cfg["dim"], "R": R, "L": cfg["L"], "C": cfg["C"], "STEPS": cfg["STEPS"],
                    "alpha": 1.2, "profile": args.profile},
         "build_seconds": round(ms_per_step / 1000.0, 3),
+        "graph_check": check,
         "recall@10": recall,
+        "recall_gate": gates or None,
+        "abi": abi,
         "stage_ms": {k: round(kp[k], 2) for k in ("medoid_ms", "init_ms", "search_ms", "reverse_ms", "merge_ms",
                                                      "prune_ms", "total_ms")},
         "counters": {k: kp[k] for k in ("search_dist", "insert_dist", "expansions", "vis_skips", "merge_dist",
@@ -427,7 +562,7 @@ def main() -> int:
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
-    return 0
+    return 0 if check["ok"] else 1
 
 
 if __name__ == "__main__":

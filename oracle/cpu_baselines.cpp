@@ -14,6 +14,9 @@
 //  * oracle_bruteforce_knn: exact top-k in double precision, ties by id.
 
 #include <algorithm>
+#include <atomic>
+#include <cstdio>
+#include <cstdlib>
 #include <cfloat>
 #include <cmath>
 #include <cstdint>
@@ -210,6 +213,10 @@ uint32_t oracle_cpu_vamana_build(const void* data, int dtype, uint32_t N, uint32
     }
   }
   const uint32_t slack = (uint32_t)std::ceil(1.3 * R);
+  // DANCE_ORACLE_PROGRESS set: a line on stderr per tenth of the points inserted
+  const bool progress = std::getenv("DANCE_ORACLE_PROGRESS") != nullptr;
+  const uint64_t tick = std::max<uint64_t>(1, N / 10);
+  std::atomic<uint64_t> inserted{0};
   std::vector<std::vector<uint32_t>> G(N);
   std::vector<std::mutex> locks(N);
   const int nt = omp_get_max_threads();
@@ -267,6 +274,9 @@ uint32_t oracle_cpu_vamana_build(const void* data, int dtype, uint32_t N, uint32
         G[n] = np;
       }
     }
+    const uint64_t done = inserted.fetch_add(1) + 1;
+    if (progress && done % tick == 0)
+      std::fprintf(stderr, "[cpu_vamana] %llu / %u points inserted\n", (unsigned long long)done, N);
   }
 #pragma omp parallel for schedule(dynamic, 256)
   for (int64_t nn = 0; nn < (int64_t)N; ++nn) {
