@@ -194,41 +194,18 @@ def run_c5(args, mode) -> int:
                                   c["C"], c["STEPS"], c["alpha"], INVALID, gstart, graph_t.data_ptr(),
                                   deg_t.data_ptr())
 
-    parts = []
+    off_s = pts_s = None
     if mode == "c5s":
-        off, pts = ls.postings()
-        parts = [torch.from_numpy(pts[off[l]:off[l + 1]].astype(np.int64)).to(dev) for l in range(ls.num_labels)]
+        off_s, pts_s = ls.postings()  # label -> ascending points
 
     def step_stitched():
-        # per label: gather the label's rows, standard build (Rsmall), remap
-        # local -> global on the device (rows are partitioned: one label each)
-        t_build = 0.0
-        medoids = np.zeros(ls.num_labels, np.uint32)
-        graph_t.fill_(-1)
-        deg_t.zero_()
-        for l, ids in enumerate(parts):
-            m = ids.numel()
-            if m == 0:
-                continue
-            xl = base_t[ids].contiguous()
-            gl = torch.empty((m, c["Rsmall"]), dtype=torch.int32, device=dev)
-            dl = torch.empty((m,), dtype=torch.int32, device=dev)
-            tb = time.perf_counter()
-            D.vamana_build_resident(xl.data_ptr(), D.DTYPE_U8, m, c["dim"], c["Rsmall"], c["Lsmall"], c["Cs"],
-                                    c["STEPS"], gl.data_ptr(), dl.data_ptr())
-            t_build += time.perf_counter() - tb
-            medoids[l] = int(ids[int(D.lib().gpu_vamana_vnew2_get_last_medoid())])
-            k = min(c["Rsmall"], c["Rstitched"])
-            loc = gl[:, :k].long()
-            ok = (loc >= 0) & (loc < m) & (torch.arange(k, device=dev)[None, :] < dl[:, None].long())
-            glob = torch.where(ok, ids[loc.clamp(0, m - 1)], torch.full_like(loc, -1))
-            # valid entries first, order kept (stable sort on the invalid flag)
-            order = torch.sort((~ok).to(torch.int8), dim=1, stable=True).indices
-            rows = torch.gather(glob, 1, order).to(torch.int32)
-            graph_t[ids, :k] = rows
-            deg_t[ids] = ok.sum(1).to(torch.int32)
-        stitched["gpu_build_sum_s"] = round(t_build, 3)
+        # dance_stitched_build_resident: per label, the rows are gathered, built
+        # (Rsmall) and remapped to global ids on the device
+        medoids = D.stitched_build_resident(base_t.data_ptr(), D.DTYPE_U8, n, c["dim"], off_s, pts_s, c["Rsmall"],
+                                            c["Lsmall"], c["Cs"], c["STEPS"], c["Rstitched"], c["R"],
+                                            graph_t.data_ptr(), deg_t.data_ptr())
         stitched["medoids"] = medoids
+        stitched["stats"] = D.last_stitched_stats()
 
     step = step_filtered if mode == "c5f" else step_stitched
     copy_calibration(torch, dev, args.copy_calibration_mib)
@@ -299,7 +276,8 @@ def run_c5(args, mode) -> int:
                                                   "out_degree_max", "out_degree_avg", "avg_common_label_out_degree",
                                                   "low_common_label_degree_count")}
     else:
-        line["stitched"] = {"gpu_build_sum_s": stitched["gpu_build_sum_s"], "labels": ls.num_labels}
+        sst = stitched["stats"]
+        line["stitched"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in sst.items()}
     print(json.dumps(line), flush=True)
     return 0
 
@@ -356,11 +334,13 @@ def gate(gpu: dict, cpu: dict) -> dict:
 
 
 def cpu_leg(torch, D, O, cfg: dict, name: str, base: np.ndarray, queries: np.ndarray, m: int, nq: int,
-            with_port: bool) -> dict:
+            with_port: bool, alpha_from: int = -1) -> dict:
     """On the first m rows of a workload: times the CPU Vamana (and the CPU
     oracle of this algorithm), builds the same rows on the GPU through the C
     ABI, checks the GPU graph against the oracle's, and scores both graphs'
-    recall@10 with the same GPU search against exact ground truth."""
+    recall@10 with the same GPU search against exact ground truth. With
+    alpha_from >= 0 the GPU build is also scored under the reference's alpha
+    schedule knob (DANCE_ALPHA_FROM_ITER: alpha from that iteration on)."""
     sample = np.ascontiguousarray(base[:m])
     R, L, C_, S = cfg["R"], cfg["L"], cfg["C"], cfg["STEPS"]
     os.environ["DANCE_ORACLE_PROGRESS"] = "1"  # the CPU build reports each tenth of its points
@@ -382,9 +362,21 @@ def cpu_leg(torch, D, O, cfg: dict, name: str, base: np.ndarray, queries: np.nda
     st = torch.from_numpy(sample).to(torch.device("cuda:0"))
     gt = ground_truth(st, sample, q)
     del st
-    out["recall_gate"] = gate(recall_curve(D, sample, res.graph, res.degree, res.medoid, q, gt),
-                              recall_curve(D, sample, gc, dc, sc, q, gt))
+    cpu_rec = recall_curve(D, sample, gc, dc, sc, q, gt)
+    out["recall_gate"] = gate(recall_curve(D, sample, res.graph, res.degree, res.medoid, q, gt), cpu_rec)
     log(f"{name}: gate {out['recall_gate']['delta']} pass={out['recall_gate']['all_pass']}")
+    if alpha_from >= 0:
+        os.environ["DANCE_ALPHA_FROM_ITER"] = str(alpha_from)
+        try:
+            ra = D.vamana_build(sample, R, L, C_, S)
+        finally:
+            del os.environ["DANCE_ALPHA_FROM_ITER"]
+        g2 = gate(recall_curve(D, sample, ra.graph, ra.degree, ra.medoid, q, gt), cpu_rec)
+        g2["schedule"] = f"alpha from iteration {alpha_from} (reference knob USE_ALPHA_FROM_FIRST_ITER / " \
+                         "VAMANA_ALPHA_FINAL_FROM_ITER)"
+        g2["gpu_build_seconds"] = round(ra.stats["gpu_build_seconds"], 3)
+        out["recall_gate_alpha_schedule"] = g2
+        log(f"{name}: gate with alpha from {alpha_from}: {g2['delta']} pass={g2['all_pass']}")
     return out
 
 
@@ -402,6 +394,9 @@ def main() -> int:
     ap.add_argument("--port-max", type=int, default=200_000,
                     help="largest sample on which the CPU oracle of this algorithm is also timed")
     ap.add_argument("--gate-c1", type=int, default=1, help="also score the recall gate on c1 (100k, CPU Vamana)")
+    ap.add_argument("--gate-alpha-from", type=int, default=0,
+                    help="also score the gates with alpha from this iteration on (the reference's "
+                         "USE_ALPHA_FROM_FIRST_ITER at 0); -1 disables")
     ap.add_argument("--abi", type=int, default=1,
                     help="also time one build through the host-buffer C ABI (H2D and D2H included)")
     ap.add_argument("--profile", default="QUALITY")
@@ -515,7 +510,8 @@ def main() -> int:
     if args.cpu_sample > 0:
         from oracle import oracle as O  # the CPU baseline legs only
         m = min(args.cpu_sample, n)
-        leg = cpu_leg(torch, D, O, cfg, args.config, base, queries, m, nq or 1000, with_port=m <= args.port_max)
+        leg = cpu_leg(torch, D, O, cfg, args.config, base, queries, m, nq or 1000, with_port=m <= args.port_max,
+                      alpha_from=args.gate_alpha_from)
         port = None
         if "oracle_seconds" in leg:
             port = {"value": round(m / leg["oracle_seconds"], 1), "seconds": leg["oracle_seconds"],
@@ -528,15 +524,21 @@ def main() -> int:
                           "(oracle/cpu_baselines.cpp); Microsoft DiskANN itself is not available offline"),
                "seconds": leg["cpu_vamana_seconds"], "oracle_port": port}
         gates[f"{args.config}_first_{m}"] = leg["recall_gate"]
+        if "recall_gate_alpha_schedule" in leg:
+            gates[f"{args.config}_first_{m}_alpha_from_{args.gate_alpha_from}"] = leg["recall_gate_alpha_schedule"]
         if args.gate_c1 and args.config != "c1":
             c1 = D.CONFIGS["c1"]
             b1, q1 = D.make_workload(c1)
-            gates["c1"] = cpu_leg(torch, D, O, c1, "c1", b1, q1, c1["n"], min(1000, q1.shape[0]),
-                                  with_port=False)["recall_gate"]
+            l1 = cpu_leg(torch, D, O, c1, "c1", b1, q1, c1["n"], min(1000, q1.shape[0]), with_port=False,
+                         alpha_from=args.gate_alpha_from)
+            gates["c1"] = l1["recall_gate"]
+            if "recall_gate_alpha_schedule" in l1:
+                gates[f"c1_alpha_from_{args.gate_alpha_from}"] = l1["recall_gate_alpha_schedule"]
         rec_file = os.path.join(ROOT, "profiles", "recall_gate_c2.json")
         if args.config != "c2" and os.path.exists(rec_file):
             with open(rec_file) as f:
-                gates["c2 (recorded)"] = json.load(f)
+                for k, v in json.load(f).items():
+                    gates[f"{k} (recorded)"] = v
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "vertices/s", "n_gpus": 1, "steps": args.steps,

@@ -123,6 +123,14 @@ class DanceSearchStats(C.Structure):
                 ("capped_queries", C.c_uint64)]
 
 
+class DanceStitchedStats(C.Structure):
+    _fields_ = ([(n, C.c_double) for n in ("setup_seconds", "materialize_seconds", "build_sum_seconds",
+                                           "build_max_seconds", "remap_seconds", "total_seconds")]
+                + [(n, C.c_uint64) for n in ("memberships", "remap_invalid_local_ids", "remap_self_loops",
+                                             "remap_duplicate_edges")]
+                + [(n, C.c_uint32) for n in ("labels", "label_npts_min", "label_npts_max", "row_cap")])
+
+
 def struct_dict(s: C.Structure) -> dict:
     return {name: getattr(s, name) for name, _ in s._fields_}
 
@@ -145,6 +153,7 @@ EXPORTS = [
     "dance_search", "dance_search_resident", "dance_get_last_search_stats",
     "dance_merge_shards", "dance_merge_get_last_stats", "dance_struct_sizes",
     "dance_partition_assign",
+    "dance_stitched_build", "dance_stitched_build_resident", "dance_get_last_stitched_stats",
 ]
 
 class DanceMergeStats(C.Structure):
@@ -168,7 +177,7 @@ def _check_struct_sizes(L) -> None:
     a layout mismatch (a library built from other headers) must fail here,
     before it can overrun a buffer."""
     mine = [GPUVamanaStats, DanceKernelProfile, GPUFilteredVamanaStats, DanceFilteredProfile, DanceSearchStats,
-            DanceMergeStats]
+            DanceMergeStats, DanceStitchedStats]
     L.dance_struct_sizes.argtypes = [C.POINTER(C.c_uint64), C.c_uint32]
     L.dance_struct_sizes.restype = C.c_uint32
     got = (C.c_uint64 * len(mine))()
@@ -265,6 +274,12 @@ def lib() -> C.CDLL:
             getattr(L, name).restype = i32
         L.dance_get_last_search_stats.argtypes = [C.POINTER(DanceSearchStats)]
         L.dance_get_last_search_stats.restype = None
+        for name in ("dance_stitched_build", "dance_stitched_build_resident"):
+            getattr(L, name).argtypes = [vp, i32, u32, u32, _u32p, _u32p, u32, u32, u32, u32, u32, u32, u32,
+                                         vp, vp, _u32p]
+            getattr(L, name).restype = i32
+        L.dance_get_last_stitched_stats.argtypes = [C.POINTER(DanceStitchedStats)]
+        L.dance_get_last_stitched_stats.restype = None
         _LIB = L
     return _LIB
 
@@ -478,6 +493,58 @@ def stage_scan(x: np.ndarray) -> np.ndarray:
     out = np.empty_like(x)
     _check(lib().dance_stage_scan(_p(x, C.c_uint32), x.shape[0], _p(out, C.c_uint32)), "dance_stage_scan")
     return out
+
+
+# ----------------------------------------------------------- stitched build
+
+def stitched_row_cap(label_offsets: np.ndarray, label_points: np.ndarray, N: int, R_small: int,
+                     R_stitched: int) -> int:
+    """Row width that holds every label of a point: max labels per point x
+    min(R_small, R_stitched)."""
+    per = np.bincount(np.asarray(label_points, np.int64), minlength=N) if len(label_points) else np.zeros(1, int)
+    return max(1, int(per.max()) * min(R_small, R_stitched))
+
+
+def stitched_build(data: np.ndarray, label_offsets: np.ndarray, label_points: np.ndarray, R_small: int = 32,
+                   L_small: int = 100, C_: int = 96, STEPS: int = 64, R_stitched: int = 64, row_cap: int | None = None):
+    """dance_stitched_build: per-label standard builds over the label postings
+    (label -> ascending point ids, CSR), remapped into one global graph on
+    the device. Returns (graph N x row_cap, degree, label medoids, stats)."""
+    data = np.ascontiguousarray(data)
+    N, dim = data.shape
+    off = np.ascontiguousarray(label_offsets, np.uint32)
+    pts = np.ascontiguousarray(label_points, np.uint32)
+    nl = off.shape[0] - 1
+    cap = row_cap or stitched_row_cap(off, pts, N, R_small, R_stitched)
+    graph = np.empty((N, cap), np.uint32)
+    degree = np.empty(N, np.uint32)
+    medoids = np.empty(max(1, nl), np.uint32)
+    _check(lib().dance_stitched_build(data.ctypes.data, dtype_code(data), N, dim, _p(off, C.c_uint32),
+                                      _p(pts, C.c_uint32), nl, R_small, L_small, C_, STEPS, R_stitched, cap,
+                                      graph.ctypes.data, degree.ctypes.data, _p(medoids, C.c_uint32)),
+           "dance_stitched_build")
+    return graph, degree, medoids[:nl], last_stitched_stats()
+
+
+def stitched_build_resident(d_data: int, dtype: int, N: int, dim: int, label_offsets: np.ndarray,
+                            label_points: np.ndarray, R_small: int, L_small: int, C_: int, STEPS: int,
+                            R_stitched: int, row_cap: int, d_graph: int, d_degree: int) -> np.ndarray:
+    """dance_stitched_build_resident on device rows and outputs; returns the
+    label medoids (host)."""
+    off = np.ascontiguousarray(label_offsets, np.uint32)
+    pts = np.ascontiguousarray(label_points, np.uint32)
+    nl = off.shape[0] - 1
+    medoids = np.empty(max(1, nl), np.uint32)
+    _check(lib().dance_stitched_build_resident(d_data, dtype, N, dim, _p(off, C.c_uint32), _p(pts, C.c_uint32), nl,
+                                               R_small, L_small, C_, STEPS, R_stitched, row_cap, d_graph, d_degree,
+                                               _p(medoids, C.c_uint32)), "dance_stitched_build_resident")
+    return medoids[:nl]
+
+
+def last_stitched_stats() -> dict:
+    s = DanceStitchedStats()
+    lib().dance_get_last_stitched_stats(C.byref(s))
+    return struct_dict(s)
 
 
 # ------------------------------------------------------------- query search

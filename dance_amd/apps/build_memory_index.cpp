@@ -49,16 +49,14 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
-#include <fstream>
 #include <iostream>
 #include <limits>
-#include <sstream>
 #include <stdexcept>
 #include <string>
 #include <type_traits>
-#include <unordered_map>
 #include <vector>
 
+#include "diskann_io.h"
 #include "gpu_vamana_filtered.h"
 
 namespace {
@@ -78,47 +76,29 @@ struct Options {
   bool gpu_filtered = false, use_opq = false;
 };
 
-uint32_t to_u32(const std::string& v, const std::string& k) {
-  if (v.empty() || v.find_first_not_of("0123456789") != std::string::npos)
-    throw std::runtime_error(k + " must be an unsigned integer");
-  const unsigned long long x = std::stoull(v);
-  if (x > std::numeric_limits<uint32_t>::max()) throw std::runtime_error(k + " is out of range");
-  return (uint32_t)x;
-}
-
 Options parse(int argc, char** argv) {
   Options o;
-  for (int i = 1; i < argc; ++i) {
-    const std::string k = argv[i];
-    if (k == "--gpu_filtered") {
-      o.gpu_filtered = true;
-      continue;
-    }
-    if (k == "--use_opq") {
-      o.use_opq = true;
-      continue;
-    }
-    if (i + 1 >= argc) throw std::runtime_error("missing value for " + k);
-    const std::string v = argv[++i];
-    if (k == "--data_type") o.data_type = v;
-    else if (k == "--dist_fn") o.dist_fn = v;
-    else if (k == "--data_path") o.data_path = v;
-    else if (k == "--index_path_prefix") o.prefix = v;
-    else if (k == "--label_file") o.label_file = v;
-    else if (k == "--universal_label") o.universal_label = v;
-    else if (k == "--label_type") o.label_type = v;
-    else if (k == "--max_degree" || k == "-R") o.R = to_u32(v, k);
-    else if (k == "--Lbuild" || k == "-L") o.L = to_u32(v, k);
-    else if (k == "--FilteredLbuild" || k == "-Lf") o.Lf = to_u32(v, k);
-    else if (k == "--num_threads" || k == "-T") o.threads = to_u32(v, k);
-    else if (k == "--build_PQ_bytes") o.pq_bytes = to_u32(v, k);
-    else if (k == "--alpha") {
-      char* end = nullptr;
-      o.alpha = std::strtof(v.c_str(), &end);
-      if (!end || *end || !(o.alpha > 0.0f)) throw std::runtime_error("--alpha must be a positive number");
-    } else
-      throw std::runtime_error("unknown argument: " + k);
-  }
+  dio::ArgTable t;
+  auto str = [](std::string* dst) { return [dst](const std::string& v, const std::string&) { *dst = v; }; };
+  auto u32 = [](uint32_t* dst) {
+    return [dst](const std::string& v, const std::string& k) { *dst = dio::parse_u32(v, k, true); };
+  };
+  t.flag({"--gpu_filtered"}, &o.gpu_filtered);
+  t.flag({"--use_opq"}, &o.use_opq);
+  t.value({"--data_type"}, str(&o.data_type));
+  t.value({"--dist_fn"}, str(&o.dist_fn));
+  t.value({"--data_path"}, str(&o.data_path));
+  t.value({"--index_path_prefix"}, str(&o.prefix));
+  t.value({"--label_file"}, str(&o.label_file));
+  t.value({"--universal_label"}, str(&o.universal_label));
+  t.value({"--label_type"}, str(&o.label_type));
+  t.value({"--max_degree", "-R"}, u32(&o.R));
+  t.value({"--Lbuild", "-L"}, u32(&o.L));
+  t.value({"--FilteredLbuild", "-Lf"}, u32(&o.Lf));
+  t.value({"--num_threads", "-T"}, u32(&o.threads));
+  t.value({"--build_PQ_bytes"}, u32(&o.pq_bytes));
+  t.value({"--alpha"}, [&](const std::string& v, const std::string& k) { o.alpha = dio::parse_positive_float(v, k); });
+  t.parse(argc, argv);
   if (o.data_type.empty() || o.data_path.empty() || o.prefix.empty())
     throw std::runtime_error("--data_type, --data_path and --index_path_prefix are required");
   if (!o.gpu_filtered)
@@ -134,76 +114,24 @@ Options parse(int argc, char** argv) {
   return o;
 }
 
-template <typename T>
-std::vector<T> read_matrix(const std::string& path, uint32_t& n, uint32_t& dim) {
-  std::ifstream in(path, std::ios::binary);
-  if (!in) throw std::runtime_error("failed to open " + path);
-  uint32_t hdr[2] = {0, 0};
-  in.read(reinterpret_cast<char*>(hdr), 8);
-  if (!in) throw std::runtime_error("failed to read the matrix header of " + path);
-  n = hdr[0];
-  dim = hdr[1];
-  in.seekg(0, std::ios::end);
-  const uint64_t bytes = (uint64_t)in.tellg();
-  if (n == 0 || dim == 0 || bytes != 8 + (uint64_t)n * dim * sizeof(T))
-    throw std::runtime_error("matrix header of " + path + " does not match its size");
-  std::vector<T> v((size_t)n * dim);
-  in.seekg(8);
-  in.read(reinterpret_cast<char*>(v.data()), (std::streamsize)(v.size() * sizeof(T)));
-  if (!in) throw std::runtime_error("failed to read " + path);
-  return v;
-}
-
+// Label rows with ids 1.. by first appearance (the universal label, when
+// named, is 0), tokens in file order with repeats, plus the canonical CSR
+// (sorted unique ids per row).
 struct Labels {
-  std::vector<std::string> names;             // id -> name (id 0 = universal when set)
-  std::vector<std::vector<uint32_t>> tokens;  // per row, ids in file order (with repeats)
-  std::vector<uint32_t> offsets, ids;         // canonical CSR: sorted unique per row
+  dio::LabelRows rows;
+  std::vector<uint32_t> offsets, ids;
   uint32_t universal = kInvalid;
+  uint32_t count() const { return (uint32_t)rows.names.size(); }
 };
 
 Labels read_labels(const Options& o, uint32_t n) {
-  std::ifstream in(o.label_file);
-  if (!in) throw std::runtime_error("failed to open label file: " + o.label_file);
   Labels lb;
-  std::unordered_map<std::string, uint32_t> id_of;
-  if (!o.universal_label.empty()) {
-    id_of.emplace(o.universal_label, 0u);
-    lb.names.push_back(o.universal_label);
-    lb.universal = 0;
-  } else {
-    lb.names.push_back("");  // id 0 unused without a universal label
-  }
-  std::string line;
-  while (std::getline(in, line)) {
-    line.erase(std::remove(line.begin(), line.end(), '\r'), line.end());
-    if (line.empty()) throw std::runtime_error("label row " + std::to_string(lb.tokens.size()) + " is empty");
-    std::vector<uint32_t> row;
-    std::stringstream ss(line);
-    std::string tok;
-    while (std::getline(ss, tok, ',')) {
-      if (tok.empty()) throw std::runtime_error("empty label token in row " + std::to_string(lb.tokens.size()));
-      auto it = id_of.find(tok);
-      if (it == id_of.end()) {
-        it = id_of.emplace(tok, (uint32_t)lb.names.size()).first;
-        lb.names.push_back(tok);
-      }
-      row.push_back(it->second);
-    }
-    if (line.back() == ',') throw std::runtime_error("empty label token in row " + std::to_string(lb.tokens.size()));
-    lb.tokens.push_back(std::move(row));
-  }
-  if (lb.tokens.size() != n)
-    throw std::runtime_error("label file has " + std::to_string(lb.tokens.size()) + " rows for " +
+  lb.rows = dio::read_labels(o.label_file, {o.universal_label, "", false, false});
+  lb.universal = lb.rows.universal;
+  if (lb.rows.rows.size() != n)
+    throw std::runtime_error("label file has " + std::to_string(lb.rows.rows.size()) + " rows for " +
                              std::to_string(n) + " points");
-  lb.offsets.assign(n + 1, 0);
-  for (uint32_t i = 0; i < n; ++i) {
-    std::vector<uint32_t> r = lb.tokens[i];
-    std::sort(r.begin(), r.end());
-    r.erase(std::unique(r.begin(), r.end()), r.end());
-    lb.offsets[i] = (uint32_t)lb.ids.size();
-    lb.ids.insert(lb.ids.end(), r.begin(), r.end());
-  }
-  lb.offsets[n] = (uint32_t)lb.ids.size();
+  dio::canonical_csr(lb.rows, lb.offsets, lb.ids);
   return lb;
 }
 
@@ -242,13 +170,9 @@ void entry_points(const std::vector<T>& x, uint32_t n, uint32_t dim, const Label
   for (uint32_t i = 0; i < n; ++i) all[i] = i;
   std::vector<double> cent;
   global_start = nearest_to_centroid(x, dim, all.data(), n, cent);
-  const uint32_t num_labels = (uint32_t)lb.names.size();
-  std::vector<uint32_t> loff(num_labels + 1, 0), pts(lb.ids.size());
-  for (uint32_t l : lb.ids) ++loff[l + 1];
-  for (uint32_t l = 0; l < num_labels; ++l) loff[l + 1] += loff[l];
-  std::vector<uint32_t> cur(loff.begin(), loff.end() - 1);
-  for (uint32_t i = 0; i < n; ++i)
-    for (uint32_t p = lb.offsets[i]; p < lb.offsets[i + 1]; ++p) pts[cur[lb.ids[p]]++] = i;
+  const uint32_t num_labels = lb.count();
+  std::vector<uint32_t> loff, pts;
+  dio::postings(lb.offsets, lb.ids, num_labels, loff, pts);
   label_start.assign(num_labels, kInvalid);
 #pragma omp parallel for schedule(dynamic, 16)
   for (uint32_t l = 0; l < num_labels; ++l) {
@@ -257,13 +181,6 @@ void entry_points(const std::vector<T>& x, uint32_t n, uint32_t dim, const Label
     std::vector<double> cl;
     label_start[l] = nearest_to_centroid(x, dim, pts.data() + loff[l], c, cl);
   }
-}
-
-void write_text(const std::string& path, const std::string& body) {
-  std::ofstream f(path);
-  if (!f) throw std::runtime_error("failed to write " + path);
-  f << body;
-  if (!f) throw std::runtime_error("failed to write " + path);
 }
 
 // Internal degree and publish choice (patch:20368-20384); sets or clears
@@ -292,7 +209,7 @@ int run(const Options& o) {
   publish_plan(o.R, builder_R, gpu_publish);
   const uint32_t R = gpu_publish ? o.R : builder_R;  // row width of the returned graph
   uint32_t n = 0, dim = 0;
-  std::vector<T> x = read_matrix<T>(o.data_path, n, dim);
+  std::vector<T> x = dio::read_bin<T>(o.data_path, n, dim);
   Labels lb = read_labels(o, n);
   uint32_t global_start = 0;
   std::vector<uint32_t> starts;
@@ -304,7 +221,7 @@ int run(const Options& o) {
   const uint32_t steps = steps_env ? (uint32_t)std::max(1, std::atoi(steps_env)) : std::min<uint32_t>(64, L);
   std::cout << "[GPU filtered] requested_R=" << o.R << " internal_R=" << builder_R
             << " publish_backend=" << (gpu_publish ? "gpu_warp_exact_csr" : "direct") << std::endl;
-  std::cout << "[GPU filtered] N=" << n << " dim=" << dim << " labels=" << lb.names.size() - (lb.universal == 0 ? 1 : 0)
+  std::cout << "[GPU filtered] N=" << n << " dim=" << dim << " labels=" << lb.count() - 1
             << " label_slots=" << lb.ids.size() << " global_start=" << global_start << " L=" << L
             << " filtered_L=" << Lf << " C=" << kDefaultMaxC << " steps=" << steps << " alpha=" << o.alpha
             << std::endl;
@@ -372,59 +289,42 @@ int run(const Options& o) {
               << " changed=" << changed << std::endl;
   }
 
-  // Install (patch:20506-20521) and save.
-  std::string body;
-  body.reserve((size_t)n * 4 * (R + 1));
-  uint32_t max_deg = 0;
-  uint64_t edges = 0;
-  std::vector<uint32_t> row;
-  for (uint32_t i = 0; i < n; ++i) {
-    row.clear();
+  // Install (patch:20506-20521): per row drop invalid / self / repeated ids;
+  // an empty row of a multi-point index gets (i + 1) mod N.
+  const dio::RowFn installed = [&](uint32_t i, std::vector<uint32_t>& row) {
     for (uint32_t j = 0; j < degree[i] && j < R; ++j) {
       const uint32_t nb = graph[(size_t)i * R + j];
       if (nb != kInvalid && nb < n && nb != i && std::find(row.begin(), row.end(), nb) == row.end())
         row.push_back(nb);
     }
     if (row.empty() && n > 1) row.push_back((i + 1) % n);
-    const uint32_t k = (uint32_t)row.size();
-    body.append(reinterpret_cast<const char*>(&k), 4);
-    body.append(reinterpret_cast<const char*>(row.data()), 4ull * k);
-    max_deg = std::max(max_deg, k);
-    edges += k;
-  }
+  };
+  dio::File gf(o.prefix, O_WRONLY | O_CREAT | O_TRUNC);
+  if (!gf.ok()) throw std::runtime_error("failed to write " + o.prefix);
+  const dio::GraphSummary gs = dio::write_graph(gf, n, global_start, installed);
+  gf.close_checked();
+  const uint64_t edges = gs.edges;
+  const uint32_t max_deg = gs.max_degree;
   {
-    std::ofstream g(o.prefix, std::ios::binary);
-    if (!g) throw std::runtime_error("failed to write " + o.prefix);
-    const uint64_t size = 24 + body.size(), frozen = 0;
-    g.write(reinterpret_cast<const char*>(&size), 8);
-    g.write(reinterpret_cast<const char*>(&max_deg), 4);
-    g.write(reinterpret_cast<const char*>(&global_start), 4);
-    g.write(reinterpret_cast<const char*>(&frozen), 8);
-    g.write(body.data(), (std::streamsize)body.size());
-    if (!g) throw std::runtime_error("failed to write " + o.prefix);
+    dio::File d(o.prefix + ".data", O_WRONLY | O_CREAT | O_TRUNC);
+    if (!d.ok()) throw std::runtime_error("failed to write " + o.prefix + ".data");
+    dio::write_bin(d, n, dim, x.data());
+    d.close_checked();
   }
-  {
-    std::ofstream d(o.prefix + ".data", std::ios::binary);
-    const uint32_t hdr[2] = {n, dim};
-    d.write(reinterpret_cast<const char*>(hdr), 8);
-    d.write(reinterpret_cast<const char*>(x.data()), (std::streamsize)(x.size() * sizeof(T)));
-    if (!d) throw std::runtime_error("failed to write " + o.prefix + ".data");
-  }
-  std::ostringstream labels, formatted, map, medoids;
-  for (uint32_t i = 0; i < n; ++i) {
-    for (uint32_t p = lb.offsets[i]; p < lb.offsets[i + 1]; ++p) labels << (p > lb.offsets[i] ? "," : "") << lb.ids[p];
-    labels << "\n";
-    for (size_t j = 0; j < lb.tokens[i].size(); ++j) formatted << (j ? "," : "") << lb.tokens[i][j];
-    formatted << "\n";
-  }
-  for (uint32_t l = lb.universal == 0 ? 0 : 1; l < lb.names.size(); ++l) map << lb.names[l] << "\t" << l << "\n";
+  const auto& tokens = lb.rows.rows;
+  dio::write_text(o.prefix + "_labels.txt", dio::id_rows_text(n, [&](size_t i, std::vector<uint32_t>& r) {
+                    r.assign(lb.ids.begin() + lb.offsets[i], lb.ids.begin() + lb.offsets[i + 1]);
+                  }));
+  dio::write_text(o.prefix + "_label_formatted.txt",
+                  dio::id_rows_text(n, [&](size_t i, std::vector<uint32_t>& r) { r = tokens[i]; }));
+  std::string map, medoids;
+  for (uint32_t l = lb.universal == 0 ? 0 : 1; l < lb.count(); ++l)
+    map += lb.rows.names[l] + "\t" + std::to_string(l) + "\n";
   for (uint32_t l = 0; l < starts.size(); ++l)
-    if (starts[l] != kInvalid) medoids << l << ", " << starts[l] << "\n";
-  write_text(o.prefix + "_labels.txt", labels.str());
-  write_text(o.prefix + "_label_formatted.txt", formatted.str());
-  write_text(o.prefix + "_labels_map.txt", map.str());
-  write_text(o.prefix + "_labels_to_medoids.txt", medoids.str());
-  if (lb.universal == 0) write_text(o.prefix + "_universal_label.txt", "0\n");
+    if (starts[l] != kInvalid) medoids += std::to_string(l) + ", " + std::to_string(starts[l]) + "\n";
+  dio::write_text(o.prefix + "_labels_map.txt", map);
+  dio::write_text(o.prefix + "_labels_to_medoids.txt", medoids);
+  if (lb.universal == 0) dio::write_text(o.prefix + "_universal_label.txt", "0\n");
   const double t_end = now_sec();
   std::cout << "[GPU filtered] graph installed: edges=" << edges << " max_degree=" << max_deg
             << " prepare_seconds=" << t_prep - t0 << " build_seconds=" << t_build - t_prep

@@ -1,324 +1,211 @@
-// gpu_vamana_memory_index: builds a DiskANN in-memory index with the GPU
-// Vamana builder (libdance_hip.so).
+// gpu_vamana_memory_index: one standard GPU Vamana build of a slice of a
+// DiskANN .bin matrix, audited and saved as a DiskANN in-memory index.
 //
-// Same command line, file formats, validation rules, JSON report and exit
-// codes as the reference app (/root/reference/apps/utils/gpu_vamana_memory_index.cpp):
-//   --data_path <bin> [--data_type uint8|float] [--offset N] [--npts N|0=all]
-//   [--index_prefix PATH] [--R 42] [--L 100] [--C 80] [--STEPS 64] [--builder vnew2|v8]
-// Input: DiskANN matrix file (uint32 N, uint32 dim, row-major payload), the
-// size checked exactly (:157-195). Output (only for a valid graph, :349-386):
-// <prefix> = DiskANN graph (uint64 file bytes, uint32 max degree, uint32
-// medoid, uint64 frozen points, then per node uint32 k + k ids) and
-// <prefix>.data, both written to temporaries and renamed, never overwriting
-// (:197-297). Exit codes: 0 ok, 2 usage/input error, 3 invalid graph, else the
-// builder's return code (:423-449).
+// Command line, report and files are those of the reference app
+// (apps/utils/gpu_vamana_memory_index.cpp): options --data_path,
+// --data_type uint8|float, --offset, --npts (0 = to the end),
+// --index_prefix, --R 42, --L 100, --C 80, --STEPS 64, --builder vnew2|v8; a
+// JSON report on stdout; <prefix> (graph) and <prefix>.data when the graph
+// passes its audit; exit 0 when it does, the builder's code when the build
+// failed, 3 when the audit failed, 2 on a usage or input error. Run under
+// the name gpu_vamana_memory_index it requires --index_prefix and the vnew2
+// builder, as the reference does.
+//
+// Flow: read the slice (pread of exactly the requested rows) -> one call of
+// gpu_vamana[_vnew2]_build[_float] -> audit every row (ids, self loops,
+// repeats, degree cap) -> publish both files through temporaries.
 
-#include <algorithm>
 #include <chrono>
 #include <cstdint>
-#include <cstdio>
-#include <fstream>
 #include <iostream>
-#include <limits>
-#include <sstream>
-#include <stdexcept>
 #include <string>
 #include <type_traits>
 #include <vector>
 
+#include "diskann_io.h"
 #include "gpu_vamana_builder.h"
 
 namespace {
 
-struct Options {
-  std::string data_path, data_type = "uint8", index_prefix, builder = "vnew2";
+struct Job {
+  std::string data_path, data_type = "uint8", prefix, builder = "vnew2";
   uint64_t offset = 0;
-  uint32_t npts = 0, R = 42, L = 100, C = 80, STEPS = 64;
+  uint32_t npts = 0;  // 0: every row from the offset on
+  uint32_t R = 42, L = 100, C = 80, STEPS = 64;
 };
 
-double seconds_since_start() {
-  static const auto t0 = std::chrono::steady_clock::now();
-  return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
-}
+const char* kUsage =
+    " --data_path <bin> [--data_type uint8|float] [--offset N] [--npts N|0=all] [--index_prefix PATH]"
+    " [--R 42] [--L 100] [--C 80] [--STEPS 64] [--builder vnew2|v8]\n";
 
-std::string json_string(const std::string& s) {
-  std::string out;
-  for (unsigned char c : s) {
-    switch (c) {
-      case '"': out += "\\\""; break;
-      case '\\': out += "\\\\"; break;
-      case '\b': out += "\\b"; break;
-      case '\f': out += "\\f"; break;
-      case '\n': out += "\\n"; break;
-      case '\r': out += "\\r"; break;
-      case '\t': out += "\\t"; break;
-      default:
-        if (c < 0x20) throw std::runtime_error("control character in JSON path");
-        out.push_back((char)c);
-    }
+Job read_job(int argc, char** argv) {
+  Job j;
+  dio::ArgTable t;
+  t.value({"--data_path"}, [&](const std::string& v, const std::string&) { j.data_path = v; });
+  t.value({"--data_type"}, [&](const std::string& v, const std::string&) { j.data_type = v; });
+  t.value({"--index_prefix"}, [&](const std::string& v, const std::string&) { j.prefix = v; });
+  t.value({"--builder"}, [&](const std::string& v, const std::string&) { j.builder = v; });
+  t.value({"--offset"}, [&](const std::string& v, const std::string& k) { j.offset = dio::parse_u64(v, k); });
+  t.value({"--npts"}, [&](const std::string& v, const std::string& k) { j.npts = dio::parse_u32(v, k, true); });
+  uint32_t* dims[] = {&j.R, &j.L, &j.C, &j.STEPS};
+  const char* names[] = {"--R", "--L", "--C", "--STEPS"};
+  for (int k = 0; k < 4; ++k) {
+    uint32_t* dst = dims[k];
+    t.value({names[k]}, [dst](const std::string& v, const std::string& key) { *dst = dio::parse_u32(v, key, false); });
   }
-  return out;
-}
-
-uint64_t to_u64(const std::string& v, const std::string& opt) {
-  if (v.empty() || v.find_first_not_of("0123456789") != std::string::npos)
-    throw std::runtime_error(opt + " must be an unsigned integer");
-  try {
-    size_t used = 0;
-    unsigned long long x = std::stoull(v, &used, 10);
-    if (used != v.size()) throw std::runtime_error("");
-    return x;
-  } catch (...) {
-    throw std::runtime_error(opt + " must be an unsigned integer");
-  }
-}
-
-uint32_t to_u32(const std::string& v, const std::string& opt, bool zero_ok) {
-  const uint64_t x = to_u64(v, opt);
-  if (x > std::numeric_limits<uint32_t>::max() || (!zero_ok && x == 0))
-    throw std::runtime_error(opt + (zero_ok ? " is out of uint32 range" : " must be in [1, UINT32_MAX]"));
-  return (uint32_t)x;
-}
-
-void print_usage(const char* prog) {
-  std::cerr << "Usage: " << prog
-            << " --data_path <bin> [--data_type uint8|float] [--offset N] [--npts N|0=all]"
-            << " [--index_prefix PATH] [--R 42] [--L 100] [--C 80] [--STEPS 64] [--builder vnew2|v8]\n";
-}
-
-Options parse(int argc, char** argv) {
-  Options o;
-  static const char* known[] = {"--data_path", "--data_type", "--index_prefix", "--offset", "--npts",
-                                "--R",         "--L",         "--C",            "--STEPS",  "--builder"};
-  for (int i = 1; i < argc; ++i) {
-    const std::string k = argv[i];
-    if (std::find(std::begin(known), std::end(known), k) == std::end(known))
-      throw std::runtime_error("unknown argument: " + k);
-    if (i + 1 >= argc) throw std::runtime_error("missing value for " + k);
-    const std::string v = argv[++i];
-    if (k == "--data_path") o.data_path = v;
-    else if (k == "--data_type") o.data_type = v;
-    else if (k == "--index_prefix") o.index_prefix = v;
-    else if (k == "--offset") o.offset = to_u64(v, k);
-    else if (k == "--npts") o.npts = to_u32(v, k, true);
-    else if (k == "--R") o.R = to_u32(v, k, false);
-    else if (k == "--L") o.L = to_u32(v, k, false);
-    else if (k == "--C") o.C = to_u32(v, k, false);
-    else if (k == "--STEPS") o.STEPS = to_u32(v, k, false);
-    else o.builder = v;
-  }
-  if (o.data_path.empty()) throw std::runtime_error("--data_path is required");
-  if (o.data_type != "uint8" && o.data_type != "float") throw std::runtime_error("--data_type must be uint8 or float");
-  if (o.builder != "vnew2" && o.builder != "v8") throw std::runtime_error("--builder must be vnew2 or v8");
-  (void)json_string(o.data_path);
-  (void)json_string(o.index_prefix);
-  return o;
+  t.parse(argc, argv);
+  if (j.data_path.empty()) throw std::runtime_error("--data_path is required");
+  if (j.data_type != "uint8" && j.data_type != "float") throw std::runtime_error("--data_type must be uint8 or float");
+  if (j.builder != "vnew2" && j.builder != "v8") throw std::runtime_error("--builder must be vnew2 or v8");
+  // paths go into the JSON report: reject what it cannot carry
+  for (const std::string* p : {&j.data_path, &j.prefix})
+    for (unsigned char c : *p)
+      if (c < 0x20 && c != '\b' && c != '\f' && c != '\n' && c != '\r' && c != '\t')
+        throw std::runtime_error("control character in JSON path");
+  return j;
 }
 
 template <typename T>
-std::vector<T> read_slice(const Options& o, uint32_t& dim, uint64_t& total, uint32_t& count) {
-  std::ifstream in(o.data_path, std::ios::binary);
-  if (!in) throw std::runtime_error("failed to open " + o.data_path);
-  uint32_t hdr[2] = {0, 0};
-  in.read(reinterpret_cast<char*>(hdr), sizeof(hdr));
-  if (!in) throw std::runtime_error("failed to read DiskANN matrix header");
-  total = hdr[0];
-  dim = hdr[1];
-  if (dim == 0 || total > (std::numeric_limits<uint64_t>::max() - 8) / ((uint64_t)dim * sizeof(T)))
-    throw std::runtime_error("DiskANN matrix shape overflows its byte-size calculation");
-  in.seekg(0, std::ios::end);
-  const std::streamoff bytes = in.tellg();
-  if (bytes < 0 || (uint64_t)bytes != 8 + total * (uint64_t)dim * sizeof(T))
-    throw std::runtime_error("DiskANN matrix header does not match exact file size");
-  const uint64_t left = total - std::min<uint64_t>(o.offset, total);
-  const uint64_t want = o.npts == 0 ? left : o.npts;
-  if (o.offset > total || want > left || want > std::numeric_limits<uint32_t>::max())
+struct Slice {
+  uint64_t file_rows = 0;
+  uint32_t dim = 0, n = 0;
+  std::vector<T> rows;
+};
+
+template <typename T>
+Slice<T> load_slice(const Job& j) {
+  dio::File f(j.data_path, O_RDONLY);
+  if (!f.ok()) throw std::runtime_error("failed to open " + j.data_path);
+  const dio::MatrixShape shape = dio::bin_shape(f, sizeof(T));
+  Slice<T> s;
+  s.file_rows = shape.rows;
+  s.dim = shape.dim;
+  const uint64_t left = j.offset <= shape.rows ? shape.rows - j.offset : 0;
+  const uint64_t want = j.npts ? j.npts : left;
+  if (j.offset > shape.rows || want > left || want > 0xFFFFFFFFull)
     throw std::runtime_error("requested slice exceeds base file point count");
   if (want == 0) throw std::runtime_error("requested slice and dimension must be nonzero");
-  count = (uint32_t)want;
-  std::vector<T> v((size_t)count * dim);
-  in.seekg((std::streamoff)(8 + o.offset * (uint64_t)dim * sizeof(T)), std::ios::beg);
-  in.read(reinterpret_cast<char*>(v.data()), (std::streamsize)(v.size() * sizeof(T)));
-  if (!in) throw std::runtime_error("failed to read requested slice");
-  return v;
+  s.n = (uint32_t)want;
+  s.rows = dio::read_bin_rows<T>(f, shape, j.offset, want);
+  return s;
 }
 
-bool exists(const std::string& p) { return (bool)std::ifstream(p, std::ios::binary); }
+struct Audit {
+  uint64_t edges = 0, invalid = 0, self_loops = 0, repeats = 0, overflows = 0;
+  uint32_t max_degree = 0;
+  bool clean() const { return invalid == 0 && self_loops == 0 && repeats == 0 && overflows == 0; }
+};
 
-template <typename T>
-void write_index(const Options& o, const std::vector<T>& data, uint32_t n, uint32_t dim,
-                 const std::vector<uint32_t>& graph, const std::vector<uint32_t>& degree, uint32_t medoid) {
-  if (o.index_prefix.empty()) return;
-  const std::string graph_path = o.index_prefix, data_path = o.index_prefix + ".data";
-  const std::string graph_tmp = o.index_prefix + ".tmp", data_tmp = data_path + ".tmp";
-  if (exists(graph_path) || exists(data_path) || exists(graph_tmp) || exists(data_tmp))
-    throw std::runtime_error("refusing to overwrite existing memory-index output");
-  size_t edges = 0;
-  for (uint32_t d : degree) edges += std::min(d, o.R);
-  const uint32_t max_deg = *std::max_element(degree.begin(), degree.end());
-  const size_t frozen = 0;
-  const size_t header = sizeof(size_t) + 2 * sizeof(uint32_t) + sizeof(size_t);
-  const size_t graph_bytes = header + (size_t)n * 4 + edges * 4;
-  const size_t data_bytes = 8 + data.size() * sizeof(T);
-  auto cleanup = [&](bool with_data) {
-    std::remove(graph_tmp.c_str());
-    if (with_data) std::remove(data_tmp.c_str());
-  };
-  {
-    std::ofstream out(graph_tmp, std::ios::binary | std::ios::trunc);
-    if (!out) throw std::runtime_error("failed to create graph temporary output " + graph_tmp);
-    out.write(reinterpret_cast<const char*>(&graph_bytes), sizeof(graph_bytes));
-    out.write(reinterpret_cast<const char*>(&max_deg), 4);
-    out.write(reinterpret_cast<const char*>(&medoid), 4);
-    out.write(reinterpret_cast<const char*>(&frozen), sizeof(frozen));
-    for (uint32_t v = 0; v < n; ++v) {
-      const uint32_t k = std::min(degree[v], o.R);
-      out.write(reinterpret_cast<const char*>(&k), 4);
-      out.write(reinterpret_cast<const char*>(graph.data() + (size_t)v * o.R), (std::streamsize)k * 4);
-    }
-    out.close();
-    if (!out) {
-      cleanup(false);
-      throw std::runtime_error("failed while writing graph temporary output " + graph_tmp);
-    }
-  }
-  {
-    std::ofstream out(data_tmp, std::ios::binary | std::ios::trunc);
-    if (!out) {
-      cleanup(true);
-      throw std::runtime_error("failed to create vector temporary output " + data_tmp);
-    }
-    out.write(reinterpret_cast<const char*>(&n), 4);
-    out.write(reinterpret_cast<const char*>(&dim), 4);
-    out.write(reinterpret_cast<const char*>(data.data()), (std::streamsize)(data.size() * sizeof(T)));
-    out.close();
-    if (!out) {
-      cleanup(true);
-      throw std::runtime_error("failed while writing vector temporary output " + data_tmp);
-    }
-  }
-  std::ifstream g(graph_tmp, std::ios::binary | std::ios::ate), d(data_tmp, std::ios::binary | std::ios::ate);
-  if (!g || g.tellg() != (std::streamoff)graph_bytes || !d || d.tellg() != (std::streamoff)data_bytes) {
-    cleanup(true);
-    throw std::runtime_error("serialized temporary output size does not match its DiskANN layout");
-  }
-  if (std::rename(data_tmp.c_str(), data_path.c_str()) != 0) {
-    cleanup(true);
-    throw std::runtime_error("failed to publish vector output " + data_path);
-  }
-  if (std::rename(graph_tmp.c_str(), graph_path.c_str()) != 0) {
-    std::remove(graph_tmp.c_str());
-    std::remove(data_path.c_str());
-    throw std::runtime_error("failed to publish graph output " + graph_path);
-  }
-}
-
-template <typename T>
-int run(const Options& o) {
-  uint32_t dim = 0, n = 0;
-  uint64_t total = 0;
-  const double t_load = seconds_since_start();
-  std::vector<T> data = read_slice<T>(o, dim, total, n);
-  const double load_s = seconds_since_start() - t_load;
-  if ((size_t)n > std::numeric_limits<size_t>::max() / 4 / o.R)
-    throw std::runtime_error("N * R overflows the host graph allocation");
-  std::vector<uint32_t> graph((size_t)n * o.R), degree(n);
-  const double t_gpu = seconds_since_start();
-  int rc;
-  if constexpr (std::is_same<T, uint8_t>::value)
-    rc = o.builder == "vnew2" ? gpu_vamana_vnew2_build(data.data(), n, dim, o.R, o.L, o.C, o.STEPS, graph.data(), degree.data())
-                              : gpu_vamana_build(data.data(), n, dim, o.R, o.L, o.C, o.STEPS, graph.data(), degree.data());
-  else
-    rc = o.builder == "vnew2"
-             ? gpu_vamana_vnew2_build_float(data.data(), n, dim, o.R, o.L, o.C, o.STEPS, graph.data(), degree.data())
-             : gpu_vamana_build_float(data.data(), n, dim, o.R, o.L, o.C, o.STEPS, graph.data(), degree.data());
-  const double gpu_s = seconds_since_start() - t_gpu;
-  GPUVamanaStats st{};
-  uint32_t medoid;
-  if (o.builder == "vnew2") {
-    medoid = gpu_vamana_vnew2_get_last_medoid();
-    gpu_vamana_vnew2_get_last_stats(&st);
-  } else {
-    medoid = gpu_vamana_get_last_medoid();
-    gpu_vamana_get_last_stats(&st);
-  }
-  uint64_t edges = 0, invalid = 0, self = 0, dup = 0, overflow = 0;
-  uint32_t max_deg = 0;
-  std::vector<uint32_t> row;
+// Per row: degree above R is an overflow; within the first min(degree, R)
+// slots, ids >= n are invalid, the row's own id is a self loop, and every
+// extra copy of a valid id is a repeat.
+Audit audit(const std::vector<uint32_t>& graph, const std::vector<uint32_t>& degree, uint32_t n, uint32_t R) {
+  Audit a;
+  std::vector<uint32_t> ids;
   for (uint32_t v = 0; v < n; ++v) {
     const uint32_t d = degree[v];
-    edges += d;
-    max_deg = std::max(max_deg, d);
-    if (d > o.R) ++overflow;
-    row.clear();
-    for (uint32_t j = 0; j < std::min(d, o.R); ++j) {
-      const uint32_t u = graph[(size_t)v * o.R + j];
+    a.edges += d;
+    a.max_degree = std::max(a.max_degree, d);
+    a.overflows += d > R;
+    ids.clear();
+    for (uint32_t s = 0; s < std::min(d, R); ++s) {
+      const uint32_t u = graph[(size_t)v * R + s];
       if (u >= n) {
-        ++invalid;
+        ++a.invalid;
         continue;
       }
-      if (u == v) ++self;
-      row.push_back(u);
+      a.self_loops += u == v;
+      ids.push_back(u);
     }
-    std::sort(row.begin(), row.end());
-    dup += (uint64_t)(row.end() - std::unique(row.begin(), row.end()));
+    std::sort(ids.begin(), ids.end());
+    for (size_t k = 1; k < ids.size(); ++k) a.repeats += ids[k] == ids[k - 1];
   }
-  const bool valid = rc == 0 && invalid == 0 && self == 0 && dup == 0 && overflow == 0 && medoid < n;
-  if (valid) write_index(o, data, n, dim, graph, degree, medoid);
-  std::ostringstream js;
-  js << "{\n"
-     << "  \"data_path\": \"" << json_string(o.data_path) << "\",\n"
-     << "  \"data_type\": \"" << o.data_type << "\",\n"
-     << "  \"base_npts\": " << total << ",\n"
-     << "  \"offset\": " << o.offset << ",\n"
-     << "  \"npts\": " << n << ",\n"
-     << "  \"dim\": " << dim << ",\n"
-     << "  \"R\": " << o.R << ",\n"
-     << "  \"L\": " << o.L << ",\n"
-     << "  \"C\": " << o.C << ",\n"
-     << "  \"STEPS\": " << o.STEPS << ",\n"
-     << "  \"builder\": \"" << o.builder << "\",\n"
-     << "  \"index_prefix\": \"" << json_string(o.index_prefix) << "\",\n"
-     << "  \"memory_index_serialized\": " << (!o.index_prefix.empty() && valid ? "true" : "false") << ",\n"
-     << "  \"load_seconds\": " << load_s << ",\n"
-     << "  \"gpu_call_seconds\": " << gpu_s << ",\n"
-     << "  \"stats_gpu_build_seconds\": " << st.gpu_build_seconds << ",\n"
-     << "  \"stats_h2d_seconds\": " << st.h2d_seconds << ",\n"
-     << "  \"stats_search_online_insert_seconds\": " << st.search_online_insert_seconds << ",\n"
-     << "  \"stats_reverse_seconds\": " << st.reverse_seconds << ",\n"
-     << "  \"stats_final_prune_seconds\": " << st.final_prune_seconds << ",\n"
-     << "  \"stats_d2h_seconds\": " << st.d2h_seconds << ",\n"
-     << "  \"selective_active_nodes\": " << st.selective_active_nodes << ",\n"
-     << "  \"medoid\": " << medoid << ",\n"
-     << "  \"edge_count\": " << edges << ",\n"
-     << "  \"avg_degree\": " << (double)edges / (double)n << ",\n"
-     << "  \"max_degree\": " << max_deg << ",\n"
-     << "  \"invalid_neighbor_count\": " << invalid << ",\n"
-     << "  \"self_loop_count\": " << self << ",\n"
-     << "  \"duplicate_edge_count\": " << dup << ",\n"
-     << "  \"degree_overflow_count\": " << overflow << ",\n"
-     << "  \"graph_valid\": " << (valid ? "true" : "false") << ",\n"
-     << "  \"return_code\": " << rc << "\n"
-     << "}\n";
-  std::cout << js.str();
-  return valid ? 0 : (rc != 0 ? rc : 3);
+  return a;
+}
+
+// <prefix>: the graph (rows cut at R), start = medoid, no frozen points;
+// <prefix>.data: the slice. Written to temporaries, checked, renamed.
+template <typename T>
+void save_index(const Job& j, const Slice<T>& s, const std::vector<uint32_t>& graph,
+                const std::vector<uint32_t>& degree, uint32_t medoid) {
+  const std::string data_path = j.prefix + ".data";
+  for (const std::string& p : {j.prefix, data_path, j.prefix + ".tmp", data_path + ".tmp"})
+    if (dio::exists(p)) throw std::runtime_error("refusing to overwrite existing memory-index output");
+  dio::Publisher pub;
+  const dio::RowFn rows = dio::padded_rows(graph.data(), degree.data(), j.R, j.R);
+  dio::File& g = pub.open(j.prefix);
+  pub.expect(dio::write_graph(g, s.n, medoid, rows).bytes);
+  dio::File& d = pub.open(data_path);
+  dio::write_bin(d, s.n, s.dim, s.rows.data());
+  pub.expect(8 + (uint64_t)s.n * s.dim * sizeof(T));
+  pub.commit("DiskANN");
+}
+
+double seconds_since(std::chrono::steady_clock::time_point t) {
+  return std::chrono::duration<double>(std::chrono::steady_clock::now() - t).count();
+}
+
+template <typename T>
+int build(const Job& j) {
+  auto t = std::chrono::steady_clock::now();
+  const Slice<T> s = load_slice<T>(j);
+  const double load_s = seconds_since(t);
+  std::vector<uint32_t> graph((size_t)s.n * j.R), degree(s.n);
+
+  const bool v8 = j.builder == "v8";
+  t = std::chrono::steady_clock::now();
+  int rc;
+  if constexpr (std::is_same<T, uint8_t>::value)
+    rc = (v8 ? gpu_vamana_build : gpu_vamana_vnew2_build)(s.rows.data(), s.n, s.dim, j.R, j.L, j.C, j.STEPS,
+                                                         graph.data(), degree.data());
+  else
+    rc = (v8 ? gpu_vamana_build_float : gpu_vamana_vnew2_build_float)(s.rows.data(), s.n, s.dim, j.R, j.L, j.C,
+                                                                     j.STEPS, graph.data(), degree.data());
+  const double call_s = seconds_since(t);
+  GPUVamanaStats st{};
+  (v8 ? gpu_vamana_get_last_stats : gpu_vamana_vnew2_get_last_stats)(&st);
+  const uint32_t medoid = (v8 ? gpu_vamana_get_last_medoid : gpu_vamana_vnew2_get_last_medoid)();
+
+  const Audit a = audit(graph, degree, s.n, j.R);
+  const bool valid = rc == 0 && a.clean() && medoid < s.n;
+  if (valid && !j.prefix.empty()) save_index(j, s, graph, degree, medoid);
+
+  dio::JsonReport r;
+  r.str("data_path", j.data_path).str("data_type", j.data_type).num("base_npts", s.file_rows)
+      .num("offset", j.offset).num("npts", s.n).num("dim", s.dim).num("R", j.R).num("L", j.L).num("C", j.C)
+      .num("STEPS", j.STEPS).str("builder", j.builder).str("index_prefix", j.prefix)
+      .boolean("memory_index_serialized", valid && !j.prefix.empty()).num("load_seconds", load_s)
+      .num("gpu_call_seconds", call_s).num("stats_gpu_build_seconds", st.gpu_build_seconds)
+      .num("stats_h2d_seconds", st.h2d_seconds).num("stats_search_online_insert_seconds", st.search_online_insert_seconds)
+      .num("stats_reverse_seconds", st.reverse_seconds).num("stats_final_prune_seconds", st.final_prune_seconds)
+      .num("stats_d2h_seconds", st.d2h_seconds).num("selective_active_nodes", st.selective_active_nodes)
+      .num("medoid", medoid).num("edge_count", a.edges).num("avg_degree", (double)a.edges / (double)s.n)
+      .num("max_degree", a.max_degree).num("invalid_neighbor_count", a.invalid)
+      .num("self_loop_count", a.self_loops).num("duplicate_edge_count", a.repeats)
+      .num("degree_overflow_count", a.overflows).boolean("graph_valid", valid).num("return_code", rc);
+  std::cout << r.text();
+  if (valid) return 0;
+  return rc != 0 ? rc : 3;
+}
+
+std::string base_name(const char* path) {
+  const std::string p = path ? path : "";
+  const size_t k = p.find_last_of("/\\");
+  return k == std::string::npos ? p : p.substr(k + 1);
 }
 
 }  // namespace
 
 int main(int argc, char** argv) {
   try {
-    const Options o = parse(argc, argv);
-    std::string exe = argc > 0 ? argv[0] : "";
-    const size_t slash = exe.find_last_of("/\\");
-    if (slash != std::string::npos) exe = exe.substr(slash + 1);
-    if (exe == "gpu_vamana_memory_index" && o.index_prefix.empty())
-      throw std::runtime_error("gpu_vamana_memory_index requires --index_prefix");
-    if (exe == "gpu_vamana_memory_index" && o.builder != "vnew2")
-      throw std::runtime_error("gpu_vamana_memory_index requires --builder vnew2");
-    return o.data_type == "uint8" ? run<uint8_t>(o) : run<float>(o);
+    const Job j = read_job(argc, argv);
+    if (base_name(argc > 0 ? argv[0] : nullptr) == "gpu_vamana_memory_index") {
+      if (j.prefix.empty()) throw std::runtime_error("gpu_vamana_memory_index requires --index_prefix");
+      if (j.builder != "vnew2") throw std::runtime_error("gpu_vamana_memory_index requires --builder vnew2");
+    }
+    return j.data_type == "uint8" ? build<uint8_t>(j) : build<float>(j);
   } catch (const std::exception& e) {
-    print_usage(argc > 0 ? argv[0] : "gpu_vamana_memory_index");
+    std::cerr << "Usage: " << (argc > 0 ? argv[0] : "gpu_vamana_memory_index") << kUsage;
     std::cerr << "error: " << e.what() << std::endl;
     return 2;
   }

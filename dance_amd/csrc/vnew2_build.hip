@@ -44,6 +44,7 @@
 #include "../../include/gpu_vamana_builder.h"
 #include "../../include/gpu_vamana_filtered.h"
 #include "host_common.h"
+#include "stitched_kernels.h"
 #include "vnew2_kernels.h"
 
 static_assert(sizeof(GPUVamanaStats) == 7 * 8 + 6 * 8 + 8 + 8, "GPUVamanaStats layout");
@@ -297,6 +298,16 @@ static int launch_merge(const Rows& rows, GraphBufs g, const uint32_t* offs, con
 // nearest pivot. Pivots are K evenly spaced rows. K comes from
 // DANCE_LOCALITY_CELLS (default 1024, the fastest c3 build of 256..4096; 0
 // disables the schedule). Uses the reverse-sort buffers as scratch.
+// Alpha schedule (gpu_vamana_alpha_for_iter, vnew2.cu:201-213): iterations
+// from DANCE_ALPHA_FROM_ITER on prune with alpha, earlier ones with 1. The
+// default is the reference's (the last iteration only); 0 is its
+// USE_ALPHA_FROM_FIRST_ITER=1 and k its VAMANA_ALPHA_FINAL_FROM_ITER=k.
+static uint32_t alpha_from_iter() {
+  const char* e = std::getenv("DANCE_ALPHA_FROM_ITER");
+  if (e && e[0]) return (uint32_t)std::strtoul(e, nullptr, 10);
+  return kIters - 1;
+}
+
 static uint32_t locality_cells() {
   const char* e = std::getenv("DANCE_LOCALITY_CELLS");
   if (e && e[0]) return (uint32_t)std::strtoul(e, nullptr, 10);
@@ -474,6 +485,7 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   const uint32_t* order = nullptr;
   DCHECK(build_schedule(rows, qb, rws, s, &order));
   const uint32_t q_iters = qbound_iters(), q_prune_iters = qbound_prune_iters();
+  const uint32_t a_from = alpha_from_iter();
   DCHECK(record(e_init, s));
 
   struct IterEv {
@@ -488,7 +500,7 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     DCHECK(E.make(&ie.p1));
   }
   for (uint32_t it = 0; it < kIters; ++it) {
-    const float alpha = (it + 1 >= kIters) ? kAlpha : 1.0f;
+    const float alpha = it >= a_from ? kAlpha : 1.0f;
     uint32_t steps = STEPS;
     if (it < kCoarseIters && steps > kWarmupSteps) steps = kWarmupSteps;
     if (verbose())
@@ -780,13 +792,13 @@ static int scratch_base(void** out) {
 // same buffers run_build, setup_rows and the radix sort allocate, each rounded
 // up to the arena's 256-byte alignment.
 static size_t resident_build_bytes(const void* d_data, int dtype, int store, uint32_t N, uint32_t dim, uint32_t R,
-                                   uint32_t C) {
+                                   uint32_t C, bool rows_ready = false) {
   size_t total = 0;
   auto add = [&](size_t b) { total += (b + 255u) & ~(size_t)255u; };
   const size_t row_bytes = (size_t)dim * elem_bytes(store);
   const int cpl = pick_cpl((uint32_t)((row_bytes + 15) / 16));
   const size_t stride = (size_t)8 * (size_t)cpl * 16;
-  if (!(dtype == store && stride == row_bytes && (reinterpret_cast<uintptr_t>(d_data) & 15u) == 0))
+  if (!rows_ready && !(dtype == store && stride == row_bytes && (reinterpret_cast<uintptr_t>(d_data) & 15u) == 0))
     add(stride * N);  // padded or converted rows
   const size_t items = std::max<size_t>((size_t)N * R, 1);
   add((size_t)N * 4);               // deg_work
@@ -878,6 +890,219 @@ static int resident_build(const void* d_data, int dtype, uint32_t N, uint32_t di
   return 0;
 }
 
+// ---------------------------------------------------------------------------
+// Stitched build: per-label standard builds stitched into one global graph
+// (reference apps/utils/gpu_stitched_vamana_index.cpp:276-341).
+// ---------------------------------------------------------------------------
+static DanceStitchedStats g_last_stitched{};
+
+struct StitchedIn {
+  const void* data;  // N x dim rows of dtype (device or host)
+  bool data_on_device;
+  int dtype;
+  uint32_t N, dim;
+  const uint32_t* label_offsets;  // host, num_labels + 1
+  const uint32_t* label_points;   // host, ascending point ids per label
+  uint32_t num_labels;
+  uint32_t Rs, Ls, C, steps, Rout, row_cap;
+  uint32_t* graph;  // N x row_cap (device or host)
+  uint32_t* degree;
+  bool out_on_device;
+  uint32_t* medoids;  // host, num_labels
+};
+
+// Local rows of a label in the build's padded layout: row i is point ids[i]
+// of the packed input, converted to the stored type.
+static int gather_label_rows(const void* src, int dtype, int store, uint32_t dim, const uint32_t* d_ids, uint32_t m,
+                             uint32_t stride_elems, void* dst, hipStream_t s) {
+  const uint64_t total = (uint64_t)m * stride_elems;
+  if (total == 0) return 0;
+  const dim3 grid((uint32_t)((total + 255) / 256)), block(256);
+  if (dtype == DANCE_F32 && store == DANCE_F32)
+    hipLaunchKernelGGL((k_gather_rows<float, float>), grid, block, 0, s, static_cast<const float*>(src), dim, d_ids, m,
+                       static_cast<float*>(dst), stride_elems);
+  else if (dtype == DANCE_F32 && store == DANCE_F16)
+    hipLaunchKernelGGL((k_gather_rows<float, _Float16>), grid, block, 0, s, static_cast<const float*>(src), dim, d_ids,
+                       m, static_cast<_Float16*>(dst), stride_elems);
+  else if (dtype == DANCE_F16)
+    hipLaunchKernelGGL((k_gather_rows<_Float16, _Float16>), grid, block, 0, s, static_cast<const _Float16*>(src), dim,
+                       d_ids, m, static_cast<_Float16*>(dst), stride_elems);
+  else
+    hipLaunchKernelGGL((k_gather_rows<uint8_t, uint8_t>), grid, block, 0, s, static_cast<const uint8_t*>(src), dim,
+                       d_ids, m, static_cast<uint8_t*>(dst), stride_elems);
+  DHIP(hipGetLastError());
+  return 0;
+}
+
+// Callers hold g_mu.
+static int stitched_build(const StitchedIn& in) {
+  const double t0 = now_sec();
+  g_last_stitched = DanceStitchedStats{};
+  if (!in.data || !in.label_offsets || (in.num_labels && !in.label_points) || !in.graph || !in.degree ||
+      (in.num_labels && !in.medoids)) {
+    std::fprintf(stderr, "[gpu_stitched] null input pointer.\n");
+    return -1;
+  }
+  if (in.dtype != DANCE_F32 && in.dtype != DANCE_U8 && in.dtype != DANCE_F16) {
+    std::fprintf(stderr, "[gpu_stitched] unsupported dtype %d\n", in.dtype);
+    return -1;
+  }
+  if (in.N == 0 || in.dim == 0) {
+    std::fprintf(stderr, "[gpu_stitched] invalid parameters N=%u dim=%u\n", in.N, in.dim);
+    return -1;
+  }
+  // Label postings: monotone offsets, point ids in range; labels per point
+  // bound the global row length.
+  const uint32_t* off = in.label_offsets;
+  if (off[0] != 0) {
+    std::fprintf(stderr, "[gpu_stitched] label_offsets[0] must be 0\n");
+    return -1;
+  }
+  uint32_t m_max = 0, m_min = UINT32_MAX;
+  std::vector<uint32_t> per_point(in.N, 0);
+  for (uint32_t l = 0; l < in.num_labels; ++l) {
+    if (off[l + 1] < off[l]) {
+      std::fprintf(stderr, "[gpu_stitched] label_offsets must not decrease\n");
+      return -1;
+    }
+    const uint32_t m = off[l + 1] - off[l];
+    for (uint32_t k = off[l]; k < off[l + 1]; ++k) {
+      const uint32_t p = in.label_points[k];
+      if (p >= in.N || (k > off[l] && p <= in.label_points[k - 1])) {
+        std::fprintf(stderr, "[gpu_stitched] label %u: point ids must be ascending and below N\n", l);
+        return -1;
+      }
+      ++per_point[p];
+    }
+    if (m) {
+      m_max = std::max(m_max, m);
+      m_min = std::min(m_min, m);
+    }
+  }
+  const uint32_t take = std::min(in.Rs, in.Rout);
+  const uint32_t most = in.N ? *std::max_element(per_point.begin(), per_point.end()) : 0;
+  if ((uint64_t)most * take > in.row_cap || in.row_cap > 256 || in.row_cap == 0) {
+    std::fprintf(stderr,
+                 "[gpu_stitched] row_cap=%u: rows need %llu slots (%u labels x %u) and at most 256 are supported\n",
+                 in.row_cap, (unsigned long long)most * take, most, take);
+    return -1;
+  }
+  uint32_t steps = in.steps;
+  if (m_max) DCHECK(validate(m_max, in.dim, in.Rs, in.Ls, in.C, steps));
+  const Profile prof = kProfiles[profile_index_locked()];
+  const int store = (in.dtype == DANCE_F32 && prof.fp16) ? DANCE_F16 : in.dtype;
+  DCHECK(check_width(in.dim, store));
+
+  hipStream_t s = nullptr;
+  DHIP(hipStreamCreate(&s));
+  struct StreamGuard {
+    hipStream_t s;
+    ~StreamGuard() {
+      if (s) (void)hipStreamDestroy(s);
+    }
+  } sg{s};
+  const size_t in_row = (size_t)in.dim * elem_bytes(in.dtype);
+  DevBuf up_data, d_pts, d_graph, d_deg, d_ctr, arena_mem;
+  const void* src = in.data;
+  if (!in.data_on_device) {
+    DCHECK(up_data.alloc(in_row * in.N));
+    DHIP(hipMemcpyAsync(up_data.p, in.data, in_row * in.N, hipMemcpyHostToDevice, s));
+    src = up_data.p;
+  }
+  const uint32_t total = in.num_labels ? off[in.num_labels] : 0;
+  DCHECK(d_pts.alloc(std::max<size_t>(total, 1) * 4));
+  if (total) DHIP(hipMemcpyAsync(d_pts.p, in.label_points, (size_t)total * 4, hipMemcpyHostToDevice, s));
+  uint32_t* gg = in.graph;
+  uint32_t* gd = in.degree;
+  const size_t gcells = (size_t)in.N * in.row_cap;
+  if (!in.out_on_device) {
+    DCHECK(d_graph.alloc(gcells * 4));
+    DCHECK(d_deg.alloc((size_t)in.N * 4));
+    gg = d_graph.as<uint32_t>();
+    gd = d_deg.as<uint32_t>();
+  }
+  hipLaunchKernelGGL(k_fill_u32, dim3((uint32_t)((gcells + 255) / 256)), dim3(256), 0, s, gg, (uint64_t)gcells,
+                     DANCE_INV);
+  hipLaunchKernelGGL(k_fill_u32, dim3((in.N + 255) / 256), dim3(256), 0, s, gd, (uint64_t)in.N, 0u);
+  DCHECK(d_ctr.alloc(3 * 8));
+  hipLaunchKernelGGL(k_fill_u32, dim3(1), dim3(64), 0, s, d_ctr.as<uint32_t>(), (uint64_t)6, 0u);
+  DHIP(hipGetLastError());
+
+  // One device arena, sized for the largest label, serves every per-label
+  // build: rows, local graph, and all of the build's own buffers.
+  const size_t row_bytes = (size_t)in.dim * elem_bytes(store);
+  const int cpl = pick_cpl((uint32_t)((row_bytes + 15) / 16));
+  const uint32_t nch = 8u * (uint32_t)cpl;
+  const size_t stride = (size_t)nch * 16;
+  auto aligned = [](size_t b) { return (b + 255u) & ~(size_t)255u; };
+  const size_t arena_bytes = m_max ? aligned(stride * m_max) + aligned((size_t)m_max * in.Rs * 4) +
+                                         aligned((size_t)m_max * 4) +
+                                         resident_build_bytes(nullptr, store, store, m_max, in.dim, in.Rs, in.C, true)
+                                   : 0;
+  DCHECK(arena_mem.alloc(arena_bytes));
+  DanceStitchedStats st{};
+  st.labels = in.num_labels;
+  st.label_npts_min = m_max ? m_min : 0;
+  st.label_npts_max = m_max;
+  st.memberships = total;
+  st.row_cap = in.row_cap;
+  const double t_setup = now_sec();
+  for (uint32_t l = 0; l < in.num_labels; ++l) {
+    const uint32_t m = off[l + 1] - off[l];
+    if (m == 0) {
+      in.medoids[l] = DANCE_INV;
+      continue;
+    }
+    Arena arena{arena_mem.as<char>(), arena_bytes, 0};
+    ArenaScope scope(&arena);
+    const uint32_t* ids = d_pts.as<uint32_t>() + off[l];
+    const double tg = now_sec();
+    Rows rows;
+    DCHECK(rows.owned.alloc(stride * m));
+    DCHECK(gather_label_rows(src, in.dtype, store, in.dim, ids, m, (uint32_t)(stride / elem_bytes(store)),
+                             rows.owned.p, s));
+    rows.dtype = store;
+    rows.N = m;
+    rows.dim = in.dim;
+    rows.rs.rows = rows.owned.as<const uint4>();
+    rows.rs.stride16 = nch;
+    rows.rs.nch = nch;
+    rows.rs.tail16 = (store == DANCE_F16 && (in.dim & 1u)) ? (int32_t)((in.dim - 1u) / 2u) : -1;
+    DHIP(hipStreamSynchronize(s));
+    const double tb = now_sec();
+    st.materialize_seconds += tb - tg;
+    State lst;
+    DCHECK(lst.cur.alloc((size_t)m * in.Rs * 4));
+    DCHECK(lst.deg_cur.alloc((size_t)m * 4));
+    uint32_t medoid = 0;
+    DCHECK(run_build(rows, in.Rs, in.Ls, in.C, steps, prof, lst, s, nullptr, nullptr, &medoid, false));
+    const double tr = now_sec();
+    st.build_sum_seconds += tr - tb;
+    st.build_max_seconds = std::max(st.build_max_seconds, tr - tb);
+    RemapArgs ra{lst.cur.as<uint32_t>(), lst.deg_cur.as<uint32_t>(), ids, m, in.Rs, in.Rout, gg, gd, in.row_cap,
+                 d_ctr.as<unsigned long long>()};
+    hipLaunchKernelGGL(k_stitch_remap, dim3((m + kRemapWaves - 1) / kRemapWaves), dim3(64 * kRemapWaves), 0, s, ra);
+    DHIP(hipGetLastError());
+    DHIP(hipStreamSynchronize(s));
+    st.remap_seconds += now_sec() - tr;
+    in.medoids[l] = in.label_points[off[l] + (medoid < m ? medoid : 0u)];
+  }
+  unsigned long long c3[3] = {0, 0, 0};
+  DHIP(hipMemcpyAsync(c3, d_ctr.p, sizeof(c3), hipMemcpyDeviceToHost, s));
+  if (!in.out_on_device) {
+    DHIP(hipMemcpyAsync(in.graph, gg, gcells * 4, hipMemcpyDeviceToHost, s));
+    DHIP(hipMemcpyAsync(in.degree, gd, (size_t)in.N * 4, hipMemcpyDeviceToHost, s));
+  }
+  DHIP(hipStreamSynchronize(s));
+  st.remap_invalid_local_ids = c3[0];
+  st.remap_self_loops = c3[1];
+  st.remap_duplicate_edges = c3[2];
+  st.setup_seconds = t_setup - t0;
+  st.total_seconds = now_sec() - t0;
+  g_last_stitched = st;
+  return 0;
+}
+
 extern "C" {
 
 int gpu_vamana_vnew2_build(const uint8_t* h_data, uint32_t N, uint32_t dim, uint32_t R, uint32_t L, uint32_t C,
@@ -926,10 +1151,36 @@ int gpu_vamana_vnew2_build_device_float(const float* h_data, uint32_t N, uint32_
 }
 
 uint32_t dance_struct_sizes(uint64_t* sizes, uint32_t count) {
-  const uint64_t all[6] = {sizeof(GPUVamanaStats),   sizeof(DanceKernelProfile), sizeof(GPUFilteredVamanaStats),
-                           sizeof(DanceFilteredProfile), sizeof(DanceSearchStats), sizeof(DanceMergeStats)};
-  for (uint32_t i = 0; sizes && i < count && i < 6; ++i) sizes[i] = all[i];
-  return 6;
+  const uint64_t all[7] = {sizeof(GPUVamanaStats),   sizeof(DanceKernelProfile), sizeof(GPUFilteredVamanaStats),
+                           sizeof(DanceFilteredProfile), sizeof(DanceSearchStats), sizeof(DanceMergeStats),
+                           sizeof(DanceStitchedStats)};
+  for (uint32_t i = 0; sizes && i < count && i < 7; ++i) sizes[i] = all[i];
+  return 7;
+}
+
+int dance_stitched_build(const void* h_data, int dtype, uint32_t num_points, uint32_t dim,
+                         const uint32_t* label_offsets, const uint32_t* label_points, uint32_t num_labels,
+                         uint32_t R_small, uint32_t L_small, uint32_t C, uint32_t STEPS, uint32_t R_stitched,
+                         uint32_t row_cap, uint32_t* h_graph, uint32_t* h_degree, uint32_t* label_medoids) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return stitched_build(StitchedIn{h_data, false, dtype, num_points, dim, label_offsets, label_points, num_labels,
+                                   R_small, L_small, C, STEPS, R_stitched, row_cap, h_graph, h_degree, false,
+                                   label_medoids});
+}
+
+int dance_stitched_build_resident(const void* d_data, int dtype, uint32_t num_points, uint32_t dim,
+                                  const uint32_t* label_offsets, const uint32_t* label_points, uint32_t num_labels,
+                                  uint32_t R_small, uint32_t L_small, uint32_t C, uint32_t STEPS,
+                                  uint32_t R_stitched, uint32_t row_cap, uint32_t* d_graph, uint32_t* d_degree,
+                                  uint32_t* label_medoids) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return stitched_build(StitchedIn{d_data, true, dtype, num_points, dim, label_offsets, label_points, num_labels,
+                                   R_small, L_small, C, STEPS, R_stitched, row_cap, d_graph, d_degree, true,
+                                   label_medoids});
+}
+
+void dance_get_last_stitched_stats(DanceStitchedStats* stats) {
+  if (stats) *stats = g_last_stitched;
 }
 
 uint32_t gpu_vamana_vnew2_get_last_medoid(void) { return g_last_medoid; }

@@ -66,6 +66,36 @@ int dance_vamana_build_resident_noalloc(const void *d_data, int dtype, uint32_t 
                                         uint32_t R, uint32_t L, uint32_t C, uint32_t STEPS, uint32_t *d_graph,
                                         uint32_t *d_degree);
 
+/* Stitched build (reference: apps/utils/gpu_stitched_vamana_index.cpp,
+ * label loop :276-341). For each label l in order 0..num_labels-1 with points
+ * label_points[label_offsets[l] .. label_offsets[l+1]) (ascending ids), a
+ * standard build over those points with R_small, L_small, C, STEPS; then
+ * every local row is mapped to global ids and appended to its point's global
+ * row: at most R_stitched leading entries of the local row, dropping invalid
+ * local ids, self loops and ids the global row already holds. Rows of the
+ * global graph have row_cap slots (INVALID-padded past the degree); row_cap
+ * must hold every label of a point (labels x min(R_small, R_stitched)) and be
+ * at most 256. label_medoids[l] is the global id of label l's medoid
+ * (INVALID for a label without points). Label postings and medoids are host
+ * arrays. Returns 0, or -1 with a message. */
+typedef struct {
+    double setup_seconds, materialize_seconds, build_sum_seconds, build_max_seconds, remap_seconds, total_seconds;
+    uint64_t memberships, remap_invalid_local_ids, remap_self_loops, remap_duplicate_edges;
+    uint32_t labels, label_npts_min, label_npts_max, row_cap;
+} DanceStitchedStats;
+
+int dance_stitched_build(const void *h_data, int dtype, uint32_t num_points, uint32_t dim,
+                         const uint32_t *label_offsets, const uint32_t *label_points, uint32_t num_labels,
+                         uint32_t R_small, uint32_t L_small, uint32_t C, uint32_t STEPS, uint32_t R_stitched,
+                         uint32_t row_cap, uint32_t *h_graph, uint32_t *h_degree, uint32_t *label_medoids);
+/* The same with device rows (packed N x dim) and device outputs. */
+int dance_stitched_build_resident(const void *d_data, int dtype, uint32_t num_points, uint32_t dim,
+                                  const uint32_t *label_offsets, const uint32_t *label_points, uint32_t num_labels,
+                                  uint32_t R_small, uint32_t L_small, uint32_t C, uint32_t STEPS,
+                                  uint32_t R_stitched, uint32_t row_cap, uint32_t *d_graph, uint32_t *d_degree,
+                                  uint32_t *label_medoids);
+void dance_get_last_stitched_stats(DanceStitchedStats *stats);
+
 /* Timings and counters of the last build on this process. */
 void dance_get_last_kernel_profile(DanceKernelProfile *profile);
 

@@ -104,7 +104,7 @@ def lib() -> C.CDLL:
         L.oracle_reverse_merge.restype = u64
         L.oracle_prune.argtypes = [vp, i32, u32, u32, u32, u32, u32, f32, _u32p, _u32p, _f32p, _u32p, _u32p]
         L.oracle_prune.restype = None
-        L.oracle_vnew2_build.argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, u32, f32, u32, u32, _u32p,
+        L.oracle_vnew2_build.argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, u32, f32, u32, u32, u32, _u32p,
                                          _u32p, _u32p]
         L.oracle_vnew2_build.restype = i32
         L.oracle_cpu_vamana_build.argtypes = [vp, i32, u32, u32, u32, u32, f32, u32, _u32p, _u32p]
@@ -263,14 +263,17 @@ def prune(data: np.ndarray, s: State, min_degree: int, alpha: float) -> State:
 
 
 def vnew2_build(data: np.ndarray, R=64, L=100, C_=80, STEPS=64, iters=4, alpha=1.2, heavy_threshold=0,
-                heavy_sample=0):
+                heavy_sample=0, alpha_from=None):
+    """alpha_from: first iteration that prunes with alpha (default: the last,
+    the reference's default schedule)."""
     data = np.ascontiguousarray(data)
+    alpha_from = iters - 1 if alpha_from is None else alpha_from
     N = data.shape[0]
     graph = np.empty((N, R), np.uint32)
     deg = np.empty(N, np.uint32)
     med = np.zeros(1, np.uint32)
     rc = lib().oracle_vnew2_build(data.ctypes.data, _dt(data), N, data.shape[1], R, L, C_, STEPS, iters, alpha,
-                                  heavy_threshold, heavy_sample, _p(graph), _p(deg), _p(med))
+                                  alpha_from, heavy_threshold, heavy_sample, _p(graph), _p(deg), _p(med))
     if rc != 0:
         raise ValueError(f"oracle_vnew2_build rejected the parameters (rc={rc})")
     return graph, deg, int(med[0])

@@ -662,10 +662,10 @@ void init_graph(const Data& D, Graph& g) {
   }
 }
 
-float alpha_for_iter(uint32_t iter, uint32_t iters, float alpha) {
-  // gpu_vamana_alpha_for_iter, vnew2.cu:201-213: alpha only in the last iteration.
-  return (iter + 1 >= iters) ? alpha : 1.0f;
-}
+// gpu_vamana_alpha_for_iter, vnew2.cu:201-213: alpha from iteration
+// `from` on (default: the last iteration only; 0 = USE_ALPHA_FROM_FIRST_ITER,
+// k = VAMANA_ALPHA_FINAL_FROM_ITER=k).
+float alpha_for_iter(uint32_t iter, uint32_t from, float alpha) { return iter >= from ? alpha : 1.0f; }
 
 }  // namespace
 
@@ -761,8 +761,9 @@ void oracle_prune(const void* data, int dtype, uint32_t N, uint32_t dim, uint32_
 // Full standard build (gpu_vamana_build_impl, vnew2.cu:2170-2855).
 // Returns 0 on success, -1 on invalid parameters (same checks as vnew2.cu:2176-2204).
 int oracle_vnew2_build(const void* data, int dtype, uint32_t N, uint32_t dim, uint32_t R, uint32_t L,
-                       uint32_t C, uint32_t STEPS, uint32_t iters, float alpha, uint32_t heavy_threshold,
-                       uint32_t heavy_sample, uint32_t* graph_out, uint32_t* degree_out, uint32_t* medoid_out) {
+                       uint32_t C, uint32_t STEPS, uint32_t iters, float alpha, uint32_t alpha_from,
+                       uint32_t heavy_threshold, uint32_t heavy_sample, uint32_t* graph_out, uint32_t* degree_out,
+                       uint32_t* medoid_out) {
   if (data == nullptr || graph_out == nullptr || degree_out == nullptr) return -1;
   if (N == 0 || dim == 0 || R == 0 || L == 0 || C == 0 || STEPS == 0) return -1;
   if (C < R) return -1;
@@ -774,7 +775,7 @@ int oracle_vnew2_build(const void* data, int dtype, uint32_t N, uint32_t dim, ui
   uint32_t start = medoid(D, nullptr, nullptr);
   init_graph(D, g);
   for (uint32_t it = 0; it < iters; ++it) {
-    float a = alpha_for_iter(it, iters, alpha);
+    float a = alpha_for_iter(it, alpha_from, alpha);
     uint32_t steps = STEPS;
     // ENABLE_COARSE_TO_FINE_STEPS: WARMUP_EXPAND_STEPS=64 for COARSE_WARMUP_ITERS=2 (config.h:66-77).
     if (it < 2 && steps > 64) steps = 64;

@@ -167,19 +167,13 @@ def test_c5_stitched_equals_oracle():
     x = D.synth_u8(42, 0, n, C5["dim"], C5["centers"], C5["sigma"])
     part = np.random.default_rng(44).integers(0, C5["parts"], n).astype(np.uint32)
     assert digest(x, part) == fx["input"]
-    graph = np.full((n, C5["Rstitched"]), INVALID, np.uint32)
-    deg = np.zeros(n, np.uint32)
-    medoids = np.full(C5["parts"], INVALID, np.uint32)
-    for l in range(C5["parts"]):
-        ids = np.nonzero(part == l)[0].astype(np.uint32)
-        res = D.vamana_build(np.ascontiguousarray(x[ids]), C5["Rsmall"], C5["Lsmall"], C5["Cs"], C5["STEPS"])
-        ok = (np.arange(C5["Rsmall"])[None, :] < res.degree[:, None]) & (res.graph < ids.size)
-        order = np.argsort(~ok, axis=1, kind="stable")  # kept entries first, in row order
-        loc = np.take_along_axis(res.graph, order, 1)
-        okc = np.take_along_axis(ok, order, 1)
-        graph[ids, :C5["Rsmall"]] = np.where(okc, ids[np.minimum(loc, ids.size - 1)], INVALID)
-        deg[ids] = ok.sum(1)
-        medoids[l] = ids[res.medoid]
-    print(f"[c5s_1m] degree sum {int(deg.sum())} (oracle {fx['degree_sum']})", flush=True)
+    # label postings: points of each partition in ascending order
+    pts = np.argsort(part, kind="stable").astype(np.uint32)
+    off = np.zeros(C5["parts"] + 1, np.uint32)
+    off[1:] = np.cumsum(np.bincount(part, minlength=C5["parts"]))
+    graph, deg, medoids, st = D.stitched_build(x, off, pts, C5["Rsmall"], C5["Lsmall"], C5["Cs"], C5["STEPS"],
+                                               C5["Rstitched"], row_cap=C5["Rstitched"])
+    print(f"[c5s_1m] degree sum {int(deg.sum())} (oracle {fx['degree_sum']}), builds {st['build_sum_seconds']:.2f} s",
+          flush=True)
     assert int(deg.sum()) == fx["degree_sum"]
     assert digest(graph, deg, medoids) == fx["graph"]

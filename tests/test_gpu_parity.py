@@ -197,6 +197,21 @@ def test_end_to_end_graph_identical(kind, n, R, L, C, steps):
     assert np.array_equal(res.graph, og)
 
 
+@pytest.mark.parametrize("alpha_from", [0, 2])
+def test_end_to_end_alpha_schedule(alpha_from, monkeypatch):
+    """The reference's alpha-schedule knobs (USE_ALPHA_FROM_FIRST_ITER = from
+    0, VAMANA_ALPHA_FINAL_FROM_ITER = k) through DANCE_ALPHA_FROM_ITER."""
+    monkeypatch.setenv("DANCE_ALPHA_FROM_ITER", str(alpha_from))
+    data = make_data("f32", 4000, 96, seed=21)
+    res = D.vamana_build(data, 32, 64, 48, 32)
+    og, od, om = O.vnew2_build(data, 32, 64, 48, 32, alpha_from=alpha_from)
+    assert res.medoid == om
+    assert np.array_equal(res.degree, od)
+    assert np.array_equal(res.graph, og)
+    default, _, _ = O.vnew2_build(data, 32, 64, 48, 32)
+    assert not np.array_equal(default, og)  # the schedule changes the graph
+
+
 @pytest.mark.parametrize("kind,dim", [("f32", 512), ("u8", 2048), ("f32", 200)])
 def test_end_to_end_wide_rows(kind, dim):
     # the widest supported rows (16 chunks of 16 bytes per lane) and a width

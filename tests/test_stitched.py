@@ -145,3 +145,59 @@ def test_stitched_multi_label_needs_global_prune(tmp_path):
     assert os.path.exists(prefix + "_full")
     adj, *_ = formats.read_graph(prefix + "_full")
     assert max(len(a) for a in adj) > 16  # two labels contribute up to Rstitched each
+
+
+def postings_from_rows(rows):
+    """Label postings (ids 1.. by first appearance, repeats in a row dropped):
+    label offsets and ascending point ids, label order = id order."""
+    names, points = [], []
+    for pid, r in enumerate(rows):
+        seen = []
+        for tok in r.replace(" ", "").split(","):
+            if tok not in seen:
+                seen.append(tok)
+        for tok in seen:
+            if tok not in names:
+                names.append(tok)
+                points.append([])
+            points[names.index(tok)].append(pid)
+    off = np.zeros(len(points) + 1, np.uint32)
+    off[1:] = np.cumsum([len(p) for p in points])
+    return names, off, np.array([i for p in points for i in p], np.uint32)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("Rs,Rout", [(16, 16), (16, 8), (12, 40)])
+def test_stitched_entry_multi_label_rows(Rs, Rout):
+    """dance_stitched_build against per-label oracle builds remapped in Python:
+    multi-label rows (ids repeated across labels are dropped), a label of one
+    point, R_stitched below R_small (only the leading entries are taken)."""
+    rng = np.random.default_rng(Rs + Rout)
+    n = 1500
+    x = rng.integers(0, 256, (n, 48), dtype=np.uint8)
+    rows = []
+    for i in range(n):
+        k = 1 + int(rng.integers(0, 3))
+        rows.append(",".join(f"L{v}" for v in rng.choice(5, k, replace=False)))
+    rows[7] = "solo"
+    names, off, pts = postings_from_rows(rows)
+    g, d, med, st = D.stitched_build(x, off, pts, Rs, 32, 24, 16, Rout)
+
+    def oracle_build(xl):
+        return O.vnew2_build(np.ascontiguousarray(xl), Rs, 32, 24, 16)
+    _, want, want_med = expected_stitched(x, rows, Rs, 32, Rout, 24, 16, oracle_build)
+    assert med.tolist() == want_med
+    for v in range(n):
+        assert g[v, :d[v]].tolist() == want[v], v
+        assert np.all(g[v, d[v]:] == D.INVALID)
+    assert st["memberships"] == pts.size and st["labels"] == len(names)
+    assert st["remap_duplicate_edges"] > 0  # rows share points across labels
+
+
+@pytest.mark.gpu
+def test_stitched_entry_rejects_short_rows():
+    x = np.zeros((10, 8), np.uint8)
+    off = np.array([0, 10, 20], np.uint32)
+    pts = np.concatenate([np.arange(10), np.arange(10)]).astype(np.uint32)
+    with pytest.raises(D.BuildError):
+        D.stitched_build(x, off, pts, 8, 16, 16, 8, 8, row_cap=8)  # two labels per point need 16 slots
