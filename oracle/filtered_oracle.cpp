@@ -7,7 +7,8 @@
 //   (canonical_round0_from_host_backbone_typed, :5663-6483) -> diagnostics
 //   (filtered_graph_diagnostics_kernel, :2716-2774).
 // Float input is searched on fp16 rows (:6497-6503); the distance is the
-// canonical one of vamana_oracle.cpp (fp16 widened to fp32, same order).
+// canonical one of vamana_oracle.cpp (binary16 differences and squares,
+// filtered.cu:4036-4047).
 // The reference fills its reverse CSR with atomics, but the CSR prune selects
 // by (distance, id) over unique ids, so its result does not depend on that
 // order; this oracle uses ascending sources.
@@ -608,6 +609,27 @@ uint32_t oracle_filtered_merge(uint32_t N, uint32_t R, uint32_t C, uint32_t per_
     out_d[i] = i < ordinary_keep ? ord_d[i] : FLT_MAX;
   }
   return merge_row(c, graph, degrees, row, C, per_label_keep, ordinary_keep, task_ids, task_d, out_ids, out_d);
+}
+
+// Pinning hooks (tests only): one per-label task search and one union
+// (ordinary) search over an explicit graph.
+void oracle_filtered_task_search(const void* data, int dtype, uint32_t N, uint32_t dim, uint32_t R,
+                                 const uint32_t* offsets, const uint32_t* labels, uint32_t total_labels,
+                                 const uint32_t* starts, uint32_t num_labels, uint32_t universal,
+                                 const uint32_t* graph, const uint32_t* degrees, uint32_t row, uint32_t label,
+                                 uint32_t pool_cap, uint32_t keep, uint32_t steps, uint32_t* out_ids,
+                                 float* out_d) {
+  Ctx c = make_ctx(data, dtype, N, dim, R, offsets, labels, total_labels, starts, num_labels, universal);
+  task_search(c, graph, degrees, row, label, pool_cap, keep, steps, out_ids, out_d);
+}
+
+void oracle_filtered_ordinary_search(const void* data, int dtype, uint32_t N, uint32_t dim, uint32_t R,
+                                     const uint32_t* offsets, const uint32_t* labels, uint32_t total_labels,
+                                     const uint32_t* starts, uint32_t num_labels, const uint32_t* graph,
+                                     const uint32_t* degrees, uint32_t row, uint32_t pool_cap, uint32_t keep,
+                                     uint32_t steps, uint32_t global_start, uint32_t* out_ids, float* out_d) {
+  Ctx c = make_ctx(data, dtype, N, dim, R, offsets, labels, total_labels, starts, num_labels, INV);
+  ordinary_search(c, graph, degrees, row, pool_cap, keep, steps, global_start, out_ids, out_d);
 }
 
 }  // extern "C"

@@ -88,6 +88,12 @@ def lib() -> C.CDLL:
         L.oracle_half_sq_of_diff.restype = f32
         L.oracle_robust_insert.argtypes = [vp, i32, u32, u32, u32, u32, u32, f32, f32, _u32p, _f32p, _u32p]
         L.oracle_robust_insert.restype = None
+        L.oracle_filtered_task_search.argtypes = [vp, i32, u32, u32, u32, _u32p, _u32p, u32, _u32p, u32, u32,
+                                                  _u32p, _u32p, u32, u32, u32, u32, u32, _u32p, _f32p]
+        L.oracle_filtered_task_search.restype = None
+        L.oracle_filtered_ordinary_search.argtypes = [vp, i32, u32, u32, u32, _u32p, _u32p, u32, _u32p, u32,
+                                                      _u32p, _u32p, u32, u32, u32, u32, u32, _u32p, _f32p]
+        L.oracle_filtered_ordinary_search.restype = None
         L.oracle_distance.argtypes = [vp, i32, u32, u32, u32]
         L.oracle_distance.restype = f32
         L.oracle_distance_many.argtypes = [vp, i32, u32, _u32p, _u32p, u64, _f32p]
@@ -368,6 +374,39 @@ def filtered_prune(data: np.ndarray, offsets: np.ndarray, labels: np.ndarray, ro
                                     _p(np.ascontiguousarray(labels, np.uint32)), row, _p(ids), _p(ds, C.c_float),
                                     ids.shape[0], _p(out))
     return out[:n]
+
+
+def _search_inputs(data, offsets, labels, starts, graph, degree):
+    return (np.ascontiguousarray(data), np.ascontiguousarray(offsets, np.uint32),
+            np.ascontiguousarray(labels, np.uint32), np.ascontiguousarray(starts, np.uint32),
+            np.ascontiguousarray(graph, np.uint32), np.ascontiguousarray(degree, np.uint32))
+
+
+def filtered_task_search(data, offsets, labels, starts, num_labels: int, universal: int, graph, degree, row: int,
+                         label: int, pool_cap: int, keep: int, steps: int):
+    """One per-label task search (the oracle's canonical_filtered_task_search);
+    returns the `keep` emitted (ids, distances)."""
+    data, offsets, labels, starts, graph, degree = _search_inputs(data, offsets, labels, starts, graph, degree)
+    ids = np.empty(keep, np.uint32)
+    d = np.empty(keep, np.float32)
+    lib().oracle_filtered_task_search(data.ctypes.data, _dt(data), data.shape[0], data.shape[1], graph.shape[1],
+                                      _p(offsets), _p(labels), labels.shape[0], _p(starts), num_labels, universal,
+                                      _p(graph), _p(degree), row, label, pool_cap, keep, steps, _p(ids),
+                                      _p(d, C.c_float))
+    return ids, d
+
+
+def filtered_ordinary_search(data, offsets, labels, starts, num_labels: int, graph, degree, row: int,
+                             pool_cap: int, keep: int, steps: int, global_start: int):
+    """One union (ordinary) search (the oracle's canonical_ordinary_search)."""
+    data, offsets, labels, starts, graph, degree = _search_inputs(data, offsets, labels, starts, graph, degree)
+    ids = np.empty(keep, np.uint32)
+    d = np.empty(keep, np.float32)
+    lib().oracle_filtered_ordinary_search(data.ctypes.data, _dt(data), data.shape[0], data.shape[1],
+                                          graph.shape[1], _p(offsets), _p(labels), labels.shape[0], _p(starts),
+                                          num_labels, _p(graph), _p(degree), row, pool_cap, keep, steps,
+                                          global_start, _p(ids), _p(d, C.c_float))
+    return ids, d
 
 
 def filtered_merge(N: int, R: int, C_: int, keep: int, offsets, labels, num_labels: int, graph, degree, row: int,

@@ -9,6 +9,7 @@ import pytest
 
 import dance_amd as D
 from dance_amd import formats
+from oracle import oracle as O
 
 APP = os.path.join(os.path.dirname(D.__file__), "gpu_vamana_memory_index")
 
@@ -66,11 +67,11 @@ def test_build_writes_diskann_index(tmp_path, kind):
     assert rep["graph_valid"] and rep["memory_index_serialized"] and rep["npts"] == 2000
     assert rep["invalid_neighbor_count"] == 0 and rep["self_loop_count"] == 0
     adj, max_deg, start, frozen = formats.read_graph(prefix)
-    want = D.vamana_build(x[500:2500], 32, 64, 48, 32)
-    assert start == want.medoid == rep["medoid"] and frozen == 0
-    assert max_deg == int(want.degree.max())
+    og, od, om = O.vnew2_build(np.ascontiguousarray(x[500:2500]), 32, 64, 48, 32)
+    assert start == om == rep["medoid"] and frozen == 0
+    assert max_deg == int(od.max())
     for v in range(2000):
-        assert np.array_equal(adj[v], want.graph[v, :want.degree[v]])
+        assert np.array_equal(adj[v], og[v, :od[v]])
     back = formats.read_bin(prefix + ".data", np.float32 if kind == "float" else np.uint8)
     assert np.array_equal(back, x[500:2500])
     # refuses to overwrite an existing index

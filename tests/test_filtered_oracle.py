@@ -303,3 +303,208 @@ def test_publish_matches_composition(PR, universal):
     # at or above R the publish step does nothing
     rc, g2, d2, _ = O.filtered_build(*args, publish_R=R)
     assert rc == 0 and np.array_equal(g2, g) and np.array_equal(d2, d)
+
+
+# ------------------------------------------------- task and union searches
+
+def search_case(seed, N=160, dim=4, vocab=6, R=6):
+    """Small-integer rows (exact, frequently tied distances), 1-3 labels per
+    point, a random graph with invalid and self entries, label starts."""
+    rng = np.random.default_rng(seed)
+    x = rng.integers(0, 4, (N, dim)).astype(np.uint8)
+    rows = [list(rng.choice(vocab, int(rng.integers(1, 4)), replace=False)) for _ in range(N)]
+    ls = F.canonical_labels(rows, vocab)
+    graph = rng.integers(0, N, (N, R)).astype(np.uint32)
+    graph[rng.random((N, R)) < 0.05] = INVALID
+    for v in range(0, N, 17):
+        graph[v, 0] = v  # self entries are skipped
+    deg = rng.integers(0, R + 1, N).astype(np.uint32)
+    starts = F.label_starts(x, ls)
+    return x, ls, graph, deg, starts
+
+
+def best_first_slots(x, row, seeds, admissible, graph, deg, cap, steps):
+    """The canonical pool of filtered.cu:4156-4263, restated with Python
+    lists: slots in insertion order; an id already present keeps its slot
+    (its distance can only be the same); a new id is appended while there is
+    room, else replaces the slot of the worst (distance, id) if it is better;
+    each step expands the unexpanded slot of smallest (distance, id).
+    `seeds` are inserted first, in order; expansions insert the admissible
+    neighbours. Returns the slots as (id, distance)."""
+    N, R = graph.shape
+    slots = []  # [id, distance, expanded]
+
+    def offer(v):
+        if any(s[0] == v for s in slots):
+            return
+        d = np.float32(O.distance(x, row, v))
+        if len(slots) < cap:
+            slots.append([v, d, False])
+            return
+        w = max(range(len(slots)), key=lambda p: (slots[p][1], slots[p][0]))
+        if (d, v) < (slots[w][1], slots[w][0]):
+            slots[w] = [v, d, False]
+
+    for v in seeds:
+        offer(v)
+    for _ in range(steps):
+        open_ = [p for p in range(len(slots)) if not slots[p][2]]
+        if not open_:
+            break
+        p = min(open_, key=lambda q: (slots[q][1], slots[q][0]))
+        slots[p][2] = True
+        e = slots[p][0]
+        for j in range(min(int(deg[e]), R)):
+            v = int(graph[e, j])
+            if v < N and v != row and admissible(v):
+                offer(v)
+    return [(s[0], s[1]) for s in slots]
+
+
+def label_seeds(ls, row, label, count):
+    """Posting-list seeds h(row + s*7919 + label*17) mod |P(label)|, in s order."""
+    off, pts = ls.postings()
+    pc = int(off[label + 1] - off[label])
+    out = []
+    for s in range(min(count, pc)):
+        out.append(int(pts[off[label] + O.hash_u32((row + s * 7919 + label * 17) & 0xFFFFFFFF) % pc]))
+    return out
+
+
+@pytest.mark.parametrize("seed", [1, 2])
+@pytest.mark.parametrize("cap", [8, 32, 200])
+def test_task_search_matches_restated_pool(seed, cap):
+    """canonical_filtered_task_search (filtered.cu:4265-4426): start, up to 16
+    posting seeds, the row's label-carrying neighbours, then 64 expansions
+    over label carriers; the first `keep` slots are emitted. cap 200 holds
+    every carrier (no eviction: the emitted ids are the first eight distinct
+    ids in insertion order); caps 8 and 32 evict."""
+    x, ls, graph, deg, starts = search_case(seed)
+    N = x.shape[0]
+    keep = 8
+    for row in range(0, N, 7):
+        for label in ls.row(row).tolist() + [int(ls.num_labels), 0]:
+            got_i, got_d = O.filtered_task_search(x, ls.offsets, ls.labels, starts, ls.num_labels, INVALID, graph,
+                                                  deg, row, label, cap, keep, 64)
+            if label >= ls.num_labels:
+                assert (got_i == INVALID).all() and (got_d == FMAX).all()
+                continue
+            carriers = labels_of
+
+            def admissible(v, label=label):
+                return label in carriers(ls, v)
+            seeds = []
+            st = int(starts[label])
+            if st < N and st != row:
+                seeds.append(st)
+            seeds += [v for v in label_seeds(ls, row, label, 16) if v != row]
+            seeds += [int(v) for v in graph[row, :min(int(deg[row]), graph.shape[1])]
+                      if v < N and v != row and admissible(int(v))]
+            slots = best_first_slots(x, row, seeds, admissible, graph, deg, cap, 64)
+            want = slots[:keep] + [(INVALID, FMAX)] * (keep - min(keep, len(slots)))
+            assert got_i.tolist() == [w[0] for w in want], (row, label)
+            assert np.array_equal(got_d, np.array([w[1] for w in want], np.float32))
+
+
+def test_task_search_universal_label_emits_nothing():
+    x, ls, graph, deg, starts = search_case(3)
+    got_i, _ = O.filtered_task_search(x, ls.offsets, ls.labels, starts, ls.num_labels, 2, graph, deg, 5, 2, 32, 8,
+                                      64)
+    assert (got_i == INVALID).all()
+
+
+@pytest.mark.parametrize("seed", [4, 5])
+@pytest.mark.parametrize("cap", [16, 64, 400])
+def test_union_search_matches_restated_pool(seed, cap):
+    """canonical_ordinary_search (filtered.cu:4529-4670): per row label its
+    start and up to 64 posting seeds, the global start when it shares a row
+    label, the row's compatible neighbours, 64 expansions over points sharing
+    a row label; the first `keep` slots are emitted (INVALID past the pool)."""
+    x, ls, graph, deg, starts = search_case(seed, N=240)
+    N = x.shape[0]
+    keep = 64
+    gstart = F.global_start(x)
+    for row in range(0, N, 11):
+        fr = labels_of(ls, row)
+
+        def admissible(v, fr=fr):
+            return bool(fr & labels_of(ls, v))
+        seeds = []
+        for label in ls.row(row).tolist():
+            st = int(starts[label])
+            if st < N and st != row:
+                seeds.append(st)
+            seeds += [v for v in label_seeds(ls, row, label, 64) if v != row]
+        if gstart != row and admissible(gstart):
+            seeds.append(gstart)
+        seeds += [int(v) for v in graph[row, :min(int(deg[row]), graph.shape[1])]
+                  if v < N and v != row and admissible(int(v))]
+        slots = best_first_slots(x, row, seeds, admissible, graph, deg, cap, 64)
+        got_i, got_d = O.filtered_ordinary_search(x, ls.offsets, ls.labels, starts, ls.num_labels, graph, deg, row,
+                                                  cap, keep, 64, gstart)
+        want = slots[:keep] + [(INVALID, FMAX)] * (keep - min(keep, len(slots)))
+        assert got_i.tolist() == [w[0] for w in want], row
+        assert np.array_equal(got_d, np.array([w[1] for w in want], np.float32))
+
+
+# ------------------------------------------------- label quota, many labels
+
+def brute_force_quota(ls, row, merged, R, keep):
+    """Label-quota compaction (filtered.cu:4703-4842) restated with Python
+    sets: each merged candidate, in order, takes the row label it carries
+    with the fewest points (ties: smaller label id) among labels whose count
+    is below quota = max(ceil(R / |F_row|), keep), or is dropped; rows with
+    no label or more than 16 keep the merged list as it is."""
+    off, _ = ls.postings()
+    card = {l: int(off[l + 1] - off[l]) for l in range(ls.num_labels)}
+    fr = sorted(ls.row(row).tolist())
+    if not (1 <= len(fr) <= 16):
+        return merged
+    quota = max(-(-R // len(fr)), keep)
+    counts = {l: 0 for l in fr}
+    kept = []
+    for c in merged:
+        options = [l for l in fr if l in labels_of(ls, c) and counts[l] < quota]
+        if not options:
+            continue
+        best = min(options, key=lambda l: (card[l], l))
+        counts[best] += 1
+        kept.append(c)
+    assert all(v <= quota for v in counts.values())
+    return kept
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_merge_multi_label_quota_with_cardinality_ties(seed):
+    """Rows with 2..16 labels, several labels of equal posting size (ties go
+    to the smaller label id), small quotas that fill up and drop candidates."""
+    rng = np.random.default_rng(40 + seed)
+    N, R, keep, vocab = 400, 12, 2, 18
+    # labels 0..5 get exactly 40 carriers each (cardinality ties), the rest random
+    rows = [[] for _ in range(N)]
+    for l in range(6):
+        for v in rng.choice(N, 40, replace=False):
+            rows[v].append(l)
+    for v in range(N):
+        rows[v] += list(rng.choice(np.arange(6, vocab), int(rng.integers(0, 4)), replace=False))
+        if not rows[v]:
+            rows[v] = [6]
+    rows[3] = list(range(16))           # 16 labels: quota applies
+    rows[4] = list(range(17))           # 17 labels: no quota
+    rows[5] = [0, 1, 2]                 # three tied labels
+    ls = F.canonical_labels(rows, vocab)
+    for row in [3, 4, 5] + list(range(6, 60)):
+        tids, td, graph, deg, oid, od = merge_inputs(rng, N, R, ls, row, keep, 96)
+        got_i, _ = O.filtered_merge(N, R, 128, keep, ls.offsets, ls.labels, vocab, graph, deg, row, tids, td, oid,
+                                    od)
+        streams = []
+        for p in range(ls.offsets[row], ls.offsets[row + 1]):
+            streams += [(int(tids[p, i]), float(td[p, i])) for i in range(keep)]
+        fr = labels_of(ls, row)
+        for i in range(min(int(deg[row]), R)):
+            c = int(graph[row, i])
+            if c < N and c != row and fr & labels_of(ls, c):
+                streams.append((c, float(FMAX)))
+        streams += [(int(c), float(d)) for c, d in zip(oid, od)]
+        merged, _ = dict_merge(row, N, 128, streams)
+        assert got_i.tolist() == brute_force_quota(ls, row, merged, R, keep), row

@@ -171,14 +171,19 @@ def test_filtered_tiny(n):
     assert_same(x, ls, starts, gs, 16, 32, 32, 64, 16)
 
 
-def test_filtered_abi_float_entry_matches_extension():
-    """gpu_vamana_filtered_build_float (reference entry) == fp16 search of the
-    rounded rows through the extension entry."""
+def test_filtered_abi_float_entry_equals_oracle():
+    """gpu_vamana_filtered_build_float (the reference entry: float input is
+    searched as round-to-nearest fp16 rows, filtered.cu:6497-6503) against
+    the oracle's filtered build of the same rows; the extension entry on the
+    rounded fp16 rows gives the same graph."""
     x, ls = make_case("f32", 2000, 96, 30, 3, seed=3)
     starts, gs = F.label_starts(x, ls), F.global_start(x)
     a = F.filtered_build(x, ls, starts, 32, 64, 64, 750, 32, 1.2, INVALID, gs)
+    orc, og, od, _ = O.filtered_build(x, ls.offsets, ls.labels, starts, ls.num_labels, 32, 64, 64, 750, 32, 1.2,
+                                      INVALID, gs, 3)
+    assert orc == 0 and np.array_equal(a.graph, og) and np.array_equal(a.degree, od)
     b = F.filtered_build(x.astype(np.float16), ls, starts, 32, 64, 64, 750, 32, 1.2, INVALID, gs)
-    assert np.array_equal(a.graph, b.graph) and np.array_equal(a.degree, b.degree)
+    assert np.array_equal(b.graph, og) and np.array_equal(b.degree, od)
     assert a.profile["rounds"] == 3 and a.stats["gpu_build_seconds"] > 0
 
 

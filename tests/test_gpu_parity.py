@@ -276,5 +276,6 @@ def test_build_device_handoff():
     for p in (dd, dg, ddeg):
         assert hip.hipFree(p) == 0
     assert np.array_equal(back, data)
-    want = D.vamana_build(data, R, 64, 48, 32)
-    assert np.array_equal(graph, want.graph) and np.array_equal(deg, want.degree)
+    og, od, om = O.vnew2_build(data, R, 64, 48, 32)
+    assert np.array_equal(graph, og) and np.array_equal(deg, od)
+    assert D.lib().gpu_vamana_vnew2_get_last_medoid() == om
