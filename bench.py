@@ -555,6 +555,8 @@ def main() -> int:
         "abi": abi,
         "stage_ms": {k: round(kp[k], 2) for k in ("medoid_ms", "init_ms", "search_ms", "reverse_ms", "merge_ms",
                                                      "prune_ms", "total_ms")},
+        "launch_ms": {"search": [round(v, 2) for v in kp["search_iter_ms"]],
+                      "prune": [round(v, 2) for v in kp["prune_iter_ms"]]},
         "counters": {k: kp[k] for k in ("search_dist", "insert_dist", "expansions", "vis_skips", "merge_dist",
                                         "prune_dist", "reverse_edges", "bound_checks", "bound_skips",
                                         "prune_bound_checks", "prune_bound_skips")},

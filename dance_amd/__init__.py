@@ -64,6 +64,7 @@ class DanceKernelProfile(C.Structure):
         ("cyc_pool", C.c_uint64), ("cyc_seed", C.c_uint64), ("cyc_total", C.c_uint64),
         ("bound_checks", C.c_uint64), ("bound_skips", C.c_uint64),
         ("prune_bound_checks", C.c_uint64), ("prune_bound_skips", C.c_uint64),
+        ("search_iter_ms", C.c_double * 4), ("prune_iter_ms", C.c_double * 4),
     ]
 
 
@@ -132,7 +133,11 @@ class DanceStitchedStats(C.Structure):
 
 
 def struct_dict(s: C.Structure) -> dict:
-    return {name: getattr(s, name) for name, _ in s._fields_}
+    out = {}
+    for name, _ in s._fields_:
+        v = getattr(s, name)
+        out[name] = list(v) if isinstance(v, C.Array) else v
+    return out
 
 
 # Every symbol the C ABI exports (include/*.h). Tests check the library

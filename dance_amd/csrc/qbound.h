@@ -167,6 +167,17 @@ __device__ __forceinline__ uint4 q_load(const QBoundSet& qb, uint32_t id, bool a
   return b;
 }
 
+// The bound's test for one pair: the querying row's scale s and a, the
+// candidate's header (sy, ry, ay), sT from q_threshold (or the prune's root)
+// and the exact integer code dot c. Every caller evaluates this expression,
+// so a decision does not depend on how c was computed.
+__device__ __forceinline__ bool q_pair_proves(float s, float a, float sT, float sy, float ry, float ay, int c) {
+  const float sa = a + ay;
+  const float q = __builtin_fmaf(-2.0f * (s * sy), (float)c, sa) - kQSlack * sa - 1e-30f;
+  const float w = (sT + ry) * (1.0f + kQSlack);
+  return q >= w * w * (1.0f + kQSlack);
+}
+
 // Octet test for a candidate: every lane of the octet holds one chunk `b` of
 // its code row (q_load); the lane with sub == 0 (which holds the header)
 // returns whether the bound proves dist >= T. `code` is chunk `sub` of the
@@ -182,12 +193,7 @@ __device__ __forceinline__ bool q_proves_reject(const QSelf& me, const uint4& co
   c += dpp<kDppHalfMirror>(0, c);
   c += dpp<kDppQuadXor2>(0, c);
   c += dpp<kDppQuadXor1>(0, c);
-  const float sy = __uint_as_float(b.x);
-  const float ry = __uint_as_float(b.y);
-  const float sa = me.a + __uint_as_float(b.z);
-  const float q = __builtin_fmaf(-2.0f * (me.s * sy), (float)c, sa) - kQSlack * sa - 1e-30f;
-  const float w = (sT + ry) * (1.0f + kQSlack);
-  return active && q >= w * w * (1.0f + kQSlack);
+  return active && q_pair_proves(me.s, me.a, sT, __uint_as_float(b.x), __uint_as_float(b.y), __uint_as_float(b.z), c);
 }
 
 // Threshold of the prune's bound for a candidate at stored distance sd: a

@@ -64,6 +64,7 @@ struct Profile {
   uint32_t heavy_threshold, heavy_sample;
 };
 constexpr uint32_t kIters = 4;              // VAMANA_ITERS
+static_assert(kIters <= 4, "DanceKernelProfile keeps per-iteration times for 4 iterations");
 constexpr float kAlpha = 1.2f;              // VAMANA_ALPHA (last iteration only)
 constexpr uint32_t kFinalMinDegree = 64;    // FINAL_MIN_DEGREE
 constexpr uint32_t kWarmupSteps = 64;       // WARMUP_EXPAND_STEPS
@@ -223,15 +224,44 @@ static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t ste
   });
 }
 
+// Which prune kernel: in the iterations whose bit is set in
+// DANCE_PRUNE_RANK_ITERS (default kPruneRankIters), rows of at most kRankCap
+// candidates take k_prune_rank (with the bound's pair decisions from MFMA
+// tiles when qb is on); otherwise, and for wider rows, k_prune. Both give the
+// same graph. The default follows the c3 per-launch times: iteration 0
+// (alpha 1 right after the random graph: few rounds per row, so the rank
+// kernel's up-front sort and all-pairs tiles do not pay) is fastest with
+// k_prune and the bound; iterations 1-3 with k_prune_rank.
+constexpr uint32_t kPruneRankIters = 0xEu;
+static uint32_t prune_rank_iters() { return env_mask("DANCE_PRUNE_RANK_ITERS", kPruneRankIters); }
+
 static int launch_prune(const Rows& rows, GraphBufs g, uint32_t min_degree, float alpha, const uint32_t* order,
-                        VCounters* ctr, const QBoundSet& qb, hipStream_t s) {
+                        VCounters* ctr, const QBoundSet& qb, bool rank_kernel, hipStream_t s) {
   const int cpl = pick_cpl(rows.rs.nch);
-  const uint32_t Cp = round64(g.C), Rp = round64(g.R);
-  const size_t lds = (size_t)kWavesPerBlock * prune_lds_words(Cp, Rp) * 4;
+  const uint32_t Cp = round64(g.C), Rp = round64(g.R), Cq = (g.C + 31u) / 32u * 32u;
   PruneArgs a{rows.rs, g, min_degree, alpha, order, ctr, qb};
+  const bool rank = Cp <= kRankCap && rank_kernel;
   return with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
-    hipLaunchKernelGGL((k_prune<decltype(dt)::value, decltype(c)::value>), dim3(xcd_grid(g.N)), dim3(kBlock), lds,
-                       s, a, Cp, Rp);
+    constexpr int DT = decltype(dt)::value, CPL = decltype(c)::value;
+    constexpr bool kHasQB = DT != DANCE_U8 && CPL <= 4;
+    if (rank) {
+      if constexpr (kHasQB) {
+        if (qb.rows) {
+          hipLaunchKernelGGL((k_prune_rank<DT, CPL, true>), dim3(xcd_grid(g.N)), dim3(kBlock),
+                             (size_t)kWavesPerBlock * prune_rank_lds_words(Cq, Rp, true) * 4, s, a, Cq, Rp);
+          DHIP(hipGetLastError());
+          return 0;
+        }
+      }
+      // without code rows the bound is off: the kernel tests every pair exactly
+      a.qb = QBoundSet{nullptr, 0.0f, 0.0f};
+      hipLaunchKernelGGL((k_prune_rank<DT, CPL, false>), dim3(xcd_grid(g.N)), dim3(kBlock),
+                         (size_t)kWavesPerBlock * prune_rank_lds_words(Cq, Rp, false) * 4, s, a, Cq, Rp);
+      DHIP(hipGetLastError());
+      return 0;
+    }
+    hipLaunchKernelGGL((k_prune<DT, CPL>), dim3(xcd_grid(g.N)), dim3(kBlock),
+                       (size_t)kWavesPerBlock * prune_lds_words(Cp, Rp) * 4, s, a, Cp, Rp);
     DHIP(hipGetLastError());
     return 0;
   });
@@ -486,6 +516,7 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   DCHECK(build_schedule(rows, qb, rws, s, &order));
   const uint32_t q_iters = qbound_iters(), q_prune_iters = qbound_prune_iters();
   const uint32_t a_from = alpha_from_iter();
+  const uint32_t p_rank = prune_rank_iters();
   DCHECK(record(e_init, s));
 
   struct IterEv {
@@ -516,7 +547,7 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     DCHECK(record(iev[it].m1, s));
     const uint32_t md = (it + 1 == kIters) ? kFinalMinDegree : 0u;
     const QBoundSet qp_it = ((q_prune_iters >> it) & 1u) ? qb : QBoundSet{nullptr, 0.0f, 0.0f};
-    DCHECK(launch_prune(rows, g, md, alpha, order, ctr, qp_it, s));
+    DCHECK(launch_prune(rows, g, md, alpha, order, ctr, qp_it, ((p_rank >> it) & 1u) != 0u, s));
     DCHECK(record(iev[it].p1, s));
   }
   DHIP(hipStreamSynchronize(s));
@@ -541,10 +572,12 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   p.medoid_ms = elapsed_ms(e0, e_med);
   p.init_ms = elapsed_ms(e_med, e_init);
   for (uint32_t it = 0; it < kIters; ++it) {
-    p.search_ms += elapsed_ms(iev[it].s0, iev[it].s1);
+    p.search_iter_ms[it] = elapsed_ms(iev[it].s0, iev[it].s1);
+    p.prune_iter_ms[it] = elapsed_ms(iev[it].m1, iev[it].p1);
+    p.search_ms += p.search_iter_ms[it];
     p.reverse_ms += elapsed_ms(iev[it].s1, iev[it].r1);
     p.merge_ms += elapsed_ms(iev[it].r1, iev[it].m1);
-    p.prune_ms += elapsed_ms(iev[it].m1, iev[it].p1);
+    p.prune_ms += p.prune_iter_ms[it];
   }
   p.total_ms = elapsed_ms(e0, iev[kIters - 1].p1);
   p.search_dist = hc_ctr.search_dist;
@@ -1385,7 +1418,9 @@ int dance_stage_prune(const void* h_data, int dtype, uint32_t N, uint32_t dim, u
   DevBuf qbuf;
   QBoundSet qb{};
   DCHECK(build_qbound(cx.rows, qbuf, cx.s, &qb));
-  DCHECK(launch_prune(cx.rows, cx.st.g(), min_degree, alpha, nullptr, nullptr, qb, cx.s));
+  // the stage hook runs the kernel the last iteration would use
+  DCHECK(launch_prune(cx.rows, cx.st.g(), min_degree, alpha, nullptr, nullptr, qb,
+                      ((prune_rank_iters() >> (kIters - 1)) & 1u) != 0u, cx.s));
   return download_state(cx.st, cur, deg_cur, work, deg_work, wd, cx.s);
 }
 

@@ -905,6 +905,314 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
 }
 
 // ---------------------------------------------------------------------------
+// The same RobustPrune for rows of at most 128 candidates, organised around
+// one sort (k_prune_rank).
+//
+// A round selects the remaining candidate of smallest (distance, index), and
+// removal never changes a distance, so the candidates are ranked once by
+// (distance, index) and everything after works on 128-bit masks over ranks,
+// held in scalar registers: a round selects the lowest remaining rank; the
+// candidates it tests (d_sel <= d) are exactly the remaining ranks; the fill
+// takes the lowest ranks not yet output. With the quantized bound, its
+// decision for every pair (selected rank i, candidate rank j > i) is made
+// before the rounds: the exact integer code dots of all pairs come from int8
+// MFMA tiles (v_mfma_i32_32x32x32_i8, 32 x 32 pairs per tile, K = 4 x 32 code
+// bytes), and each pair is tested with the expression of q_pair_proves on the
+// same inputs as the per-round test of k_prune, so the proven pairs, the
+// exact distances left to compute, and the graph are those of k_prune. Only
+// the pairs the bound leaves open cost a gathered exact distance.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kRankCap = 128;  // candidates per row this kernel takes (C <= 128)
+
+// Per-wave LDS: arrays of Cq = C rounded up to 32 entries (sid, sd by index;
+// rid, rd by rank; the exact-test list; per-rank flags), the outputs, and
+// with the bound the per-rank headers s, r, a, root and 4 proof words.
+__host__ __device__ constexpr uint32_t prune_rank_lds_words(uint32_t Cq, uint32_t Rp, bool qb) {
+  return 6u * Cq + 2u * Rp + (qb ? 8u * Cq : 0u);
+}
+
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef int v16i_t __attribute__((ext_vector_type(16)));
+
+// 16 code bytes of rank row `row` for MFMA K-step `step`: code chunk
+// 1 + 2 step + lane/32 (chunk 0 is the header; chunks past 7 are zero).
+// Both operands of a Gram tile take their rows this way, so the tile sums
+// every code byte of a pair exactly once (layout checked on gfx950: lane l
+// supplies row l % 32, and D[i][j] sits in accumulator v of lane l with
+// j = l % 32, i = 8 (v / 4) + 4 (l / 32) + v % 4).
+__device__ __forceinline__ v4i_t code_frag(const QBoundSet& qb, const uint32_t* rid, uint32_t row, uint32_t nvalid,
+                                           uint32_t step, uint32_t lane) {
+  const uint32_t chunk = 1u + 2u * step + (lane >> 5);
+  v4i_t v = {0, 0, 0, 0};
+  if (row < nvalid && chunk < kQChunks) {
+    const uint4 c = qb.rows[(size_t)rid[row] * kQChunks + chunk];
+    v = v4i_t{(int)c.x, (int)c.y, (int)c.z, (int)c.w};
+  }
+  return v;
+}
+
+__device__ __forceinline__ uint32_t ffs128(uint64_t m0, uint64_t m1) {
+  return m0 ? (uint32_t)ffs64(m0) : (m1 ? 64u + (uint32_t)ffs64(m1) : 0xFFFFFFFFu);
+}
+
+// waves_per_eu(6): the bound's variant fits 6 waves per SIMD in registers
+// (its MFMA accumulators then live in VGPRs); LDS allows the same at C <= 96.
+template <int DT, int CPL, bool QB>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_prune_rank(PruneArgs a,
+                                                                                                 uint32_t Cq,
+                                                                                                 uint32_t Rp) {
+  extern __shared__ uint32_t smem[];
+  const uint32_t w = wave_index();
+  const uint32_t gw = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + w;
+  const GraphBufs& g = a.g;
+  if (gw >= g.N) return;
+  const uint32_t node = a.order ? a.order[gw] : gw;
+  const uint32_t N = g.N, R = g.R, C = g.C;
+  const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;
+  uint32_t* const base = smem + w * prune_rank_lds_words(Cq, Rp, QB);
+  uint32_t* sid = base;  // index -> id (INV: no candidate); in the rounds, ids of the exact-test list
+  float* sd = reinterpret_cast<float*>(base + Cq);    // index -> distance
+  uint32_t* rid = base + 2 * Cq;                      // rank -> id
+  float* rd = reinterpret_cast<float*>(base + 3 * Cq);  // rank -> distance
+  uint32_t* lst = base + 4 * Cq;                      // ranks needing an exact distance
+  uint32_t* rmf = base + 5 * Cq;                      // per rank: removed this round / repeated id
+  uint32_t* oid = base + 6 * Cq;
+  float* od = reinterpret_cast<float*>(oid + Rp);
+  float* hs = reinterpret_cast<float*>(oid + 2 * Rp);  // QB: per rank s, r, a, root
+  float* hr = hs + Cq;
+  float* ha = hr + Cq;
+  float* hroot = ha + Cq;
+  uint32_t* proof = reinterpret_cast<uint32_t*>(hroot + Cq);  // QB: [rank][4] candidate ranks proven kept
+  const bool lo_in = lane < Cq, hi_in = lane + 64u < Cq;      // this lane's two slots exist
+
+  const size_t wb = (size_t)node * C, cb = (size_t)node * R;
+  const uint32_t deg = min(g.deg_work[node], C);
+  // 1. candidates (a lane holds indices lane and lane + 64)
+  uint32_t myid[2];
+  int mykey[2];
+  float mydist[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t i = lane + 64u * (uint32_t)h;
+    uint32_t id = DANCE_INV;
+    float dist = FLT_MAX;
+    if (i < deg) {
+      id = g.work[wb + i];
+      dist = g.wd[wb + i];
+      if (!(valid_for(id, N, node) && dist < FLT_MAX)) id = DANCE_INV;
+    }
+    if (i < Cq) {
+      sid[i] = id;
+      sd[i] = dist;
+      rmf[i] = 0u;
+      lst[i] = 0u;
+    }
+    myid[h] = id;
+    mydist[h] = dist;
+    mykey[h] = fkey(dist);
+  }
+  wave_sync();
+  // 2. rank = number of candidates before it in (distance, index) order; an
+  // id met twice marks both copies
+  uint32_t myrank[2] = {0u, 0u};
+  bool mydup[2] = {false, false};
+  for (uint32_t k = 0; k < deg; ++k) {
+    const uint32_t idk = sid[k];
+    if (idk == DANCE_INV) continue;
+    const int kk = fkey(sd[k]);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t i = lane + 64u * (uint32_t)h;
+      myrank[h] += (kk < mykey[h] || (kk == mykey[h] && k < i)) ? 1u : 0u;
+      mydup[h] = mydup[h] || (idk == myid[h] && k != i);
+    }
+  }
+  const uint64_t v0 = wballot(myid[0] != DANCE_INV), v1 = wballot(myid[1] != DANCE_INV);
+  const uint32_t nvalid = popc64(v0) + popc64(v1);
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    if (myid[h] != DANCE_INV) {
+      rid[myrank[h]] = myid[h];
+      rd[myrank[h]] = mydist[h];
+      rmf[myrank[h]] = mydup[h] ? 2u : 0u;
+    }
+  wave_sync();
+  const uint64_t dup0 = wballot(lo_in && (rmf[lane] & 2u) != 0u);
+  const uint64_t dup1 = wballot(hi_in && (rmf[lane + 64] & 2u) != 0u);
+  const uint64_t all0 = nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull);
+  const uint64_t all1 = nvalid >= 128 ? ~0ull : (nvalid > 64 ? ((1ull << (nvalid - 64)) - 1ull) : 0ull);
+  if (lo_in) rmf[lane] = 0u;
+  if (hi_in) rmf[lane + 64] = 0u;
+  wave_sync();
+
+  // 3. the bound's decision for every pair (QB)
+  if constexpr (QB) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t r = lane + 64u * (uint32_t)h;
+      if (r < nvalid) {
+        const uint4 hd = a.qb.rows[(size_t)rid[r] * kQChunks];
+        hs[r] = __uint_as_float(hd.x);
+        hr[r] = __uint_as_float(hd.y);
+        ha[r] = __uint_as_float(hd.z);
+        hroot[r] = prune_bound_root(a.qb, rd[r], a.alpha);
+      }
+      if (r < Cq) {
+        proof[4 * r + 0] = 0u;
+        proof[4 * r + 1] = 0u;
+        proof[4 * r + 2] = 0u;
+        proof[4 * r + 3] = 0u;
+      }
+    }
+    wave_sync();
+    const uint32_t nt = (nvalid + 31u) >> 5;
+    for (uint32_t ti = 0; ti < nt; ++ti) {
+      v4i_t fa[4];
+#pragma unroll
+      for (uint32_t s = 0; s < 4; ++s) fa[s] = code_frag(a.qb, rid, ti * 32u + (lane & 31u), nvalid, s, lane);
+
+      for (uint32_t tj = ti; tj < nt; ++tj) {
+        v16i_t acc = {};
+#pragma unroll
+        for (uint32_t s = 0; s < 4; ++s) {
+          const v4i_t fb = tj == ti ? fa[s] : code_frag(a.qb, rid, tj * 32u + (lane & 31u), nvalid, s, lane);
+          acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[s], fb, acc, 0, 0, 0);
+        }
+        const uint32_t j = tj * 32u + (lane & 31u);
+        const bool jin = j < nvalid;
+        const float sy = jin ? hs[j] : 0.0f, ry = jin ? hr[j] : 0.0f, ay = jin ? ha[j] : 0.0f;
+        const float rootj = jin ? hroot[j] : 0.0f;
+#pragma unroll
+        for (uint32_t v = 0; v < 16; ++v) {
+          const uint32_t i = ti * 32u + 8u * (v >> 2) + 4u * (lane >> 5) + (v & 3u);
+          const bool on = jin && i < j;
+          const float si = on ? hs[i] : 0.0f, ri = on ? hr[i] : 0.0f, ai = on ? ha[i] : 0.0f;
+          const float sT = (rootj + ri) * (1.0f + kQSlack);
+          const bool pr = on && q_pair_proves(si, ai, sT, sy, ry, ay, acc[v]);
+          const uint64_t m = wballot(pr);
+          if (lane == 0) {
+            const uint32_t i0 = ti * 32u + 8u * (v >> 2) + (v & 3u);
+            proof[4 * i0 + tj] = (uint32_t)m;
+            proof[4 * (i0 + 4u) + tj] = (uint32_t)(m >> 32);
+          }
+        }
+      }
+    }
+    wave_sync();
+  }
+
+  // 4. selection rounds on rank masks
+  uint64_t rem0 = all0, rem1 = all1, io0 = 0ull, io1 = 0ull;
+  uint32_t oc = 0, npair = 0, nbchk = 0, nbskip = 0;
+  auto drop_same_id = [&](uint32_t r, uint32_t id) {  // every copy of id leaves and counts as output
+    const uint64_t s0 = wballot(lane < nvalid && rid[min(lane, Cq - 1u)] == id);
+    const uint64_t s1 = wballot(lane + 64u < nvalid && rid[min(lane + 64u, Cq - 1u)] == id);
+    rem0 &= ~s0;
+    rem1 &= ~s1;
+    io0 |= s0;
+    io1 |= s1;
+  };
+  while (oc < R) {
+    const uint32_t r = ffs128(rem0, rem1);
+    if (r == 0xFFFFFFFFu) break;
+    const uint32_t sel = uni_u(rid[r]);
+    const float seld = uni_f(rd[r]);
+    if (lane == 0) {
+      oid[oc] = sel;
+      od[oc] = seld;
+    }
+    oc++;
+    if (r < 64) {
+      rem0 &= ~(1ull << r);
+      io0 |= 1ull << r;
+    } else {
+      rem1 &= ~(1ull << (r - 64));
+      io1 |= 1ull << (r - 64);
+    }
+    if ((r < 64 ? (dup0 >> r) : (dup1 >> (r - 64))) & 1ull) drop_same_id(r, sel);
+    if (oc >= R) break;
+    uint64_t need0 = rem0, need1 = rem1;
+    if (need0 == 0 && need1 == 0) continue;
+    if constexpr (QB) {
+      const uint64_t p0 = (uint64_t)uni_u(proof[4 * r + 0]) | ((uint64_t)uni_u(proof[4 * r + 1]) << 32);
+      const uint64_t p1 = (uint64_t)uni_u(proof[4 * r + 2]) | ((uint64_t)uni_u(proof[4 * r + 3]) << 32);
+      nbchk += popc64(need0) + popc64(need1);
+      need0 &= ~p0;
+      need1 &= ~p1;
+      nbskip += popc64(rem0 & p0) + popc64(rem1 & p1);
+      if (need0 == 0 && need1 == 0) continue;
+    }
+    uint4 sv[CPL];  // the selected row, in flight while the list is built
+    load_row<CPL>(a.rs, sel, true, sub, sv);
+    const uint32_t n0 = popc64(need0), nn = n0 + popc64(need1);
+    // the list holds each rank and, in sid, its id
+    if ((need0 >> lane) & 1ull) lst[mbcnt64(need0)] = lane;
+    if ((need1 >> lane) & 1ull) lst[n0 + mbcnt64(need1)] = lane + 64u;
+    if ((need0 >> lane) & 1ull) sid[mbcnt64(need0)] = rid[lane];
+    if ((need1 >> lane) & 1ull) sid[n0 + mbcnt64(need1)] = rid[lane + 64u];
+    wave_sync();
+    for (uint32_t p = 0; p < nn; p += 16) {
+      const uint32_t k0 = p + grp, k1 = p + 8 + grp;
+      const bool a0 = k0 < nn, a1 = k1 < nn;
+      const uint32_t r0 = min(lst[min(k0, Cq - 1u)], Cq - 1u);
+      const uint32_t r1 = min(lst[min(k1, Cq - 1u)], Cq - 1u);
+      uint4 b0[CPL], b1[CPL];
+      load_row<CPL>(a.rs, sid[min(k0, Cq - 1u)], a0, sub, b0);
+      load_row<CPL>(a.rs, sid[min(k1, Cq - 1u)], a1, sub, b1);
+      const float d0 = octet_finish<DT, CPL>(a.rs, sub, sv, b0);
+      const float d1 = octet_finish<DT, CPL>(a.rs, sub, sv, b1);
+      if (sub == 0) {
+        if (a0 && a.alpha * d0 <= rd[r0]) rmf[r0] = 1u;
+        if (a1 && a.alpha * d1 <= rd[r1]) rmf[r1] = 1u;
+      }
+    }
+    npair += nn;
+    wave_sync();
+    const bool f0 = lo_in && rmf[lane] != 0u, f1 = hi_in && rmf[lane + 64] != 0u;
+    rem0 &= ~wballot(f0);
+    rem1 &= ~wballot(f1);
+    if (f0) rmf[lane] = 0u;
+    if (f1) rmf[lane + 64] = 0u;
+    wave_sync();
+  }
+  // 5. degree fill to min(min_degree, R): lowest ranks not yet output,
+  // occluded ones included (vnew2.cu:2076-2126)
+  const uint32_t md = min(a.min_degree, R);
+  while (oc < md) {
+    const uint32_t r = ffs128(all0 & ~io0, all1 & ~io1);
+    if (r == 0xFFFFFFFFu) break;
+    const uint32_t pick = uni_u(rid[r]);
+    if (lane == 0) {
+      oid[oc] = pick;
+      od[oc] = rd[r];
+    }
+    oc++;
+    if (r < 64)
+      io0 |= 1ull << r;
+    else
+      io1 |= 1ull << (r - 64);
+    if ((r < 64 ? (dup0 >> r) : (dup1 >> (r - 64))) & 1ull) drop_same_id(r, pick);
+  }
+  wave_sync();
+  for (uint32_t i = lane; i < C; i += 64) {
+    g.work[wb + i] = i < oc ? oid[i] : DANCE_INV;
+    g.wd[wb + i] = i < oc ? od[i] : FLT_MAX;
+  }
+  for (uint32_t i = lane; i < R; i += 64) g.cur[cb + i] = i < oc ? oid[i] : DANCE_INV;
+  if (lane == 0) {
+    g.deg_work[node] = oc;
+    g.deg_cur[node] = oc;
+  }
+  if (a.ctr && lane == 0) {
+    atomicAdd(&ctr_stripe(a.ctr)->prune_dist, (unsigned long long)npair);
+    if (QB) {
+      atomicAdd(&ctr_stripe(a.ctr)->prune_bound_checks, (unsigned long long)nbchk);
+      atomicAdd(&ctr_stripe(a.ctr)->prune_bound_skips, (unsigned long long)nbskip);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Reverse edges. k_rev_keys emits one (target, slot) item per forward slot j =
 // s*R + i in source order and snapshots that slot's stored distance; a stable
 // LSD radix sort by target then yields every segment in ascending source

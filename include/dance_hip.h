@@ -40,6 +40,8 @@ typedef struct DanceKernelProfile {
      * enough that the candidate survives (DANCE_QBOUND_PRUNE_ITERS selects
      * the iterations). */
     uint64_t prune_bound_checks, prune_bound_skips;
+    /* per iteration (launch order): search and prune launch times in ms */
+    double search_iter_ms[4], prune_iter_ms[4];
 } DanceKernelProfile;
 
 /* Full standard (vnew2) build with the vectors already resident in device

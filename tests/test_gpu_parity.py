@@ -143,6 +143,23 @@ def test_prune_shapes_bitexact(kind, R, C):
         assert_state_equal(g, s)
 
 
+@pytest.mark.parametrize("rank,qbound", [("0", "1"), ("1", "0"), ("1", "1"), ("0", "0")])
+@pytest.mark.parametrize("R,C", [(64, 80), (32, 128), (64, 64), (16, 100)])
+def test_prune_kernels_bitexact(monkeypatch, rank, qbound, R, C):
+    """Both prune kernels (k_prune; k_prune_rank for rows of at most 128
+    candidates, with and without the bound's MFMA pair decisions) against
+    the oracle, on rows with invalid ids, self loops, repeated ids and
+    FLT_MAX distances."""
+    monkeypatch.setenv("DANCE_PRUNE_RANK_ITERS", "0xF" if rank == "1" else "0x0")
+    monkeypatch.setenv("DANCE_QBOUND", qbound)
+    data = make_data("f32", 3000, 96, seed=R + C)
+    s0 = random_work_state(data, R, C, seed=C)
+    for alpha, md in ((1.0, 0), (1.2, 64), (1.2, 0)):
+        g = D.stage_prune(data, to_dance(s0), md, alpha)
+        s = O.prune(data, s0, md, alpha)
+        assert_state_equal(g, s)
+
+
 @pytest.mark.parametrize("kind", ["f32", "u8"])
 @pytest.mark.parametrize("heavy", [(0, 0), (8, 12)])
 def test_reverse_merge_bitexact(kind, heavy):
@@ -192,6 +209,18 @@ def test_end_to_end_graph_identical(kind, n, R, L, C, steps):
     data = make_data(kind, n, dim, seed=17)
     res = D.vamana_build(data, R, L, C, steps)
     og, od, om = O.vnew2_build(data, R, L, C, steps)
+    assert res.medoid == om
+    assert np.array_equal(res.degree, od)
+    assert np.array_equal(res.graph, og)
+
+
+@pytest.mark.parametrize("rank_iters", ["0x0", "0xF", "0x5"])
+def test_end_to_end_prune_kernel_choice(rank_iters, monkeypatch):
+    """The whole build with each prune kernel in every iteration, and mixed."""
+    monkeypatch.setenv("DANCE_PRUNE_RANK_ITERS", rank_iters)
+    data = make_data("f32", 5000, 96, seed=23)
+    res = D.vamana_build(data, 64, 100, 80, 64)
+    og, od, om = O.vnew2_build(data, 64, 100, 80, 64)
     assert res.medoid == om
     assert np.array_equal(res.degree, od)
     assert np.array_equal(res.graph, og)
