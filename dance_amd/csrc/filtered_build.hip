@@ -69,6 +69,17 @@ struct FParams {
 
 const char* kTag = "[gpu_vamana_filtered]";
 
+// The reference's build log (navigation-policy banner, one line per round,
+// the coverage-repair line, the degree percentiles of the published graph;
+// gpu_vamana_filtered.cu:5723-5730, :6294-6297, :6325, :94-160) goes to
+// stdout unless DANCE_FILTERED_LOG=0. The per-round counts and the
+// percentiles cost extra work (a copy of the round's input graph and two
+// small kernels), done only while the log is on.
+bool filtered_log() {
+  const char* e = std::getenv("DANCE_FILTERED_LOG");
+  return !(e && e[0] == '0');
+}
+
 // Parameter and label checks of gpu_vamana_filtered_build_impl (:6558-6568),
 // plus offsets consistency (the reference reads out of bounds otherwise).
 int validate(const FParams& p, const uint32_t* off, const uint32_t* lab, const uint32_t* starts) {
@@ -113,6 +124,7 @@ struct FState {
   DevBuf ga, gb, da, db, tids, td;
   DevBuf roff, cursor, rids, boff, bd, brem, bmask, lrows, lsort, lcount;
   DevBuf ctr, d32, d64;
+  DevBuf prev_g, prev_d, rcnt, compat, minpl;  // build log only
   size_t big_cap = 0;
   // the output graph: ga / da, or gb / db after the publish step
   uint32_t out_R = 0;
@@ -164,6 +176,54 @@ uint32_t grid_thr(uint64_t n) { return (uint32_t)((n + 255) / 256); }
 void peak_mem(double& peak) {
   size_t fr = 0, tot = 0;
   if (hipMemGetInfo(&fr, &tot) == hipSuccess) peak = std::max(peak, (double)(tot - fr) / (1024.0 * 1024.0 * 1024.0));
+}
+
+// canonical_print_round_diagnostics (gpu_vamana_filtered.cu:94-160) over the
+// published graph: the per-row figures come from k_degree_profile, the
+// percentiles (entry floor(q * (N - 1)) of the ascending values) from the host.
+int print_degree_profile(FState& st, const Labels& Ld, uint32_t N, hipStream_t s) {
+  const double t0 = now_sec();
+  const uint32_t R = st.out_R;
+  DCHECK(st.compat.alloc((size_t)N * 4));
+  DCHECK(st.minpl.alloc((size_t)N * 4));
+  hipLaunchKernelGGL(k_degree_profile, dim3(grid_thr(N)), dim3(256), 0, s,
+                     Graph{N, R, static_cast<const uint32_t*>(st.out_g), static_cast<const uint32_t*>(st.out_d)}, Ld,
+                     st.compat.as<uint32_t>(), st.minpl.as<uint32_t>());
+  DHIP(hipGetLastError());
+  std::vector<uint32_t> deg(N), compat(N), minpl(N);
+  DHIP(hipMemcpyAsync(deg.data(), st.out_d, (size_t)N * 4, hipMemcpyDeviceToHost, s));
+  DHIP(hipMemcpyAsync(compat.data(), st.compat.p, (size_t)N * 4, hipMemcpyDeviceToHost, s));
+  DHIP(hipMemcpyAsync(minpl.data(), st.minpl.p, (size_t)N * 4, hipMemcpyDeviceToHost, s));
+  DHIP(hipStreamSynchronize(s));
+  uint64_t deg_sum = 0, at_R = 0, compat_sum = 0, minpl_sum = 0;
+  for (uint32_t r = 0; r < N; ++r) {
+    const uint32_t d = std::min(deg[r], R);
+    deg_sum += d;
+    at_R += d == R;
+    compat_sum += compat[r];
+    minpl_sum += minpl[r];
+  }
+  auto pct = [N](std::vector<uint32_t>& v, double q) {
+    const size_t k = (size_t)(q * (double)(N - 1));
+    std::nth_element(v.begin(), v.begin() + k, v.end());
+    return v[k];
+  };
+  uint32_t pd[3], pc[3], pm[3];
+  const double qs[3] = {0.50, 0.95, 0.99};
+  for (int i = 0; i < 3; ++i) {
+    pd[i] = pct(deg, qs[i]);
+    pc[i] = pct(compat, qs[i]);
+    pm[i] = pct(minpl, qs[i]);
+  }
+  const double n = (double)N;
+  std::printf("[gpu_vamana_filtered_canonical_degree] avg=%.3f p50=%u p95=%u p99=%u degree_eq_R_frac=%.6f "
+              "compatible_avg=%.3f compatible_p50=%u compatible_p95=%u compatible_p99=%u "
+              "min_per_label_avg=%.3f min_per_label_p50=%u min_per_label_p95=%u min_per_label_p99=%u "
+              "diagnostic_seconds=%.6f\n",
+              deg_sum / n, pd[0], pd[1], pd[2], at_R / n, compat_sum / n, pc[0], pc[1], pc[2], minpl_sum / n, pm[0],
+              pm[1], pm[2], now_sec() - t0);
+  std::fflush(stdout);
+  return 0;
 }
 
 // Runs the build on resident rows; on success st.ga / st.da hold the graph.
@@ -266,9 +326,30 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   const size_t search_lds = (size_t)kWaves * kSearchLds * 4;
   const size_t csr_lds = (size_t)kWaves * kCsrLds * 4;
   uint64_t reverse_edges = 0;
+  const bool log = filtered_log();
+  if (log) {
+    // The knobs behind the fixed values are the reference's defaults
+    // (:5689-5700): no round-0 ordinary search variants, no posting or round-0
+    // anchors, the bridge reserve (used only by the true-ordinary round 0),
+    // no active frontier.
+    std::printf("[gpu_vamana_filtered_navigation_policy] per_label_pool=%u per_label_keep=%u "
+                "true_ordinary_round0=0 pure_ordinary_round0=0 ordinary_pool=%u ordinary_steps=32 "
+                "posting_anchor=0 additional_round0_anchor=0 bridge_work_reserve=8 active_frontier=0 "
+                "label_quota=1 exact_csr_reverse=1\n",
+                per_label_pool, per_label_keep, ordinary_pool);
+    if (p.rounds) {
+      DCHECK(st.prev_g.alloc(NR * 4));
+      DCHECK(st.prev_d.alloc((size_t)N * 4));
+      DCHECK(st.rcnt.alloc(2 * 8));
+    }
+  }
 
   for (uint32_t round = 0; round < p.rounds; ++round) {
     const Graph Ga{N, R, ga, da};
+    if (log) {
+      DHIP(hipMemcpyAsync(st.prev_g.p, ga, NR * 4, hipMemcpyDeviceToDevice, s));
+      DHIP(hipMemcpyAsync(st.prev_d.p, da, (size_t)N * 4, hipMemcpyDeviceToDevice, s));
+    }
     hipEvent_t r0 = E.mark(s);
     if (T > 0) {
       DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
@@ -338,7 +419,22 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
     rev_ms += ms_between(r2, r3);
     csr_ms += ms_between(r3, r4);
     peak_mem(gs.peak_gpu_mem_gb);
+    if (log) {
+      unsigned long long rc[2] = {0, 0};
+      DHIP(hipMemsetAsync(st.rcnt.p, 0, sizeof(rc), s));
+      hipLaunchKernelGGL(k_round_changes, dim3((N + 3) / 4), dim3(256), 0, s, N, R, st.prev_g.as<const uint32_t>(),
+                         st.prev_d.as<const uint32_t>(), static_cast<const uint32_t*>(ga),
+                         static_cast<const uint32_t*>(da), static_cast<const uint32_t*>(roff),
+                         st.rcnt.as<unsigned long long>());
+      DHIP(hipGetLastError());
+      DHIP(hipMemcpyAsync(rc, st.rcnt.p, sizeof(rc), hipMemcpyDeviceToHost, s));
+      DHIP(hipStreamSynchronize(s));
+      std::printf("[gpu_vamana_filtered_canonical_round] round=%u kind=full alpha=%.3f active=%u tasks=%u "
+                  "changed=%llu touched=%llu reverse_proposals=%u deficient=0 next_active=%u\n",
+                  round, p.alpha, N, T, rc[0], rc[1], tails[0], N);
+    }
   }
+  if (log) std::printf("[gpu_vamana_filtered_label_coverage_repair] disabled=1\n");
   if (p.rounds == 0) DHIP(hipStreamSynchronize(s));
 
   // publish step (gpu_vamana_filtered.cu:6328-6432)
@@ -443,6 +539,7 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   gs.final_prune_rows = N;
   gs.semantic_stage = kStageLabelSync;
   gs.semantic_complete = 1;
+  if (log) DCHECK(print_degree_profile(st, Ld, N, s));
   peak_mem(gs.peak_gpu_mem_gb);
 
   kp.rounds = p.rounds;

@@ -1305,5 +1305,64 @@ static __global__ void k_diagnostics(Graph G, Labels L, uint32_t* d32, unsigned 
   }
 }
 
+// Per-round counts of the round line (gpu_vamana_filtered.cu:6106-6297), one
+// wave per row: out[0] += rows whose new row differs from the round's input
+// row (degree differs, or a new entry is absent from the old row: the test of
+// canonical_exact_prune / canonical_exact_prune_csr, :4979-4990, :5218-5228);
+// out[1] += rows with at least one reverse source (the touched flag of
+// canonical_reverse_candidate_count, :5049).
+static __global__ void k_round_changes(uint32_t N, uint32_t R, const uint32_t* old_g, const uint32_t* old_d,
+                                       const uint32_t* new_g, const uint32_t* new_d, const uint32_t* roff,
+                                       unsigned long long* out) {
+  const uint32_t row = blockIdx.x * (blockDim.x / 64) + wave_index(), lane = lane_id();
+  if (row >= N) return;
+  const uint32_t od = min(old_d[row], R), nd = min(new_d[row], R);
+  bool changed = od != nd;
+  for (uint32_t b = 0; !changed && b < nd; b += 64) {
+    const uint32_t j = b + lane;
+    const uint32_t v = j < nd ? new_g[(size_t)row * R + j] : DANCE_INV;
+    bool found = j >= nd;
+    for (uint32_t k = 0; k < od; ++k) found |= old_g[(size_t)row * R + k] == v;
+    changed = wballot(!found) != 0ull;
+  }
+  if (lane == 0) {
+    if (changed) atomicAdd(out, 1ull);
+    if (roff[row + 1] > roff[row]) atomicAdd(out + 1, 1ull);
+  }
+}
+
+// Per-row figures of canonical_print_round_diagnostics (:94-160), one thread
+// per row over the first min(degree, R) entries: compat[row] = entries whose
+// id is < N and that carry one of the row's labels (any entry when the row
+// has the universal label); minpl[row] = the least, over the row's labels
+// other than the universal one, of the entries carrying that label (compat
+// when the row has no such label).
+static __global__ void k_degree_profile(Graph G, Labels L, uint32_t* compat, uint32_t* minpl) {
+  const uint32_t row = blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= G.N) return;
+  const uint32_t n = min(G.d[row], G.R);
+  const uint32_t* nb = G.g + (size_t)row * G.R;
+  const uint32_t b = L.off[row], e = L.off[row + 1];
+  uint32_t mn = G.R, c = 0;
+  bool specific = false;
+  for (uint32_t p = b; p < e; ++p) {
+    const uint32_t l = L.lab[p];
+    if (l == L.universal) continue;
+    specific = true;
+    uint32_t k = 0;
+    for (uint32_t i = 0; i < n; ++i) k += nb[i] < G.N && has_exact(L, nb[i], l);
+    mn = min(mn, k);
+  }
+  for (uint32_t i = 0; i < n; ++i) {
+    const uint32_t v = nb[i];
+    bool shares = false;
+    for (uint32_t p = b; !shares && p < e && v < G.N; ++p)
+      shares = L.lab[p] == L.universal || has_exact(L, v, L.lab[p]);
+    c += shares;
+  }
+  compat[row] = c;
+  minpl[row] = specific ? mn : c;
+}
+
 }  // namespace filt
 }  // namespace dance

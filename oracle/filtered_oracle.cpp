@@ -460,6 +460,12 @@ void oracle_filtered_random_graph(uint32_t N, uint32_t R, uint32_t initial_degre
   }
 }
 
+// Per round of the last oracle_filtered_build: changed, touched, reverse proposals.
+uint64_t g_round_log[9] = {};
+
+// The last build's per-round counts (9 entries, zero beyond its rounds).
+void oracle_filtered_round_log(uint64_t* out) { std::memcpy(out, g_round_log, sizeof(g_round_log)); }
+
 // Full canonical_v2 build. dtype: float input is searched as fp16, so pass
 // dtype 2 with rows already rounded to fp16; 1 = uint8. work_C = min(C, 128).
 // rounds: canonical rounds (3 in the reference; 0 = random backbone only).
@@ -479,6 +485,7 @@ int oracle_filtered_build(const void* data, int dtype, uint32_t N, uint32_t dim,
   if ((uint64_t)N * work_C < (uint64_t)2 * N * R) return 1;
   Ctx c = make_ctx(data, dtype, N, dim, R, offsets, labels, total_labels, label_starts, num_labels,
                    universal_label);
+  std::fill(std::begin(g_round_log), std::end(g_round_log), 0ull);
   const uint32_t per_label_pool = std::min(filtered_L, 32u), per_label_keep = std::min(per_label_pool, 8u);
   const uint32_t ordinary_keep = std::min(R, L), ordinary_pool = std::min(64u, filtered_L);
   std::vector<uint32_t> ga((size_t)N * R), gb((size_t)N * R), da(N), db(N);
@@ -532,6 +539,25 @@ int oracle_filtered_build(const void* data, int dtype, uint32_t N, uint32_t dim,
       dnew[row] = filtered_prune(c, row, ids.data(), ds.data(), (uint32_t)ids.size(), alpha, &gnew[(size_t)row * R],
                                  R);
     }
+    // The round line's counts (gpu_vamana_filtered.cu:6106-6297): rows whose
+    // row set or degree changed against the round's input, rows with a
+    // reverse source, reverse proposals.
+    uint64_t changed = 0, touched = 0, proposals = 0;
+    for (uint32_t row = 0; row < N; ++row) {
+      touched += !rev[row].empty();
+      proposals += rev[row].size();
+      const uint32_t od = std::min(da[row], R), nd = std::min(dnew[row], R);
+      bool ch = od != nd;
+      for (uint32_t i = 0; !ch && i < nd; ++i) {
+        bool found = false;
+        for (uint32_t k = 0; !found && k < od; ++k) found = ga[(size_t)row * R + k] == gnew[(size_t)row * R + i];
+        ch = !found;
+      }
+      changed += ch;
+    }
+    g_round_log[3 * round] = changed;
+    g_round_log[3 * round + 1] = touched;
+    g_round_log[3 * round + 2] = proposals;
     ga.swap(gnew);
     da.swap(dnew);
   }

@@ -124,6 +124,8 @@ def lib() -> C.CDLL:
         L.oracle_filtered_build.argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, u32, f32, _u32p, _u32p, u32,
                                             _u32p, u32, u32, u32, u32, u32, _u32p, _u32p, C.POINTER(u64)]
         L.oracle_filtered_build.restype = i32
+        L.oracle_filtered_round_log.argtypes = [C.POINTER(C.c_uint64)]
+        L.oracle_filtered_round_log.restype = None
         L.oracle_filtered_prune.argtypes = [vp, i32, u32, u32, u32, f32, _u32p, _u32p, u32, _u32p, _f32p, u32,
                                             _u32p]
         L.oracle_filtered_prune.restype = u32
@@ -361,6 +363,14 @@ def filtered_build(data: np.ndarray, offsets: np.ndarray, labels: np.ndarray, st
     if 0 < publish_R < R:
         g = np.ascontiguousarray(g.ravel()[:N * publish_R].reshape(N, publish_R))
     return rc, g, d, diag
+
+
+def filtered_round_log() -> np.ndarray:
+    """Per round of the last filtered_build (rows x [changed, touched,
+    reverse proposals]; 3 rows, zero beyond its rounds)."""
+    out = np.zeros(9, np.uint64)
+    lib().oracle_filtered_round_log(out.ctypes.data_as(C.POINTER(C.c_uint64)))
+    return out.reshape(3, 3)
 
 
 def filtered_prune(data: np.ndarray, offsets: np.ndarray, labels: np.ndarray, row: int, ids: np.ndarray,

@@ -196,6 +196,32 @@ def test_build_invariants_and_determinism():
     assert np.array_equal(g, g2) and np.array_equal(d, d2)
 
 
+def test_round_log_changed_rows():
+    """The per-round changed count equals the number of rows whose neighbour
+    set differs between the graphs after r and r + 1 rounds (builds of 0..3
+    rounds are prefixes of one another); touched rows are at most the reverse
+    proposals, which are at most the edges of a forward graph."""
+    rng = np.random.default_rng(8)
+    N, R = 1200, 24
+    x = rng.integers(0, 256, (N, 32), dtype=np.uint8)
+    ls = F.synth_labels(N, 20, 1, 3, 1.0, seed=9)
+    st, gs = F.label_starts(x, ls), F.global_start(x)
+    graphs = []
+    for rounds in range(4):
+        rc, g, d, _ = O.filtered_build(x, ls.offsets, ls.labels, st, 20, R, 48, 48, 750, 24, 1.2, INVALID, gs,
+                                       rounds=rounds)
+        assert rc == 0
+        graphs.append([set(g[r, :d[r]].tolist()) for r in range(N)])
+    log = O.filtered_round_log()
+    for r in range(3):
+        changed = sum(1 for v in range(N) if graphs[r][v] != graphs[r + 1][v])
+        assert log[r, 0] == changed
+        assert 0 < log[r, 1] <= log[r, 2] <= N * R
+    O.filtered_build(x, ls.offsets, ls.labels, st, 20, R, 48, 48, 750, 24, 1.2, INVALID, gs, rounds=1)
+    log1 = O.filtered_round_log()
+    assert np.array_equal(log1[0], log[0]) and not log1[1:].any()
+
+
 def test_build_parameter_errors():
     x = np.zeros((10, 4), np.uint8)
     ls = F.canonical_labels([[0]] * 10, 1)

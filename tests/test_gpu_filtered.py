@@ -171,6 +171,73 @@ def test_filtered_tiny(n):
     assert_same(x, ls, starts, gs, 16, 32, 32, 64, 16)
 
 
+def log_fields(line):
+    return dict(tok.split("=", 1) for tok in line.split()[1:])
+
+
+def degree_profile(g, d, ls, universal):
+    """canonical_print_round_diagnostics (gpu_vamana_filtered.cu:94-160)
+    restated over the returned graph: entry floor(q * (N - 1)) of the sorted
+    degrees, label-compatible degrees and per-label minimum degrees."""
+    N, R = g.shape
+    sets = [set(ls.row(i).tolist()) for i in range(N)]
+    deg = np.minimum(d, R)
+    compat, minpl = np.zeros(N, np.int64), np.zeros(N, np.int64)
+    for r in range(N):
+        nb = [int(v) for v in g[r, :deg[r]] if v < N]
+        labs = ls.row(r).tolist()
+        compat[r] = sum(1 for v in nb if any(lab == universal or lab in sets[v] for lab in labs))
+        spec = [lab for lab in labs if lab != universal]
+        minpl[r] = min(sum(1 for v in nb if lab in sets[v]) for lab in spec) if spec else compat[r]
+
+    def pct(v, q):
+        return int(np.sort(v)[int(q * (N - 1))])
+    out = {"avg": f"{deg.sum() / N:.3f}", "degree_eq_R_frac": f"{(deg == R).sum() / N:.6f}",
+           "compatible_avg": f"{compat.sum() / N:.3f}", "min_per_label_avg": f"{minpl.sum() / N:.3f}"}
+    for q, tag in ((0.50, "p50"), (0.95, "p95"), (0.99, "p99")):
+        out[tag] = str(pct(d, q))
+        out["compatible_" + tag] = str(pct(compat, q))
+        out["min_per_label_" + tag] = str(pct(minpl, q))
+    return out
+
+
+@pytest.mark.parametrize("universal,PR", [(INVALID, 0), (0, 0), (INVALID, 24)])
+def test_filtered_build_log(capfd, monkeypatch, universal, PR):
+    """The reference-format build log (gpu_vamana_filtered.cu:5723-5730,
+    :6294-6297, :6325, :94-160): the policy banner, one line per round whose
+    changed / touched / reverse-proposal counts equal the oracle's, the
+    coverage-repair line, and the degree percentiles of the published graph."""
+    monkeypatch.setenv("DANCE_FILTERED_LOG", "1")
+    if PR:
+        monkeypatch.setenv("DISKANN_GPU_FILTERED_PUBLISH_DEGREE", str(PR))
+    x, ls = make_case("u8", 2500, 64, 30, 4, seed=13)
+    starts, gs = F.label_starts(x, ls), F.global_start(x)
+    capfd.readouterr()
+    g, d, _ = assert_same(x, ls, starts, gs, 32, 64, 48, 750, 32, universal=universal, rounds=3, publish_R=PR)
+    want = O.filtered_round_log()
+    lines = capfd.readouterr().out.splitlines()
+    pol = [log_fields(s) for s in lines if s.startswith("[gpu_vamana_filtered_navigation_policy]")]
+    assert len(pol) == 1
+    assert pol[0] == {"per_label_pool": "32", "per_label_keep": "8", "true_ordinary_round0": "0",
+                      "pure_ordinary_round0": "0", "ordinary_pool": "48", "ordinary_steps": "32",
+                      "posting_anchor": "0", "additional_round0_anchor": "0", "bridge_work_reserve": "8",
+                      "active_frontier": "0", "label_quota": "1", "exact_csr_reverse": "1"}
+    rounds = [log_fields(s) for s in lines if s.startswith("[gpu_vamana_filtered_canonical_round]")]
+    assert len(rounds) == 3
+    N, T = x.shape[0], ls.labels.size
+    for r, f in enumerate(rounds):
+        assert f == {"round": str(r), "kind": "full", "alpha": "1.200", "active": str(N), "tasks": str(T),
+                     "changed": str(want[r, 0]), "touched": str(want[r, 1]),
+                     "reverse_proposals": str(want[r, 2]), "deficient": "0", "next_active": str(N)}
+        assert 0 < want[r, 1] <= N and want[r, 2] >= want[r, 1]
+    assert "[gpu_vamana_filtered_label_coverage_repair] disabled=1" in lines
+    deg = [log_fields(s) for s in lines if s.startswith("[gpu_vamana_filtered_canonical_degree]")]
+    assert len(deg) == 1
+    secs = float(deg[0].pop("diagnostic_seconds"))
+    assert secs >= 0
+    assert deg[0] == degree_profile(g, d, ls, universal)
+
+
 def test_filtered_abi_float_entry_equals_oracle():
     """gpu_vamana_filtered_build_float (the reference entry: float input is
     searched as round-to-nearest fp16 rows, filtered.cu:6497-6503) against
