@@ -556,3 +556,31 @@ def test_search_expansion_order_matches_best_first(N, R, L, steps):
         k = int(s.deg_work[v])
         assert k == len(row), v
         assert s.work[v, :k].tolist() == row, v
+
+
+@pytest.mark.parametrize("alpha_from", [0, 1, 2, 3])
+def test_alpha_schedule_composes_the_stages(alpha_from):
+    """The reference's schedule knob (vnew2.cu:201-213: alpha from iteration
+    VAMANA_ALPHA_FINAL_FROM_ITER on, 1 before; USE_ALPHA_FROM_FIRST_ITER is
+    from = 0) composed from the separately pinned stages: medoid, init, then
+    per iteration search (steps capped at 64 in the first two), reverse merge
+    and prune (fill to 64 in the last). From = 3 is the default schedule, and
+    with alpha 1 the knob changes nothing."""
+    rng = np.random.default_rng(30 + alpha_from)
+    x = rng.standard_normal((300, 16)).astype(np.float32)
+    R, L, C_, steps, iters, alpha = 12, 32, 24, 80, 4, 1.2
+    start, _, _ = O.medoid(x)
+    s = O.init_graph(x, R, C_)
+    for it in range(iters):
+        a = alpha if it >= alpha_from else 1.0
+        s = O.search(x, s, L, min(steps, L, 64) if it < 2 else min(steps, L), a, start)
+        s, _, _ = O.reverse_merge(x, s)
+        s = O.prune(x, s, 64 if it == iters - 1 else 0, a)
+    g, d, m = O.vnew2_build(x, R, L, C_, steps, iters, alpha, alpha_from=alpha_from)
+    assert m == start and np.array_equal(d, s.deg_cur) and np.array_equal(g, s.cur)
+    if alpha_from == iters - 1:
+        g0, d0, _ = O.vnew2_build(x, R, L, C_, steps, iters, alpha)
+        assert np.array_equal(g, g0) and np.array_equal(d, d0)
+    g1, d1, _ = O.vnew2_build(x, R, L, C_, steps, iters, 1.0, alpha_from=alpha_from)
+    g2, d2, _ = O.vnew2_build(x, R, L, C_, steps, iters, 1.0)
+    assert np.array_equal(g1, g2) and np.array_equal(d1, d2)
