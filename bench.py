@@ -318,7 +318,20 @@ def graph_check(torch, graph_t, deg_t, n: int, R: int) -> dict:
     out = {"invalid": invalid, "self_loops": selfl, "duplicates": dup, "bad_padding": pad,
            "min_degree": int(d.min()), "max_degree": int(d.max()), "mean_degree": round(float(d.float().mean()), 3)}
     out["ok"] = invalid == selfl == dup == pad == 0 and out["max_degree"] <= R and out["min_degree"] >= 1
+    out["digest"] = graph_digest(torch, graph_t, deg_t)
     return out
+
+
+def graph_digest(torch, graph_t, deg_t) -> str:
+    """A 64-bit position-weighted checksum of the graph and degree arrays
+    (int64 arithmetic wraps), computed on the device: equal across builds iff
+    (with overwhelming likelihood) every id, slot and degree is equal."""
+    def mix(x):
+        x = x.reshape(-1).long() & 0xFFFFFFFF
+        pos = torch.arange(x.numel(), device=x.device, dtype=torch.int64)
+        w = pos * -7046029254386353131 + 1442695040888963407  # odd multiplier, wraps
+        return int(((x + 1) * (w | 1)).sum())
+    return f"{(mix(graph_t) * 31 + mix(deg_t)) & 0xFFFFFFFFFFFFFFFF:016x}"
 
 
 def recall_curve(D, data, graph, degree, start, queries, gt) -> dict:
@@ -560,6 +573,14 @@ def main() -> int:
                                                      "prune_ms", "total_ms")},
         "launch_ms": {"search": [round(v, 2) for v in kp["search_iter_ms"]],
                       "prune": [round(v, 2) for v in kp["prune_iter_ms"]]},
+        "launch_counters": {k: list(kp[k]) for k in (
+            "search_dist_iter", "insert_dist_iter", "expansions_iter", "bound_checks_iter", "bound_skips_iter",
+            "merge_dist_iter", "prune_dist_iter", "prune_bound_checks_iter", "prune_bound_skips_iter")},
+        "launch_algorithmic_GB": {"search": [round(v / 1e9, 2) for v in kp["search_bytes_iter"]],
+                                  "prune": [round(v / 1e9, 2) for v in kp["prune_bytes_iter"]]},
+        "prune_rounds": {"rounds": kp["prune_rounds"], "exact_rounds": kp["prune_exact_rounds"]},
+        "prune_cycles": ({k: kp[k] for k in ("cyc_prune_rank", "cyc_prune_gram", "cyc_prune_rounds",
+                                             "cyc_prune_fill")} if kp["cyc_prune_rounds"] else None),
         "counters": {k: kp[k] for k in ("search_dist", "insert_dist", "expansions", "vis_skips", "merge_dist",
                                         "prune_dist", "reverse_edges", "bound_checks", "bound_skips",
                                         "prune_bound_checks", "prune_bound_skips")},

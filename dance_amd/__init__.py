@@ -65,6 +65,15 @@ class DanceKernelProfile(C.Structure):
         ("bound_checks", C.c_uint64), ("bound_skips", C.c_uint64),
         ("prune_bound_checks", C.c_uint64), ("prune_bound_skips", C.c_uint64),
         ("search_iter_ms", C.c_double * 4), ("prune_iter_ms", C.c_double * 4),
+        ("search_dist_iter", C.c_uint64 * 4), ("insert_dist_iter", C.c_uint64 * 4),
+        ("expansions_iter", C.c_uint64 * 4), ("bound_checks_iter", C.c_uint64 * 4),
+        ("bound_skips_iter", C.c_uint64 * 4), ("merge_dist_iter", C.c_uint64 * 4),
+        ("prune_dist_iter", C.c_uint64 * 4), ("prune_bound_checks_iter", C.c_uint64 * 4),
+        ("prune_bound_skips_iter", C.c_uint64 * 4),
+        ("search_bytes_iter", C.c_double * 4), ("prune_bytes_iter", C.c_double * 4),
+        ("prune_rounds", C.c_uint64), ("prune_exact_rounds", C.c_uint64),
+        ("cyc_prune_rank", C.c_uint64), ("cyc_prune_gram", C.c_uint64), ("cyc_prune_rounds", C.c_uint64),
+        ("cyc_prune_fill", C.c_uint64),
     ]
 
 

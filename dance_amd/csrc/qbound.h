@@ -178,6 +178,17 @@ __device__ __forceinline__ bool q_pair_proves(float s, float a, float sT, float 
   return q >= w * w * (1.0f + kQSlack);
 }
 
+// q_pair_proves with the querying row's scale passed as m2s = -2 s. Scaling
+// by -2 commutes with rounding for the scales k_quantize keeps ([2^-60,
+// 2^50], or 0), so fl(m2s * sy) = -2 fl(s * sy) and the decision is that of
+// q_pair_proves on the same inputs.
+__device__ __forceinline__ bool q_pair_proves_m2(float m2s, float a, float sT, float sy, float ry, float ay, int c) {
+  const float sa = a + ay;
+  const float q = __builtin_fmaf(m2s * sy, (float)c, sa) - kQSlack * sa - 1e-30f;
+  const float w = (sT + ry) * (1.0f + kQSlack);
+  return q >= w * w * (1.0f + kQSlack);
+}
+
 // Octet test for a candidate: every lane of the octet holds one chunk `b` of
 // its code row (q_load); the lane with sub == 0 (which holds the header)
 // returns whether the bound proves dist >= T. `code` is chunk `sub` of the

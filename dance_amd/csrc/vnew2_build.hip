@@ -154,7 +154,7 @@ static int launch_init(const Rows& rows, GraphBufs g, hipStream_t s) {
 constexpr uint32_t kQBoundIters = 0x1u;  // first iteration: random graph, HBM-bound
 // The prune uses it in the iterations of DANCE_QBOUND_PRUNE_ITERS (default
 // kQBoundPruneIters).
-constexpr uint32_t kQBoundPruneIters = 0x9u;  // first and last (alpha) iterations
+constexpr uint32_t kQBoundPruneIters = 0xDu;  // iterations 0, 2 and 3 (measured at c3: 1 is faster without)
 static bool qbound_enabled() {
   const char* e = std::getenv("DANCE_QBOUND");
   return !(e && e[0] == '0');
@@ -248,7 +248,7 @@ static int launch_prune(const Rows& rows, GraphBufs g, uint32_t min_degree, floa
       if constexpr (kHasQB) {
         if (qb.rows) {
           hipLaunchKernelGGL((k_prune_rank<DT, CPL, true>), dim3(xcd_grid(g.N)), dim3(kBlock),
-                             (size_t)kWavesPerBlock * prune_rank_lds_words(Cq, Rp, true) * 4, s, a, Cq, Rp);
+                             (size_t)kWavesPerBlock * prune_rank_lds_words(Cq, true) * 4, s, a, Cq);
           DHIP(hipGetLastError());
           return 0;
         }
@@ -256,7 +256,7 @@ static int launch_prune(const Rows& rows, GraphBufs g, uint32_t min_degree, floa
       // without code rows the bound is off: the kernel tests every pair exactly
       a.qb = QBoundSet{nullptr, 0.0f, 0.0f};
       hipLaunchKernelGGL((k_prune_rank<DT, CPL, false>), dim3(xcd_grid(g.N)), dim3(kBlock),
-                         (size_t)kWavesPerBlock * prune_rank_lds_words(Cq, Rp, false) * 4, s, a, Cq, Rp);
+                         (size_t)kWavesPerBlock * prune_rank_lds_words(Cq, false) * 4, s, a, Cq);
       DHIP(hipGetLastError());
       return 0;
     }
@@ -519,6 +519,8 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   const uint32_t p_rank = prune_rank_iters();
   DCHECK(record(e_init, s));
 
+  DevBuf snaps;  // timed builds: kIters cumulative counter snapshots
+  if (timed) DCHECK(snaps.alloc(sizeof(VCounters) * kIters));
   struct IterEv {
     hipEvent_t s0, s1, r1, m1, p1;
   };
@@ -549,6 +551,11 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     const QBoundSet qp_it = ((q_prune_iters >> it) & 1u) ? qb : QBoundSet{nullptr, 0.0f, 0.0f};
     DCHECK(launch_prune(rows, g, md, alpha, order, ctr, qp_it, ((p_rank >> it) & 1u) != 0u, s));
     DCHECK(record(iev[it].p1, s));
+    if (timed) {  // cumulative counters after this iteration
+      hipLaunchKernelGGL(k_ctr_sum, dim3(1), dim3(64), 0, s, static_cast<const VCounters*>(ctr),
+                         snaps.as<VCounters>() + it);
+      DHIP(hipGetLastError());
+    }
   }
   DHIP(hipStreamSynchronize(s));
   DHIP(hipGetLastError());
@@ -565,6 +572,11 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
       const auto* src = reinterpret_cast<const unsigned long long*>(&st);
       for (size_t f = 0; f < nf; ++f) dst[f] += src[f];
     }
+  }
+  VCounters hsnap[kIters] = {};
+  if (timed) {
+    DHIP(hipMemcpyAsync(hsnap, snaps.p, sizeof(hsnap), hipMemcpyDeviceToHost, s));
+    DHIP(hipStreamSynchronize(s));
   }
   DanceKernelProfile p{};
   p.iterations = kIters;
@@ -598,7 +610,38 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   p.bound_skips = hc_ctr.bound_skips;
   p.prune_bound_checks = hc_ctr.prune_bound_checks;
   p.prune_bound_skips = hc_ctr.prune_bound_skips;
+  p.prune_rounds = hc_ctr.prune_rounds;
+  p.prune_exact_rounds = hc_ctr.prune_exact_rounds;
+  p.cyc_prune_rank = hc_ctr.cyc_prune_rank;
+  p.cyc_prune_gram = hc_ctr.cyc_prune_gram;
+  p.cyc_prune_rounds = hc_ctr.cyc_prune_rounds;
+  p.cyc_prune_fill = hc_ctr.cyc_prune_fill;
   const double V = rows.vbytes();
+  for (uint32_t it = 0; timed && it < kIters; ++it) {
+    const VCounters& c = hsnap[it];
+    const VCounters z{};
+    const VCounters& b = it ? hsnap[it - 1] : z;
+    p.search_dist_iter[it] = c.search_dist - b.search_dist;
+    p.insert_dist_iter[it] = c.insert_dist - b.insert_dist;
+    p.expansions_iter[it] = c.expansions - b.expansions;
+    p.bound_checks_iter[it] = c.bound_checks - b.bound_checks;
+    p.bound_skips_iter[it] = c.bound_skips - b.bound_skips;
+    p.merge_dist_iter[it] = c.merge_dist - b.merge_dist;
+    p.prune_dist_iter[it] = c.prune_dist - b.prune_dist;
+    p.prune_bound_checks_iter[it] = c.prune_bound_checks - b.prune_bound_checks;
+    p.prune_bound_skips_iter[it] = c.prune_bound_skips - b.prune_bound_skips;
+    p.search_bytes_iter[it] = (double)(p.search_dist_iter[it] + p.insert_dist_iter[it]) * V +
+                              (double)p.expansions_iter[it] * (4.0 * R + 4.0) + (double)N * (V + 4.0 * R + 4.0 + 16.0 * C) +
+                              (double)p.bound_checks_iter[it] * (kQChunks * 16.0);
+    // the rank kernel with the bound reads every candidate's code row once;
+    // k_prune reads the code rows of the pairs it tests
+    const bool q_it = qb.rows && ((q_prune_iters >> it) & 1u);
+    const bool rank_it = ((p_rank >> it) & 1u) && C <= kRankCap;
+    const double qbytes = !q_it ? 0.0
+                          : rank_it ? (double)N * C * (kQChunks * 16.0)
+                                    : (double)p.prune_bound_checks_iter[it] * (kQChunks * 16.0);
+    p.prune_bytes_iter[it] = (double)p.prune_dist_iter[it] * V + (double)N * (24.0 * C) + qbytes;
+  }
   p.search_bytes = (double)(p.search_dist + p.insert_dist) * V + (double)p.expansions * (4.0 * R + 4.0) +
                    (double)kIters * N * (V + 4.0 * R + 4.0 + 16.0 * C) + (double)p.bound_checks * (kQChunks * 16.0);
   p.merge_bytes = (double)p.merge_dist * 4.0 + (double)p.reverse_edges * 4.0 +

@@ -14,6 +14,8 @@
 // and distances are a deterministic function of the id).
 #pragma once
 
+#include <type_traits>
+
 #include "qbound.h"
 #include "wave.h"
 
@@ -59,7 +61,11 @@ struct VCounters {
   unsigned long long bound_checks;  // candidates tested with the quantized lower bound
   unsigned long long bound_skips;   // candidates whose exact distance the bound made unnecessary
   unsigned long long prune_bound_checks, prune_bound_skips;  // the same for prune pairs
+  unsigned long long prune_rounds, prune_exact_rounds;       // selection rounds; those with exact pairs
+  // DANCE_SEARCH_TIMING: k_prune_rank phase cycles, summed over waves.
+  unsigned long long cyc_prune_rank, cyc_prune_gram, cyc_prune_rounds, cyc_prune_fill;
 };
+
 
 // Counters are striped over kCtrStripes copies (by workgroup) so that the
 // per-wave atomics of millions of waves do not serialise on one address; the
@@ -67,6 +73,16 @@ struct VCounters {
 constexpr uint32_t kCtrStripes = 64;
 __device__ __forceinline__ VCounters* ctr_stripe(VCounters* base) {
   return base + (blockIdx.x & (kCtrStripes - 1u));
+}
+
+// Sums the counter stripes into one VCounters (a snapshot after a launch).
+static __global__ void k_ctr_sum(const VCounters* __restrict__ stripes, VCounters* __restrict__ out) {
+  constexpr uint32_t nf = sizeof(VCounters) / sizeof(unsigned long long);
+  const uint32_t f = threadIdx.x;
+  if (f >= nf) return;
+  unsigned long long s = 0;
+  for (uint32_t k = 0; k < kCtrStripes; ++k) s += reinterpret_cast<const unsigned long long*>(stripes + k)[f];
+  reinterpret_cast<unsigned long long*>(out)[f] = s;
 }
 
 
@@ -762,7 +778,7 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
     if (qon) sroot[i] = prune_bound_root(a.qb, dist, a.alpha);
   }
   wave_sync();
-  uint32_t oc = 0, npair = 0, nbchk = 0, nbskip = 0;
+  uint32_t oc = 0, npair = 0, nbchk = 0, nbskip = 0, nround = 0, nexact = 0;
   for (uint32_t round = 0; round < R; ++round) {
     // smallest distance, lowest index on ties: each lane keeps its first
     // entry of its smallest key (entries ascend per lane)
@@ -784,6 +800,7 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
       od[oc] = seld;
     }
     oc++;
+    nround++;
     if (oc >= R) break;
     uint32_t nq = 0;
     for (uint32_t b = 0; b < Cp; b += 64) {
@@ -841,6 +858,7 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
     }
     uint4 sv[CPL];
     load_row<CPL>(a.rs, sel, true, sub, sv);
+    nexact++;
     for (uint32_t p = 0; p < nq; p += 16) {
       const uint32_t k0 = p + grp, k1 = p + 8 + grp;
       const bool a0 = k0 < nq, a1 = k1 < nq;
@@ -897,6 +915,8 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
   }
   if (a.ctr && lane == 0) {
     atomicAdd(&ctr_stripe(a.ctr)->prune_dist, (unsigned long long)npair);
+    atomicAdd(&ctr_stripe(a.ctr)->prune_rounds, (unsigned long long)nround);
+    atomicAdd(&ctr_stripe(a.ctr)->prune_exact_rounds, (unsigned long long)nexact);
     if (qon) {
       atomicAdd(&ctr_stripe(a.ctr)->prune_bound_checks, (unsigned long long)nbchk);
       atomicAdd(&ctr_stripe(a.ctr)->prune_bound_skips, (unsigned long long)nbskip);
@@ -918,17 +938,26 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
 // before the rounds: the exact integer code dots of all pairs come from int8
 // MFMA tiles (v_mfma_i32_32x32x32_i8, 32 x 32 pairs per tile, K = 4 x 32 code
 // bytes), and each pair is tested with the expression of q_pair_proves on the
-// same inputs as the per-round test of k_prune, so the proven pairs, the
-// exact distances left to compute, and the graph are those of k_prune. Only
-// the pairs the bound leaves open cost a gathered exact distance.
+// same inputs as the per-round test of k_prune. The pairs the bound leaves
+// open are then listed and their exact distances computed in one batch (all
+// loads of a pass in flight together), and the occlusion decision of every
+// pair is a bit in LDS, so the rounds run on masks alone: a round removes
+// occ[selected] from the remaining ranks. The decisions are those the rounds
+// would make one pair at a time (same distance, operands in the same order,
+// same test), so the graph is that of k_prune. More pairs are computed than
+// the rounds would test (some open pairs involve ranks already removed), in
+// exchange for no gather inside a round. Rows whose open pairs exceed the
+// list (4 Cq) fall back to exact tests inside the rounds; without the bound
+// (QB false) every round tests its remaining ranks exactly.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kRankCap = 128;  // candidates per row this kernel takes (C <= 128)
 
-// Per-wave LDS: arrays of Cq = C rounded up to 32 entries (sid, sd by index;
-// rid, rd by rank; the exact-test list; per-rank flags), the outputs, and
-// with the bound the per-rank headers s, r, a, root and 4 proof words.
-__host__ __device__ constexpr uint32_t prune_rank_lds_words(uint32_t Cq, uint32_t Rp, bool qb) {
-  return 6u * Cq + 2u * Rp + (qb ? 8u * Cq : 0u);
+// Per-wave LDS: arrays of Cq = C rounded up to 32 entries (ids of the
+// exact-test list; rid, rd by rank; the exact-test list of ranks; per-rank
+// flags), and with the bound the per-rank header {-2 s, r, a, root} (later
+// the open-pair list) and 4 mask words per rank.
+__host__ __device__ constexpr uint32_t prune_rank_lds_words(uint32_t Cq, bool qb) {
+  return 5u * Cq + (qb ? 8u * Cq : 0u);
 }
 
 typedef int v4i_t __attribute__((ext_vector_type(4)));
@@ -951,16 +980,37 @@ __device__ __forceinline__ v4i_t code_frag(const QBoundSet& qb, const uint32_t* 
   return v;
 }
 
+// v_writelane_b32: lane L of `words` takes the wave-uniform value v; the
+// other lanes keep theirs.
+template <uint32_t L>
+__device__ __forceinline__ uint32_t write_lane(uint32_t words, uint32_t v) {
+  static_assert(L < 64u, "lane index");
+  asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(words) : "s"(v), "n"(L));
+  return words;
+}
+
+// f(integral_constant<uint32_t, 0>) ... f(integral_constant<uint32_t, N-1>).
+template <uint32_t I, uint32_t N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<uint32_t, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
 __device__ __forceinline__ uint32_t ffs128(uint64_t m0, uint64_t m1) {
   return m0 ? (uint32_t)ffs64(m0) : (m1 ? 64u + (uint32_t)ffs64(m1) : 0xFFFFFFFFu);
 }
 
-// waves_per_eu(6): the bound's variant fits 6 waves per SIMD in registers
-// (its MFMA accumulators then live in VGPRs); LDS allows the same at C <= 96.
+// Occupancy floor: the bound's variant holds every code fragment of up to 96
+// ranks (48 registers) next to its MFMA accumulators, which fits 5 waves per
+// SIMD; the variant without it fits 6 at rows of up to 4 chunks per lane.
+// Wider rows (and fp16 rows of 4 chunks per lane, whose tail selects take a
+// few more registers) get no floor, so no variant spills.
 template <int DT, int CPL, bool QB>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_prune_rank(PruneArgs a,
-                                                                                                 uint32_t Cq,
-                                                                                                 uint32_t Rp) {
+constexpr int kRankMinWaves = QB ? 5 : (CPL < 4 || (CPL == 4 && DT != DANCE_F16)) ? 6 : 1;
+template <int DT, int CPL, bool QB>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kRankMinWaves<DT, CPL, QB>, 8))) void k_prune_rank(PruneArgs a, uint32_t Cq) {
   extern __shared__ uint32_t smem[];
   const uint32_t w = wave_index();
   const uint32_t gw = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + w;
@@ -969,24 +1019,23 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6, 8))) 
   const uint32_t node = a.order ? a.order[gw] : gw;
   const uint32_t N = g.N, R = g.R, C = g.C;
   const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;
-  uint32_t* const base = smem + w * prune_rank_lds_words(Cq, Rp, QB);
-  uint32_t* sid = base;  // index -> id (INV: no candidate); in the rounds, ids of the exact-test list
-  float* sd = reinterpret_cast<float*>(base + Cq);    // index -> distance
-  uint32_t* rid = base + 2 * Cq;                      // rank -> id
-  float* rd = reinterpret_cast<float*>(base + 3 * Cq);  // rank -> distance
-  uint32_t* lst = base + 4 * Cq;                      // ranks needing an exact distance
-  uint32_t* rmf = base + 5 * Cq;                      // per rank: removed this round / repeated id
-  uint32_t* oid = base + 6 * Cq;
-  float* od = reinterpret_cast<float*>(oid + Rp);
-  float* hs = reinterpret_cast<float*>(oid + 2 * Rp);  // QB: per rank s, r, a, root
-  float* hr = hs + Cq;
-  float* ha = hr + Cq;
-  float* hroot = ha + Cq;
-  uint32_t* proof = reinterpret_cast<uint32_t*>(hroot + Cq);  // QB: [rank][4] candidate ranks proven kept
-  const bool lo_in = lane < Cq, hi_in = lane + 64u < Cq;      // this lane's two slots exist
+  uint32_t* const base = smem + w * prune_rank_lds_words(Cq, QB);
+  uint32_t* sid = base;                               // ids of the exact-test list (rounds)
+  uint32_t* rid = base + Cq;                          // rank -> id
+  float* rd = reinterpret_cast<float*>(base + 2 * Cq);  // rank -> distance
+  uint32_t* lst = base + 3 * Cq;                      // ranks needing an exact distance
+  uint32_t* rmf = base + 4 * Cq;                      // per rank: removed this round / repeated id
+  // QB: per rank {-2 s, r, a, root} (a = -inf past the valid ranks), reused
+  // after the bound tiles as the list of open pairs; then per rank 4 words:
+  // the candidate ranks the bound proves kept, later those it occludes.
+  float4* hq = reinterpret_cast<float4*>(base + 5 * Cq);
+  uint32_t* plist = reinterpret_cast<uint32_t*>(hq);
+  uint32_t* pm = reinterpret_cast<uint32_t*>(hq + Cq);
+  const bool lo_in = lane < Cq, hi_in = lane + 64u < Cq;  // this lane's two slots exist
 
   const size_t wb = (size_t)node * C, cb = (size_t)node * R;
   const uint32_t deg = min(g.deg_work[node], C);
+  [[maybe_unused]] const uint64_t t0 = dclock();
   // 1. candidates (a lane holds indices lane and lane + 64)
   uint32_t myid[2];
   int mykey[2];
@@ -1002,8 +1051,6 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6, 8))) 
       if (!(valid_for(id, N, node) && dist < FLT_MAX)) id = DANCE_INV;
     }
     if (i < Cq) {
-      sid[i] = id;
-      sd[i] = dist;
       rmf[i] = 0u;
       lst[i] = 0u;
     }
@@ -1011,21 +1058,29 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6, 8))) 
     mydist[h] = dist;
     mykey[h] = fkey(dist);
   }
-  wave_sync();
   // 2. rank = number of candidates before it in (distance, index) order; an
-  // id met twice marks both copies
+  // id met twice marks both copies. Candidate k is read from lane k % 64 of
+  // slot k / 64 (wave-uniform k, so the reads are register reads).
   uint32_t myrank[2] = {0u, 0u};
   bool mydup[2] = {false, false};
-  for (uint32_t k = 0; k < deg; ++k) {
-    const uint32_t idk = sid[k];
+  const uint32_t dlo = min(deg, 64u);
+  for (uint32_t k = 0; k < dlo; ++k) {  // k < 64 <= index of slot 1
+    const uint32_t idk = (uint32_t)__builtin_amdgcn_readlane((int)myid[0], (int)k);
     if (idk == DANCE_INV) continue;
-    const int kk = fkey(sd[k]);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t i = lane + 64u * (uint32_t)h;
-      myrank[h] += (kk < mykey[h] || (kk == mykey[h] && k < i)) ? 1u : 0u;
-      mydup[h] = mydup[h] || (idk == myid[h] && k != i);
-    }
+    const int kk = __builtin_amdgcn_readlane(mykey[0], (int)k);
+    myrank[0] += (kk < mykey[0] || (kk == mykey[0] && k < lane)) ? 1u : 0u;
+    myrank[1] += kk <= mykey[1] ? 1u : 0u;
+    mydup[0] = mydup[0] || (idk == myid[0] && k != lane);
+    mydup[1] = mydup[1] || idk == myid[1];
+  }
+  for (uint32_t k = 64; k < deg; ++k) {  // k >= 64 > index of slot 0
+    const uint32_t idk = (uint32_t)__builtin_amdgcn_readlane((int)myid[1], (int)(k - 64u));
+    if (idk == DANCE_INV) continue;
+    const int kk = __builtin_amdgcn_readlane(mykey[1], (int)(k - 64u));
+    myrank[0] += kk < mykey[0] ? 1u : 0u;
+    myrank[1] += (kk < mykey[1] || (kk == mykey[1] && k - 64u < lane)) ? 1u : 0u;
+    mydup[0] = mydup[0] || idk == myid[0];
+    mydup[1] = mydup[1] || (idk == myid[1] && k - 64u != lane);
   }
   const uint64_t v0 = wballot(myid[0] != DANCE_INV), v1 = wballot(myid[1] != DANCE_INV);
   const uint32_t nvalid = popc64(v0) + popc64(v1);
@@ -1044,69 +1099,202 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6, 8))) 
   if (lo_in) rmf[lane] = 0u;
   if (hi_in) rmf[lane + 64] = 0u;
   wave_sync();
+  [[maybe_unused]] const uint64_t t1 = dclock();
 
-  // 3. the bound's decision for every pair (QB)
+  uint32_t npair = 0, nbchk = 0, nbskip = 0;
+  bool batched = false;  // QB: every open pair's decision is in pm before the rounds
   if constexpr (QB) {
+    // 3. the bound's decision for every pair (i, j > i), from int8 MFMA Gram
+    // tiles of the code rows: bit j of pm[4 i ..] = pair proven kept.
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const uint32_t r = lane + 64u * (uint32_t)h;
-      if (r < nvalid) {
-        const uint4 hd = a.qb.rows[(size_t)rid[r] * kQChunks];
-        hs[r] = __uint_as_float(hd.x);
-        hr[r] = __uint_as_float(hd.y);
-        ha[r] = __uint_as_float(hd.z);
-        hroot[r] = prune_bound_root(a.qb, rd[r], a.alpha);
-      }
       if (r < Cq) {
-        proof[4 * r + 0] = 0u;
-        proof[4 * r + 1] = 0u;
-        proof[4 * r + 2] = 0u;
-        proof[4 * r + 3] = 0u;
+        float4 v = make_float4(0.0f, 0.0f, -__builtin_inff(), 0.0f);
+        if (r < nvalid) {
+          const uint4 hd = a.qb.rows[(size_t)rid[r] * kQChunks];
+          v = make_float4(-2.0f * __uint_as_float(hd.x), __uint_as_float(hd.y), __uint_as_float(hd.z),
+                          prune_bound_root(a.qb, rd[r], a.alpha));
+        }
+        hq[r] = v;
       }
     }
     wave_sync();
     const uint32_t nt = (nvalid + 31u) >> 5;
-    for (uint32_t ti = 0; ti < nt; ++ti) {
-      v4i_t fa[4];
+    const uint32_t jl = lane & 31u, ih = 4u * (lane >> 5);
+    // One 32 x 32 tile of pair decisions: rows ti, columns tj >= ti.
+    auto tile = [&](uint32_t ti, uint32_t tj, const v4i_t(&fa)[4], const v4i_t(&fb)[4]) {
+      v16i_t acc = {};
 #pragma unroll
-      for (uint32_t s = 0; s < 4; ++s) fa[s] = code_frag(a.qb, rid, ti * 32u + (lane & 31u), nvalid, s, lane);
-
-      for (uint32_t tj = ti; tj < nt; ++tj) {
-        v16i_t acc = {};
+      for (uint32_t s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[s], fb[s], acc, 0, 0, 0);
+      // j-side values per lane; i-side per accumulator from LDS. Invalid
+      // ranks carry a = -inf, which fails the test.
+      const uint32_t j = tj * 32u + jl;
+      const float4 hj = hq[j];
+      const float sy = -0.5f * hj.x, ry = hj.y, ay = hj.z, rootj = hj.w;
+      uint32_t words = 0u;  // lane l < 32 collects the proof word of tile row l
+      static_for<0, 16>([&](auto vc) {
+        constexpr uint32_t v = decltype(vc)::value, ir = 8u * (v >> 2) + (v & 3u);
+        const uint32_t i = ti * 32u + ir + ih;
+        const float4 hi = hq[i];
+        const float sT = (rootj + hi.y) * (1.0f + kQSlack);
+        const bool pr = i < j && q_pair_proves_m2(hi.x, hi.z, sT, sy, ry, ay, acc[v]);
+        const uint64_t m = wballot(pr);
+        words = write_lane<ir>(words, (uint32_t)m);
+        words = write_lane<ir + 4u>(words, (uint32_t)(m >> 32));
+      });
+      if (lane < 32u) pm[4u * (ti * 32u + lane) + tj] = words;
+    };
+    if (nt <= 3u) {
+      // up to 96 ranks: every code fragment loaded at once, then the tiles
+      v4i_t F[3][4];
+      static_for<0, 3>([&](auto tc) {
+        constexpr uint32_t t = decltype(tc)::value;
 #pragma unroll
-        for (uint32_t s = 0; s < 4; ++s) {
-          const v4i_t fb = tj == ti ? fa[s] : code_frag(a.qb, rid, tj * 32u + (lane & 31u), nvalid, s, lane);
-          acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[s], fb, acc, 0, 0, 0);
-        }
-        const uint32_t j = tj * 32u + (lane & 31u);
-        const bool jin = j < nvalid;
-        const float sy = jin ? hs[j] : 0.0f, ry = jin ? hr[j] : 0.0f, ay = jin ? ha[j] : 0.0f;
-        const float rootj = jin ? hroot[j] : 0.0f;
+        for (uint32_t s = 0; s < 4; ++s) F[t][s] = code_frag(a.qb, rid, t * 32u + jl, nvalid, s, lane);
+      });
+      static_for<0, 3>([&](auto ic) {
+        constexpr uint32_t ti = decltype(ic)::value;
+        static_for<ti, 3>([&](auto jc) {
+          constexpr uint32_t tj = decltype(jc)::value;
+          if (tj < nt) tile(ti, tj, F[ti], F[tj]);
+        });
+      });
+    } else {
+      for (uint32_t ti = 0; ti < nt; ++ti) {
+        v4i_t fa[4];
 #pragma unroll
-        for (uint32_t v = 0; v < 16; ++v) {
-          const uint32_t i = ti * 32u + 8u * (v >> 2) + 4u * (lane >> 5) + (v & 3u);
-          const bool on = jin && i < j;
-          const float si = on ? hs[i] : 0.0f, ri = on ? hr[i] : 0.0f, ai = on ? ha[i] : 0.0f;
-          const float sT = (rootj + ri) * (1.0f + kQSlack);
-          const bool pr = on && q_pair_proves(si, ai, sT, sy, ry, ay, acc[v]);
-          const uint64_t m = wballot(pr);
-          if (lane == 0) {
-            const uint32_t i0 = ti * 32u + 8u * (v >> 2) + (v & 3u);
-            proof[4 * i0 + tj] = (uint32_t)m;
-            proof[4 * (i0 + 4u) + tj] = (uint32_t)(m >> 32);
-          }
+        for (uint32_t s = 0; s < 4; ++s) fa[s] = code_frag(a.qb, rid, ti * 32u + jl, nvalid, s, lane);
+        tile(ti, ti, fa, fa);
+        for (uint32_t tj = ti + 1u; tj < nt; ++tj) {
+          v4i_t fb[4];
+#pragma unroll
+          for (uint32_t s = 0; s < 4; ++s) fb[s] = code_frag(a.qb, rid, tj * 32u + jl, nvalid, s, lane);
+          tile(ti, tj, fa, fb);
         }
       }
     }
+    // Words of tiles below the diagonal or past the last tile stay unset:
+    // every reader masks them (open pairs keep j > i, j < nvalid; the rounds
+    // keep only remaining ranks, which lie above the selected one).
     wave_sync();
+    // 3b. open pairs (valid j > i that the bound leaves undecided): listed
+    // and computed exactly in one batch when they fit the list (4 Cq pairs),
+    // so the rounds read their decisions from LDS. The occlusion bits
+    // replace the proof words: bit j of pm[4 i ..] = i occludes j.
+    uint32_t op[2][4], cnt[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t i = lane + 64u * (uint32_t)h;
+      cnt[h] = 0u;
+#pragma unroll
+      for (uint32_t q = 0; q < 4; ++q) {
+        uint32_t m = 0u;
+        if (i < nvalid) {
+          const uint32_t lo = 32u * q;
+          // j in [max(i + 1, lo), min(nvalid, lo + 32)) of this word
+          const uint32_t b = i + 1u > lo ? i + 1u - lo : 0u, e = nvalid > lo ? min(nvalid - lo, 32u) : 0u;
+          const uint32_t span = b < e ? ((e - b == 32u ? 0xFFFFFFFFu : ((1u << (e - b)) - 1u)) << b) : 0u;
+          m = span & ~pm[4u * i + q];
+        }
+        op[h][q] = m;
+        cnt[h] += __builtin_popcount(m);
+      }
+    }
+    const uint32_t c0 = wave_reduce_i((int)cnt[0], 0, [](int x, int y) { return x + y; });
+    const uint32_t c1 = wave_reduce_i((int)cnt[1], 0, [](int x, int y) { return x + y; });
+    const uint32_t T = c0 + c1;
+    nbchk = nvalid > 1u ? nvalid * (nvalid - 1u) / 2u : 0u;
+    nbskip = nbchk - T;
+    batched = T <= 4u * Cq;
+    if (batched) {
+      uint32_t w0 = wave_excl_scan_u(cnt[0]), w1 = c0 + wave_excl_scan_u(cnt[1]);
+      wave_sync();  // the open masks are in registers: pm becomes the occlusion words
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t i = lane + 64u * (uint32_t)h;
+        if (i < Cq) {
+          pm[4u * i + 0] = 0u;
+          pm[4u * i + 1] = 0u;
+          pm[4u * i + 2] = 0u;
+          pm[4u * i + 3] = 0u;
+        }
+        uint32_t& wp = h == 0 ? w0 : w1;
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) {
+          uint32_t m = op[h][q];
+          while (m) {
+            const uint32_t bj = (uint32_t)__builtin_ctz(m);
+            m &= m - 1u;
+            plist[wp++] = i | ((32u * q + bj) << 8);
+          }
+        }
+      }
+      wave_sync();
+      // exact distances, two pairs per octet in flight; the distance of
+      // (i, j) is taken with i's row first, as the rounds would take it
+      for (uint32_t p = 0; p < T; p += 16) {
+        const uint32_t k0 = p + grp, k1 = p + 8 + grp;
+        const bool a0 = k0 < T, a1 = k1 < T;
+        const uint32_t e0 = plist[min(k0, T - 1u)], e1 = plist[min(k1, T - 1u)];
+        const uint32_t i0 = e0 & 0xFFu, j0 = e0 >> 8, i1 = e1 & 0xFFu, j1 = e1 >> 8;
+        uint4 x0[CPL], y0[CPL], x1[CPL], y1[CPL];
+        load_row<CPL>(a.rs, rid[i0], a0, sub, x0);
+        load_row<CPL>(a.rs, rid[j0], a0, sub, y0);
+        load_row<CPL>(a.rs, rid[i1], a1, sub, x1);
+        load_row<CPL>(a.rs, rid[j1], a1, sub, y1);
+        const float d0 = octet_finish<DT, CPL>(a.rs, sub, x0, y0);
+        const float d1 = octet_finish<DT, CPL>(a.rs, sub, x1, y1);
+        if (sub == 0) {
+          if (a0 && a.alpha * d0 <= rd[j0]) atomicOr(&pm[4u * i0 + (j0 >> 5)], 1u << (j0 & 31u));
+          if (a1 && a.alpha * d1 <= rd[j1]) atomicOr(&pm[4u * i1 + (j1 >> 5)], 1u << (j1 & 31u));
+        }
+      }
+      npair = T;
+      wave_sync();
+    }
   }
 
-  // 4. selection rounds on rank masks
+  // 4. selection rounds on rank masks. Rank r's id, distance and (batched)
+  // occlusion words sit in lane r % 64 of register slot r / 64, read with
+  // v_readlane; outputs collect in registers (output k in lane k % 64 of
+  // slot k / 64). The exact-test path of the rounds keeps its lists in LDS.
+  [[maybe_unused]] const uint64_t t2 = dclock();
+  uint32_t r_id[2], r_occ[2][4];
+  float r_d[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t r = min(lane + 64u * (uint32_t)h, Cq - 1u);
+    r_id[h] = rid[r];
+    r_d[h] = rd[r];
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) r_occ[h][q] = 0u;
+    if constexpr (QB) {
+      if (batched) {
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) r_occ[h][q] = pm[4u * r + q];
+      }
+    }
+  }
+  auto rank_u = [&](const uint32_t (&v)[2], uint32_t r) -> uint32_t {
+    return (uint32_t)__builtin_amdgcn_readlane((int)(r < 64u ? v[0] : v[1]), (int)(r & 63u));
+  };
+  uint32_t o_id[2] = {DANCE_INV, DANCE_INV};
+  float o_d[2] = {FLT_MAX, FLT_MAX};
+  auto emit = [&](uint32_t k, uint32_t id, float d) {  // output k (uniform)
+    if (k < 64u) {
+      o_id[0] = lane == k ? id : o_id[0];
+      o_d[0] = lane == k ? d : o_d[0];
+    } else {
+      o_id[1] = lane == k - 64u ? id : o_id[1];
+      o_d[1] = lane == k - 64u ? d : o_d[1];
+    }
+  };
   uint64_t rem0 = all0, rem1 = all1, io0 = 0ull, io1 = 0ull;
-  uint32_t oc = 0, npair = 0, nbchk = 0, nbskip = 0;
-  auto drop_same_id = [&](uint32_t r, uint32_t id) {  // every copy of id leaves and counts as output
-    const uint64_t s0 = wballot(lane < nvalid && rid[min(lane, Cq - 1u)] == id);
-    const uint64_t s1 = wballot(lane + 64u < nvalid && rid[min(lane + 64u, Cq - 1u)] == id);
+  uint32_t oc = 0, nround = 0, nexact = 0;
+  auto drop_same_id = [&](uint32_t id) {  // every copy of id leaves and counts as output
+    const uint64_t s0 = wballot(lane < nvalid && r_id[0] == id);
+    const uint64_t s1 = wballot(lane + 64u < nvalid && r_id[1] == id);
     rem0 &= ~s0;
     rem1 &= ~s1;
     io0 |= s0;
@@ -1115,13 +1303,11 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6, 8))) 
   while (oc < R) {
     const uint32_t r = ffs128(rem0, rem1);
     if (r == 0xFFFFFFFFu) break;
-    const uint32_t sel = uni_u(rid[r]);
-    const float seld = uni_f(rd[r]);
-    if (lane == 0) {
-      oid[oc] = sel;
-      od[oc] = seld;
-    }
+    const uint32_t sel = rank_u(r_id, r);
+    const float seld = __uint_as_float(rank_u(reinterpret_cast<const uint32_t(&)[2]>(r_d), r));
+    emit(oc, sel, seld);
     oc++;
+    nround++;
     if (r < 64) {
       rem0 &= ~(1ull << r);
       io0 |= 1ull << r;
@@ -1129,27 +1315,37 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6, 8))) 
       rem1 &= ~(1ull << (r - 64));
       io1 |= 1ull << (r - 64);
     }
-    if ((r < 64 ? (dup0 >> r) : (dup1 >> (r - 64))) & 1ull) drop_same_id(r, sel);
+    if ((r < 64 ? (dup0 >> r) : (dup1 >> (r - 64))) & 1ull) drop_same_id(sel);
     if (oc >= R) break;
+    if (batched) {  // QB only: the decisions of every open pair are in r_occ
+      const uint32_t l = r & 63u;
+      const bool hi = r >= 64u;
+      const uint32_t w0 = (uint32_t)__builtin_amdgcn_readlane((int)(hi ? r_occ[1][0] : r_occ[0][0]), (int)l);
+      const uint32_t w1 = (uint32_t)__builtin_amdgcn_readlane((int)(hi ? r_occ[1][1] : r_occ[0][1]), (int)l);
+      const uint32_t w2 = (uint32_t)__builtin_amdgcn_readlane((int)(hi ? r_occ[1][2] : r_occ[0][2]), (int)l);
+      const uint32_t w3 = (uint32_t)__builtin_amdgcn_readlane((int)(hi ? r_occ[1][3] : r_occ[0][3]), (int)l);
+      rem0 &= ~((uint64_t)w0 | ((uint64_t)w1 << 32));
+      rem1 &= ~((uint64_t)w2 | ((uint64_t)w3 << 32));
+      continue;
+    }
     uint64_t need0 = rem0, need1 = rem1;
     if (need0 == 0 && need1 == 0) continue;
     if constexpr (QB) {
-      const uint64_t p0 = (uint64_t)uni_u(proof[4 * r + 0]) | ((uint64_t)uni_u(proof[4 * r + 1]) << 32);
-      const uint64_t p1 = (uint64_t)uni_u(proof[4 * r + 2]) | ((uint64_t)uni_u(proof[4 * r + 3]) << 32);
-      nbchk += popc64(need0) + popc64(need1);
+      const uint64_t p0 = (uint64_t)uni_u(pm[4 * r + 0]) | ((uint64_t)uni_u(pm[4 * r + 1]) << 32);
+      const uint64_t p1 = (uint64_t)uni_u(pm[4 * r + 2]) | ((uint64_t)uni_u(pm[4 * r + 3]) << 32);
       need0 &= ~p0;
       need1 &= ~p1;
-      nbskip += popc64(rem0 & p0) + popc64(rem1 & p1);
       if (need0 == 0 && need1 == 0) continue;
     }
     uint4 sv[CPL];  // the selected row, in flight while the list is built
     load_row<CPL>(a.rs, sel, true, sub, sv);
+    nexact++;
     const uint32_t n0 = popc64(need0), nn = n0 + popc64(need1);
     // the list holds each rank and, in sid, its id
     if ((need0 >> lane) & 1ull) lst[mbcnt64(need0)] = lane;
     if ((need1 >> lane) & 1ull) lst[n0 + mbcnt64(need1)] = lane + 64u;
-    if ((need0 >> lane) & 1ull) sid[mbcnt64(need0)] = rid[lane];
-    if ((need1 >> lane) & 1ull) sid[n0 + mbcnt64(need1)] = rid[lane + 64u];
+    if ((need0 >> lane) & 1ull) sid[mbcnt64(need0)] = r_id[0];
+    if ((need1 >> lane) & 1ull) sid[n0 + mbcnt64(need1)] = r_id[1];
     wave_sync();
     for (uint32_t p = 0; p < nn; p += 16) {
       const uint32_t k0 = p + grp, k1 = p + 8 + grp;
@@ -1177,38 +1373,49 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6, 8))) 
   }
   // 5. degree fill to min(min_degree, R): lowest ranks not yet output,
   // occluded ones included (vnew2.cu:2076-2126)
+  [[maybe_unused]] const uint64_t t3 = dclock();
   const uint32_t md = min(a.min_degree, R);
   while (oc < md) {
     const uint32_t r = ffs128(all0 & ~io0, all1 & ~io1);
     if (r == 0xFFFFFFFFu) break;
-    const uint32_t pick = uni_u(rid[r]);
-    if (lane == 0) {
-      oid[oc] = pick;
-      od[oc] = rd[r];
-    }
+    const uint32_t pick = rank_u(r_id, r);
+    emit(oc, pick, __uint_as_float(rank_u(reinterpret_cast<const uint32_t(&)[2]>(r_d), r)));
     oc++;
     if (r < 64)
       io0 |= 1ull << r;
     else
       io1 |= 1ull << (r - 64);
-    if ((r < 64 ? (dup0 >> r) : (dup1 >> (r - 64))) & 1ull) drop_same_id(r, pick);
+    if ((r < 64 ? (dup0 >> r) : (dup1 >> (r - 64))) & 1ull) drop_same_id(pick);
   }
-  wave_sync();
-  for (uint32_t i = lane; i < C; i += 64) {
-    g.work[wb + i] = i < oc ? oid[i] : DANCE_INV;
-    g.wd[wb + i] = i < oc ? od[i] : FLT_MAX;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t i = lane + 64u * (uint32_t)h;
+    if (i < C) {
+      g.work[wb + i] = i < oc ? o_id[h] : DANCE_INV;
+      g.wd[wb + i] = i < oc ? o_d[h] : FLT_MAX;
+    }
+    if (i < R) g.cur[cb + i] = i < oc ? o_id[h] : DANCE_INV;
   }
-  for (uint32_t i = lane; i < R; i += 64) g.cur[cb + i] = i < oc ? oid[i] : DANCE_INV;
   if (lane == 0) {
     g.deg_work[node] = oc;
     g.deg_cur[node] = oc;
   }
   if (a.ctr && lane == 0) {
-    atomicAdd(&ctr_stripe(a.ctr)->prune_dist, (unsigned long long)npair);
+    VCounters* c = ctr_stripe(a.ctr);
+    atomicAdd(&c->prune_dist, (unsigned long long)npair);
+    atomicAdd(&c->prune_rounds, (unsigned long long)nround);
+    atomicAdd(&c->prune_exact_rounds, (unsigned long long)nexact);
     if (QB) {
-      atomicAdd(&ctr_stripe(a.ctr)->prune_bound_checks, (unsigned long long)nbchk);
-      atomicAdd(&ctr_stripe(a.ctr)->prune_bound_skips, (unsigned long long)nbskip);
+      atomicAdd(&c->prune_bound_checks, (unsigned long long)nbchk);
+      atomicAdd(&c->prune_bound_skips, (unsigned long long)nbskip);
     }
+#if DANCE_SEARCH_TIMING
+    const uint64_t t4 = dclock();
+    atomicAdd(&c->cyc_prune_rank, (unsigned long long)(t1 - t0));
+    atomicAdd(&c->cyc_prune_gram, (unsigned long long)(t2 - t1));
+    atomicAdd(&c->cyc_prune_rounds, (unsigned long long)(t3 - t2));
+    atomicAdd(&c->cyc_prune_fill, (unsigned long long)(t4 - t3));
+#endif
   }
 }
 

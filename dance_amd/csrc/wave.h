@@ -104,6 +104,17 @@ __device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
   return (uint32_t)wave_reduce_i((int)v, -1, [](int a, int b) { return (int)min((uint32_t)a, (uint32_t)b); });
 }
 
+// Exclusive prefix sum over the 64 lanes.
+__device__ __forceinline__ uint32_t wave_excl_scan_u(uint32_t v) {
+  uint32_t x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t y = (uint32_t)__shfl_up((int)x, (unsigned int)d);
+    if (lane_id() >= (uint32_t)d) x += y;
+  }
+  return x - v;
+}
+
 // Workgroup -> logical block. Workgroups are dispatched round-robin over the 8
 // XCDs; this mapping hands XCD k the contiguous logical range
 // [k*per, (k+1)*per) so each XCD's L2 walks one region of the processing

@@ -42,6 +42,19 @@ typedef struct DanceKernelProfile {
     uint64_t prune_bound_checks, prune_bound_skips;
     /* per iteration (launch order): search and prune launch times in ms */
     double search_iter_ms[4], prune_iter_ms[4];
+    /* per iteration: the counters above split by launch, and the algorithmic
+     * bytes of each search and prune launch (the totals above are their sums) */
+    uint64_t search_dist_iter[4], insert_dist_iter[4], expansions_iter[4], bound_checks_iter[4],
+        bound_skips_iter[4];
+    uint64_t merge_dist_iter[4], prune_dist_iter[4], prune_bound_checks_iter[4], prune_bound_skips_iter[4];
+    double search_bytes_iter[4], prune_bytes_iter[4];
+    /* RobustPrune selection rounds (vertices x rounds) and the rounds that
+     * computed at least one exact pair distance, over all iterations; phase
+     * cycles of the rank-mask prune (zero unless built with
+     * DANCE_SEARCH_TIMING=1): ranking, bound tiles, selection rounds, fill and
+     * write-back, summed over waves */
+    uint64_t prune_rounds, prune_exact_rounds;
+    uint64_t cyc_prune_rank, cyc_prune_gram, cyc_prune_rounds, cyc_prune_fill;
 } DanceKernelProfile;
 
 /* Full standard (vnew2) build with the vectors already resident in device
