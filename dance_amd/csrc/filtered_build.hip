@@ -120,7 +120,7 @@ int validate(const FParams& p, const uint32_t* off, const uint32_t* lab, const u
 }
 
 struct FState {
-  DevBuf off, lab, lab8, lpo, lpts, starts, task_rows;
+  DevBuf off, lab, lab8, sig, gsig, lpo, lpts, starts, task_rows;
   DevBuf ga, gb, da, db, tids, td;
   DevBuf roff, cursor, rids, boff, bd, brem, bmask, lrows, lsort, lcount;
   DevBuf ctr, d32, d64;
@@ -177,6 +177,13 @@ void peak_mem(double& peak) {
   size_t fr = 0, tot = 0;
   if (hipMemGetInfo(&fr, &tot) == hipSuccess) peak = std::max(peak, (double)(tot - fr) / (1024.0 * 1024.0 * 1024.0));
 }
+
+struct StreamGuard {
+  hipStream_t s = nullptr;
+  ~StreamGuard() {
+    if (s) (void)hipStreamDestroy(s);
+  }
+};
 
 // canonical_print_round_diagnostics (gpu_vamana_filtered.cu:94-160) over the
 // published graph: the per-row figures come from k_degree_profile, the
@@ -294,17 +301,23 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   ScanWorkspace scan;
   SortWorkspace sort_ws;
 
-  // Fixed-width label rows for membership tests (DANCE_FILTERED_LAB8=0: list walks only).
+  // Fixed-width label rows for membership tests (DANCE_FILTERED_LAB8=0: list
+  // walks only), and per-point label signatures carried next to the round's
+  // input graph so the searches reject most neighbours without a label read
+  // (DANCE_FILTERED_SIG=0: off). Neither changes a result.
   const char* l8e = std::getenv("DANCE_FILTERED_LAB8");
   const bool use_lab8 = !(l8e && l8e[0] == '0');
-  if (use_lab8) {
-    DCHECK(st.lab8.alloc((size_t)N * 32));
-    hipLaunchKernelGGL(k_lab8, dim3(grid_thr(N)), dim3(256), 0, s, N, st.off.as<uint32_t>(), st.lab.as<uint32_t>(),
-                       st.lab8.as<uint4>());
-    DHIP(hipGetLastError());
-  }
+  const char* sge = std::getenv("DANCE_FILTERED_SIG");
+  const bool use_sig = !(sge && sge[0] == '0');
+  if (use_lab8) DCHECK(st.lab8.alloc((size_t)N * 32));
+  DCHECK(st.sig.alloc((size_t)N * 4));
+  if (use_sig && p.rounds) DCHECK(st.gsig.alloc(NR * 4));
+  hipLaunchKernelGGL(k_lab8, dim3(grid_thr(N)), dim3(256), 0, s, N, st.off.as<uint32_t>(), st.lab.as<uint32_t>(),
+                     use_lab8 ? st.lab8.as<uint4>() : nullptr, st.sig.as<uint32_t>());
+  DHIP(hipGetLastError());
   Labels Ld{st.off.as<uint32_t>(), st.lab.as<uint32_t>(), st.lpo.as<uint32_t>(), st.lpts.as<uint32_t>(),
-            st.starts.as<uint32_t>(), p.num_labels, p.universal, use_lab8 ? st.lab8.as<const uint4>() : nullptr};
+            st.starts.as<uint32_t>(), p.num_labels, p.universal, use_lab8 ? st.lab8.as<const uint4>() : nullptr,
+            use_sig ? st.sig.as<const uint32_t>() : nullptr};
   uint32_t* ga = st.ga.as<uint32_t>();
   uint32_t* gb = st.gb.as<uint32_t>();
   uint32_t* da = st.da.as<uint32_t>();
@@ -313,6 +326,12 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   uint32_t* boff = st.boff.as<uint32_t>();
 
   FEvents E;
+  // Rows of more than kCsrRegMax candidates (label hubs) are pruned on a
+  // second stream, concurrently with the short rows: the largest hub holds
+  // one workgroup for tens of ms, which the short rows' kernel then hides.
+  StreamGuard s2g;
+  DHIP(hipStreamCreate(&s2g.s));
+  const hipStream_t s2 = s2g.s;
   hipEvent_t e0 = E.mark(s);
   hipLaunchKernelGGL(k_random_graph, dim3(grid_thr(N)), dim3(256), 0, s, N, R,
                      std::min(std::min(kBackboneDegree, R), N - 1), kBackboneSeed, ga, da);
@@ -345,7 +364,13 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   }
 
   for (uint32_t round = 0; round < p.rounds; ++round) {
-    const Graph Ga{N, R, ga, da};
+    Graph Ga{N, R, ga, da};
+    if (use_sig) {
+      hipLaunchKernelGGL(k_graph_sig, dim3(grid_thr(NR)), dim3(256), 0, s, N, R, static_cast<const uint32_t*>(ga),
+                         static_cast<const uint32_t*>(da), st.sig.as<const uint32_t>(), st.gsig.as<uint32_t>());
+      DHIP(hipGetLastError());
+      Ga.sig = st.gsig.as<const uint32_t>();
+    }
     if (log) {
       DHIP(hipMemcpyAsync(st.prev_g.p, ga, NR * 4, hipMemcpyDeviceToDevice, s));
       DHIP(hipMemcpyAsync(st.prev_d.p, da, (size_t)N * 4, hipMemcpyDeviceToDevice, s));
@@ -402,14 +427,19 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
     CsrArgs Cs{p.alpha, roff, st.rids.as<const uint32_t>(), boff, st.bd.as<float>(), st.brem.as<uint8_t>(),
                st.bmask.as<uint32_t>(), ga, da, ctr};
     DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
+      hipEvent_t long_done = nullptr;
+      if (tails[2] > 0) {  // the two kernels write disjoint rows
+        DHIP(hipStreamWaitEvent(s2, r3, 0));
+        hipLaunchKernelGGL((k_csr_long<decltype(dt)::value, decltype(c)::value>), dim3(tails[2]), dim3(kLongBlock), 0,
+                           s2, rows.rs, Gb, Ld, Cs, lvals[lr]);
+        DHIP(hipGetLastError());
+        long_done = E.mark(s2);
+        if (!long_done) return -1;
+      }
       hipLaunchKernelGGL((k_csr<decltype(dt)::value, decltype(c)::value>), dim3(grid_xcd(N)), dim3(kBlock), csr_lds,
                          s, rows.rs, Gb, Ld, Cs);
       DHIP(hipGetLastError());
-      if (tails[2] > 0) {
-        hipLaunchKernelGGL((k_csr_long<decltype(dt)::value, decltype(c)::value>), dim3(tails[2]), dim3(kLongBlock), 0,
-                           s, rows.rs, Gb, Ld, Cs, lvals[lr]);
-        DHIP(hipGetLastError());
-      }
+      if (long_done) DHIP(hipStreamWaitEvent(s, long_done, 0));
       return 0;
     }));
     hipEvent_t r4 = E.mark(s);
@@ -575,13 +605,6 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
                 p.dim, R, p.L, p.filtered_L, p.C, p.num_labels, T, p.rounds, kp.total_ms);
   return 0;
 }
-
-struct StreamGuard {
-  hipStream_t s = nullptr;
-  ~StreamGuard() {
-    if (s) (void)hipStreamDestroy(s);
-  }
-};
 
 // Host-input build. src_dtype: DANCE_F32 (searched as fp16), DANCE_U8 or
 // DANCE_F16 (host fp16 rows, used by tests).

@@ -82,14 +82,24 @@ struct Labels {
   // (more than 8 labels, or the label DANCE_INV): membership tests then read
   // one 32-byte row instead of walking the list. nullptr: list walks only.
   const uint4* lab8;
+  // Per point, a 32-bit label signature: bit sig_bit(l) set for each label l
+  // of the point. A clear bit proves the label absent; a set bit leaves the
+  // answer to the exact test.
+  const uint32_t* sig;
 };
 
-// Builds Labels::lab8 (one thread per point).
+__device__ __forceinline__ uint32_t sig_bit(uint32_t label) { return (label * 0x9E3779B1u) >> 27; }
+
+// Builds Labels::lab8 (nullptr: skipped) and Labels::sig (one thread per point).
 static __global__ void k_lab8(uint32_t N, const uint32_t* __restrict__ off, const uint32_t* __restrict__ lab,
-                              uint4* __restrict__ lab8) {
+                              uint4* __restrict__ lab8, uint32_t* __restrict__ sig) {
   const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
   if (p >= N) return;
   const uint32_t b = off[p], n = off[p + 1] - b;
+  uint32_t sg = 0u;
+  for (uint32_t i = 0; i < n; ++i) sg |= 1u << sig_bit(lab[b + i]);
+  sig[p] = sg;
+  if (!lab8) return;
   uint32_t v[8];
   bool fits = n <= 8;
 #pragma unroll
@@ -121,7 +131,23 @@ struct Graph {
   uint32_t N, R;
   const uint32_t* g;  // N x R
   const uint32_t* d;  // N
+  // Optional, N x R: the label signature (Labels::sig) of each entry's
+  // point, read with the row so that label filters reject most neighbours
+  // without a per-candidate label read (k_graph_sig).
+  const uint32_t* sig = nullptr;
 };
+
+// Graph::sig of a graph: entry i of row r = sig[g[r][i]] for i < min(d[r], R)
+// and valid ids, else 0 (one thread per entry).
+static __global__ void k_graph_sig(uint32_t N, uint32_t R, const uint32_t* __restrict__ g,
+                                   const uint32_t* __restrict__ d, const uint32_t* __restrict__ sig,
+                                   uint32_t* __restrict__ out) {
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (uint64_t)N * R) return;
+  const uint32_t r = (uint32_t)(t / R), i = (uint32_t)(t % R);
+  const uint32_t id = g[t];
+  out[t] = (i < min(d[r], R) && id < N) ? sig[id] : 0u;
+}
 
 // point_has_exact_label_device (gpu_vamana_filtered.cu:557-573)
 __device__ __forceinline__ bool has_exact(const Labels& L, uint32_t p, uint32_t label) {
@@ -320,13 +346,15 @@ struct FSearch {
   }
 
   // One batch of up to 64 candidates in insertion order (lane order; DANCE_INV
-  // = no candidate). accept() is the label filter of the current phase.
+  // = no candidate). accept(c, sg) is the label filter of the current phase;
+  // sg is c's label signature when the caller has it (a graph row with
+  // signatures), else all ones (no information).
   template <typename F>
-  __device__ __forceinline__ void batch(uint32_t c, F&& accept) {
+  __device__ __forceinline__ void batch(uint32_t c, F&& accept, uint32_t sg = 0xFFFFFFFFu) {
     const bool v = c < N && c != row;
     const uint32_t slot = (c * 0x9E3779B1u) >> (32 - kVisBits);
     const bool seen = v && vis[slot] == c;
-    const bool need = v && !seen && accept(c);
+    const bool need = v && !seen && accept(c, sg);
     const uint64_t m = wballot(need);
     if (m) {
       const uint32_t n = popc64(m);
@@ -351,7 +379,10 @@ struct FSearch {
   __device__ __forceinline__ void neighbours(const Graph& G, uint32_t u, F&& accept) {
     const uint32_t deg = min(G.d[u], G.R);
     const size_t b = (size_t)u * G.R;
-    for (uint32_t j = 0; j < deg; j += 64) batch(j + lane < deg ? G.g[b + j + lane] : DANCE_INV, accept);
+    for (uint32_t j = 0; j < deg; j += 64) {
+      const bool in = j + lane < deg;
+      batch(in ? G.g[b + j + lane] : DANCE_INV, accept, in && G.sig ? G.sig[b + j + lane] : 0xFFFFFFFFu);
+    }
   }
 
   template <typename F>
@@ -492,8 +523,9 @@ __global__ __launch_bounds__(kBlock) void k_task_search(RowSet rs, Graph G, Labe
   }
   FSearch<DT, CPL> S;
   S.init(rs, N, row, smem + w * kSearchLds, cap);
-  auto any = [](uint32_t) { return true; };
-  auto exact = [&](uint32_t c) { return has_exact(L, c, label); };
+  auto any = [](uint32_t, uint32_t) { return true; };
+  const uint32_t lbit = 1u << sig_bit(label);
+  auto exact = [&](uint32_t c, uint32_t sg) { return (sg & lbit) != 0u && has_exact(L, c, label); };
   S.batch(lane == 0 ? L.starts[label] : DANCE_INV, any);
   const uint32_t pb = L.lpo[label], pc = L.lpo[label + 1] - pb;
   const uint32_t sc = min(16u, pc);
@@ -580,8 +612,9 @@ __global__ __launch_bounds__(kBlock) void k_row(RowSet rs, Graph G, Labels L, Ro
   //    then the global start and the traversal restricted to compatible ids
   FSearch<DT, CPL> S;
   S.init(rs, N, row, lds, A.ocap);
-  auto any = [](uint32_t) { return true; };
-  auto compat = [&](uint32_t c) { return compatible(L, row, c); };
+  auto any = [](uint32_t, uint32_t) { return true; };
+  const uint32_t rsig = L.sig ? L.sig[row] : 0xFFFFFFFFu;
+  auto compat = [&](uint32_t c, uint32_t sg) { return (sg & rsig) != 0u && compatible(L, row, c); };
   for (uint32_t p = lb; p < le; ++p) {
     const uint32_t label = L.lab[p];
     if (label >= L.num_labels) continue;
