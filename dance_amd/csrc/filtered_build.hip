@@ -120,7 +120,7 @@ int validate(const FParams& p, const uint32_t* off, const uint32_t* lab, const u
 }
 
 struct FState {
-  DevBuf off, lab, lab8, sig, gsig, lpo, lpts, starts, task_rows;
+  DevBuf off, lab, lab8, sig, gsig, lpo, lpts, starts, task_rows, rorder, torder;
   DevBuf ga, gb, da, db, tids, td;
   DevBuf roff, cursor, rids, boff, bd, brem, bmask, lrows, lsort, lcount;
   DevBuf ctr, d32, d64;
@@ -233,6 +233,50 @@ int print_degree_profile(FState& st, const Labels& Ld, uint32_t N, hipStream_t s
   return 0;
 }
 
+// Processing order of the rows (row kernels) and of the per-label tasks:
+// rows sorted by nearest of K evenly spaced pivot rows (the standard build's
+// locality schedule, K from DANCE_LOCALITY_CELLS, default 1024, 0: identity
+// order), and each row's tasks in that row order. Waves in flight then work
+// on neighbouring rows, whose searches share rows in L2. Results do not depend
+// on the order. Scratch: lsort / lrows (sort), roff (task offsets).
+int locality_order(const Rows& rows, const Labels& Ld, uint32_t N, uint32_t T, FState& st, ScanWorkspace& scan,
+                   SortWorkspace& sort_ws, hipStream_t s, const uint32_t** rorder, const uint32_t** torder) {
+  const char* e = std::getenv("DANCE_LOCALITY_CELLS");
+  const uint32_t K = std::min(e && e[0] ? (uint32_t)std::strtoul(e, nullptr, 10) : 1024u, N);
+  *rorder = *torder = nullptr;
+  if (K < 2) return 0;
+  DevBuf piv;
+  DCHECK(piv.alloc((size_t)K * 4));
+  hipLaunchKernelGGL(k_pivots, dim3((K + 255) / 256), dim3(256), 0, s, N, K, piv.as<uint32_t>());
+  DHIP(hipGetLastError());
+  uint32_t* kb[2] = {st.lsort.as<uint32_t>(), st.lsort.as<uint32_t>() + N};
+  uint32_t* vb[2] = {st.lrows.as<uint32_t>(), st.lsort.as<uint32_t>() + 2 * (size_t)N};
+  DCHECK(with_dt_cpl(rows.dtype, pick_cpl(rows.rs.nch), [&](auto dt, auto c) {
+    hipLaunchKernelGGL((k_cells<decltype(dt)::value, decltype(c)::value>), dim3(cells_grid(N)), dim3(kCellsBlock), 0,
+                       s, rows.rs, N, piv.as<const uint32_t>(), K, kb[0], vb[0]);
+    DHIP(hipGetLastError());
+    return 0;
+  }));
+  int which = 0;
+  DCHECK(radix_sort_pairs(kb, vb, N, bit_length(K - 1), sort_ws, s, &which));
+  DCHECK(st.rorder.alloc((size_t)N * 4));
+  DHIP(hipMemcpyAsync(st.rorder.p, vb[which], (size_t)N * 4, hipMemcpyDeviceToDevice, s));
+  if (T) {
+    uint32_t* pos = st.roff.as<uint32_t>();  // N + 1 entries, free until the rounds
+    DCHECK(st.torder.alloc((size_t)T * 4));
+    hipLaunchKernelGGL(k_task_counts, dim3(grid_thr((uint64_t)N + 1)), dim3(256), 0, s, N, Ld.off,
+                       st.rorder.as<const uint32_t>(), pos);
+    DHIP(hipGetLastError());
+    DCHECK(scan_exclusive(pos, (size_t)N + 1, scan, s));
+    hipLaunchKernelGGL(k_task_fill, dim3(grid_thr(N)), dim3(256), 0, s, N, Ld.off, st.rorder.as<const uint32_t>(),
+                       pos, st.torder.as<uint32_t>());
+    DHIP(hipGetLastError());
+    *torder = st.torder.as<const uint32_t>();
+  }
+  *rorder = st.rorder.as<const uint32_t>();
+  return 0;
+}
+
 // Runs the build on resident rows; on success st.ga / st.da hold the graph.
 int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, const uint32_t* h_lab,
                  const uint32_t* h_starts, hipStream_t s, FState& st, GPUFilteredVamanaStats& gs,
@@ -271,6 +315,7 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   DCHECK(st.lpts.alloc(lpts.size() * 4));
   DCHECK(st.starts.alloc((size_t)nl * 4));
   DCHECK(st.task_rows.alloc((size_t)std::max(1u, T) * 4));
+
   DHIP(hipMemcpyAsync(st.off.p, h_off, (size_t)(N + 1) * 4, hipMemcpyHostToDevice, s));
   if (T) DHIP(hipMemcpyAsync(st.lab.p, h_lab, (size_t)T * 4, hipMemcpyHostToDevice, s));
   DHIP(hipMemcpyAsync(st.lpo.p, lpo.data(), lpo.size() * 4, hipMemcpyHostToDevice, s));
@@ -339,6 +384,9 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   hipEvent_t e1 = E.mark(s);
   hipLaunchKernelGGL(k_task_rows, dim3(grid_thr(N)), dim3(256), 0, s, N, Ld.off, st.task_rows.as<uint32_t>());
   DHIP(hipGetLastError());
+  const uint32_t* rorder = nullptr;
+  const uint32_t* torder = nullptr;
+  DCHECK(locality_order(rows, Ld, N, T, st, scan, sort_ws, s, &rorder, &torder));
   hipEvent_t e2 = E.mark(s);
   kp.backbone_ms = ms_between(e0, e1);
   double task_ms = 0, row_ms = 0, rev_ms = 0, csr_ms = 0;
@@ -379,15 +427,16 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
     if (T > 0) {
       DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
         hipLaunchKernelGGL((k_task_search<decltype(dt)::value, decltype(c)::value>), dim3(grid_xcd(T)),
-                           dim3(kBlock), search_lds, s, rows.rs, Ga, Ld, st.task_rows.as<const uint32_t>(), T,
-                           per_label_pool, per_label_keep, p.STEPS, st.tids.as<uint32_t>(), st.td.as<float>(), ctr);
+                           dim3(kBlock), search_lds, s, rows.rs, Ga, Ld, st.task_rows.as<const uint32_t>(), torder,
+                           T, per_label_pool, per_label_keep, p.STEPS, st.tids.as<uint32_t>(), st.td.as<float>(),
+                           ctr);
         DHIP(hipGetLastError());
         return 0;
       }));
     }
     hipEvent_t r1 = E.mark(s);
     RowArgs A{ordinary_pool, ordinary_keep, p.STEPS, p.global_start, work_C, per_label_keep, p.alpha,
-              st.tids.as<const uint32_t>(), st.td.as<const float>(), gb, db, ctr};
+              st.tids.as<const uint32_t>(), st.td.as<const float>(), gb, db, ctr, rorder};
     DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
       hipLaunchKernelGGL((k_row<decltype(dt)::value, decltype(c)::value>), dim3(grid_xcd(N)), dim3(kBlock),
                          search_lds, s, rows.rs, Ga, Ld, A);

@@ -23,6 +23,7 @@
 // traversal, so skipping a cached id never changes the pool.
 #pragma once
 
+#include "locality.h"
 #include "wave.h"
 
 namespace dance {
@@ -492,6 +493,23 @@ static __global__ void k_random_graph(uint32_t N, uint32_t R, uint32_t target, u
 }
 
 // canonical_make_task_rows: task p (a position in the label array) -> its row.
+// Task order from a row order: pos[k] = label count of row order[k] (pos[N]
+// = 0, then an exclusive scan), and the tasks of row order[k] (its label
+// positions off[r] .. off[r + 1]) at pos[k] .. (one thread per row).
+static __global__ void k_task_counts(uint32_t N, const uint32_t* __restrict__ off, const uint32_t* __restrict__ order,
+                                     uint32_t* __restrict__ pos) {
+  const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k > N) return;
+  pos[k] = k == N ? 0u : off[order[k] + 1] - off[order[k]];
+}
+static __global__ void k_task_fill(uint32_t N, const uint32_t* __restrict__ off, const uint32_t* __restrict__ order,
+                                   const uint32_t* __restrict__ pos, uint32_t* __restrict__ torder) {
+  const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= N) return;
+  const uint32_t r = order[k], b = off[r], n = off[r + 1] - b, p = pos[k];
+  for (uint32_t j = 0; j < n; ++j) torder[p + j] = b + j;
+}
+
 static __global__ void k_task_rows(uint32_t N, const uint32_t* off, uint32_t* task_rows) {
   const uint32_t row = blockIdx.x * blockDim.x + threadIdx.x;
   if (row >= N) return;
@@ -503,13 +521,14 @@ static __global__ void k_task_rows(uint32_t N, const uint32_t* off, uint32_t* ta
 // then the exact-label traversal; the first `keep` pool slots are the output.
 template <int DT, int CPL>
 __global__ __launch_bounds__(kBlock) void k_task_search(RowSet rs, Graph G, Labels L, const uint32_t* task_rows,
-                                                        uint32_t tasks, uint32_t cap, uint32_t keep,
-                                                        uint32_t steps, uint32_t* out_ids, float* out_d,
-                                                        unsigned long long* ctr) {
+                                                        const uint32_t* order, uint32_t tasks, uint32_t cap,
+                                                        uint32_t keep, uint32_t steps, uint32_t* out_ids,
+                                                        float* out_d, unsigned long long* ctr) {
   extern __shared__ uint32_t smem[];
   const uint32_t w = wave_index();
-  const uint32_t t = xcd_block(blockIdx.x, gridDim.x) * kWaves + w;
-  if (t >= tasks) return;
+  const uint32_t k = xcd_block(blockIdx.x, gridDim.x) * kWaves + w;
+  if (k >= tasks) return;
+  const uint32_t t = order ? order[k] : k;  // order: a permutation of the tasks
   const uint32_t lane = lane_id();
   const uint32_t row = task_rows[t], label = L.lab[t];
   const uint32_t N = G.N;
@@ -548,6 +567,7 @@ struct RowArgs {
   uint32_t* gout;  // N x R forward graph
   uint32_t* dout;  // N
   unsigned long long* ctr;
+  const uint32_t* order;  // processing order of the rows (a permutation), or nullptr
 };
 
 // Merged candidate list of one row: entry i in lane i % 64, slot i / 64.
@@ -601,9 +621,10 @@ template <int DT, int CPL>
 __global__ __launch_bounds__(kBlock) void k_row(RowSet rs, Graph G, Labels L, RowArgs A) {
   extern __shared__ uint32_t smem[];
   const uint32_t w = wave_index();
-  const uint32_t row = xcd_block(blockIdx.x, gridDim.x) * kWaves + w;
+  const uint32_t k = xcd_block(blockIdx.x, gridDim.x) * kWaves + w;
   const uint32_t N = G.N, R = G.R;
-  if (row >= N) return;
+  if (k >= N) return;
+  const uint32_t row = A.order ? A.order[k] : k;
   const uint32_t lane = lane_id();
   uint32_t* lds = smem + w * kSearchLds;
   const uint32_t lb = L.off[row], le = L.off[row + 1];

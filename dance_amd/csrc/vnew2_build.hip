@@ -324,10 +324,6 @@ static int launch_merge(const Rows& rows, GraphBufs g, const uint32_t* offs, con
   });
 }
 
-// Locality schedule (see k_cells_q / k_cells): order[] = vertices sorted by
-// nearest pivot. Pivots are K evenly spaced rows. K comes from
-// DANCE_LOCALITY_CELLS (default 1024, the fastest c3 build of 256..4096; 0
-// disables the schedule). Uses the reverse-sort buffers as scratch.
 // Alpha schedule (gpu_vamana_alpha_for_iter, vnew2.cu:201-213): iterations
 // from DANCE_ALPHA_FROM_ITER on prune with alpha, earlier ones with 1. The
 // default is the reference's (the last iteration only); 0 is its
@@ -338,17 +334,16 @@ static uint32_t alpha_from_iter() {
   return kIters - 1;
 }
 
+// Locality schedule (see k_cells_q / k_cells): order[] = vertices sorted by
+// nearest pivot. Pivots are K evenly spaced rows. K comes from
+// DANCE_LOCALITY_CELLS (default 1024, the fastest c3 build of 256..4096; 0
+// disables the schedule). Uses the reverse-sort buffers as scratch.
 static uint32_t locality_cells() {
   const char* e = std::getenv("DANCE_LOCALITY_CELLS");
   if (e && e[0]) return (uint32_t)std::strtoul(e, nullptr, 10);
   return 1024;
 }
 
-// Pivot k of K is row floor(k N / K) (evenly spaced).
-static __global__ void k_pivots(uint32_t N, uint32_t K, uint32_t* __restrict__ piv) {
-  const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
-  if (k < K) piv[k] = (uint32_t)(((uint64_t)k * N) / K);
-}
 
 static int build_schedule(const Rows& rows, const QBoundSet& qb, ReverseWs& ws, hipStream_t s,
                           const uint32_t** order_out) {
@@ -374,9 +369,8 @@ static int build_schedule(const Rows& rows, const QBoundSet& qb, ReverseWs& ws, 
     DHIP(hipGetLastError());
   } else {
     DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
-      const uint32_t waves = (N + 7) / 8;
-      hipLaunchKernelGGL((k_cells<decltype(dt)::value, decltype(c)::value>), dim3(wave_grid(waves)), dim3(kBlock), 0,
-                         s, rows.rs, N, dpiv.as<uint32_t>(), K, kb[0], vb[0]);
+      hipLaunchKernelGGL((k_cells<decltype(dt)::value, decltype(c)::value>), dim3(cells_grid(N)),
+                         dim3(kCellsBlock), 0, s, rows.rs, N, dpiv.as<uint32_t>(), K, kb[0], vb[0]);
       DHIP(hipGetLastError());
       return 0;
     }));

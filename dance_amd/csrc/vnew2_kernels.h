@@ -16,6 +16,7 @@
 
 #include <type_traits>
 
+#include "locality.h"
 #include "qbound.h"
 #include "wave.h"
 
@@ -1828,42 +1829,6 @@ __global__ __launch_bounds__(kBlock) void k_init(RowSet rs, GraphBufs g) {
     g.deg_work[node] = deg;
   }
 }
-
-// ---------------------------------------------------------------------------
-// Locality schedule: each vertex's nearest of K pivot rows (one octet per
-// vertex, eight vertices per wave). Vertices sorted by cell make the waves in
-// flight work on neighbouring vertices, whose searches, candidate rows and
-// reverse sources overlap in L2 and the MALL. The schedule only changes the
-// order in which independent vertices are processed, never a result.
-// ---------------------------------------------------------------------------
-template <int DT, int CPL>
-__global__ __launch_bounds__(kBlock) void k_cells(RowSet rs, uint32_t N, const uint32_t* __restrict__ pivots,
-                                                  uint32_t K, uint32_t* __restrict__ cell,
-                                                  uint32_t* __restrict__ vid) {
-  const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;
-  const uint32_t w = wave_index();
-  const uint32_t v = (blockIdx.x * kWavesPerBlock + w) * 8 + grp;
-  if ((blockIdx.x * kWavesPerBlock + w) * 8 >= N) return;
-  const bool act = v < N;
-  uint4 xv[CPL];
-  load_row<CPL>(rs, act ? v : 0u, act, sub, xv);
-  float best = FLT_MAX;
-  uint32_t bi = 0;
-  for (uint32_t k = 0; k < K; ++k) {
-    uint4 pv[CPL];
-    load_row<CPL>(rs, pivots[k], true, sub, pv);
-    const float d = octet_finish<DT, CPL>(rs, sub, xv, pv);
-    if (d < best) {
-      best = d;
-      bi = k;
-    }
-  }
-  if (act && sub == 0) {
-    cell[v] = bi;
-    vid[v] = v;
-  }
-}
-
 
 // Approximate nearest pivot for the locality schedule, from integer codes:
 // one thread per vertex, pivot codes staged in LDS 64 at a time. U8 = false
