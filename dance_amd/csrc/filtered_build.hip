@@ -170,7 +170,9 @@ float ms_between(hipEvent_t a, hipEvent_t b) {
   return 0.f;
 }
 
-uint32_t grid_xcd(uint64_t waves) { return (uint32_t)(((waves + kWaves - 1) / kWaves + 7) / 8 * 8); }
+// Grid of wave-per-item kernels remapped across XCDs (xcd_block): a multiple
+// of 8 workgroups, 2-D beyond 2^32 work-items (grid_dims).
+dim3 grid_xcd(uint64_t waves) { return grid_dims((waves + kWaves - 1) / kWaves, kBlock, 8); }
 uint32_t grid_thr(uint64_t n) { return (uint32_t)((n + 255) / 256); }
 
 void peak_mem(double& peak) {
@@ -414,7 +416,7 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   for (uint32_t round = 0; round < p.rounds; ++round) {
     Graph Ga{N, R, ga, da};
     if (use_sig) {
-      hipLaunchKernelGGL(k_graph_sig, dim3(grid_thr(NR)), dim3(256), 0, s, N, R, static_cast<const uint32_t*>(ga),
+      hipLaunchKernelGGL(k_graph_sig, grid_dims((NR + 255) / 256, 256), dim3(256), 0, s, N, R, static_cast<const uint32_t*>(ga),
                          static_cast<const uint32_t*>(da), st.sig.as<const uint32_t>(), st.gsig.as<uint32_t>());
       DHIP(hipGetLastError());
       Ga.sig = st.gsig.as<const uint32_t>();
@@ -426,7 +428,7 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
     hipEvent_t r0 = E.mark(s);
     if (T > 0) {
       DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
-        hipLaunchKernelGGL((k_task_search<decltype(dt)::value, decltype(c)::value>), dim3(grid_xcd(T)),
+        hipLaunchKernelGGL((k_task_search<decltype(dt)::value, decltype(c)::value>), grid_xcd(T),
                            dim3(kBlock), search_lds, s, rows.rs, Ga, Ld, st.task_rows.as<const uint32_t>(), torder,
                            T, per_label_pool, per_label_keep, p.STEPS, st.tids.as<uint32_t>(), st.td.as<float>(),
                            ctr);
@@ -438,7 +440,7 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
     RowArgs A{ordinary_pool, ordinary_keep, p.STEPS, p.global_start, work_C, per_label_keep, p.alpha,
               st.tids.as<const uint32_t>(), st.td.as<const float>(), gb, db, ctr, rorder};
     DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
-      hipLaunchKernelGGL((k_row<decltype(dt)::value, decltype(c)::value>), dim3(grid_xcd(N)), dim3(kBlock),
+      hipLaunchKernelGGL((k_row<decltype(dt)::value, decltype(c)::value>), grid_xcd(N), dim3(kBlock),
                          search_lds, s, rows.rs, Ga, Ld, A);
       DHIP(hipGetLastError());
       return 0;
@@ -485,7 +487,7 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
         long_done = E.mark(s2);
         if (!long_done) return -1;
       }
-      hipLaunchKernelGGL((k_csr<decltype(dt)::value, decltype(c)::value>), dim3(grid_xcd(N)), dim3(kBlock), csr_lds,
+      hipLaunchKernelGGL((k_csr<decltype(dt)::value, decltype(c)::value>), grid_xcd(N), dim3(kBlock), csr_lds,
                          s, rows.rs, Gb, Ld, Cs);
       DHIP(hipGetLastError());
       if (long_done) DHIP(hipStreamWaitEvent(s, long_done, 0));
@@ -528,7 +530,7 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
     hipEvent_t p0 = E.mark(s);
     PubArgs P{p.alpha, PR, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, gb, db, ctr};
     DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
-      hipLaunchKernelGGL((k_publish<decltype(dt)::value, decltype(c)::value, false>), dim3(grid_xcd(N)),
+      hipLaunchKernelGGL((k_publish<decltype(dt)::value, decltype(c)::value, false>), grid_xcd(N),
                          dim3(kBlock), pub_lds, s, rows.rs, Graph{N, R, ga, da}, Ld, P);
       DHIP(hipGetLastError());
       return 0;
@@ -553,7 +555,7 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
     P = PubArgs{p.alpha, PR, roff, st.rids.as<const uint32_t>(), boff, st.bmask.as<uint32_t>(), st.bd.as<float>(),
                 st.brem.as<uint8_t>(), gb, db, ctr};
     DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
-      hipLaunchKernelGGL((k_publish<decltype(dt)::value, decltype(c)::value, true>), dim3(grid_xcd(N)),
+      hipLaunchKernelGGL((k_publish<decltype(dt)::value, decltype(c)::value, true>), grid_xcd(N),
                          dim3(kBlock), pub_lds, s, rows.rs, Graph{N, PR, gb, db}, Ld, P);
       DHIP(hipGetLastError());
       return 0;

@@ -143,7 +143,7 @@ struct Graph {
 static __global__ void k_graph_sig(uint32_t N, uint32_t R, const uint32_t* __restrict__ g,
                                    const uint32_t* __restrict__ d, const uint32_t* __restrict__ sig,
                                    uint32_t* __restrict__ out) {
-  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t t = (uint64_t)grid_block() * blockDim.x + threadIdx.x;
   if (t >= (uint64_t)N * R) return;
   const uint32_t r = (uint32_t)(t / R), i = (uint32_t)(t % R);
   const uint32_t id = g[t];
@@ -526,7 +526,7 @@ __global__ __launch_bounds__(kBlock) void k_task_search(RowSet rs, Graph G, Labe
                                                         float* out_d, unsigned long long* ctr) {
   extern __shared__ uint32_t smem[];
   const uint32_t w = wave_index();
-  const uint32_t k = xcd_block(blockIdx.x, gridDim.x) * kWaves + w;
+  const uint32_t k = xcd_block(grid_block(), grid_blocks()) * kWaves + w;
   if (k >= tasks) return;
   const uint32_t t = order ? order[k] : k;  // order: a permutation of the tasks
   const uint32_t lane = lane_id();
@@ -621,7 +621,7 @@ template <int DT, int CPL>
 __global__ __launch_bounds__(kBlock) void k_row(RowSet rs, Graph G, Labels L, RowArgs A) {
   extern __shared__ uint32_t smem[];
   const uint32_t w = wave_index();
-  const uint32_t k = xcd_block(blockIdx.x, gridDim.x) * kWaves + w;
+  const uint32_t k = xcd_block(grid_block(), grid_blocks()) * kWaves + w;
   const uint32_t N = G.N, R = G.R;
   if (k >= N) return;
   const uint32_t row = A.order ? A.order[k] : k;
@@ -852,7 +852,7 @@ template <int DT, int CPL>
 __global__ __launch_bounds__(kBlock) void k_csr(RowSet rs, Graph G, Labels L, CsrArgs A) {
   extern __shared__ uint32_t smem[];
   const uint32_t w = wave_index();
-  const uint32_t row = xcd_block(blockIdx.x, gridDim.x) * kWaves + w;
+  const uint32_t row = xcd_block(grid_block(), grid_blocks()) * kWaves + w;
   const uint32_t N = G.N, R = G.R;
   if (row >= N) return;
   const uint32_t lane = lane_id();
@@ -1214,7 +1214,7 @@ template <int DT, int CPL, bool REV>
 __global__ __launch_bounds__(kBlock) void k_publish(RowSet rs, Graph G, Labels L, PubArgs A) {
   extern __shared__ uint32_t smem[];
   const uint32_t w = wave_index();
-  const uint32_t row = xcd_block(blockIdx.x, gridDim.x) * kWaves + w;
+  const uint32_t row = xcd_block(grid_block(), grid_blocks()) * kWaves + w;
   const uint32_t N = G.N;
   if (row >= N) return;
   const uint32_t lane = lane_id();

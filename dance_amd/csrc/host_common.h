@@ -46,6 +46,16 @@ inline bool verbose() {
 inline uint32_t elem_bytes(int dtype) { return dtype == DANCE_F32 ? 4u : dtype == DANCE_F16 ? 2u : 1u; }
 
 // Smallest compiled chunks-per-lane count covering nch chunks.
+// Grid of at least `blocks` workgroups of `threads` work-items, rounded up
+// to a multiple of `mult` (8 for xcd_block): 1-D while it holds fewer than
+// 2^32 work-items, else 2^20 x gy (kernels index with grid_block()).
+inline dim3 grid_dims(uint64_t blocks, uint32_t threads, uint32_t mult = 1) {
+  blocks = (blocks + mult - 1) / mult * mult;
+  if (blocks * threads < (1ull << 32)) return dim3((uint32_t)std::max<uint64_t>(blocks, 1));
+  const uint64_t gx = 1ull << 20;
+  return dim3((uint32_t)gx, (uint32_t)((blocks + gx - 1) / gx));
+}
+
 inline int pick_cpl(uint32_t nch) {
   const uint32_t need = (nch + 7u) / 8u;
   static const int opts[] = {1, 2, 3, 4, 8, 16};

@@ -83,7 +83,7 @@ struct ExpandArgs {
 // One wave per shard row. FILL = false counts, FILL = true writes targets.
 template <bool FILL>
 __global__ __launch_bounds__(kBlock) void k_expand(ExpandArgs a) {
-  const uint32_t row = blockIdx.x * kWaves + wave_index();
+  const uint32_t row = grid_block() * kWaves + wave_index();
   if (row >= a.nrows) return;
   const uint32_t lane = lane_id();
   const uint32_t off = a.row_off[row];
@@ -147,7 +147,7 @@ __global__ __launch_bounds__(kBlock) void k_rank(const uint32_t* __restrict__ of
                                                  uint32_t* __restrict__ long_count) {
   __shared__ uint64_t lds[kWaves * kBuf];
   const uint32_t w = wave_index();
-  const uint32_t s = blockIdx.x * kWaves + w;
+  const uint32_t s = grid_block() * kWaves + w;
   if (s >= nodes) return;
   const uint32_t lane = lane_id();
   const uint32_t begin = offs[s], len = offs[s + 1] - begin;
@@ -201,7 +201,7 @@ __global__ __launch_bounds__(kBlock) void k_long_gather(const uint32_t* __restri
                                                         const uint32_t* __restrict__ loff, uint32_t nlong,
                                                         uint32_t* __restrict__ ldst, uint32_t* __restrict__ lord,
                                                         uint32_t* __restrict__ keys, uint32_t* __restrict__ idx) {
-  const uint32_t k = blockIdx.x * kWaves + wave_index();
+  const uint32_t k = grid_block() * kWaves + wave_index();
   if (k >= nlong) return;
   const uint32_t s = list[k];
   const uint32_t begin = offs[s], len = offs[s + 1] - begin, o = loff[k];
@@ -240,7 +240,7 @@ __global__ __launch_bounds__(kBlock) void k_long_select(const uint32_t* __restri
                                                         const uint32_t* __restrict__ idx,
                                                         const uint32_t* __restrict__ ldst, uint32_t K,
                                                         uint32_t* __restrict__ deg, uint32_t* __restrict__ uniq) {
-  const uint32_t k = blockIdx.x * kWaves + wave_index();
+  const uint32_t k = grid_block() * kWaves + wave_index();
   if (k >= nlong) return;
   const uint32_t lane = lane_id();
   const uint32_t s = list[k];
@@ -273,7 +273,7 @@ __global__ void k_row_words(const uint32_t* __restrict__ deg, uint32_t nodes, ui
 __global__ __launch_bounds__(kBlock) void k_pack(const uint32_t* __restrict__ offs, const uint32_t* __restrict__ seg,
                                                  const uint32_t* __restrict__ deg, const uint32_t* __restrict__ pos,
                                                  uint32_t nodes, uint32_t* __restrict__ body) {
-  const uint32_t s = blockIdx.x * kWaves + wave_index();
+  const uint32_t s = grid_block() * kWaves + wave_index();
   if (s >= nodes) return;
   const uint32_t lane = lane_id();
   const uint32_t d = deg[s], p = pos[s], o = offs[s];
@@ -561,9 +561,9 @@ static int run_merge(const std::string& vamana_prefix, const std::string& vamana
                    fill ? d_cur.as<uint32_t>() : d_cnt.as<uint32_t>(), d_seg.as<uint32_t>(),
                    d_flags.as<uint32_t>(), d_loops.as<unsigned long long>()};
       if (fill)
-        hipLaunchKernelGGL(k_expand<true>, dim3(blocks_for(n, kWaves)), dim3(kBlock), 0, st, a);
+        hipLaunchKernelGGL(k_expand<true>, grid_dims(blocks_for(n, kWaves), kBlock), dim3(kBlock), 0, st, a);
       else
-        hipLaunchKernelGGL(k_expand<false>, dim3(blocks_for(n, kWaves)), dim3(kBlock), 0, st, a);
+        hipLaunchKernelGGL(k_expand<false>, grid_dims(blocks_for(n, kWaves), kBlock), dim3(kBlock), 0, st, a);
       DHIP(hipGetLastError());
       if (!resident) DHIP(hipStreamSynchronize(st));  // the staging buffers are reused by the next shard
     }
@@ -625,7 +625,7 @@ static int run_merge(const std::string& vamana_prefix, const std::string& vamana
     DCHECK(expand_pass(true, lo, hi));
     DHIP(hipMemsetAsync(d_flags.p, 0, 8, st));
     uint32_t* long_count = d_flags.as<uint32_t>() + 1;
-    hipLaunchKernelGGL(k_rank, dim3(blocks_for(nodes, kWaves)), dim3(kBlock), 0, st, d_cnt.as<uint32_t>(),
+    hipLaunchKernelGGL(k_rank, grid_dims(blocks_for(nodes, kWaves), kBlock), dim3(kBlock), 0, st, d_cnt.as<uint32_t>(),
                        d_seg.as<uint32_t>(), nodes, lo, K, seed, d_deg.as<uint32_t>(), d_uniq.as<uint32_t>(),
                        d_long.as<uint32_t>(), long_count);
     DHIP(hipGetLastError());
@@ -655,7 +655,7 @@ static int run_merge(const std::string& vamana_prefix, const std::string& vamana
       DHIP(hipMemcpyAsync(d_loff.p, loff.data(), 4ull * (nlong + 1), hipMemcpyHostToDevice, st));
       uint32_t* keys[2] = {kb0.as<uint32_t>(), kb1.as<uint32_t>()};
       uint32_t* vals[2] = {vb0.as<uint32_t>(), vb1.as<uint32_t>()};
-      hipLaunchKernelGGL(k_long_gather, dim3(blocks_for(nlong, kWaves)), dim3(kBlock), 0, st,
+      hipLaunchKernelGGL(k_long_gather, grid_dims(blocks_for(nlong, kWaves), kBlock), dim3(kBlock), 0, st,
                          d_cnt.as<uint32_t>(), d_seg.as<uint32_t>(), d_list.as<uint32_t>(),
                          d_loff.as<uint32_t>(), nlong, d_ldst.as<uint32_t>(), d_lord.as<uint32_t>(), keys[0],
                          vals[0]);
@@ -683,7 +683,7 @@ static int run_merge(const std::string& vamana_prefix, const std::string& vamana
         std::swap(keys[0], keys[1]);
         std::swap(vals[0], vals[1]);
       }
-      hipLaunchKernelGGL(k_long_select, dim3(blocks_for(nlong, kWaves)), dim3(kBlock), 0, st,
+      hipLaunchKernelGGL(k_long_select, grid_dims(blocks_for(nlong, kWaves), kBlock), dim3(kBlock), 0, st,
                          d_cnt.as<uint32_t>(), d_seg.as<uint32_t>(), d_list.as<uint32_t>(),
                          d_loff.as<uint32_t>(), nlong, vals[0], d_ldst.as<uint32_t>(), K, d_deg.as<uint32_t>(),
                          d_uniq.as<uint32_t>());
@@ -694,7 +694,7 @@ static int run_merge(const std::string& vamana_prefix, const std::string& vamana
                        d_deg.as<uint32_t>(), nodes, d_pos.as<uint32_t>());
     DHIP(hipGetLastError());
     DCHECK(scan_exclusive(d_pos.as<uint32_t>(), (size_t)nodes + 1, scan_ws, st));
-    hipLaunchKernelGGL(k_pack, dim3(blocks_for(nodes, kWaves)), dim3(kBlock), 0, st, d_cnt.as<uint32_t>(),
+    hipLaunchKernelGGL(k_pack, grid_dims(blocks_for(nodes, kWaves), kBlock), dim3(kBlock), 0, st, d_cnt.as<uint32_t>(),
                        d_seg.as<uint32_t>(), d_deg.as<uint32_t>(), d_pos.as<uint32_t>(), nodes,
                        d_body.as<uint32_t>());
     DHIP(hipGetLastError());

@@ -16,7 +16,7 @@ namespace dance {
 template <typename SrcT, typename DstT>
 __global__ void k_gather_rows(const SrcT* __restrict__ src, uint32_t dim, const uint32_t* __restrict__ ids, uint32_t m,
                               DstT* __restrict__ dst, uint32_t dst_elems_per_row) {
-  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t t = (uint64_t)grid_block() * blockDim.x + threadIdx.x;
   if (t >= (uint64_t)m * dst_elems_per_row) return;
   const uint32_t r = (uint32_t)(t / dst_elems_per_row), e = (uint32_t)(t % dst_elems_per_row);
   DstT v = (DstT)0;
@@ -25,7 +25,7 @@ __global__ void k_gather_rows(const SrcT* __restrict__ src, uint32_t dim, const 
 }
 
 __global__ void k_fill_u32(uint32_t* __restrict__ p, uint64_t n, uint32_t v) {
-  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t t = (uint64_t)grid_block() * blockDim.x + threadIdx.x;
   if (t < n) p[t] = v;
 }
 
@@ -54,7 +54,7 @@ __global__ __launch_bounds__(64 * kRemapWaves) void k_stitch_remap(RemapArgs a) 
   __shared__ uint32_t s_row[kRemapWaves][256];
   __shared__ uint32_t s_new[kRemapWaves][64];
   const uint32_t w = wave_index(), lane = lane_id();
-  const uint32_t i = blockIdx.x * kRemapWaves + w;
+  const uint32_t i = grid_block() * kRemapWaves + w;
   if (i >= a.m) return;
   const uint32_t me = a.ids[i];
   const uint32_t deg = min(min(a.local_deg[i], a.take), a.Rs);

@@ -124,8 +124,9 @@ struct State {
 static uint32_t round64(uint32_t x) { return (x + 63u) / 64u * 64u; }
 
 static uint32_t wave_grid(uint32_t n) { return (n + kWavesPerBlock - 1) / kWavesPerBlock; }
-// Grid for kernels that remap workgroups across XCDs (xcd_block): a multiple of 8.
-static uint32_t xcd_grid(uint32_t n) { return (wave_grid(n) + 7u) / 8u * 8u; }
+// Grid for kernels that remap workgroups across XCDs (xcd_block): a multiple
+// of 8 workgroups, 2-D beyond 2^32 work-items (grid_dims).
+static dim3 xcd_grid(uint32_t n) { return grid_dims(wave_grid(n), kBlock, 8); }
 
 static int launch_medoid(const Rows& rows, hipStream_t s, float* d_scores, uint32_t* d_cands, uint32_t nc,
                          uint32_t ns) {
@@ -141,7 +142,7 @@ static int launch_medoid(const Rows& rows, hipStream_t s, float* d_scores, uint3
 static int launch_init(const Rows& rows, GraphBufs g, hipStream_t s) {
   const int cpl = pick_cpl(rows.rs.nch);
   return with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
-    hipLaunchKernelGGL((k_init<decltype(dt)::value, decltype(c)::value>), dim3(wave_grid(g.N)), dim3(kBlock), 0, s,
+    hipLaunchKernelGGL((k_init<decltype(dt)::value, decltype(c)::value>), grid_dims(wave_grid(g.N), kBlock), dim3(kBlock), 0, s,
                        rows.rs, g);
     DHIP(hipGetLastError());
     return 0;
@@ -208,17 +209,17 @@ static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t ste
     if constexpr (kHasQB) {
       if (qb.rows) {
         if (L <= 128)
-          hipLaunchKernelGGL((k_search<DT, CPL, 2, true>), dim3(xcd_grid(g.N)), dim3(kBlock), lds, s, a, Cp);
+          hipLaunchKernelGGL((k_search<DT, CPL, 2, true>), xcd_grid(g.N), dim3(kBlock), lds, s, a, Cp);
         else
-          hipLaunchKernelGGL((k_search<DT, CPL, 4, true>), dim3(xcd_grid(g.N)), dim3(kBlock), lds, s, a, Cp);
+          hipLaunchKernelGGL((k_search<DT, CPL, 4, true>), xcd_grid(g.N), dim3(kBlock), lds, s, a, Cp);
         DHIP(hipGetLastError());
         return 0;
       }
     }
     if (L <= 128)
-      hipLaunchKernelGGL((k_search<DT, CPL, 2, false>), dim3(xcd_grid(g.N)), dim3(kBlock), lds, s, a, Cp);
+      hipLaunchKernelGGL((k_search<DT, CPL, 2, false>), xcd_grid(g.N), dim3(kBlock), lds, s, a, Cp);
     else
-      hipLaunchKernelGGL((k_search<DT, CPL, 4, false>), dim3(xcd_grid(g.N)), dim3(kBlock), lds, s, a, Cp);
+      hipLaunchKernelGGL((k_search<DT, CPL, 4, false>), xcd_grid(g.N), dim3(kBlock), lds, s, a, Cp);
     DHIP(hipGetLastError());
     return 0;
   });
@@ -247,7 +248,7 @@ static int launch_prune(const Rows& rows, GraphBufs g, uint32_t min_degree, floa
     if (rank) {
       if constexpr (kHasQB) {
         if (qb.rows) {
-          hipLaunchKernelGGL((k_prune_rank<DT, CPL, true>), dim3(xcd_grid(g.N)), dim3(kBlock),
+          hipLaunchKernelGGL((k_prune_rank<DT, CPL, true>), xcd_grid(g.N), dim3(kBlock),
                              (size_t)kWavesPerBlock * prune_rank_lds_words(Cq, true) * 4, s, a, Cq);
           DHIP(hipGetLastError());
           return 0;
@@ -255,69 +256,161 @@ static int launch_prune(const Rows& rows, GraphBufs g, uint32_t min_degree, floa
       }
       // without code rows the bound is off: the kernel tests every pair exactly
       a.qb = QBoundSet{nullptr, 0.0f, 0.0f};
-      hipLaunchKernelGGL((k_prune_rank<DT, CPL, false>), dim3(xcd_grid(g.N)), dim3(kBlock),
+      hipLaunchKernelGGL((k_prune_rank<DT, CPL, false>), xcd_grid(g.N), dim3(kBlock),
                          (size_t)kWavesPerBlock * prune_rank_lds_words(Cq, false) * 4, s, a, Cq);
       DHIP(hipGetLastError());
       return 0;
     }
-    hipLaunchKernelGGL((k_prune<DT, CPL>), dim3(xcd_grid(g.N)), dim3(kBlock),
+    hipLaunchKernelGGL((k_prune<DT, CPL>), xcd_grid(g.N), dim3(kBlock),
                        (size_t)kWavesPerBlock * prune_lds_words(Cp, Rp) * 4, s, a, Cp, Rp);
     DHIP(hipGetLastError());
     return 0;
   });
 }
 
+// The reverse sort's items (forward slots) per part: below 2^32, so that
+// its items and offsets stay 32-bit. Graphs with more slots are sorted in
+// parts of whole sources (k_wide_gather). DANCE_REVERSE_PART_ITEMS lowers the
+// cap so that tests run the split path on small graphs; results are equal.
+static size_t reverse_part_cap(uint32_t R) {
+  size_t cap = 0xFFFFFFFFull;
+  const char* e = std::getenv("DANCE_REVERSE_PART_ITEMS");
+  if (e && e[0]) {
+    const size_t v = (size_t)std::strtoull(e, nullptr, 10);
+    if (v > 0 && v < cap) cap = v;
+  }
+  return std::max<size_t>(cap, std::max(R, 1u));
+}
+// Parts (1: one sort over every slot) and sources per part.
+static void reverse_parts(uint32_t N, uint32_t R, uint32_t* parts, uint32_t* per) {
+  const size_t items = (size_t)N * R, cap = reverse_part_cap(R);
+  if (items <= cap) {
+    *parts = 1;
+    *per = N;
+    return;
+  }
+  size_t np = (items + cap - 1) / cap;
+  size_t ps = (N + np - 1) / np;
+  while (ps * R > cap) {
+    ++np;
+    ps = (N + np - 1) / np;
+  }
+  *per = (uint32_t)ps;
+  *parts = (uint32_t)((N + ps - 1) / ps);
+}
+
 struct ReverseWs {
   DevBuf keys[2], vals[2], offs, order, snap;
   SortWorkspace sort;
   ScanWorkspace scan;
+  // split sort (graphs of 2^32 or more slots)
+  uint32_t parts = 1, per = 0;
+  DevBuf pvals, poffs, offs64, src_sorted, snap_sorted;
   int alloc(uint32_t N, uint32_t R) {
     const size_t items = (size_t)N * R;
+    reverse_parts(N, R, &parts, &per);
+    // the locality schedule sorts N items in these buffers first
+    const size_t sort_items = std::max<size_t>(parts == 1 ? items : (size_t)per * R, std::max(N, 1u));
     for (int i = 0; i < 2; ++i) {
-      DCHECK(keys[i].alloc(std::max<size_t>(items, 1) * 4));
-      DCHECK(vals[i].alloc(std::max<size_t>(items, 1) * 4));
+      DCHECK(keys[i].alloc(sort_items * 4));
+      DCHECK(vals[i].alloc(sort_items * 4));
     }
     DCHECK(snap.alloc(std::max<size_t>(items, 1) * 4));
     DCHECK(offs.alloc(((size_t)N + 1) * 4));
+    if (parts > 1) {
+      DCHECK(pvals.alloc(items * 4));
+      DCHECK(poffs.alloc((size_t)parts * ((size_t)N + 1) * 4));
+      DCHECK(offs64.alloc(((size_t)N + 1) * 8));
+      DCHECK(src_sorted.alloc(items * 4));
+      DCHECK(snap_sorted.alloc(items * 4));
+    }
     return 0;
   }
 };
 
-// Reverse CSR in canonical (ascending source) order. Returns the sorted
-// forward slots (s*R + i) through *srcs_out; ws.snap holds their distances.
-static int build_reverse_csr(GraphBufs g, ReverseWs& ws, hipStream_t s, const uint32_t** srcs_out) {
+// The reverse CSR as the merge reads it (MergeArgs: offsets, srcs, snap,
+// offsets64).
+struct RevCsr {
+  const uint32_t* offs;
+  const uint32_t* srcs;
+  const float* snap;
+  const uint64_t* offs64;
+};
+
+// Reverse CSR in canonical (ascending source) order. One sort: srcs are the
+// sorted forward slots (s*R + i) and snap their distances by slot. Split sort:
+// srcs and snap hold each sorted position's source and distance, offs64 the
+// 64-bit offsets.
+static int build_reverse_csr(GraphBufs g, ReverseWs& ws, hipStream_t s, RevCsr* out) {
   const size_t items = (size_t)g.N * g.R;
-  if (items > 0) {
-    hipLaunchKernelGGL(k_rev_keys, dim3((uint32_t)((items + 255) / 256)), dim3(256), 0, s, g.work, g.deg_work, g.wd,
-                       g.N, g.R, g.C, ws.keys[0].as<uint32_t>(), ws.vals[0].as<uint32_t>(), ws.snap.as<float>());
-    DHIP(hipGetLastError());
-  }
   uint32_t* kb[2] = {ws.keys[0].as<uint32_t>(), ws.keys[1].as<uint32_t>()};
   uint32_t* vb[2] = {ws.vals[0].as<uint32_t>(), ws.vals[1].as<uint32_t>()};
-  int which = 0;
-  DCHECK(radix_sort_pairs(kb, vb, items, bit_length(g.N), ws.sort, s, &which));
-  hipLaunchKernelGGL(k_seg_offsets, dim3((uint32_t)((items + 1 + 255) / 256)), dim3(256), 0, s, kb[which], items, g.N,
-                     ws.offs.as<uint32_t>());
+  if (ws.parts == 1) {
+    if (items > 0) {
+      hipLaunchKernelGGL(k_rev_keys, dim3((uint32_t)((items + 255) / 256)), dim3(256), 0, s, g.work, g.deg_work,
+                         g.wd, g.N, g.R, g.C, 0u, items, kb[0], vb[0], ws.snap.as<float>());
+      DHIP(hipGetLastError());
+    }
+    int which = 0;
+    DCHECK(radix_sort_pairs(kb, vb, items, bit_length(g.N), ws.sort, s, &which));
+    hipLaunchKernelGGL(k_seg_offsets, dim3((uint32_t)((items + 1 + 255) / 256)), dim3(256), 0, s, kb[which], items,
+                       g.N, ws.offs.as<uint32_t>());
+    DHIP(hipGetLastError());
+    *out = RevCsr{ws.offs.as<const uint32_t>(), vb[which], ws.snap.as<const float>(), nullptr};
+    return 0;
+  }
+  if (ws.parts > kMaxRevParts) {
+    std::fprintf(stderr, "[gpu_vamana_build] N*R=%zu needs %u reverse parts, above %u\n", items, ws.parts,
+                 kMaxRevParts);
+    return -1;
+  }
+  WideParts wp{};
+  wp.P = ws.parts;
+  size_t base = 0;
+  for (uint32_t p = 0; p < ws.parts; ++p) {
+    const uint32_t s_lo = p * ws.per, s_hi = std::min(g.N, s_lo + ws.per);
+    const size_t items_p = (size_t)(s_hi - s_lo) * g.R;
+    wp.s_lo[p] = s_lo;
+    wp.vbase[p] = base;
+    hipLaunchKernelGGL(k_rev_keys, dim3((uint32_t)((items_p + 255) / 256)), dim3(256), 0, s, g.work, g.deg_work,
+                       g.wd, g.N, g.R, g.C, s_lo, items_p, kb[0], vb[0], ws.snap.as<float>());
+    DHIP(hipGetLastError());
+    int which = 0;
+    DCHECK(radix_sort_pairs(kb, vb, items_p, bit_length(g.N), ws.sort, s, &which));
+    hipLaunchKernelGGL(k_seg_offsets, dim3((uint32_t)((items_p + 1 + 255) / 256)), dim3(256), 0, s, kb[which],
+                       items_p, g.N, ws.poffs.as<uint32_t>() + (size_t)p * ((size_t)g.N + 1));
+    DHIP(hipGetLastError());
+    DHIP(hipMemcpyAsync(ws.pvals.as<uint32_t>() + base, vb[which], items_p * 4, hipMemcpyDeviceToDevice, s));
+    base += items_p;
+  }
+  hipLaunchKernelGGL(k_wide_offsets, dim3((g.N + 1 + 255) / 256), dim3(256), 0, s, g.N, wp,
+                     ws.poffs.as<const uint32_t>(), ws.offs64.as<uint64_t>());
   DHIP(hipGetLastError());
-  *srcs_out = vb[which];
+  hipLaunchKernelGGL(k_wide_gather, grid_dims(((uint64_t)g.N + 3) / 4, 256), dim3(256), 0, s, g.N, g.R, wp, ws.poffs.as<const uint32_t>(),
+                     ws.pvals.as<const uint32_t>(), ws.snap.as<const float>(), ws.offs64.as<const uint64_t>(),
+                     ws.src_sorted.as<uint32_t>(), ws.snap_sorted.as<float>());
+  DHIP(hipGetLastError());
+  *out = RevCsr{nullptr, ws.src_sorted.as<const uint32_t>(), ws.snap_sorted.as<const float>(),
+                ws.offs64.as<const uint64_t>()};
   return 0;
 }
 
-static int launch_merge(const Rows& rows, GraphBufs g, const uint32_t* offs, const uint32_t* srcs, const float* snap,
-                        const Profile& prof, const uint32_t* order, VCounters* ctr, hipStream_t s) {
+static int launch_merge(const Rows& rows, GraphBufs g, const RevCsr& rev, const Profile& prof, const uint32_t* order,
+                        VCounters* ctr, hipStream_t s) {
   const int cpl = pick_cpl(rows.rs.nch);
   const uint32_t Cp = round64(g.C);
-  MergeArgs a{rows.rs, g, offs, srcs, snap, prof.heavy_threshold, prof.heavy_sample, order, ctr};
+  MergeArgs a{rows.rs, g, rev.offs, rev.srcs, rev.snap, prof.heavy_threshold, prof.heavy_sample, order, ctr,
+              rev.offs64};
   return with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
     constexpr int DT = decltype(dt)::value, CPL = decltype(c)::value;
     if (g.C <= 64)
-      hipLaunchKernelGGL((k_merge_reg<DT, CPL, 1>), dim3(xcd_grid(g.N)), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((k_merge_reg<DT, CPL, 1>), xcd_grid(g.N), dim3(kBlock), 0, s, a);
     else if (g.C <= 128)
-      hipLaunchKernelGGL((k_merge_reg<DT, CPL, 2>), dim3(xcd_grid(g.N)), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((k_merge_reg<DT, CPL, 2>), xcd_grid(g.N), dim3(kBlock), 0, s, a);
     else if (g.C <= 256)
-      hipLaunchKernelGGL((k_merge_reg<DT, CPL, 4>), dim3(xcd_grid(g.N)), dim3(kBlock), 0, s, a);
+      hipLaunchKernelGGL((k_merge_reg<DT, CPL, 4>), xcd_grid(g.N), dim3(kBlock), 0, s, a);
     else
-      hipLaunchKernelGGL((k_merge<DT, CPL>), dim3(xcd_grid(g.N)), dim3(kBlock),
+      hipLaunchKernelGGL((k_merge<DT, CPL>), xcd_grid(g.N), dim3(kBlock),
                          (size_t)kWavesPerBlock * merge_lds_words(Cp) * 4, s, a, Cp);
     DHIP(hipGetLastError());
     return 0;
@@ -446,9 +539,11 @@ static int validate(uint32_t N, uint32_t dim, uint32_t R, uint32_t L, uint32_t C
     std::fprintf(stderr, "[gpu_vamana_build] L=%u exceeds the supported maximum 256\n", L);
     return -1;
   }
-  if ((uint64_t)N * R > 0xFFFFFFFFull) {
-    std::fprintf(stderr, "[gpu_vamana_build] N*R=%llu exceeds 2^32 reverse edges\n",
-                 (unsigned long long)N * R);
+  uint32_t parts = 1, per = 0;
+  reverse_parts(N, R, &parts, &per);
+  if (parts > kMaxRevParts) {
+    std::fprintf(stderr, "[gpu_vamana_build] N*R=%llu exceeds %u reverse-sort parts of 2^32 - 1 slots\n",
+                 (unsigned long long)N * R, kMaxRevParts);
     return -1;
   }
   return 0;
@@ -536,10 +631,10 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     const QBoundSet qb_it = ((q_iters >> it) & 1u) ? qb : QBoundSet{nullptr, 0.0f, 0.0f};
     DCHECK(launch_search(rows, g, L, steps, alpha, start, order, ctr, qb_it, s));
     DCHECK(record(iev[it].s1, s));
-    const uint32_t* srcs = nullptr;
-    DCHECK(build_reverse_csr(g, rws, s, &srcs));
+    RevCsr rev{};
+    DCHECK(build_reverse_csr(g, rws, s, &rev));
     DCHECK(record(iev[it].r1, s));
-    DCHECK(launch_merge(rows, g, rws.offs.as<uint32_t>(), srcs, rws.snap.as<float>(), prof, order, ctr, s));
+    DCHECK(launch_merge(rows, g, rev, prof, order, ctr, s));
     DCHECK(record(iev[it].m1, s));
     const uint32_t md = (it + 1 == kIters) ? kFinalMinDegree : 0u;
     const QBoundSet qp_it = ((q_prune_iters >> it) & 1u) ? qb : QBoundSet{nullptr, 0.0f, 0.0f};
@@ -871,18 +966,29 @@ static size_t resident_build_bytes(const void* d_data, int dtype, int store, uin
   if (!rows_ready && !(dtype == store && stride == row_bytes && (reinterpret_cast<uintptr_t>(d_data) & 15u) == 0))
     add(stride * N);  // padded or converted rows
   const size_t items = std::max<size_t>((size_t)N * R, 1);
+  uint32_t parts = 1, per = 0;
+  reverse_parts(N, R, &parts, &per);
+  const size_t sort_items = std::max<size_t>(parts == 1 ? items : (size_t)per * R, std::max(N, 1u));
   add((size_t)N * 4);               // deg_work
   add((size_t)N * C * 4);           // work
   add((size_t)N * C * 4);           // wd
-  for (int i = 0; i < 5; ++i) add(items * 4);  // keys[2], vals[2], snap
+  for (int i = 0; i < 4; ++i) add(sort_items * 4);  // keys[2], vals[2]
+  add(items * 4);                   // snap
   add(((size_t)N + 1) * 4);         // offs
+  if (parts > 1) {                  // split sort
+    add(items * 4);                 // pvals
+    add((size_t)parts * ((size_t)N + 1) * 4);
+    add(((size_t)N + 1) * 8);       // offs64
+    add(items * 4);                 // src_sorted
+    add(items * 4);                 // snap_sorted
+  }
   add(sizeof(VCounters) * kCtrStripes);
   add(kMedoidCandidates * 4);       // scores
   add(kMedoidCandidates * 4);       // cands
   add((size_t)N * kQChunks * 16);   // code rows of the bound
   add((size_t)std::min(locality_cells(), N) * 4);  // pivots
   add((size_t)N * 4);               // order
-  for (size_t n : {(size_t)N, items}) {  // the schedule's sort, then the reverse sort
+  for (size_t n : {(size_t)N, sort_items}) {  // the schedule's sort, then the reverse sort
     const size_t tiles = (n + kRadixTile - 1) / kRadixTile;
     add(tiles * 256 * 4);           // histograms
     size_t levels = 0, m = tiles * 256;
@@ -987,7 +1093,7 @@ static int gather_label_rows(const void* src, int dtype, int store, uint32_t dim
                              uint32_t stride_elems, void* dst, hipStream_t s) {
   const uint64_t total = (uint64_t)m * stride_elems;
   if (total == 0) return 0;
-  const dim3 grid((uint32_t)((total + 255) / 256)), block(256);
+  const dim3 grid = grid_dims((total + 255) / 256, 256), block(256);
   if (dtype == DANCE_F32 && store == DANCE_F32)
     hipLaunchKernelGGL((k_gather_rows<float, float>), grid, block, 0, s, static_cast<const float*>(src), dim, d_ids, m,
                        static_cast<float*>(dst), stride_elems);
@@ -1091,7 +1197,7 @@ static int stitched_build(const StitchedIn& in) {
     gg = d_graph.as<uint32_t>();
     gd = d_deg.as<uint32_t>();
   }
-  hipLaunchKernelGGL(k_fill_u32, dim3((uint32_t)((gcells + 255) / 256)), dim3(256), 0, s, gg, (uint64_t)gcells,
+  hipLaunchKernelGGL(k_fill_u32, grid_dims(((uint64_t)gcells + 255) / 256, 256), dim3(256), 0, s, gg, (uint64_t)gcells,
                      DANCE_INV);
   hipLaunchKernelGGL(k_fill_u32, dim3((in.N + 255) / 256), dim3(256), 0, s, gd, (uint64_t)in.N, 0u);
   DCHECK(d_ctr.alloc(3 * 8));
@@ -1151,7 +1257,8 @@ static int stitched_build(const StitchedIn& in) {
     st.build_max_seconds = std::max(st.build_max_seconds, tr - tb);
     RemapArgs ra{lst.cur.as<uint32_t>(), lst.deg_cur.as<uint32_t>(), ids, m, in.Rs, in.Rout, gg, gd, in.row_cap,
                  d_ctr.as<unsigned long long>()};
-    hipLaunchKernelGGL(k_stitch_remap, dim3((m + kRemapWaves - 1) / kRemapWaves), dim3(64 * kRemapWaves), 0, s, ra);
+    hipLaunchKernelGGL(k_stitch_remap, grid_dims(((uint64_t)m + kRemapWaves - 1) / kRemapWaves, 64 * kRemapWaves),
+                       dim3(64 * kRemapWaves), 0, s, ra);
     DHIP(hipGetLastError());
     DHIP(hipStreamSynchronize(s));
     st.remap_seconds += now_sec() - tr;
@@ -1428,20 +1535,28 @@ int dance_stage_reverse_merge(const void* h_data, int dtype, uint32_t N, uint32_
   DCHECK(upload_state(cx.st, N, R, C, nullptr, nullptr, work, deg_work, wd, cx.s));
   ReverseWs rws;
   DCHECK(rws.alloc(N, R));
-  const uint32_t* srcs = nullptr;
   GraphBufs g = cx.st.g();
-  DCHECK(build_reverse_csr(g, rws, cx.s, &srcs));
+  RevCsr rev{};
+  DCHECK(build_reverse_csr(g, rws, cx.s, &rev));
   std::vector<uint32_t> off((size_t)N + 1);
-  DCHECK(down(off.data(), rws.offs.p, ((size_t)N + 1) * 4, cx.s));
-  DHIP(hipStreamSynchronize(cx.s));
+  if (rev.offs64) {  // split sort: 64-bit offsets, srcs already sources
+    std::vector<uint64_t> off64((size_t)N + 1);
+    DCHECK(down(off64.data(), rev.offs64, ((size_t)N + 1) * 8, cx.s));
+    DHIP(hipStreamSynchronize(cx.s));
+    for (size_t t = 0; t <= N; ++t) off[t] = (uint32_t)off64[t];
+  } else {
+    DCHECK(down(off.data(), rev.offs, ((size_t)N + 1) * 4, cx.s));
+    DHIP(hipStreamSynchronize(cx.s));
+  }
   if (offsets) std::memcpy(offsets, off.data(), off.size() * 4);
   if (ids) {
-    DCHECK(down(ids, srcs, (size_t)off[N] * 4, cx.s));
+    DCHECK(down(ids, rev.srcs, (size_t)off[N] * 4, cx.s));
     DHIP(hipStreamSynchronize(cx.s));
-    for (uint32_t e = 0; e < off[N]; ++e) ids[e] /= R;  // forward slot -> source
+    if (!rev.offs64)
+      for (uint32_t e = 0; e < off[N]; ++e) ids[e] /= R;  // forward slot -> source
   }
   Profile prof{"stage", false, heavy_threshold, heavy_sample};
-  DCHECK(launch_merge(cx.rows, g, rws.offs.as<uint32_t>(), srcs, rws.snap.as<float>(), prof, nullptr, nullptr, cx.s));
+  DCHECK(launch_merge(cx.rows, g, rev, prof, nullptr, nullptr, cx.s));
   return download_state(cx.st, nullptr, nullptr, work, deg_work, wd, cx.s);
 }
 

@@ -715,7 +715,7 @@ template <int DT, int CPL, int PS, bool QB>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kSearchMinWaves<CPL, PS, QB>))) void k_search(SearchArgs a, uint32_t Cp) {
   extern __shared__ uint32_t smem[];
   const uint32_t w = wave_index();
-  const uint32_t gw = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + w;
+  const uint32_t gw = xcd_block(grid_block(), grid_blocks()) * kWavesPerBlock + w;
   if (gw >= a.g.N) return;
   const uint32_t node = a.order ? a.order[gw] : gw;
   SearchWave<DT, CPL, PS, QB> sw(a, node, smem + w * search_lds_words(Cp), Cp);
@@ -744,7 +744,7 @@ template <int DT, int CPL>
 __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint32_t Rp) {
   extern __shared__ uint32_t smem[];
   const uint32_t w = wave_index();
-  const uint32_t gw = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + w;
+  const uint32_t gw = xcd_block(grid_block(), grid_blocks()) * kWavesPerBlock + w;
   const GraphBufs& g = a.g;
   if (gw >= g.N) return;
   const uint32_t node = a.order ? a.order[gw] : gw;
@@ -1014,7 +1014,7 @@ template <int DT, int CPL, bool QB>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kRankMinWaves<DT, CPL, QB>, 8))) void k_prune_rank(PruneArgs a, uint32_t Cq) {
   extern __shared__ uint32_t smem[];
   const uint32_t w = wave_index();
-  const uint32_t gw = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + w;
+  const uint32_t gw = xcd_block(grid_block(), grid_blocks()) * kWavesPerBlock + w;
   const GraphBufs& g = a.g;
   if (gw >= g.N) return;
   const uint32_t node = a.order ? a.order[gw] : gw;
@@ -1432,20 +1432,66 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kRankMin
 // keep them), and the canonical distance is bitwise symmetric (a-b and b-a
 // differ only in sign). The snapshot is taken before any merge writes rows.
 // ---------------------------------------------------------------------------
+// Sources [s_lo, s_lo + items / R): item j covers forward slot s_lo R + j.
+// With s_lo = 0 and items = N R this is the whole graph (item = slot); a
+// graph of 2^32 or more slots is done in parts of fewer (see k_wide_gather).
 static __global__ void k_rev_keys(const uint32_t* __restrict__ work, const uint32_t* __restrict__ deg_work,
-                                  const float* __restrict__ wd, uint32_t N, uint32_t R, uint32_t C,
-                                  uint32_t* __restrict__ keys, uint32_t* __restrict__ vals,
+                                  const float* __restrict__ wd, uint32_t N, uint32_t R, uint32_t C, uint32_t s_lo,
+                                  size_t items, uint32_t* __restrict__ keys, uint32_t* __restrict__ vals,
                                   float* __restrict__ snap) {
   const size_t j = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (j >= (size_t)N * R) return;
-  const uint32_t s = (uint32_t)(j / R), i = (uint32_t)(j % R);
+  if (j >= items) return;
+  const uint32_t s = s_lo + (uint32_t)(j / R), i = (uint32_t)(j % R);
   const uint32_t deg = min(deg_work[s], R);
   const size_t wi = (size_t)s * C + i;
   const uint32_t t = i < deg ? work[wi] : DANCE_INV;
   const bool v = t != DANCE_INV && t < N && t != s;
   keys[j] = v ? t : N;
   vals[j] = (uint32_t)j;
-  snap[j] = v ? wd[wi] : FLT_MAX;
+  snap[(size_t)s_lo * R + j] = v ? wd[wi] : FLT_MAX;
+}
+
+// Graphs of 2^32 or more forward slots: the sources are split into P parts
+// of fewer than 2^32 slots each, and each part is sorted by target on its
+// own (32-bit items, as for smaller graphs). A target's sources are then the
+// concatenation of its part segments in part order, which is still ascending
+// source order. k_wide_offsets adds the parts' offsets (64-bit), and
+// k_wide_gather (one wave per target) writes each segment's sources and
+// slot snapshots in that order, so the merge reads them by sorted position.
+constexpr uint32_t kMaxRevParts = 16;
+struct WideParts {
+  uint32_t P;
+  uint32_t s_lo[kMaxRevParts];    // first source of each part
+  size_t vbase[kMaxRevParts];     // each part's sorted local slots start here in pvals
+};
+static __global__ void k_wide_offsets(uint32_t N, WideParts wp, const uint32_t* __restrict__ poffs,
+                                      uint64_t* __restrict__ offs64) {
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t > N) return;
+  uint64_t sum = 0;
+  for (uint32_t p = 0; p < wp.P; ++p) sum += poffs[(size_t)p * (N + 1) + t];
+  offs64[t] = sum;
+}
+static __global__ __launch_bounds__(256) void k_wide_gather(uint32_t N, uint32_t R, WideParts wp,
+                                                            const uint32_t* __restrict__ poffs,
+                                                            const uint32_t* __restrict__ pvals,
+                                                            const float* __restrict__ snap,
+                                                            const uint64_t* __restrict__ offs64,
+                                                            uint32_t* __restrict__ src_sorted,
+                                                            float* __restrict__ snap_sorted) {
+  const uint32_t t = grid_block() * 4u + (threadIdx.x >> 6), lane = threadIdx.x & 63u;
+  if (t >= N) return;
+  uint64_t out = offs64[t];
+  for (uint32_t p = 0; p < wp.P; ++p) {
+    const uint32_t* po = poffs + (size_t)p * (N + 1);
+    const uint32_t b = po[t], e = po[t + 1];
+    for (uint32_t k = b + lane; k < e; k += 64u) {
+      const uint32_t local = pvals[wp.vbase[p] + k];
+      src_sorted[out + (k - b)] = wp.s_lo[p] + local / R;
+      snap_sorted[out + (k - b)] = snap[(size_t)wp.s_lo[p] * R + local];
+    }
+    out += e - b;
+  }
 }
 
 // CSR offsets from the sorted keys (invalid items carry key N and sort last):
@@ -1469,6 +1515,29 @@ struct MergeArgs {
   uint32_t heavy_threshold, heavy_sample;
   const uint32_t* order;
   VCounters* ctr;
+  // Graphs of 2^32 or more slots (k_wide_gather): 64-bit offsets, and srcs /
+  // snap hold each sorted position's source and distance. nullptr otherwise.
+  const uint64_t* offsets64;
+  // Source and snapshot distance of sorted position idx.
+  __device__ __forceinline__ void at(size_t idx, uint32_t R, uint32_t& src, float& d) const {
+    if (offsets64) {
+      src = srcs[idx];
+      d = snap[idx];
+    } else {
+      const uint32_t slot = srcs[idx];
+      src = slot / R;
+      d = snap[slot];
+    }
+  }
+  __device__ __forceinline__ void segment(uint32_t t, size_t& begin, size_t& end) const {
+    if (offsets64) {
+      begin = offsets64[t];
+      end = offsets64[t + 1];
+    } else {
+      begin = offsets[t];
+      end = offsets[t + 1];
+    }
+  }
 };
 
 __host__ __device__ constexpr uint32_t merge_lds_words(uint32_t Cp) { return 2u * Cp + 128u; }
@@ -1477,7 +1546,7 @@ template <int DT, int CPL>
 __global__ __launch_bounds__(kBlock) void k_merge(MergeArgs a, uint32_t Cp) {
   extern __shared__ uint32_t smem[];
   const uint32_t w = wave_index();
-  const uint32_t gw = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + w;
+  const uint32_t gw = xcd_block(grid_block(), grid_blocks()) * kWavesPerBlock + w;
   const GraphBufs& g = a.g;
   if (gw >= g.N) return;
   const uint32_t t = a.order ? a.order[gw] : gw;
@@ -1487,8 +1556,9 @@ __global__ __launch_bounds__(kBlock) void k_merge(MergeArgs a, uint32_t Cp) {
   float* wdd = reinterpret_cast<float*>(wid + Cp);
   uint32_t* lst = wid + 2 * Cp;
   float* lsd = reinterpret_cast<float*>(lst + 64);
-  const uint32_t begin = a.offsets[t], end = a.offsets[t + 1];
-  const uint32_t indeg = end - begin;
+  size_t begin, end;
+  a.segment(t, begin, end);
+  const uint32_t indeg = (uint32_t)(end - begin);
   if (indeg == 0) return;
   uint32_t count = indeg;
   if (a.heavy_threshold != 0 && indeg > a.heavy_threshold) {
@@ -1508,12 +1578,11 @@ __global__ __launch_bounds__(kBlock) void k_merge(MergeArgs a, uint32_t Cp) {
   uint32_t ncand = 0;
   for (uint32_t b = 0; b < count; b += 64) {
     const uint32_t k = b + lane;
-    uint32_t src = DANCE_INV, slot = 0;
+    uint32_t src = DANCE_INV;
+    float dsrc = FLT_MAX;
     if (k < count) {
-      const uint32_t idx =
-          count < indeg ? begin + (uint32_t)(((unsigned long long)k * indeg) / count) : begin + k;
-      slot = a.srcs[idx];
-      src = slot / R;
+      const size_t idx = count < indeg ? begin + (size_t)(((unsigned long long)k * indeg) / count) : begin + k;
+      a.at(idx, R, src, dsrc);
     }
     const bool v = valid_for(src, N, t);
     bool inrow = false;
@@ -1524,7 +1593,7 @@ __global__ __launch_bounds__(kBlock) void k_merge(MergeArgs a, uint32_t Cp) {
     if (n == 0) continue;
     if (need) {
       lst[mbcnt64(m)] = src;
-      lsd[mbcnt64(m)] = a.snap[slot];
+      lsd[mbcnt64(m)] = dsrc;
     }
     wave_sync();
     ncand += n;
@@ -1651,14 +1720,15 @@ struct MergeRow {
 template <int DT, int CPL, int MS>
 __global__ __launch_bounds__(kBlock) void k_merge_reg(MergeArgs a) {
   const uint32_t w = wave_index();
-  const uint32_t gw = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + w;
+  const uint32_t gw = xcd_block(grid_block(), grid_blocks()) * kWavesPerBlock + w;
   const GraphBufs& g = a.g;
   if (gw >= g.N) return;
   const uint32_t t = a.order ? a.order[gw] : gw;
   const uint32_t N = g.N, C = g.C, R = g.R;
   const uint32_t lane = lane_id();
-  const uint32_t begin = a.offsets[t], end = a.offsets[t + 1];
-  const uint32_t indeg = end - begin;
+  size_t begin, end;
+  a.segment(t, begin, end);
+  const uint32_t indeg = (uint32_t)(end - begin);
   if (indeg == 0) return;
   uint32_t count = indeg;
   if (a.heavy_threshold != 0 && indeg > a.heavy_threshold) {
@@ -1680,15 +1750,14 @@ __global__ __launch_bounds__(kBlock) void k_merge_reg(MergeArgs a) {
   uint32_t ncand = 0;
   for (uint32_t b = 0; b < count; b += 64) {
     const uint32_t k = b + lane;
-    uint32_t src = DANCE_INV, slot = 0;
+    uint32_t src = DANCE_INV;
+    float dsrc = FLT_MAX;
     if (k < count) {
-      const uint32_t idx =
-          count < indeg ? begin + (uint32_t)(((unsigned long long)k * indeg) / count) : begin + k;
-      slot = a.srcs[idx];
-      src = slot / R;
+      const size_t idx = count < indeg ? begin + (size_t)(((unsigned long long)k * indeg) / count) : begin + k;
+      a.at(idx, R, src, dsrc);
     }
     const bool v = valid_for(src, N, t);
-    const float dsv = v ? a.snap[slot] : FLT_MAX;
+    const float dsv = v ? dsrc : FLT_MAX;
     ncand += popc64(wballot(v));
     // Once the row is full its worst only decreases, so a source that does
     // not beat the batch-start worst is rejected at its turn as well: the
@@ -1748,7 +1817,7 @@ __global__ __launch_bounds__(kBlock) void k_medoid(RowSet rs, uint32_t N, uint32
                                                    float* scores, uint32_t* cands) {
   __shared__ float buf[kWavesPerBlock][512];
   const uint32_t w = wave_index();
-  const uint32_t cw = blockIdx.x * kWavesPerBlock + w;
+  const uint32_t cw = grid_block() * kWavesPerBlock + w;
   if (cw >= nc) return;
   const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;
   const uint32_t c = d_hash_u32(cw * 9973u + 17u) % N;
@@ -1794,7 +1863,7 @@ __global__ __launch_bounds__(kBlock) void k_init(RowSet rs, GraphBufs g) {
   __shared__ uint32_t lstb[kWavesPerBlock][64];
   __shared__ float lsdb[kWavesPerBlock][64];
   const uint32_t w = wave_index();
-  const uint32_t node = blockIdx.x * kWavesPerBlock + w;
+  const uint32_t node = grid_block() * kWavesPerBlock + w;
   const uint32_t N = g.N, R = g.R, C = g.C;
   if (node >= N) return;
   const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;

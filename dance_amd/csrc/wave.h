@@ -115,6 +115,12 @@ __device__ __forceinline__ uint32_t wave_excl_scan_u(uint32_t v) {
   return x - v;
 }
 
+// Workgroup index of a launch of up to 2^32 workgroups. A dispatch holds
+// fewer than 2^32 work-items per dimension, so larger launches are 2-D
+// (grid_dims): gx x gy workgroups, dispatched in row-major order.
+__device__ __forceinline__ uint32_t grid_block() { return blockIdx.y * gridDim.x + blockIdx.x; }
+__device__ __forceinline__ uint32_t grid_blocks() { return gridDim.x * gridDim.y; }
+
 // Workgroup -> logical block. Workgroups are dispatched round-robin over the 8
 // XCDs; this mapping hands XCD k the contiguous logical range
 // [k*per, (k+1)*per) so each XCD's L2 walks one region of the processing

@@ -174,6 +174,34 @@ def test_reverse_merge_bitexact(kind, heavy):
     assert_state_equal(g, s, ("work", "deg_work", "wd"))
 
 
+@pytest.mark.parametrize("cap", [32 * 1000, 32 * 300 + 5, 32 * 2999])
+def test_reverse_merge_split_sort(monkeypatch, cap):
+    """The reverse CSR sorted in parts of at most `cap` slots (the path of
+    graphs with 2^32 or more slots, forced small): offsets, sources and the
+    merged rows equal the oracle's (3, 10 and 2 parts; the last part short)."""
+    monkeypatch.setenv("DANCE_REVERSE_PART_ITEMS", str(cap))
+    data = make_data("f32", 3000, 96, seed=5)
+    R, C = 32, 48
+    s0 = random_work_state(data, R, C, seed=22, flt_max_noise=False)
+    for heavy in ((0, 0), (8, 12)):
+        g, goff, gids = D.stage_reverse_merge(data, to_dance(s0), *heavy)
+        s, ooff, oids = O.reverse_merge(data, s0, *heavy)
+        assert np.array_equal(goff, ooff)
+        assert np.array_equal(gids, oids)
+        assert_state_equal(g, s, ("work", "deg_work", "wd"))
+
+
+def test_end_to_end_split_reverse_sort(monkeypatch):
+    """The whole build with the reverse sort in parts equals the oracle."""
+    monkeypatch.setenv("DANCE_REVERSE_PART_ITEMS", str(64 * 1237))
+    data = make_data("f32", 4000, 96, seed=29)
+    res = D.vamana_build(data, 64, 100, 80, 64)
+    og, od, om = O.vnew2_build(data, 64, 100, 80, 64)
+    assert res.medoid == om
+    assert np.array_equal(res.degree, od)
+    assert np.array_equal(res.graph, og)
+
+
 @pytest.mark.parametrize("kind,R,L,C,steps", [("f32", 32, 64, 48, 32), ("f32", 64, 100, 80, 64),
                                               ("u8", 32, 64, 48, 48), ("f32", 16, 150, 40, 100)])
 def test_search_bitexact(kind, R, L, C, steps):
