@@ -344,15 +344,25 @@ def last_kernel_profile() -> dict:
     return struct_dict(p)
 
 
-def last_stats() -> dict:
+def last_stats(entry: str = "vnew2") -> dict:
+    """GPUVamanaStats of the last vnew2 build, or of the last v8 build."""
     s = GPUVamanaStats()
-    lib().gpu_vamana_vnew2_get_last_stats(C.byref(s))
+    getter = lib().gpu_vamana_get_last_stats if entry == "v8" else lib().gpu_vamana_vnew2_get_last_stats
+    getter(C.byref(s))
     return struct_dict(s)
+
+
+def last_medoid(entry: str = "vnew2") -> int:
+    getter = lib().gpu_vamana_get_last_medoid if entry == "v8" else lib().gpu_vamana_vnew2_get_last_medoid
+    return int(getter())
 
 
 def vamana_build(data: np.ndarray, R: int = 64, L: int = 100, C_: int = 80, STEPS: int = 64,
                  entry: str = "vnew2") -> BuildResult:
-    """gpu_vamana_vnew2_build[_float] on host vectors (uint8 or float32)."""
+    """gpu_vamana_vnew2_build[_float] (entry "vnew2") or the v8 builder's
+    gpu_vamana_build[_float] (entry "v8") on host vectors (uint8 or float32)."""
+    if entry not in ("vnew2", "v8"):
+        raise ValueError(f"unknown builder entry {entry!r}")
     data = np.ascontiguousarray(data)
     if data.ndim != 2:
         raise ValueError("data must be N x dim")
@@ -367,9 +377,8 @@ def vamana_build(data: np.ndarray, R: int = 64, L: int = 100, C_: int = 80, STEP
     else:
         raise TypeError("vamana_build takes uint8 or float32 vectors")
     rc = fn(data.ctypes.data, N, dim, R, L, C_, STEPS, _p(graph, C.c_uint32), _p(degree, C.c_uint32))
-    _check(rc, "gpu_vamana_vnew2_build")
-    return BuildResult(graph, degree, int(L_.gpu_vamana_vnew2_get_last_medoid()), last_stats(),
-                       last_kernel_profile())
+    _check(rc, "gpu_vamana_vnew2_build" if entry == "vnew2" else "gpu_vamana_build")
+    return BuildResult(graph, degree, last_medoid(entry), last_stats(entry), last_kernel_profile())
 
 
 def vamana_build_resident(d_data: int, dtype: int, N: int, dim: int, R: int, L: int, C_: int, STEPS: int,

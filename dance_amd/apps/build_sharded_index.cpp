@@ -20,7 +20,10 @@
 //      with k_base assignments, fits G GB of device memory for its build.
 //      Finally every row goes to its k_base nearest centers.
 //   2. per shard (patch:2811-2984): the shard's rows in ascending id order,
-//      built with gpu_vamana_build[_float] at shard_R = 2R/3
+//      built with the v8 builder gpu_vamana_build[_float] (or vnew2's
+//      gpu_vamana_vnew2_build[_float] when DISKANN_GPU_VAMANA_VERSION=vnew2 or
+//      DISKANN_USE_GPU_VAMANA_VNEW2 is set and not 0, patch:2576-2584), with
+//      that builder's medoid (patch:2947), at shard_R = 2R/3
 //      (DISKANN_GPU_SHARD_R caps it at R), C = max(2 shard_R, shard_R + 32)
 //      (DISKANN_GPU_C), STEPS = min(L, 20) (DISKANN_GPU_STEPS), C at least
 //      shard_R and STEPS at most L (patch:3271-3335); saved with the builder's
@@ -145,6 +148,15 @@ void write_bin(const std::string& path, const T* data, uint32_t rows, uint32_t c
 uint32_t env_u32(const char* name, uint32_t fallback) {
   const char* e = std::getenv(name);
   return e ? (uint32_t)std::atoi(e) : fallback;
+}
+
+// Shard builder choice (patch:2576-2584): v8 unless DISKANN_GPU_VAMANA_VERSION
+// is "vnew2" or DISKANN_USE_GPU_VAMANA_VNEW2 is set, non-empty and not "0".
+bool use_vnew2() {
+  const char* v = std::getenv("DISKANN_GPU_VAMANA_VERSION");
+  if (v != nullptr && std::strcmp(v, "vnew2") == 0) return true;
+  const char* e = std::getenv("DISKANN_USE_GPU_VAMANA_VNEW2");
+  return e != nullptr && e[0] != '\0' && std::strcmp(e, "0") != 0;
 }
 
 template <typename T>
@@ -314,6 +326,7 @@ int run(const Options& o) {
             << std::endl;
 
   // 2. per-shard GPU builds
+  const bool vnew2 = use_vnew2();
   const std::string tmp = o.prefix + "_tempFiles_subshard-";
   for (uint32_t k = 0; k < K; ++k) {
     const std::vector<uint32_t>& ids = shards[k];
@@ -325,16 +338,22 @@ int run(const Options& o) {
       std::vector<T> rows((size_t)m * dim);
       for (uint32_t i = 0; i < m; ++i)
         std::memcpy(&rows[(size_t)i * dim], &x[(size_t)ids[i] * dim], (size_t)dim * sizeof(T));
+      std::cout << "[GPU shard] build start: shard=" << k << " type=" << (std::is_same<T, float>::value ? "float" : "uint8")
+                << " builder=" << (vnew2 ? "vnew2" : "v8") << " npts=" << m << " dim=" << dim << " R=" << shard_R
+                << " L=" << o.L << " C=" << C << " STEPS=" << steps << std::endl;
       const double tb = now_sec();
       int rc;
-      if (std::is_same<T, float>::value)
-        rc = gpu_vamana_build_float(reinterpret_cast<const float*>(rows.data()), m, dim, shard_R, o.L, C, steps,
-                                    graph.data(), degree.data());
-      else
-        rc = gpu_vamana_build(reinterpret_cast<const uint8_t*>(rows.data()), m, dim, shard_R, o.L, C, steps,
-                              graph.data(), degree.data());
+      if (std::is_same<T, float>::value) {
+        const float* r = reinterpret_cast<const float*>(rows.data());
+        rc = vnew2 ? gpu_vamana_vnew2_build_float(r, m, dim, shard_R, o.L, C, steps, graph.data(), degree.data())
+                   : gpu_vamana_build_float(r, m, dim, shard_R, o.L, C, steps, graph.data(), degree.data());
+      } else {
+        const uint8_t* r = reinterpret_cast<const uint8_t*>(rows.data());
+        rc = vnew2 ? gpu_vamana_vnew2_build(r, m, dim, shard_R, o.L, C, steps, graph.data(), degree.data())
+                   : gpu_vamana_build(r, m, dim, shard_R, o.L, C, steps, graph.data(), degree.data());
+      }
       if (rc != 0) throw std::runtime_error("gpu_vamana_build failed for shard " + std::to_string(k));
-      medoid = gpu_vamana_get_last_medoid();
+      medoid = vnew2 ? gpu_vamana_vnew2_get_last_medoid() : gpu_vamana_get_last_medoid();
       if (medoid >= m) medoid = 0;
       std::cout << "[gpu_shard_timing] shard=" << k << " npts=" << m << " gpu_vamana_call_seconds=" << (now_sec() - tb)
                 << std::endl;

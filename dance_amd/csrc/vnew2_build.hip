@@ -97,6 +97,26 @@ static uint32_t g_last_medoid = 0;
 static GPUVamanaStats g_last_stats{};
 static DanceKernelProfile g_last_prof{};
 
+// The two standard builders of the reference keep their own last-build state
+// (gpu_vamana_vnew2.cu and gpu_vamana_uint8.cu each hold a file-static medoid
+// and GPUVamanaStats, uint8.cu:2416-2435), so a v8 build leaves the vnew2
+// getters untouched and the other way round.
+enum class Builder { vnew2, v8 };
+static uint32_t g_last_medoid_v8 = 0;
+static GPUVamanaStats g_last_stats_v8{};
+
+// The v8 builder (gpu_vamana_uint8.cu) runs the vnew2 kernels' algorithm with
+// C-stride double-buffered graphs and has no reverse heavy cap in any profile:
+// its reverse_merge_csr_kernel (uint8.cu:1795-1940) takes every reverse
+// candidate. Its search (uint8.cu:1123-1540), insert (:817-950), init
+// (:1074-1121), medoid (:1040-1072) and prune (:2020-2298) compute what the
+// vnew2 ones do; the graph layout changes no result, so the same kernels serve.
+static Profile profile_for(Builder b) {
+  Profile p = kProfiles[profile_index_locked()];
+  if (b == Builder::v8) p.heavy_threshold = p.heavy_sample = 0;
+  return p;
+}
+
 
 // ---------------------------------------------------------------------------
 // Graph state + per-stage launchers.
@@ -762,9 +782,9 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
 template <typename HostT>
 static int build_host(const HostT* h_data, int src_dtype, uint32_t N, uint32_t dim, uint32_t R, uint32_t L,
                       uint32_t C, uint32_t STEPS, uint32_t* h_graph, uint32_t* h_degree, void** keep_data,
-                      uint32_t** keep_graph, uint32_t** keep_degree) {
+                      uint32_t** keep_graph, uint32_t** keep_degree, Builder builder = Builder::vnew2) {
   std::lock_guard<std::mutex> lk(g_mu);
-  g_last_stats = GPUVamanaStats{};
+  (builder == Builder::v8 ? g_last_stats_v8 : g_last_stats) = GPUVamanaStats{};
   const double t0 = now_sec();
   const bool handoff = keep_data != nullptr;
   if (h_data == nullptr || (!handoff && (h_graph == nullptr || h_degree == nullptr))) {
@@ -772,8 +792,13 @@ static int build_host(const HostT* h_data, int src_dtype, uint32_t N, uint32_t d
     return -1;
   }
   DCHECK(validate(N, dim, R, L, C, STEPS));
-  const Profile prof = kProfiles[profile_index_locked()];
+  const Profile prof = profile_for(builder);
   const int store = (src_dtype == DANCE_F32 && prof.fp16) ? DANCE_F16 : src_dtype;
+  if (builder == Builder::v8 && verbose())
+    std::printf("[gpu_vamana_build] type=%s N=%u dim=%u R=%u L=%u C=%u STEPS=%u alpha=%.3f iters=%u builder=v8 "
+                "profile=%s fp16=%u heavy_cap=0\n",
+                store == DANCE_F16 ? "float16" : (src_dtype == DANCE_U8 ? "uint8" : "float"), N, dim, R, L,
+                C, std::min(STEPS, L), (double)kAlpha, kIters, prof.name, prof.fp16 ? 1u : 0u);
   DCHECK(check_width(dim, store));
   hipStream_t s = nullptr;
   DHIP(hipStreamCreate(&s));
@@ -814,8 +839,13 @@ static int build_host(const HostT* h_data, int src_dtype, uint32_t N, uint32_t d
   }
   stats.d2h_seconds = now_sec() - td;
   stats.gpu_build_seconds = now_sec() - t0;
-  g_last_stats = stats;
-  g_last_medoid = medoid;
+  if (builder == Builder::v8) {
+    g_last_stats_v8 = stats;
+    g_last_medoid_v8 = medoid;
+  } else {
+    g_last_stats = stats;
+    g_last_medoid = medoid;
+  }
   g_last_prof = kp;
   return 0;
 }
@@ -1292,14 +1322,19 @@ int gpu_vamana_vnew2_build_float(const float* h_data, uint32_t N, uint32_t dim, 
   return build_host<float>(h_data, DANCE_F32, N, dim, R, L, C, STEPS, h_graph, h_degree, nullptr, nullptr, nullptr);
 }
 
+// The v8 builder (gpu_vamana_uint8.cu:3093-3120): the reference converts float
+// input to binary16 on the host under the fp16 profiles (:3100-3115); the same
+// round-to-nearest-even conversion runs here on the device after the upload.
 int gpu_vamana_build(const uint8_t* h_data, uint32_t N, uint32_t dim, uint32_t R, uint32_t L, uint32_t C,
                      uint32_t STEPS, uint32_t* h_graph, uint32_t* h_degree) {
-  return gpu_vamana_vnew2_build(h_data, N, dim, R, L, C, STEPS, h_graph, h_degree);
+  return build_host<uint8_t>(h_data, DANCE_U8, N, dim, R, L, C, STEPS, h_graph, h_degree, nullptr, nullptr, nullptr,
+                             Builder::v8);
 }
 
 int gpu_vamana_build_float(const float* h_data, uint32_t N, uint32_t dim, uint32_t R, uint32_t L, uint32_t C,
                            uint32_t STEPS, uint32_t* h_graph, uint32_t* h_degree) {
-  return gpu_vamana_vnew2_build_float(h_data, N, dim, R, L, C, STEPS, h_graph, h_degree);
+  return build_host<float>(h_data, DANCE_F32, N, dim, R, L, C, STEPS, h_graph, h_degree, nullptr, nullptr, nullptr,
+                           Builder::v8);
 }
 
 int gpu_vamana_vnew2_build_device(const uint8_t* h_data, uint32_t N, uint32_t dim, uint32_t R, uint32_t L, uint32_t C,
@@ -1364,9 +1399,9 @@ uint32_t gpu_vamana_vnew2_get_last_medoid(void) { return g_last_medoid; }
 void gpu_vamana_vnew2_get_last_stats(GPUVamanaStats* stats) {
   if (stats) *stats = g_last_stats;
 }
-uint32_t gpu_vamana_get_last_medoid(void) { return g_last_medoid; }
+uint32_t gpu_vamana_get_last_medoid(void) { return g_last_medoid_v8; }
 void gpu_vamana_get_last_stats(GPUVamanaStats* stats) {
-  if (stats) *stats = g_last_stats;
+  if (stats) *stats = g_last_stats_v8;
 }
 
 // ===========================================================================

@@ -39,9 +39,11 @@ typedef struct GPUVamanaStats {
     uint32_t selective_active_nodes;
 } GPUVamanaStats;
 
-/* "v8" symbols (reference: include/gpu_vamana_builder.h:30-48). The v8
- * algorithm (src/gpu_vamana_uint8.cu) is the sharded pipeline's builder and is
- * out of scope here; these symbols run the vnew2 build. */
+/* "v8" build (reference: include/gpu_vamana_builder.h:30-48,
+ * src/gpu_vamana_uint8.cu:2437-3120), the sharded pipeline's default shard
+ * builder. Same schedule, search, online insert, reverse merge and prune as
+ * vnew2, without the reverse heavy cap in any profile; the float entry stores
+ * fp16 rows under the fp16 profiles, as vnew2 does. */
 int gpu_vamana_build(const uint8_t *h_data, uint32_t num_points, uint32_t dim, uint32_t R, uint32_t L,
                      uint32_t C, uint32_t STEPS, uint32_t *h_graph, uint32_t *h_degree);
 int gpu_vamana_build_float(const float *h_data, uint32_t num_points, uint32_t dim, uint32_t R, uint32_t L,
@@ -67,7 +69,9 @@ int gpu_vamana_vnew2_build_device_float(const float *h_data, uint32_t num_points
                                         uint32_t L, uint32_t C, uint32_t STEPS, float **d_data,
                                         uint32_t **d_graph, uint32_t **d_degree);
 
-/* Last-build getters (reference: include/gpu_vamana_builder.h:78-81). */
+/* Last-build getters (reference: include/gpu_vamana_builder.h:78-81). The
+ * gpu_vamana_* pair reports the last v8 build, the gpu_vamana_vnew2_* pair the
+ * last vnew2 build (hand-off and resident builds included). */
 uint32_t gpu_vamana_get_last_medoid(void);
 void gpu_vamana_get_last_stats(GPUVamanaStats *stats);
 uint32_t gpu_vamana_vnew2_get_last_medoid(void);

@@ -16,13 +16,21 @@ Parity status of each oracle function (how it is pinned; see tests/test_oracle.p
   reverse_merge           pinned: CSR == transpose of the first-R forward
                           entries with ascending sources; merge invariants and an
                           independent Python restatement.
-  search (online insert)  partially pinned: invariants (row = cur row and
-                          expanded nodes, no duplicates/self, capacity C) and the
-                          independent batched GPU implementation; the reference
-                          cannot be executed here, so its exact step semantics
-                          are pinned by source reading only.
-  vnew2_build             pinned end to end by recall@10 against exact
-                          brute-force ground truth.
+  robust_insert           pinned: an independent Python restatement of the
+                          occlude / victim / append / replace rule on tiny
+                          integer rows with exact ties, full rows, invalid and
+                          self members, FLT_MAX and NaN stored distances.
+  search                  pinned: with a huge alpha nothing is occluded or
+                          replaced, so the work row is the current row followed
+                          by the expansion order, compared with an independent
+                          best-first search (whole graph and beam eviction).
+  vnew2_build             pinned as the composition of the pinned stages
+                          (alpha schedule, coarse steps, final fill) and end to
+                          end by recall@10 against exact brute force.
+  v8_build                pinned: its own C-stride double-buffered composition
+                          of the pinned stages equals vnew2_build without the
+                          heavy cap, and differs from vnew2_build with the cap
+                          where a reverse list exceeds the threshold.
   cpu_vamana_build        baseline only (DiskANN restated; parity unpinned:
                           upstream DiskANN is not available offline).
   merge_shards            pinned: mix64 by its closed-form inverse; the merge by
@@ -44,9 +52,11 @@ Parity status of each oracle function (how it is pinned; see tests/test_oracle.p
   filtered_build          pinned by the stages above plus build invariants
                           (no self / duplicate / invalid edge, degree <= R,
                           label-compatible edges) and recall on labelled
-                          queries; task and union search semantics are pinned
-                          by source reading and by the independent GPU
-                          implementation only (parity unpinned beyond that).
+                          queries.
+  filtered task / union   pinned: a restated canonical pool in Python (slot =
+  searches                insertion order, eviction of the worst) with and
+                          without eviction; multi-label quota by a brute-force
+                          restatement with cardinality ties.
 """
 from __future__ import annotations
 
@@ -113,6 +123,8 @@ def lib() -> C.CDLL:
         L.oracle_vnew2_build.argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, u32, f32, u32, u32, u32, _u32p,
                                          _u32p, _u32p]
         L.oracle_vnew2_build.restype = i32
+        L.oracle_v8_build.argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, u32, f32, u32, _u32p, _u32p, _u32p]
+        L.oracle_v8_build.restype = i32
         L.oracle_cpu_vamana_build.argtypes = [vp, i32, u32, u32, u32, u32, f32, u32, _u32p, _u32p]
         L.oracle_cpu_vamana_build.restype = u32
         L.oracle_beam_search.argtypes = [vp, i32, u32, u32, _u32p, _u32p, u32, u32, vp, u32, u32, u32, _u32p]
@@ -284,6 +296,22 @@ def vnew2_build(data: np.ndarray, R=64, L=100, C_=80, STEPS=64, iters=4, alpha=1
                                   alpha_from, heavy_threshold, heavy_sample, _p(graph), _p(deg), _p(med))
     if rc != 0:
         raise ValueError(f"oracle_vnew2_build rejected the parameters (rc={rc})")
+    return graph, deg, int(med[0])
+
+
+def v8_build(data: np.ndarray, R=64, L=100, C_=80, STEPS=64, iters=4, alpha=1.2, alpha_from=None):
+    """The v8 builder (gpu_vamana_uint8.cu) with its C-stride double-buffered
+    graphs and no reverse heavy cap; alpha_from as in vnew2_build."""
+    data = np.ascontiguousarray(data)
+    alpha_from = iters - 1 if alpha_from is None else alpha_from
+    N = data.shape[0]
+    graph = np.empty((N, R), np.uint32)
+    deg = np.empty(N, np.uint32)
+    med = np.zeros(1, np.uint32)
+    rc = lib().oracle_v8_build(data.ctypes.data, _dt(data), N, data.shape[1], R, L, C_, STEPS, iters, alpha,
+                               alpha_from, _p(graph), _p(deg), _p(med))
+    if rc != 0:
+        raise ValueError(f"oracle_v8_build rejected the parameters (rc={rc})")
     return graph, deg, int(med[0])
 
 

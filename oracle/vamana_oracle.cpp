@@ -305,6 +305,9 @@ struct Pool {
   }
 };
 
+// cur rows are `cs` entries apart: R for vnew2's packed current graph, C for
+// the v8 builder's double-buffered C-stride graphs (0 means R). The prune
+// writes cur only when it is given (v8 prunes in place in the work graph).
 struct Graph {
   uint32_t N, R, C;
   uint32_t* cur;
@@ -312,6 +315,8 @@ struct Graph {
   uint32_t* work;
   uint32_t* deg_work;
   float* wd;
+  uint32_t cs = 0;
+  size_t stride() const { return cs ? cs : R; }
 };
 
 // dynamic_robust_insert_C_warp, vnew2.cu:759-877 (ENABLE_FAST_ONLINE_REPLACE=0)
@@ -375,7 +380,7 @@ void robust_insert(const Data& D, Graph& g, uint32_t node, uint32_t x, float d_p
 uint64_t search_one(const Data& D, Graph& g, uint32_t node, uint32_t L, uint32_t steps, float alpha,
                     uint32_t start, uint64_t* n_dist) {
   const uint32_t N = g.N, R = g.R, C = g.C;
-  const size_t cb = (size_t)node * R, wb = (size_t)node * C;
+  const size_t cb = (size_t)node * g.stride(), wb = (size_t)node * C;
   uint32_t deg_self = std::min(g.deg_cur[node], R);
   // Work row := current row with stored distances (vnew2.cu:1186-1212).
   for (uint32_t i = 0; i < C; ++i) {
@@ -421,7 +426,7 @@ uint64_t search_one(const Data& D, Graph& g, uint32_t node, uint32_t L, uint32_t
     ++expansions;
     robust_insert(D, g, node, x, dx, alpha);
     uint32_t deg = std::min(g.deg_cur[x], R);
-    const size_t xb = (size_t)x * R;
+    const size_t xb = (size_t)x * g.stride();
     for (uint32_t j = 0; j < deg; ++j) {
       uint32_t c = g.cur[xb + j];
       if (!valid_for(c, N, node)) continue;
@@ -513,7 +518,7 @@ void reverse_merge(const Data& D, Graph& g, uint32_t heavy_threshold, uint32_t h
 // to R with alpha, plus the minimum-degree fill used in the last iteration.
 void prune_one(const Data& D, Graph& g, uint32_t node, uint32_t min_degree, float alpha) {
   const uint32_t N = g.N, R = g.R, C = g.C;
-  const size_t wb = (size_t)node * C, cb = (size_t)node * R;
+  const size_t wb = (size_t)node * C, cb = (size_t)node * g.stride();
   uint32_t deg = std::min(g.deg_work[node], C);
   std::vector<uint32_t> sid(C);
   std::vector<float> sd(C);
@@ -599,9 +604,10 @@ void prune_one(const Data& D, Graph& g, uint32_t node, uint32_t min_degree, floa
     g.work[wb + i] = i < oc ? out_id[i] : INV;
     g.wd[wb + i] = i < oc ? out_d[i] : FLT_MAX;
   }
-  for (uint32_t i = 0; i < R; ++i) g.cur[cb + i] = i < oc ? out_id[i] : INV;
+  if (g.cur)
+    for (uint32_t i = 0; i < R; ++i) g.cur[cb + i] = i < oc ? out_id[i] : INV;
   g.deg_work[node] = oc;
-  g.deg_cur[node] = oc;
+  if (g.deg_cur) g.deg_cur[node] = oc;
 }
 
 // medoid_score_kernel_warp + host top-1, vnew2.cu:1032-1064, 2359-2479.
@@ -641,11 +647,11 @@ void init_graph(const Data& D, Graph& g) {
 #pragma omp parallel for schedule(static)
   for (int64_t nn = 0; nn < (int64_t)N; ++nn) {
     uint32_t node = (uint32_t)nn;
-    const size_t cb = (size_t)node * R, wb = (size_t)node * C;
+    const size_t cb = (size_t)node * g.stride(), wb = (size_t)node * C;
     for (uint32_t i = 0; i < C; ++i) {
       g.work[wb + i] = INV;
       g.wd[wb + i] = FLT_MAX;
-      if (i < R) g.cur[cb + i] = INV;
+      if (i < g.stride()) g.cur[cb + i] = INV;
     }
     for (uint32_t i = 0; i < R; ++i) {
       uint32_t nb = det_neighbor(node, i, N);
@@ -787,6 +793,54 @@ int oracle_vnew2_build(const void* data, int dtype, uint32_t N, uint32_t dim, ui
     for (int64_t nn = 0; nn < (int64_t)N; ++nn) prune_one(D, g, (uint32_t)nn, md, a);
   }
   std::memcpy(degree_out, deg_cur.data(), (size_t)N * sizeof(uint32_t));
+  if (medoid_out) *medoid_out = start;
+  return 0;
+}
+
+// Full v8 build (gpu_vamana_build_impl, gpu_vamana_uint8.cu:2437-3090) with
+// its own buffer scheme: two C-stride graphs initialised alike and one
+// distance array (init_random_graph, uint8.cu:1074-1121); each search copies
+// the current graph's row into the next graph (uint8.cu:1173-1198) and expands
+// the current graph's C-stride rows; the reverse merge (reverse_merge_csr_kernel,
+// uint8.cu:1795-1940, no heavy cap: v8 has none) and the prune
+// (final_prune_kernel_shared, uint8.cu:2020-2298) work in place on the next
+// graph; the graphs swap after every iteration (uint8.cu:2936-2942). The
+// output is the first R entries of every current row (cudaMemcpy2D,
+// uint8.cu:3046). Parameter checks as uint8.cu:2443-2466.
+int oracle_v8_build(const void* data, int dtype, uint32_t N, uint32_t dim, uint32_t R, uint32_t L, uint32_t C,
+                    uint32_t STEPS, uint32_t iters, float alpha, uint32_t alpha_from, uint32_t* graph_out,
+                    uint32_t* degree_out, uint32_t* medoid_out) {
+  if (data == nullptr || graph_out == nullptr || degree_out == nullptr) return -1;
+  if (N == 0 || dim == 0 || R == 0 || L == 0 || C == 0 || STEPS == 0) return -1;
+  if (C < R) return -1;
+  if (STEPS > L) STEPS = L;
+  Data D{data, dtype, N, dim};
+  std::vector<uint32_t> ga((size_t)N * C), gb((size_t)N * C), da(N), db(N);
+  std::vector<float> dists((size_t)N * C);
+  uint32_t start = medoid(D, nullptr, nullptr);
+  {
+    Graph g0{N, R, C, ga.data(), da.data(), gb.data(), db.data(), dists.data(), C};
+    init_graph(D, g0);
+  }
+  uint32_t *cur = ga.data(), *dcur = da.data(), *next = gb.data(), *dnext = db.data();
+  for (uint32_t it = 0; it < iters; ++it) {
+    float a = alpha_for_iter(it, alpha_from, alpha);
+    uint32_t steps = STEPS;
+    if (it < 2 && steps > 64) steps = 64;  // ENABLE_COARSE_TO_FINE_STEPS (uint8.cu:2788-2791)
+    Graph g{N, R, C, cur, dcur, next, dnext, dists.data(), C};
+#pragma omp parallel for schedule(dynamic, 64)
+    for (int64_t nn = 0; nn < (int64_t)N; ++nn) search_one(D, g, (uint32_t)nn, L, steps, a, start, nullptr);
+    reverse_merge(D, g, 0, 0, nullptr, nullptr);
+    Graph gp{N, R, C, nullptr, nullptr, next, dnext, dists.data(), C};
+    const uint32_t md = (it + 1 == iters) ? 64u : 0u;  // FINAL_MIN_DEGREE in the last iteration (uint8.cu:2871-2874)
+#pragma omp parallel for schedule(dynamic, 64)
+    for (int64_t nn = 0; nn < (int64_t)N; ++nn) prune_one(D, gp, (uint32_t)nn, md, a);
+    std::swap(cur, next);
+    std::swap(dcur, dnext);
+  }
+  for (uint32_t n = 0; n < N; ++n)
+    std::memcpy(graph_out + (size_t)n * R, cur + (size_t)n * C, (size_t)R * sizeof(uint32_t));
+  std::memcpy(degree_out, dcur, (size_t)N * sizeof(uint32_t));
   if (medoid_out) *medoid_out = start;
   return 0;
 }

@@ -4,7 +4,8 @@ build_merged_vamana_index (integrations/dance-diskann-78256bba.patch:1209-1560).
 CPU: option errors, decided before any device call.
 GPU: given the centroids the app wrote, its shard id lists, shard graphs,
 merged graph and medoid file equal an oracle pipeline built from the pinned
-parts (oracle assignment, oracle vnew2 build per shard at shard_R = 2R/3,
+parts (oracle assignment, the oracle of the shard builder per shard: v8 by
+default, vnew2 under DISKANN_GPU_VAMANA_VERSION=vnew2, at shard_R = 2R/3,
 C = max(2 shard_R, shard_R + 32), STEPS = min(L, 20), the reference's shard
 save format, oracle merge), byte for byte. The k-means that produces the
 centroids restates DiskANN's upstream partitioner (absent): parity unpinned
@@ -55,7 +56,21 @@ def test_option_errors(tmp_path, extra, msg):
     assert r.returncode == 255 and msg in r.stderr, r.stderr
 
 
-def oracle_pipeline(tmp_path, x, centroids, R, L, k_base):
+HEAVY = {"QUALITY": (0, 0), "FAST_SMALL": (0, 0), "PRO6000_100M": (256, 384), "FILTERED_PAPER": (256, 384)}
+
+
+def shard_build(rows, builder, profile, **kw):
+    """The oracle of one shard build: v8 (no heavy cap) or vnew2 with the
+    profile's cap; float rows are stored as binary16 under the fp16 profiles."""
+    if rows.dtype == np.float32 and profile != "QUALITY":
+        rows = rows.astype(np.float16)
+    if builder == "v8":
+        return O.v8_build(rows, **kw)
+    t, smp = HEAVY[profile]
+    return O.vnew2_build(rows, heavy_threshold=t, heavy_sample=smp, **kw)
+
+
+def oracle_pipeline(tmp_path, x, centroids, R, L, k_base, builder="v8", profile="QUALITY"):
     shard_R = 2 * R // 3
     C_ = max(2 * shard_R, shard_R + 32, shard_R)
     steps = min(L, 20)
@@ -70,7 +85,7 @@ def oracle_pipeline(tmp_path, x, centroids, R, L, k_base):
         body = bytearray()
         med = 0
         if ids.size:
-            g, d, med = O.vnew2_build(x[ids], R=shard_R, L=L, C_=C_, STEPS=steps)
+            g, d, med = shard_build(x[ids], builder, profile, R=shard_R, L=L, C_=C_, STEPS=steps)
             med = med if med < ids.size else 0
             for i in range(ids.size):
                 k_i = min(int(d[i]), shard_R)
@@ -108,6 +123,47 @@ def test_sharded_build_matches_oracle_pipeline(tmp_path, kind, n, dim, R, L, sha
         assert f.read() == g.read(), "merged graph differs from the oracle's"
     with open(prefix + "_medoids.bin", "rb") as f, open(meds, "rb") as g:
         assert f.read() == g.read()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", ["uint8", "float"])
+def test_sharded_builder_choice_under_heavy_cap_profile(tmp_path, kind):
+    """Under PRO6000_100M the default shard builder is v8 (no heavy cap) and
+    DISKANN_GPU_VAMANA_VERSION=vnew2 selects vnew2 (cap 256/384), as the
+    patch's use_gpu_vamana_vnew2 (patch:2576-2584); each run equals the oracle
+    pipeline of its builder, and the shard graphs of the two differ."""
+    # Uniform rows: their k-NN graphs have hubs whose reverse lists pass 384.
+    n, dim, R, L, shards, k_base = 6000, 32, 48, 60, 2, 1
+    rng = np.random.default_rng(5)
+    if kind == "uint8":
+        x = rng.integers(0, 256, (n, dim), dtype=np.uint8)
+    else:
+        x = rng.standard_normal((n, dim)).astype(np.float32)
+    path = str(tmp_path / "base.bin")
+    formats.write_bin(path, x)
+    outs = {}
+    for builder in ("v8", "vnew2"):
+        env = dict(os.environ, DANCE_PROFILE="PRO6000_100M")
+        if builder == "vnew2":
+            env["DISKANN_GPU_VAMANA_VERSION"] = "vnew2"
+        prefix = str(tmp_path / f"idx_{builder}")
+        print(f"sharded {kind} builder={builder}", flush=True)
+        r = run_app("--data_type", kind, "--data_path", path, "--index_path_prefix", prefix, "-R", str(R), "-L",
+                    str(L), "--num_shards", str(shards), "--k_base", str(k_base), "--sampling_rate", "0.5",
+                    "--seed", "7", env=env)
+        assert r.returncode == 0, r.stdout + r.stderr
+        assert f"builder={builder}" in r.stdout
+        cen = formats.read_bin(prefix + "_centroids.bin", np.float32)
+        sub = tmp_path / f"oracle_{builder}"
+        sub.mkdir()
+        _, pre, out, meds = oracle_pipeline(sub, x, cen, R, L, k_base, builder, "PRO6000_100M")
+        for k in range(shards):
+            with open(f"{prefix}_tempFiles_subshard-{k}_mem.index", "rb") as f, open(f"{pre}{k}_mem.index", "rb") as g:
+                assert f.read() == g.read(), f"{builder} shard {k} differs from its oracle"
+        with open(prefix, "rb") as f, open(out, "rb") as g:
+            outs[builder] = f.read()
+            assert outs[builder] == g.read(), f"{builder} merged graph differs from its oracle"
+    assert outs["v8"] != outs["vnew2"]
 
 
 @pytest.mark.gpu
