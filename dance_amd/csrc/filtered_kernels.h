@@ -934,10 +934,25 @@ static __global__ void k_long_rows(uint32_t N, const uint32_t* boff, uint32_t* l
 // k_csr) is distanced by all kLongWaves waves into the row's scratch (bd
 // distances, brem removed flags, bmask row-label masks), then
 // FilteredRobustPrune runs over it: each selection is the smallest live
-// (distance, id, index), reduced over the waves through LDS, and every wave
-// applies the occlusion rule to its own entries. Entry i belongs to wave
-// (i / 64) % kLongWaves, lane i % 64, which alone writes its scratch after
-// the distance pass.
+// (distance, id, index), reduced over the waves through LDS, and the
+// occlusion rule of the selected entry is applied to the live entries.
+//
+// Selections come in ascending (distance, id, index) order, and an entry's
+// fate depends only on the selections made before it, so the list is
+// processed in windows of ascending distance keys: the occlusion passes of a
+// window cover only its own entries, after replaying on them the selections
+// of earlier windows. A row of at most kLongWin entries is one window (the
+// whole list); a hub row (label hubs reach 358,549 candidates at c5) takes
+// its next window as the ~kLongWin smallest remaining keys (two LDS histogram
+// passes: key bits 30..19, then 18..7 inside the crossing bin), kept as an
+// index list in LDS, and usually finishes its R selections in the first one.
+// Entry i belongs to wave (i / 64) % kLongWaves, lane i % 64 in the distance
+// pass and in full-list windows; in a listed window, list slot j belongs to
+// thread j. Every pass touches an entry from one thread only.
+constexpr uint32_t kLongWin = 2048;   // target entries of a hub window
+constexpr uint32_t kLongList = 4096;  // LDS capacity of a window list
+constexpr uint32_t kLongBins = 4096;  // histogram bins per radix pass
+
 template <int DT, int CPL>
 __global__ __launch_bounds__(kLongBlock) void k_csr_long(RowSet rs, Graph G, Labels L, CsrArgs A,
                                                           const uint32_t* rows) {
@@ -946,9 +961,14 @@ __global__ __launch_bounds__(kLongBlock) void k_csr_long(RowSet rs, Graph G, Lab
   __shared__ float wd[kLongWaves][64];
   __shared__ int rk[kLongWaves];
   __shared__ uint32_t ri[kLongWaves], rx[kLongWaves];
-  __shared__ uint32_t out[64];
+  __shared__ uint32_t out[64], outx[64];
+  __shared__ uint32_t hist[kLongBins];
+  __shared__ uint32_t wlist[kLongList];
+  __shared__ uint32_t wtot[kLongWaves];
+  __shared__ uint32_t sh[3];
   const uint32_t row = rows[blockIdx.x];
   const uint32_t w = wave_index(), lane = lane_id();
+  const uint32_t tid = w * 64u + lane;
   const uint32_t grp = lane >> 3, sub = lane & 7u;
   const uint32_t N = G.N, R = G.R;
   const size_t gb = (size_t)row * R;
@@ -1001,75 +1021,200 @@ __global__ __launch_bounds__(kLongBlock) void k_csr_long(RowSet rs, Graph G, Lab
       }
     }
   }
-  // Each lane tracks the smallest live (distance, id, index) of its own
-  // entries; entries ascend per lane, so ties keep the first.
-  int bk = INT_MAX;
-  uint32_t bid = DANCE_INV, bix = DANCE_INV;
-  auto consider = [&](float d, uint32_t c, uint32_t i) {
-    if (!(d <= FLT_MAX)) return;
-    const int k = fkey(d);
-    if (k < bk || (k == bk && c < bid)) {
-      bk = k;
-      bid = c;
-      bix = i;
-    }
+  __syncthreads();  // windows read entries of other waves
+
+  // Key of a selectable entry (live, finite distance >= 0): its bit pattern.
+  auto key_of = [&](uint32_t i, uint32_t& u) -> bool {
+    if (brem[i]) return false;
+    const float d = bd[i];
+    if (!(d <= FLT_MAX)) return false;
+    u = (uint32_t)fkey(d);
+    return true;
   };
-  for (uint32_t b = w * 64u; b < n; b += kStride) {
-    const uint32_t i = b + lane;
-    if (i < n && !brem[i]) consider(bd[i], id_at(i), i);
-  }
-  uint32_t sel = 0;
-  while (sel < R) {
-    const int M = wave_min_i(bk);
-    const uint32_t I = wave_min_u(bk == M ? bid : DANCE_INV);
-    const uint32_t X = wave_min_u(bk == M && bid == I ? bix : DANCE_INV);
-    if (lane == 0) {
-      rk[w] = M;
-      ri[w] = I;
-      rx[w] = X;
+  // Block-wide exclusive scan of one value per thread; *total gets the sum.
+  auto block_scan = [&](uint32_t v, uint32_t* total) -> uint32_t {
+    const uint32_t ex = wave_excl_scan_u(v);
+    if (lane == 63) wtot[w] = ex + v;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+    for (uint32_t q = 0; q < kLongWaves; ++q) {
+      const uint32_t t = wtot[q];
+      before += q < w ? t : 0u;
+      all += t;
+    }
+    __syncthreads();  // wtot is rewritten by the next scan
+    *total = all;
+    return before + ex;
+  };
+  // Radix pass over the selectable keys >= lo (and with bits 30..19 equal to
+  // `bin` unless bin is ~0u): histogram of key bits [shift, shift + 12).
+  // Returns the bin where the running count, offset by `prior`, reaches
+  // kLongWin (sh[0]) and the count before it (sh[1]); *total as block_scan.
+  auto radix_pass = [&](uint32_t lo, uint32_t bin, uint32_t shift, uint32_t prior, uint32_t* total) {
+    for (uint32_t q = tid; q < kLongBins; q += kLongBlock) hist[q] = 0u;
+    __syncthreads();
+    for (uint32_t i = tid; i < n; i += kLongBlock) {
+      uint32_t u;
+      if (key_of(i, u) && u >= lo && (bin == ~0u || (u >> 19) == bin)) atomicAdd(&hist[(u >> shift) & 4095u], 1u);
     }
     __syncthreads();
-    const int mk = lane < kLongWaves ? rk[lane] : INT_MAX;
-    const uint32_t mi = lane < kLongWaves ? ri[lane] : DANCE_INV;
-    const uint32_t mx = lane < kLongWaves ? rx[lane] : DANCE_INV;
-    __syncthreads();  // rk / ri / rx are rewritten by the next selection
-    const int GM = wave_min_i(mk);
-    if (GM == INT_MAX) break;
-    const uint32_t GI = wave_min_u(mk == GM ? mi : DANCE_INV);
-    const uint32_t GX = wave_min_u(mk == GM && mi == GI ? mx : DANCE_INV);
-    const uint32_t msel = use_mask ? bmask[GX] : 0u;
-    if (w == 0 && lane == 0) out[sel] = GI;
-    if (w == ((GX >> 6) % kLongWaves) && lane == (GX & 63u)) brem[GX] = 1;
-    if (++sel == R) break;  // removals after the last selection change nothing
-    // one pass per selection: the occlusion rule on this lane's entries,
-    // then the survivors' minimum for the next selection
-    uint4 bv[CPL];
-    load_row<CPL>(rs, GI, true, sub, bv);
-    bk = INT_MAX;
-    bid = bix = DANCE_INV;
-    for (uint32_t b = w * 64u; b < n; b += kStride) {
-      const uint32_t i = b + lane;
-      bool live = i < n && !brem[i];
-      const uint32_t c = live ? id_at(i) : DANCE_INV;
-      const bool need = live && (use_mask ? (bmask[i] & ~msel) == 0u : covers(L, row, GI, c));
-      const uint64_t m = wballot(need);
-      if (m) {
-        const uint32_t cnt = popc64(m), pos = mbcnt64(m);
-        if (need) lst[pos] = c;
-        wave_sync();
-        batch_dist<DT, CPL>(rs, bv, lst, lsd, cnt, grp, sub);
-        npd += cnt;
-        if (need) {
-          const float pd = lsd[pos];
-          if (pd > 0.0f && A.alpha * pd <= bd[i]) {
-            brem[i] = 1;
-            live = false;
-          }
+    constexpr uint32_t kPer = kLongBins / kLongBlock;
+    uint32_t v = 0;
+    for (uint32_t q = 0; q < kPer; ++q) v += hist[tid * kPer + q];
+    const uint32_t ex = prior + block_scan(v, total);
+    if (ex < kLongWin && kLongWin <= ex + v) {
+      uint32_t c = ex;
+      for (uint32_t q = 0; q < kPer; ++q) {
+        const uint32_t h = hist[tid * kPer + q];
+        if (c + h >= kLongWin) {
+          sh[0] = tid * kPer + q;
+          sh[1] = c;
+          break;
         }
-        wave_sync();
+        c += h;
       }
-      if (live) consider(bd[i], c, i);
     }
+    __syncthreads();
+  };
+
+  uint32_t sel = 0;
+  uint32_t lo = 0u, hi = ~0u;
+  bool listed = false;
+  uint32_t m = n;  // entries of the current window's iteration space
+  bool done = false;
+  bool first = true;
+  while (!done) {
+    if (!first || n > kLongWin) {
+      if (!first) {
+        if (hi == ~0u) break;
+        lo = hi + 1u;
+      }
+      uint32_t total;
+      radix_pass(lo, ~0u, 19u, 0u, &total);
+      if (total == 0u) break;
+      if (total <= kLongWin) {
+        hi = ~0u;
+      } else {
+        const uint32_t bin = sh[0], prior = sh[1];
+        __syncthreads();
+        uint32_t t2;
+        radix_pass(lo, bin, 7u, prior, &t2);
+        hi = (bin << 19) | (sh[0] << 7) | 127u;
+        __syncthreads();
+      }
+      if (tid == 0) sh[2] = 0u;
+      __syncthreads();
+      for (uint32_t i = tid; i < n; i += kLongBlock) {
+        uint32_t u;
+        if (key_of(i, u) && u >= lo && u <= hi) {
+          const uint32_t p = atomicAdd(&sh[2], 1u);
+          if (p < kLongList) wlist[p] = i;
+        }
+      }
+      __syncthreads();
+      const uint32_t cnt = sh[2];
+      listed = cnt <= kLongList;
+      m = listed ? cnt : n;
+      __syncthreads();
+    }
+    first = false;
+    // Entry of iteration slot j of the window (j < m), or none.
+    auto entry = [&](uint32_t j, uint32_t& i) -> bool {
+      if (j >= m) return false;
+      if (listed) {
+        i = wlist[j];
+        return true;
+      }
+      i = j;
+      if (lo == 0u && hi == ~0u) return true;
+      uint32_t u;
+      return key_of(i, u) && u >= lo && u <= hi;
+    };
+    // Each lane tracks the smallest live (distance, id) of its own window
+    // entries and the iteration slot that holds it (live ids are unique, so
+    // the slot only names the entry's owner).
+    int bk = INT_MAX;
+    uint32_t bid = DANCE_INV, bix = DANCE_INV;
+    auto consider = [&](float d, uint32_t c, uint32_t j) {
+      if (!(d <= FLT_MAX)) return;
+      const int k = fkey(d);
+      if (k < bk || (k == bk && c < bid)) {
+        bk = k;
+        bid = c;
+        bix = j;
+      }
+    };
+    // The occlusion rule of selection (gi, gx) on the window's live entries;
+    // with track, the survivors' minimum for the next selection.
+    auto occlude = [&](uint32_t gi, uint32_t gx, bool track) {
+      const uint32_t msel = use_mask ? bmask[gx] : 0u;
+      uint4 bv[CPL];
+      load_row<CPL>(rs, gi, true, sub, bv);
+      for (uint32_t jb = w * 64u; jb < m; jb += kStride) {
+        uint32_t i = 0;
+        bool live = entry(jb + lane, i) && i != gx && !brem[i];
+        const uint32_t c = live ? id_at(i) : DANCE_INV;
+        const bool need = live && (use_mask ? (bmask[i] & ~msel) == 0u : covers(L, row, gi, c));
+        const uint64_t mk = wballot(need);
+        if (mk) {
+          const uint32_t cnt = popc64(mk), pos = mbcnt64(mk);
+          if (need) lst[pos] = c;
+          wave_sync();
+          batch_dist<DT, CPL>(rs, bv, lst, lsd, cnt, grp, sub);
+          npd += cnt;
+          if (need) {
+            const float pd = lsd[pos];
+            if (pd > 0.0f && A.alpha * pd <= bd[i]) {
+              brem[i] = 1;
+              live = false;
+            }
+          }
+          wave_sync();
+        }
+        if (track && live) consider(bd[i], c, jb + lane);
+      }
+    };
+    // earlier windows' selections, then the window's own minimum
+    for (uint32_t q = 0; q < sel; ++q) occlude(out[q], outx[q], q + 1 == sel);
+    if (sel == 0) {
+      for (uint32_t jb = w * 64u; jb < m; jb += kStride) {
+        uint32_t i = 0;
+        if (entry(jb + lane, i) && !brem[i]) consider(bd[i], id_at(i), jb + lane);
+      }
+    }
+    while (true) {
+      const int M = wave_min_i(bk);
+      const uint32_t I = wave_min_u(bk == M ? bid : DANCE_INV);
+      const uint32_t X = wave_min_u(bk == M && bid == I ? bix : DANCE_INV);
+      if (lane == 0) {
+        rk[w] = M;
+        ri[w] = I;
+        rx[w] = X;
+      }
+      __syncthreads();
+      const int mk = lane < kLongWaves ? rk[lane] : INT_MAX;
+      const uint32_t mi = lane < kLongWaves ? ri[lane] : DANCE_INV;
+      const uint32_t mx = lane < kLongWaves ? rx[lane] : DANCE_INV;
+      __syncthreads();  // rk / ri / rx are rewritten by the next selection
+      const int GM = wave_min_i(mk);
+      if (GM == INT_MAX) break;  // window exhausted
+      const uint32_t GI = wave_min_u(mk == GM ? mi : DANCE_INV);
+      const uint32_t GJ = wave_min_u(mk == GM && mi == GI ? mx : DANCE_INV);
+      const uint32_t GX = listed ? wlist[GJ] : GJ;
+      if (tid == 0) {
+        out[sel] = GI;
+        outx[sel] = GX;
+      }
+      if (tid == GJ % kLongBlock) brem[GX] = 1;  // the slot's owner, which alone reads it in this window
+      if (++sel == R) {  // removals after the last selection change nothing
+        done = true;
+        break;
+      }
+      bk = INT_MAX;
+      bid = bix = DANCE_INV;
+      occlude(GI, GX, true);
+    }
+    __syncthreads();  // out / outx / brem visible to the next window
   }
   __syncthreads();
   if (w == 0) {

@@ -164,6 +164,42 @@ def test_filtered_hub_deep_selection():
     assert p["long_max_candidates"] > 2048  # the hub's entries wrap around the workgroup's 16 waves
 
 
+@pytest.mark.parametrize("alpha", [0.5, 1.2])
+def test_filtered_hub_key_windows(alpha):
+    """A hub whose candidate list (distances spread by radius) is longer than
+    the long prune's key window (2048): the prune walks several windows,
+    replaying earlier selections on each."""
+    rng = np.random.default_rng(31)
+    n = 20000
+    x = rng.standard_normal((n, 32)).astype(np.float32)
+    x /= np.linalg.norm(x, axis=1, keepdims=True)
+    x *= rng.uniform(1.0, 3.0, (n, 1)).astype(np.float32)
+    x[0] = 0  # every point's nearest neighbour
+    ls = F.canonical_labels([[0]] * n, 1)
+    starts, gs = F.label_starts(x, ls), F.global_start(x)
+    assert_same(x, ls, starts, gs, 32, 64, 64, 750, 32, alpha=alpha, rounds=1)
+    p = F.last_profile()
+    assert p["long_max_candidates"] > 2 * 2048
+
+
+@pytest.mark.parametrize("alpha", [0.5, 1.2])
+def test_filtered_hub_tied_keys(alpha):
+    """Every candidate of the hub lies at the same distance (u8 rows with
+    exactly eight ones around an all-zero hub): one key window holds more
+    entries than its LDS list (4096), so the prune scans the list with the
+    window's key filter instead."""
+    rng = np.random.default_rng(33)
+    n = 6000
+    x = np.zeros((n, 64), np.uint8)
+    for i in range(1, n):
+        x[i, rng.choice(64, 8, replace=False)] = 1
+    ls = F.canonical_labels([[0]] * n, 1)
+    starts, gs = F.label_starts(x, ls), F.global_start(x)
+    assert_same(x, ls, starts, gs, 32, 64, 64, 750, 32, alpha=alpha, rounds=1)
+    p = F.last_profile()
+    assert p["long_max_candidates"] > 4096
+
+
 @pytest.mark.parametrize("n", [1, 2, 17, 50])
 def test_filtered_tiny(n):
     x, ls = make_case("u8", n, 32, 5, 3, seed=n)
