@@ -249,6 +249,8 @@ def run_c5(args, mode) -> int:
             "scaling": "weak", "vs_baseline": None, "dtype": "u8", "data": "synthetic",
             "config": {"workload": WORKLOADS[mode] + (f" (N overridden to {n})" if args.n else ""), "N": n},
             "build_seconds": round(ms_per_step / 1000.0, 3), "recall@10": recall}
+    Rg = int(F.last_profile()["publish_degree"]) if mode == "c5f" else c["R"]
+    line["graph_check"] = graph_check(torch, graph_t.view(-1)[:n * Rg].view(n, Rg), deg_t, n, Rg)
     if mode == "c5f":
         kp = F.last_profile()
         st = F.last_stats()

@@ -241,6 +241,15 @@ int print_degree_profile(FState& st, const Labels& Ld, uint32_t N, hipStream_t s
 // order), and each row's tasks in that row order. Waves in flight then work
 // on neighbouring rows, whose searches share rows in L2. Results do not depend
 // on the order. Scratch: lsort / lrows (sort), roff (task offsets).
+// Target entries of a long-list prune key window (k_csr_long):
+// DANCE_LONG_WINDOW, default 2048, clamped to 64 .. kLongList / 2. Results do
+// not depend on it.
+static uint32_t long_window() {
+  const char* e = std::getenv("DANCE_LONG_WINDOW");
+  const uint32_t v = e && e[0] ? (uint32_t)std::strtoul(e, nullptr, 10) : 2048u;
+  return std::min(std::max(v, 64u), kLongList / 2u);
+}
+
 int locality_order(const Rows& rows, const Labels& Ld, uint32_t N, uint32_t T, FState& st, ScanWorkspace& scan,
                    SortWorkspace& sort_ws, hipStream_t s, const uint32_t** rorder, const uint32_t** torder) {
   const char* e = std::getenv("DANCE_LOCALITY_CELLS");
@@ -376,9 +385,10 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   // Rows of more than kCsrRegMax candidates (label hubs) are pruned on a
   // second stream, concurrently with the short rows: the largest hub holds
   // one workgroup for tens of ms, which the short rows' kernel then hides.
-  StreamGuard s2g;
+  StreamGuard s2g, s3g;
   DHIP(hipStreamCreate(&s2g.s));
-  const hipStream_t s2 = s2g.s;
+  DHIP(hipStreamCreate(&s3g.s));
+  const hipStream_t s2 = s2g.s, s3 = s3g.s;
   hipEvent_t e0 = E.mark(s);
   hipLaunchKernelGGL(k_random_graph, dim3(grid_thr(N)), dim3(256), 0, s, N, R,
                      std::min(std::min(kBackboneDegree, R), N - 1), kBackboneSeed, ga, da);
@@ -476,21 +486,32 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
     hipEvent_t r3 = E.mark(s);
     const Graph Gb{N, R, gb, db};
     CsrArgs Cs{p.alpha, roff, st.rids.as<const uint32_t>(), boff, st.bd.as<float>(), st.brem.as<uint8_t>(),
-               st.bmask.as<uint32_t>(), ga, da, ctr};
+               st.bmask.as<uint32_t>(), ga, da, ctr, long_window()};
     DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
-      hipEvent_t long_done = nullptr;
-      if (tails[2] > 0) {  // the two kernels write disjoint rows
+      // The three kernels write disjoint rows and run side by side: long
+      // rows beyond the key window (workgroups of kLongWaves waves), the
+      // other long rows (kLongSmallWaves), and k_csr for the short lists.
+      // Both long kernels take the whole longest-first list; each skips the
+      // other's rows.
+      hipEvent_t long_done = nullptr, hub_done = nullptr;
+      if (tails[2] > 0) {
         DHIP(hipStreamWaitEvent(s2, r3, 0));
-        hipLaunchKernelGGL((k_csr_long<decltype(dt)::value, decltype(c)::value>), dim3(tails[2]), dim3(kLongBlock), 0,
-                           s2, rows.rs, Gb, Ld, Cs, lvals[lr]);
+        DHIP(hipStreamWaitEvent(s3, r3, 0));
+        hipLaunchKernelGGL((k_csr_long<decltype(dt)::value, decltype(c)::value, (int)kLongWaves>), dim3(tails[2]),
+                           dim3(kLongBlock), 0, s3, rows.rs, Gb, Ld, Cs, lvals[lr]);
+        DHIP(hipGetLastError());
+        hub_done = E.mark(s3);
+        hipLaunchKernelGGL((k_csr_long<decltype(dt)::value, decltype(c)::value, (int)kLongSmallWaves>),
+                           dim3(tails[2]), dim3(64u * kLongSmallWaves), 0, s2, rows.rs, Gb, Ld, Cs, lvals[lr]);
         DHIP(hipGetLastError());
         long_done = E.mark(s2);
-        if (!long_done) return -1;
+        if (!long_done || !hub_done) return -1;
       }
       hipLaunchKernelGGL((k_csr<decltype(dt)::value, decltype(c)::value>), grid_xcd(N), dim3(kBlock), csr_lds,
                          s, rows.rs, Gb, Ld, Cs);
       DHIP(hipGetLastError());
       if (long_done) DHIP(hipStreamWaitEvent(s, long_done, 0));
+      if (hub_done) DHIP(hipStreamWaitEvent(s, hub_done, 0));
       return 0;
     }));
     hipEvent_t r4 = E.mark(s);

@@ -45,6 +45,8 @@ constexpr uint32_t kCsrLds = 64u + 128u;
 // workgroup of kLongWaves waves per row.
 constexpr uint32_t kLongWaves = 16;
 constexpr uint32_t kLongBlock = 64u * kLongWaves;
+// Long rows that fit one key window use workgroups of this many waves.
+constexpr uint32_t kLongSmallWaves = 4;
 
 // Device counters (u64 each).
 enum : uint32_t {
@@ -839,6 +841,7 @@ struct CsrArgs {
   uint32_t* gout;
   uint32_t* dout;
   unsigned long long* ctr;
+  uint32_t win;  // k_csr_long key-window target, 1 .. kLongList / 2
 };
 
 // canonical_reverse_candidate_count/fill, canonical_csr_candidate_distances
@@ -942,29 +945,36 @@ static __global__ void k_long_rows(uint32_t N, const uint32_t* boff, uint32_t* l
 // processed in windows of ascending distance keys: the occlusion passes of a
 // window cover only its own entries, after replaying on them the selections
 // of earlier windows. A row of at most kLongWin entries is one window (the
-// whole list); a hub row (label hubs reach 358,549 candidates at c5) takes
+// whole list); a longer row (label hubs reach 358,549 candidates at c5) takes
 // its next window as the ~kLongWin smallest remaining keys (two LDS histogram
 // passes: key bits 30..19, then 18..7 inside the crossing bin), kept as an
 // index list in LDS, and usually finishes its R selections in the first one.
-// Entry i belongs to wave (i / 64) % kLongWaves, lane i % 64 in the distance
-// pass and in full-list windows; in a listed window, list slot j belongs to
-// thread j. Every pass touches an entry from one thread only.
-constexpr uint32_t kLongWin = 2048;   // target entries of a hub window
+// kLongWin is the host's CsrArgs::win.
+// Entry i belongs to wave (i / 64) % W, lane i % 64 in the distance pass and
+// in full-list windows; in a listed window, list slot j belongs to thread j.
+// Every pass touches an entry from one thread only. Rows longer than the
+// window run with W = kLongWaves; the other long rows (one window each) run
+// with fewer waves per workgroup, so that more of them share a CU.
 constexpr uint32_t kLongList = 4096;  // LDS capacity of a window list
 constexpr uint32_t kLongBins = 4096;  // histogram bins per radix pass
 
-template <int DT, int CPL>
-__global__ __launch_bounds__(kLongBlock) void k_csr_long(RowSet rs, Graph G, Labels L, CsrArgs A,
-                                                          const uint32_t* rows) {
+template <int DT, int CPL, int W>
+__global__ __launch_bounds__(64 * W) void k_csr_long(RowSet rs, Graph G, Labels L, CsrArgs A, const uint32_t* rows) {
+  // W == kLongWaves: rows longer than the key window; fewer waves: the other
+  // long rows, which are one window (the whole list), more rows per CU.
+  constexpr bool kWin = W == (int)kLongWaves;
+  constexpr uint32_t kBlk = 64u * W;
+  constexpr uint32_t kBins = kWin ? kLongBins : 1u;
+  constexpr uint32_t kList = kWin ? kLongList : 1u;
   __shared__ uint32_t fw[64];
-  __shared__ uint32_t wl[kLongWaves][64];
-  __shared__ float wd[kLongWaves][64];
-  __shared__ int rk[kLongWaves];
-  __shared__ uint32_t ri[kLongWaves], rx[kLongWaves];
+  __shared__ uint32_t wl[W][64];
+  __shared__ float wd[W][64];
+  __shared__ int rk[W];
+  __shared__ uint32_t ri[W], rx[W];
   __shared__ uint32_t out[64], outx[64];
-  __shared__ uint32_t hist[kLongBins];
-  __shared__ uint32_t wlist[kLongList];
-  __shared__ uint32_t wtot[kLongWaves];
+  __shared__ uint32_t hist[kBins];
+  __shared__ uint32_t wlist[kList];
+  __shared__ uint32_t wtot[W];
   __shared__ uint32_t sh[3];
   const uint32_t row = rows[blockIdx.x];
   const uint32_t w = wave_index(), lane = lane_id();
@@ -975,6 +985,7 @@ __global__ __launch_bounds__(kLongBlock) void k_csr_long(RowSet rs, Graph G, Lab
   const uint32_t s0 = A.roff[row], s1 = A.roff[row + 1];
   const uint32_t deg = min(G.d[row], R);
   const uint32_t n = deg + (s1 - s0);
+  if (kWin != (n > A.win)) return;  // the other variant's row (uniform)
   if (w == 0) fw[lane] = lane < deg ? G.g[gb + lane] : DANCE_INV;
   __syncthreads();
   const uint32_t base = A.boff[row];
@@ -986,7 +997,8 @@ __global__ __launch_bounds__(kLongBlock) void k_csr_long(RowSet rs, Graph G, Lab
   float* lsd = wd[w];
   auto id_at = [&](uint32_t i) -> uint32_t { return i < deg ? fw[i] : rids[i - deg]; };
   const bool use_mask = L.off[row + 1] - L.off[row] <= kMaskLabels;
-  constexpr uint32_t kStride = 64u * kLongWaves;
+  constexpr uint32_t kStride = kBlk;
+  const uint32_t kLongWin = A.win;
   uint32_t nd = 0, npd = 0;
   {
     uint4 av[CPL];
@@ -1037,7 +1049,7 @@ __global__ __launch_bounds__(kLongBlock) void k_csr_long(RowSet rs, Graph G, Lab
     if (lane == 63) wtot[w] = ex + v;
     __syncthreads();
     uint32_t before = 0, all = 0;
-    for (uint32_t q = 0; q < kLongWaves; ++q) {
+    for (uint32_t q = 0; q < (uint32_t)W; ++q) {
       const uint32_t t = wtot[q];
       before += q < w ? t : 0u;
       all += t;
@@ -1051,16 +1063,17 @@ __global__ __launch_bounds__(kLongBlock) void k_csr_long(RowSet rs, Graph G, Lab
   // Returns the bin where the running count, offset by `prior`, reaches
   // kLongWin (sh[0]) and the count before it (sh[1]); *total as block_scan.
   auto radix_pass = [&](uint32_t lo, uint32_t bin, uint32_t shift, uint32_t prior, uint32_t* total) {
-    for (uint32_t q = tid; q < kLongBins; q += kLongBlock) hist[q] = 0u;
+    for (uint32_t q = tid; q < kBins; q += kBlk) hist[q] = 0u;
     __syncthreads();
-    for (uint32_t i = tid; i < n; i += kLongBlock) {
+    for (uint32_t i = tid; i < n; i += kBlk) {
       uint32_t u;
-      if (key_of(i, u) && u >= lo && (bin == ~0u || (u >> 19) == bin)) atomicAdd(&hist[(u >> shift) & 4095u], 1u);
+      if (key_of(i, u) && u >= lo && (bin == ~0u || (u >> 19) == bin))
+        atomicAdd(&hist[((u >> shift) & 4095u) % kBins], 1u);
     }
     __syncthreads();
-    constexpr uint32_t kPer = kLongBins / kLongBlock;
+    constexpr uint32_t kPer = (kBins + kBlk - 1u) / kBlk;
     uint32_t v = 0;
-    for (uint32_t q = 0; q < kPer; ++q) v += hist[tid * kPer + q];
+    for (uint32_t q = 0; q < kPer; ++q) v += tid * kPer + q < kBins ? hist[tid * kPer + q] : 0u;
     const uint32_t ex = prior + block_scan(v, total);
     if (ex < kLongWin && kLongWin <= ex + v) {
       uint32_t c = ex;
@@ -1084,11 +1097,9 @@ __global__ __launch_bounds__(kLongBlock) void k_csr_long(RowSet rs, Graph G, Lab
   bool done = false;
   bool first = true;
   while (!done) {
-    if (!first || n > kLongWin) {
-      if (!first) {
-        if (hi == ~0u) break;
-        lo = hi + 1u;
-      }
+    if (!first && hi == ~0u) break;  // the last window is done
+    if (kWin && (!first || n > kLongWin)) {
+      if (!first) lo = hi + 1u;
       uint32_t total;
       radix_pass(lo, ~0u, 19u, 0u, &total);
       if (total == 0u) break;
@@ -1104,16 +1115,16 @@ __global__ __launch_bounds__(kLongBlock) void k_csr_long(RowSet rs, Graph G, Lab
       }
       if (tid == 0) sh[2] = 0u;
       __syncthreads();
-      for (uint32_t i = tid; i < n; i += kLongBlock) {
+      for (uint32_t i = tid; i < n; i += kBlk) {
         uint32_t u;
         if (key_of(i, u) && u >= lo && u <= hi) {
           const uint32_t p = atomicAdd(&sh[2], 1u);
-          if (p < kLongList) wlist[p] = i;
+          if (p < kList) wlist[p] = i;
         }
       }
       __syncthreads();
       const uint32_t cnt = sh[2];
-      listed = cnt <= kLongList;
+      listed = cnt <= kList;
       m = listed ? cnt : n;
       __syncthreads();
     }
@@ -1122,7 +1133,7 @@ __global__ __launch_bounds__(kLongBlock) void k_csr_long(RowSet rs, Graph G, Lab
     auto entry = [&](uint32_t j, uint32_t& i) -> bool {
       if (j >= m) return false;
       if (listed) {
-        i = wlist[j];
+        i = wlist[j % kList];  // j < m <= kList when listed
         return true;
       }
       i = j;
@@ -1192,20 +1203,20 @@ __global__ __launch_bounds__(kLongBlock) void k_csr_long(RowSet rs, Graph G, Lab
         rx[w] = X;
       }
       __syncthreads();
-      const int mk = lane < kLongWaves ? rk[lane] : INT_MAX;
-      const uint32_t mi = lane < kLongWaves ? ri[lane] : DANCE_INV;
-      const uint32_t mx = lane < kLongWaves ? rx[lane] : DANCE_INV;
+      const int mk = lane < (uint32_t)W ? rk[lane] : INT_MAX;
+      const uint32_t mi = lane < (uint32_t)W ? ri[lane] : DANCE_INV;
+      const uint32_t mx = lane < (uint32_t)W ? rx[lane] : DANCE_INV;
       __syncthreads();  // rk / ri / rx are rewritten by the next selection
       const int GM = wave_min_i(mk);
       if (GM == INT_MAX) break;  // window exhausted
       const uint32_t GI = wave_min_u(mk == GM ? mi : DANCE_INV);
       const uint32_t GJ = wave_min_u(mk == GM && mi == GI ? mx : DANCE_INV);
-      const uint32_t GX = listed ? wlist[GJ] : GJ;
+      const uint32_t GX = listed ? wlist[GJ % kList] : GJ;
       if (tid == 0) {
         out[sel] = GI;
         outx[sel] = GX;
       }
-      if (tid == GJ % kLongBlock) brem[GX] = 1;  // the slot's owner, which alone reads it in this window
+      if (tid == GJ % kBlk) brem[GX] = 1;  // the slot's owner, which alone reads it in this window
       if (++sel == R) {  // removals after the last selection change nothing
         done = true;
         break;
