@@ -255,28 +255,46 @@ def run_c5(args, mode) -> int:
         kp = F.last_profile()
         st = F.last_stats()
         V = c["dim"]
-        kernels = {"k_task_search": (kp["task_search_ms"], kp["task_dist"] * V),
-                   "k_row": (kp["row_ms"], (kp["union_dist"] + kp["work_dist"] + kp["prune_dist"]) * V),
+        # algorithmic bytes: vector rows of the distances, adjacency rows of
+        # the expansions (4 R + 4 bytes: ids and degree) and the 32-byte label
+        # rows of the membership tests
+        adj = 4 * c["R"] + 4
+        task_b = kp["task_dist"] * V + kp["task_expansions"] * adj + kp["task_label_reads"] * 32
+        row_b = ((kp["union_dist"] + kp["work_dist"] + kp["prune_dist"]) * V + kp["union_expansions"] * adj
+                 + kp["union_label_reads"] * 32)
+        kernels = {"k_task_search": (kp["task_search_ms"], task_b), "k_row": (kp["row_ms"], row_b),
                    "k_csr": (kp["csr_ms"], (kp["csr_dist"] + kp["csr_prune_dist"]) * V)}
         name = max(kernels, key=lambda k: kernels[k][0])
         ms, by = kernels[name]
-        achieved = by / (ms * 1e-3) / 1e9 if ms > 0 else 0.0  # bytes and time summed over the rounds
-        line["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
-                            "avg_launch_ms": round(ms / kp["rounds"], 3),
-                            "algorithmic_bytes_per_launch": by / kp["rounds"]}
+        rounds = kp["rounds"]
+        avg_ms = ms / rounds
+        algo_gbs = by / (ms * 1e-3) / 1e9 if ms > 0 else 0.0  # bytes and time summed over the rounds
+        line["roofline"] = {"bound": "hbm", "achieved": None, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": None,
+                            "traffic": None, "kernel": name, "avg_launch_ms": round(avg_ms, 3),
+                            "algorithmic_bytes_per_launch": by / rounds, "algorithmic_GBps": round(algo_gbs, 1),
+                            "vector_bytes_per_launch": kp["task_dist"] * V / rounds if name == "k_task_search"
+                            else None}
         traffic_file = os.path.join(ROOT, "profiles", "traffic_c5f.json")
         if os.path.exists(traffic_file) and args.n is None:
             with open(traffic_file) as f:
                 tj = json.load(f)
-            if tj.get("kernel") == name:
-                line["roofline"]["traffic"] = tj.get("hbm_bytes_per_launch")
+            per = [x["read_bytes"] + x["write_bytes"] for x in tj.get("kernels", {}).get(name, [])]
+            if per:
+                traffic = sum(per) / len(per)
+                achieved = traffic / (avg_ms * 1e-3) / 1e9
+                line["roofline"].update({"achieved": round(achieved, 1), "frac": round(achieved / HBM_PEAK_GBS, 4),
+                                         "traffic": traffic, "traffic_source": tj["source"],
+                                         "traffic_over_algorithmic": round(traffic / (by / rounds), 3)})
+        if line["roofline"]["achieved"] is None:  # no measured traffic: the algorithmic rate
+            line["roofline"].update({"achieved": round(algo_gbs, 1), "frac": round(algo_gbs / HBM_PEAK_GBS, 4)})
         line["stage_ms"] = {k: round(kp[k], 2) for k in ("backbone_ms", "task_search_ms", "row_ms", "reverse_ms",
                                                         "csr_ms", "publish_ms", "diagnostics_ms", "total_ms")}
         line["config"]["published_degree"] = kp["publish_degree"]
         line["counters"] = {k: kp[k] for k in ("task_dist", "union_dist", "work_dist", "prune_dist", "csr_dist",
                                                "csr_prune_dist", "merged_candidates", "quota_dropped",
-                                               "reverse_edges", "touched_rows", "long_lists", "long_max_candidates")}
+                                               "reverse_edges", "touched_rows", "long_lists", "long_max_candidates",
+                                               "task_expansions", "task_label_reads", "union_expansions",
+                                               "union_label_reads")}
         line["diagnostics"] = {k: st[k] for k in ("invalid_neighbor_count", "self_loop_count", "out_degree_min",
                                                   "out_degree_max", "out_degree_avg", "avg_common_label_out_degree",
                                                   "low_common_label_degree_count")}

@@ -125,6 +125,8 @@ class DanceFilteredProfile(C.Structure):
         + [("publish_ms", C.c_double)]
         + [(n, C.c_uint64) for n in ("publish_dist", "publish_touched", "publish_long_entries")]
         + [("publish_degree", C.c_uint32), ("reserved0", C.c_uint32)]
+        + [(n, C.c_uint64) for n in ("task_expansions", "task_label_reads", "union_expansions",
+                                     "union_label_reads")]
     )
 
 

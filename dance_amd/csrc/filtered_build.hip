@@ -348,7 +348,7 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   DCHECK(st.boff.alloc((size_t)(N + 1) * 4));
   DCHECK(st.lrows.alloc((size_t)N * 4));
   DCHECK(st.lsort.alloc((size_t)N * 12));  // keys (2 buffers) + a second value buffer
-  DCHECK(st.lcount.alloc(4));
+  DCHECK(st.lcount.alloc(8));  // long rows, rows beyond the key window
   DCHECK(st.ctr.alloc((size_t)kCtrStripes * kNumCounters * 8));
   DCHECK(st.d32.alloc(8 * 4));
   DCHECK(st.d64.alloc(8 * 8));
@@ -468,16 +468,17 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
     hipLaunchKernelGGL(k_big_sizes, dim3(grid_thr((uint64_t)N + 1)), dim3(256), 0, s, N, R, db, roff, boff);
     DHIP(hipGetLastError());
     DCHECK(scan_exclusive(boff, (size_t)N + 1, scan, s));
-    DHIP(hipMemsetAsync(st.lcount.p, 0, 4, s));
+    DHIP(hipMemsetAsync(st.lcount.p, 0, 8, s));
+    const uint32_t win = long_window();
     uint32_t* lkeys[2] = {st.lsort.as<uint32_t>(), st.lsort.as<uint32_t>() + N};
     uint32_t* lvals[2] = {st.lrows.as<uint32_t>(), st.lsort.as<uint32_t>() + 2 * (size_t)N};
-    hipLaunchKernelGGL(k_long_rows, dim3(grid_thr(N)), dim3(256), 0, s, N, boff, lvals[0], lkeys[0],
+    hipLaunchKernelGGL(k_long_rows, dim3(grid_thr(N)), dim3(256), 0, s, N, boff, win, lvals[0], lkeys[0],
                        st.lcount.as<uint32_t>());
     DHIP(hipGetLastError());
-    uint32_t tails[3] = {0, 0, 0};
+    uint32_t tails[4] = {0, 0, 0, 0};
     DHIP(hipMemcpyAsync(&tails[0], roff + N, 4, hipMemcpyDeviceToHost, s));
     DHIP(hipMemcpyAsync(&tails[1], boff + N, 4, hipMemcpyDeviceToHost, s));
-    DHIP(hipMemcpyAsync(&tails[2], st.lcount.p, 4, hipMemcpyDeviceToHost, s));
+    DHIP(hipMemcpyAsync(&tails[2], st.lcount.p, 8, hipMemcpyDeviceToHost, s));
     DHIP(hipStreamSynchronize(s));
     reverse_edges += tails[0];
     DCHECK(ensure_big(st, tails[1]));
@@ -486,26 +487,29 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
     hipEvent_t r3 = E.mark(s);
     const Graph Gb{N, R, gb, db};
     CsrArgs Cs{p.alpha, roff, st.rids.as<const uint32_t>(), boff, st.bd.as<float>(), st.brem.as<uint8_t>(),
-               st.bmask.as<uint32_t>(), ga, da, ctr, long_window()};
+               st.bmask.as<uint32_t>(), ga, da, ctr, win};
     DCHECK(with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
       // The three kernels write disjoint rows and run side by side: long
-      // rows beyond the key window (workgroups of kLongWaves waves), the
-      // other long rows (kLongSmallWaves), and k_csr for the short lists.
-      // Both long kernels take the whole longest-first list; each skips the
-      // other's rows.
+      // rows beyond the key window (the first tails[3] of the longest-first
+      // list; workgroups of kLongWaves waves), the other long rows
+      // (kLongSmallWaves), and k_csr for the short lists.
       hipEvent_t long_done = nullptr, hub_done = nullptr;
-      if (tails[2] > 0) {
-        DHIP(hipStreamWaitEvent(s2, r3, 0));
+      const uint32_t hubs = tails[3], rest = tails[2] - tails[3];
+      if (hubs > 0) {
         DHIP(hipStreamWaitEvent(s3, r3, 0));
-        hipLaunchKernelGGL((k_csr_long<decltype(dt)::value, decltype(c)::value, (int)kLongWaves>), dim3(tails[2]),
+        hipLaunchKernelGGL((k_csr_long<decltype(dt)::value, decltype(c)::value, (int)kLongWaves>), dim3(hubs),
                            dim3(kLongBlock), 0, s3, rows.rs, Gb, Ld, Cs, lvals[lr]);
         DHIP(hipGetLastError());
         hub_done = E.mark(s3);
-        hipLaunchKernelGGL((k_csr_long<decltype(dt)::value, decltype(c)::value, (int)kLongSmallWaves>),
-                           dim3(tails[2]), dim3(64u * kLongSmallWaves), 0, s2, rows.rs, Gb, Ld, Cs, lvals[lr]);
+        if (!hub_done) return -1;
+      }
+      if (rest > 0) {
+        DHIP(hipStreamWaitEvent(s2, r3, 0));
+        hipLaunchKernelGGL((k_csr_long<decltype(dt)::value, decltype(c)::value, (int)kLongSmallWaves>), dim3(rest),
+                           dim3(64u * kLongSmallWaves), 0, s2, rows.rs, Gb, Ld, Cs, lvals[lr] + hubs);
         DHIP(hipGetLastError());
         long_done = E.mark(s2);
-        if (!long_done || !hub_done) return -1;
+        if (!long_done) return -1;
       }
       hipLaunchKernelGGL((k_csr<decltype(dt)::value, decltype(c)::value>), grid_xcd(N), dim3(kBlock), csr_lds,
                          s, rows.rs, Gb, Ld, Cs);
@@ -668,6 +672,10 @@ int run_filtered(const Rows& rows, const FParams& p, const uint32_t* h_off, cons
   kp.publish_ms = pub_ms;
   kp.publish_dist = hc[kPubDist];
   kp.publish_touched = hc[kPubTouched];
+  kp.task_expansions = hc[kTaskExp];
+  kp.task_label_reads = hc[kTaskLab];
+  kp.union_expansions = hc[kUnionExp];
+  kp.union_label_reads = hc[kUnionLab];
   kp.publish_long_entries = pub_tail;
   kp.publish_degree = st.out_R;
   kp.out_edges = h64[0];

@@ -64,6 +64,10 @@ enum : uint32_t {
   kBigMax,
   kPubDist,
   kPubTouched,
+  kTaskExp,
+  kTaskLab,
+  kUnionExp,
+  kUnionLab,
   kNumCounters
 };
 // Counters are striped over kCtrStripes copies (by workgroup) so that per-wave
@@ -330,6 +334,7 @@ struct FSearch {
   uint4 av[CPL];
   CanonPool P;
   uint32_t ndist;
+  uint32_t nexp;  // adjacency rows read (uniform)
 
   __device__ __forceinline__ void init(const RowSet& rs_, uint32_t N_, uint32_t row_, uint32_t* lds, uint32_t cap) {
     rs = rs_;
@@ -342,6 +347,7 @@ struct FSearch {
     lst = lds + kVis;
     lsd = reinterpret_cast<float*>(lds + kVis + 64);
     ndist = 0;
+    nexp = 0;
     for (uint32_t i = lane; i < kVis; i += 64) vis[i] = DANCE_INV;
     load_row<CPL>(rs, row, true, sub, av);
     P.init(cap);
@@ -382,6 +388,7 @@ struct FSearch {
   __device__ __forceinline__ void neighbours(const Graph& G, uint32_t u, F&& accept) {
     const uint32_t deg = min(G.d[u], G.R);
     const size_t b = (size_t)u * G.R;
+    ++nexp;
     for (uint32_t j = 0; j < deg; j += 64) {
       const bool in = j + lane < deg;
       batch(in ? G.g[b + j + lane] : DANCE_INV, accept, in && G.sig ? G.sig[b + j + lane] : 0xFFFFFFFFu);
@@ -546,7 +553,12 @@ __global__ __launch_bounds__(kBlock) void k_task_search(RowSet rs, Graph G, Labe
   S.init(rs, N, row, smem + w * kSearchLds, cap);
   auto any = [](uint32_t, uint32_t) { return true; };
   const uint32_t lbit = 1u << sig_bit(label);
-  auto exact = [&](uint32_t c, uint32_t sg) { return (sg & lbit) != 0u && has_exact(L, c, label); };
+  uint32_t nlab = 0;  // per lane: label rows read
+  auto exact = [&](uint32_t c, uint32_t sg) {
+    const bool maybe = (sg & lbit) != 0u;
+    nlab += maybe ? 1u : 0u;
+    return maybe && has_exact(L, c, label);
+  };
   S.batch(lane == 0 ? L.starts[label] : DANCE_INV, any);
   const uint32_t pb = L.lpo[label], pc = L.lpo[label + 1] - pb;
   const uint32_t sc = min(16u, pc);
@@ -558,7 +570,14 @@ __global__ __launch_bounds__(kBlock) void k_task_search(RowSet rs, Graph G, Labe
     out_ids[ob + lane] = h ? S.P.id : DANCE_INV;
     out_d[ob + lane] = h ? S.P.d : FLT_MAX;
   }
-  if (ctr && lane == 0) atomicAdd(ctr_at(ctr, kTaskDist), (unsigned long long)S.ndist);
+  if (ctr) {
+    const uint32_t lab = wave_sum_u(nlab);
+    if (lane == 0) {
+      atomicAdd(ctr_at(ctr, kTaskDist), (unsigned long long)S.ndist);
+      atomicAdd(ctr_at(ctr, kTaskExp), (unsigned long long)S.nexp);
+      atomicAdd(ctr_at(ctr, kTaskLab), (unsigned long long)lab);
+    }
+  }
 }
 
 struct RowArgs {
@@ -637,7 +656,12 @@ __global__ __launch_bounds__(kBlock) void k_row(RowSet rs, Graph G, Labels L, Ro
   S.init(rs, N, row, lds, A.ocap);
   auto any = [](uint32_t, uint32_t) { return true; };
   const uint32_t rsig = L.sig ? L.sig[row] : 0xFFFFFFFFu;
-  auto compat = [&](uint32_t c, uint32_t sg) { return (sg & rsig) != 0u && compatible(L, row, c); };
+  uint32_t nlab = 0;  // per lane: label rows read
+  auto compat = [&](uint32_t c, uint32_t sg) {
+    const bool maybe = (sg & rsig) != 0u;
+    nlab += maybe ? 1u : 0u;
+    return maybe && compatible(L, row, c);
+  };
   for (uint32_t p = lb; p < le; ++p) {
     const uint32_t label = L.lab[p];
     if (label >= L.num_labels) continue;
@@ -654,6 +678,7 @@ __global__ __launch_bounds__(kBlock) void k_row(RowSet rs, Graph G, Labels L, Ro
   const float o_d = oh ? S.P.d : FLT_MAX;
   uint32_t ndist_prune = 0, ndist_work = 0;
   const uint32_t ndist_union = S.ndist;
+  const uint32_t nlab_union = A.ctr ? wave_sum_u(nlab) : 0u;
 
   // 2. merge: task results, old label-sharing neighbours, union results
   MList M;
@@ -781,6 +806,8 @@ __global__ __launch_bounds__(kBlock) void k_row(RowSet rs, Graph G, Labels L, Ro
     A.dout[row] = sel;
     if (A.ctr) {
       atomicAdd(ctr_at(A.ctr, kUnionDist), (unsigned long long)ndist_union);
+      atomicAdd(ctr_at(A.ctr, kUnionExp), (unsigned long long)S.nexp);
+      atomicAdd(ctr_at(A.ctr, kUnionLab), (unsigned long long)nlab_union);
       atomicAdd(ctr_at(A.ctr, kWorkDist), (unsigned long long)ndist_work);
       atomicAdd(ctr_at(A.ctr, kPruneDist), (unsigned long long)ndist_prune);
       atomicAdd(ctr_at(A.ctr, kMergedCands), (unsigned long long)count);
@@ -924,13 +951,18 @@ __global__ __launch_bounds__(kBlock) void k_csr(RowSet rs, Graph G, Labels L, Cs
 
 // Rows whose candidate list is longer than kCsrRegMax (k_big_sizes gave them
 // scratch), with the sort key ~length, so that an ascending sort puts the
-// longest lists (the slowest workgroups) first.
-static __global__ void k_long_rows(uint32_t N, const uint32_t* boff, uint32_t* list, uint32_t* key, uint32_t* count) {
+// longest lists (the slowest workgroups) first. count[0] counts the rows,
+// count[1] those longer than `win` (the prefix of the sorted list that the
+// key-window variant of k_csr_long takes).
+static __global__ void k_long_rows(uint32_t N, const uint32_t* boff, uint32_t win, uint32_t* list, uint32_t* key,
+                                   uint32_t* count) {
   const uint32_t row = blockIdx.x * blockDim.x + threadIdx.x;
   if (row >= N || boff[row + 1] == boff[row]) return;
+  const uint32_t len = boff[row + 1] - boff[row];
   const uint32_t pos = atomicAdd(count, 1u);
   list[pos] = row;
-  key[pos] = ~(boff[row + 1] - boff[row]);
+  key[pos] = ~len;
+  if (len > win) atomicAdd(count + 1, 1u);
 }
 
 // k_csr for one long row per workgroup: the candidate list (same entries as

@@ -79,8 +79,8 @@ __device__ __forceinline__ int dpp(int old, int v) {
   return __builtin_amdgcn_update_dpp(old, v, CTRL, ROWS, 0xF, false);
 }
 
-// Wave-wide reductions with DPP; max/min are exact, so the tree shape does not
-// matter. The full result lands in lane 63 and is read back as a scalar.
+// Wave-wide reductions with DPP; max/min and integer sums are exact, so the
+// tree shape does not matter. The full result lands in lane 63 and is read back as a scalar.
 template <typename Op>
 __device__ __forceinline__ int wave_reduce_i(int v, int ident, Op op) {
   v = op(v, dpp<kDppQuadXor1>(ident, v));
@@ -96,6 +96,9 @@ __device__ __forceinline__ int wave_max_i(int v) {
 }
 __device__ __forceinline__ int wave_min_i(int v) {
   return wave_reduce_i(v, INT_MAX, [](int a, int b) { return min(a, b); });
+}
+__device__ __forceinline__ uint32_t wave_sum_u(uint32_t v) {
+  return (uint32_t)wave_reduce_i((int)v, 0, [](int a, int b) { return (int)((uint32_t)a + (uint32_t)b); });
 }
 __device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
   return (uint32_t)wave_reduce_i((int)v, 0, [](int a, int b) { return (int)max((uint32_t)a, (uint32_t)b); });

@@ -142,6 +142,9 @@ typedef struct DanceFilteredProfile {
     double publish_ms;
     uint64_t publish_dist, publish_touched, publish_long_entries;
     uint32_t publish_degree, reserved0;
+    /* per-label (task) and union-label searches: expansions (adjacency rows
+     * read) and label-row reads of candidates that pass the signature filter */
+    uint64_t task_expansions, task_label_reads, union_expansions, union_label_reads;
 } DanceFilteredProfile;
 
 /* The filtered build of gpu_vamana_filtered_build_{uint8,float} (reference:
