@@ -36,8 +36,13 @@ __device__ __forceinline__ uint64_t dclock() {
 #endif
 }
 
+// 512 slots: a search wave's LDS (visited cache, work row, batch, order) is
+// then 4 KB at C <= 128, so the register budget, not LDS, sets the waves per
+// SIMD (7 for the exact search instead of 6 with 1024 slots; c3 search
+// iterations 1-2 543 -> 499 and 663 -> 624 ms). The cache never changes a
+// result, only how many exact distances repeat.
 #ifndef DANCE_VIS_BITS
-#define DANCE_VIS_BITS 10
+#define DANCE_VIS_BITS 9
 #endif
 constexpr uint32_t kVisBits = DANCE_VIS_BITS;
 constexpr uint32_t kVis = 1u << kVisBits;  // visited cache slots per wave
@@ -699,8 +704,9 @@ struct SearchWave {
 // Waves per SIMD the register allocator must leave room for, for the
 // narrow-row, L <= 128 variants (the common case): DANCE_SEARCH_WAVES_QB
 // (default 5) with the bound compiled in (the allocator would otherwise
-// settle at 4 by a few registers), and DANCE_SEARCH_WAVES (default 6, the
-// LDS limit of 4-wave blocks) without it. No constraint elsewhere.
+// settle at 4 by a few registers), and DANCE_SEARCH_WAVES (default 6)
+// without it; the exact search fits in 68 registers and runs 7 waves per
+// SIMD (asking for 7 changes nothing). No constraint elsewhere.
 #ifndef DANCE_SEARCH_WAVES
 #define DANCE_SEARCH_WAVES 6
 #endif
