@@ -92,7 +92,10 @@ int dance_vamana_build_resident_noalloc(const void *d_data, int dtype, uint32_t 
  * must hold every label of a point (labels x min(R_small, R_stitched)) and be
  * at most 256. label_medoids[l] is the global id of label l's medoid
  * (INVALID for a label without points). Label postings and medoids are host
- * arrays. Returns 0, or -1 with a message. */
+ * arrays. Returns 0, or -1 with a message. The per-label builds run on
+ * several streams at once (DANCE_STITCHED_WORKERS, default 8);
+ * materialize_seconds and build_sum_seconds add up the per-label times, so
+ * they can exceed total_seconds. */
 typedef struct {
     double setup_seconds, materialize_seconds, build_sum_seconds, build_max_seconds, remap_seconds, total_seconds;
     uint64_t memberships, remap_invalid_local_ids, remap_self_loops, remap_duplicate_edges;
