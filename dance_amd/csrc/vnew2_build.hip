@@ -1141,7 +1141,6 @@ static int gather_label_rows(const void* src, int dtype, int store, uint32_t dim
   return 0;
 }
 
-// Callers hold g_mu.
 // Worker threads (streams) of the stitched build: DANCE_STITCHED_WORKERS,
 // default 8, 1..16 (c5 stitched, 100 labels of ~10k rows: 481 ms with 1,
 // 302 ms with 4, 289 ms with 8). Results do not depend on it.
@@ -1151,6 +1150,8 @@ static uint32_t stitched_workers() {
   return std::min(std::max(v, 1u), 16u);
 }
 
+// Callers hold g_mu (the workers take no lock: they touch only their own
+// arena, stream and staging slices).
 static int stitched_build(const StitchedIn& in) {
   const double t0 = now_sec();
   g_last_stitched = DanceStitchedStats{};
