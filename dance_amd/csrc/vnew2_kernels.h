@@ -451,7 +451,29 @@ struct SearchWave {
     const float dj = wdd[j];
     return dj < d || (dj == d && j > s);
   }
+  // Ranks by counting, over one 64-bit key per slot: (usable, distance bits,
+  // ~slot) for usable entries and (0, ~slot) for the others, so that key_j <
+  // key_i exactly when j orders before i (distances are non-negative, their
+  // bits ascend with their values). The keys are staged in the visited cache's
+  // LDS, which run() clears afterwards; rows longer than it holds count on the
+  // row itself.
   __device__ __forceinline__ void ord_init() {
+    if (2u * wdeg <= kVis) {
+      uint64_t* key = reinterpret_cast<uint64_t*>(vis);
+      for (uint32_t i = lane; i < wdeg; i += 64) {
+        const uint32_t hi = usable(i) ? (0x80000000u | __float_as_uint(wdd[i])) : 0u;
+        key[i] = ((uint64_t)hi << 32) | (uint64_t)(0xFFFFFFFFu - i);
+      }
+      wave_sync();
+      for (uint32_t i = lane; i < wdeg; i += 64) {
+        const uint64_t ki = key[i];
+        uint32_t r = 0;
+        for (uint32_t j = 0; j < wdeg; ++j) r += key[j] < ki ? 1u : 0u;
+        ord[r] = i;
+      }
+      wave_sync();
+      return;
+    }
     for (uint32_t i = lane; i < wdeg; i += 64) {
       const bool ui = usable(i);
       const float di = wdd[i];
@@ -601,7 +623,6 @@ struct SearchWave {
     const uint64_t t_run = dclock();
     const GraphBufs& g = a.g;
     const uint32_t N = g.N, R = g.R, C = g.C;
-    for (uint32_t i = lane; i < kVis; i += 64) vis[i] = DANCE_INV;
     load_row<CPL>(a.rs, node, true, sub, av);
     if (QB && a.qb.rows) q_load_self(a.qb, node, qme);
     // Work row := current row with its stored distances (vnew2.cu:1186-1212).
@@ -624,10 +645,60 @@ struct SearchWave {
     P.init(a.L);
     wave_sync();
     ord_init();
+    for (uint32_t i = lane; i < kVis; i += 64) vis[i] = DANCE_INV;
+    wave_sync();
     // Entry point (vnew2.cu:1223-1244).
     process_batch(lane == 0 && a.start < N && a.start != node ? a.start : DANCE_INV);
-    // Own neighbours with stored distances (vnew2.cu:1246-1278).
-    for (uint32_t b = 0; b < deg_self; b += 64) {
+    // Own neighbours with stored distances (vnew2.cu:1246-1278), inserted in
+    // row order. When they fit in one batch, the pool holds at most the entry
+    // point, no two of them (nor one and the entry point) share a visited
+    // slot and none has a NaN distance, the inserts are plain appends: they
+    // go in as one batch (slots in row order, the running max as the
+    // sequential appends leave it). Otherwise one insert after another.
+    bool appended = false;
+    if (deg_self <= 64u && P.size <= 1u) {
+      const uint32_t nb = lane < deg_self ? wid[lane] : DANCE_INV;
+      const float dd = lane < deg_self ? wdd[lane] : FLT_MAX;
+      const bool v = nb != DANCE_INV;
+      const uint64_t m = wballot(v);
+      const uint32_t n = popc64(m);
+      const uint32_t p0 = P.get_id(0);  // the entry point, or DANCE_INV
+      const uint32_t slot = vis_slot(nb);
+      if (v) vis[slot] = lane;
+      wave_sync();
+      const bool clash = v && (vis[slot] != lane || nb == p0 || dd != dd);
+      wave_sync();
+      if (!wballot(clash) && P.size + n <= P.L) {
+        const uint32_t base = P.size;
+        if (v) {
+          lst[mbcnt64(m)] = nb;
+          lsd[mbcnt64(m)] = dd;
+        }
+        wave_sync();
+#pragma unroll
+        for (int r = 0; r < PS; ++r) {
+          const uint32_t p = (uint32_t)r * 64u + lane;
+          if (p >= base && p < base + n) {
+            const float d = lsd[p - base];
+            P.id[r] = lst[p - base];
+            P.mkey[r] = pool_mkey(d);
+            P.skey[r] = pool_skey(P.mkey[r]);
+          }
+        }
+        // sequential appends keep the first strictly larger distance
+        const int M = wave_max_i(v ? fkey(dd) : INT_MIN);
+        if (n > 0 && (P.max_pos < 0 || __int_as_float(M) > P.max_d)) {
+          const int first = ffs64(wballot(v && fkey(dd) == M));  // lowest lane holding the max
+          P.max_pos = uni_i((int)(base + popc64(m & ((1ull << first) - 1ull))));
+          P.max_d = uni_f(__int_as_float(M));
+        }
+        P.size = uni_u(base + n);
+        if (v) vis[slot] = nb;
+        wave_sync();
+        appended = true;
+      }
+    }
+    for (uint32_t b = 0; !appended && b < deg_self; b += 64) {
       const uint32_t i = b + lane;
       const uint32_t nb = i < deg_self ? wid[i] : DANCE_INV;
       const float dd = i < deg_self ? wdd[i] : FLT_MAX;
