@@ -84,3 +84,14 @@ def test_v8_rejects_bad_parameters():
     assert lib.gpu_vamana_build(x.ctypes.data, 64, 8, 16, 32, 8, 16, gp, dp) == -1  # C < R
     assert lib.gpu_vamana_build(x.ctypes.data, 0, 8, 16, 32, 16, 16, gp, dp) == -1
     assert lib.gpu_vamana_build(None, 64, 8, 16, 32, 16, 16, gp, dp) == -1
+
+
+@pytest.mark.parametrize("n", [1, 2, 17, 130])
+def test_v8_tiny_inputs(n):
+    """Tiny builds: one point (no neighbours), two points, rows shorter than R."""
+    x = data("f32", n, 8, seed=n)
+    res = D.vamana_build(x, 8, 16, 16, 8, entry="v8")
+    og, od, om = O.v8_build(x, R=8, L=16, C_=16, STEPS=8)
+    assert res.medoid == om
+    assert np.array_equal(res.degree, od)
+    assert np.array_equal(res.graph, og)
