@@ -257,6 +257,14 @@ static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t ste
 constexpr uint32_t kPruneRankIters = 0xEu;
 static uint32_t prune_rank_iters() { return env_mask("DANCE_PRUNE_RANK_ITERS", kPruneRankIters); }
 
+// uint8 rows in k_prune_rank: every pair's exact distance from MFMA Gram
+// tiles (default), or DANCE_PRUNE_GRAM=0 for exact tests inside the rounds.
+// Both give the same graph.
+static bool prune_gram() {
+  const char* e = std::getenv("DANCE_PRUNE_GRAM");
+  return !(e && e[0] == '0');
+}
+
 static int launch_prune(const Rows& rows, GraphBufs g, uint32_t min_degree, float alpha, const uint32_t* order,
                         VCounters* ctr, const QBoundSet& qb, bool rank_kernel, hipStream_t s) {
   const int cpl = pick_cpl(rows.rs.nch);
@@ -269,15 +277,24 @@ static int launch_prune(const Rows& rows, GraphBufs g, uint32_t min_degree, floa
     if (rank) {
       if constexpr (kHasQB) {
         if (qb.rows) {
-          hipLaunchKernelGGL((k_prune_rank<DT, CPL, true>), xcd_grid(g.N), dim3(kBlock),
+          hipLaunchKernelGGL((k_prune_rank<DT, CPL, kRankBound>), xcd_grid(g.N), dim3(kBlock),
                              (size_t)kWavesPerBlock * prune_rank_lds_words(Cq, true) * 4, s, a, Cq);
           DHIP(hipGetLastError());
           return 0;
         }
       }
-      // without code rows the bound is off: the kernel tests every pair exactly
+      // without code rows the bound is off: uint8 rows take every pair's
+      // distance from Gram tiles, other rows test every pair exactly
       a.qb = QBoundSet{nullptr, 0.0f, 0.0f};
-      hipLaunchKernelGGL((k_prune_rank<DT, CPL, false>), xcd_grid(g.N), dim3(kBlock),
+      if constexpr (DT == DANCE_U8) {
+        if (prune_gram()) {
+          hipLaunchKernelGGL((k_prune_rank<DT, CPL, kRankGram>), xcd_grid(g.N), dim3(kBlock),
+                             (size_t)kWavesPerBlock * prune_rank_lds_words(Cq, true) * 4, s, a, Cq);
+          DHIP(hipGetLastError());
+          return 0;
+        }
+      }
+      hipLaunchKernelGGL((k_prune_rank<DT, CPL, kRankExact>), xcd_grid(g.N), dim3(kBlock),
                          (size_t)kWavesPerBlock * prune_rank_lds_words(Cq, false) * 4, s, a, Cq);
       DHIP(hipGetLastError());
       return 0;
@@ -744,13 +761,16 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
                               (double)p.expansions_iter[it] * (4.0 * R + 4.0) + (double)N * (V + 4.0 * R + 4.0 + 16.0 * C) +
                               (double)p.bound_checks_iter[it] * (kQChunks * 16.0);
     // the rank kernel with the bound reads every candidate's code row once;
-    // k_prune reads the code rows of the pairs it tests
+    // k_prune reads the code rows of the pairs it tests; the rank kernel's
+    // Gram tiles (uint8 rows) read every candidate's row once for all pairs
     const bool q_it = qb.rows && ((q_prune_iters >> it) & 1u);
     const bool rank_it = ((p_rank >> it) & 1u) && C <= kRankCap;
+    const bool gram_it = rank_it && rows.dtype == DANCE_U8 && prune_gram();
     const double qbytes = !q_it ? 0.0
                           : rank_it ? (double)N * C * (kQChunks * 16.0)
                                     : (double)p.prune_bound_checks_iter[it] * (kQChunks * 16.0);
-    p.prune_bytes_iter[it] = (double)p.prune_dist_iter[it] * V + (double)N * (24.0 * C) + qbytes;
+    const double pair_rows = gram_it ? (double)N * C : (double)p.prune_dist_iter[it];
+    p.prune_bytes_iter[it] = pair_rows * V + (double)N * (24.0 * C) + qbytes;
   }
   p.search_bytes = (double)(p.search_dist + p.insert_dist) * V + (double)p.expansions * (4.0 * R + 4.0) +
                    (double)kIters * N * (V + 4.0 * R + 4.0 + 16.0 * C) + (double)p.bound_checks * (kQChunks * 16.0);
@@ -758,6 +778,10 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
                   (double)p.touched_rows * (16.0 * C + 8.0);
   p.prune_bytes = (double)p.prune_dist * V + (double)kIters * N * (24.0 * C) +
                   (double)p.prune_bound_checks * (kQChunks * 16.0);
+  if (timed) {  // the per-launch figures know which launches used Gram tiles
+    p.prune_bytes = 0.0;
+    for (uint32_t it = 0; it < kIters; ++it) p.prune_bytes += p.prune_bytes_iter[it];
+  }
   const double items = (double)N * R;
   const double passes = (bit_length(N) + 7) / 8;
   p.reverse_bytes = (double)kIters * (items * 16.0 + passes * items * 20.0);

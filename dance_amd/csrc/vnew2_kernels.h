@@ -1026,16 +1026,26 @@ __global__ __launch_bounds__(kBlock) void k_prune(PruneArgs a, uint32_t Cp, uint
 // the rounds would test (some open pairs involve ranks already removed), in
 // exchange for no gather inside a round. Rows whose open pairs exceed the
 // list (4 Cq) fall back to exact tests inside the rounds; without the bound
-// (QB false) every round tests its remaining ranks exactly.
+// every round tests its remaining ranks exactly. uint8 rows need no bound:
+// their exact distance of every pair comes from int8 MFMA Gram tiles of the
+// rows themselves (see kRankGram), so every decision is in LDS before the
+// rounds and no pair is gathered twice.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kRankCap = 128;  // candidates per row this kernel takes (C <= 128)
 
+// How k_prune_rank decides its pairs: each round tests its remaining ranks
+// exactly (kRankExact); the quantized bound's MFMA tiles first, then one
+// exact batch for the pairs it leaves open (kRankBound); or, for uint8 rows,
+// the exact distance of every pair from MFMA Gram tiles (kRankGram).
+enum : int { kRankExact = 0, kRankBound = 1, kRankGram = 2 };
+
 // Per-wave LDS: arrays of Cq = C rounded up to 32 entries (ids of the
 // exact-test list; rid, rd by rank; the exact-test list of ranks; per-rank
-// flags), and with the bound the per-rank header {-2 s, r, a, root} (later
-// the open-pair list) and 4 mask words per rank.
-__host__ __device__ constexpr uint32_t prune_rank_lds_words(uint32_t Cq, bool qb) {
-  return 5u * Cq + (qb ? 8u * Cq : 0u);
+// flags), and with MFMA tiles (bound or Gram) 4 words per rank of headers
+// (the bound's {-2 s, r, a, root}, later the open-pair list; the Gram's
+// squared row norms) and 4 mask words per rank.
+__host__ __device__ constexpr uint32_t prune_rank_lds_words(uint32_t Cq, bool tiles) {
+  return 5u * Cq + (tiles ? 8u * Cq : 0u);
 }
 
 typedef int v4i_t __attribute__((ext_vector_type(4)));
@@ -1085,10 +1095,12 @@ __device__ __forceinline__ uint32_t ffs128(uint64_t m0, uint64_t m1) {
 // SIMD; the variant without it fits 6 at rows of up to 4 chunks per lane.
 // Wider rows (and fp16 rows of 4 chunks per lane, whose tail selects take a
 // few more registers) get no floor, so no variant spills.
-template <int DT, int CPL, bool QB>
-constexpr int kRankMinWaves = QB ? 5 : (CPL < 4 || (CPL == 4 && DT != DANCE_F16)) ? 6 : 1;
-template <int DT, int CPL, bool QB>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kRankMinWaves<DT, CPL, QB>, 8))) void k_prune_rank(PruneArgs a, uint32_t Cq) {
+template <int DT, int CPL, int PM>
+constexpr int kRankMinWaves = PM != kRankExact ? 5 : (CPL < 4 || (CPL == 4 && DT != DANCE_F16)) ? 6 : 1;
+template <int DT, int CPL, int PM>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kRankMinWaves<DT, CPL, PM>, 8))) void k_prune_rank(PruneArgs a, uint32_t Cq) {
+  constexpr bool QB = PM == kRankBound, XG = PM == kRankGram;
+  static_assert(!XG || DT == DANCE_U8, "Gram tiles give exact distances of uint8 rows only");
   extern __shared__ uint32_t smem[];
   const uint32_t w = wave_index();
   const uint32_t gw = xcd_block(grid_block(), grid_blocks()) * kWavesPerBlock + w;
@@ -1097,7 +1109,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kRankMin
   const uint32_t node = a.order ? a.order[gw] : gw;
   const uint32_t N = g.N, R = g.R, C = g.C;
   const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;
-  uint32_t* const base = smem + w * prune_rank_lds_words(Cq, QB);
+  uint32_t* const base = smem + w * prune_rank_lds_words(Cq, PM != kRankExact);
   uint32_t* sid = base;                               // ids of the exact-test list (rounds)
   uint32_t* rid = base + Cq;                          // rank -> id
   float* rd = reinterpret_cast<float*>(base + 2 * Cq);  // rank -> distance
@@ -1180,7 +1192,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kRankMin
   [[maybe_unused]] const uint64_t t1 = dclock();
 
   uint32_t npair = 0, nbchk = 0, nbskip = 0;
-  bool batched = false;  // QB: every open pair's decision is in pm before the rounds
+  bool batched = false;  // every needed pair decision is in pm before the rounds
   if constexpr (QB) {
     // 3. the bound's decision for every pair (i, j > i), from int8 MFMA Gram
     // tiles of the code rows: bit j of pm[4 i ..] = pair proven kept.
@@ -1331,6 +1343,106 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kRankMin
       npair = T;
       wave_sync();
     }
+  } else if constexpr (XG) {
+    // 3'. uint8 rows: the exact distance of every pair from int8 MFMA Gram
+    // tiles of the rows themselves. Bytes shifted by -128 (b ^ 0x80) fit
+    // int8, and |a - b|^2 = |a'|^2 + |b'|^2 - 2 a'.b' holds in 32-bit
+    // integers, so each distance is the integer of the octet sum, converted
+    // to float the same way (padding bytes are -128 in both rows and add
+    // nothing). Bit j of pm[4 i ..] = i occludes j, for valid j > i: the test
+    // the rounds would make (alpha d <= d(node, j)); every pair is decided
+    // before the rounds, and each candidate row is gathered once.
+    constexpr uint32_t S = 4u * CPL;  // K-steps of 32 bytes over the padded row
+    int* nrm = reinterpret_cast<int*>(hq);  // |row'|^2 by rank
+    const uint32_t nt = (nvalid + 31u) >> 5;
+    const uint32_t jl = lane & 31u, ih = 4u * (lane >> 5);
+    // 16 shifted bytes of rank `row` for K-step `step` (chunk 2 step + lane/32)
+    auto frag = [&](uint32_t row, uint32_t step) -> v4i_t {
+      v4i_t v = {0, 0, 0, 0};
+      if (row < nvalid) {
+        const uint4 c = a.rs.rows[(size_t)rid[row] * a.rs.stride16 + 2u * step + (lane >> 5)];
+        v = v4i_t{(int)(c.x ^ 0x80808080u), (int)(c.y ^ 0x80808080u), (int)(c.z ^ 0x80808080u),
+                  (int)(c.w ^ 0x80808080u)};
+      }
+      return v;
+    };
+    auto sq4 = [](const v4i_t& f, int acc) {
+      acc = __builtin_amdgcn_sdot4(f.x, f.x, acc, false);
+      acc = __builtin_amdgcn_sdot4(f.y, f.y, acc, false);
+      acc = __builtin_amdgcn_sdot4(f.z, f.z, acc, false);
+      return __builtin_amdgcn_sdot4(f.w, f.w, acc, false);
+    };
+    // lanes l and l + 32 hold the two halves of row t * 32 + l % 32
+    auto put_norm = [&](uint32_t t, int part) {
+      const int n = part + __shfl_xor(part, 32);
+      if (lane < 32u) nrm[t * 32u + lane] = n;
+    };
+    auto decide = [&](uint32_t ti, uint32_t tj, const v16i_t& acc) {
+      const uint32_t j = tj * 32u + jl;  // < nt * 32 <= Cq
+      const bool jv = j < nvalid;
+      const uint32_t nj = (uint32_t)nrm[j];
+      const float dj = rd[j];
+      uint32_t words = 0u;  // lane l < 32 collects the occlusion word of tile row l
+      static_for<0, 16>([&](auto vc) {
+        constexpr uint32_t v = decltype(vc)::value, ir = 8u * (v >> 2) + (v & 3u);
+        const uint32_t i = ti * 32u + ir + ih;
+        const float d = (float)((uint32_t)nrm[i] + nj - 2u * (uint32_t)acc[v]);
+        const uint64_t m = wballot(jv && i < j && a.alpha * d <= dj);
+        words = write_lane<ir>(words, (uint32_t)m);
+        words = write_lane<ir + 4u>(words, (uint32_t)(m >> 32));
+      });
+      if (lane < 32u) pm[4u * (ti * 32u + lane) + tj] = words;
+    };
+    if (CPL == 1 && nt <= 3u) {
+      // up to 96 ranks of 128-byte rows: every fragment loaded at once
+      v4i_t F[3][S];
+      static_for<0, 3>([&](auto tc) {
+        constexpr uint32_t t = decltype(tc)::value;
+#pragma unroll
+        for (uint32_t s = 0; s < S; ++s) F[t][s] = frag(t * 32u + jl, s);
+      });
+      static_for<0, 3>([&](auto tc) {
+        constexpr uint32_t t = decltype(tc)::value;
+        int part = 0;
+#pragma unroll
+        for (uint32_t s = 0; s < S; ++s) part = sq4(F[t][s], part);
+        put_norm(t, part);
+      });
+      wave_sync();
+      static_for<0, 3>([&](auto ic) {
+        constexpr uint32_t ti = decltype(ic)::value;
+        static_for<ti, 3>([&](auto jc) {
+          constexpr uint32_t tj = decltype(jc)::value;
+          if (tj < nt) {
+            v16i_t acc = {};
+#pragma unroll
+            for (uint32_t s = 0; s < S; ++s) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(F[ti][s], F[tj][s], acc, 0, 0, 0);
+            decide(ti, tj, acc);
+          }
+        });
+      });
+    } else {
+      for (uint32_t t = 0; t < nt; ++t) {
+        int part = 0;
+#pragma unroll
+        for (uint32_t s = 0; s < S; ++s) part = sq4(frag(t * 32u + jl, s), part);
+        put_norm(t, part);
+      }
+      wave_sync();
+      for (uint32_t ti = 0; ti < nt; ++ti)
+        for (uint32_t tj = ti; tj < nt; ++tj) {
+          v16i_t acc = {};
+#pragma unroll
+          for (uint32_t s = 0; s < S; ++s)
+            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(frag(ti * 32u + jl, s), frag(tj * 32u + jl, s), acc, 0, 0, 0);
+          decide(ti, tj, acc);
+        }
+    }
+    // Words of tiles below the diagonal or past the last tile stay unset:
+    // the rounds keep only remaining ranks, which lie above the selected one.
+    npair = nvalid > 1u ? nvalid * (nvalid - 1u) / 2u : 0u;
+    batched = true;
+    wave_sync();
   }
 
   // 4. selection rounds on rank masks. Rank r's id, distance and (batched)
@@ -1347,7 +1459,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kRankMin
     r_d[h] = rd[r];
 #pragma unroll
     for (uint32_t q = 0; q < 4; ++q) r_occ[h][q] = 0u;
-    if constexpr (QB) {
+    if constexpr (QB || XG) {
       if (batched) {
 #pragma unroll
         for (uint32_t q = 0; q < 4; ++q) r_occ[h][q] = pm[4u * r + q];
@@ -1395,7 +1507,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kRankMin
     }
     if ((r < 64 ? (dup0 >> r) : (dup1 >> (r - 64))) & 1ull) drop_same_id(sel);
     if (oc >= R) break;
-    if (batched) {  // QB only: the decisions of every open pair are in r_occ
+    if (batched) {  // bound or Gram tiles: every needed decision is in r_occ
       const uint32_t l = r & 63u;
       const bool hi = r >= 64u;
       const uint32_t w0 = (uint32_t)__builtin_amdgcn_readlane((int)(hi ? r_occ[1][0] : r_occ[0][0]), (int)l);

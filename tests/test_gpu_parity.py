@@ -160,6 +160,31 @@ def test_prune_kernels_bitexact(monkeypatch, rank, qbound, R, C):
         assert_state_equal(g, s)
 
 
+@pytest.mark.parametrize("gram", ["1", "0"])
+@pytest.mark.parametrize("dim,levels", [(128, 256), (33, 256), (192, 256), (512, 256), (2048, 256), (128, 3)])
+@pytest.mark.parametrize("R,C", [(64, 80), (32, 128), (16, 100)])
+def test_prune_rank_u8_bitexact(monkeypatch, gram, dim, levels, R, C):
+    """k_prune_rank on uint8 rows, with every pair's distance from int8 MFMA
+    Gram tiles (gram 1) or tested inside the rounds (gram 0), against the
+    oracle: rows of 1, 2, 4 and 16 chunks per lane, a width that is not a
+    multiple of 32 bytes, rows of up to 128 candidates (four tiles), distances
+    above 2^24 (rounded to float), and three-level data (many equal
+    distances), on rows with invalid ids, self loops, repeated ids and FLT_MAX
+    distances."""
+    monkeypatch.setenv("DANCE_PRUNE_RANK_ITERS", "0xF")
+    monkeypatch.setenv("DANCE_PRUNE_GRAM", gram)
+    n = 1500 if dim <= 512 else 300
+    rng = np.random.default_rng(dim + levels + C)
+    data = rng.integers(0, levels, (n, dim)).astype(np.uint8)
+    if levels == 3:
+        data *= 100  # values 0, 100, 200
+    s0 = random_work_state(data, R, C, seed=C + dim)
+    for alpha, md in ((1.0, 0), (1.2, 64), (1.2, 0)):
+        g = D.stage_prune(data, to_dance(s0), md, alpha)
+        s = O.prune(data, s0, md, alpha)
+        assert_state_equal(g, s)
+
+
 @pytest.mark.parametrize("kind", ["f32", "u8"])
 @pytest.mark.parametrize("heavy", [(0, 0), (8, 12)])
 def test_reverse_merge_bitexact(kind, heavy):
