@@ -250,12 +250,16 @@ static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t ste
 // DANCE_PRUNE_RANK_ITERS (default kPruneRankIters), rows of at most kRankCap
 // candidates take k_prune_rank (with the bound's pair decisions from MFMA
 // tiles when qb is on); otherwise, and for wider rows, k_prune. Both give the
-// same graph. The default follows the c3 per-launch times: iteration 0
-// (alpha 1 right after the random graph: few rounds per row, so the rank
-// kernel's up-front sort and all-pairs tiles do not pay) is fastest with
-// k_prune and the bound; iterations 1-3 with k_prune_rank.
-constexpr uint32_t kPruneRankIters = 0xEu;
-static uint32_t prune_rank_iters() { return env_mask("DANCE_PRUNE_RANK_ITERS", kPruneRankIters); }
+// same graph. The default follows the per-launch times: for float rows
+// (c3) iteration 0 (alpha 1 right after the random graph: few rounds per
+// row, so the rank kernel's up-front sort and all-pairs tiles do not pay) is
+// fastest with k_prune and the bound, iterations 1-3 with k_prune_rank; uint8
+// rows (c4), whose rank kernel takes every pair from Gram tiles, are fastest
+// with k_prune_rank in every iteration.
+constexpr uint32_t kPruneRankIters = 0xEu, kPruneRankItersU8 = 0xFu;
+static uint32_t prune_rank_iters(int dtype) {
+  return env_mask("DANCE_PRUNE_RANK_ITERS", dtype == DANCE_U8 ? kPruneRankItersU8 : kPruneRankIters);
+}
 
 // uint8 rows in k_prune_rank: every pair's exact distance from MFMA Gram
 // tiles (default), or DANCE_PRUNE_GRAM=0 for exact tests inside the rounds.
@@ -643,7 +647,7 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   DCHECK(build_schedule(rows, qb, rws, s, &order));
   const uint32_t q_iters = qbound_iters(), q_prune_iters = qbound_prune_iters();
   const uint32_t a_from = alpha_from_iter();
-  const uint32_t p_rank = prune_rank_iters();
+  const uint32_t p_rank = prune_rank_iters(rows.dtype);
   DCHECK(record(e_init, s));
 
   DevBuf snaps;  // timed builds: kIters cumulative counter snapshots
@@ -1700,7 +1704,7 @@ int dance_stage_prune(const void* h_data, int dtype, uint32_t N, uint32_t dim, u
   DCHECK(build_qbound(cx.rows, qbuf, cx.s, &qb));
   // the stage hook runs the kernel the last iteration would use
   DCHECK(launch_prune(cx.rows, cx.st.g(), min_degree, alpha, nullptr, nullptr, qb,
-                      ((prune_rank_iters() >> (kIters - 1)) & 1u) != 0u, cx.s));
+                      ((prune_rank_iters(cx.rows.dtype) >> (kIters - 1)) & 1u) != 0u, cx.s));
   return download_state(cx.st, cur, deg_cur, work, deg_work, wd, cx.s);
 }
 
