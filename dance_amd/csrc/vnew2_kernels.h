@@ -1048,9 +1048,6 @@ __host__ __device__ constexpr uint32_t prune_rank_lds_words(uint32_t Cq, bool ti
   return 5u * Cq + (tiles ? 8u * Cq : 0u);
 }
 
-typedef int v4i_t __attribute__((ext_vector_type(4)));
-typedef int v16i_t __attribute__((ext_vector_type(16)));
-
 // 16 code bytes of rank row `row` for MFMA K-step `step`: code chunk
 // 1 + 2 step + lane/32 (chunk 0 is the header; chunks past 7 are zero).
 // Both operands of a Gram tile take their rows this way, so the tile sums
@@ -1066,24 +1063,6 @@ __device__ __forceinline__ v4i_t code_frag(const QBoundSet& qb, const uint32_t* 
     v = v4i_t{(int)c.x, (int)c.y, (int)c.z, (int)c.w};
   }
   return v;
-}
-
-// v_writelane_b32: lane L of `words` takes the wave-uniform value v; the
-// other lanes keep theirs.
-template <uint32_t L>
-__device__ __forceinline__ uint32_t write_lane(uint32_t words, uint32_t v) {
-  static_assert(L < 64u, "lane index");
-  asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(words) : "s"(v), "n"(L));
-  return words;
-}
-
-// f(integral_constant<uint32_t, 0>) ... f(integral_constant<uint32_t, N-1>).
-template <uint32_t I, uint32_t N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<uint32_t, I>{});
-    static_for<I + 1, N>(f);
-  }
 }
 
 __device__ __forceinline__ uint32_t ffs128(uint64_t m0, uint64_t m1) {
@@ -1358,20 +1337,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kRankMin
     const uint32_t jl = lane & 31u, ih = 4u * (lane >> 5);
     // 16 shifted bytes of rank `row` for K-step `step` (chunk 2 step + lane/32)
     auto frag = [&](uint32_t row, uint32_t step) -> v4i_t {
-      v4i_t v = {0, 0, 0, 0};
-      if (row < nvalid) {
-        const uint4 c = a.rs.rows[(size_t)rid[row] * a.rs.stride16 + 2u * step + (lane >> 5)];
-        v = v4i_t{(int)(c.x ^ 0x80808080u), (int)(c.y ^ 0x80808080u), (int)(c.z ^ 0x80808080u),
-                  (int)(c.w ^ 0x80808080u)};
-      }
-      return v;
+      return row < nvalid ? u8_frag(a.rs, rid[row], step, lane) : v4i_t{0, 0, 0, 0};
     };
-    auto sq4 = [](const v4i_t& f, int acc) {
-      acc = __builtin_amdgcn_sdot4(f.x, f.x, acc, false);
-      acc = __builtin_amdgcn_sdot4(f.y, f.y, acc, false);
-      acc = __builtin_amdgcn_sdot4(f.z, f.z, acc, false);
-      return __builtin_amdgcn_sdot4(f.w, f.w, acc, false);
-    };
+    auto sq4 = [](const v4i_t& f, int acc) { return i8_sq4(f, acc); };
     // lanes l and l + 32 hold the two halves of row t * 32 + l % 32
     auto put_norm = [&](uint32_t t, int part) {
       const int n = part + __shfl_xor(part, 32);
@@ -1380,13 +1348,13 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kRankMin
     auto decide = [&](uint32_t ti, uint32_t tj, const v16i_t& acc) {
       const uint32_t j = tj * 32u + jl;  // < nt * 32 <= Cq
       const bool jv = j < nvalid;
-      const uint32_t nj = (uint32_t)nrm[j];
+      const int nj = nrm[j];
       const float dj = rd[j];
       uint32_t words = 0u;  // lane l < 32 collects the occlusion word of tile row l
       static_for<0, 16>([&](auto vc) {
         constexpr uint32_t v = decltype(vc)::value, ir = 8u * (v >> 2) + (v & 3u);
         const uint32_t i = ti * 32u + ir + ih;
-        const float d = (float)((uint32_t)nrm[i] + nj - 2u * (uint32_t)acc[v]);
+        const float d = u8_gram_dist(nrm[i], nj, acc[v]);
         const uint64_t m = wballot(jv && i < j && a.alpha * d <= dj);
         words = write_lane<ir>(words, (uint32_t)m);
         words = write_lane<ir + 4u>(words, (uint32_t)(m >> 32));

@@ -27,6 +27,7 @@
 #include <stdint.h>
 #include <float.h>
 #include <limits.h>
+#include <type_traits>
 
 #define DANCE_INV 0xFFFFFFFFu
 
@@ -318,4 +319,53 @@ __device__ __forceinline__ void batch_dist(const RowSet& rs, const uint4 (&av)[C
   wave_sync();
 }
 
+// ---------------------------------------------------------------------------
+// int8 MFMA operands (v_mfma_i32_32x32x32_i8: 16 bytes of K per lane).
+// ---------------------------------------------------------------------------
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef int v16i_t __attribute__((ext_vector_type(16)));
+
+// v_writelane_b32: lane L of `words` takes the wave-uniform value v; the
+// other lanes keep theirs.
+template <uint32_t L>
+__device__ __forceinline__ uint32_t write_lane(uint32_t words, uint32_t v) {
+  static_assert(L < 64u, "lane index");
+  asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(words) : "s"(v), "n"(L));
+  return words;
+}
+
+// f(integral_constant<uint32_t, 0>) ... f(integral_constant<uint32_t, N-1>).
+template <uint32_t I, uint32_t N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<uint32_t, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+// Bytes 32 step + 16 (lane / 32) .. +16 of uint8 row `id`, shifted by -128
+// (b ^ 0x80 maps [0, 255] onto int8): one MFMA operand fragment, row id
+// supplied by lane l for tile row l % 32. Rows are zero padded to their
+// chunk group (8 CPL chunks), so steps < 4 CPL stay inside the row; padding
+// bytes become -128 in every row and add nothing to a pair's distance.
+__device__ __forceinline__ v4i_t u8_frag(const RowSet& rs, uint32_t id, uint32_t step, uint32_t lane) {
+  const uint4 c = rs.rows[(size_t)id * rs.stride16 + 2u * step + (lane >> 5)];
+  return v4i_t{(int)(c.x ^ 0x80808080u), (int)(c.y ^ 0x80808080u), (int)(c.z ^ 0x80808080u),
+               (int)(c.w ^ 0x80808080u)};
+}
+
+// acc + the sum of squares of a fragment's 16 int8 values (exact).
+__device__ __forceinline__ int i8_sq4(const v4i_t& f, int acc) {
+  acc = __builtin_amdgcn_sdot4(f.x, f.x, acc, false);
+  acc = __builtin_amdgcn_sdot4(f.y, f.y, acc, false);
+  acc = __builtin_amdgcn_sdot4(f.z, f.z, acc, false);
+  return __builtin_amdgcn_sdot4(f.w, f.w, acc, false);
+}
+
+// Exact uint8 squared distance from a Gram entry: |a'|^2 + |b'|^2 - 2 a'.b'
+// over the shifted rows equals sum (a - b)^2 as an integer (32-bit
+// wrap-around included), converted to float once, as octet_finish does.
+__device__ __forceinline__ float u8_gram_dist(int na, int nb, int dot) {
+  return (float)((uint32_t)na + (uint32_t)nb - 2u * (uint32_t)dot);
+}
 
