@@ -420,7 +420,8 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1)
-    ap.add_argument("--warmup", type=int, default=0)
+    ap.add_argument("--warmup", type=int, default=1,
+                    help="untimed builds first (the first also loads the code objects)")
     ap.add_argument("--config", default="c3", choices=sorted(WORKLOADS))
     ap.add_argument("--n", type=int, default=None, help="override N (parity/debug runs)")
     ap.add_argument("--recall-queries", type=int, default=1000)
