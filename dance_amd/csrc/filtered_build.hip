@@ -712,8 +712,9 @@ int filtered_host(const void* h_data, int src_dtype, const FParams& p, const uin
   const int rc = run_filtered(rows, p, off, lab, starts, s, st, gs, kp);
   if (rc != 0) return rc;
   const double td = now_sec();
-  DHIP(hipMemcpy(h_graph, st.out_g, (size_t)p.N * st.out_R * 4, hipMemcpyDeviceToHost));
-  DHIP(hipMemcpy(h_degree, st.out_d, (size_t)p.N * 4, hipMemcpyDeviceToHost));
+  DHIP(hipDeviceSynchronize());  // every build stream; the staged copies run on streams of their own
+  DCHECK(copy_pageable(h_graph, st.out_g, (size_t)p.N * st.out_R * 4, hipMemcpyDeviceToHost));
+  DCHECK(copy_pageable(h_degree, st.out_d, (size_t)p.N * 4, hipMemcpyDeviceToHost));
   gs.d2h_seconds = now_sec() - td;
   gs.gpu_build_seconds = now_sec() - t0;
   g_fstats = gs;

@@ -863,8 +863,9 @@ static int build_host(const HostT* h_data, int src_dtype, uint32_t N, uint32_t d
     *keep_degree = st.deg_cur.as<uint32_t>();
     st.deg_cur.release();
   } else {
-    DHIP(hipMemcpy(h_graph, st.cur.p, (size_t)N * R * 4, hipMemcpyDeviceToHost));
-    DHIP(hipMemcpy(h_degree, st.deg_cur.p, (size_t)N * 4, hipMemcpyDeviceToHost));
+    DHIP(hipStreamSynchronize(s));  // the staged copies run on streams of their own
+    DCHECK(copy_pageable(h_graph, st.cur.p, (size_t)N * R * 4, hipMemcpyDeviceToHost));
+    DCHECK(copy_pageable(h_degree, st.deg_cur.p, (size_t)N * 4, hipMemcpyDeviceToHost));
   }
   stats.d2h_seconds = now_sec() - td;
   stats.gpu_build_seconds = now_sec() - t0;
@@ -1393,11 +1394,11 @@ static int stitched_build(const StitchedIn& in) {
   st.remap_seconds = now_sec() - tr;
   unsigned long long c3[3] = {0, 0, 0};
   DHIP(hipMemcpyAsync(c3, d_ctr.p, sizeof(c3), hipMemcpyDeviceToHost, s));
-  if (!in.out_on_device) {
-    DHIP(hipMemcpyAsync(in.graph, gg, gcells * 4, hipMemcpyDeviceToHost, s));
-    DHIP(hipMemcpyAsync(in.degree, gd, (size_t)in.N * 4, hipMemcpyDeviceToHost, s));
-  }
   DHIP(hipStreamSynchronize(s));
+  if (!in.out_on_device) {
+    DCHECK(copy_pageable(in.graph, gg, gcells * 4, hipMemcpyDeviceToHost));
+    DCHECK(copy_pageable(in.degree, gd, (size_t)in.N * 4, hipMemcpyDeviceToHost));
+  }
   st.remap_invalid_local_ids = c3[0];
   st.remap_self_loops = c3[1];
   st.remap_duplicate_edges = c3[2];
