@@ -43,6 +43,8 @@ WORKLOADS = {
 }
 C5 = dict(n=1_000_000, dim=192, centers=1024, sigma=0.3, nq=10_000, vocab=20_000, min_labels=1, max_labels=8,
           R=64, L=100, FL=100, C=750, STEPS=64, alpha=1.2, parts=100, Rsmall=32, Lsmall=100, Rstitched=64, Cs=96)
+# profiles that store float input as fp16 (dance_set_profile in include/dance_hip.h)
+FP16_PROFILES = ("FAST_SMALL", "PRO6000_100M", "FILTERED_PAPER")
 METRIC = "Vamana build seconds + vertices/sec at 10M×96 fp32 R64/L100; recall@10"
 
 
@@ -580,7 +582,9 @@ def main() -> int:
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "vertices/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 2), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f32" if dcode == D.DTYPE_F32 else "u8",
+        "scaling": "weak", "vs_baseline": None,
+        # float rows are stored and differenced in binary16 under the fp16 profiles
+        "dtype": ("f16" if args.profile in FP16_PROFILES else "f32") if dcode == D.DTYPE_F32 else "u8",
         "data": "synthetic",
         "config": {"workload": WORKLOADS[args.config] + (f" (N overridden to {n})" if args.n else ""),
                    "N": n, "dim": cfg["dim"], "R": R, "L": cfg["L"], "C": cfg["C"], "STEPS": cfg["STEPS"],
