@@ -1,4 +1,6 @@
-"""Builds dance_amd/libdance_hip.so (gfx950) and the CLI apps in-tree.
+"""Builds dance_amd/libdance_hip.so and libdance_hip.a (gfx950) and the CLI
+apps in-tree. The archive holds the same objects, for callers that link the
+builders statically (as DANCE's CMake links its CUDA builder libraries).
 
 The HIP sources are compiled with hipcc for gfx950 only. Flags that matter:
   -ffp-contract=off   the canonical distance uses explicit fmaf only
@@ -17,6 +19,7 @@ CSRC = os.path.join(HERE, "csrc")
 APPS = os.path.join(HERE, "apps")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libdance_hip.so")
+ARCHIVE = os.path.join(HERE, "libdance_hip.a")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -57,6 +60,11 @@ def build(jobs: int | None = None) -> str:
     tmp = LIB + ".tmp"
     _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *[o for _, o in steps], "-o", tmp, "-pthread"])
     os.replace(tmp, LIB)
+    tmp_a = ARCHIVE + ".tmp"
+    if os.path.exists(tmp_a):
+        os.remove(tmp_a)
+    _run(["ar", "rcs", tmp_a, *[o for _, o in steps]])
+    os.replace(tmp_a, ARCHIVE)
     for src in APP_SOURCES:
         path = os.path.join(APPS, src)
         if os.path.exists(path):

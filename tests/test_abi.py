@@ -38,6 +38,83 @@ def test_library_exports_every_declared_symbol():
         getattr(lib, n)
 
 
+def test_static_archive_defines_every_declared_symbol(tmp_path):
+    """libdance_hip.a (the same objects as the shared library) defines every
+    declared entry point, and a C caller links against it statically."""
+    archive = os.path.join(os.path.dirname(D.LIB_PATH), "libdance_hip.a")
+    assert os.path.exists(archive), "build() writes the archive beside the shared library"
+    out = subprocess.run(["nm", "--defined-only", archive], capture_output=True, text=True).stdout
+    defined = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    missing = header_functions() - defined
+    assert not missing, missing
+    src = tmp_path / "caller.c"
+    src.write_text('#include "gpu_vamana_builder.h"\n#include "gpu_vamana_filtered.h"\n'
+                   "int main(void) { GPUVamanaStats s; GPUFilteredVamanaStats f;\n"
+                   "  gpu_vamana_vnew2_get_last_stats(&s); gpu_vamana_filtered_get_last_stats(&f);\n"
+                   "  return (int)gpu_vamana_vnew2_get_last_medoid(); }\n")
+    exe = tmp_path / "caller"
+    r = subprocess.run(["g++", "-x", "c", str(src), "-x", "none", "-I", os.path.join(ROOT, "include"), archive,
+                        "-L/opt/rocm/lib", "-lamdhip64", "-pthread", "-o", str(exe)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+
+
+STATIC_CALLER = r"""
+#include <stdio.h>
+#include <stdlib.h>
+#include "gpu_vamana_builder.h"
+/* caller N dim R L C STEPS in.u8 out.graph out.degree */
+int main(int argc, char** argv) {
+  if (argc != 10) return 2;
+  const uint32_t N = atoi(argv[1]), dim = atoi(argv[2]), R = atoi(argv[3]), L = atoi(argv[4]),
+                 C = atoi(argv[5]), S = atoi(argv[6]);
+  uint8_t* x = malloc((size_t)N * dim);
+  uint32_t* g = malloc((size_t)N * R * 4);
+  uint32_t* d = malloc((size_t)N * 4);
+  FILE* f = fopen(argv[7], "rb");
+  if (!f || fread(x, 1, (size_t)N * dim, f) != (size_t)N * dim) return 3;
+  fclose(f);
+  if (gpu_vamana_vnew2_build(x, N, dim, R, L, C, S, g, d) != 0) return 4;
+  f = fopen(argv[8], "wb");
+  fwrite(g, 4, (size_t)N * R, f);
+  fclose(f);
+  f = fopen(argv[9], "wb");
+  fwrite(d, 4, N, f);
+  fclose(f);
+  printf("%u\n", gpu_vamana_vnew2_get_last_medoid());
+  return 0;
+}
+"""
+
+
+@pytest.mark.gpu
+def test_static_archive_build_equals_oracle(tmp_path):
+    """A C program linked against libdance_hip.a (no shared library) builds a
+    graph on the GPU, identical to the oracle's."""
+    from oracle import oracle as O
+    archive = os.path.join(os.path.dirname(D.LIB_PATH), "libdance_hip.a")
+    src = tmp_path / "caller.c"
+    src.write_text(STATIC_CALLER)
+    exe = tmp_path / "caller"
+    r = subprocess.run(["g++", "-x", "c", str(src), "-x", "none", "-I", os.path.join(ROOT, "include"), archive,
+                        "-L/opt/rocm/lib", "-lamdhip64", "-pthread", "-o", str(exe)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert "libdance_hip" not in subprocess.run(["ldd", str(exe)], capture_output=True, text=True).stdout
+    N, dim, R, L, Cc, S = 1500, 64, 32, 64, 48, 32
+    x = np.random.default_rng(5).integers(0, 256, (N, dim), dtype=np.uint8)
+    x.tofile(tmp_path / "x.u8")
+    r = subprocess.run([str(exe), *map(str, (N, dim, R, L, Cc, S)), str(tmp_path / "x.u8"), str(tmp_path / "g.u32"),
+                        str(tmp_path / "d.u32")], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    g = np.fromfile(tmp_path / "g.u32", np.uint32).reshape(N, R)
+    d = np.fromfile(tmp_path / "d.u32", np.uint32)
+    og, od, om = O.vnew2_build(x, R, L, Cc, S)
+    assert int(r.stdout.strip()) == om
+    assert np.array_equal(d, od)
+    assert np.array_equal(g, og)
+
+
 def test_merge_cpp_symbol_exported():
     """include/gpu_merge.h declares diskann::merge_shards_gpu with std::string
     arguments (reference include/gpu_merge.h:8-12): the C++ symbol is exported."""
