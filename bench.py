@@ -514,6 +514,28 @@ def main() -> int:
         roofline.update({"achieved": round(achieved, 1), "frac": round(achieved / HBM_PEAK_GBS, 4),
                          "traffic": traffic, "traffic_source": tj["source"],
                          "algorithmic_over_traffic": round(algo / traffic, 3)})
+    else:
+        tj = None
+
+    # Every search and prune launch on its own: live HIP-event time, the
+    # device-counted algorithmic bytes, and (with a committed counter profile
+    # of this workload) the measured HBM bytes, each as a rate and a fraction
+    # of the HBM peak.
+    def per_launch(stage, ms, algo_b, prof):
+        out = []
+        for i, (t, b) in enumerate(zip(ms, algo_b)):
+            e = {"iteration": i, "ms": round(t, 2), "algorithmic_GB": round(b / 1e9, 2),
+                 "algorithmic_frac": round(b / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
+            if prof and i < len(prof):
+                mb = prof[i]["read_bytes"] + prof[i]["write_bytes"]
+                e.update({"measured_GB": round(mb / 1e9, 2),
+                          "measured_frac": round(mb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)})
+            out.append(e)
+        return out
+    kernels = {"search": per_launch("search", kp["search_iter_ms"], kp["search_bytes_iter"],
+                                    tj["search_launches"] if tj else None),
+               "prune": per_launch("prune", kp["prune_iter_ms"], kp["prune_bytes_iter"],
+                                   tj.get("prune_launches") if tj else None)}
 
     # Recall@10 of the resident graph on a query subset.
     nq = min(args.recall_queries, queries.shape[0])
@@ -603,6 +625,7 @@ def main() -> int:
             "merge_dist_iter", "prune_dist_iter", "prune_bound_checks_iter", "prune_bound_skips_iter")},
         "launch_algorithmic_GB": {"search": [round(v / 1e9, 2) for v in kp["search_bytes_iter"]],
                                   "prune": [round(v / 1e9, 2) for v in kp["prune_bytes_iter"]]},
+        "kernels": kernels,
         "prune_rounds": {"rounds": kp["prune_rounds"], "exact_rounds": kp["prune_exact_rounds"]},
         "prune_cycles": ({k: kp[k] for k in ("cyc_prune_rank", "cyc_prune_gram", "cyc_prune_rounds",
                                              "cyc_prune_fill")} if kp["cyc_prune_rounds"] else None),
