@@ -18,7 +18,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 # DANCE_HIP_LIB points at another build of the same library (e.g. one compiled
 # with DANCE_SEARCH_TIMING=1); default is the in-tree build.
-LIB_PATH = os.environ.get("DANCE_HIP_LIB", os.path.join(HERE, "libdance_hip.so"))
+LIB_PATH = os.environ.get("DANCE_HIP_LIB") or os.path.join(HERE, "libdance_hip.so")
 
 DTYPE_F32, DTYPE_U8, DTYPE_F16 = 0, 1, 2
 INVALID = 0xFFFFFFFF
