@@ -175,8 +175,17 @@ static int launch_init(const Rows& rows, GraphBufs g, hipStream_t s) {
 // (default kQBoundIters). Results are identical either way.
 constexpr uint32_t kQBoundIters = 0x1u;  // first iteration: random graph, HBM-bound
 // The prune uses it in the iterations of DANCE_QBOUND_PRUNE_ITERS (default
-// kQBoundPruneIters).
-constexpr uint32_t kQBoundPruneIters = 0xDu;  // iterations 0, 2 and 3 (measured at c3: 1 is faster without)
+// kQBoundPruneIters), and by default also in iteration 1 when iteration 0's
+// prune reached more than a quarter of all candidate pairs (its bound checks
+// per vertex above C (C - 1) / 8): the bound's one batch then replaces dense
+// exact rounds. Measured: iteration 1's prune at c1 (isotropic data, 41% of
+// the pairs reached in iteration 0) 7.07 -> 1.05 ms with the bound; at c2 and
+// c3 (clustered, 7.6%) 4.46 -> 5.54 and 47.4 -> 57.2 ms, so it stays off there.
+constexpr uint32_t kQBoundPruneIters = 0xDu;  // iterations 0, 2 and 3
+static bool qbound_prune_adaptive() {
+  const char* e = std::getenv("DANCE_QBOUND_PRUNE_ITERS");
+  return !(e && e[0]);
+}
 static bool qbound_enabled() {
   const char* e = std::getenv("DANCE_QBOUND");
   return !(e && e[0] == '0');
@@ -604,8 +613,9 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   DCHECK(st.alloc(N, R, C, st.cur.p == nullptr, st.deg_cur.p == nullptr));
   ReverseWs rws;
   DCHECK(rws.alloc(N, R));
-  DevBuf ctr_buf, scores, cands;
+  DevBuf ctr_buf, csum, scores, cands;
   DCHECK(ctr_buf.alloc(sizeof(VCounters) * kCtrStripes));
+  DCHECK(csum.alloc(sizeof(VCounters)));
   DHIP(hipMemsetAsync(ctr_buf.p, 0, sizeof(VCounters) * kCtrStripes, s));
   VCounters* ctr = ctr_buf.as<VCounters>();
   GraphBufs g = st.g();
@@ -645,7 +655,8 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   DCHECK(build_qbound(rows, qbuf, s, &qb));
   const uint32_t* order = nullptr;
   DCHECK(build_schedule(rows, qb, rws, s, &order));
-  const uint32_t q_iters = qbound_iters(), q_prune_iters = qbound_prune_iters();
+  const uint32_t q_iters = qbound_iters();
+  uint32_t q_prune_iters = qbound_prune_iters();  // iteration 1's bit may be set after iteration 0
   const uint32_t a_from = alpha_from_iter();
   const uint32_t p_rank = prune_rank_iters(rows.dtype);
   DCHECK(record(e_init, s));
@@ -682,6 +693,17 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     const QBoundSet qp_it = ((q_prune_iters >> it) & 1u) ? qb : QBoundSet{nullptr, 0.0f, 0.0f};
     DCHECK(launch_prune(rows, g, md, alpha, order, ctr, qp_it, ((p_rank >> it) & 1u) != 0u, s));
     DCHECK(record(iev[it].p1, s));
+    if (it == 0 && qb.rows && qbound_prune_adaptive() && !((q_prune_iters >> 1) & 1u) && kIters > 1) {
+      // pair density of iteration 0's prune (its bound checks), read once
+      hipLaunchKernelGGL(k_ctr_sum, dim3(1), dim3(64), 0, s, static_cast<const VCounters*>(ctr),
+                         csum.as<VCounters>());
+      DHIP(hipGetLastError());
+      VCounters h{};
+      DHIP(hipMemcpyAsync(&h, csum.p, sizeof(VCounters), hipMemcpyDeviceToHost, s));
+      DHIP(hipStreamSynchronize(s));
+      const double pairs = (double)g.C * (double)(g.C > 0 ? g.C - 1 : 0) / 8.0;
+      if ((double)h.prune_bound_checks > pairs * (double)g.N) q_prune_iters |= 2u;
+    }
     if (timed) {  // cumulative counters after this iteration
       hipLaunchKernelGGL(k_ctr_sum, dim3(1), dim3(64), 0, s, static_cast<const VCounters*>(ctr),
                          snaps.as<VCounters>() + it);
@@ -1043,6 +1065,7 @@ static size_t resident_build_bytes(const void* d_data, int dtype, int store, uin
     add(items * 4);                 // snap_sorted
   }
   add(sizeof(VCounters) * kCtrStripes);
+  add(sizeof(VCounters));           // summed counters (the prune bound's choice for iteration 1)
   add(kMedoidCandidates * 4);       // scores
   add(kMedoidCandidates * 4);       // cands
   add((size_t)N * kQChunks * 16);   // code rows of the bound

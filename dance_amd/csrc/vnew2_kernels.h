@@ -84,6 +84,7 @@ __device__ __forceinline__ VCounters* ctr_stripe(VCounters* base) {
 // Sums the counter stripes into one VCounters (a snapshot after a launch).
 static __global__ void k_ctr_sum(const VCounters* __restrict__ stripes, VCounters* __restrict__ out) {
   constexpr uint32_t nf = sizeof(VCounters) / sizeof(unsigned long long);
+  static_assert(nf <= 64, "one thread of the 64-thread launch per field");
   const uint32_t f = threadIdx.x;
   if (f >= nf) return;
   unsigned long long s = 0;
