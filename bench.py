@@ -418,6 +418,139 @@ def cpu_leg(torch, D, O, cfg: dict, name: str, base: np.ndarray, queries: np.nda
     return out
 
 
+def parse_settings(text: str) -> list:
+    """'iters:alpha_from,...' -> [(iters, alpha_from or None)]; alpha_from
+    -1 (or empty) is the reference default, alpha in the last iteration."""
+    out = []
+    for item in text.split(","):
+        it, _, af = item.strip().partition(":")
+        a = int(af) if af.strip() else -1
+        out.append((int(it), None if a < 0 else a))
+    return out
+
+
+def run_gate(args) -> int:
+    """The recall gate of the north star on a whole workload: recall@10 of the
+    GPU graph >= the CPU Vamana's - 0.005 at equal R, L and alpha, both graphs
+    scored by the same GPU search (dance_search_resident) against exact ground
+    truth at L in LS. The GPU graph is built under each (iterations, alpha
+    from) setting (the reference's VAMANA_ITERS and USE_ALPHA_FROM_FIRST_ITER /
+    VAMANA_ALPHA_FINAL_FROM_ITER, here DANCE_VAMANA_ITERS and
+    DANCE_ALPHA_FROM_ITER) and timed (warm, vectors resident). The CPU Vamana
+    (oracle/cpu_baselines.cpp, every host thread) runs --gate-cpu-runs times,
+    each timed; its insertion order depends on thread timing, so the record
+    holds every run's recall, their mean and spread, and each setting passes
+    per L against the mean. Writes one JSON record to --gate-out."""
+    import torch
+    import dance_amd as D
+    from oracle import oracle as O  # the CPU comparator of the gate
+
+    cfg = dict(D.CONFIGS[args.config])
+    n = args.n or cfg["n"]
+    R, L, C_, S = cfg["R"], cfg["L"], cfg["C"], cfg["STEPS"]
+    t0 = time.time()
+    base, queries = D.make_workload(cfg, n=n)
+    nq = min(args.gate_queries, queries.shape[0])
+    q = queries[:nq]
+    dev = torch.device("cuda:0")
+    base_t = torch.from_numpy(base).to(dev)
+    dcode = D.DTYPE_F32 if base.dtype == np.float32 else D.DTYPE_U8
+    gt = ground_truth(base_t, base, q)
+    log(f"gate {args.config}: N={n} queries={nq} workload and ground truth in {time.time() - t0:.1f}s")
+    graph_t = torch.empty((n, R), dtype=torch.int32, device=dev)
+    deg_t = torch.empty((n,), dtype=torch.int32, device=dev)
+
+    def score(start) -> dict:
+        out = {}
+        for Ls in LS:
+            found, _ = D.search_resident(base_t.data_ptr(), dcode, n, cfg["dim"], graph_t.data_ptr(),
+                                         deg_t.data_ptr(), R, start, q, 10, Ls)
+            out[f"L{Ls}"] = round(D.recall_at_k(found, gt, 10), 4)
+        return out
+
+    def set_env(iters, alpha_from):
+        os.environ["DANCE_VAMANA_ITERS"] = str(iters)
+        if alpha_from is None:
+            os.environ.pop("DANCE_ALPHA_FROM_ITER", None)
+        else:
+            os.environ["DANCE_ALPHA_FROM_ITER"] = str(alpha_from)
+
+    def build():
+        D.vamana_build_resident(base_t.data_ptr(), dcode, n, cfg["dim"], R, L, C_, S, graph_t.data_ptr(),
+                                deg_t.data_ptr())
+
+    settings = parse_settings(args.gate_settings)
+    gpu = []
+    for k, (iters, af) in enumerate(settings):
+        set_env(iters, af)
+        if k == 0:
+            build()  # untimed: loads the code objects
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        build()
+        torch.cuda.synchronize()
+        secs = time.perf_counter() - t1
+        medoid = int(D.lib().gpu_vamana_vnew2_get_last_medoid())
+        check = graph_check(torch, graph_t, deg_t, n, R)
+        rec = score(medoid)
+        e = {"iters": iters, "alpha_from": iters - 1 if af is None else af, "reference_default": iters == 4 and af in (None, 3),
+             "build_seconds": round(secs, 3), "vertices_per_s": round(n / secs, 1), "digest": check["digest"],
+             "graph_ok": check["ok"], "mean_degree": check["mean_degree"], "recall": rec}
+        if n <= args.gate_oracle_max:
+            og, od, om = O.vnew2_build(base, R, L, C_, S, iters=iters, alpha_from=af)
+            e["graph_equals_oracle"] = bool(om == medoid and np.array_equal(od, deg_t.cpu().numpy().view(np.uint32))
+                                            and np.array_equal(og, graph_t.cpu().numpy().view(np.uint32)))
+        gpu.append(e)
+        log(f"gate {args.config}: GPU iters={iters} alpha_from={e['alpha_from']} {secs:.3f}s {rec}")
+    os.environ.pop("DANCE_VAMANA_ITERS", None)
+    os.environ.pop("DANCE_ALPHA_FROM_ITER", None)
+
+    runs = []
+    os.environ["DANCE_ORACLE_PROGRESS"] = "1"
+    for r in range(args.gate_cpu_runs):
+        t1 = time.perf_counter()
+        gc, dc, sc = O.cpu_vamana_build(base, R, L, 1.2, 750)
+        secs = time.perf_counter() - t1
+        graph_t.copy_(torch.from_numpy(gc.view(np.int32)))
+        deg_t.copy_(torch.from_numpy(dc.view(np.int32)))
+        rec = score(sc)
+        runs.append({"seconds": round(secs, 2), "vertices_per_s": round(n / secs, 1),
+                     "mean_degree": round(float(dc.mean()), 3), "recall": rec})
+        log(f"gate {args.config}: CPU Vamana run {r + 1} {secs:.1f}s {rec}")
+        del gc, dc
+    keys = [f"L{Ls}" for Ls in LS]
+    cpu_mean = {k: round(float(np.mean([x["recall"][k] for x in runs])), 4) for k in keys}
+    spread = {k: round(float(max(x["recall"][k] for x in runs) - min(x["recall"][k] for x in runs)), 4)
+              for k in keys}
+    for e in gpu:
+        e["delta_vs_cpu_mean"] = {k: round(e["recall"][k] - cpu_mean[k], 4) for k in keys}
+        e["pass"] = {k: e["recall"][k] >= cpu_mean[k] - GATE_TOL for k in keys}
+        e["all_pass"] = all(e["pass"].values())
+        e["passes_every_cpu_run"] = all(e["recall"][k] >= x["recall"][k] - GATE_TOL for x in runs for k in keys)
+    passing = [e for e in gpu if e["all_pass"]]
+    rec = {"config": args.config, "workload": WORKLOADS[args.config] + (f" (N overridden to {n})" if args.n else ""),
+           "N": n, "queries": nq, "tolerance": GATE_TOL,
+           "rule": "GPU recall@10 >= mean CPU Vamana recall@10 - tolerance at every L; same GPU search, exact "
+                   "ground truth (GPU fp32 shortlist, fp64 re-rank)",
+           "cpu_vamana": {"what": "DiskANN's in-memory Vamana build restated in C++/OpenMP (oracle/cpu_baselines.cpp), "
+                                  "R/L/alpha of the workload, maxc 750; Microsoft DiskANN is not available offline",
+                          "threads": O.num_threads(), "cpu_model": cpu_model(), "runs": runs,
+                          "recall_mean": cpu_mean, "recall_spread": spread},
+           "gpu": gpu,
+           "cheapest_passing": (min(passing, key=lambda e: e["build_seconds"])["iters"],
+                                min(passing, key=lambda e: e["build_seconds"])["alpha_from"]) if passing else None,
+           "command": "python bench.py " + " ".join(sys.argv[1:]),
+           "date": time.strftime("%Y-%m-%d %H:%M:%S")}
+    if args.gate_out:
+        os.makedirs(os.path.dirname(os.path.abspath(args.gate_out)), exist_ok=True)
+        with open(args.gate_out, "w") as f:
+            json.dump(rec, f, indent=1)
+    print(json.dumps({"gate": args.config, "cpu_mean": cpu_mean, "spread": spread,
+                      "gpu": [(e["iters"], e["alpha_from"], e["build_seconds"], e["all_pass"]) for e in gpu]}),
+          flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -441,6 +574,15 @@ def main() -> int:
     ap.add_argument("--profile", default="QUALITY")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="run one device copy of this size first (HBM counter calibration)")
+    ap.add_argument("--gate", action="store_true",
+                    help="score the recall gate on the whole workload instead of the bench line (run_gate)")
+    ap.add_argument("--gate-settings", default="4:-1,5:-1,6:-1,4:0,5:0,6:0",
+                    help="GPU settings iterations:alpha_from (-1 = the last iteration, the reference default)")
+    ap.add_argument("--gate-cpu-runs", type=int, default=1, help="timed CPU Vamana runs")
+    ap.add_argument("--gate-queries", type=int, default=10_000)
+    ap.add_argument("--gate-oracle-max", type=int, default=0,
+                    help="largest N at which each GPU graph is also compared with the CPU oracle's")
+    ap.add_argument("--gate-out", default="", help="JSON record of the gate")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -450,6 +592,8 @@ def main() -> int:
 
     if args.config in ("c5f", "c5s"):
         return run_c5(args, args.config)
+    if args.gate:
+        return run_gate(args)
 
     import torch
     import dance_amd as D

@@ -49,6 +49,10 @@ class GPUVamanaStats(C.Structure):
     ]
 
 
+# DANCE_MAX_ITERS of include/dance_hip.h: length of the per-iteration arrays
+MAX_ITERS = 8
+
+
 class DanceKernelProfile(C.Structure):
     _fields_ = [
         ("medoid_ms", C.c_double), ("init_ms", C.c_double), ("search_ms", C.c_double),
@@ -64,13 +68,13 @@ class DanceKernelProfile(C.Structure):
         ("cyc_pool", C.c_uint64), ("cyc_seed", C.c_uint64), ("cyc_total", C.c_uint64),
         ("bound_checks", C.c_uint64), ("bound_skips", C.c_uint64),
         ("prune_bound_checks", C.c_uint64), ("prune_bound_skips", C.c_uint64),
-        ("search_iter_ms", C.c_double * 4), ("prune_iter_ms", C.c_double * 4),
-        ("search_dist_iter", C.c_uint64 * 4), ("insert_dist_iter", C.c_uint64 * 4),
-        ("expansions_iter", C.c_uint64 * 4), ("bound_checks_iter", C.c_uint64 * 4),
-        ("bound_skips_iter", C.c_uint64 * 4), ("merge_dist_iter", C.c_uint64 * 4),
-        ("prune_dist_iter", C.c_uint64 * 4), ("prune_bound_checks_iter", C.c_uint64 * 4),
-        ("prune_bound_skips_iter", C.c_uint64 * 4),
-        ("search_bytes_iter", C.c_double * 4), ("prune_bytes_iter", C.c_double * 4),
+        ("search_iter_ms", C.c_double * MAX_ITERS), ("prune_iter_ms", C.c_double * MAX_ITERS),
+        ("search_dist_iter", C.c_uint64 * MAX_ITERS), ("insert_dist_iter", C.c_uint64 * MAX_ITERS),
+        ("expansions_iter", C.c_uint64 * MAX_ITERS), ("bound_checks_iter", C.c_uint64 * MAX_ITERS),
+        ("bound_skips_iter", C.c_uint64 * MAX_ITERS), ("merge_dist_iter", C.c_uint64 * MAX_ITERS),
+        ("prune_dist_iter", C.c_uint64 * MAX_ITERS), ("prune_bound_checks_iter", C.c_uint64 * MAX_ITERS),
+        ("prune_bound_skips_iter", C.c_uint64 * MAX_ITERS),
+        ("search_bytes_iter", C.c_double * MAX_ITERS), ("prune_bytes_iter", C.c_double * MAX_ITERS),
         ("prune_rounds", C.c_uint64), ("prune_exact_rounds", C.c_uint64),
         ("cyc_prune_rank", C.c_uint64), ("cyc_prune_gram", C.c_uint64), ("cyc_prune_rounds", C.c_uint64),
         ("cyc_prune_fill", C.c_uint64),
@@ -341,9 +345,16 @@ def get_profile() -> str:
 
 
 def last_kernel_profile() -> dict:
+    """DanceKernelProfile of the last standard build; the per-iteration
+    lists hold one entry per iteration the build ran."""
     p = DanceKernelProfile()
     lib().dance_get_last_kernel_profile(C.byref(p))
-    return struct_dict(p)
+    out = struct_dict(p)
+    n = int(out["iterations"])
+    for k, v in out.items():
+        if k.endswith(("_iter", "_iter_ms")):
+            out[k] = v[:n]
+    return out
 
 
 def last_stats(entry: str = "vnew2") -> dict:

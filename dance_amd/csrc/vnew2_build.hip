@@ -64,8 +64,8 @@ struct Profile {
   bool fp16;
   uint32_t heavy_threshold, heavy_sample;
 };
-constexpr uint32_t kIters = 4;              // VAMANA_ITERS
-static_assert(kIters <= 4, "DanceKernelProfile keeps per-iteration times for 4 iterations");
+constexpr uint32_t kDefaultIters = 4;       // VAMANA_ITERS
+constexpr uint32_t kMaxIters = DANCE_MAX_ITERS;  // per-iteration arrays of DanceKernelProfile
 constexpr float kAlpha = 1.2f;              // VAMANA_ALPHA (last iteration only)
 constexpr uint32_t kFinalMinDegree = 64;    // FINAL_MIN_DEGREE
 constexpr uint32_t kWarmupSteps = 64;       // WARMUP_EXPAND_STEPS
@@ -181,7 +181,7 @@ constexpr uint32_t kQBoundIters = 0x1u;  // first iteration: random graph, HBM-b
 // exact rounds. Measured: iteration 1's prune at c1 (isotropic data, 41% of
 // the pairs reached in iteration 0) 7.07 -> 1.05 ms with the bound; at c2 and
 // c3 (clustered, 7.6%) 4.46 -> 5.54 and 47.4 -> 57.2 ms, so it stays off there.
-constexpr uint32_t kQBoundPruneIters = 0xDu;  // iterations 0, 2 and 3
+constexpr uint32_t kQBoundPruneIters = ~0x2u;  // every iteration but 1 (0, 2 and 3 of the default 4)
 static bool qbound_prune_adaptive() {
   const char* e = std::getenv("DANCE_QBOUND_PRUNE_ITERS");
   return !(e && e[0]);
@@ -265,7 +265,7 @@ static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t ste
 // fastest with k_prune and the bound, iterations 1-3 with k_prune_rank; uint8
 // rows (c4), whose rank kernel takes every pair from Gram tiles, are fastest
 // with k_prune_rank in every iteration.
-constexpr uint32_t kPruneRankIters = 0xEu, kPruneRankItersU8 = 0xFu;
+constexpr uint32_t kPruneRankIters = ~0x1u, kPruneRankItersU8 = ~0u;  // from iteration 1 on / all
 static uint32_t prune_rank_iters(int dtype) {
   return env_mask("DANCE_PRUNE_RANK_ITERS", dtype == DANCE_U8 ? kPruneRankItersU8 : kPruneRankIters);
 }
@@ -468,14 +468,28 @@ static int launch_merge(const Rows& rows, GraphBufs g, const RevCsr& rev, const 
   });
 }
 
+// Iteration count (VAMANA_ITERS, gpu_vamana_config.h:78-79, a compile-time
+// constant of the reference; the loop at vnew2.cu:2517-2637): the run-time
+// setting DANCE_VAMANA_ITERS, 1..kMaxIters, default 4. The schedule follows
+// the count: alpha in the last iteration, the fill to kFinalMinDegree in the
+// last, the coarse STEPS cap in the first kCoarseIters. Returns 0 (no
+// iteration) for a value outside the range.
+static uint32_t vamana_iters() {
+  const char* e = std::getenv("DANCE_VAMANA_ITERS");
+  if (!(e && e[0])) return kDefaultIters;
+  char* end = nullptr;
+  const unsigned long v = std::strtoul(e, &end, 10);
+  return (end && *end == '\0' && v >= 1 && v <= kMaxIters) ? (uint32_t)v : 0u;
+}
+
 // Alpha schedule (gpu_vamana_alpha_for_iter, vnew2.cu:201-213): iterations
 // from DANCE_ALPHA_FROM_ITER on prune with alpha, earlier ones with 1. The
 // default is the reference's (the last iteration only); 0 is its
 // USE_ALPHA_FROM_FIRST_ITER=1 and k its VAMANA_ALPHA_FINAL_FROM_ITER=k.
-static uint32_t alpha_from_iter() {
+static uint32_t alpha_from_iter(uint32_t iters) {
   const char* e = std::getenv("DANCE_ALPHA_FROM_ITER");
   if (e && e[0]) return (uint32_t)std::strtoul(e, nullptr, 10);
-  return kIters - 1;
+  return iters - 1;
 }
 
 // Locality schedule (see k_cells_q / k_cells): order[] = vertices sorted by
@@ -590,6 +604,11 @@ static int validate(uint32_t N, uint32_t dim, uint32_t R, uint32_t L, uint32_t C
     std::fprintf(stderr, "[gpu_vamana_build] L=%u exceeds the supported maximum 256\n", L);
     return -1;
   }
+  if (vamana_iters() == 0) {
+    std::fprintf(stderr, "[gpu_vamana_build] DANCE_VAMANA_ITERS=%s is not an iteration count in 1..%u\n",
+                 std::getenv("DANCE_VAMANA_ITERS"), kMaxIters);
+    return -1;
+  }
   uint32_t parts = 1, per = 0;
   reverse_parts(N, R, &parts, &per);
   if (parts > kMaxRevParts) {
@@ -657,16 +676,18 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   DCHECK(build_schedule(rows, qb, rws, s, &order));
   const uint32_t q_iters = qbound_iters();
   uint32_t q_prune_iters = qbound_prune_iters();  // iteration 1's bit may be set after iteration 0
-  const uint32_t a_from = alpha_from_iter();
+  const uint32_t iters = vamana_iters();
+  if (iters == 0) return -1;  // validate() reports it
+  const uint32_t a_from = alpha_from_iter(iters);
   const uint32_t p_rank = prune_rank_iters(rows.dtype);
   DCHECK(record(e_init, s));
 
-  DevBuf snaps;  // timed builds: kIters cumulative counter snapshots
-  if (timed) DCHECK(snaps.alloc(sizeof(VCounters) * kIters));
+  DevBuf snaps;  // timed builds: iters cumulative counter snapshots
+  if (timed) DCHECK(snaps.alloc(sizeof(VCounters) * kMaxIters));
   struct IterEv {
     hipEvent_t s0, s1, r1, m1, p1;
   };
-  IterEv iev[kIters];
+  IterEv iev[kMaxIters];
   for (auto& ie : iev) {
     DCHECK(E.make(&ie.s0));
     DCHECK(E.make(&ie.s1));
@@ -674,12 +695,12 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     DCHECK(E.make(&ie.m1));
     DCHECK(E.make(&ie.p1));
   }
-  for (uint32_t it = 0; it < kIters; ++it) {
+  for (uint32_t it = 0; it < iters; ++it) {
     const float alpha = it >= a_from ? kAlpha : 1.0f;
     uint32_t steps = STEPS;
     if (it < kCoarseIters && steps > kWarmupSteps) steps = kWarmupSteps;
     if (verbose())
-      std::printf("[gpu_vamana_build] iteration %u / %u, alpha=%.3f\n", it + 1, kIters, (double)alpha);
+      std::printf("[gpu_vamana_build] iteration %u / %u, alpha=%.3f\n", it + 1, iters, (double)alpha);
     DCHECK(record(iev[it].s0, s));
     const QBoundSet qb_it = ((q_iters >> it) & 1u) ? qb : QBoundSet{nullptr, 0.0f, 0.0f};
     DCHECK(launch_search(rows, g, L, steps, alpha, start, order, ctr, qb_it, s));
@@ -689,11 +710,11 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     DCHECK(record(iev[it].r1, s));
     DCHECK(launch_merge(rows, g, rev, prof, order, ctr, s));
     DCHECK(record(iev[it].m1, s));
-    const uint32_t md = (it + 1 == kIters) ? kFinalMinDegree : 0u;
+    const uint32_t md = (it + 1 == iters) ? kFinalMinDegree : 0u;
     const QBoundSet qp_it = ((q_prune_iters >> it) & 1u) ? qb : QBoundSet{nullptr, 0.0f, 0.0f};
     DCHECK(launch_prune(rows, g, md, alpha, order, ctr, qp_it, ((p_rank >> it) & 1u) != 0u, s));
     DCHECK(record(iev[it].p1, s));
-    if (it == 0 && qb.rows && qbound_prune_adaptive() && !((q_prune_iters >> 1) & 1u) && kIters > 1) {
+    if (it == 0 && qb.rows && qbound_prune_adaptive() && !((q_prune_iters >> 1) & 1u) && iters > 1) {
       // pair density of iteration 0's prune (its bound checks), read once
       hipLaunchKernelGGL(k_ctr_sum, dim3(1), dim3(64), 0, s, static_cast<const VCounters*>(ctr),
                          csum.as<VCounters>());
@@ -726,17 +747,17 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
       for (size_t f = 0; f < nf; ++f) dst[f] += src[f];
     }
   }
-  VCounters hsnap[kIters] = {};
+  VCounters hsnap[kMaxIters] = {};
   if (timed) {
-    DHIP(hipMemcpyAsync(hsnap, snaps.p, sizeof(hsnap), hipMemcpyDeviceToHost, s));
+    DHIP(hipMemcpyAsync(hsnap, snaps.p, sizeof(VCounters) * iters, hipMemcpyDeviceToHost, s));
     DHIP(hipStreamSynchronize(s));
   }
   DanceKernelProfile p{};
-  p.iterations = kIters;
+  p.iterations = iters;
   p.vector_bytes = rows.vbytes();
   p.medoid_ms = elapsed_ms(e0, e_med);
   p.init_ms = elapsed_ms(e_med, e_init);
-  for (uint32_t it = 0; it < kIters; ++it) {
+  for (uint32_t it = 0; it < iters; ++it) {
     p.search_iter_ms[it] = elapsed_ms(iev[it].s0, iev[it].s1);
     p.prune_iter_ms[it] = elapsed_ms(iev[it].m1, iev[it].p1);
     p.search_ms += p.search_iter_ms[it];
@@ -744,7 +765,7 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     p.merge_ms += elapsed_ms(iev[it].r1, iev[it].m1);
     p.prune_ms += p.prune_iter_ms[it];
   }
-  p.total_ms = elapsed_ms(e0, iev[kIters - 1].p1);
+  p.total_ms = elapsed_ms(e0, iev[iters - 1].p1);
   p.search_dist = hc_ctr.search_dist;
   p.insert_dist = hc_ctr.insert_dist;
   p.expansions = hc_ctr.expansions;
@@ -770,7 +791,7 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   p.cyc_prune_rounds = hc_ctr.cyc_prune_rounds;
   p.cyc_prune_fill = hc_ctr.cyc_prune_fill;
   const double V = rows.vbytes();
-  for (uint32_t it = 0; timed && it < kIters; ++it) {
+  for (uint32_t it = 0; timed && it < iters; ++it) {
     const VCounters& c = hsnap[it];
     const VCounters z{};
     const VCounters& b = it ? hsnap[it - 1] : z;
@@ -799,18 +820,18 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     p.prune_bytes_iter[it] = pair_rows * V + (double)N * (24.0 * C) + qbytes;
   }
   p.search_bytes = (double)(p.search_dist + p.insert_dist) * V + (double)p.expansions * (4.0 * R + 4.0) +
-                   (double)kIters * N * (V + 4.0 * R + 4.0 + 16.0 * C) + (double)p.bound_checks * (kQChunks * 16.0);
+                   (double)iters * N * (V + 4.0 * R + 4.0 + 16.0 * C) + (double)p.bound_checks * (kQChunks * 16.0);
   p.merge_bytes = (double)p.merge_dist * 4.0 + (double)p.reverse_edges * 4.0 +
                   (double)p.touched_rows * (16.0 * C + 8.0);
-  p.prune_bytes = (double)p.prune_dist * V + (double)kIters * N * (24.0 * C) +
+  p.prune_bytes = (double)p.prune_dist * V + (double)iters * N * (24.0 * C) +
                   (double)p.prune_bound_checks * (kQChunks * 16.0);
   if (timed) {  // the per-launch figures know which launches used Gram tiles
     p.prune_bytes = 0.0;
-    for (uint32_t it = 0; it < kIters; ++it) p.prune_bytes += p.prune_bytes_iter[it];
+    for (uint32_t it = 0; it < iters; ++it) p.prune_bytes += p.prune_bytes_iter[it];
   }
   const double items = (double)N * R;
   const double passes = (bit_length(N) + 7) / 8;
-  p.reverse_bytes = (double)kIters * (items * 16.0 + passes * items * 20.0);
+  p.reverse_bytes = (double)iters * (items * 16.0 + passes * items * 20.0);
   if (kp) *kp = p;
   if (stats) {
     stats->search_online_insert_seconds = p.search_ms * 1e-3;
@@ -849,7 +870,7 @@ static int build_host(const HostT* h_data, int src_dtype, uint32_t N, uint32_t d
     std::printf("[gpu_vamana_build] type=%s N=%u dim=%u R=%u L=%u C=%u STEPS=%u alpha=%.3f iters=%u builder=v8 "
                 "profile=%s fp16=%u heavy_cap=0\n",
                 store == DANCE_F16 ? "float16" : (src_dtype == DANCE_U8 ? "uint8" : "float"), N, dim, R, L,
-                C, std::min(STEPS, L), (double)kAlpha, kIters, prof.name, prof.fp16 ? 1u : 0u);
+                C, std::min(STEPS, L), (double)kAlpha, vamana_iters(), prof.name, prof.fp16 ? 1u : 0u);
   DCHECK(check_width(dim, store));
   hipStream_t s = nullptr;
   DHIP(hipStreamCreate(&s));
@@ -1728,7 +1749,7 @@ int dance_stage_prune(const void* h_data, int dtype, uint32_t N, uint32_t dim, u
   DCHECK(build_qbound(cx.rows, qbuf, cx.s, &qb));
   // the stage hook runs the kernel the last iteration would use
   DCHECK(launch_prune(cx.rows, cx.st.g(), min_degree, alpha, nullptr, nullptr, qb,
-                      ((prune_rank_iters(cx.rows.dtype) >> (kIters - 1)) & 1u) != 0u, cx.s));
+                      ((prune_rank_iters(cx.rows.dtype) >> (kDefaultIters - 1)) & 1u) != 0u, cx.s));
   return download_state(cx.st, cur, deg_cur, work, deg_work, wd, cx.s);
 }
 

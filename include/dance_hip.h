@@ -18,6 +18,12 @@ extern "C" {
 /* Element types of the vector rows. */
 enum { DANCE_DTYPE_F32 = 0, DANCE_DTYPE_U8 = 1, DANCE_DTYPE_F16 = 2 };
 
+/* Most build iterations the library runs (the reference's VAMANA_ITERS,
+ * include/gpu_vamana_config.h:78-79, compile-time there; here the run-time
+ * setting DANCE_VAMANA_ITERS, 1..DANCE_MAX_ITERS, default 4), and the length
+ * of the per-iteration arrays below. */
+#define DANCE_MAX_ITERS 8
+
 /* Per-kernel timings (HIP events on the build stream) and algorithmic work
  * counted on the device by each wave. Bytes are algorithmic: one vector row
  * per distance gathered, plus adjacency and work rows as documented in
@@ -40,14 +46,16 @@ typedef struct DanceKernelProfile {
      * enough that the candidate survives (DANCE_QBOUND_PRUNE_ITERS selects
      * the iterations). */
     uint64_t prune_bound_checks, prune_bound_skips;
-    /* per iteration (launch order): search and prune launch times in ms */
-    double search_iter_ms[4], prune_iter_ms[4];
+    /* per iteration (launch order; entries from `iterations` on are 0):
+     * search and prune launch times in ms */
+    double search_iter_ms[DANCE_MAX_ITERS], prune_iter_ms[DANCE_MAX_ITERS];
     /* per iteration: the counters above split by launch, and the algorithmic
      * bytes of each search and prune launch (the totals above are their sums) */
-    uint64_t search_dist_iter[4], insert_dist_iter[4], expansions_iter[4], bound_checks_iter[4],
-        bound_skips_iter[4];
-    uint64_t merge_dist_iter[4], prune_dist_iter[4], prune_bound_checks_iter[4], prune_bound_skips_iter[4];
-    double search_bytes_iter[4], prune_bytes_iter[4];
+    uint64_t search_dist_iter[DANCE_MAX_ITERS], insert_dist_iter[DANCE_MAX_ITERS],
+        expansions_iter[DANCE_MAX_ITERS], bound_checks_iter[DANCE_MAX_ITERS], bound_skips_iter[DANCE_MAX_ITERS];
+    uint64_t merge_dist_iter[DANCE_MAX_ITERS], prune_dist_iter[DANCE_MAX_ITERS],
+        prune_bound_checks_iter[DANCE_MAX_ITERS], prune_bound_skips_iter[DANCE_MAX_ITERS];
+    double search_bytes_iter[DANCE_MAX_ITERS], prune_bytes_iter[DANCE_MAX_ITERS];
     /* RobustPrune selection rounds (vertices x rounds) and the rounds that
      * computed at least one exact pair distance, over all iterations; phase
      * cycles of the rank-mask prune (zero unless built with

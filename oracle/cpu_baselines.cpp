@@ -8,7 +8,11 @@
 //    /root/reference/integrations/dance-diskann-78256bba.patch) cannot be
 //    fetched offline, so this restatement stands in as the CPU reference
 //    build for recall and timing. It is parallel with per-vertex locks, like
-//    DiskANN's OpenMP build, so its output depends on thread timing.
+//    DiskANN's OpenMP build, so its output depends on thread timing (one
+//    thread gives the deterministic id-order build). Its RobustPrune
+//    (oracle_cpu_occlude) and greedy search (oracle_cpu_greedy) are also
+//    exported alone; tests/test_cpu_vamana.py pins all three against an
+//    independent Python statement of the paper's rules.
 //  * oracle_beam_search: DiskANN search_memory_index semantics (best-first
 //    search with a sorted candidate list of size L from the start point).
 //  * oracle_bruteforce_knn: exact top-k in double precision, ties by id.
@@ -21,9 +25,11 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
-#include <mutex>
 #include <vector>
 #include <omp.h>
+#if defined(__AVX2__) && defined(__FMA__)
+#include <immintrin.h>
+#endif
 
 namespace {
 
@@ -50,8 +56,7 @@ inline float h2f(uint16_t h) {
   return f;
 }
 
-// Plain squared L2 in fp32 (sequential). The baselines need a good distance,
-// not the canonical GPU order.
+// Row access for the baselines (element type 0 fp32, 1 uint8, 2 fp16).
 struct Vecs {
   const void* p;
   int dtype;
@@ -63,30 +68,79 @@ struct Vecs {
       default: return h2f(((const uint16_t*)p)[row * dim + e]);
     }
   }
+  inline void prefetch(size_t row) const {
+    const size_t bytes = (size_t)dim * (dtype == 0 ? 4 : dtype == 1 ? 1 : 2);
+    const char* r = (const char*)p + row * bytes;
+    for (size_t off = 0; off < bytes; off += 64) __builtin_prefetch(r + off, 0, 3);
+  }
 };
+
+// Squared L2 for the baselines, which need a fast, good distance, not the
+// canonical GPU order.
+#if defined(__AVX2__) && defined(__FMA__)
+// SIMD squared L2, as DiskANN's distance functions (AVX2 fp32 with fused
+// multiply-add; uint8 through 16-bit differences and pairwise madd, exact).
+inline float l2_f32(const float* x, const float* y, uint32_t dim) {
+  __m256 acc = _mm256_setzero_ps();
+  uint32_t e = 0;
+  for (; e + 8 <= dim; e += 8) {
+    const __m256 t = _mm256_sub_ps(_mm256_loadu_ps(x + e), _mm256_loadu_ps(y + e));
+    acc = _mm256_fmadd_ps(t, t, acc);
+  }
+  __m128 h = _mm_add_ps(_mm256_castps256_ps128(acc), _mm256_extractf128_ps(acc, 1));
+  h = _mm_hadd_ps(h, h);
+  h = _mm_hadd_ps(h, h);
+  float s = _mm_cvtss_f32(h);
+  for (; e < dim; ++e) {
+    const float t = x[e] - y[e];
+    s += t * t;
+  }
+  return s;
+}
+inline float l2_u8(const uint8_t* x, const uint8_t* y, uint32_t dim) {
+  __m256i acc = _mm256_setzero_si256();
+  uint32_t e = 0;
+  for (; e + 16 <= dim; e += 16) {
+    const __m256i a = _mm256_cvtepu8_epi16(_mm_loadu_si128((const __m128i*)(x + e)));
+    const __m256i b = _mm256_cvtepu8_epi16(_mm_loadu_si128((const __m128i*)(y + e)));
+    const __m256i t = _mm256_sub_epi16(a, b);
+    acc = _mm256_add_epi32(acc, _mm256_madd_epi16(t, t));
+  }
+  alignas(32) int32_t part[8];
+  _mm256_store_si256((__m256i*)part, acc);
+  int64_t s = 0;
+  for (int i = 0; i < 8; ++i) s += part[i];
+  for (; e < dim; ++e) {
+    const int t = (int)x[e] - (int)y[e];
+    s += t * t;
+  }
+  return (float)s;
+}
+#else
+inline float l2_f32(const float* x, const float* y, uint32_t dim) {
+  float s = 0.f;
+  for (uint32_t e = 0; e < dim; ++e) {
+    const float t = x[e] - y[e];
+    s += t * t;
+  }
+  return s;
+}
+inline float l2_u8(const uint8_t* x, const uint8_t* y, uint32_t dim) {
+  int64_t s = 0;
+  for (uint32_t e = 0; e < dim; ++e) {
+    const int t = (int)x[e] - (int)y[e];
+    s += t * t;
+  }
+  return (float)s;
+}
+#endif
 
 inline float l2(const Vecs& A, size_t a, const Vecs& B, size_t b) {
   const uint32_t dim = A.dim;
-  if (A.dtype == 0 && B.dtype == 0) {
-    const float* x = (const float*)A.p + a * dim;
-    const float* y = (const float*)B.p + b * dim;
-    float s = 0.f;
-    for (uint32_t e = 0; e < dim; ++e) {
-      float t = x[e] - y[e];
-      s += t * t;
-    }
-    return s;
-  }
-  if (A.dtype == 1 && B.dtype == 1) {
-    const uint8_t* x = (const uint8_t*)A.p + a * dim;
-    const uint8_t* y = (const uint8_t*)B.p + b * dim;
-    int64_t s = 0;
-    for (uint32_t e = 0; e < dim; ++e) {
-      int t = (int)x[e] - (int)y[e];
-      s += t * t;
-    }
-    return (float)s;
-  }
+  if (A.dtype == 0 && B.dtype == 0)
+    return l2_f32((const float*)A.p + a * dim, (const float*)B.p + b * dim, dim);
+  if (A.dtype == 1 && B.dtype == 1)
+    return l2_u8((const uint8_t*)A.p + a * dim, (const uint8_t*)B.p + b * dim, dim);
   float s = 0.f;
   for (uint32_t e = 0; e < dim; ++e) {
     float t = A.elem(a, e) - B.elem(b, e);
@@ -94,6 +148,20 @@ inline float l2(const Vecs& A, size_t a, const Vecs& B, size_t b) {
   }
   return s;
 }
+
+// Per-point lock of the CPU build (DiskANN locks each point's row the same
+// way): a test-and-set flag, held only while a row is copied or written.
+struct SpinLock {
+  std::atomic_flag f = ATOMIC_FLAG_INIT;
+  void lock() {
+    while (f.test_and_set(std::memory_order_acquire)) {
+#if defined(__x86_64__)
+      __builtin_ia32_pause();
+#endif
+    }
+  }
+  void unlock() { f.clear(std::memory_order_release); }
+};
 
 struct Cand {
   float d;
@@ -153,13 +221,23 @@ void greedy(const Vecs& base, const Vecs& q, size_t qrow, uint32_t start, uint32
     if (expanded_out) expanded_out->push_back(c);
     tmp.clear();
     nbrs(c.id, tmp);
+    // the unvisited neighbours first, their rows prefetched, then the
+    // distances (DiskANN's iterate_to_fixed_point gathers and prefetches the
+    // same way: the rows are random DRAM reads once the base outgrows the
+    // caches)
+    size_t fresh = 0;
     for (uint32_t n : tmp) {
       if (seen[n]) continue;
       seen[n] = 1;
       seen_list.push_back(n);
-      beam.insert({l2(q, qrow, base, n), n});
-      if (ndist) ++*ndist;
+      tmp[fresh++] = n;
+      base.prefetch(n);
     }
+    for (size_t k = 0; k < fresh; ++k) {
+      const uint32_t n = tmp[k];
+      beam.insert({l2(q, qrow, base, n), n});
+    }
+    if (ndist) *ndist += fresh;
   }
 }
 
@@ -191,9 +269,26 @@ extern "C" {
 
 // DiskANN-style CPU Vamana build (see file header). graph_out is N x R,
 // INV-padded; returns the start point (closest point to the centroid, like
-// DiskANN's calculate_entry_point).
+// DiskANN's calculate_entry_point). threads <= 0 uses every OpenMP thread;
+// with 1 thread the points are inserted in id order and the graph is
+// deterministic.
+//
+// Per point p, in id order over the threads (Alg. 1 of the paper, one pass
+// at the given alpha):
+//   1. greedy search for p from the start with a beam of L; V = the
+//      expanded points;
+//   2. RobustPrune(p, V u N_out(p) \ {p}) (Alg. 2: candidates sorted by
+//      (distance, id), repeated ids dropped, the occlude alpha ladder) becomes
+//      N_out(p);
+//   3. for every n in N_out(p) without p: append p while n holds fewer than
+//      ceil(1.3 R) neighbours (DiskANN's graph slack), else RobustPrune(n,
+//      N_out(n) u {p}).
+// A last pass prunes rows still above R. Rows live in flat N x max(slack, R)
+// arrays with a spinlock per point, so the search copies a neighbour row
+// without allocating.
 uint32_t oracle_cpu_vamana_build(const void* data, int dtype, uint32_t N, uint32_t dim, uint32_t R, uint32_t L,
-                                 float alpha, uint32_t maxc, uint32_t* graph_out, uint32_t* degree_out) {
+                                 float alpha, uint32_t maxc, int threads, uint32_t* graph_out,
+                                 uint32_t* degree_out) {
   Vecs base{data, dtype, dim};
   std::vector<double> centroid(dim, 0.0);
   for (size_t i = 0; i < N; ++i)
@@ -213,87 +308,132 @@ uint32_t oracle_cpu_vamana_build(const void* data, int dtype, uint32_t N, uint32
     }
   }
   const uint32_t slack = (uint32_t)std::ceil(1.3 * R);
+  const uint32_t cap = std::max(slack, R);
   // DANCE_ORACLE_PROGRESS set: a line on stderr per tenth of the points inserted
   const bool progress = std::getenv("DANCE_ORACLE_PROGRESS") != nullptr;
   const uint64_t tick = std::max<uint64_t>(1, N / 10);
   std::atomic<uint64_t> inserted{0};
-  std::vector<std::vector<uint32_t>> G(N);
-  std::vector<std::mutex> locks(N);
-  const int nt = omp_get_max_threads();
+  std::vector<uint32_t> adj((size_t)N * cap);
+  std::vector<uint32_t> deg(N, 0);
+  std::vector<SpinLock> locks(N);
+  const int nt = threads > 0 ? threads : omp_get_max_threads();
   std::vector<std::vector<uint8_t>> seen(nt, std::vector<uint8_t>(N, 0));
-#pragma omp parallel for schedule(dynamic, 64)
+  auto row = [&](uint32_t u) { return adj.data() + (size_t)u * cap; };
+  // RobustPrune of n over ids (n itself and repeats dropped) into n's row
+  auto prune_into = [&](uint32_t n, const uint32_t* ids, uint32_t count, std::vector<Cand>& cp,
+                        std::vector<uint32_t>& np) {
+    cp.clear();
+    for (uint32_t i = 0; i < count; ++i)
+      if (ids[i] != n) cp.push_back({l2(base, n, base, ids[i]), ids[i]});
+    std::sort(cp.begin(), cp.end());
+    cp.erase(std::unique(cp.begin(), cp.end(), [](const Cand& a, const Cand& b) { return a.id == b.id; }),
+             cp.end());
+    occlude(base, cp, R, alpha, maxc, np);
+  };
+#pragma omp parallel for schedule(dynamic, 64) num_threads(nt)
   for (int64_t nn = 0; nn < (int64_t)N; ++nn) {
     const uint32_t node = (uint32_t)nn;
     const int tid = omp_get_thread_num();
-    std::vector<uint32_t> seen_list;
-    std::vector<Cand> pool;
+    std::vector<uint32_t> seen_list, ids, copy, pruned, np;
+    std::vector<Cand> pool, cp;
     Beam beam(L);
     auto nbrs = [&](uint32_t u, std::vector<uint32_t>& out) {
-      std::lock_guard<std::mutex> lk(locks[u]);
-      out = G[u];
+      locks[u].lock();
+      out.assign(row(u), row(u) + deg[u]);
+      locks[u].unlock();
     };
     greedy(base, base, node, start, L, nbrs, seen[tid], seen_list, &pool, beam, nullptr);
     for (uint32_t s : seen_list) seen[tid][s] = 0;
-    {
-      std::lock_guard<std::mutex> lk(locks[node]);
-      for (uint32_t u : G[node]) pool.push_back({l2(base, node, base, u), u});
-    }
-    pool.erase(std::remove_if(pool.begin(), pool.end(), [&](const Cand& c) { return c.id == node; }),
-               pool.end());
-    std::sort(pool.begin(), pool.end());
-    pool.erase(std::unique(pool.begin(), pool.end(), [](const Cand& a, const Cand& b) { return a.id == b.id; }),
-               pool.end());
-    std::vector<uint32_t> pruned;
-    occlude(base, pool, R, alpha, maxc, pruned);
-    {
-      std::lock_guard<std::mutex> lk(locks[node]);
-      G[node] = pruned;
-    }
+    ids.clear();
+    for (const Cand& c : pool) ids.push_back(c.id);
+    locks[node].lock();
+    ids.insert(ids.end(), row(node), row(node) + deg[node]);
+    locks[node].unlock();
+    prune_into(node, ids.data(), (uint32_t)ids.size(), cp, pruned);
+    locks[node].lock();
+    std::copy(pruned.begin(), pruned.end(), row(node));
+    deg[node] = (uint32_t)pruned.size();
+    locks[node].unlock();
     for (uint32_t n : pruned) {
-      std::vector<uint32_t> copy;
-      bool need_prune = false;
-      {
-        std::lock_guard<std::mutex> lk(locks[n]);
-        if (std::find(G[n].begin(), G[n].end(), node) != G[n].end()) continue;
-        if (G[n].size() < slack) {
-          G[n].push_back(node);
-          continue;
-        }
-        copy = G[n];
-        copy.push_back(node);
-        need_prune = true;
+      locks[n].lock();
+      const uint32_t* r = row(n);
+      if (std::find(r, r + deg[n], node) != r + deg[n]) {
+        locks[n].unlock();
+        continue;
       }
-      if (need_prune) {
-        std::vector<Cand> cp;
-        for (uint32_t u : copy)
-          if (u != n) cp.push_back({l2(base, n, base, u), u});
-        std::sort(cp.begin(), cp.end());
-        std::vector<uint32_t> np;
-        occlude(base, cp, R, alpha, maxc, np);
-        std::lock_guard<std::mutex> lk(locks[n]);
-        G[n] = np;
+      if (deg[n] < slack) {
+        row(n)[deg[n]++] = node;
+        locks[n].unlock();
+        continue;
       }
+      copy.assign(r, r + deg[n]);
+      locks[n].unlock();
+      copy.push_back(node);
+      prune_into(n, copy.data(), (uint32_t)copy.size(), cp, np);
+      locks[n].lock();
+      std::copy(np.begin(), np.end(), row(n));
+      deg[n] = (uint32_t)np.size();
+      locks[n].unlock();
     }
     const uint64_t done = inserted.fetch_add(1) + 1;
     if (progress && done % tick == 0)
       std::fprintf(stderr, "[cpu_vamana] %llu / %u points inserted\n", (unsigned long long)done, N);
   }
-#pragma omp parallel for schedule(dynamic, 256)
+#pragma omp parallel for schedule(dynamic, 256) num_threads(nt)
   for (int64_t nn = 0; nn < (int64_t)N; ++nn) {
     const uint32_t n = (uint32_t)nn;
-    if (G[n].size() > R) {
+    if (deg[n] > R) {
       std::vector<Cand> cp;
-      for (uint32_t u : G[n]) cp.push_back({l2(base, n, base, u), u});
-      std::sort(cp.begin(), cp.end());
       std::vector<uint32_t> np;
-      occlude(base, cp, R, alpha, maxc, np);
-      G[n] = np;
+      prune_into(n, row(n), deg[n], cp, np);
+      std::copy(np.begin(), np.end(), row(n));
+      deg[n] = (uint32_t)np.size();
     }
-    uint32_t k = (uint32_t)std::min<size_t>(G[n].size(), R);
+    const uint32_t k = std::min(deg[n], R);
     degree_out[n] = k;
-    for (uint32_t i = 0; i < R; ++i) graph_out[(size_t)n * R + i] = i < k ? G[n][i] : INV;
+    for (uint32_t i = 0; i < R; ++i) graph_out[(size_t)n * R + i] = i < k ? row(n)[i] : INV;
   }
   return start;
+}
+
+// RobustPrune alone (the occlude step of the build above): candidates
+// (ids[i], dists[i]) of point p, sorted by (distance, id) here, cut to maxc,
+// then the alpha ladder. Writes at most R ids to out and returns the count.
+uint32_t oracle_cpu_occlude(const void* data, int dtype, uint32_t dim, const uint32_t* ids, const float* dists,
+                            uint32_t count, uint32_t R, float alpha, uint32_t maxc, uint32_t* out) {
+  Vecs base{data, dtype, dim};
+  std::vector<Cand> pool(count);
+  for (uint32_t i = 0; i < count; ++i) pool[i] = {dists[i], ids[i]};
+  std::sort(pool.begin(), pool.end());
+  std::vector<uint32_t> res;
+  occlude(base, pool, R, alpha, maxc, res);
+  std::copy(res.begin(), res.end(), out);
+  return (uint32_t)res.size();
+}
+
+// The build's greedy search alone, over an N x R graph (INV-padded rows with
+// degrees) for query row qrow of `queries`: writes the expanded ids in
+// expansion order (at most N) and returns their count; beam_ids (L entries,
+// INV-padded) gets the final beam.
+uint32_t oracle_cpu_greedy(const void* data, int dtype, uint32_t N, uint32_t dim, const uint32_t* graph,
+                           const uint32_t* degree, uint32_t R, uint32_t start, const void* queries, uint32_t qrow,
+                           uint32_t L, uint32_t* expanded_out, uint32_t* beam_ids) {
+  Vecs base{data, dtype, dim}, qv{queries, dtype, dim};
+  std::vector<uint8_t> seen(N, 0);
+  std::vector<uint32_t> seen_list;
+  std::vector<Cand> exp;
+  Beam beam(L);
+  auto nbrs = [&](uint32_t u, std::vector<uint32_t>& out) {
+    const uint32_t d = std::min(degree[u], R);
+    for (uint32_t i = 0; i < d; ++i) {
+      const uint32_t v = graph[(size_t)u * R + i];
+      if (v < N) out.push_back(v);
+    }
+  };
+  greedy(base, qv, qrow, start, L, nbrs, seen, seen_list, &exp, beam, nullptr);
+  for (size_t i = 0; i < exp.size(); ++i) expanded_out[i] = exp[i].id;
+  for (uint32_t i = 0; i < L; ++i) beam_ids[i] = i < beam.v.size() ? beam.v[i].id : INV;
+  return (uint32_t)exp.size();
 }
 
 // Best-first beam search over an N x R graph (INV-padded rows with degrees).

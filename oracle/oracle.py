@@ -31,8 +31,14 @@ Parity status of each oracle function (how it is pinned; see tests/test_oracle.p
                           of the pinned stages equals vnew2_build without the
                           heavy cap, and differs from vnew2_build with the cap
                           where a reverse list exceeds the threshold.
-  cpu_vamana_build        baseline only (DiskANN restated; parity unpinned:
-                          upstream DiskANN is not available offline).
+  cpu_vamana_build        the recall gate's comparator and the timed CPU
+                          baseline (DiskANN's algorithm restated; upstream
+                          DiskANN is not available offline). Pinned against
+                          independent Python statements of the paper's
+                          RobustPrune with DiskANN's alpha ladder, of the
+                          best-first search, and of the whole single-thread
+                          build, on tie-heavy integer rows; a full-beam search
+                          equals brute force (tests/test_cpu_vamana.py).
   merge_shards            pinned: mix64 by its closed-form inverse; the merge by
                           an independent Python restatement (sets, sorted())
                           on random shard sets, plus invariants; error codes
@@ -125,8 +131,12 @@ def lib() -> C.CDLL:
         L.oracle_vnew2_build.restype = i32
         L.oracle_v8_build.argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, u32, f32, u32, _u32p, _u32p, _u32p]
         L.oracle_v8_build.restype = i32
-        L.oracle_cpu_vamana_build.argtypes = [vp, i32, u32, u32, u32, u32, f32, u32, _u32p, _u32p]
+        L.oracle_cpu_vamana_build.argtypes = [vp, i32, u32, u32, u32, u32, f32, u32, i32, _u32p, _u32p]
         L.oracle_cpu_vamana_build.restype = u32
+        L.oracle_cpu_occlude.argtypes = [vp, i32, u32, _u32p, _f32p, u32, u32, f32, u32, _u32p]
+        L.oracle_cpu_occlude.restype = u32
+        L.oracle_cpu_greedy.argtypes = [vp, i32, u32, u32, _u32p, _u32p, u32, u32, vp, u32, u32, _u32p, _u32p]
+        L.oracle_cpu_greedy.restype = u32
         L.oracle_beam_search.argtypes = [vp, i32, u32, u32, _u32p, _u32p, u32, u32, vp, u32, u32, u32, _u32p]
         L.oracle_beam_search.restype = u64
         L.oracle_bruteforce_knn.argtypes = [vp, i32, u32, u32, vp, u32, u32, _u32p, _f32p]
@@ -315,14 +325,43 @@ def v8_build(data: np.ndarray, R=64, L=100, C_=80, STEPS=64, iters=4, alpha=1.2,
     return graph, deg, int(med[0])
 
 
-def cpu_vamana_build(data: np.ndarray, R=64, L=100, alpha=1.2, maxc=750):
+def cpu_vamana_build(data: np.ndarray, R=64, L=100, alpha=1.2, maxc=750, threads=0):
+    """DiskANN-style CPU Vamana (cpu_baselines.cpp); threads=1 inserts in id
+    order (deterministic), 0 uses every OpenMP thread."""
     data = np.ascontiguousarray(data)
     N = data.shape[0]
     graph = np.empty((N, R), np.uint32)
     deg = np.empty(N, np.uint32)
     start = lib().oracle_cpu_vamana_build(data.ctypes.data, _dt(data), N, data.shape[1], R, L, alpha, maxc,
-                                          _p(graph), _p(deg))
+                                          threads, _p(graph), _p(deg))
     return graph, deg, int(start)
+
+
+def cpu_occlude(data: np.ndarray, ids, dists, R, alpha, maxc=750):
+    """The CPU Vamana's RobustPrune alone: candidates sorted by (distance,
+    id), cut to maxc, alpha ladder; returns the kept ids in selection order."""
+    data = np.ascontiguousarray(data)
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    dists = np.ascontiguousarray(dists, dtype=np.float32)
+    out = np.empty(max(1, R), np.uint32)
+    k = lib().oracle_cpu_occlude(data.ctypes.data, _dt(data), data.shape[1], _p(ids), dists.ctypes.data_as(_f32p),
+                                 ids.shape[0], R, alpha, maxc, _p(out))
+    return out[:k].tolist()
+
+
+def cpu_greedy(data: np.ndarray, graph, degree, start, query: np.ndarray, L):
+    """The CPU Vamana's greedy search alone from `start` for one query row:
+    (expanded ids in expansion order, final beam ids)."""
+    data = np.ascontiguousarray(data)
+    graph = np.ascontiguousarray(graph, dtype=np.uint32)
+    degree = np.ascontiguousarray(degree, dtype=np.uint32)
+    q = np.ascontiguousarray(query.reshape(1, -1).astype(data.dtype))
+    N, R = graph.shape
+    exp = np.empty(N, np.uint32)
+    beam = np.empty(L, np.uint32)
+    k = lib().oracle_cpu_greedy(data.ctypes.data, _dt(data), N, data.shape[1], _p(graph), _p(degree), R, start,
+                                q.ctypes.data, 0, L, _p(exp), _p(beam))
+    return exp[:k].tolist(), [int(b) for b in beam if b != INVALID]
 
 
 def beam_search(data, graph, degree, start, queries, k, L):

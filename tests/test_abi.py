@@ -185,6 +185,23 @@ def test_parameter_errors_return_minus_one():
                                             gw.ctypes.data_as(u32p), dp) == -1
 
 
+@pytest.mark.parametrize("iters", ["0", "9", "four", "-1"])
+def test_iteration_count_outside_range_is_an_error(iters, monkeypatch):
+    """DANCE_VAMANA_ITERS (the reference's VAMANA_ITERS) takes 1..DANCE_MAX_ITERS;
+    anything else fails validation with -1 before any device call."""
+    monkeypatch.setenv("DANCE_VAMANA_ITERS", iters)
+    lib = D.lib()
+    x = np.zeros((16, 8), np.float32)
+    g = np.zeros((16, 8), np.uint32)
+    deg = np.zeros(16, np.uint32)
+    u32p = C.POINTER(C.c_uint32)
+    assert lib.gpu_vamana_vnew2_build_float(x.ctypes.data, 16, 8, 8, 16, 8, 8, g.ctypes.data_as(u32p),
+                                            deg.ctypes.data_as(u32p)) == -1
+    assert lib.gpu_vamana_build_float(x.ctypes.data, 16, 8, 8, 16, 8, 8, g.ctypes.data_as(u32p),
+                                      deg.ctypes.data_as(u32p)) == -1
+    assert D.MAX_ITERS == 8
+
+
 def test_partition_assign_errors_before_device():
     from dance_amd import partition as P
     x = np.zeros((10, 8), np.float32)

@@ -294,6 +294,27 @@ def test_end_to_end_alpha_schedule(alpha_from, monkeypatch):
     assert not np.array_equal(default, og)  # the schedule changes the graph
 
 
+@pytest.mark.parametrize("kind,iters,alpha_from", [("f32", 5, None), ("f32", 6, None), ("f32", 6, 0),
+                                                    ("u8", 6, None), ("f32", 1, None), ("f32", 8, 5)])
+def test_end_to_end_iteration_count(kind, iters, alpha_from, monkeypatch):
+    """The reference's VAMANA_ITERS (gpu_vamana_config.h:78-79) through
+    DANCE_VAMANA_ITERS, alone and with the alpha schedule knob; the kernel
+    profile reports one launch per iteration."""
+    monkeypatch.setenv("DANCE_VAMANA_ITERS", str(iters))
+    if alpha_from is not None:
+        monkeypatch.setenv("DANCE_ALPHA_FROM_ITER", str(alpha_from))
+    dim = 96 if kind == "f32" else 128
+    data = make_data(kind, 4000, dim, seed=29 + iters)
+    res = D.vamana_build(data, 32, 64, 48, 32)
+    og, od, om = O.vnew2_build(data, 32, 64, 48, 32, iters=iters, alpha_from=alpha_from)
+    assert res.medoid == om
+    assert np.array_equal(res.degree, od)
+    assert np.array_equal(res.graph, og)
+    kp = D.last_kernel_profile()
+    assert kp["iterations"] == iters and len(kp["search_iter_ms"]) == iters
+    assert all(t > 0 for t in kp["search_iter_ms"]) and all(t > 0 for t in kp["prune_iter_ms"])
+
+
 @pytest.mark.parametrize("kind,dim", [("f32", 512), ("u8", 2048), ("f32", 200)])
 def test_end_to_end_wide_rows(kind, dim):
     # the widest supported rows (16 chunks of 16 bytes per lane) and a width

@@ -558,17 +558,19 @@ def test_search_expansion_order_matches_best_first(N, R, L, steps):
         assert s.work[v, :k].tolist() == row, v
 
 
-@pytest.mark.parametrize("alpha_from", [0, 1, 2, 3])
-def test_alpha_schedule_composes_the_stages(alpha_from):
-    """The reference's schedule knob (vnew2.cu:201-213: alpha from iteration
-    VAMANA_ALPHA_FINAL_FROM_ITER on, 1 before; USE_ALPHA_FROM_FIRST_ITER is
-    from = 0) composed from the separately pinned stages: medoid, init, then
-    per iteration search (steps capped at 64 in the first two), reverse merge
-    and prune (fill to 64 in the last). From = 3 is the default schedule, and
-    with alpha 1 the knob changes nothing."""
-    rng = np.random.default_rng(30 + alpha_from)
+@pytest.mark.parametrize("iters,alpha_from", [(4, 0), (4, 1), (4, 2), (4, 3), (1, 0), (2, 1), (5, 4), (5, 0),
+                                              (6, 5), (6, 0)])
+def test_alpha_schedule_composes_the_stages(iters, alpha_from):
+    """The reference's schedule knobs composed from the separately pinned
+    stages: VAMANA_ITERS iterations (gpu_vamana_config.h:78-79, the loop at
+    vnew2.cu:2517-2637), alpha from iteration VAMANA_ALPHA_FINAL_FROM_ITER on
+    and 1 before (vnew2.cu:201-213; USE_ALPHA_FROM_FIRST_ITER is from = 0).
+    Medoid, init, then per iteration search (steps capped at 64 in the first
+    two), reverse merge and prune (fill to 64 in the last). From = iters - 1
+    is the default schedule, and with alpha 1 the knob changes nothing."""
+    rng = np.random.default_rng(30 + 7 * iters + alpha_from)
     x = rng.standard_normal((300, 16)).astype(np.float32)
-    R, L, C_, steps, iters, alpha = 12, 32, 24, 80, 4, 1.2
+    R, L, C_, steps, alpha = 12, 32, 24, 80, 1.2
     start, _, _ = O.medoid(x)
     s = O.init_graph(x, R, C_)
     for it in range(iters):
@@ -584,3 +586,13 @@ def test_alpha_schedule_composes_the_stages(alpha_from):
     g1, d1, _ = O.vnew2_build(x, R, L, C_, steps, iters, 1.0, alpha_from=alpha_from)
     g2, d2, _ = O.vnew2_build(x, R, L, C_, steps, iters, 1.0)
     assert np.array_equal(g1, g2) and np.array_equal(d1, d2)
+
+
+def test_more_iterations_change_the_graph():
+    """The iteration count is live: one more search / merge / prune pass over
+    the same rows gives another graph (a build that ignored the count would
+    pass the composition test only at the default)."""
+    x = np.random.default_rng(5).standard_normal((400, 16)).astype(np.float32)
+    g4, d4, _ = O.vnew2_build(x, 12, 32, 24, 32, 4)
+    g5, d5, _ = O.vnew2_build(x, 12, 32, 24, 32, 5)
+    assert not (np.array_equal(g4, g5) and np.array_equal(d4, d5))
