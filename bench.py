@@ -167,6 +167,68 @@ def copy_calibration(torch, dev, mib):
     del src, dst
 
 
+BUCKET_LS = (20, 40, 80, 160, 320, 650, 1000)  # the reference's filtered recall sweep (REPRODUCIBILITY.md:96-104)
+
+
+def label_reachability(graph: np.ndarray, deg: np.ndarray, ls, qlabels: np.ndarray, query_starts: list,
+                       gt: np.ndarray) -> dict:
+    """Per query: the fraction of its ground-truth points reachable from its
+    start points through edges between carriers of its label (the only edges
+    a label-filtered search can follow). Mean over queries, and the fraction
+    of queries whose whole ground truth is reachable: the recall ceiling of
+    the filtered search on this graph at any L."""
+    from dance_amd import INVALID
+    n, R = graph.shape
+    off, pts = ls.postings()
+    carrier = np.zeros(n, bool)
+    vis = np.zeros(n, bool)
+    col = np.arange(R)[None, :]
+    fr, full = [], []
+    by_label = {}
+    for r, l in enumerate(qlabels):
+        by_label.setdefault((int(l), tuple(query_starts[r])), []).append(r)
+    for (l, starts), rows in by_label.items():
+        c = pts[off[l]:off[l + 1]]
+        carrier[c] = True
+        front = np.array([s for s in starts if s < n], np.int64)
+        vis[front] = True
+        touched = [front]
+        while front.size:
+            nb = graph[front]
+            nb = nb[col < deg[front][:, None]].astype(np.int64)
+            nb = nb[nb < n]
+            nb = np.unique(nb[carrier[nb]])
+            nb = nb[~vis[nb]]
+            vis[nb] = True
+            touched.append(nb)
+            front = nb
+        for r in rows:
+            t = gt[r][gt[r] != INVALID].astype(np.int64)
+            if t.size:
+                hit = vis[t]
+                fr.append(float(hit.mean()))
+                full.append(bool(hit.all()))
+        carrier[c] = False
+        for t in touched:
+            vis[t] = False
+    return {"mean_reachable_fraction": round(float(np.mean(fr)), 4) if fr else None,
+            "queries_fully_reachable": round(float(np.mean(full)), 4) if full else None}
+
+
+def cardinality_buckets(ls, names=(("P50", 50.0), ("P1", 1.0)), per_bucket: int = 5) -> dict:
+    """The reference's query buckets (tools/prepare_multilabel_workload.py:
+    243-253): per percentile of the label cardinalities, the per_bucket labels
+    nearest to it (ties to the smaller label)."""
+    off, _ = ls.postings()
+    counts = np.diff(off).astype(np.int64)
+    out = {}
+    for name, p in names:
+        target = float(np.percentile(counts, p))
+        order = sorted(range(len(counts)), key=lambda l: (abs(counts[l] - target), l))[:per_bucket]
+        out[name] = {"target_cardinality": target, "labels": order, "cardinalities": [int(counts[l]) for l in order]}
+    return out
+
+
 def run_c5(args, mode) -> int:
     import torch
     import dance_amd as D
@@ -187,7 +249,11 @@ def run_c5(args, mode) -> int:
         part = np.random.default_rng(44).integers(0, c["parts"], n)
         ls = F.LabelSet(np.arange(n + 1, dtype=np.uint32), part.astype(np.uint32), c["parts"])
         qlab = np.random.default_rng(45).integers(0, c["parts"], c["nq"]).astype(np.uint32)
-    starts, gstart = label_starts_gpu(torch, base_t, ls)
+    cstarts, gstart = label_starts_gpu(torch, base_t, ls)
+    # label starts: DiskANN's load-balanced rule (build_memory_index's
+    # default) or, with --label-starts centroid, the carrier nearest the
+    # label centroid
+    starts = cstarts if args.label_starts == "centroid" else F.balanced_label_starts(ls, INVALID, seed=1)
     log(f"generated {mode} N={n} labels={ls.labels.shape[0]} in {time.time() - t0:.1f}s")
     R = c["R"] if mode == "c5f" else c["Rsmall"]
     graph_t = torch.empty((n, c["R"]), dtype=torch.int32, device=dev)
@@ -244,13 +310,51 @@ def run_c5(args, mode) -> int:
                                          deg_t.data_ptr(), Rg, ent, qs, 10, Ls, ls.offsets, ls.labels, ql)
             recall[f"L{Ls}"] = round(D.recall_at_k(found, gt, 10), 4)
         log(f"recall {recall} ({time.time() - t1:.1f}s)")
+    analysis = None
+    if nq > 0 and args.filtered_analysis:
+        # what bounds label-filtered recall on this graph: the reachable share
+        # of each query's ground truth, recall with the reference's extra
+        # search starts, and the reference's P50 / P1 cardinality buckets
+        t1 = time.time()
+        Rg = int(F.last_profile()["publish_degree"]) if mode == "c5f" else c["R"]
+        g_host = graph_t.view(-1)[:n * Rg].view(n, Rg).cpu().numpy().view(np.uint32)
+        d_host = deg_t.cpu().numpy().view(np.uint32)
+        primary = starts if mode == "c5f" else stitched["medoids"]
+        one = [[int(primary[l])] for l in ql]
+        extra = F.extra_label_starts(ls, primary, 16)
+        many = F.query_starts(base, qs, ql, primary, extra)
+        analysis = {"label_starts": args.label_starts,
+                    "reachability": {"start": label_reachability(g_host, d_host, ls, ql, one, gt),
+                                     "start_and_16_extra": label_reachability(g_host, d_host, ls, ql, many, gt)}}
+        rec16 = {}
+        for Ls in (10, 20, 50, 100, 200):
+            found, _ = D.search_resident(base_t.data_ptr(), D.DTYPE_U8, n, c["dim"], graph_t.data_ptr(),
+                                         deg_t.data_ptr(), Rg, many, qs, 10, Ls, ls.offsets, ls.labels, ql)
+            rec16[f"L{Ls}"] = round(D.recall_at_k(found, gt, 10), 4)
+        analysis["recall@10_start_and_16_extra"] = rec16
+        buckets = cardinality_buckets(ls)
+        bq = queries[:args.bucket_queries]
+        for name, b in buckets.items():
+            bl = np.repeat(np.array(b["labels"], np.uint32), bq.shape[0])
+            bqs = np.tile(bq, (len(b["labels"]), 1))
+            bgt = label_ground_truth(torch, base_t, ls, bqs, bl)
+            bent = [[int(primary[l])] for l in bl]
+            b["queries"] = int(bqs.shape[0])
+            b["recall@10"] = {}
+            for Ls in BUCKET_LS:
+                found, _ = D.search_resident(base_t.data_ptr(), D.DTYPE_U8, n, c["dim"], graph_t.data_ptr(),
+                                             deg_t.data_ptr(), Rg, bent, bqs, 10, Ls, ls.offsets, ls.labels, bl)
+                b["recall@10"][f"L{Ls}"] = round(D.recall_at_k(found, bgt, 10), 4)
+            b["reachability"] = label_reachability(g_host, d_host, ls, bl, bent, bgt)
+        analysis["buckets"] = buckets
+        log(f"filtered analysis {json.dumps(analysis)} ({time.time() - t1:.1f}s)")
 
     line = {"metric": ("filtered" if mode == "c5f" else "stitched") + " Vamana build vertices/sec (1M x 192 uint8)",
             "value": round(value, 1), "unit": "vertices/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(ms_per_step, 2), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "u8", "data": "synthetic",
             "config": {"workload": WORKLOADS[mode] + (f" (N overridden to {n})" if args.n else ""), "N": n},
-            "build_seconds": round(ms_per_step / 1000.0, 3), "recall@10": recall}
+            "build_seconds": round(ms_per_step / 1000.0, 3), "recall@10": recall, "filtered_analysis": analysis}
     Rg = int(F.last_profile()["publish_degree"]) if mode == "c5f" else c["R"]
     line["graph_check"] = graph_check(torch, graph_t.view(-1)[:n * Rg].view(n, Rg), deg_t, n, Rg)
     if mode == "c5f":
@@ -418,14 +522,17 @@ def cpu_leg(torch, D, O, cfg: dict, name: str, base: np.ndarray, queries: np.nda
     return out
 
 
-def parse_settings(text: str) -> list:
-    """'iters:alpha_from,...' -> [(iters, alpha_from or None)]; alpha_from
-    -1 (or empty) is the reference default, alpha in the last iteration."""
+def parse_settings(text: str, C_: int, S: int) -> list:
+    """'iters:alpha_from[:C[:STEPS]],...' -> [(iters, alpha_from or None, C,
+    STEPS)]; alpha_from -1 (or empty) is the reference default, alpha in the
+    last iteration; C and STEPS default to the workload's."""
     out = []
     for item in text.split(","):
-        it, _, af = item.strip().partition(":")
-        a = int(af) if af.strip() else -1
-        out.append((int(it), None if a < 0 else a))
+        f = [x.strip() for x in item.strip().split(":")]
+        a = int(f[1]) if len(f) > 1 and f[1] else -1
+        c = int(f[2]) if len(f) > 2 and f[2] else C_
+        st = int(f[3]) if len(f) > 3 and f[3] else S
+        out.append((int(f[0]), None if a < 0 else a, c, st))
     return out
 
 
@@ -475,78 +582,109 @@ def run_gate(args) -> int:
         else:
             os.environ["DANCE_ALPHA_FROM_ITER"] = str(alpha_from)
 
-    def build():
-        D.vamana_build_resident(base_t.data_ptr(), dcode, n, cfg["dim"], R, L, C_, S, graph_t.data_ptr(),
+    def build(c, st):
+        D.vamana_build_resident(base_t.data_ptr(), dcode, n, cfg["dim"], R, L, c, st, graph_t.data_ptr(),
                                 deg_t.data_ptr())
 
-    settings = parse_settings(args.gate_settings)
+    settings = parse_settings(args.gate_settings, C_, S)
     gpu = []
-    for k, (iters, af) in enumerate(settings):
+    for k, (iters, af, c, st) in enumerate(settings):
         set_env(iters, af)
         if k == 0:
-            build()  # untimed: loads the code objects
+            build(c, st)  # untimed: loads the code objects
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-        build()
+        build(c, st)
         torch.cuda.synchronize()
         secs = time.perf_counter() - t1
         medoid = int(D.lib().gpu_vamana_vnew2_get_last_medoid())
         check = graph_check(torch, graph_t, deg_t, n, R)
         rec = score(medoid)
-        e = {"iters": iters, "alpha_from": iters - 1 if af is None else af, "reference_default": iters == 4 and af in (None, 3),
-             "build_seconds": round(secs, 3), "vertices_per_s": round(n / secs, 1), "digest": check["digest"],
+        e = {"iters": iters, "alpha_from": iters - 1 if af is None else af, "C": c, "STEPS": st,
+             "reference_default": iters == 4 and af in (None, 3) and (c, st) == (C_, S), "build_seconds": round(secs, 3), "vertices_per_s": round(n / secs, 1), "digest": check["digest"],
              "graph_ok": check["ok"], "mean_degree": check["mean_degree"], "recall": rec}
         if n <= args.gate_oracle_max:
-            og, od, om = O.vnew2_build(base, R, L, C_, S, iters=iters, alpha_from=af)
+            og, od, om = O.vnew2_build(base, R, L, c, st, iters=iters, alpha_from=af)
             e["graph_equals_oracle"] = bool(om == medoid and np.array_equal(od, deg_t.cpu().numpy().view(np.uint32))
                                             and np.array_equal(og, graph_t.cpu().numpy().view(np.uint32)))
         gpu.append(e)
-        log(f"gate {args.config}: GPU iters={iters} alpha_from={e['alpha_from']} {secs:.3f}s {rec}")
+        log(f"gate {args.config}: GPU iters={iters} alpha_from={e['alpha_from']} C={c} STEPS={st} {secs:.3f}s "
+            f"{rec}")
     os.environ.pop("DANCE_VAMANA_ITERS", None)
     os.environ.pop("DANCE_ALPHA_FROM_ITER", None)
 
-    runs = []
+    keys = [f"L{Ls}" for Ls in LS]
+    runs, alt_runs = [], []
+
+    def record() -> dict:
+        """The gate record so far (rewritten after every CPU run, so a run
+        cut short still leaves the finished parts)."""
+        cpu_mean = spread = None
+        if runs:
+            cpu_mean = {k: round(float(np.mean([x["recall"][k] for x in runs])), 4) for k in keys}
+            spread = {k: round(float(max(x["recall"][k] for x in runs) - min(x["recall"][k] for x in runs)), 4)
+                      for k in keys}
+            for e in gpu:
+                e["delta_vs_cpu_mean"] = {k: round(e["recall"][k] - cpu_mean[k], 4) for k in keys}
+                e["pass"] = {k: e["recall"][k] >= cpu_mean[k] - GATE_TOL for k in keys}
+                e["all_pass"] = all(e["pass"].values())
+                e["passes_every_cpu_run"] = all(e["recall"][k] >= x["recall"][k] - GATE_TOL
+                                                for x in runs for k in keys)
+        alt_mean = ({k: round(float(np.mean([x["recall"][k] for x in alt_runs])), 4) for k in keys}
+                    if alt_runs else None)
+        if alt_mean:
+            for e in gpu:
+                e["delta_vs_alt_pool_mean"] = {k: round(e["recall"][k] - alt_mean[k], 4) for k in keys}
+        passing = [e for e in gpu if e.get("all_pass")]
+        best = min(passing, key=lambda e: e["build_seconds"]) if passing else None
+        rec = {"config": args.config,
+               "workload": WORKLOADS[args.config] + (f" (N overridden to {n})" if args.n else ""),
+               "N": n, "queries": nq, "tolerance": GATE_TOL,
+               "rule": "GPU recall@10 >= mean CPU Vamana recall@10 - tolerance at every L; same GPU search, "
+                       "exact ground truth (GPU fp32 shortlist, fp64 re-rank)",
+               "cpu_vamana": {"what": "DiskANN's in-memory Vamana build restated in C++/OpenMP "
+                                      "(oracle/cpu_baselines.cpp), R/L/alpha of the workload, maxc 750; Microsoft "
+                                      "DiskANN is not available offline",
+                              "pool": args.gate_cpu_pool,
+                              "pools": {"diskann": "RobustPrune over the search's expanded points "
+                                                   "(DiskANN's search_for_point_and_prune)",
+                                        "paper": "RobustPrune over the expanded points and the point's current "
+                                                 "neighbours (Alg. 2 of the DiskANN paper)"},
+                              "threads": O.num_threads(), "cpu_model": cpu_model(), "runs": runs,
+                              "recall_mean": cpu_mean, "recall_spread": spread,
+                              "alt_pool_runs": alt_runs, "alt_pool_recall_mean": alt_mean},
+               "gpu": gpu,
+               "cheapest_passing": ({k: best[k] for k in ("iters", "alpha_from", "C", "STEPS", "build_seconds")}
+                                    if best else None),
+               "command": "python bench.py " + " ".join(sys.argv[1:]),
+               "date": time.strftime("%Y-%m-%d %H:%M:%S")}
+        if args.gate_out:
+            os.makedirs(os.path.dirname(os.path.abspath(args.gate_out)), exist_ok=True)
+            with open(args.gate_out, "w") as f:
+                json.dump(rec, f, indent=1)
+        return rec
+
+    record()
     os.environ["DANCE_ORACLE_PROGRESS"] = "1"
-    for r in range(args.gate_cpu_runs):
+    plan = [args.gate_cpu_pool] * args.gate_cpu_runs + [args.gate_cpu_alt_pool] * args.gate_cpu_alt_runs
+    for r, pool in enumerate(plan):
         t1 = time.perf_counter()
-        gc, dc, sc = O.cpu_vamana_build(base, R, L, 1.2, 750)
+        gc, dc, sc = O.cpu_vamana_build(base, R, L, 1.2, 750, pool=pool)
         secs = time.perf_counter() - t1
         graph_t.copy_(torch.from_numpy(gc.view(np.int32)))
         deg_t.copy_(torch.from_numpy(dc.view(np.int32)))
         rec = score(sc)
-        runs.append({"seconds": round(secs, 2), "vertices_per_s": round(n / secs, 1),
-                     "mean_degree": round(float(dc.mean()), 3), "recall": rec})
-        log(f"gate {args.config}: CPU Vamana run {r + 1} {secs:.1f}s {rec}")
+        (runs if pool == args.gate_cpu_pool else alt_runs).append(
+            {"pool": pool, "seconds": round(secs, 2), "vertices_per_s": round(n / secs, 1),
+             "mean_degree": round(float(dc.mean()), 3), "recall": rec})
+        log(f"gate {args.config}: CPU Vamana ({pool} pool) run {r + 1} {secs:.1f}s {rec}")
         del gc, dc
-    keys = [f"L{Ls}" for Ls in LS]
-    cpu_mean = {k: round(float(np.mean([x["recall"][k] for x in runs])), 4) for k in keys}
-    spread = {k: round(float(max(x["recall"][k] for x in runs) - min(x["recall"][k] for x in runs)), 4)
-              for k in keys}
-    for e in gpu:
-        e["delta_vs_cpu_mean"] = {k: round(e["recall"][k] - cpu_mean[k], 4) for k in keys}
-        e["pass"] = {k: e["recall"][k] >= cpu_mean[k] - GATE_TOL for k in keys}
-        e["all_pass"] = all(e["pass"].values())
-        e["passes_every_cpu_run"] = all(e["recall"][k] >= x["recall"][k] - GATE_TOL for x in runs for k in keys)
-    passing = [e for e in gpu if e["all_pass"]]
-    rec = {"config": args.config, "workload": WORKLOADS[args.config] + (f" (N overridden to {n})" if args.n else ""),
-           "N": n, "queries": nq, "tolerance": GATE_TOL,
-           "rule": "GPU recall@10 >= mean CPU Vamana recall@10 - tolerance at every L; same GPU search, exact "
-                   "ground truth (GPU fp32 shortlist, fp64 re-rank)",
-           "cpu_vamana": {"what": "DiskANN's in-memory Vamana build restated in C++/OpenMP (oracle/cpu_baselines.cpp), "
-                                  "R/L/alpha of the workload, maxc 750; Microsoft DiskANN is not available offline",
-                          "threads": O.num_threads(), "cpu_model": cpu_model(), "runs": runs,
-                          "recall_mean": cpu_mean, "recall_spread": spread},
-           "gpu": gpu,
-           "cheapest_passing": (min(passing, key=lambda e: e["build_seconds"])["iters"],
-                                min(passing, key=lambda e: e["build_seconds"])["alpha_from"]) if passing else None,
-           "command": "python bench.py " + " ".join(sys.argv[1:]),
-           "date": time.strftime("%Y-%m-%d %H:%M:%S")}
-    if args.gate_out:
-        os.makedirs(os.path.dirname(os.path.abspath(args.gate_out)), exist_ok=True)
-        with open(args.gate_out, "w") as f:
-            json.dump(rec, f, indent=1)
+        rec_all = record()
+    cpu_mean = rec_all["cpu_vamana"]["recall_mean"] if runs else None
+    spread = rec_all["cpu_vamana"]["recall_spread"] if runs else None
     print(json.dumps({"gate": args.config, "cpu_mean": cpu_mean, "spread": spread,
-                      "gpu": [(e["iters"], e["alpha_from"], e["build_seconds"], e["all_pass"]) for e in gpu]}),
+                      "gpu": [(e["iters"], e["alpha_from"], e["C"], e["STEPS"], e["build_seconds"], e.get("all_pass"))
+                              for e in gpu]}),
           flush=True)
     return 0
 
@@ -574,11 +712,22 @@ def main() -> int:
     ap.add_argument("--profile", default="QUALITY")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="run one device copy of this size first (HBM counter calibration)")
+    ap.add_argument("--label-starts", default="balanced", choices=("balanced", "centroid"),
+                    help="c5 label entry points: DiskANN's load-balanced rule or the carrier nearest the centroid")
+    ap.add_argument("--filtered-analysis", type=int, default=1,
+                    help="c5: reachability, extra-start recall and the P50 / P1 cardinality buckets")
+    ap.add_argument("--bucket-queries", type=int, default=200, help="c5: queries per bucket label")
     ap.add_argument("--gate", action="store_true",
                     help="score the recall gate on the whole workload instead of the bench line (run_gate)")
     ap.add_argument("--gate-settings", default="4:-1,5:-1,6:-1,4:0,5:0,6:0",
-                    help="GPU settings iterations:alpha_from (-1 = the last iteration, the reference default)")
-    ap.add_argument("--gate-cpu-runs", type=int, default=1, help="timed CPU Vamana runs")
+                    help="GPU settings iterations:alpha_from[:C[:STEPS]] (alpha_from -1 = the last iteration, the "
+                         "reference default; C and STEPS default to the workload's)")
+    ap.add_argument("--gate-cpu-runs", type=int, default=1, help="timed CPU Vamana runs (the gate's comparator)")
+    ap.add_argument("--gate-cpu-pool", default="diskann", choices=("diskann", "paper"),
+                    help="the comparator's RobustPrune candidates: the expanded points (DiskANN's code) or those "
+                         "plus the point's current neighbours (the paper's Alg. 2)")
+    ap.add_argument("--gate-cpu-alt-pool", default="paper", choices=("diskann", "paper"))
+    ap.add_argument("--gate-cpu-alt-runs", type=int, default=0, help="CPU Vamana runs with the other pool, reported")
     ap.add_argument("--gate-queries", type=int, default=10_000)
     ap.add_argument("--gate-oracle-max", type=int, default=0,
                     help="largest N at which each GPU graph is also compared with the CPU oracle's")

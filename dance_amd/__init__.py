@@ -170,7 +170,8 @@ EXPORTS = [
     "dance_synth_f32", "dance_synth_u8",
     "gpu_vamana_filtered_build_uint8", "gpu_vamana_filtered_build_float", "gpu_vamana_filtered_get_last_stats",
     "dance_filtered_build", "dance_filtered_build_resident", "dance_get_last_filtered_profile",
-    "dance_search", "dance_search_resident", "dance_get_last_search_stats",
+    "dance_search", "dance_search_resident", "dance_search_multistart", "dance_search_multistart_resident",
+    "dance_get_last_search_stats",
     "dance_merge_shards", "dance_merge_get_last_stats", "dance_struct_sizes",
     "dance_partition_assign",
     "dance_stitched_build", "dance_stitched_build_resident", "dance_get_last_stitched_stats",
@@ -291,6 +292,10 @@ def lib() -> C.CDLL:
         search_args = [vp, i32, u32, u32, vp, vp, u32, _u32p, u32, vp, u32, u32, u32, vp, vp, vp, _u32p, _f32p]
         for name in ("dance_search", "dance_search_resident"):
             getattr(L, name).argtypes = search_args
+            getattr(L, name).restype = i32
+        multi_args = [vp, i32, u32, u32, vp, vp, u32, _u32p, _u32p, vp, u32, u32, u32, vp, vp, vp, _u32p, _f32p]
+        for name in ("dance_search_multistart", "dance_search_multistart_resident"):
+            getattr(L, name).argtypes = multi_args
             getattr(L, name).restype = i32
         L.dance_get_last_search_stats.argtypes = [C.POINTER(DanceSearchStats)]
         L.dance_get_last_search_stats.restype = None
@@ -592,13 +597,14 @@ def _opt_ptr(a):
 def search(data: np.ndarray, graph: np.ndarray, degree: np.ndarray, starts, queries: np.ndarray, k: int, L: int,
            label_offsets=None, labels=None, query_labels=None):
     """dance_search: best-first search of host queries over a built graph on
-    host arrays. starts: int (shared entry point) or one per query; the label
-    arrays (all or none) restrict the search to points carrying the query's
-    label. Returns (ids, dists), each nq x k."""
+    host arrays. starts: int (shared entry point), one per query, or a list
+    with one sequence of entry points per query (dance_search_multistart);
+    the label arrays (all or none) restrict the search to points carrying the
+    query's label. Returns (ids, dists), each nq x k."""
     data = np.ascontiguousarray(data)
     graph = np.ascontiguousarray(graph, np.uint32)
     degree = np.ascontiguousarray(degree, np.uint32)
-    return _search(lib().dance_search, data.ctypes.data, dtype_code(data), data.shape[0], data.shape[1],
+    return _search(False, data.ctypes.data, dtype_code(data), data.shape[0], data.shape[1],
                    graph.ctypes.data, degree.ctypes.data, graph.shape[1], starts, queries, k, L, label_offsets,
                    labels, query_labels)
 
@@ -607,21 +613,43 @@ def search_resident(d_data: int, dtype: int, N: int, dim: int, d_graph: int, d_d
                     queries: np.ndarray, k: int, L: int, label_offsets=None, labels=None, query_labels=None):
     """dance_search_resident: as search() with base rows, graph and degrees
     given as device pointers (e.g. torch data_ptr())."""
-    return _search(lib().dance_search_resident, d_data, dtype, N, dim, d_graph, d_degree, R, starts, queries, k, L,
+    return _search(True, d_data, dtype, N, dim, d_graph, d_degree, R, starts, queries, k, L,
                    label_offsets, labels, query_labels)
 
 
-def _search(fn, data_p, dtype, N, dim, graph_p, degree_p, R, starts, queries, k, L, label_offsets, labels,
+def start_lists(starts, nq: int):
+    """A list of per-query start sequences -> (offsets nq + 1, flat ids);
+    None for a single start or one start per query."""
+    if not (isinstance(starts, (list, tuple)) and any(np.ndim(x) > 0 for x in starts)):
+        return None
+    lists = [np.atleast_1d(np.asarray(x, np.uint32)) for x in starts]
+    if len(lists) != nq:
+        raise ValueError(f"{len(lists)} start lists for {nq} queries")
+    off = np.zeros(nq + 1, np.uint32)
+    off[1:] = np.cumsum([x.shape[0] for x in lists])
+    flat = np.concatenate(lists) if off[-1] else np.zeros(1, np.uint32)
+    return off, np.ascontiguousarray(flat, np.uint32)
+
+
+def _search(resident, data_p, dtype, N, dim, graph_p, degree_p, R, starts, queries, k, L, label_offsets, labels,
             query_labels):
     queries = np.ascontiguousarray(queries)
-    starts = np.atleast_1d(np.asarray(starts, np.uint32))
     nq = queries.shape[0]
     ids = np.empty((nq, k), np.uint32)
     dists = np.empty((nq, k), np.float32)
     opt = [None if a is None else np.ascontiguousarray(a, np.uint32) for a in (label_offsets, labels, query_labels)]
     ptrs = [_opt_ptr(a) for a in opt]
-    rc = fn(data_p, dtype, N, dim, graph_p, degree_p, R, _p(starts, C.c_uint32), starts.shape[0], queries.ctypes.data,
-            nq, k, L, *ptrs, _p(ids, C.c_uint32), _p(dists, C.c_float))
+    multi = start_lists(starts, nq)
+    if multi is None:
+        st = np.atleast_1d(np.asarray(starts, np.uint32))
+        fn = lib().dance_search_resident if resident else lib().dance_search
+        rc = fn(data_p, dtype, N, dim, graph_p, degree_p, R, _p(st, C.c_uint32), st.shape[0], queries.ctypes.data,
+                nq, k, L, *ptrs, _p(ids, C.c_uint32), _p(dists, C.c_float))
+    else:
+        off, flat = multi
+        fn = lib().dance_search_multistart_resident if resident else lib().dance_search_multistart
+        rc = fn(data_p, dtype, N, dim, graph_p, degree_p, R, _p(off, C.c_uint32), _p(flat, C.c_uint32),
+                queries.ctypes.data, nq, k, L, *ptrs, _p(ids, C.c_uint32), _p(dists, C.c_float))
     _check(rc, "dance_search")
     return ids, dists
 

@@ -18,8 +18,11 @@
 //      (DiskANN convert_labels_string_to_int, upstream); rows become sorted
 //      unique id lists (the canonical CSR, patch:20269-20286);
 //   2. entry points: global start = the point nearest to the centroid of all
-//      points; label start = the carrier of the label nearest to the centroid
-//      of its carriers (squared L2 in fp64, ties to the lower id);
+//      points; label starts by Filtered-DiskANN's load-balanced FindMedoid
+//      (25 random carriers per label, the least-loaded wins; see
+//      balanced_label_starts), or with DANCE_LABEL_STARTS=centroid the carrier
+//      nearest to the centroid of the label's carriers (squared L2 in fp64,
+//      ties to the lower id);
 //   3. gpu_vamana_filtered_build_{uint8,float} with the internal degree
 //      R_b = max(max_degree, 64) (or max(max_degree,
 //      DISKANN_GPU_FILTERED_INTERNAL_DEGREE)), L = Lbuild, filtered_L =
@@ -50,6 +53,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <iostream>
+#include <iterator>
 #include <limits>
 #include <stdexcept>
 #include <string>
@@ -163,6 +167,56 @@ uint32_t nearest_to_centroid(const std::vector<T>& x, uint32_t dim, const uint32
   return best;
 }
 
+// Label starts by Filtered-DiskANN's load-balanced FindMedoid, as upstream
+// DiskANN's Index::build_filtered_index picks them right before the patch's
+// GPU branch (patch:20239, `_medoid_counts[best_medoid]++`, is that loop's
+// last line; the starts reach the builder at :20288-20296): per label, in
+// ascending id order, draw kStartCands carriers uniformly with replacement,
+// keep the first drawn among those that already start the fewest labels, and
+// count it once more. Carriers of the universal label carry every label. The
+// draws are splitmix64 outputs modulo the carrier count, seeded with
+// DISKANN_GPU_FILTERED_LABEL_START_SEED (default 1), in place of rand().
+constexpr uint32_t kStartCands = 25;
+
+uint64_t splitmix64(uint64_t& s) {
+  uint64_t z = (s += 0x9e3779b97f4a7c15ull);
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+std::vector<uint32_t> balanced_label_starts(const Labels& lb, uint32_t n, uint64_t seed) {
+  const uint32_t num_labels = lb.count();
+  std::vector<uint32_t> loff, pts;
+  dio::postings(lb.offsets, lb.ids, num_labels, loff, pts);
+  std::vector<uint32_t> universal;  // carriers of the universal label, ascending
+  if (lb.universal < num_labels)
+    universal.assign(pts.begin() + loff[lb.universal], pts.begin() + loff[lb.universal + 1]);
+  std::vector<uint32_t> load(n, 0), starts(num_labels, kInvalid), carriers;
+  uint64_t state = seed;
+  for (uint32_t l = 0; l < num_labels; ++l) {
+    carriers.clear();
+    std::set_union(pts.begin() + loff[l], pts.begin() + loff[l + 1], universal.begin(), universal.end(),
+                   std::back_inserter(carriers));
+    if (carriers.empty()) continue;
+    uint32_t best = kInvalid, best_load = kInvalid;
+    for (uint32_t c = 0; c < kStartCands; ++c) {
+      const uint32_t cand = carriers[splitmix64(state) % carriers.size()];
+      if (load[cand] < best_load) {
+        best_load = load[cand];
+        best = cand;
+      }
+    }
+    starts[l] = best;
+    ++load[best];
+  }
+  return starts;
+}
+
+// The global start is the point nearest to the centroid (DiskANN
+// calculate_entry_point, patch:20267). Label starts follow the rule above, or
+// with DANCE_LABEL_STARTS=centroid the carrier of each label nearest to the
+// centroid of its carriers.
 template <typename T>
 void entry_points(const std::vector<T>& x, uint32_t n, uint32_t dim, const Labels& lb, uint32_t& global_start,
                   std::vector<uint32_t>& label_start) {
@@ -170,6 +224,15 @@ void entry_points(const std::vector<T>& x, uint32_t n, uint32_t dim, const Label
   for (uint32_t i = 0; i < n; ++i) all[i] = i;
   std::vector<double> cent;
   global_start = nearest_to_centroid(x, dim, all.data(), n, cent);
+  const char* rule = std::getenv("DANCE_LABEL_STARTS");
+  if (!(rule && std::string(rule) == "centroid")) {
+    if (rule && rule[0] && std::string(rule) != "balanced")
+      throw std::runtime_error(std::string("DANCE_LABEL_STARTS=") + rule + " is neither balanced nor centroid");
+    const char* seed_env = std::getenv("DISKANN_GPU_FILTERED_LABEL_START_SEED");
+    const uint64_t seed = seed_env && seed_env[0] ? std::strtoull(seed_env, nullptr, 10) : 1ull;
+    label_start = balanced_label_starts(lb, n, seed);
+    return;
+  }
   const uint32_t num_labels = lb.count();
   std::vector<uint32_t> loff, pts;
   dio::postings(lb.offsets, lb.ids, num_labels, loff, pts);

@@ -3,9 +3,10 @@
 //
 // One wave64 per query. The candidate list holds the L smallest
 // (distance, id) seen so far, PS slots per lane (entry p = slot p / 64 of
-// lane p % 64), unsorted: the worst entry is tracked for rejection and
-// replacement, and expansion takes the smallest unexpanded entry, which is
-// exactly the first unexpanded position of DiskANN's sorted list. The
+// lane p % 64; PS = 1 .. 16 covers L up to 1024), unsorted: the worst entry
+// is tracked for rejection and replacement, and expansion takes the smallest
+// unexpanded entry, which is exactly the first unexpanded position of
+// DiskANN's sorted list. The
 // visited set is a forgetful LDS cache; it is transparent because a node
 // still in the list is found by the duplicate check and a node that left the
 // list (or never entered it) is rejected again: once the list is full its
@@ -147,6 +148,7 @@ struct QArgs {
   const uint32_t* deg;
   const uint32_t* starts;
   uint32_t nstarts;
+  const uint32_t* start_off;  // nq + 1 (nullptr: starts[0] shared, or starts[q])
   uint32_t nq, k, L, max_expansions;
   const uint32_t* off;   // label CSR (nullptr: no filter)
   const uint32_t* lab;
@@ -185,9 +187,10 @@ __global__ __launch_bounds__(kBlock) void k_query(RowSet base, RowSet qrows, QAr
   const bool filt = a.off != nullptr;
   const uint32_t ql = filt ? a.qlab[q] : DANCE_INV;
   uint32_t ndist = 0, nexp = 0;
-  // One batch of candidates (lane order = insertion order).
-  auto batch = [&](uint32_t c) {
-    const bool v = c < a.N && (!filt || q_has_label(a, c, ql));
+  // One batch of candidates (lane order = insertion order); start nodes skip
+  // the label check.
+  auto batch = [&](uint32_t c, bool check_label) {
+    const bool v = c < a.N && (!filt || !check_label || q_has_label(a, c, ql));
     const uint32_t slot = (c * 0x9E3779B1u) >> (32 - kVisBits);
     const bool need = v && vis[slot] != c;
     const uint64_t m = wballot(need);
@@ -209,20 +212,12 @@ __global__ __launch_bounds__(kBlock) void k_query(RowSet base, RowSet qrows, QAr
     if (need) vis[slot] = c;
     wave_sync();
   };
-  // The start node is inserted without the label check (it is the label's
-  // entry point).
+  // The start nodes (the label's entry points) go in first, 64 at a time,
+  // without the label check.
   {
-    const uint32_t s = a.starts[a.nstarts == 1 ? 0 : q];
-    const bool ok = s < a.N && a.L > 0;
-    if (ok) {
-      if (lane == 0) lst[0] = s;
-      wave_sync();
-      batch_dist<DT, CPL>(base, av, lst, lsd, 1, grp, sub);
-      ndist += 1;
-      P.insert(s, lsd[0], lane);
-      if (lane == 0) vis[(s * 0x9E3779B1u) >> (32 - kVisBits)] = s;
-      wave_sync();
-    }
+    const uint32_t b0 = a.start_off ? a.start_off[q] : (a.nstarts == 1 ? 0u : q);
+    const uint32_t b1 = a.start_off ? a.start_off[q + 1] : b0 + 1u;
+    for (uint32_t b = b0; b < b1; b += 64) batch(b + lane < b1 ? a.starts[b + lane] : DANCE_INV, false);
   }
   bool capped = false;
   while (true) {
@@ -238,7 +233,7 @@ __global__ __launch_bounds__(kBlock) void k_query(RowSet base, RowSet qrows, QAr
     ++nexp;
     const uint32_t du = min(a.deg[u], a.R);
     const size_t b = (size_t)u * a.R;
-    for (uint32_t j = 0; j < du; j += 64) batch(j + lane < du ? a.g[b + j + lane] : DANCE_INV);
+    for (uint32_t j = 0; j < du; j += 64) batch(j + lane < du ? a.g[b + j + lane] : DANCE_INV, true);
   }
   // k best in (distance, id) order: lane i receives the i-th.
   uint32_t taken = 0, oid = DANCE_INV;

@@ -23,7 +23,8 @@ using namespace qs;
 std::mutex g_qmu;
 DanceSearchStats g_qstats{};
 
-int pick_ps(uint32_t L) { return L <= 64 ? 1 : L <= 128 ? 2 : 4; }
+constexpr uint32_t kMaxL = 1024;  // 16 slots per lane
+int pick_ps(uint32_t L) { return L <= 64 ? 1 : L <= 128 ? 2 : L <= 256 ? 4 : L <= 512 ? 8 : 16; }
 
 struct SearchIn {
   const void* data;  // device rows (resident) or host rows
@@ -36,6 +37,7 @@ struct SearchIn {
   uint32_t R;
   const uint32_t* starts;
   uint32_t nstarts;
+  const uint32_t* start_off;  // host, nq + 1 entries (nullptr: 1 shared or nq starts)
   const void* queries;  // host
   uint32_t nq, k, L;
   const uint32_t* label_offsets;  // host, optional
@@ -51,10 +53,18 @@ int run_search(const SearchIn& in) {
     return -1;
   }
   if (in.N == 0 || in.dim == 0 || in.R == 0 || in.nq == 0 || in.k == 0 || in.k > kMaxK || in.L < in.k ||
-      in.L > 256 || (in.nstarts != 1 && in.nstarts != in.nq)) {
+      in.L > kMaxL || (!in.start_off && in.nstarts != 1 && in.nstarts != in.nq)) {
     std::fprintf(stderr, "[dance_search] invalid parameters N=%u dim=%u R=%u nq=%u k=%u L=%u nstarts=%u\n", in.N,
                  in.dim, in.R, in.nq, in.k, in.L, in.nstarts);
     return -1;
+  }
+  if (in.start_off) {
+    bool ok = in.start_off[0] == 0;
+    for (uint32_t q = 0; ok && q < in.nq; ++q) ok = in.start_off[q] <= in.start_off[q + 1];
+    if (!ok) {
+      std::fprintf(stderr, "[dance_search] start_offsets must start at 0 and not decrease\n");
+      return -1;
+    }
   }
   const bool filt = in.label_offsets || in.labels || in.query_labels;
   if (filt && !(in.label_offsets && in.labels && in.query_labels)) {
@@ -83,7 +93,7 @@ int run_search(const SearchIn& in) {
     std::fprintf(stderr, "[dance_search] dim=%u is beyond the supported row width\n", in.dim);
     return -1;
   }
-  DevBuf g, dg, st, off, lab, qlab, oi, od, ctr;
+  DevBuf g, dg, st, soff, off, lab, qlab, oi, od, ctr;
   const uint32_t* dgraph = in.graph;
   const uint32_t* ddeg = in.degree;
   if (!in.graph_on_device) {
@@ -94,8 +104,12 @@ int run_search(const SearchIn& in) {
     dgraph = g.as<uint32_t>();
     ddeg = dg.as<uint32_t>();
   }
-  DCHECK(st.alloc((size_t)in.nstarts * 4));
-  DHIP(hipMemcpyAsync(st.p, in.starts, (size_t)in.nstarts * 4, hipMemcpyHostToDevice, s));
+  DCHECK(st.alloc((size_t)std::max(1u, in.nstarts) * 4));
+  if (in.nstarts) DHIP(hipMemcpyAsync(st.p, in.starts, (size_t)in.nstarts * 4, hipMemcpyHostToDevice, s));
+  if (in.start_off) {
+    DCHECK(soff.alloc((size_t)(in.nq + 1) * 4));
+    DHIP(hipMemcpyAsync(soff.p, in.start_off, (size_t)(in.nq + 1) * 4, hipMemcpyHostToDevice, s));
+  }
   if (filt) {
     const uint32_t total = in.label_offsets[in.N];
     DCHECK(off.alloc((size_t)(in.N + 1) * 4));
@@ -109,7 +123,8 @@ int run_search(const SearchIn& in) {
   DCHECK(od.alloc((size_t)in.nq * in.k * 4));
   DCHECK(ctr.alloc(3 * 8));
   DHIP(hipMemsetAsync(ctr.p, 0, 3 * 8, s));
-  QArgs a{in.N, in.R, dgraph, ddeg, st.as<uint32_t>(), in.nstarts, in.nq, in.k, in.L, 16u * in.L + 1024u,
+  QArgs a{in.N, in.R, dgraph, ddeg, st.as<uint32_t>(), in.nstarts,
+          in.start_off ? soff.as<uint32_t>() : nullptr, in.nq, in.k, in.L, 16u * in.L + 1024u,
           filt ? off.as<uint32_t>() : nullptr, filt ? lab.as<uint32_t>() : nullptr,
           filt ? qlab.as<uint32_t>() : nullptr, oi.as<uint32_t>(), od.as<float>(),
           ctr.as<unsigned long long>()};
@@ -126,8 +141,12 @@ int run_search(const SearchIn& in) {
       hipLaunchKernelGGL((k_query<DT, CPL, 1>), dim3(grid), dim3(kBlock), lds, s, base.rs, qr.rs, a);
     else if (ps == 2)
       hipLaunchKernelGGL((k_query<DT, CPL, 2>), dim3(grid), dim3(kBlock), lds, s, base.rs, qr.rs, a);
-    else
+    else if (ps == 4)
       hipLaunchKernelGGL((k_query<DT, CPL, 4>), dim3(grid), dim3(kBlock), lds, s, base.rs, qr.rs, a);
+    else if (ps == 8)
+      hipLaunchKernelGGL((k_query<DT, CPL, 8>), dim3(grid), dim3(kBlock), lds, s, base.rs, qr.rs, a);
+    else
+      hipLaunchKernelGGL((k_query<DT, CPL, 16>), dim3(grid), dim3(kBlock), lds, s, base.rs, qr.rs, a);
     DHIP(hipGetLastError());
     return 0;
   }));
@@ -161,8 +180,8 @@ int dance_search(const void* h_data, int dtype, uint32_t num_points, uint32_t di
                  const uint32_t* point_label_offsets, const uint32_t* point_labels, const uint32_t* query_labels,
                  uint32_t* ids_out, float* dists_out) {
   return run_search(SearchIn{h_data, false, dtype, num_points, dim, h_graph, h_degree, false, R, starts, num_starts,
-                             h_queries, num_queries, k, L, point_label_offsets, point_labels, query_labels, ids_out,
-                             dists_out});
+                             nullptr, h_queries, num_queries, k, L, point_label_offsets, point_labels, query_labels,
+                             ids_out, dists_out});
 }
 
 int dance_search_resident(const void* d_data, int dtype, uint32_t num_points, uint32_t dim, const uint32_t* d_graph,
@@ -171,7 +190,33 @@ int dance_search_resident(const void* d_data, int dtype, uint32_t num_points, ui
                           const uint32_t* point_label_offsets, const uint32_t* point_labels,
                           const uint32_t* query_labels, uint32_t* ids_out, float* dists_out) {
   return run_search(SearchIn{d_data, true, dtype, num_points, dim, d_graph, d_degree, true, R, starts, num_starts,
-                             h_queries, num_queries, k, L, point_label_offsets, point_labels, query_labels, ids_out,
+                             nullptr, h_queries, num_queries, k, L, point_label_offsets, point_labels, query_labels,
+                             ids_out, dists_out});
+}
+
+int dance_search_multistart(const void* h_data, int dtype, uint32_t num_points, uint32_t dim,
+                            const uint32_t* h_graph, const uint32_t* h_degree, uint32_t R,
+                            const uint32_t* start_offsets, const uint32_t* starts, const void* h_queries,
+                            uint32_t num_queries, uint32_t k, uint32_t L, const uint32_t* point_label_offsets,
+                            const uint32_t* point_labels, const uint32_t* query_labels, uint32_t* ids_out,
+                            float* dists_out) {
+  if (!start_offsets) return -1;
+  return run_search(SearchIn{h_data, false, dtype, num_points, dim, h_graph, h_degree, false, R,
+                             starts, num_queries ? start_offsets[num_queries] : 0u, start_offsets, h_queries,
+                             num_queries, k, L, point_label_offsets, point_labels, query_labels, ids_out,
+                             dists_out});
+}
+
+int dance_search_multistart_resident(const void* d_data, int dtype, uint32_t num_points, uint32_t dim,
+                                     const uint32_t* d_graph, const uint32_t* d_degree, uint32_t R,
+                                     const uint32_t* start_offsets, const uint32_t* starts, const void* h_queries,
+                                     uint32_t num_queries, uint32_t k, uint32_t L,
+                                     const uint32_t* point_label_offsets, const uint32_t* point_labels,
+                                     const uint32_t* query_labels, uint32_t* ids_out, float* dists_out) {
+  if (!start_offsets) return -1;
+  return run_search(SearchIn{d_data, true, dtype, num_points, dim, d_graph, d_degree, true, R,
+                             starts, num_queries ? start_offsets[num_queries] : 0u, start_offsets, h_queries,
+                             num_queries, k, L, point_label_offsets, point_labels, query_labels, ids_out,
                              dists_out});
 }
 

@@ -337,6 +337,7 @@ struct SearchWave {
   uint32_t *vis, *wid, *lst, *ord;
   float *wdd, *lsd;
   uint4 av[CPL];
+  uint32_t av_sq;  // self_term(av): the vertex row's share of every pair distance
   RegPool<PS> P;
   QSelf qme;
   uint32_t wdeg;
@@ -408,7 +409,7 @@ struct SearchWave {
     const uint64_t t0 = dclock();
     const bool full = P.size >= P.L && P.max_pos >= 0;
     const uint32_t nx = (QB && full && a.qb.rows) ? bound_filter(n) : n;
-    if (nx) batch_dist<DT, CPL>(a.rs, av, lst, lsd, nx, grp, sub);
+    if (nx) batch_dist<DT, CPL>(a.rs, av, av_sq, lst, lsd, nx, grp, sub);
     n_search += nx;
     const uint64_t t1 = dclock();
     c_dist += t1 - t0;
@@ -543,6 +544,7 @@ struct SearchWave {
     }
     uint4 xv[CPL];
     load_row<CPL>(a.rs, x, true, sub, xv);
+    const uint32_t xv_sq = self_term<DT, CPL>(xv);
     uint32_t nA = 0, nB = 0, nU = 0;
     for (uint32_t b = 0; b < wdeg; b += 64) {
       const uint32_t i = b + lane;
@@ -566,7 +568,7 @@ struct SearchWave {
       const uint32_t y0 = a0 ? wid[ord[nU + k0]] : 0u;
       uint4 b0[CPL];
       load_row<CPL>(a.rs, y0, a0, sub, b0);
-      const float d0 = octet_finish<DT, CPL>(a.rs, sub, xv, b0);
+      const float d0 = octet_finish<DT, CPL>(a.rs, sub, xv, b0, xv_sq);
       n_insert += min(8u, nA - p);
       occluded = wballot(sub == 0 && a0 && a.alpha * d0 <= dpx) != 0;
     }
@@ -592,7 +594,7 @@ struct SearchWave {
       const uint32_t y0 = a0 ? wid[s0] : 0u;
       uint4 b0[CPL];
       load_row<CPL>(a.rs, y0, a0, sub, b0);
-      const float d0 = octet_finish<DT, CPL>(a.rs, sub, xv, b0);
+      const float d0 = octet_finish<DT, CPL>(a.rs, sub, xv, b0, xv_sq);
       n_insert += min(8u, nB - p);
       const uint64_t hit = wballot(sub == 0 && a0 && a.alpha * d0 <= wdd[s0]);
       if (hit) vpos = (int)ord[wdeg - 1u - (p + ((uint32_t)ffs64(hit) >> 3))];
@@ -625,6 +627,7 @@ struct SearchWave {
     const GraphBufs& g = a.g;
     const uint32_t N = g.N, R = g.R, C = g.C;
     load_row<CPL>(a.rs, node, true, sub, av);
+    av_sq = self_term<DT, CPL>(av);
     if (QB && a.qb.rows) q_load_self(a.qb, node, qme);
     // Work row := current row with its stored distances (vnew2.cu:1186-1212).
     const uint32_t deg_self = min(g.deg_cur[node], R);

@@ -236,26 +236,45 @@ __device__ __forceinline__ float octet_partial_f(const RowSet& rs, uint32_t sub,
   return acc;
 }
 
+// The lane's share of sum a^2 over a uint8 row: the part of a pair's partial
+// that depends on `a` alone. Loops that pair one cached row with many others
+// compute it once (the search's vertex row, the online insert's expanded
+// row) instead of per pair.
 template <int CPL>
-__device__ __forceinline__ int octet_partial_u8(const uint4 (&a)[CPL], const uint4 (&b)[CPL]) {
-  // sum over bytes of a^2 + b^2 - 2ab, exact in 32-bit integers
-  uint32_t sq = 0u, cr = 0u;
+__device__ __forceinline__ uint32_t u8_self_sq(const uint4 (&a)[CPL]) {
+  uint32_t sq = 0u;
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     sq = __builtin_amdgcn_udot4(a[c].x, a[c].x, sq, false);
+    sq = __builtin_amdgcn_udot4(a[c].y, a[c].y, sq, false);
+    sq = __builtin_amdgcn_udot4(a[c].z, a[c].z, sq, false);
+    sq = __builtin_amdgcn_udot4(a[c].w, a[c].w, sq, false);
+  }
+  return sq;
+}
+
+// Sum over the lane's bytes of a^2 + b^2 - 2ab given a_sq = u8_self_sq(a):
+// exact in 32-bit integers (wrap-around included), so the grouping of the
+// terms never changes the value.
+template <int CPL>
+__device__ __forceinline__ int octet_partial_u8(const uint4 (&a)[CPL], const uint4 (&b)[CPL], uint32_t a_sq) {
+  uint32_t sq = a_sq, cr = 0u;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
     sq = __builtin_amdgcn_udot4(b[c].x, b[c].x, sq, false);
     cr = __builtin_amdgcn_udot4(a[c].x, b[c].x, cr, false);
-    sq = __builtin_amdgcn_udot4(a[c].y, a[c].y, sq, false);
     sq = __builtin_amdgcn_udot4(b[c].y, b[c].y, sq, false);
     cr = __builtin_amdgcn_udot4(a[c].y, b[c].y, cr, false);
-    sq = __builtin_amdgcn_udot4(a[c].z, a[c].z, sq, false);
     sq = __builtin_amdgcn_udot4(b[c].z, b[c].z, sq, false);
     cr = __builtin_amdgcn_udot4(a[c].z, b[c].z, cr, false);
-    sq = __builtin_amdgcn_udot4(a[c].w, a[c].w, sq, false);
     sq = __builtin_amdgcn_udot4(b[c].w, b[c].w, sq, false);
     cr = __builtin_amdgcn_udot4(a[c].w, b[c].w, cr, false);
   }
   return (int)(sq - 2u * cr);
+}
+template <int CPL>
+__device__ __forceinline__ int octet_partial_u8(const uint4 (&a)[CPL], const uint4 (&b)[CPL]) {
+  return octet_partial_u8<CPL>(a, b, u8_self_sq<CPL>(a));
 }
 
 // Canonical octet combination of per-lane partial sums (see the header).
@@ -267,12 +286,13 @@ __device__ __forceinline__ float octet_combine(float p) {
 }
 
 // Full distance of a pair held by an octet; every lane of the octet returns it.
-// Must be called by all 64 lanes (the butterfly crosses lanes).
+// Must be called by all 64 lanes (the butterfly crosses lanes). a_sq is
+// u8_self_sq(a) for uint8 rows (unused otherwise).
 template <int DT, int CPL>
 __device__ __forceinline__ float octet_finish(const RowSet& rs, uint32_t sub, const uint4 (&a)[CPL],
-                                              const uint4 (&b)[CPL]) {
+                                              const uint4 (&b)[CPL], uint32_t a_sq) {
   if constexpr (DT == DANCE_U8) {
-    int p = octet_partial_u8<CPL>(a, b);
+    int p = octet_partial_u8<CPL>(a, b, a_sq);
     p += dpp<kDppHalfMirror>(0, p);
     p += dpp<kDppQuadXor2>(0, p);
     p += dpp<kDppQuadXor1>(0, p);
@@ -280,6 +300,20 @@ __device__ __forceinline__ float octet_finish(const RowSet& rs, uint32_t sub, co
   } else {
     return octet_combine(octet_partial_f<DT, CPL>(rs, sub, a, b));
   }
+}
+template <int DT, int CPL>
+__device__ __forceinline__ float octet_finish(const RowSet& rs, uint32_t sub, const uint4 (&a)[CPL],
+                                              const uint4 (&b)[CPL]) {
+  return octet_finish<DT, CPL>(rs, sub, a, b, DT == DANCE_U8 ? u8_self_sq<CPL>(a) : 0u);
+}
+
+// The per-lane self term octet_finish takes for a row cached in registers.
+template <int DT, int CPL>
+__device__ __forceinline__ uint32_t self_term(const uint4 (&a)[CPL]) {
+  if constexpr (DT == DANCE_U8)
+    return u8_self_sq<CPL>(a);
+  else
+    return 0u;
 }
 
 // Float ordering keys for wave reductions over non-negative distances.
@@ -291,8 +325,9 @@ __device__ __forceinline__ int fkey(float d) { return __float_as_int(d); }
 // lst holds 64 entries; every index read stays below 64. Returns after lsd
 // is visible.
 template <int DT, int CPL>
-__device__ __forceinline__ void batch_dist(const RowSet& rs, const uint4 (&av)[CPL], const uint32_t* lst,
-                                           float* lsd, uint32_t n, uint32_t grp, uint32_t sub) {
+__device__ __forceinline__ void batch_dist(const RowSet& rs, const uint4 (&av)[CPL], uint32_t a_sq,
+                                           const uint32_t* lst, float* lsd, uint32_t n, uint32_t grp,
+                                           uint32_t sub) {
   uint32_t p = 0;
   for (; p + 8 < n; p += 16) {
     const uint32_t k0 = p + grp, k1 = p + 8 + grp;
@@ -301,8 +336,8 @@ __device__ __forceinline__ void batch_dist(const RowSet& rs, const uint4 (&av)[C
     uint4 b0[CPL], b1[CPL];
     load_row<CPL>(rs, id0, a0, sub, b0);
     load_row<CPL>(rs, id1, a1, sub, b1);
-    const float d0 = octet_finish<DT, CPL>(rs, sub, av, b0);
-    const float d1 = octet_finish<DT, CPL>(rs, sub, av, b1);
+    const float d0 = octet_finish<DT, CPL>(rs, sub, av, b0, a_sq);
+    const float d1 = octet_finish<DT, CPL>(rs, sub, av, b1, a_sq);
     if (sub == 0) {
       if (a0) lsd[k0] = d0;
       if (a1) lsd[k1] = d1;
@@ -313,10 +348,15 @@ __device__ __forceinline__ void batch_dist(const RowSet& rs, const uint4 (&av)[C
     const bool a0 = k0 < n;
     uint4 b0[CPL];
     load_row<CPL>(rs, lst[k0], a0, sub, b0);
-    const float d0 = octet_finish<DT, CPL>(rs, sub, av, b0);
+    const float d0 = octet_finish<DT, CPL>(rs, sub, av, b0, a_sq);
     if (sub == 0 && a0) lsd[k0] = d0;
   }
   wave_sync();
+}
+template <int DT, int CPL>
+__device__ __forceinline__ void batch_dist(const RowSet& rs, const uint4 (&av)[CPL], const uint32_t* lst,
+                                           float* lsd, uint32_t n, uint32_t grp, uint32_t sub) {
+  batch_dist<DT, CPL>(rs, av, self_term<DT, CPL>(av), lst, lsd, n, grp, sub);
 }
 
 // ---------------------------------------------------------------------------

@@ -97,11 +97,107 @@ def zipf_labels(count: int, vocab: int, zipf_s: float = 1.0, seed: int = 43) -> 
     return np.minimum(np.searchsorted(cdf, rng.random(count), side="right"), vocab - 1).astype(np.uint32)
 
 
+START_CANDS = 25  # carriers drawn per label by the load-balanced rule
+
+
+def _splitmix64(state: int) -> tuple[int, int]:
+    state = (state + 0x9E3779B97F4A7C15) & 0xFFFFFFFFFFFFFFFF
+    z = state
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & 0xFFFFFFFFFFFFFFFF
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & 0xFFFFFFFFFFFFFFFF
+    return state, z ^ (z >> 31)
+
+
+def balanced_label_starts(ls: LabelSet, universal: int = INVALID, seed: int = 1) -> np.ndarray:
+    """Entry point per label by Filtered-DiskANN's load-balanced FindMedoid,
+    the rule upstream DiskANN's Index::build_filtered_index applies right
+    before the reference's GPU branch (patch:20239, consumed at :20288-20296):
+    per label in ascending id order, START_CANDS carriers drawn uniformly with
+    replacement, the first drawn of those that start the fewest labels so far
+    wins and its count rises by one. Carriers of `universal` carry every label.
+    Draws are splitmix64 outputs modulo the carrier count from `seed`, the
+    stream build_memory_index uses (DISKANN_GPU_FILTERED_LABEL_START_SEED,
+    default 1). INVALID for labels without carriers."""
+    off, pts = ls.postings()
+    nl = ls.num_labels
+    uni = pts[off[universal]:off[universal + 1]] if universal < nl else np.empty(0, pts.dtype)
+    starts = np.full(max(1, nl), INVALID, np.uint32)
+    load = {}
+    state = seed & 0xFFFFFFFFFFFFFFFF
+    for l in range(nl):
+        carriers = np.union1d(pts[off[l]:off[l + 1]], uni) if uni.size else pts[off[l]:off[l + 1]]
+        if carriers.size == 0:
+            continue
+        best, best_load = None, None
+        for _ in range(START_CANDS):
+            state, r = _splitmix64(state)
+            c = int(carriers[r % carriers.size])
+            if best_load is None or load.get(c, 0) < best_load:
+                best, best_load = c, load.get(c, 0)
+        starts[l] = best
+        load[best] = best_load + 1
+    return starts
+
+
+def start_hash(point: np.ndarray, label: int) -> np.ndarray:
+    """The reference's hash of a (point, label) pair for extra search starts
+    (integrations/dance-diskann-78256bba.patch:19836-19844): x = point << 32
+    ^ label ^ 0x9e3779b97f4a7c15, the splitmix64 finaliser, low 32 bits."""
+    with np.errstate(over="ignore"):
+        x = (np.asarray(point, np.uint64) << np.uint64(32)) ^ np.uint64(label) ^ np.uint64(0x9E3779B97F4A7C15)
+        x ^= x >> np.uint64(30)
+        x *= np.uint64(0xBF58476D1CE4E5B9)
+        x ^= x >> np.uint64(27)
+        x *= np.uint64(0x94D049BB133111EB)
+        x ^= x >> np.uint64(31)
+    return (x & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+
+
+def extra_label_starts(ls: LabelSet, starts: np.ndarray, per_label: int) -> list:
+    """Extra search starts per label, as the reference's filtered search picks
+    them under DISKANN_FILTERED_SEARCH_EXTRA_STARTS=per_label (at most 16;
+    patch:19817-19873): the label's carriers other than its start, the
+    per_label smallest by (start_hash, point), in that order. One array per
+    label (empty for labels without a start)."""
+    per_label = min(int(per_label), 16)
+    off, pts = ls.postings()
+    out = []
+    for l in range(ls.num_labels):
+        c = pts[off[l]:off[l + 1]]
+        if per_label <= 0 or l >= len(starts) or starts[l] == INVALID or c.size == 0:
+            out.append(np.zeros(0, np.uint32))
+            continue
+        c = c[c != starts[l]]
+        h = start_hash(c, l)
+        order = np.lexsort((c, h))[:per_label]
+        out.append(c[order].astype(np.uint32))
+    return out
+
+
+def query_starts(data: np.ndarray, queries: np.ndarray, qlabels: np.ndarray, starts: np.ndarray, extra: list,
+                 select: int = 0) -> list:
+    """Entry points of each query's filtered search (patch:20583-20625): the
+    label's start and its extra starts, or with select > 0 only the select
+    extra starts nearest to the query (DISKANN_FILTERED_SEARCH_EXTRA_START_SELECT,
+    squared L2, ties to the smaller id), sorted and deduplicated."""
+    out = []
+    for r, l in enumerate(qlabels):
+        ids = [int(starts[l])] if starts[l] != INVALID else []
+        ex = extra[l]
+        if select > 0 and ex.size:
+            diff = data[ex].astype(np.float64) - queries[r].astype(np.float64)
+            d = (diff * diff).sum(1)
+            ex = ex[np.lexsort((ex, d))[:select]]
+        out.append(sorted(set(ids) | set(int(v) for v in ex)))
+    return out
+
+
 def label_starts(data: np.ndarray, ls: LabelSet) -> np.ndarray:
     """Entry point per label: the point of the label nearest (squared L2, fp64)
-    to the label's centroid; INVALID for labels without points. DiskANN picks
-    label entry points with its own sampler (upstream, not part of the
-    reference); any in-label point is a valid entry for the builder."""
+    to the label's centroid; INVALID for labels without points (the
+    build_memory_index option DANCE_LABEL_STARTS=centroid; its default is
+    balanced_label_starts). Any in-label point is a valid entry for the
+    builder."""
     off, pts = ls.postings()
     starts = np.full(max(1, ls.num_labels), INVALID, np.uint32)
     lab_of = np.repeat(np.arange(ls.num_labels), np.diff(off).astype(np.int64))
@@ -218,6 +314,6 @@ def filtered_build_resident(d_data: int, dtype: int, N: int, dim: int, ls: Label
         gstart, d_graph, d_degree), "dance_filtered_build_resident")
 
 
-__all__ = ["LabelSet", "canonical_labels", "synth_labels", "zipf_labels", "label_starts", "global_start", "FilteredResult",
-           "filtered_build", "filtered_build_resident", "build_rc", "last_stats", "last_profile", "ROUNDS",
+__all__ = ["LabelSet", "canonical_labels", "synth_labels", "zipf_labels", "label_starts", "balanced_label_starts",
+           "extra_label_starts", "query_starts", "start_hash", "global_start", "FilteredResult", "filtered_build", "filtered_build_resident", "build_rc", "last_stats", "last_profile", "ROUNDS",
            "DISKANN_MAXC", "DTYPE_F16", "DTYPE_F32", "DTYPE_U8"]

@@ -198,8 +198,10 @@ typedef struct DanceSearchStats {
  * distances per query in order (0xFFFFFFFF / FLT_MAX past the end). starts
  * holds 1 shared or num_queries entry points. With point_label_offsets /
  * point_labels / query_labels (all or none), only points carrying the query's
- * label are visited besides the start. 1 <= k <= 64, k <= L <= 256.
- * Expansions are capped at 16 L + 1024 per query (capped_queries counts hits). */
+ * label are visited besides the start. 1 <= k <= 64, k <= L <= 1024 (the
+ * reference's published sweeps run to L = 1000, REPRODUCIBILITY.md:44-52,
+ * 96-104). Expansions are capped at 16 L + 1024 per query (capped_queries
+ * counts hits). */
 int dance_search(const void *h_data, int dtype, uint32_t num_points, uint32_t dim, const uint32_t *h_graph,
                  const uint32_t *h_degree, uint32_t R, const uint32_t *starts, uint32_t num_starts,
                  const void *h_queries, uint32_t num_queries, uint32_t k, uint32_t L,
@@ -212,6 +214,28 @@ int dance_search_resident(const void *d_data, int dtype, uint32_t num_points, ui
                           const void *h_queries, uint32_t num_queries, uint32_t k, uint32_t L,
                           const uint32_t *point_label_offsets, const uint32_t *point_labels,
                           const uint32_t *query_labels, uint32_t *ids_out, float *dists_out);
+
+/* dance_search with several entry points per query: query q starts from
+ * starts[start_offsets[q] .. start_offsets[q + 1]) (start_offsets holds
+ * num_queries + 1 non-decreasing entries from 0), all inserted into the
+ * candidate list before the first expansion, without the label check; ids
+ * >= num_points are skipped. This is DiskANN's filtered search seeded with a
+ * label's start and its extra starts (the medoid list of
+ * _labels_to_medoids.txt and DISKANN_FILTERED_SEARCH_EXTRA_STARTS,
+ * integrations/dance-diskann-78256bba.patch:19780-19880; init_ids sorted and
+ * deduplicated, :20583-20625). */
+int dance_search_multistart(const void *h_data, int dtype, uint32_t num_points, uint32_t dim, const uint32_t *h_graph,
+                            const uint32_t *h_degree, uint32_t R, const uint32_t *start_offsets,
+                            const uint32_t *starts, const void *h_queries, uint32_t num_queries, uint32_t k,
+                            uint32_t L, const uint32_t *point_label_offsets, const uint32_t *point_labels,
+                            const uint32_t *query_labels, uint32_t *ids_out, float *dists_out);
+/* Same with the base rows, graph and degrees resident in device memory. */
+int dance_search_multistart_resident(const void *d_data, int dtype, uint32_t num_points, uint32_t dim,
+                                     const uint32_t *d_graph, const uint32_t *d_degree, uint32_t R,
+                                     const uint32_t *start_offsets, const uint32_t *starts, const void *h_queries,
+                                     uint32_t num_queries, uint32_t k, uint32_t L,
+                                     const uint32_t *point_label_offsets, const uint32_t *point_labels,
+                                     const uint32_t *query_labels, uint32_t *ids_out, float *dists_out);
 
 void dance_get_last_search_stats(DanceSearchStats *stats);
 

@@ -277,9 +277,12 @@ extern "C" {
 // at the given alpha):
 //   1. greedy search for p from the start with a beam of L; V = the
 //      expanded points;
-//   2. RobustPrune(p, V u N_out(p) \ {p}) (Alg. 2: candidates sorted by
-//      (distance, id), repeated ids dropped, the occlude alpha ladder) becomes
-//      N_out(p);
+//   2. RobustPrune(p, V \ {p}) (pool = 0: DiskANN's
+//      search_for_point_and_prune, which prunes the expanded set and
+//      overwrites the row) or RobustPrune(p, V u N_out(p) \ {p}) (pool = 1:
+//      the paper's Alg. 2, which keeps the reverse edges p received so far
+//      among the candidates); candidates sorted by (distance, id), repeated
+//      ids dropped, the occlude alpha ladder; the result becomes N_out(p);
 //   3. for every n in N_out(p) without p: append p while n holds fewer than
 //      ceil(1.3 R) neighbours (DiskANN's graph slack), else RobustPrune(n,
 //      N_out(n) u {p}).
@@ -287,7 +290,7 @@ extern "C" {
 // arrays with a spinlock per point, so the search copies a neighbour row
 // without allocating.
 uint32_t oracle_cpu_vamana_build(const void* data, int dtype, uint32_t N, uint32_t dim, uint32_t R, uint32_t L,
-                                 float alpha, uint32_t maxc, int threads, uint32_t* graph_out,
+                                 float alpha, uint32_t maxc, int threads, int pool, uint32_t* graph_out,
                                  uint32_t* degree_out) {
   Vecs base{data, dtype, dim};
   std::vector<double> centroid(dim, 0.0);
@@ -335,20 +338,22 @@ uint32_t oracle_cpu_vamana_build(const void* data, int dtype, uint32_t N, uint32
     const uint32_t node = (uint32_t)nn;
     const int tid = omp_get_thread_num();
     std::vector<uint32_t> seen_list, ids, copy, pruned, np;
-    std::vector<Cand> pool, cp;
+    std::vector<Cand> cand, cp;
     Beam beam(L);
     auto nbrs = [&](uint32_t u, std::vector<uint32_t>& out) {
       locks[u].lock();
       out.assign(row(u), row(u) + deg[u]);
       locks[u].unlock();
     };
-    greedy(base, base, node, start, L, nbrs, seen[tid], seen_list, &pool, beam, nullptr);
+    greedy(base, base, node, start, L, nbrs, seen[tid], seen_list, &cand, beam, nullptr);
     for (uint32_t s : seen_list) seen[tid][s] = 0;
     ids.clear();
-    for (const Cand& c : pool) ids.push_back(c.id);
-    locks[node].lock();
-    ids.insert(ids.end(), row(node), row(node) + deg[node]);
-    locks[node].unlock();
+    for (const Cand& c : cand) ids.push_back(c.id);
+    if (pool == 1) {
+      locks[node].lock();
+      ids.insert(ids.end(), row(node), row(node) + deg[node]);
+      locks[node].unlock();
+    }
     prune_into(node, ids.data(), (uint32_t)ids.size(), cp, pruned);
     locks[node].lock();
     std::copy(pruned.begin(), pruned.end(), row(node));

@@ -131,7 +131,7 @@ def lib() -> C.CDLL:
         L.oracle_vnew2_build.restype = i32
         L.oracle_v8_build.argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, u32, f32, u32, _u32p, _u32p, _u32p]
         L.oracle_v8_build.restype = i32
-        L.oracle_cpu_vamana_build.argtypes = [vp, i32, u32, u32, u32, u32, f32, u32, i32, _u32p, _u32p]
+        L.oracle_cpu_vamana_build.argtypes = [vp, i32, u32, u32, u32, u32, f32, u32, i32, i32, _u32p, _u32p]
         L.oracle_cpu_vamana_build.restype = u32
         L.oracle_cpu_occlude.argtypes = [vp, i32, u32, _u32p, _f32p, u32, u32, f32, u32, _u32p]
         L.oracle_cpu_occlude.restype = u32
@@ -154,8 +154,8 @@ def lib() -> C.CDLL:
         L.oracle_filtered_merge.argtypes = [u32, u32, u32, u32, _u32p, _u32p, u32, u32, _u32p, _u32p, u32,
                                             _u32p, _f32p, _u32p, _f32p, u32, _u32p, _f32p]
         L.oracle_filtered_merge.restype = u32
-        L.oracle_query_search.argtypes = [vp, i32, u32, u32, _u32p, _u32p, u32, _u32p, u32, vp, u32, u32, u32,
-                                          vp, vp, vp, _u32p, _f32p]
+        L.oracle_query_search.argtypes = [vp, i32, u32, u32, _u32p, _u32p, u32, _u32p, u32, _u32p, vp, u32, u32,
+                                          u32, vp, vp, vp, _u32p, _f32p]
         L.oracle_query_search.restype = u64
         L.oracle_filtered_shortlist.argtypes = [u32, u32, _u32p, _u32p, u32, u32, u32, u32, _u32p, _f32p, u32,
                                                 _u32p, _f32p]
@@ -325,15 +325,21 @@ def v8_build(data: np.ndarray, R=64, L=100, C_=80, STEPS=64, iters=4, alpha=1.2,
     return graph, deg, int(med[0])
 
 
-def cpu_vamana_build(data: np.ndarray, R=64, L=100, alpha=1.2, maxc=750, threads=0):
+CPU_POOLS = {"diskann": 0, "paper": 1}
+
+
+def cpu_vamana_build(data: np.ndarray, R=64, L=100, alpha=1.2, maxc=750, threads=0, pool="diskann"):
     """DiskANN-style CPU Vamana (cpu_baselines.cpp); threads=1 inserts in id
-    order (deterministic), 0 uses every OpenMP thread."""
+    order (deterministic), 0 uses every OpenMP thread. pool "diskann" prunes
+    the expanded set of the search (DiskANN's search_for_point_and_prune),
+    "paper" that set plus the point's current neighbours (Alg. 2 of the
+    paper)."""
     data = np.ascontiguousarray(data)
     N = data.shape[0]
     graph = np.empty((N, R), np.uint32)
     deg = np.empty(N, np.uint32)
     start = lib().oracle_cpu_vamana_build(data.ctypes.data, _dt(data), N, data.shape[1], R, L, alpha, maxc,
-                                          threads, _p(graph), _p(deg))
+                                          threads, CPU_POOLS[pool], _p(graph), _p(deg))
     return graph, deg, int(start)
 
 
@@ -505,22 +511,37 @@ def filtered_merge(N: int, R: int, C_: int, keep: int, offsets, labels, num_labe
     return out_i[:n], out_d[:n]
 
 
+def start_csr(starts, nq):
+    """starts as one id, one id per query, or one sequence of ids per query
+    -> (offsets or None, flat starts)."""
+    if isinstance(starts, (list, tuple)) and any(np.ndim(s) > 0 for s in starts):
+        lists = [np.atleast_1d(np.asarray(s, np.uint32)) for s in starts]
+        if len(lists) != nq:
+            raise ValueError("one start list per query")
+        off = np.zeros(nq + 1, np.uint32)
+        off[1:] = np.cumsum([x.shape[0] for x in lists])
+        flat = np.concatenate(lists) if lists else np.zeros(0, np.uint32)
+        return off, np.ascontiguousarray(flat if flat.size else np.zeros(1, np.uint32))
+    return None, np.atleast_1d(np.asarray(starts, np.uint32))
+
+
 def query_search(data, graph, degree, starts, queries, k, L, label_offsets=None, labels=None, query_labels=None):
     """Canonical-distance best-first search (DiskANN search semantics);
+    starts: one id, one per query, or a list of start lists (one per query);
     returns (ids, dists, distance count)."""
     data = np.ascontiguousarray(data)
     queries = np.ascontiguousarray(queries)
     graph = np.ascontiguousarray(graph, np.uint32)
     degree = np.ascontiguousarray(degree, np.uint32)
-    starts = np.atleast_1d(np.asarray(starts, np.uint32))
     nq = queries.shape[0]
+    soff, starts = start_csr(starts, nq)
     ids = np.empty((nq, k), np.uint32)
     dd = np.empty((nq, k), np.float32)
     opt = [None if a is None else np.ascontiguousarray(a, np.uint32) for a in (label_offsets, labels, query_labels)]
     ptrs = [None if a is None else a.ctypes.data for a in opt]
     n = lib().oracle_query_search(data.ctypes.data, _dt(data), data.shape[0], data.shape[1], _p(graph), _p(degree),
-                                  graph.shape[1], _p(starts), starts.shape[0], queries.ctypes.data, nq, k, L, *ptrs,
-                                  _p(ids), _p(dd, C.c_float))
+                                  graph.shape[1], _p(starts), starts.shape[0], None if soff is None else _p(soff),
+                                  queries.ctypes.data, nq, k, L, *ptrs, _p(ids), _p(dd, C.c_float))
     return ids, dd, int(n)
 
 

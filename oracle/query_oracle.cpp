@@ -41,14 +41,20 @@ bool has_label(const uint32_t* off, const uint32_t* lab, uint32_t p, uint32_t l)
 
 extern "C" {
 
-// starts: one entry (shared) or nq entries (per query); labels: optional
-// filter (offsets/labels per point, one label per query). Outputs the k best
+// starts: with start_offsets null, one entry (shared) or nq entries (per
+// query); with start_offsets (nq + 1 entries), query q starts from
+// starts[start_offsets[q] .. start_offsets[q + 1]) (DiskANN's init_ids of a
+// filtered search: the label's start plus its extra starts,
+// integrations/dance-diskann-78256bba.patch:20583-20625; they are inserted
+// without the label check, ids >= N skipped). labels: optional filter
+// (offsets/labels per point, one label per query). Outputs the k best
 // (distance, id) in order, INV / FLT_MAX past the end. Returns the number of
 // distances computed.
 uint64_t oracle_query_search(const void* data, int dtype, uint32_t N, uint32_t dim, const uint32_t* graph,
                              const uint32_t* degree, uint32_t R, const uint32_t* starts, uint32_t nstarts,
-                             const void* queries, uint32_t nq, uint32_t k, uint32_t L, const uint32_t* offsets,
-                             const uint32_t* labels, const uint32_t* qlabels, uint32_t* ids_out, float* d_out) {
+                             const uint32_t* start_offsets, const void* queries, uint32_t nq, uint32_t k,
+                             uint32_t L, const uint32_t* offsets, const uint32_t* labels, const uint32_t* qlabels,
+                             uint32_t* ids_out, float* d_out) {
   const size_t row = (size_t)dim * elem_size(dtype);
   const char* base = (const char*)data;
   const char* qs = (const char*)queries;
@@ -71,12 +77,16 @@ uint64_t oracle_query_search(const void* data, int dtype, uint32_t N, uint32_t d
         ex.pop_back();
       }
     };
-    const uint32_t start = starts[nstarts == 1 ? 0 : q];
     const uint32_t ql = qlabels ? qlabels[q] : INV;
-    if (start < N && L > 0) {
-      seen[start] = 1;
-      insert({dist(start), start});
-      ++total;
+    const uint32_t b0 = start_offsets ? start_offsets[q] : (nstarts == 1 ? 0u : (uint32_t)q);
+    const uint32_t b1 = start_offsets ? start_offsets[q + 1] : b0 + 1;
+    for (uint32_t b = b0; b < b1; ++b) {
+      const uint32_t start = starts[b];
+      if (start < N && L > 0 && !seen[start]) {
+        seen[start] = 1;
+        insert({dist(start), start});
+        ++total;
+      }
     }
     while (true) {
       size_t p = 0;

@@ -89,6 +89,14 @@ def test_cpu_publish_request_is_an_error(tmp_path):
     assert not os.path.exists(str(tmp_path / "idx"))
 
 
+def test_unknown_label_start_rule_is_an_error(tmp_path):
+    _, _, dp, lp = make_case(tmp_path, n=20)
+    env = dict(os.environ, DANCE_LABEL_STARTS="medoid")
+    r = run_app(*base_args(dp, lp, str(tmp_path / "idx")), env=env)
+    assert r.returncode == 255 and "neither balanced nor centroid" in r.stderr, r.stderr
+    assert not os.path.exists(str(tmp_path / "idx"))
+
+
 def expected_ids(rows, universal=None):
     """Label numbering: universal 0, others 1.. by first appearance."""
     ids = {} if universal is None else {universal: 0}
@@ -112,15 +120,21 @@ def centroid_start(x, carriers):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("kind,universal_every,R", [("uint8", 0, 64), ("float", 0, 64), ("uint8", 7, 64),
-                                                    ("uint8", 0, 32), ("float", 7, 12)])
-def test_app_matches_oracle(tmp_path, kind, universal_every, R):
+@pytest.mark.parametrize("kind,universal_every,R,rule", [("uint8", 0, 64, "balanced"), ("float", 0, 64, "balanced"),
+                                                         ("uint8", 7, 64, "balanced"), ("uint8", 0, 32, "balanced"),
+                                                         ("float", 7, 12, "balanced"), ("uint8", 7, 64, "centroid"),
+                                                         ("float", 0, 32, "centroid")])
+def test_app_matches_oracle(tmp_path, kind, universal_every, R, rule):
     # R below 64: built at internal degree 64, published at R by the GPU
-    # publish step (patch:20368-20384, gpu_vamana_filtered.cu:6328-6432)
+    # publish step (patch:20368-20384, gpu_vamana_filtered.cu:6328-6432).
+    # Label starts: DiskANN's load-balanced rule (default) or the centroid
+    # option.
     x, rows, dp, lp = make_case(tmp_path, kind=kind, universal_every=universal_every)
     prefix = str(tmp_path / "idx")
     args = base_args(dp, lp, prefix, kind) + (["--universal_label", "ANY"] if universal_every else [])
-    env = {k: v for k, v in os.environ.items() if not k.startswith("DISKANN_GPU_FILTERED_")}
+    env = {k: v for k, v in os.environ.items() if not k.startswith(("DISKANN_GPU_FILTERED_", "DANCE_LABEL"))}
+    if rule == "centroid":
+        env["DANCE_LABEL_STARTS"] = "centroid"
     r = run_app(*args, "--max_degree", str(R), env=env)
     assert r.returncode == 0, r.stdout + r.stderr
     assert f"requested_R={R} internal_R=64" in r.stdout
@@ -146,15 +160,19 @@ def test_app_matches_oracle(tmp_path, kind, universal_every, R):
         for l in f:
             a, b = l.split(",")
             starts[int(a)] = int(b)
-    for lab in range(num_labels):
-        carriers = np.array([i for i in range(n) if lab in canon[i]], np.int64)
-        assert (starts[lab] == INV) == (carriers.size == 0)
-        if carriers.size:
-            assert starts[lab] == centroid_start(x, carriers)
+    ls = F.canonical_labels(canon, num_labels)
+    if rule == "balanced":
+        want_starts = F.balanced_label_starts(ls, 0 if universal_every else INV, seed=1)
+        assert np.array_equal(starts, want_starts)
+    else:
+        for lab in range(num_labels):
+            carriers = np.array([i for i in range(n) if lab in canon[i]], np.int64)
+            assert (starts[lab] == INV) == (carriers.size == 0)
+            if carriers.size:
+                assert starts[lab] == centroid_start(x, carriers)
     adj, max_deg, start, frozen = formats.read_graph(prefix)
     assert start == centroid_start(x, np.arange(n)) and frozen == 0
     # graph vs the oracle's build with the same inputs, then the install rule
-    ls = F.canonical_labels(canon, num_labels)
     rc, g, deg, _ = O.filtered_build(x, ls.offsets, ls.labels, starts, num_labels, R=64, L=100, filtered_L=100,
                                      C_=750, STEPS=64, alpha=1.2, universal=0 if universal_every else INV,
                                      global_start=start, publish_R=R if R < 64 else 0)
@@ -182,7 +200,7 @@ def test_reselected_label_starts(tmp_path, kind, universal_every, R):
     x, rows, dp, lp = make_case(tmp_path, kind=kind, universal_every=universal_every, seed=9)
     prefix = str(tmp_path / "idx")
     args = base_args(dp, lp, prefix, kind) + (["--universal_label", "ANY"] if universal_every else [])
-    env = {k: v for k, v in os.environ.items() if not k.startswith("DISKANN_GPU_FILTERED_")}
+    env = {k: v for k, v in os.environ.items() if not k.startswith(("DISKANN_GPU_FILTERED_", "DANCE_LABEL"))}
     env["DISKANN_GPU_FILTERED_RESELECT_LABEL_STARTS"] = "common_degree"
     r = run_app(*args, "--max_degree", str(R), env=env)
     assert r.returncode == 0, r.stdout + r.stderr
@@ -192,13 +210,9 @@ def test_reselected_label_starts(tmp_path, kind, universal_every, R):
     canon = [sorted(set(rw)) for rw in per_row]
     num_labels = max(ids.values()) + 1
     universal = 0 if universal_every else INV
-    starts = np.full(num_labels, INV, np.uint32)
-    for lab in range(num_labels):
-        carriers = np.array([i for i in range(n) if lab in canon[i]], np.int64)
-        if carriers.size:
-            starts[lab] = centroid_start(x, carriers)
-    _, _, start, _ = formats.read_graph(prefix)
     ls = F.canonical_labels(canon, num_labels)
+    starts = F.balanced_label_starts(ls, universal, seed=1)
+    _, _, start, _ = formats.read_graph(prefix)
     rc, g, deg, _ = O.filtered_build(x, ls.offsets, ls.labels, starts, num_labels, R=64, L=100, filtered_L=100,
                                      C_=750, STEPS=64, alpha=1.2, universal=universal, global_start=start,
                                      publish_R=R if R < 64 else 0)

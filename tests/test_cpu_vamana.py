@@ -82,12 +82,13 @@ def py_greedy(x, q, neighbours, start, L):
     return order, [b[1] for b in beam]
 
 
-def py_vamana(x, R, L, alpha, maxc):
+def py_vamana(x, R, L, alpha, maxc, keep_own=False):
     """The paper's Alg. 3 as one pass in id order with DiskANN's graph slack:
-    search from the start, prune V u N_out(p), then for each new neighbour n
-    append p while n holds fewer than ceil(1.3 R) ids, else prune N_out(n) u
-    {p}; rows above R are pruned at the end. The start is the point nearest to
-    the centroid (fp64, first on ties)."""
+    search from the start, prune V (DiskANN's code) or V u N_out(p) (the
+    paper's Alg. 2, keep_own), then for each new neighbour n append p while n
+    holds fewer than ceil(1.3 R) ids, else prune N_out(n) u {p}; rows above R
+    are pruned at the end. The start is the point nearest to the centroid
+    (fp64, first on ties)."""
     n, dim = x.shape
     cent = [0.0] * dim
     for i in range(n):
@@ -106,7 +107,7 @@ def py_vamana(x, R, L, alpha, maxc):
     G = [[] for _ in range(n)]
     for p in range(n):
         order, _ = py_greedy(x, x[p], lambda u: list(G[u]), start, L)
-        G[p] = py_robust_prune(x, p, order + G[p], R, alpha, maxc)
+        G[p] = py_robust_prune(x, p, order + (G[p] if keep_own else []), R, alpha, maxc)
         for m in G[p]:
             if p in G[m]:
                 continue
@@ -198,16 +199,18 @@ def test_greedy_with_full_beam_is_exact_on_reachable_points():
 
 @pytest.mark.parametrize("seed,n,dim,levels,R,L,alpha,maxc", [
     (0, 150, 6, 4, 8, 16, 1.2, 750), (1, 120, 4, 3, 6, 10, 1.2, 750),
-    (2, 160, 8, 6, 10, 20, 1.5, 40), (3, 100, 5, 2, 5, 8, 1.0, 750)])
-def test_single_thread_build_matches_restatement(seed, n, dim, levels, R, L, alpha, maxc):
+    (2, 160, 8, 6, 10, 20, 1.5, 40), (3, 100, 5, 2, 5, 8, 1.0, 750), (5, 1000, 8, 6, 8, 8, 1.2, 750)])
+@pytest.mark.parametrize("pool", ["diskann", "paper"])
+def test_single_thread_build_matches_restatement(seed, n, dim, levels, R, L, alpha, maxc, pool):
     rng = np.random.default_rng(40 + seed)
     x = tie_rows(rng, n, dim, levels)
-    g, deg, start = O.cpu_vamana_build(x, R, L, alpha, maxc, threads=1)
-    G, s2 = py_vamana(x, R, L, alpha, maxc)
+    g, deg, start = O.cpu_vamana_build(x, R, L, alpha, maxc, threads=1, pool=pool)
+    G, s2 = py_vamana(x, R, L, alpha, maxc, keep_own=pool == "paper")
     assert start == s2
     for v in range(n):
         assert g[v, :deg[v]].tolist() == G[v], v
         assert np.all(g[v, deg[v]:] == 0xFFFFFFFF)
+
 
 
 def test_parallel_build_is_a_valid_graph():
@@ -223,3 +226,14 @@ def test_parallel_build_is_a_valid_graph():
     q = rng.standard_normal((100, 16)).astype(np.float32)
     gt, _ = O.bruteforce_knn(x, q, 10)
     assert O.recall_at_k(O.beam_search(x, g, deg, start, q, 10, 64), gt) > 0.95
+
+
+def test_pools_differ():
+    """The two candidate pools give different graphs once points receive
+    reverse edges before their own turn (a build that ignored the setting
+    would pass the restatement test of only one of them)."""
+    rng = np.random.default_rng(45)
+    x = tie_rows(rng, 1000, 8, 6)  # a beam of 8: searches often miss earlier reverse edges
+    g1, d1, _ = O.cpu_vamana_build(x, 8, 8, 1.2, 750, threads=1, pool="diskann")
+    g2, d2, _ = O.cpu_vamana_build(x, 8, 8, 1.2, 750, threads=1, pool="paper")
+    assert not (np.array_equal(g1, g2) and np.array_equal(d1, d2))
