@@ -537,6 +537,17 @@ def parse_settings(text: str, C_: int, S: int) -> list:
 
 
 def run_gate(args) -> int:
+    """bench.py --gate: score_gate on the workload of --config, one summary
+    line on stdout."""
+    rec = score_gate(args)
+    print(json.dumps({"gate": args.config, "cpu_mean": rec["cpu_vamana"]["recall_mean"],
+                      "spread": rec["cpu_vamana"]["recall_spread"],
+                      "gpu": [(e["iters"], e["alpha_from"], e["C"], e["STEPS"], e["build_seconds"], e.get("all_pass"))
+                              for e in rec["gpu"]]}), flush=True)
+    return 0
+
+
+def score_gate(args) -> dict:
     """The recall gate of the north star on a whole workload: recall@10 of the
     GPU graph >= the CPU Vamana's - 0.005 at equal R, L and alpha, both graphs
     scored by the same GPU search (dance_search_resident) against exact ground
@@ -547,7 +558,8 @@ def run_gate(args) -> int:
     (oracle/cpu_baselines.cpp, every host thread) runs --gate-cpu-runs times,
     each timed; its insertion order depends on thread timing, so the record
     holds every run's recall, their mean and spread, and each setting passes
-    per L against the mean. Writes one JSON record to --gate-out."""
+    per L against the mean. Writes the record to --gate-out (when set) after
+    the GPU settings and after every CPU run, and returns it."""
     import torch
     import dance_amd as D
     from oracle import oracle as O  # the CPU comparator of the gate
@@ -679,14 +691,35 @@ def run_gate(args) -> int:
              "mean_degree": round(float(dc.mean()), 3), "recall": rec})
         log(f"gate {args.config}: CPU Vamana ({pool} pool) run {r + 1} {secs:.1f}s {rec}")
         del gc, dc
-        rec_all = record()
-    cpu_mean = rec_all["cpu_vamana"]["recall_mean"] if runs else None
-    spread = rec_all["cpu_vamana"]["recall_spread"] if runs else None
-    print(json.dumps({"gate": args.config, "cpu_mean": cpu_mean, "spread": spread,
-                      "gpu": [(e["iters"], e["alpha_from"], e["C"], e["STEPS"], e["build_seconds"], e.get("all_pass"))
-                              for e in gpu]}),
-          flush=True)
-    return 0
+        record()
+    del base_t, graph_t, deg_t
+    torch.cuda.empty_cache()
+    return record()
+
+
+def recorded_gate(config: str):
+    """The committed whole-workload gate record of a config (bench.py --gate
+    on the GPU box, copied to profiles/), or None."""
+    path = os.path.join(ROOT, "profiles", f"recall_gate_{config}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)
+
+
+def compact_gate(rec: dict, source: str | None = None) -> dict:
+    """The parts of a gate record the bench line carries."""
+    cv = rec["cpu_vamana"]
+    out = {"N": rec["N"], "queries": rec["queries"], "tolerance": rec["tolerance"],
+           "cpu_vamana": {"pool": cv.get("pool"), "threads": cv["threads"], "cpu_model": cv["cpu_model"],
+                          "seconds": [r["seconds"] for r in cv["runs"]], "recall_mean": cv["recall_mean"],
+                          "recall_spread": cv["recall_spread"], "alt_pool_recall_mean": cv.get("alt_pool_recall_mean")},
+           "gpu": [{k: e.get(k) for k in ("iters", "alpha_from", "C", "STEPS", "build_seconds", "digest", "recall",
+                                          "delta_vs_cpu_mean", "all_pass")} for e in rec["gpu"]],
+           "cheapest_passing": rec.get("cheapest_passing"), "command": rec["command"], "date": rec["date"]}
+    if source:
+        out["source"] = source
+    return out
 
 
 def main() -> int:
@@ -796,7 +829,10 @@ def main() -> int:
                 "traffic": None, "kernel": "k_search (search + online robust insert)",
                 "avg_launch_ms": round(avg_ms, 3), "launches": launches,
                 "algorithmic_bytes_per_launch": algo,
-                "algorithmic_GBps": round(algo / (avg_ms * 1e-3) / 1e9, 1)}
+                "algorithmic_GBps": round(algo / (avg_ms * 1e-3) / 1e9, 1),
+                "algorithmic_frac": round(algo / (avg_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "algorithmic_note": "cache-inclusive demand: every distance counts its whole row, every expansion "
+                                    "its adjacency row; L2 and the MALL serve the part above 1"}
     traffic_file = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
     if os.path.exists(traffic_file) and args.n is None and args.profile == "QUALITY":
         with open(traffic_file) as f:
@@ -806,6 +842,8 @@ def main() -> int:
         achieved = traffic / (avg_ms * 1e-3) / 1e9
         roofline.update({"achieved": round(achieved, 1), "frac": round(achieved / HBM_PEAK_GBS, 4),
                          "traffic": traffic, "traffic_source": tj["source"],
+                         "traffic_note": "fabric traffic (FETCH_SIZE + WRITE_SIZE, calibrated on a device copy): "
+                                         "Infinity Cache hits included, so an upper bound on HBM bytes",
                          "algorithmic_over_traffic": round(algo / traffic, 3)})
     else:
         tj = None
@@ -881,18 +919,23 @@ def main() -> int:
         if "recall_gate_alpha_schedule" in leg:
             gates[f"{args.config}_first_{m}_alpha_from_{args.gate_alpha_from}"] = leg["recall_gate_alpha_schedule"]
         if args.gate_c1 and args.config != "c1":
-            c1 = D.CONFIGS["c1"]
-            b1, q1 = D.make_workload(c1)
-            l1 = cpu_leg(torch, D, O, c1, "c1", b1, q1, c1["n"], min(1000, q1.shape[0]), with_port=False,
-                         alpha_from=args.gate_alpha_from)
-            gates["c1"] = l1["recall_gate"]
-            if "recall_gate_alpha_schedule" in l1:
-                gates[f"c1_alpha_from_{args.gate_alpha_from}"] = l1["recall_gate_alpha_schedule"]
-        rec_file = os.path.join(ROOT, "profiles", "recall_gate_c2.json")
-        if args.config != "c2" and os.path.exists(rec_file):
-            with open(rec_file) as f:
-                for k, v in json.load(f).items():
-                    gates[f"{k} (recorded)"] = v
+            # the whole c1 workload, live: the default schedule and 5
+            # iterations, against one CPU Vamana run
+            g1 = score_gate(argparse.Namespace(config="c1", n=None, gate_queries=1000, gate_settings="4:-1,5:-1",
+                                               gate_oracle_max=0, gate_cpu_pool="diskann", gate_cpu_alt_pool="paper",
+                                               gate_cpu_runs=1, gate_cpu_alt_runs=0, gate_out=""))
+            gates["c1 (live)"] = compact_gate(g1)
+        full = recorded_gate(args.config)
+        if full and cpu is not None:
+            rs = full["cpu_vamana"]["runs"]
+            secs = float(np.mean([r["seconds"] for r in rs]))
+            cpu["full_n"] = {"value": round(full["N"] / secs, 1), "seconds": round(secs, 2), "runs": len(rs),
+                             "cores": full["cpu_vamana"]["threads"], "N": full["N"],
+                             "source": f"profiles/recall_gate_{args.config}.json (recorded {full['date']})"}
+    for c in ("c1", "c2", "c3"):
+        rec = recorded_gate(c)
+        if rec:
+            gates[f"{c} (recorded)"] = compact_gate(rec, f"profiles/recall_gate_{c}.json")
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "vertices/s", "n_gpus": 1, "steps": args.steps,

@@ -144,7 +144,8 @@ class DanceStitchedStats(C.Structure):
                                            "build_max_seconds", "remap_seconds", "total_seconds")]
                 + [(n, C.c_uint64) for n in ("memberships", "remap_invalid_local_ids", "remap_self_loops",
                                              "remap_duplicate_edges")]
-                + [(n, C.c_uint32) for n in ("labels", "label_npts_min", "label_npts_max", "row_cap")])
+                + [(n, C.c_uint32) for n in ("labels", "label_npts_min", "label_npts_max", "row_cap")]
+                + [("peak_gpu_mem_gb", C.c_double)])
 
 
 def struct_dict(s: C.Structure) -> dict:

@@ -218,7 +218,7 @@ int run(const Opts& o) {
             << " per_label_gpu_build_max_seconds=" << st.build_max_seconds
             << " local_to_global_remap_seconds=" << st.remap_seconds << " write_index_seconds=" << write_index_s
             << " final_prune_seconds=0 metadata_seconds=" << metadata_s << " total_seconds=" << total_s
-            << " peak_gpu_mem_gb=0 output_edges=" << gs.edges << std::endl;
+            << " peak_gpu_mem_gb=" << st.peak_gpu_mem_gb << " output_edges=" << gs.edges << std::endl;
   if (!o.timing_json.empty()) {
     dio::JsonReport j;
     j.num("num_labels", num_labels).num("npts_per_label_min", lmin).num("npts_per_label_mean", mean)
@@ -230,7 +230,7 @@ int run(const Opts& o) {
         .num("per_label_gpu_build_max_seconds", st.build_max_seconds)
         .num("local_to_global_remap_seconds", st.remap_seconds).num("write_index_seconds", write_index_s)
         .num("final_prune_seconds", 0).num("metadata_seconds", metadata_s).num("total_seconds", total_s)
-        .num("peak_gpu_mem_gb", 0).num("output_edges", gs.edges);
+        .num("peak_gpu_mem_gb", st.peak_gpu_mem_gb).num("output_edges", gs.edges);
     dio::write_text(o.timing_json, j.text());
   }
   return 0;

@@ -1176,6 +1176,12 @@ static int resident_build(const void* d_data, int dtype, uint32_t N, uint32_t di
 // ---------------------------------------------------------------------------
 static DanceStitchedStats g_last_stitched{};
 
+// Device memory in use on the current GPU (total - free), 0 if unknown.
+static uint64_t device_used_bytes() {
+  size_t fr = 0, tot = 0;
+  return hipMemGetInfo(&fr, &tot) == hipSuccess && tot >= fr ? (uint64_t)(tot - fr) : 0u;
+}
+
 struct StitchedIn {
   const void* data;  // N x dim rows of dtype (device or host)
   bool data_on_device;
@@ -1351,6 +1357,7 @@ static int stitched_build(const StitchedIn& in) {
   const double t_setup = now_sec();
   int device = 0;
   DHIP(hipGetDevice(&device));
+  std::atomic<uint64_t> peak_used{device_used_bytes()};  // arenas and staging are allocated by now
   std::vector<uint32_t> local_medoid(in.num_labels, 0);
   std::atomic<uint32_t> next{0};
   std::atomic<int> failed{0};
@@ -1389,6 +1396,9 @@ static int stitched_build(const StitchedIn& in) {
     lst.deg_cur.borrowed = true;
     DCHECK(run_build(rows, in.Rs, in.Ls, in.C, steps, prof, lst, ws, nullptr, nullptr, &local_medoid[l], false));
     const double dt = now_sec() - tb;
+    const uint64_t used = device_used_bytes();
+    for (uint64_t cur = peak_used.load(); used > cur && !peak_used.compare_exchange_weak(cur, used);) {
+    }
     times[w].build_sum += dt;
     times[w].build_max = std::max(times[w].build_max, dt);
     return 0;
@@ -1436,6 +1446,7 @@ static int stitched_build(const StitchedIn& in) {
   }
   DHIP(hipStreamSynchronize(s));
   st.remap_seconds = now_sec() - tr;
+  st.peak_gpu_mem_gb = (double)std::max<uint64_t>(peak_used.load(), device_used_bytes()) / (1024.0 * 1024.0 * 1024.0);
   unsigned long long c3[3] = {0, 0, 0};
   DHIP(hipMemcpyAsync(c3, d_ctr.p, sizeof(c3), hipMemcpyDeviceToHost, s));
   DHIP(hipStreamSynchronize(s));

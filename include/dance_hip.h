@@ -75,11 +75,14 @@ int dance_vamana_build_resident(const void *d_data, int dtype, uint32_t num_poin
 
 /* dance_vamana_build_resident without any device allocation. No counterpart
  * in the reference: it is for callers that cannot allocate device memory
- * (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). Every buffer the build needs beyond the caller's inputs and
- * outputs comes from a per-GPU scratch array of 256 MiB that the library
- * holds until the process ends (at R=64, C=80, fp32 rows of 96 dimensions
- * that is about 120k vertices). Larger inputs return -1 with a message. The
+ * (tight serving loops, harnesses that forbid hipMalloc). It cannot be
+ * recorded into a HIP graph: the build waits on its stream and reads the
+ * medoid scores and the locality order back mid-build. Every buffer the
+ * build needs beyond the caller's inputs and outputs comes from a per-GPU
+ * scratch array of 256 MiB that the library holds until the process ends
+ * (at R=64, C=80, fp32 rows of 96 dimensions that is about 120k vertices);
+ * every process that loads the library reserves it on each GPU it uses.
+ * Larger inputs return -1 with a message. The
  * work runs on the null stream and creates no event, so the stage times of
  * dance_get_last_kernel_profile read 0 after it (the counters are kept).
  * Calls share their GPU's scratch array and keep nothing from one call to the
@@ -108,6 +111,11 @@ typedef struct {
     double setup_seconds, materialize_seconds, build_sum_seconds, build_max_seconds, remap_seconds, total_seconds;
     uint64_t memberships, remap_invalid_local_ids, remap_self_loops, remap_duplicate_edges;
     uint32_t labels, label_npts_min, label_npts_max, row_cap;
+    /* device memory in use (hipMemGetInfo: total - free, GiB, every process
+     * on the GPU counted), the largest of the samples before the label loop,
+     * after each label build and after the remap, as the reference's app
+     * reports it (apps/utils/gpu_stitched_vamana_index.cpp:231-306) */
+    double peak_gpu_mem_gb;
 } DanceStitchedStats;
 
 int dance_stitched_build(const void *h_data, int dtype, uint32_t num_points, uint32_t dim,

@@ -45,12 +45,13 @@ def digest(*arrays) -> str:
     return h.hexdigest()
 
 
-def standard_case(cfg_name: str, n: int):
-    """vnew2 build of the first n rows of a standard config's generator."""
+def standard_case(cfg_name: str, n: int, iters: int = 4):
+    """vnew2 build of the first n rows of a standard config's generator
+    (iters: the reference's VAMANA_ITERS, DANCE_VAMANA_ITERS on the GPU)."""
     cfg = D.CONFIGS[cfg_name]
     base, _ = D.make_workload(cfg, n=n)
-    g, d, m = O.vnew2_build(base, cfg["R"], cfg["L"], cfg["C"], cfg["STEPS"])
-    return {"config": cfg_name, "n": n, "input": digest(base),
+    g, d, m = O.vnew2_build(base, cfg["R"], cfg["L"], cfg["C"], cfg["STEPS"], iters=iters)
+    return {"config": cfg_name, "n": n, "iters": iters, "input": digest(base),
             "graph": digest(g, d, np.array([m], np.uint32)),
             "medoid": int(m), "degree_sum": int(d.sum())}
 
@@ -107,6 +108,8 @@ def stitched_case(n: int):
 
 
 CASES = {
+    "c1_100k": lambda: standard_case("c1", 100_000),
+    "c1_100k_iters5": lambda: standard_case("c1", 100_000, iters=5),
     "c2_1m": lambda: standard_case("c2", 1_000_000),
     "c3_200k": lambda: standard_case("c3", 200_000),
     "c4_200k": lambda: standard_case("c4", 200_000),

@@ -1,6 +1,7 @@
 """The BASELINE configurations, built on the GPU through the C ABI.
 
-c2 at its full 1M, the c3 and c4 generators at 200k, the c5 filtered build
+c1 and c2 at their full 100k and 1M (c1 also with 5 iterations, the setting
+that passes c1's recall gate), the c3 and c4 generators at 200k, the c5 filtered build
 at 50k and the c5 stitched build at its full 1M: the device graph must equal
 the CPU oracle's graph on the same generator output. The oracle graphs are
 committed as SHA-256 digests (tests/golden/config_fixtures.json, written by
@@ -72,12 +73,13 @@ def standard_input(name, n):
     return base
 
 
-@pytest.mark.parametrize("case", ["c2_1m", "c3_200k", "c4_200k"])
-def test_standard_config_equals_oracle(case):
+@pytest.mark.parametrize("case", ["c1_100k", "c1_100k_iters5", "c2_1m", "c3_200k", "c4_200k"])
+def test_standard_config_equals_oracle(case, monkeypatch):
     fx = FIX[case]
     cfg = D.CONFIGS[fx["config"]]
     base = standard_input(fx["config"], fx["n"])
     assert digest(base) == fx["input"], "generator output changed"
+    monkeypatch.setenv("DANCE_VAMANA_ITERS", str(fx.get("iters", 4)))
     res = D.vamana_build(base, cfg["R"], cfg["L"], cfg["C"], cfg["STEPS"])
     print(f"[{case}] medoid {res.medoid} (oracle {fx['medoid']}), degree sum {int(res.degree.sum())} "
           f"(oracle {fx['degree_sum']})", flush=True)

@@ -130,6 +130,9 @@ def test_stitched_equals_per_label_builds(tmp_path, kind):
     t = json.load(open(tj))
     assert t["num_labels"] == len(names) and t["total_label_memberships"] == n
     assert t["output_edges"] == sum(len(r) for r in want)
+    # device memory in use during the build (hipMemGetInfo): at least the
+    # build's own rows and graphs, at most one MI355X's HBM
+    assert x.nbytes / 2**30 < t["peak_gpu_mem_gb"] < 288
 
 
 @pytest.mark.gpu
@@ -192,6 +195,7 @@ def test_stitched_entry_multi_label_rows(Rs, Rout):
         assert np.all(g[v, d[v]:] == D.INVALID)
     assert st["memberships"] == pts.size and st["labels"] == len(names)
     assert st["remap_duplicate_edges"] > 0  # rows share points across labels
+    assert 0 < st["peak_gpu_mem_gb"] < 288
 
 
 @pytest.mark.gpu
