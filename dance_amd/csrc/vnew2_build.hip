@@ -65,6 +65,10 @@ struct Profile {
   uint32_t heavy_threshold, heavy_sample;
 };
 constexpr uint32_t kDefaultIters = 4;       // VAMANA_ITERS
+// Largest build list L: the search pool holds 16 slots per lane (the
+// reference sizes its LDS pool by L, vnew2.cu:193-199, 2221; DiskANN callers
+// build with L of several hundred).
+constexpr uint32_t kMaxBuildL = 1024;
 constexpr uint32_t kMaxIters = DANCE_MAX_ITERS;  // per-iteration arrays of DanceKernelProfile
 constexpr float kAlpha = 1.2f;              // VAMANA_ALPHA (last iteration only)
 constexpr uint32_t kFinalMinDegree = 64;    // FINAL_MIN_DEGREE
@@ -228,8 +232,8 @@ static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t ste
   const uint32_t Cp = round64(g.C);
   const size_t lds = (size_t)kWavesPerBlock * search_lds_words(Cp) * 4;
   SearchArgs a{rows.rs, g, L, steps, start, alpha, order, ctr, qb};
-  if (L > 256) {
-    std::fprintf(stderr, "[dance_hip] L=%u exceeds the supported maximum 256\n", L);
+  if (L > kMaxBuildL) {
+    std::fprintf(stderr, "[dance_hip] L=%u exceeds the supported maximum %u\n", L, kMaxBuildL);
     return -1;
   }
   return with_dt_cpl(rows.dtype, cpl, [&](auto dt, auto c) {
@@ -237,7 +241,7 @@ static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t ste
     // Bounded variants exist only where build_qbound can produce code rows.
     constexpr bool kHasQB = DT != DANCE_U8 && CPL <= 4;
     if constexpr (kHasQB) {
-      if (qb.rows) {
+      if (qb.rows && L <= 256) {
         if (L <= 128)
           hipLaunchKernelGGL((k_search<DT, CPL, 2, true>), xcd_grid(g.N), dim3(kBlock), lds, s, a, Cp);
         else
@@ -246,10 +250,13 @@ static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t ste
         return 0;
       }
     }
+    // pools above 256 entries (16 slots per lane) run the exact variant only
     if (L <= 128)
       hipLaunchKernelGGL((k_search<DT, CPL, 2, false>), xcd_grid(g.N), dim3(kBlock), lds, s, a, Cp);
-    else
+    else if (L <= 256)
       hipLaunchKernelGGL((k_search<DT, CPL, 4, false>), xcd_grid(g.N), dim3(kBlock), lds, s, a, Cp);
+    else
+      hipLaunchKernelGGL((k_search<DT, CPL, 16, false>), xcd_grid(g.N), dim3(kBlock), lds, s, a, Cp);
     DHIP(hipGetLastError());
     return 0;
   });
@@ -600,8 +607,8 @@ static int validate(uint32_t N, uint32_t dim, uint32_t R, uint32_t L, uint32_t C
     std::fprintf(stderr, "[gpu_vamana_build] STEPS=%u is larger than L=%u, clamp STEPS to L.\n", STEPS, L);
     STEPS = L;
   }
-  if (L > 256) {
-    std::fprintf(stderr, "[gpu_vamana_build] L=%u exceeds the supported maximum 256\n", L);
+  if (L > kMaxBuildL) {
+    std::fprintf(stderr, "[gpu_vamana_build] L=%u exceeds the supported maximum %u\n", L, kMaxBuildL);
     return -1;
   }
   if (vamana_iters() == 0) {

@@ -178,6 +178,8 @@ def test_parameter_errors_return_minus_one():
     assert lib.gpu_vamana_vnew2_build_float(x.ctypes.data, 16, 8, 8, 16, 8, 8, None, dp) == -1
     assert lib.dance_vamana_build_resident(None, 0, 16, 8, 8, 16, 8, 8, None, None) == -1
     assert lib.dance_set_profile(b"NOPE") == -1
+    # build lists up to 1024 entries; more is rejected before any device call
+    assert lib.gpu_vamana_vnew2_build_float(x.ctypes.data, 16, 8, 8, 1025, 8, 8, gp, dp) == -1
     # rows wider than 16 chunks of 16 bytes per lane are rejected before any device call
     wide = np.zeros((16, 513), np.float32)
     gw = np.zeros((16, 8), np.uint32)

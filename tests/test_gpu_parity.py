@@ -294,6 +294,21 @@ def test_end_to_end_alpha_schedule(alpha_from, monkeypatch):
     assert not np.array_equal(default, og)  # the schedule changes the graph
 
 
+@pytest.mark.parametrize("kind,L,steps", [("f32", 300, 64), ("u8", 500, 80), ("f32", 1000, 100),
+                                          ("f32", 257, 257)])
+def test_end_to_end_wide_search_list(kind, L, steps):
+    """Build lists above 256 entries (the 16-slot pool; DiskANN callers build
+    with L of several hundred and the reference sizes its pool by L,
+    vnew2.cu:193-199, 2221), against the oracle."""
+    dim = 96 if kind != "u8" else 128
+    data = make_data(kind, 3000, dim, seed=L)
+    res = D.vamana_build(data, 32, L, 48, steps)
+    og, od, om = O.vnew2_build(data, 32, L, 48, steps)
+    assert res.medoid == om
+    assert np.array_equal(res.degree, od)
+    assert np.array_equal(res.graph, og)
+
+
 @pytest.mark.parametrize("kind,iters,alpha_from", [("f32", 5, None), ("f32", 6, None), ("f32", 6, 0),
                                                     ("u8", 6, None), ("f32", 1, None), ("f32", 8, 5)])
 def test_end_to_end_iteration_count(kind, iters, alpha_from, monkeypatch):
