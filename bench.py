@@ -215,6 +215,48 @@ def label_reachability(graph: np.ndarray, deg: np.ndarray, ls, qlabels: np.ndarr
             "queries_fully_reachable": round(float(np.mean(full)), 4) if full else None}
 
 
+def label_subgraph_stats(graph: np.ndarray, deg: np.ndarray, ls, labels, starts) -> dict:
+    """For each label: its carriers' out-edges to other carriers (the edges a
+    filtered search can follow), the carriers with none, the start's own
+    count, and the share of carriers reachable from the start; means over
+    the labels."""
+    n, R = graph.shape
+    off, pts = ls.postings()
+    col = np.arange(R)[None, :]
+    carrier = np.zeros(n, bool)
+    vis = np.zeros(n, bool)
+    out = {"in_label_out_degree": [], "carriers_without_in_label_edge": [], "start_in_label_out_degree": [],
+           "carriers_reachable_from_start": []}
+    for l in labels:
+        c = pts[off[l]:off[l + 1]].astype(np.int64)
+        carrier[c] = True
+        rows = graph[c]
+        live = (col < deg[c][:, None]) & (rows < n)
+        nb = np.where(live, rows, 0).astype(np.int64)
+        inl = (live & carrier[nb]).sum(1)
+        out["in_label_out_degree"].append(float(inl.mean()))
+        out["carriers_without_in_label_edge"].append(float((inl == 0).mean()))
+        s0 = int(starts[l])
+        out["start_in_label_out_degree"].append(float(inl[np.searchsorted(c, s0)]) if s0 in set(c.tolist()) else 0.0)
+        front = np.array([s0], np.int64)
+        vis[front] = True
+        touched = [front]
+        while front.size:
+            r = graph[front]
+            r = r[col < deg[front][:, None]].astype(np.int64)
+            r = r[r < n]
+            r = np.unique(r[carrier[r]])
+            r = r[~vis[r]]
+            vis[r] = True
+            touched.append(r)
+            front = r
+        out["carriers_reachable_from_start"].append(float(vis[c].mean()))
+        carrier[c] = False
+        for t in touched:
+            vis[t] = False
+    return {k: round(float(np.mean(v)), 4) for k, v in out.items()}
+
+
 def cardinality_buckets(ls, names=(("P50", 50.0), ("P1", 1.0)), per_bucket: int = 5) -> dict:
     """The reference's query buckets (tools/prepare_multilabel_workload.py:
     243-253): per percentile of the label cardinalities, the per_bucket labels
@@ -346,6 +388,13 @@ def run_c5(args, mode) -> int:
                                              deg_t.data_ptr(), Rg, bent, bqs, 10, Ls, ls.offsets, ls.labels, bl)
                 b["recall@10"][f"L{Ls}"] = round(D.recall_at_k(found, bgt, 10), 4)
             b["reachability"] = label_reachability(g_host, d_host, ls, bl, bent, bgt)
+            b["subgraph"] = label_subgraph_stats(g_host, d_host, ls, b["labels"], primary)
+            bmany = [F.query_starts(base, bqs[r:r + 1], bl[r:r + 1], primary, extra)[0] for r in range(bl.size)]
+            b["recall@10_start_and_16_extra"] = {}
+            for Ls in BUCKET_LS:
+                found, _ = D.search_resident(base_t.data_ptr(), D.DTYPE_U8, n, c["dim"], graph_t.data_ptr(),
+                                             deg_t.data_ptr(), Rg, bmany, bqs, 10, Ls, ls.offsets, ls.labels, bl)
+                b["recall@10_start_and_16_extra"][f"L{Ls}"] = round(D.recall_at_k(found, bgt, 10), 4)
         analysis["buckets"] = buckets
         log(f"filtered analysis {json.dumps(analysis)} ({time.time() - t1:.1f}s)")
 
@@ -842,8 +891,11 @@ def main() -> int:
         achieved = traffic / (avg_ms * 1e-3) / 1e9
         roofline.update({"achieved": round(achieved, 1), "frac": round(achieved / HBM_PEAK_GBS, 4),
                          "traffic": traffic, "traffic_source": tj["source"],
-                         "traffic_note": "fabric traffic (FETCH_SIZE + WRITE_SIZE, calibrated on a device copy): "
-                                         "Infinity Cache hits included, so an upper bound on HBM bytes",
+                         "traffic_measured": tj.get("measured"), "traffic_graph_digest": tj.get("graph_digest"),
+                         "traffic_graph_is_this_graph": tj.get("graph_digest") == check["digest"],
+                         "traffic_note": "fabric traffic (FETCH_SIZE + WRITE_SIZE, calibrated on a device copy) of a "
+                                         "committed counter run: Infinity Cache hits included, so an upper bound on "
+                                         "HBM bytes",
                          "algorithmic_over_traffic": round(algo / traffic, 3)})
     else:
         tj = None
