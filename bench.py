@@ -972,10 +972,11 @@ def main() -> int:
             gates[f"{args.config}_first_{m}_alpha_from_{args.gate_alpha_from}"] = leg["recall_gate_alpha_schedule"]
         if args.gate_c1 and args.config != "c1":
             # the whole c1 workload, live: the default schedule and 5
-            # iterations, against one CPU Vamana run
+            # iterations, against three CPU Vamana runs (1k queries: one run
+            # alone is within the gate's width of noise)
             g1 = score_gate(argparse.Namespace(config="c1", n=None, gate_queries=1000, gate_settings="4:-1,5:-1",
                                                gate_oracle_max=0, gate_cpu_pool="diskann", gate_cpu_alt_pool="paper",
-                                               gate_cpu_runs=1, gate_cpu_alt_runs=0, gate_out=""))
+                                               gate_cpu_runs=3, gate_cpu_alt_runs=0, gate_out=""))
             gates["c1 (live)"] = compact_gate(g1)
         full = recorded_gate(args.config)
         if full and cpu is not None:
