@@ -262,33 +262,48 @@ struct RegPool {
 
   // insert() for a pool with size >= L and max_pos >= 0 (which every path
   // below preserves) and a valid candidate id.
-  // The slot registers are updated by selects on one straight path (no
-  // branch around them), so the compiler keeps them in place instead of
-  // copying them at every join; only the max recomputation is a (uniform)
-  // branch.
+  // The slot registers are updated by selects (no branch around them), so
+  // the compiler keeps them in place instead of copying them at every join;
+  // the uniform branches are the rare refresh of a duplicate and the max
+  // recomputation.
+  //
+  // An id already in the pool (rare: the visited cache filters repeats until
+  // it forgets them) refreshes its slot when closer. A new id replaces the
+  // worst slot; its distance is below max_d, so not NaN: its mkey is its bits
+  // and its skey those bits unless the distance is FLT_MAX or more (below an
+  // infinite worst entry), which pool_skey marks unselectable.
   __device__ __forceinline__ void insert_full(uint32_t nid, float nd, uint32_t lane) {
     max_pos = uni_i(max_pos);
     max_d = uni_f(max_d);
     if (!(nd < max_d)) return;  // uniform; a NaN distance changes nothing either
-    int same = -1;
+    uint64_t dup = 0;
 #pragma unroll
-    for (int r = PS - 1; r >= 0; --r) {
-      const uint64_t m = wballot(id[r] == nid);
-      same = m ? r * 64 + ffs64(m) : same;  // the lowest register wins
+    for (int r = 0; r < PS; ++r) dup |= wballot(id[r] == nid);
+    if (dup) {
+      int same = -1;
+#pragma unroll
+      for (int r = PS - 1; r >= 0; --r) {
+        const uint64_t m = wballot(id[r] == nid);
+        same = m ? r * 64 + ffs64(m) : same;  // the lowest register wins
+      }
+      same = uni_i(same);
+      if (!(nd < get_d(same))) return;
+      set_d(same, nd, lane);  // a duplicate keeps its id
+      if (same == max_pos) recompute_max();
+      return;
     }
-    same = uni_i(same);
-    const bool write = same < 0 || nd < get_d(same);
-    const int pos = same >= 0 ? same : max_pos;
-    const int mk = pool_mkey(nd), sk = pool_skey(mk);
-    const bool hit = write && (int)lane == (pos & 63);
+    const int mk = __float_as_int(nd);
+    const int sk = mk < kSelLimit ? mk : INT_MAX;
+    const bool at = (int)lane == (max_pos & 63);
+    const int reg = max_pos >> 6;
 #pragma unroll
     for (int r = 0; r < PS; ++r) {
-      const bool h = hit && r == (pos >> 6);
-      id[r] = h ? nid : id[r];  // a duplicate keeps its id
+      const bool h = at && r == reg;
+      id[r] = h ? nid : id[r];
       mkey[r] = h ? mk : mkey[r];
       skey[r] = h ? sk : skey[r];
     }
-    if (write && pos == max_pos) recompute_max();
+    recompute_max();
   }
 
   // select_next_unexpanded_size_warp: smallest distance among unexpanded
