@@ -553,24 +553,26 @@ struct SearchWave {
     const uint32_t N = a.g.N, C = a.g.C;
     if (x == DANCE_INV || x >= N || x == node) return;
     n_try++;
-    for (uint32_t b = 0; b < wdeg; b += 64) {
-      const uint32_t i = b + lane;
-      if (wballot(i < wdeg && wid[i] == x)) return;
-    }
+    // x's row is requested first (x < N), so its load overlaps the pass
+    // below; a repeated x leaves it unused.
     uint4 xv[CPL];
     load_row<CPL>(a.rs, x, true, sub, xv);
-    const uint32_t xv_sq = self_term<DT, CPL>(xv);
+    // One pass over the row: x already there ends the insert; otherwise the
+    // usable entries nearer (nA) and farther (nB) than x, and the unusable
+    // ones (nU), which rank lowest in the order.
     uint32_t nA = 0, nB = 0, nU = 0;
     for (uint32_t b = 0; b < wdeg; b += 64) {
       const uint32_t i = b + lane;
       const bool in = i < wdeg;
       const uint32_t y = in ? wid[i] : DANCE_INV;
+      if (wballot(in && y == x)) return;
       const float dpy = in ? wdd[i] : 0.0f;
       const bool v = in && valid_for(y, N, node);
       nA += popc64(wballot(v && dpy <= dpx));
       nB += popc64(wballot(v && dpy > dpx));
       nU += popc64(wballot(in && !(v && dpy == dpy)));
     }
+    const uint32_t xv_sq = self_term<DT, CPL>(xv);
     // Occlusion: exists y with d_py <= d_px and alpha * d(y, x) <= d_px. The
     // answer does not depend on the order; the candidates are the order's
     // ranks [nU, nU + nA) (usable entries with d_py <= d_px, nearest to the
