@@ -165,14 +165,19 @@ struct RegPool {
     const int k = __builtin_amdgcn_readlane(v, pos & 63);
     return k == INT_MIN ? __builtin_nanf("") : __int_as_float(k);
   }
+  // Whether this lane's register r holds slot pos (never for pos < 0): one
+  // vector compare of the lane against the uniform pos - 64 r, which lies in
+  // [0, 64) only for the register that holds the slot.
+  static __device__ __forceinline__ bool at_slot(uint32_t lane, int r, int pos) {
+    return lane == (uint32_t)pos - 64u * (uint32_t)r;
+  }
   // Slot updates are select instructions on every lane (no divergent
   // branch, so no register copies at the merge).
   __device__ __forceinline__ void set_slot(int pos, uint32_t nid, float nd, uint32_t lane) {
     const int mk = pool_mkey(nd), sk = pool_skey(mk);
-    const bool hit = (int)lane == (pos & 63);
 #pragma unroll
     for (int r = 0; r < PS; ++r) {
-      const bool h = hit && r == (pos >> 6);
+      const bool h = at_slot(lane, r, pos);
       id[r] = h ? nid : id[r];
       mkey[r] = h ? mk : mkey[r];
       skey[r] = h ? sk : skey[r];
@@ -180,27 +185,28 @@ struct RegPool {
   }
   __device__ __forceinline__ void set_d(int pos, float nd, uint32_t lane) {
     const int mk = pool_mkey(nd), sk = pool_skey(mk);
-    const bool hit = (int)lane == (pos & 63);
 #pragma unroll
     for (int r = 0; r < PS; ++r) {
-      const bool h = hit && r == (pos >> 6);
+      const bool h = at_slot(lane, r, pos);
       mkey[r] = h ? mk : mkey[r];
       skey[r] = h ? sk : skey[r];
     }
   }
   __device__ __forceinline__ void set_expanded(int pos, uint32_t lane) {
-    const bool hit = (int)lane == (pos & 63);
 #pragma unroll
-    for (int r = 0; r < PS; ++r) skey[r] = (hit && r == (pos >> 6)) ? INT_MAX : skey[r];
+    for (int r = 0; r < PS; ++r) skey[r] = at_slot(lane, r, pos) ? INT_MAX : skey[r];
   }
 
   // recompute_max_pos_size_warp: largest distance, lowest slot on ties.
+  // kHasNumber: the caller knows some slot holds a non-NaN distance, so the
+  // empty case (every mkey INT_MIN) cannot occur and is not tested.
+  template <bool kHasNumber = false>
   __device__ __forceinline__ void recompute_max() {
     int best = mkey[0];
 #pragma unroll
     for (int r = 1; r < PS; ++r) best = max(best, mkey[r]);
     const int M = wave_max_i(best);
-    if (M == INT_MIN) {
+    if (!kHasNumber && M == INT_MIN) {
       max_pos = -1;
       max_d = -FLT_MAX;
       return;
@@ -241,10 +247,10 @@ struct RegPool {
     const bool replace = same < 0 && size >= L && max_pos >= 0 && nd < max_d;
     const int pos = same >= 0 ? same : (append ? (int)size : max_pos);
     const int mk = pool_mkey(nd), sk = pool_skey(mk);
-    const bool hit = (refresh || append || replace) && (int)lane == (pos & 63);
+    const bool any = refresh || append || replace;
 #pragma unroll
     for (int r = 0; r < PS; ++r) {
-      const bool h = hit && r == (pos >> 6);
+      const bool h = any && at_slot(lane, r, pos);
       id[r] = h ? nid : id[r];  // a duplicate keeps its id
       mkey[r] = h ? mk : mkey[r];
       skey[r] = h ? sk : skey[r];
@@ -256,7 +262,7 @@ struct RegPool {
         max_d = uni_f(nd);
       }
     } else if (replace || (refresh && same == max_pos)) {
-      recompute_max();
+      recompute_max<true>();  // nd is a number
     }
   }
 
@@ -289,21 +295,19 @@ struct RegPool {
       same = uni_i(same);
       if (!(nd < get_d(same))) return;
       set_d(same, nd, lane);  // a duplicate keeps its id
-      if (same == max_pos) recompute_max();
+      if (same == max_pos) recompute_max<true>();  // nd is a number
       return;
     }
     const int mk = __float_as_int(nd);
     const int sk = mk < kSelLimit ? mk : INT_MAX;
-    const bool at = (int)lane == (max_pos & 63);
-    const int reg = max_pos >> 6;
 #pragma unroll
     for (int r = 0; r < PS; ++r) {
-      const bool h = at && r == reg;
+      const bool h = at_slot(lane, r, max_pos);
       id[r] = h ? nid : id[r];
       mkey[r] = h ? mk : mkey[r];
       skey[r] = h ? sk : skey[r];
     }
-    recompute_max();
+    recompute_max<true>();  // nd is a number
   }
 
   // select_next_unexpanded_size_warp: smallest distance among unexpanded
@@ -439,13 +443,13 @@ struct SearchWave {
       // refresh a duplicate, else replace the worst slot.
       while (km) {
         const int k = ffs64(km);
-        km &= km - 1;
+        km &= ~(1ull << k);
         P.insert_full(rdlane_u(ck, k), rdlane_f(dk, k), lane);
       }
     } else {
       while (km) {
         const int k = ffs64(km);
-        km &= km - 1;
+        km &= ~(1ull << k);
         P.insert(rdlane_u(ck, k), rdlane_f(dk, k), lane);
       }
     }
