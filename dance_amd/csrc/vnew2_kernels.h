@@ -311,13 +311,15 @@ struct RegPool {
   }
 
   // select_next_unexpanded_size_warp: smallest distance among unexpanded
-  // entries with distance < FLT_MAX, lowest slot on ties; -1 if none.
-  __device__ __forceinline__ int select() const {
+  // entries with distance < FLT_MAX, lowest slot on ties; -1 if none. The
+  // selected entry's distance goes to *dist (its skey holds the bits).
+  __device__ __forceinline__ int select(float* dist) const {
     int best = skey[0];
 #pragma unroll
     for (int r = 1; r < PS; ++r) best = min(best, skey[r]);
     const int M = wave_min_i(best);
     if (M == INT_MAX) return -1;
+    *dist = __int_as_float(M);
     int pos = -1;
 #pragma unroll
     for (int r = 0; r < PS; ++r) {
@@ -562,9 +564,10 @@ struct SearchWave {
     uint4 xv[CPL];
     load_row<CPL>(a.rs, x, true, sub, xv);
     // One pass over the row: x already there ends the insert; otherwise the
-    // usable entries nearer (nA) and farther (nB) than x, and the unusable
-    // ones (nU), which rank lowest in the order.
-    uint32_t nA = 0, nB = 0, nU = 0;
+    // usable entries nearer (nA) and farther (nB) than x (dpx is a number,
+    // so a usable entry is exactly one of the two). The rest (nU), unusable,
+    // rank lowest in the order.
+    uint32_t nA = 0, nB = 0;
     for (uint32_t b = 0; b < wdeg; b += 64) {
       const uint32_t i = b + lane;
       const bool in = i < wdeg;
@@ -574,8 +577,8 @@ struct SearchWave {
       const bool v = in && valid_for(y, N, node);
       nA += popc64(wballot(v && dpy <= dpx));
       nB += popc64(wballot(v && dpy > dpx));
-      nU += popc64(wballot(in && !(v && dpy == dpy)));
     }
+    const uint32_t nU = wdeg - nA - nB;
     const uint32_t xv_sq = self_term<DT, CPL>(xv);
     // Occlusion: exists y with d_py <= d_px and alpha * d(y, x) <= d_px. The
     // answer does not depend on the order; the candidates are the order's
@@ -745,10 +748,10 @@ struct SearchWave {
     (void)t_seed;
     for (uint32_t step = 0; step < max_steps; ++step) {
       const uint64_t ts0 = dclock();
-      const int pos = P.select();
+      float dx;
+      const int pos = P.select(&dx);
       if (pos < 0) break;
       const uint32_t x = P.get_id(pos);
-      const float dx = P.get_d(pos);
       P.set_expanded(pos, lane);
       if (x == DANCE_INV || x >= N) break;
       n_exp++;
