@@ -510,23 +510,18 @@ struct SearchWave {
     }
     wave_sync();
   }
-  // Slot s now holds a usable entry of distance d; deg is the row length
-  // after the change (s == deg - 1 and fresh when appended).
-  __device__ __forceinline__ void ord_update(uint32_t s, float d, bool appended, uint32_t deg) {
-    uint32_t rnew = 0;
-    for (uint32_t b = 0; b < deg; b += 64) {
-      const uint32_t j = b + lane;
-      rnew += popc64(wballot(j < deg && j != s && before(j, d, s)));
-    }
-    uint32_t rold = deg - 1;
-    if (!appended) {
-      uint64_t m = 0;
-      uint32_t base = 0;
-      for (uint32_t b = 0; b < deg && !m; b += 64) {
-        m = wballot(b + lane < deg && ord[b + lane] == s);
-        base = b;
+  // Slot s now holds a usable entry of distance d; it left rank rold (deg - 1
+  // when appended: the new slot is appended at the top); deg is the row
+  // length after the change. rnew is its new rank when the caller knows it
+  // (no other entry has distance d), else kRankUnknown: then it is counted.
+  static constexpr uint32_t kRankUnknown = 0xFFFFFFFFu;
+  __device__ __forceinline__ void ord_update(uint32_t s, float d, uint32_t rold, uint32_t rnew, uint32_t deg) {
+    if (rnew == kRankUnknown) {
+      rnew = 0;
+      for (uint32_t b = 0; b < deg; b += 64) {
+        const uint32_t j = b + lane;
+        rnew += popc64(wballot(j < deg && j != s && before(j, d, s)));
       }
-      rold = base + (uint32_t)ffs64(m);
     }
     // ranks between rnew and rold move one step toward rold; rnew receives s.
     // Chunks of 64 are read before they are written and walk away from the
@@ -564,10 +559,10 @@ struct SearchWave {
     uint4 xv[CPL];
     load_row<CPL>(a.rs, x, true, sub, xv);
     // One pass over the row: x already there ends the insert; otherwise the
-    // usable entries nearer (nA) and farther (nB) than x (dpx is a number,
-    // so a usable entry is exactly one of the two). The rest (nU), unusable,
-    // rank lowest in the order.
-    uint32_t nA = 0, nB = 0;
+    // usable entries nearer than x (nA, of which nL strictly) and farther
+    // (nB); dpx is a number, so a usable entry is exactly one of nA and nB.
+    // The rest (nU), unusable, rank lowest in the order.
+    uint32_t nA = 0, nL = 0, nB = 0;
     for (uint32_t b = 0; b < wdeg; b += 64) {
       const uint32_t i = b + lane;
       const bool in = i < wdeg;
@@ -576,6 +571,7 @@ struct SearchWave {
       const float dpy = in ? wdd[i] : 0.0f;
       const bool v = in && valid_for(y, N, node);
       nA += popc64(wballot(v && dpy <= dpx));
+      nL += popc64(wballot(v && dpy < dpx));
       nB += popc64(wballot(v && dpy > dpx));
     }
     const uint32_t nU = wdeg - nA - nB;
@@ -586,16 +582,17 @@ struct SearchWave {
     // vertex first), and the test stops at the first pass of 8 that finds an
     // occluder.
     bool occluded = false;
-    for (uint32_t p = 0; p < nA && !occluded; p += 8) {
+    uint32_t p = 0;
+    for (; p < nA && !occluded; p += 8) {
       const uint32_t k0 = p + grp;
       const bool a0 = k0 < nA;
       const uint32_t y0 = a0 ? wid[ord[nU + k0]] : 0u;
       uint4 b0[CPL];
       load_row<CPL>(a.rs, y0, a0, sub, b0);
       const float d0 = octet_finish<DT, CPL>(a.rs, sub, xv, b0, xv_sq);
-      n_insert += min(8u, nA - p);
       occluded = wballot(sub == 0 && a0 && a.alpha * d0 <= dpx) != 0;
     }
+    n_insert += min(p, nA);  // distances of the passes made
     if (occluded) return;
     // Worst usable entry (largest d_py, lowest slot): the top of the order.
     int wpos = -1;
@@ -611,7 +608,8 @@ struct SearchWave {
     // and alpha * d(x, y) <= d_py. The nB candidates are the top nB ranks of
     // the order, already in that sequence, so only a prefix is gathered.
     int vpos = -1;
-    for (uint32_t p = 0; p < nB && vpos < 0; p += 8) {
+    uint32_t vrank = 0;
+    for (p = 0; p < nB && vpos < 0; p += 8) {
       const uint32_t k0 = p + grp;
       const bool a0 = k0 < nB;
       const uint32_t s0 = a0 ? ord[wdeg - 1u - k0] : 0u;
@@ -619,19 +617,29 @@ struct SearchWave {
       uint4 b0[CPL];
       load_row<CPL>(a.rs, y0, a0, sub, b0);
       const float d0 = octet_finish<DT, CPL>(a.rs, sub, xv, b0, xv_sq);
-      n_insert += min(8u, nB - p);
       const uint64_t hit = wballot(sub == 0 && a0 && a.alpha * d0 <= wdd[s0]);
-      if (hit) vpos = (int)ord[wdeg - 1u - (p + ((uint32_t)ffs64(hit) >> 3))];
+      if (hit) {
+        const int l = ffs64(hit);  // lane 8 g + 0 of the first octet that hit
+        vpos = (int)rdlane_u(s0, l);
+        vrank = wdeg - 1u - (p + ((uint32_t)l >> 3));
+      }
     }
+    n_insert += min(p, nB);
+    // The changed slot and the rank its old entry held: the victim's, the
+    // top rank for the worst entry, the new top for an appended slot.
     int mslot = -1;
+    uint32_t rold = 0;
     bool appended = false;
     if (vpos >= 0) {
       mslot = vpos;
+      rold = vrank;
     } else if (wdeg < C) {
       mslot = (int)wdeg;
+      rold = wdeg;
       appended = true;
     } else if (wpos >= 0 && dpx < wdist) {
       mslot = wpos;
+      rold = wdeg - 1u;
     }
     if (mslot >= 0) {
       wave_sync();
@@ -642,7 +650,10 @@ struct SearchWave {
       if (appended) wdeg++;
       n_mut++;
       wave_sync();
-      ord_update((uint32_t)mslot, dpx, appended, wdeg);
+      // Its new rank: the unusable entries and the usable ones strictly
+      // nearer than x rank below it (the replaced entry was farther); ties
+      // at distance dpx are ordered by slot, which only a count resolves.
+      ord_update((uint32_t)mslot, dpx, rold, nA == nL ? nU + nL : kRankUnknown, wdeg);
     }
   }
 
