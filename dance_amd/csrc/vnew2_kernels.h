@@ -226,11 +226,6 @@ struct RegPool {
 
   // insert_top_l_state_warp with ENABLE_TOPL_EARLY_REJECT=1. `nid`/`nd` are uniform.
   __device__ __forceinline__ void insert(uint32_t nid, float nd, uint32_t lane) {
-    // The pool state is wave-uniform; reading it through readfirstlane makes
-    // every branch below a scalar branch (no exec-masked regions).
-    size = uni_u(size);
-    max_pos = uni_i(max_pos);
-    max_d = uni_f(max_d);
     if (nid == DANCE_INV) return;
     if (size >= L && max_pos >= 0 && nd >= max_d) return;
     int same = -1;
@@ -279,8 +274,6 @@ struct RegPool {
   // and its skey those bits unless the distance is FLT_MAX or more (below an
   // infinite worst entry), which pool_skey marks unselectable.
   __device__ __forceinline__ void insert_full(uint32_t nid, float nd, uint32_t lane) {
-    max_pos = uni_i(max_pos);
-    max_d = uni_f(max_d);
     if (!(nd < max_d)) return;  // uniform; a NaN distance changes nothing either
     uint64_t dup = 0;
 #pragma unroll
