@@ -36,16 +36,24 @@ __device__ __forceinline__ uint64_t dclock() {
 #endif
 }
 
-// 512 slots: a search wave's LDS (visited cache, work row, batch, order) is
-// then 4 KB at C <= 128, so the register budget, not LDS, sets the waves per
-// SIMD (7 for the exact search instead of 6 with 1024 slots; c3 search
-// iterations 1-2 543 -> 499 and 663 -> 624 ms). The cache never changes a
-// result, only how many exact distances repeat.
+// 768 slots: a search wave's LDS (visited cache, work row, batch, order) is
+// then 5 KB at C <= 128, which still lets the register budget, not LDS, set
+// the waves per SIMD (8 for the uint8 rows of width 128, 7 for the exact
+// fp32 search: 8 x 4 waves of 5 KB fill the 160 KB of a CU). 1024 slots
+// cost the fp32 search a wave per SIMD and were slower (c3 iterations 1-2:
+// 543 and 663 ms against 499 and 624 ms with 512 slots, kernels of that
+// time); 768 against 512 saves 14 ms of the c4 build and 7 ms of c3. The
+// cache never changes a result, only how many exact distances repeat. A
+// slot count that is not a power of two hashes by a multiply-high.
 #ifndef DANCE_VIS_BITS
 #define DANCE_VIS_BITS 9
 #endif
-constexpr uint32_t kVisBits = DANCE_VIS_BITS;
-constexpr uint32_t kVis = 1u << kVisBits;  // visited cache slots per wave
+#ifndef DANCE_VIS_SLOTS
+#define DANCE_VIS_SLOTS 768u
+#endif
+constexpr uint32_t kVisBits = DANCE_VIS_BITS;  // used when the slot count is 2^kVisBits
+constexpr uint32_t kVis = DANCE_VIS_SLOTS;     // visited cache slots per wave
+static_assert(kVis % 64u == 0u && kVis >= 128u, "visited cache: whole 64-slot rows");
 constexpr uint32_t kWavesPerBlock = 4;
 constexpr uint32_t kBlock = 64 * kWavesPerBlock;
 constexpr uint32_t kQInFlight = 4;  // bound-filter passes whose loads are in flight together
@@ -325,7 +333,10 @@ struct RegPool {
   }
 };
 
-__device__ __forceinline__ uint32_t vis_slot(uint32_t id) { return (id * 0x9E3779B1u) >> (32 - kVisBits); }
+__device__ __forceinline__ uint32_t vis_slot(uint32_t id) {
+  if constexpr (kVis == (1u << kVisBits)) return (id * 0x9E3779B1u) >> (32 - kVisBits);
+  return __umulhi(id * 0x9E3779B1u, kVis);
+}
 
 struct SearchArgs {
   RowSet rs;
