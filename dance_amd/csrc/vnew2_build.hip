@@ -178,6 +178,19 @@ static int launch_init(const Rows& rows, GraphBufs g, hipStream_t s) {
 // the build uses it in the iterations whose bit is set in DANCE_QBOUND_ITERS
 // (default kQBoundIters). Results are identical either way.
 constexpr uint32_t kQBoundIters = 0x1u;  // first iteration: random graph, HBM-bound
+// Without DANCE_QBOUND_ITERS the search also uses it in the last iteration
+// when the iteration before it computed more than kQBoundLastMinDist
+// candidate distances per expansion: the last iteration (alpha > 1) then
+// gathers more rows than the bound's extra work costs. Measured with both
+// variants of the last search launch (4 iterations): c1 (isotropic, 49.5
+// distances per expansion in iteration 2) 23.6 -> 14.7 ms with the bound; c3
+// (26.7) 935 -> 875 ms; c2 (20.1) 54.2 -> 69.3 ms and c2 with fp16 rows
+// (20.1) 70.3 -> 85.7 ms, so it stays off there.
+constexpr double kQBoundLastMinDist = 24.0;
+static bool qbound_iters_adaptive() {
+  const char* e = std::getenv("DANCE_QBOUND_ITERS");
+  return !(e && e[0]);
+}
 // The prune uses it in the iterations of DANCE_QBOUND_PRUNE_ITERS (default
 // kQBoundPruneIters), and by default also in iteration 1 when iteration 0's
 // prune reached more than a quarter of all candidate pairs (its bound checks
@@ -681,7 +694,7 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   DCHECK(build_qbound(rows, qbuf, s, &qb));
   const uint32_t* order = nullptr;
   DCHECK(build_schedule(rows, qb, rws, s, &order));
-  const uint32_t q_iters = qbound_iters();
+  uint32_t q_iters = qbound_iters();  // the last iteration's bit may be set after the one before it
   uint32_t q_prune_iters = qbound_prune_iters();  // iteration 1's bit may be set after iteration 0
   const uint32_t iters = vamana_iters();
   if (iters == 0) return -1;  // validate() reports it
@@ -689,6 +702,7 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   const uint32_t p_rank = prune_rank_iters(rows.dtype);
   DCHECK(record(e_init, s));
 
+  VCounters before_last{};  // cumulative counters after iteration iters - 3 (zero if none)
   DevBuf snaps;  // timed builds: iters cumulative counter snapshots
   if (timed) DCHECK(snaps.alloc(sizeof(VCounters) * kMaxIters));
   struct IterEv {
@@ -731,6 +745,24 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
       DHIP(hipStreamSynchronize(s));
       const double pairs = (double)g.C * (double)(g.C > 0 ? g.C - 1 : 0) / 8.0;
       if ((double)h.prune_bound_checks > pairs * (double)g.N) q_prune_iters |= 2u;
+    }
+    if (qb.rows && qbound_iters_adaptive() && iters > 1 && it + 3 >= iters && it + 1 < iters) {
+      // candidate distances per expansion of the iteration before the last:
+      // cumulative counters after iterations iters - 3 and iters - 2
+      hipLaunchKernelGGL(k_ctr_sum, dim3(1), dim3(64), 0, s, static_cast<const VCounters*>(ctr),
+                         csum.as<VCounters>());
+      DHIP(hipGetLastError());
+      VCounters h{};
+      DHIP(hipMemcpyAsync(&h, csum.p, sizeof(VCounters), hipMemcpyDeviceToHost, s));
+      DHIP(hipStreamSynchronize(s));
+      if (it + 3 == iters) {
+        before_last = h;
+      } else {
+        const double cand = (double)(h.search_dist + h.bound_skips) -
+                            (double)(before_last.search_dist + before_last.bound_skips);
+        const double exps = (double)(h.expansions - before_last.expansions);
+        if (cand > kQBoundLastMinDist * exps) q_iters |= 1u << (iters - 1);
+      }
     }
     if (timed) {  // cumulative counters after this iteration
       hipLaunchKernelGGL(k_ctr_sum, dim3(1), dim3(64), 0, s, static_cast<const VCounters*>(ctr),
