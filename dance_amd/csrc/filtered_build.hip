@@ -264,7 +264,7 @@ int locality_order(const Rows& rows, const Labels& Ld, uint32_t N, uint32_t T, F
   uint32_t* vb[2] = {st.lrows.as<uint32_t>(), st.lsort.as<uint32_t>() + 2 * (size_t)N};
   DCHECK(with_dt_cpl(rows.dtype, pick_cpl(rows.rs.nch), [&](auto dt, auto c) {
     hipLaunchKernelGGL((k_cells<decltype(dt)::value, decltype(c)::value>), dim3(cells_grid(N)), dim3(kCellsBlock), 0,
-                       s, rows.rs, N, piv.as<const uint32_t>(), K, kb[0], vb[0]);
+                       s, rows.rs, N, piv.as<const uint32_t>(), K, 1u, kb[0], vb[0]);
     DHIP(hipGetLastError());
     return 0;
   }));

@@ -2099,7 +2099,7 @@ __global__ __launch_bounds__(kBlock) void k_init(RowSet rs, GraphBufs g) {
   }
 }
 
-// Approximate nearest pivot for the locality schedule, from integer codes:
+// Approximate nearest pivots for the locality schedule, from integer codes:
 // one thread per vertex, pivot codes staged in LDS 64 at a time. U8 = false
 // reads the quantized rows (header {s, r, a} + 7 chunks of int8 codes;
 // distance ~ a_x + a_p - 2 s_x s_p <q_x, q_p>); U8 = true reads uint8 rows of
@@ -2108,7 +2108,8 @@ __global__ __launch_bounds__(kBlock) void k_init(RowSet rs, GraphBufs g) {
 template <bool U8>
 __global__ __launch_bounds__(256) void k_cells_q(const uint4* __restrict__ rows, uint32_t stride16, uint32_t nch,
                                                  uint32_t N, const uint32_t* __restrict__ pivots, uint32_t K,
-                                                 uint32_t* __restrict__ cell, uint32_t* __restrict__ vid) {
+                                                 uint32_t levels, uint32_t* __restrict__ cell,
+                                                 uint32_t* __restrict__ vid) {
   constexpr uint32_t NC = U8 ? 8u : 7u;  // code chunks per row
   constexpr uint32_t OFF = U8 ? 0u : 1u;  // q-rows keep their header in chunk 0
   __shared__ uint4 pc[64][NC];
@@ -2138,8 +2139,7 @@ __global__ __launch_bounds__(256) void k_cells_q(const uint4* __restrict__ rows,
       ax = __uint_as_float(h.z);
     }
   }
-  float best = FLT_MAX;
-  uint32_t bi = 0;
+  Nearest3 nb;
   for (uint32_t k0 = 0; k0 < K; k0 += 64) {
     const uint32_t np = min(64u, K - k0);
     __syncthreads();
@@ -2192,14 +2192,11 @@ __global__ __launch_bounds__(256) void k_cells_q(const uint4* __restrict__ rows,
         }
         d = ax + pn[p] - 2.0f * sx * psc[p] * (float)dot;
       }
-      if (d < best) {
-        best = d;
-        bi = k0 + p;
-      }
+      nb.add(d, k0 + p);
     }
   }
   if (act) {
-    cell[v] = bi;
+    cell[v] = cell_key(nb.k1, nb.k2, nb.k3, K, levels);
     vid[v] = v;
   }
 }
