@@ -40,7 +40,9 @@ typedef struct DanceKernelProfile {
     /* Quantized lower bound of the search (fp32/fp16 rows of <= 112 dims):
      * candidates tested, and those whose exact distance it made unnecessary
      * (proved >= the pool threshold). DANCE_QBOUND=0 disables the bound;
-     * DANCE_QBOUND_ITERS selects the iterations (bit i = iteration i). */
+     * DANCE_QBOUND_ITERS selects the iterations (bit i = iteration i);
+     * unset, the first iteration and, when the iteration before it computed
+     * more than 24 candidate distances per expansion, the last. */
     uint64_t bound_checks, bound_skips;
     /* The same bound in RobustPrune: pairs tested, and pairs it proved far
      * enough that the candidate survives (DANCE_QBOUND_PRUNE_ITERS selects
