@@ -180,3 +180,36 @@ def test_build_identical_with_bound_off_first_and_every_iteration(profile):
     assert seen["first"][0] > 0 and seen["first"][1] > 0 and seen["first"][3] > 0
     assert seen["all"][0] > seen["first"][0]
     assert seen["prune_none"][2:] == (0, 0)
+
+
+def isotropic(n, dim, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((n, dim))
+    x /= np.linalg.norm(x, axis=1, keepdims=True)
+    return x.astype(np.float32)
+
+
+@pytest.mark.parametrize("n,R,L,C,steps", [(6000, 64, 100, 80, 64), (3000, 32, 64, 48, 32)])
+def test_last_iteration_bound_follows_candidate_count(n, R, L, C, steps):
+    """With DANCE_QBOUND_ITERS unset the build adds the bound to the last
+    search iteration exactly when the iteration before it computed more than
+    24 candidate distances (exact ones plus those the bound skipped) per
+    expansion; R64 isotropic rows cross that line, R32 rows (at most 32
+    candidates per expansion, most already seen) do not. The graph is the
+    oracle's either way, and an explicit mask keeps the last iteration exact."""
+    x = isotropic(n, 96, seed=n + R)
+    og, od, om = O.vnew2_build(x, R, L, C, steps)
+    prof = {}
+    for name, env in (("auto", {}), ("first", {"DANCE_QBOUND_ITERS": "1"})):
+        with _env(**env):
+            res = D.vamana_build(x, R, L, C, steps)
+        assert res.medoid == om and np.array_equal(res.degree, od) and np.array_equal(res.graph, og), name
+        prof[name] = res.kernel_profile
+    a, f = prof["auto"], prof["first"]
+    last = int(a["iterations"]) - 1
+    cand = a["search_dist_iter"][last - 1] + a["bound_skips_iter"][last - 1]
+    fired = cand > 24 * a["expansions_iter"][last - 1]
+    assert fired == (R == 64)
+    assert (a["bound_checks_iter"][last] > 0) == fired
+    assert f["bound_checks_iter"][last] == 0 and f["bound_checks_iter"][0] > 0
+    assert all(a["bound_checks_iter"][i] == 0 for i in range(1, last))
