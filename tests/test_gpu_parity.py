@@ -294,6 +294,26 @@ def test_end_to_end_alpha_schedule(alpha_from, monkeypatch):
     assert not np.array_equal(default, og)  # the schedule changes the graph
 
 
+@pytest.mark.parametrize("kind", ["f32", "u8"])
+def test_end_to_end_locality_schedule(kind, monkeypatch):
+    """The processing order never changes the graph: vertices sorted by their
+    three nearest of K pivots (K = 1024 and K = 37), by the nearest alone
+    (K = 2000, past the three-level key's range), or in id order (K = 0)."""
+    data = make_data(kind, 4000, 96 if kind == "f32" else 64, seed=23)
+    og, od, om = O.vnew2_build(data, 32, 64, 48, 32)
+    runs = [("1024", None), ("37", None), ("2000", None), ("0", None)]
+    if kind == "f32":
+        runs.append(("1024", "0"))  # no code rows: the pivots from the fp32 rows (k_cells)
+    for cells, qbound in runs:
+        monkeypatch.setenv("DANCE_LOCALITY_CELLS", cells)
+        if qbound is not None:
+            monkeypatch.setenv("DANCE_QBOUND", qbound)
+        res = D.vamana_build(data, 32, 64, 48, 32)
+        assert res.medoid == om, cells
+        assert np.array_equal(res.degree, od), cells
+        assert np.array_equal(res.graph, og), cells
+
+
 @pytest.mark.parametrize("kind,L,steps", [("f32", 300, 64), ("u8", 500, 80), ("f32", 1000, 100),
                                           ("f32", 257, 257)])
 def test_end_to_end_wide_search_list(kind, L, steps):
