@@ -1173,8 +1173,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kRankMin
   // 2. rank = number of candidates before it in (distance, index) order; an
   // id met twice marks both copies. Candidate k is read from lane k % 64 of
   // slot k / 64 (wave-uniform k, so the reads are register reads).
+  // Repeats are counted, not or-ed: a counter is one add per step, where a
+  // carried flag costs the compiler a 0/1 register and its re-test.
   uint32_t myrank[2] = {0u, 0u};
-  bool mydup[2] = {false, false};
+  uint32_t ndup[2] = {0u, 0u};
   const uint32_t dlo = min(deg, 64u);
   for (uint32_t k = 0; k < dlo; ++k) {  // k < 64 <= index of slot 1
     const uint32_t idk = (uint32_t)__builtin_amdgcn_readlane((int)myid[0], (int)k);
@@ -1182,8 +1184,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kRankMin
     const int kk = __builtin_amdgcn_readlane(mykey[0], (int)k);
     myrank[0] += (kk < mykey[0] || (kk == mykey[0] && k < lane)) ? 1u : 0u;
     myrank[1] += kk <= mykey[1] ? 1u : 0u;
-    mydup[0] = mydup[0] || (idk == myid[0] && k != lane);
-    mydup[1] = mydup[1] || idk == myid[1];
+    ndup[0] += (idk == myid[0] && k != lane) ? 1u : 0u;
+    ndup[1] += idk == myid[1] ? 1u : 0u;
   }
   for (uint32_t k = 64; k < deg; ++k) {  // k >= 64 > index of slot 0
     const uint32_t idk = (uint32_t)__builtin_amdgcn_readlane((int)myid[1], (int)(k - 64u));
@@ -1191,9 +1193,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kRankMin
     const int kk = __builtin_amdgcn_readlane(mykey[1], (int)(k - 64u));
     myrank[0] += kk < mykey[0] ? 1u : 0u;
     myrank[1] += (kk < mykey[1] || (kk == mykey[1] && k - 64u < lane)) ? 1u : 0u;
-    mydup[0] = mydup[0] || idk == myid[0];
-    mydup[1] = mydup[1] || (idk == myid[1] && k - 64u != lane);
+    ndup[0] += idk == myid[0] ? 1u : 0u;
+    ndup[1] += (idk == myid[1] && k - 64u != lane) ? 1u : 0u;
   }
+  const bool mydup[2] = {ndup[0] != 0u, ndup[1] != 0u};
   const uint64_t v0 = wballot(myid[0] != DANCE_INV), v1 = wballot(myid[1] != DANCE_INV);
   const uint32_t nvalid = popc64(v0) + popc64(v1);
 #pragma unroll
