@@ -421,13 +421,15 @@ struct SearchWave {
   // lane; DANCE_INV = none): visited filter, distances, ordered inserts.
   __device__ __forceinline__ void process_batch(uint32_t c) {
     const uint32_t N = a.g.N;
-    const bool v = valid_for(c, N, node);
     const uint32_t slot = vis_slot(c);
-    const bool seen = v && vis[slot] == c;
-    const bool need = v && !seen;
-    const uint64_t m = wballot(need);
+    const uint32_t at = vis[slot];
+    // Masks from ballots of single compares (c < N also excludes DANCE_INV).
+    const uint64_t mv = wballot(c < N) & wballot(c != node);
+    const uint64_t ms = mv & wballot(at == c);
+    const uint64_t m = mv & ~ms;
+    const bool need = c < N && c != node && at != c;
     const uint32_t n = popc64(m);
-    n_skip += popc64(wballot(seen));
+    n_skip += popc64(ms);
     if (n == 0) return;
     if (need) lst[mbcnt64(m)] = c;
     wave_sync();
@@ -440,9 +442,8 @@ struct SearchWave {
     c_dist += t1 - t0;
     const uint32_t ck = lst[lane];  // read only where lane < nx (keep below)
     const float dk = lsd[lane];
-    bool keep = lane < nx;
-    if (full) keep = keep && dk < P.max_d;
-    uint64_t km = wballot(keep);
+    uint64_t km = lanes_below(nx);
+    if (full) km &= wballot(dk < P.max_d);
     if (full) {
       // A pool that starts the batch full stays full with a valid worst
       // entry, so insert() reduces to: reject unless below the worst,
@@ -568,15 +569,15 @@ struct SearchWave {
     // The rest (nU), unusable, rank lowest in the order.
     uint32_t nA = 0, nL = 0, nB = 0;
     for (uint32_t b = 0; b < wdeg; b += 64) {
-      const uint32_t i = b + lane;
-      const bool in = i < wdeg;
-      const uint32_t y = in ? wid[i] : DANCE_INV;
-      if (wballot(in && y == x)) return;
-      const float dpy = in ? wdd[i] : 0.0f;
-      const bool v = in && valid_for(y, N, node);
-      nA += popc64(wballot(v && dpy <= dpx));
-      nL += popc64(wballot(v && dpy < dpx));
-      nB += popc64(wballot(v && dpy > dpx));
+      const uint32_t i = b + lane;  // < Cp: b < wdeg <= Cp, both multiples of 64
+      const uint64_t in = lanes_below(wdeg - b);
+      const uint32_t y = wid[i];
+      if (in & wballot(y == x)) return;
+      const float dpy = wdd[i];
+      const uint64_t v = in & wballot(y < N) & wballot(y != node);
+      nA += popc64(v & wballot(dpy <= dpx));
+      nL += popc64(v & wballot(dpy < dpx));
+      nB += popc64(v & wballot(dpy > dpx));
     }
     const uint32_t nU = wdeg - nA - nB;
     const uint32_t xv_sq = self_term<DT, CPL>(xv);
@@ -594,7 +595,7 @@ struct SearchWave {
       uint4 b0[CPL];
       load_row<CPL>(a.rs, y0, a0, sub, b0);
       const float d0 = octet_finish<DT, CPL>(a.rs, sub, xv, b0, xv_sq);
-      occluded = wballot(sub == 0 && a0 && a.alpha * d0 <= dpx) != 0;
+      occluded = (wballot(a.alpha * d0 <= dpx) & kOctetLeads & lanes_below(8u * (nA - p))) != 0;
     }
     n_insert += min(p, nA);  // distances of the passes made
     if (occluded) return;
@@ -621,7 +622,7 @@ struct SearchWave {
       uint4 b0[CPL];
       load_row<CPL>(a.rs, y0, a0, sub, b0);
       const float d0 = octet_finish<DT, CPL>(a.rs, sub, xv, b0, xv_sq);
-      const uint64_t hit = wballot(sub == 0 && a0 && a.alpha * d0 <= wdd[s0]);
+      const uint64_t hit = wballot(a.alpha * d0 <= wdd[s0]) & kOctetLeads & lanes_below(8u * (nB - p));
       if (hit) {
         const int l = ffs64(hit);  // lane 8 g + 0 of the first octet that hit
         vpos = (int)rdlane_u(s0, l);

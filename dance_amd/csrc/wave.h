@@ -41,6 +41,10 @@ __device__ __forceinline__ uint32_t mbcnt64(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 __device__ __forceinline__ int ffs64(uint64_t m) { return __ffsll((unsigned long long)m) - 1; }
+// Lanes [0, n) as a mask (n >= 64: every lane).
+__device__ __forceinline__ uint64_t lanes_below(uint32_t n) { return n >= 64u ? ~0ull : ((1ull << n) - 1ull); }
+// Lane 8 g of each octet g (the lanes that hold an octet's result).
+constexpr uint64_t kOctetLeads = 0x0101010101010101ull;
 __device__ __forceinline__ uint32_t popc64(uint64_t m) { return (uint32_t)__popcll((unsigned long long)m); }
 
 __device__ __forceinline__ int uni_i(int v) { return __builtin_amdgcn_readfirstlane(v); }
