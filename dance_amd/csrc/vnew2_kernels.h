@@ -286,6 +286,11 @@ struct RegPool {
     uint64_t dup = 0;
 #pragma unroll
     for (int r = 0; r < PS; ++r) dup |= wballot(id[r] == nid);
+    // Both outcomes write one slot through the same selects below; only the
+    // uniform slot and whether the max moves differ, so the slot registers
+    // are not copied between the two paths.
+    int pos = max_pos;
+    bool moved = true;
     if (dup) {
       int same = -1;
 #pragma unroll
@@ -295,20 +300,19 @@ struct RegPool {
       }
       same = uni_i(same);
       if (!(nd < get_d(same))) return;
-      set_d(same, nd, lane);  // a duplicate keeps its id
-      if (same == max_pos) recompute_max<true>();  // nd is a number
-      return;
+      pos = same;  // a duplicate keeps its id (nid)
+      moved = same == max_pos;
     }
     const int mk = __float_as_int(nd);
     const int sk = mk < kSelLimit ? mk : INT_MAX;
 #pragma unroll
     for (int r = 0; r < PS; ++r) {
-      const bool h = at_slot(lane, r, max_pos);
+      const bool h = at_slot(lane, r, pos);
       id[r] = h ? nid : id[r];
       mkey[r] = h ? mk : mkey[r];
       skey[r] = h ? sk : skey[r];
     }
-    recompute_max<true>();  // nd is a number
+    if (moved) recompute_max<true>();  // nd is a number
   }
 
   // select_next_unexpanded_size_warp: smallest distance among unexpanded
