@@ -350,6 +350,36 @@ def test_end_to_end_iteration_count(kind, iters, alpha_from, monkeypatch):
     assert all(t > 0 for t in kp["search_iter_ms"]) and all(t > 0 for t in kp["prune_iter_ms"])
 
 
+@pytest.mark.parametrize("kind", ["f32", "u8"])
+@pytest.mark.parametrize("n", [1, 2, 3, 17, 130])
+def test_end_to_end_tiny_inputs(kind, n):
+    # one point (no neighbours), two, three, and rows shorter than R
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal((n, 24)).astype(np.float32) if kind == "f32"
+         else rng.integers(0, 256, (n, 32), dtype=np.uint8))
+    res = D.vamana_build(x, 16, 24, 20, 12)
+    og, od, om = O.vnew2_build(x, 16, 24, 20, 12)
+    assert res.medoid == om
+    assert np.array_equal(res.degree, od)
+    assert np.array_equal(res.graph, og)
+
+
+@pytest.mark.parametrize("kind", ["f32", "u8"])
+def test_end_to_end_duplicate_rows(kind):
+    # 600 rows drawn from 12 distinct vectors: every search, insert and prune
+    # decision is a tie at distance 0 or between equal distances, resolved by
+    # slot and id order alone
+    rng = np.random.default_rng(5)
+    base = (rng.standard_normal((12, 24)).astype(np.float32) if kind == "f32"
+            else rng.integers(0, 256, (12, 32), dtype=np.uint8))
+    x = np.ascontiguousarray(base[rng.integers(0, 12, 600)])
+    res = D.vamana_build(x, 16, 32, 24, 16)
+    og, od, om = O.vnew2_build(x, 16, 32, 24, 16)
+    assert res.medoid == om
+    assert np.array_equal(res.degree, od)
+    assert np.array_equal(res.graph, og)
+
+
 @pytest.mark.parametrize("kind,dim", [("f32", 512), ("u8", 2048), ("f32", 200)])
 def test_end_to_end_wide_rows(kind, dim):
     # the widest supported rows (16 chunks of 16 bytes per lane) and a width
