@@ -182,6 +182,31 @@ def test_build_identical_with_bound_off_first_and_every_iteration(profile):
     assert seen["prune_none"][2:] == (0, 0)
 
 
+@pytest.mark.parametrize("profile", ["QUALITY", "FAST_SMALL"])
+def test_build_with_non_finite_rows(profile):
+    """Rows holding inf, -inf and NaN among the adversarial ones: their
+    distances are inf or NaN, which no pool selects and no prune keeps, with
+    the bound on and off; the graph is the oracle's."""
+    x = adversarial(3000, 96, seed=51, huge=profile == "QUALITY")
+    x[100] = np.inf
+    x[101, 3] = np.nan
+    x[102, 5] = -np.inf
+    x[103:110] = np.nan
+    x[110, :2] = [np.inf, -np.inf]
+    ox = x if profile == "QUALITY" else x.astype(np.float16)
+    og, od, om = O.vnew2_build(ox, 32, 64, 48, 32)
+    try:
+        D.set_profile(profile)
+        for env in ({}, {"DANCE_QBOUND": "0"}, {"DANCE_QBOUND_ITERS": "15", "DANCE_QBOUND_PRUNE_ITERS": "15"}):
+            with _env(**env):
+                res = D.vamana_build(x, 32, 64, 48, 32)
+            assert res.medoid == om, env
+            assert np.array_equal(res.degree, od), env
+            assert np.array_equal(res.graph, og), env
+    finally:
+        D.set_profile("QUALITY")
+
+
 def isotropic(n, dim, seed):
     rng = np.random.default_rng(seed)
     x = rng.standard_normal((n, dim))
