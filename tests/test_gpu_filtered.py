@@ -207,6 +207,18 @@ def test_filtered_tiny(n):
     assert_same(x, ls, starts, gs, 16, 32, 32, 64, 16)
 
 
+@pytest.mark.parametrize("kind", ["u8", "f32"])
+def test_filtered_duplicate_rows(kind):
+    """1500 rows drawn from 10 distinct vectors: the canonical pools, the
+    merge and FilteredRobustPrune meet equal distances everywhere and order
+    them by id alone."""
+    x, ls = make_case(kind, 1500, 32, 12, 3, seed=23)
+    rng = np.random.default_rng(3)
+    x = np.ascontiguousarray(x[rng.integers(0, 10, 1500)])
+    starts, gs = F.label_starts(x, ls), F.global_start(x)
+    assert_same(x, ls, starts, gs, 16, 32, 32, 64, 16)
+
+
 def log_fields(line):
     return dict(tok.split("=", 1) for tok in line.split()[1:])
 
