@@ -176,3 +176,21 @@ def test_gpu_multistart_search_matches_oracle(L, filtered):
     oi, od, _ = O.query_search(x, res.graph, res.degree, starts, q, 10, L, *lab)
     assert np.array_equal(ids, oi) and np.array_equal(dd.view(np.uint32), od.view(np.uint32))
     assert D.last_search_stats()["capped_queries"] == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", ["u8", "f32"])
+@pytest.mark.parametrize("L", [10, 100, 1000])
+def test_gpu_search_on_duplicate_rows(kind, L):
+    """2000 rows drawn from 15 distinct vectors and queries equal to some of
+    them: every result list is a run of equal distances (many of them 0)
+    ordered by id alone; ids and distances bit-exact with the oracle."""
+    base, _ = make(kind, 15, 32, seed=L + 1)
+    rng = np.random.default_rng(L)
+    x = np.ascontiguousarray(base[rng.integers(0, 15, 2000)])
+    q = np.ascontiguousarray(np.concatenate([base[rng.integers(0, 15, 100)], make(kind, 100, 32, seed=L)[1][:100]]))
+    g, d, med = O.vnew2_build(x, 16, 32, 24, 16)
+    ids, dd = D.search(x, g, d, med, q, 10, L)
+    oi, od, _ = O.query_search(x, g, d, med, q, 10, L)
+    assert np.array_equal(ids, oi)
+    assert np.array_equal(dd.view(np.uint32), od.view(np.uint32))
