@@ -1015,7 +1015,8 @@ def main() -> int:
                       "prune": [round(v, 2) for v in kp["prune_iter_ms"]]},
         "launch_counters": {k: list(kp[k]) for k in (
             "search_dist_iter", "insert_dist_iter", "expansions_iter", "bound_checks_iter", "bound_skips_iter",
-            "merge_dist_iter", "prune_dist_iter", "prune_bound_checks_iter", "prune_bound_skips_iter")},
+            "merge_dist_iter", "prune_dist_iter", "prune_bound_checks_iter", "prune_bound_skips_iter",
+            "insert_bound_checks_iter", "insert_bound_skips_iter")},
         "launch_algorithmic_GB": {"search": [round(v / 1e9, 2) for v in kp["search_bytes_iter"]],
                                   "prune": [round(v / 1e9, 2) for v in kp["prune_bytes_iter"]]},
         "kernels": kernels,
@@ -1024,7 +1025,8 @@ def main() -> int:
                                              "cyc_prune_fill")} if kp["cyc_prune_rounds"] else None),
         "counters": {k: kp[k] for k in ("search_dist", "insert_dist", "expansions", "vis_skips", "merge_dist",
                                         "prune_dist", "reverse_edges", "bound_checks", "bound_skips",
-                                        "prune_bound_checks", "prune_bound_skips")},
+                                        "prune_bound_checks", "prune_bound_skips", "insert_bound_checks",
+                                        "insert_bound_skips")},
         "search_cycles": ({k: kp[k] for k in ("cyc_select", "cyc_insert", "cyc_dist", "cyc_pool", "cyc_seed",
                                               "cyc_total")} if kp["cyc_total"] else None),
         "roofline": roofline,

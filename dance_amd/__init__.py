@@ -78,6 +78,8 @@ class DanceKernelProfile(C.Structure):
         ("prune_rounds", C.c_uint64), ("prune_exact_rounds", C.c_uint64),
         ("cyc_prune_rank", C.c_uint64), ("cyc_prune_gram", C.c_uint64), ("cyc_prune_rounds", C.c_uint64),
         ("cyc_prune_fill", C.c_uint64),
+        ("insert_bound_checks", C.c_uint64), ("insert_bound_skips", C.c_uint64),
+        ("insert_bound_checks_iter", C.c_uint64 * MAX_ITERS), ("insert_bound_skips_iter", C.c_uint64 * MAX_ITERS),
     ]
 
 
@@ -166,7 +168,8 @@ EXPORTS = [
     "gpu_vamana_vnew2_get_last_medoid", "gpu_vamana_vnew2_get_last_stats",
     "dance_vamana_build_resident", "dance_vamana_build_resident_noalloc", "dance_get_last_kernel_profile",
     "dance_set_profile", "dance_get_profile",
-    "dance_stage_distances", "dance_stage_qbound", "dance_stage_medoid", "dance_stage_init", "dance_stage_search",
+    "dance_stage_distances", "dance_stage_qbound", "dance_stage_insert_bound", "dance_stage_medoid",
+    "dance_stage_init", "dance_stage_search",
     "dance_stage_reverse_merge", "dance_stage_prune", "dance_stage_sort_pairs", "dance_stage_scan",
     "dance_synth_f32", "dance_synth_u8",
     "gpu_vamana_filtered_build_uint8", "gpu_vamana_filtered_build_float", "gpu_vamana_filtered_get_last_stats",
@@ -257,6 +260,7 @@ def lib() -> C.CDLL:
         L.dance_get_profile.restype = C.c_char_p
         L.dance_stage_distances.argtypes = [vp, i32, u32, u32, _u32p, _u32p, C.c_uint64, _f32p]
         L.dance_stage_qbound.argtypes = [vp, i32, u32, u32, _u32p, _u32p, _f32p, C.c_uint64, _u32p]
+        L.dance_stage_insert_bound.argtypes = [vp, i32, u32, u32, _u32p, _u32p, _f32p, f32, C.c_uint64, _u32p]
         L.dance_stage_medoid.argtypes = [vp, i32, u32, u32, _f32p, _u32p, _u32p]
         L.dance_stage_init.argtypes = [vp, i32, u32, u32, u32, u32, _u32p, _u32p, _u32p, _u32p, _f32p]
         L.dance_stage_search.argtypes = [vp, i32, u32, u32, u32, u32, u32, u32, f32, u32,
@@ -267,8 +271,8 @@ def lib() -> C.CDLL:
                                         _u32p, _u32p]
         L.dance_stage_sort_pairs.argtypes = [_u32p, _u32p, C.c_uint64, u32, _u32p, _u32p]
         L.dance_stage_scan.argtypes = [_u32p, C.c_uint64, _u32p]
-        for name in ("dance_stage_distances", "dance_stage_qbound", "dance_stage_medoid", "dance_stage_init",
-                     "dance_stage_search", "dance_stage_reverse_merge", "dance_stage_prune",
+        for name in ("dance_stage_distances", "dance_stage_qbound", "dance_stage_insert_bound", "dance_stage_medoid",
+                     "dance_stage_init", "dance_stage_search", "dance_stage_reverse_merge", "dance_stage_prune",
                      "dance_stage_sort_pairs", "dance_stage_scan"):
             getattr(L, name).restype = i32
         L.dance_synth_f32.argtypes = [C.c_uint64, u32, u32, u32, u32, f32, i32, _f32p]
@@ -438,6 +442,21 @@ def stage_qbound(data: np.ndarray, a: np.ndarray, b: np.ndarray, T: np.ndarray) 
     _check(lib().dance_stage_qbound(data.ctypes.data, dtype_code(data), data.shape[0], data.shape[1],
                                     _p(a, C.c_uint32), _p(b, C.c_uint32), _p(T, C.c_float), a.shape[0],
                                     _p(out, C.c_uint32)), "dance_stage_qbound")
+    return out
+
+
+def stage_insert_bound(data: np.ndarray, a: np.ndarray, b: np.ndarray, T0: np.ndarray, alpha: float) -> np.ndarray:
+    """The online insert's occlusion-pair bounds (x = a, y = b, T0 = d_px):
+    1 where the code rows prove fl(alpha * dist) <= T0, 2 where they prove
+    fl(alpha * dist) > T0, 0 where the pair is left to the exact distance."""
+    data = np.ascontiguousarray(data)
+    a = np.ascontiguousarray(a, dtype=np.uint32)
+    b = np.ascontiguousarray(b, dtype=np.uint32)
+    T0 = np.ascontiguousarray(T0, dtype=np.float32)
+    out = np.empty(a.shape[0], dtype=np.uint32)
+    _check(lib().dance_stage_insert_bound(data.ctypes.data, dtype_code(data), data.shape[0], data.shape[1],
+                                          _p(a, C.c_uint32), _p(b, C.c_uint32), _p(T0, C.c_float), float(alpha),
+                                          a.shape[0], _p(out, C.c_uint32)), "dance_stage_insert_bound")
     return out
 
 

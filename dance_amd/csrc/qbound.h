@@ -24,6 +24,8 @@
 // rejected by the pool's threshold test, so skipping its exact distance
 // leaves every result bit-identical. Rows with non-finite values, or whose
 // scale leaves [2^-60, 2^50], get r = +inf and are never skipped.
+// The same rows give an upper bound, sqrt(Q) + r_x + r_y >= ||x - y||
+// (q_pair_ub), which proves pair tests of the form fl(alpha * dist) <= T0.
 #pragma once
 
 #include "wave.h"
@@ -189,12 +191,10 @@ __device__ __forceinline__ bool q_pair_proves_m2(float m2s, float a, float sT, f
   return q >= w * w * (1.0f + kQSlack);
 }
 
-// Octet test for a candidate: every lane of the octet holds one chunk `b` of
-// its code row (q_load); the lane with sub == 0 (which holds the header)
-// returns whether the bound proves dist >= T. `code` is chunk `sub` of the
-// querying row. Must be called by all 64 lanes.
-__device__ __forceinline__ bool q_proves_reject(const QSelf& me, const uint4& code, float sT, const uint4& b,
-                                                bool active, uint32_t sub) {
+// Exact integer code dot of two rows whose chunk `sub` every lane of an
+// octet holds (chunk 0, the header, left out); every lane of the octet
+// receives it. Must be called by all 64 lanes.
+__device__ __forceinline__ int q_octet_dot(const uint4& code, const uint4& b, uint32_t sub) {
   int c = 0;
   c = __builtin_amdgcn_sdot4((int)code.x, (int)b.x, c, false);
   c = __builtin_amdgcn_sdot4((int)code.y, (int)b.y, c, false);
@@ -204,7 +204,56 @@ __device__ __forceinline__ bool q_proves_reject(const QSelf& me, const uint4& co
   c += dpp<kDppHalfMirror>(0, c);
   c += dpp<kDppQuadXor2>(0, c);
   c += dpp<kDppQuadXor1>(0, c);
+  return c;
+}
+
+// Octet test for a candidate: every lane of the octet holds one chunk `b` of
+// its code row (q_load); the lane with sub == 0 (which holds the header)
+// returns whether the bound proves dist >= T. `code` is chunk `sub` of the
+// querying row. Must be called by all 64 lanes.
+__device__ __forceinline__ bool q_proves_reject(const QSelf& me, const uint4& code, float sT, const uint4& b,
+                                                bool active, uint32_t sub) {
+  const int c = q_octet_dot(code, b, sub);
   return active && q_pair_proves(me.s, me.a, sT, __uint_as_float(b.x), __uint_as_float(b.y), __uint_as_float(b.z), c);
+}
+
+// The upper-bound side, for a pair test fl(alpha * dist) <= T0 (the online
+// insert's occlusion test). The canonical distance satisfies dist <= D (1 +
+// u)^(n_lane + 5) + 1e-30 <= D (1 + kappa2) + eta' by the rounding argument of
+// the lower side (binary16 terms: at most t^2 (1 + 2^-11)^3 + 2^-24 each),
+// with eta' <= 2 eta, and fl(alpha * dist) <= alpha dist (1 + u). So D <=
+// (T0 / (alpha (1 + u)) - 2 eta) / (1 + kappa2) proves the test. q_ub_root
+// returns the square root of that bound on D, rounded down (every step's
+// rounding absorbed by the 2^-20 and kQSlack factors), or -1 (never proved)
+// when T0 is below 1e-30 or not finite or the bound is not a positive finite
+// number.
+__device__ __forceinline__ float q_ub_root(const QBoundSet& qb, float T0, float alpha) {
+  if (!(T0 >= 1e-30f) || !(T0 <= FLT_MAX)) return -1.0f;
+  const float t = T0 / alpha * (1.0f - 0x1p-20f);
+  const float t2 = (t - 2.0f * qb.eta) / (1.0f + qb.kappa2) * (1.0f - kQSlack);
+  if (!(t2 > 0.0f) || !(t2 <= FLT_MAX)) return -1.0f;
+  return __builtin_sqrtf(t2) * (1.0f - kQSlack);
+}
+// q_ub_root for rows of type DT. The binary16 distance squares each
+// difference in binary16, which overflows to +inf past 65504; D <= 254^2
+// keeps every term finite (a difference of at most 254 (1 + 2^-11) squares
+// to below 65504), so the root is capped there for fp16 rows.
+template <int DT>
+__device__ __forceinline__ float q_ub_root_of(const QBoundSet& qb, float T0, float alpha) {
+  const float r = q_ub_root(qb, T0, alpha);
+  return DT == DANCE_F16 ? fminf(r, 254.0f) : r;
+}
+// Proves D <= root_ub^2 for the pair (querying row s, a, r; candidate
+// header sy, ry, ay; code dot c): by the triangle inequality ||x - y|| <=
+// sqrt(Q) + r_x + r_y, and Q <= Q_computed + 6 u (a_x + a_y); the fp32
+// evaluation adds kQSlack (a_x + a_y) + 1e-30 instead and rounds the sum up
+// by kQSlack. Rows with r = +inf are never proved.
+__device__ __forceinline__ bool q_pair_ub(float s, float a, float r, float root_ub, float sy, float ry, float ay,
+                                          int c) {
+  const float sa = a + ay;
+  const float q = __builtin_fmaf(-2.0f * (s * sy), (float)c, sa) + kQSlack * sa + 1e-30f;
+  const float lhs = (__builtin_sqrtf(fmaxf(q, 0.0f)) + r + ry) * (1.0f + kQSlack);
+  return lhs <= root_ub;
 }
 
 // Threshold of the prune's bound for a candidate at stored distance sd: a

@@ -213,6 +213,15 @@ static uint32_t env_mask(const char* name, uint32_t def) {
   return def;
 }
 static uint32_t qbound_iters() { return env_mask("DANCE_QBOUND_ITERS", kQBoundIters); }
+// Iterations whose search also bounds the online insert's occlusion pairs
+// (where the search bound is on): by default iteration 0 only, whose work
+// rows are the random initial graph, so the rows the exact test gathers
+// miss the caches. Measured (iteration 0 / build): c3 1249 -> 1211 ms, 3.676
+// -> 3.638 s; c2 120.6 -> 108.3 ms, 310 -> 298 ms; c1 13.6 -> 11.5 ms. In the
+// last iteration the rows are mostly cache hits and the bound's per-pair
+// work costs more than it saves (c3 857 -> 988 ms).
+constexpr uint32_t kInsertBoundIters = 0x1u;
+static uint32_t insert_bound_iters() { return env_mask("DANCE_INSERT_BOUND_ITERS", kInsertBoundIters); }
 static uint32_t qbound_prune_iters() { return env_mask("DANCE_QBOUND_PRUNE_ITERS", kQBoundPruneIters); }
 
 // Builds the code rows for `rows` into buf; returns a disabled set when the
@@ -239,8 +248,12 @@ static int build_qbound(const Rows& rows, DevBuf& buf, hipStream_t s, QBoundSet*
   return 0;
 }
 
+// insert_bound: with the search bound on, the online insert's occlusion test
+// also decides pairs on the code rows (fp32/fp16 rows of at most 3 chunks
+// per lane, C <= 128, L <= 128; elsewhere the request is ignored).
 static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t steps, float alpha, uint32_t start,
-                         const uint32_t* order, VCounters* ctr, const QBoundSet& qb, hipStream_t s) {
+                         const uint32_t* order, VCounters* ctr, const QBoundSet& qb, hipStream_t s,
+                         bool insert_bound) {
   const int cpl = pick_cpl(rows.rs.nch);
   const uint32_t Cp = round64(g.C);
   const size_t lds = (size_t)kWavesPerBlock * search_lds_words(Cp) * 4;
@@ -255,6 +268,14 @@ static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t ste
     constexpr bool kHasQB = DT != DANCE_U8 && CPL <= 4;
     if constexpr (kHasQB) {
       if (qb.rows && L <= 256) {
+        // (fp16 rows of at most 112 dims take 2 chunks per lane)
+        if constexpr (CPL <= (DT == DANCE_F16 ? 2 : 3)) {
+          if (insert_bound && L <= 128 && g.C <= 128) {  // nA <= C <= 128 fits the open-pair list
+            hipLaunchKernelGGL((k_search<DT, CPL, 2, true, true>), xcd_grid(g.N), dim3(kBlock), lds, s, a, Cp);
+            DHIP(hipGetLastError());
+            return 0;
+          }
+        }
         if (L <= 128)
           hipLaunchKernelGGL((k_search<DT, CPL, 2, true>), xcd_grid(g.N), dim3(kBlock), lds, s, a, Cp);
         else
@@ -700,6 +721,7 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   const uint32_t* order = nullptr;
   DCHECK(build_schedule(rows, qb, rws, s, &order));
   uint32_t q_iters = qbound_iters();  // the last iteration's bit may be set after the one before it
+  const uint32_t ib_iters = insert_bound_iters();
   uint32_t q_prune_iters = qbound_prune_iters();  // iteration 1's bit may be set after iteration 0
   const uint32_t iters = vamana_iters();
   if (iters == 0) return -1;  // validate() reports it
@@ -729,7 +751,7 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
       std::printf("[gpu_vamana_build] iteration %u / %u, alpha=%.3f\n", it + 1, iters, (double)alpha);
     DCHECK(record(iev[it].s0, s));
     const QBoundSet qb_it = ((q_iters >> it) & 1u) ? qb : QBoundSet{nullptr, 0.0f, 0.0f};
-    DCHECK(launch_search(rows, g, L, steps, alpha, start, order, ctr, qb_it, s));
+    DCHECK(launch_search(rows, g, L, steps, alpha, start, order, ctr, qb_it, s, ((ib_iters >> it) & 1u) != 0));
     DCHECK(record(iev[it].s1, s));
     RevCsr rev{};
     DCHECK(build_reverse_csr(g, rws, s, &rev));
@@ -834,6 +856,8 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   p.cyc_prune_gram = hc_ctr.cyc_prune_gram;
   p.cyc_prune_rounds = hc_ctr.cyc_prune_rounds;
   p.cyc_prune_fill = hc_ctr.cyc_prune_fill;
+  p.insert_bound_checks = hc_ctr.insert_bound_checks;
+  p.insert_bound_skips = hc_ctr.insert_bound_skips;
   const double V = rows.vbytes();
   for (uint32_t it = 0; timed && it < iters; ++it) {
     const VCounters& c = hsnap[it];
@@ -848,9 +872,11 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     p.prune_dist_iter[it] = c.prune_dist - b.prune_dist;
     p.prune_bound_checks_iter[it] = c.prune_bound_checks - b.prune_bound_checks;
     p.prune_bound_skips_iter[it] = c.prune_bound_skips - b.prune_bound_skips;
+    p.insert_bound_checks_iter[it] = c.insert_bound_checks - b.insert_bound_checks;
+    p.insert_bound_skips_iter[it] = c.insert_bound_skips - b.insert_bound_skips;
     p.search_bytes_iter[it] = (double)(p.search_dist_iter[it] + p.insert_dist_iter[it]) * V +
                               (double)p.expansions_iter[it] * (4.0 * R + 4.0) + (double)N * (V + 4.0 * R + 4.0 + 16.0 * C) +
-                              (double)p.bound_checks_iter[it] * (kQChunks * 16.0);
+                              (double)(p.bound_checks_iter[it] + p.insert_bound_checks_iter[it]) * (kQChunks * 16.0);
     // the rank kernel with the bound reads every candidate's code row once;
     // k_prune reads the code rows of the pairs it tests; the rank kernel's
     // Gram tiles (uint8 rows) read every candidate's row once for all pairs
@@ -864,7 +890,8 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     p.prune_bytes_iter[it] = pair_rows * V + (double)N * (24.0 * C) + qbytes;
   }
   p.search_bytes = (double)(p.search_dist + p.insert_dist) * V + (double)p.expansions * (4.0 * R + 4.0) +
-                   (double)iters * N * (V + 4.0 * R + 4.0 + 16.0 * C) + (double)p.bound_checks * (kQChunks * 16.0);
+                   (double)iters * N * (V + 4.0 * R + 4.0 + 16.0 * C) +
+                   (double)(p.bound_checks + p.insert_bound_checks) * (kQChunks * 16.0);
   p.merge_bytes = (double)p.merge_dist * 4.0 + (double)p.reverse_edges * 4.0 +
                   (double)p.touched_rows * (16.0 * C + 8.0);
   p.prune_bytes = (double)p.prune_dist * V + (double)iters * N * (24.0 * C) +
@@ -1058,6 +1085,39 @@ __global__ __launch_bounds__(kBlock) void k_qbound_pairs(QBoundSet qb, const uin
     const uint4 bc = q_load(qb, act ? b[k] : 0u, act, sub);
     const bool rej = q_proves_reject(me, code, sT, bc, act, sub);
     if (act && sub == 0) flag[k] = rej ? 1u : 0u;
+  }
+}
+
+// The online insert's occlusion-pair bounds on explicit pairs, as
+// occlusion_bounded evaluates them (x = a[k], y = b[k], T0 = d_px):
+// out[k] = 1 when the upper bound proves fl(alpha * dist) <= T0[k], 2 when
+// the lower bound proves fl(alpha * dist) > T0[k], 0 when the pair is open.
+template <int DT>
+__global__ __launch_bounds__(kBlock) void k_insert_bound_pairs(QBoundSet qb, const uint32_t* __restrict__ a,
+                                                               const uint32_t* __restrict__ b,
+                                                               const float* __restrict__ T0, float alpha, uint64_t n,
+                                                               uint32_t* __restrict__ out) {
+  const uint32_t w = wave_index();
+  const uint64_t base = ((uint64_t)blockIdx.x * kWavesPerBlock + w) * 64;
+  if (base >= n) return;
+  const uint32_t lane = lane_id(), grp = lane >> 3, sub = lane & 7u;
+  for (uint32_t p = 0; p < 64; p += 8) {
+    const uint64_t k = base + p + grp;
+    const bool act = k < n;
+    // x differs per octet here, so its header is read per lane
+    const uint4* qx = qb.rows + (size_t)(act ? a[k] : 0u) * kQChunks;
+    const uint4 h = qx[0];
+    const float xs = __uint_as_float(h.x), xr = __uint_as_float(h.y), xa = __uint_as_float(h.z);
+    const float t0 = act ? T0[k] : 0.0f;
+    const float ub = q_ub_root_of<DT>(qb, t0, alpha);
+    const float lbT = (prune_bound_root(qb, t0, alpha) + xr) * (1.0f + kQSlack);
+    const uint4 xcode = qx[sub];
+    const uint4 bc = q_load(qb, act ? b[k] : 0u, act, sub);
+    const int c = q_octet_dot(xcode, bc, sub);
+    const float sy = __uint_as_float(bc.x), ry = __uint_as_float(bc.y), ay = __uint_as_float(bc.z);
+    const bool yes = q_pair_ub(xs, xa, xr, ub, sy, ry, ay, c);
+    const bool no = q_pair_proves(xs, xa, lbT, sy, ry, ay, c);
+    if (act && sub == 0) out[k] = yes ? 1u : (no ? 2u : 0u);
   }
 }
 
@@ -1705,6 +1765,47 @@ int dance_stage_qbound(const void* h_data, int dtype, uint32_t N, uint32_t dim, 
   return 0;
 }
 
+int dance_stage_insert_bound(const void* h_data, int dtype, uint32_t N, uint32_t dim, const uint32_t* a,
+                             const uint32_t* b, const float* T0, float alpha, uint64_t n, uint32_t* out) {
+  if (!h_data || !a || !b || !T0 || !out || N == 0 || dim == 0) return -1;
+  for (uint64_t i = 0; i < n; ++i)
+    if (a[i] >= N || b[i] >= N) {
+      std::fprintf(stderr, "[dance_hip] bound index out of range\n");
+      return -1;
+    }
+  StageCtx cx;
+  DCHECK(cx.open(h_data, dtype, N, dim));
+  DevBuf qbuf, da, db, dt, dout;
+  QBoundSet qb{};
+  DCHECK(build_qbound(cx.rows, qbuf, cx.s, &qb));
+  if (!qb.rows) {
+    std::fprintf(stderr, "[dance_hip] no distance bound for this row type / width (or DANCE_QBOUND=0)\n");
+    return -1;
+  }
+  const uint64_t m = std::max<uint64_t>(n, 1);
+  DCHECK(da.alloc(m * 4));
+  DCHECK(db.alloc(m * 4));
+  DCHECK(dt.alloc(m * 4));
+  DCHECK(dout.alloc(m * 4));
+  DCHECK(up(da.p, a, n * 4, cx.s));
+  DCHECK(up(db.p, b, n * 4, cx.s));
+  DCHECK(up(dt.p, T0, n * 4, cx.s));
+  const uint64_t waves = (n + 63) / 64;
+  if (waves) {
+    const dim3 grid((uint32_t)((waves + kWavesPerBlock - 1) / kWavesPerBlock));
+    if (cx.rows.dtype == DANCE_F16)
+      hipLaunchKernelGGL(k_insert_bound_pairs<DANCE_F16>, grid, dim3(kBlock), 0, cx.s, qb, da.as<uint32_t>(),
+                         db.as<uint32_t>(), dt.as<float>(), alpha, n, dout.as<uint32_t>());
+    else
+      hipLaunchKernelGGL(k_insert_bound_pairs<DANCE_F32>, grid, dim3(kBlock), 0, cx.s, qb, da.as<uint32_t>(),
+                         db.as<uint32_t>(), dt.as<float>(), alpha, n, dout.as<uint32_t>());
+    DHIP(hipGetLastError());
+  }
+  DCHECK(down(out, dout.p, n * 4, cx.s));
+  DHIP(hipStreamSynchronize(cx.s));
+  return 0;
+}
+
 int dance_stage_medoid(const void* h_data, int dtype, uint32_t N, uint32_t dim, float* scores, uint32_t* cands,
                        uint32_t* medoid) {
   if (!h_data || N == 0 || dim == 0) return -1;
@@ -1754,7 +1855,8 @@ int dance_stage_search(const void* h_data, int dtype, uint32_t N, uint32_t dim, 
   DevBuf qbuf;
   QBoundSet qb{};
   DCHECK(build_qbound(cx.rows, qbuf, cx.s, &qb));
-  DCHECK(launch_search(cx.rows, cx.st.g(), L, steps, alpha, start, nullptr, nullptr, qb, cx.s));
+  DCHECK(launch_search(cx.rows, cx.st.g(), L, steps, alpha, start, nullptr, nullptr, qb, cx.s,
+                       (insert_bound_iters() & 1u) != 0));
   return download_state(cx.st, cur, deg_cur, work, deg_work, wd, cx.s);
 }
 

@@ -78,6 +78,8 @@ struct VCounters {
   unsigned long long prune_rounds, prune_exact_rounds;       // selection rounds; those with exact pairs
   // DANCE_SEARCH_TIMING: k_prune_rank phase cycles, summed over waves.
   unsigned long long cyc_prune_rank, cyc_prune_gram, cyc_prune_rounds, cyc_prune_fill;
+  unsigned long long insert_bound_checks;  // online-insert occlusion pairs tested with the code-row bounds
+  unsigned long long insert_bound_skips;   // those whose exact distance the bounds made unnecessary
 };
 
 
@@ -359,7 +361,9 @@ __host__ __device__ constexpr uint32_t search_lds_words(uint32_t Cp) { return kV
 // QB compiles the quantized-bound path in (the launcher picks QB = true only
 // when the bound is on for the launch); QB = false kernels carry no bound code
 // and keep their register budget for the exact path.
-template <int DT, int CPL, int PS, bool QB>
+// IB (with QB, fp32/fp16 rows and C <= 128 only) adds the insert bound: the
+// online insert's occlusion test decides pairs on the code rows first.
+template <int DT, int CPL, int PS, bool QB, bool IB = false>
 struct SearchWave {
   const SearchArgs& a;
   uint32_t node, lane, grp, sub, Cp;
@@ -370,7 +374,7 @@ struct SearchWave {
   RegPool<PS> P;
   QSelf qme;
   uint32_t wdeg;
-  uint32_t n_search, n_insert, n_skip, n_mut, n_try, n_bchk, n_bskip;
+  uint32_t n_search, n_insert, n_skip, n_mut, n_try, n_bchk, n_bskip, n_ibchk, n_ibskip;
   uint64_t c_select = 0, c_insert = 0, c_dist = 0, c_pool = 0;
 
   __device__ SearchWave(const SearchArgs& args, uint32_t node_, uint32_t* base, uint32_t Cp_)
@@ -384,7 +388,7 @@ struct SearchWave {
     lst = reinterpret_cast<uint32_t*>(wdd + Cp);
     lsd = reinterpret_cast<float*>(lst + 64);
     ord = reinterpret_cast<uint32_t*>(lsd + 64);
-    n_search = n_insert = n_skip = n_mut = n_try = n_bchk = n_bskip = 0;
+    n_search = n_insert = n_skip = n_mut = n_try = n_bchk = n_bskip = n_ibchk = n_ibskip = 0;
   }
 
   // Drops from lst[0..n) the candidates whose distance the quantized bound
@@ -558,15 +562,79 @@ struct SearchWave {
     wave_sync();
   }
 
+  // The occlusion test of robust_insert with the insert bound: a pass of 8
+  // candidates first tests its pairs on the code rows (x's chunk in xcode).
+  // An upper bound that proves fl(alpha * d(y, x)) <= d_px proves an
+  // occluder and ends the test; pairs whose lower bound proves the opposite
+  // need nothing more; the others collect their ids in lst and lsd (128
+  // words, unused during the insert; nA <= C <= 128) and get exact
+  // distances, in passes of 8, once the bound passes end. The answer is the
+  // exact test's: every decision the bounds make is the one the exact
+  // distance would give, and the answer does not depend on the order.
+  __device__ __forceinline__ bool occlusion_bounded(uint32_t x, float dpx, const uint4& xcode, uint32_t nU,
+                                                    uint32_t nA) {
+    // x's header: lane 0 holds chunk 0 of its code row
+    const float xs = __uint_as_float(rdlane_u(xcode.x, 0));
+    const float xr = __uint_as_float(rdlane_u(xcode.y, 0));
+    const float xa = __uint_as_float(rdlane_u(xcode.z, 0));
+    const float ub = q_ub_root_of<DT>(a.qb, dpx, a.alpha);
+    const float lbT = (prune_bound_root(a.qb, dpx, a.alpha) + xr) * (1.0f + kQSlack);
+    uint32_t* open = lst;
+    uint32_t nopen = 0;
+    for (uint32_t p = 0; p < nA; p += 8) {
+      const uint32_t k0 = p + grp;
+      const bool a0 = k0 < nA;
+      const uint32_t y0 = a0 ? wid[ord[nU + k0]] : 0u;
+      const uint4 b = q_load(a.qb, y0, a0, sub);
+      const int c = q_octet_dot(xcode, b, sub);
+      const float sy = __uint_as_float(b.x), ry = __uint_as_float(b.y), ay = __uint_as_float(b.z);
+      const bool lead = sub == 0u && a0;
+      const uint32_t np = min(8u, nA - p);
+      n_ibchk += np;
+      if (wballot(lead && q_pair_ub(xs, xa, xr, ub, sy, ry, ay, c))) {
+        n_ibskip += np;
+        return true;
+      }
+      const uint64_t und = wballot(lead && !q_pair_proves(xs, xa, lbT, sy, ry, ay, c));
+      n_ibskip += np - popc64(und);
+      if (lead && ((und >> lane) & 1ull)) open[nopen + popc64(und & lanes_below(lane))] = y0;
+      nopen += popc64(und);
+    }
+    if (nopen == 0) return false;
+    wave_sync();
+    uint4 xv[CPL];
+    load_row<CPL>(a.rs, x, true, sub, xv);
+    bool occ = false;
+    uint32_t q = 0;
+    for (; q < nopen && !occ; q += 8) {
+      const uint32_t k = q + grp;
+      const bool act = k < nopen;
+      uint4 b0[CPL];
+      load_row<CPL>(a.rs, open[act ? k : 0u], act, sub, b0);
+      const float d0 = octet_finish<DT, CPL>(a.rs, sub, xv, b0, self_term<DT, CPL>(xv));
+      occ = (wballot(a.alpha * d0 <= dpx) & kOctetLeads & lanes_below(8u * (nopen - q))) != 0;
+    }
+    n_insert += min(q, nopen);  // distances of the passes made
+    wave_sync();
+    return occ;
+  }
+
   // dynamic_robust_insert_C_warp (vnew2.cu:759-877) on the LDS work row.
   __device__ __forceinline__ void robust_insert(uint32_t x, float dpx) {
     const uint32_t N = a.g.N, C = a.g.C;
     if (x == DANCE_INV || x >= N || x == node) return;
     n_try++;
-    // x's row is requested first (x < N), so its load overlaps the pass
-    // below; a repeated x leaves it unused.
+    // With the insert bound the occlusion test starts from x's code chunk
+    // and x's row is loaded where exact distances are needed; otherwise x's
+    // row is requested first (x < N), so its load overlaps the pass below (a
+    // repeated x leaves it unused).
+    constexpr bool kIB = QB && IB && DT != DANCE_U8;
     uint4 xv[CPL];
-    load_row<CPL>(a.rs, x, true, sub, xv);
+    uint4 xcode;
+    if constexpr (kIB)
+      xcode = a.qb.rows[(size_t)x * kQChunks + sub];  // launched only with code rows present
+    else
+      load_row<CPL>(a.rs, x, true, sub, xv);
     // One pass over the row: x already there ends the insert; otherwise the
     // usable entries nearer than x (nA, of which nL strictly) and farther
     // (nB); dpx is a number, so a usable entry is exactly one of nA and nB.
@@ -584,7 +652,6 @@ struct SearchWave {
       nB += popc64(v & wballot(dpy > dpx));
     }
     const uint32_t nU = wdeg - nA - nB;
-    const uint32_t xv_sq = self_term<DT, CPL>(xv);
     // Occlusion: exists y with d_py <= d_px and alpha * d(y, x) <= d_px. The
     // answer does not depend on the order; the candidates are the order's
     // ranks [nU, nU + nA) (usable entries with d_py <= d_px, nearest to the
@@ -592,17 +659,25 @@ struct SearchWave {
     // occluder.
     bool occluded = false;
     uint32_t p = 0;
-    for (; p < nA && !occluded; p += 8) {
-      const uint32_t k0 = p + grp;
-      const bool a0 = k0 < nA;
-      const uint32_t y0 = a0 ? wid[ord[nU + k0]] : 0u;
-      uint4 b0[CPL];
-      load_row<CPL>(a.rs, y0, a0, sub, b0);
-      const float d0 = octet_finish<DT, CPL>(a.rs, sub, xv, b0, xv_sq);
-      occluded = (wballot(a.alpha * d0 <= dpx) & kOctetLeads & lanes_below(8u * (nA - p))) != 0;
+    if constexpr (kIB) {
+      occluded = occlusion_bounded(x, dpx, xcode, nU, nA);
+      if (occluded) return;
+      load_row<CPL>(a.rs, x, true, sub, xv);  // for the victim test
+    } else {
+      const uint32_t xv_sq = self_term<DT, CPL>(xv);
+      for (; p < nA && !occluded; p += 8) {
+        const uint32_t k0 = p + grp;
+        const bool a0 = k0 < nA;
+        const uint32_t y0 = a0 ? wid[ord[nU + k0]] : 0u;
+        uint4 b0[CPL];
+        load_row<CPL>(a.rs, y0, a0, sub, b0);
+        const float d0 = octet_finish<DT, CPL>(a.rs, sub, xv, b0, xv_sq);
+        occluded = (wballot(a.alpha * d0 <= dpx) & kOctetLeads & lanes_below(8u * (nA - p))) != 0;
+      }
+      n_insert += min(p, nA);  // distances of the passes made
+      if (occluded) return;
     }
-    n_insert += min(p, nA);  // distances of the passes made
-    if (occluded) return;
+    const uint32_t xv_sq = self_term<DT, CPL>(xv);
     // Worst usable entry (largest d_py, lowest slot): the top of the order.
     int wpos = -1;
     float wdist = -FLT_MAX;
@@ -806,6 +881,10 @@ struct SearchWave {
         if (QB && a.qb.rows) {
           atomicAdd(&ctr_stripe(a.ctr)->bound_checks, (unsigned long long)n_bchk);
           atomicAdd(&ctr_stripe(a.ctr)->bound_skips, (unsigned long long)n_bskip);
+          if constexpr (IB) {
+            atomicAdd(&ctr_stripe(a.ctr)->insert_bound_checks, (unsigned long long)n_ibchk);
+            atomicAdd(&ctr_stripe(a.ctr)->insert_bound_skips, (unsigned long long)n_ibskip);
+          }
         }
 #if DANCE_SEARCH_TIMING
         atomicAdd(&ctr_stripe(a.ctr)->cyc_select, (unsigned long long)c_select);
@@ -825,25 +904,32 @@ struct SearchWave {
 // (default 5) with the bound compiled in (the allocator would otherwise
 // settle at 4 by a few registers), and DANCE_SEARCH_WAVES (default 6)
 // without it; the exact search fits in 68 registers and runs 7 waves per
-// SIMD (asking for 7 changes nothing). No constraint elsewhere.
+// SIMD (asking for 7 changes nothing). The insert-bound variant asks for
+// DANCE_SEARCH_WAVES_IB (default 6: 79 registers at 3 chunks per lane, no
+// spills). No constraint elsewhere.
 #ifndef DANCE_SEARCH_WAVES
 #define DANCE_SEARCH_WAVES 6
 #endif
 #ifndef DANCE_SEARCH_WAVES_QB
 #define DANCE_SEARCH_WAVES_QB 5
 #endif
-template <int CPL, int PS, bool QB>
-constexpr int kSearchMinWaves = (CPL <= 3 && PS == 2) ? (QB ? DANCE_SEARCH_WAVES_QB : DANCE_SEARCH_WAVES) : 1;
+#ifndef DANCE_SEARCH_WAVES_IB
+#define DANCE_SEARCH_WAVES_IB 6
+#endif
+template <int CPL, int PS, bool QB, bool IB>
+constexpr int kSearchMinWaves = (CPL <= 3 && PS == 2)
+                                    ? (IB ? DANCE_SEARCH_WAVES_IB : QB ? DANCE_SEARCH_WAVES_QB : DANCE_SEARCH_WAVES)
+                                    : 1;
 
 // search_prune_kernel_shared (vnew2.cu:1119-1439).
-template <int DT, int CPL, int PS, bool QB>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kSearchMinWaves<CPL, PS, QB>))) void k_search(SearchArgs a, uint32_t Cp) {
+template <int DT, int CPL, int PS, bool QB, bool IB = false>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kSearchMinWaves<CPL, PS, QB, IB>))) void k_search(SearchArgs a, uint32_t Cp) {
   extern __shared__ uint32_t smem[];
   const uint32_t w = wave_index();
   const uint32_t gw = xcd_block(grid_block(), grid_blocks()) * kWavesPerBlock + w;
   if (gw >= a.g.N) return;
   const uint32_t node = a.order ? a.order[gw] : gw;
-  SearchWave<DT, CPL, PS, QB> sw(a, node, smem + w * search_lds_words(Cp), Cp);
+  SearchWave<DT, CPL, PS, QB, IB> sw(a, node, smem + w * search_lds_words(Cp), Cp);
   sw.run();
 }
 

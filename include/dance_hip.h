@@ -65,6 +65,13 @@ typedef struct DanceKernelProfile {
      * write-back, summed over waves */
     uint64_t prune_rounds, prune_exact_rounds;
     uint64_t cyc_prune_rank, cyc_prune_gram, cyc_prune_rounds, cyc_prune_fill;
+    /* The insert bound (fp32/fp16 rows of <= 112 dims, C <= 128, L <= 128):
+     * online-insert occlusion pairs tested on the code rows, and those whose
+     * exact distance the code-row bounds made unnecessary, in total and per
+     * iteration. DANCE_INSERT_BOUND_ITERS selects the iterations (bit i =
+     * iteration i, among those with the search bound on; default 0x1). */
+    uint64_t insert_bound_checks, insert_bound_skips;
+    uint64_t insert_bound_checks_iter[DANCE_MAX_ITERS], insert_bound_skips_iter[DANCE_MAX_ITERS];
 } DanceKernelProfile;
 
 /* Full standard (vnew2) build with the vectors already resident in device
@@ -305,6 +312,14 @@ int dance_stage_distances(const void *h_data, int dtype, uint32_t num_points, ui
  * dist(a[i], b[i]) >= T[i]. fp32/fp16 rows of <= 112 dims; -1 otherwise. */
 int dance_stage_qbound(const void *h_data, int dtype, uint32_t num_points, uint32_t dim, const uint32_t *a,
                        const uint32_t *b, const float *T, uint64_t n, uint32_t *flags);
+
+/* The online insert's occlusion-pair bounds on explicit pairs (no
+ * counterpart in the reference; they only skip work), with x = a[i], y = b[i]
+ * and T0[i] = d_px: out[i] = 1 when the code rows prove
+ * fl(alpha * dist(x, y)) <= T0[i], 2 when they prove it > T0[i], 0 when
+ * neither. fp32/fp16 rows of <= 112 dims; -1 otherwise. */
+int dance_stage_insert_bound(const void *h_data, int dtype, uint32_t num_points, uint32_t dim, const uint32_t *a,
+                             const uint32_t *b, const float *T0, float alpha, uint64_t n, uint32_t *out);
 
 /* medoid_score_kernel_warp + host top-1 (src/gpu_vamana_vnew2.cu:1032-1064, 2359-2479).
  * scores/cands: min(1024, N) entries. */

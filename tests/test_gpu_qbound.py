@@ -76,6 +76,71 @@ def test_bound_is_sound_f16():
     assert check_sound(x, a, b) > 0
 
 
+def check_insert_bound_sound(x, a, b, alpha):
+    """Every pair the insert bound decides is decided as the exact test
+    fl(alpha * dist) <= T0 would decide it, for T0 at, one ulp either side
+    of, and well away from fl(alpha * dist), and for degenerate T0."""
+    d = D.stage_distances(x, a, b)
+    al = np.float32(alpha)
+    ad = al * d  # fl(alpha * dist), as the insert evaluates it
+    yes_total = no_total = 0
+    with np.errstate(invalid="ignore", over="ignore"):
+        for T0 in (ad, np.nextafter(ad, np.float32(-np.inf)), np.nextafter(ad, np.float32(np.inf)),
+                   ad * np.float32(1.5), ad * np.float32(0.7), ad * np.float32(1 + 1e-6), ad * np.float32(1 - 1e-6),
+                   np.zeros_like(d), np.full_like(d, FMAX), np.full_like(d, 1e-38), np.full_like(d, 1e30),
+                   np.full_like(d, np.float32(np.nanmedian(ad[np.isfinite(ad)])))):
+            T0 = np.ascontiguousarray(T0, np.float32)
+            f = D.stage_insert_bound(x, a, b, T0, alpha)
+            holds = ad <= T0
+            bad_yes = (f == 1) & ~holds
+            bad_no = (f == 2) & holds
+            assert not bad_yes.any(), f"upper bound wrong at {np.nonzero(bad_yes)[0][:5]}: ad={ad[bad_yes][:3]} T0={T0[bad_yes][:3]}"
+            assert not bad_no.any(), f"lower bound wrong at {np.nonzero(bad_no)[0][:5]}: ad={ad[bad_no][:3]} T0={T0[bad_no][:3]}"
+            assert set(np.unique(f)) <= {0, 1, 2}
+            yes_total += int((f == 1).sum())
+            no_total += int((f == 2).sum())
+    return yes_total, no_total
+
+
+@pytest.mark.parametrize("alpha", [1.0, 1.2, 2.0, 0.8])
+@pytest.mark.parametrize("dim", [96, 112, 20, 7])
+def test_insert_bound_is_sound_f32(dim, alpha):
+    x = adversarial(4000, dim, seed=dim + 3)
+    a, b = pairs(4000, 20000, seed=dim + 4)
+    yes, no = check_insert_bound_sound(x, a, b, alpha)
+    assert yes > 0 and no > 0
+
+
+@pytest.mark.parametrize("alpha", [1.0, 1.2])
+def test_insert_bound_is_sound_f16(alpha):
+    """fp16 rows up to 3e4 (binary16 squares overflow to +inf past a
+    difference of 256): the upper bound's cap keeps it from proving those."""
+    x = adversarial(3000, 96, seed=9, dtype=np.float16, huge=False)
+    a, b = pairs(3000, 20000, seed=10)
+    yes, no = check_insert_bound_sound(x, a, b, alpha)
+    assert yes > 0 and no > 0
+    big = np.arange(60, 70, dtype=np.uint32)  # rows scaled by 3e4
+    aa = np.repeat(big, 3000)
+    bb = np.tile(np.arange(3000, dtype=np.uint32), 10)
+    d = D.stage_distances(x, aa, bb)
+    assert np.isinf(d).any()
+    f = D.stage_insert_bound(x, aa, bb, np.full(aa.shape[0], 1e30, np.float32), alpha)
+    assert not (f[np.isinf(d)] == 1).any()
+
+
+def test_insert_bound_never_decides_non_finite_rows_wrongly():
+    x = adversarial(500, 96, seed=8)
+    x[100] = np.inf
+    x[101, 3] = np.nan
+    x[102, 5] = -np.inf
+    a = np.repeat(np.arange(100, 103, dtype=np.uint32), 500)
+    b = np.tile(np.arange(500, dtype=np.uint32), 3)
+    for aa, bb in ((a, b), (b, a)):
+        for T0 in (np.full(aa.shape[0], FMAX, np.float32), np.full(aa.shape[0], 1.0, np.float32)):
+            f = D.stage_insert_bound(x, aa, bb, T0, 1.2)
+            assert not f.any()  # r = +inf rows: neither bound proves anything
+
+
 def test_bound_never_flags_non_finite_rows():
     x = adversarial(500, 96, seed=8)
     x[100] = np.inf
@@ -166,20 +231,28 @@ def test_build_identical_with_bound_off_first_and_every_iteration(profile):
         D.set_profile(profile)
         for name, env in (("off", {"DANCE_QBOUND": "0"}), ("first", {}),
                           ("all", {"DANCE_QBOUND_ITERS": "15", "DANCE_QBOUND_PRUNE_ITERS": "15"}),
-                          ("prune_none", {"DANCE_QBOUND_PRUNE_ITERS": "0"})):
+                          ("prune_none", {"DANCE_QBOUND_PRUNE_ITERS": "0"}),
+                          ("insert_all", {"DANCE_QBOUND_ITERS": "15", "DANCE_INSERT_BOUND_ITERS": "15"}),
+                          ("insert_none", {"DANCE_INSERT_BOUND_ITERS": "0"})):
             with _env(**env):
                 res = D.vamana_build(x, 32, 64, 48, 32)
             assert res.medoid == om, name
             assert np.array_equal(res.degree, od), name
             assert np.array_equal(res.graph, og), name
             kp = res.kernel_profile
-            seen[name] = (kp["bound_checks"], kp["bound_skips"], kp["prune_bound_checks"], kp["prune_bound_skips"])
+            seen[name] = (kp["bound_checks"], kp["bound_skips"], kp["prune_bound_checks"], kp["prune_bound_skips"],
+                          kp["insert_bound_checks"], kp["insert_bound_skips"], kp["insert_bound_checks_iter"][0],
+                          kp["insert_bound_checks_iter"][3])
     finally:
         D.set_profile("QUALITY")
-    assert seen["off"] == (0, 0, 0, 0)
+    assert seen["off"] == (0,) * 8
+    # the insert bound: iteration 0 by default, every iteration on request, never without the search bound
+    assert seen["first"][4] > 0 and seen["first"][5] > 0 and seen["first"][6] == seen["first"][4]
+    assert seen["insert_all"][7] > 0 and seen["insert_all"][4] > seen["first"][4]
+    assert seen["insert_none"][4] == 0
     assert seen["first"][0] > 0 and seen["first"][1] > 0 and seen["first"][3] > 0
     assert seen["all"][0] > seen["first"][0]
-    assert seen["prune_none"][2:] == (0, 0)
+    assert seen["prune_none"][2:4] == (0, 0)
 
 
 @pytest.mark.parametrize("profile", ["QUALITY", "FAST_SMALL"])
@@ -197,7 +270,8 @@ def test_build_with_non_finite_rows(profile):
     og, od, om = O.vnew2_build(ox, 32, 64, 48, 32)
     try:
         D.set_profile(profile)
-        for env in ({}, {"DANCE_QBOUND": "0"}, {"DANCE_QBOUND_ITERS": "15", "DANCE_QBOUND_PRUNE_ITERS": "15"}):
+        for env in ({}, {"DANCE_QBOUND": "0"}, {"DANCE_QBOUND_ITERS": "15", "DANCE_QBOUND_PRUNE_ITERS": "15",
+                                                 "DANCE_INSERT_BOUND_ITERS": "15"}):
             with _env(**env):
                 res = D.vamana_build(x, 32, 64, 48, 32)
             assert res.medoid == om, env
