@@ -251,9 +251,12 @@ static int build_qbound(const Rows& rows, DevBuf& buf, hipStream_t s, QBoundSet*
 // insert_bound: with the search bound on, the online insert's occlusion test
 // also decides pairs on the code rows (fp32/fp16 rows of at most 3 chunks
 // per lane, C <= 128, L <= 128; elsewhere the request is ignored).
+// hashed_cur: cur is still k_init's graph (the first iteration), so the L <=
+// 128 variants recompute expanded vertices' neighbours instead of gathering
+// them.
 static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t steps, float alpha, uint32_t start,
                          const uint32_t* order, VCounters* ctr, const QBoundSet& qb, hipStream_t s,
-                         bool insert_bound) {
+                         bool insert_bound, bool hashed_cur) {
   const int cpl = pick_cpl(rows.rs.nch);
   const uint32_t Cp = round64(g.C);
   const size_t lds = (size_t)kWavesPerBlock * search_lds_words(Cp) * 4;
@@ -271,12 +274,17 @@ static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t ste
         // (fp16 rows of at most 112 dims take 2 chunks per lane)
         if constexpr (CPL <= (DT == DANCE_F16 ? 2 : 3)) {
           if (insert_bound && L <= 128 && g.C <= 128) {  // nA <= C <= 128 fits the open-pair list
-            hipLaunchKernelGGL((k_search<DT, CPL, 2, true, true>), xcd_grid(g.N), dim3(kBlock), lds, s, a, Cp);
+            if (hashed_cur)
+              hipLaunchKernelGGL((k_search<DT, CPL, 2, true, true, true>), xcd_grid(g.N), dim3(kBlock), lds, s, a, Cp);
+            else
+              hipLaunchKernelGGL((k_search<DT, CPL, 2, true, true>), xcd_grid(g.N), dim3(kBlock), lds, s, a, Cp);
             DHIP(hipGetLastError());
             return 0;
           }
         }
-        if (L <= 128)
+        if (L <= 128 && hashed_cur)
+          hipLaunchKernelGGL((k_search<DT, CPL, 2, true, false, true>), xcd_grid(g.N), dim3(kBlock), lds, s, a, Cp);
+        else if (L <= 128)
           hipLaunchKernelGGL((k_search<DT, CPL, 2, true>), xcd_grid(g.N), dim3(kBlock), lds, s, a, Cp);
         else
           hipLaunchKernelGGL((k_search<DT, CPL, 4, true>), xcd_grid(g.N), dim3(kBlock), lds, s, a, Cp);
@@ -285,7 +293,9 @@ static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t ste
       }
     }
     // pools above 256 entries (16 slots per lane) run the exact variant only
-    if (L <= 128)
+    if (L <= 128 && hashed_cur)
+      hipLaunchKernelGGL((k_search<DT, CPL, 2, false, false, true>), xcd_grid(g.N), dim3(kBlock), lds, s, a, Cp);
+    else if (L <= 128)
       hipLaunchKernelGGL((k_search<DT, CPL, 2, false>), xcd_grid(g.N), dim3(kBlock), lds, s, a, Cp);
     else if (L <= 256)
       hipLaunchKernelGGL((k_search<DT, CPL, 4, false>), xcd_grid(g.N), dim3(kBlock), lds, s, a, Cp);
@@ -751,7 +761,8 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
       std::printf("[gpu_vamana_build] iteration %u / %u, alpha=%.3f\n", it + 1, iters, (double)alpha);
     DCHECK(record(iev[it].s0, s));
     const QBoundSet qb_it = ((q_iters >> it) & 1u) ? qb : QBoundSet{nullptr, 0.0f, 0.0f};
-    DCHECK(launch_search(rows, g, L, steps, alpha, start, order, ctr, qb_it, s, ((ib_iters >> it) & 1u) != 0));
+    DCHECK(launch_search(rows, g, L, steps, alpha, start, order, ctr, qb_it, s, ((ib_iters >> it) & 1u) != 0,
+                         it == 0));  // k_init wrote cur just before
     DCHECK(record(iev[it].s1, s));
     RevCsr rev{};
     DCHECK(build_reverse_csr(g, rws, s, &rev));
@@ -1856,7 +1867,7 @@ int dance_stage_search(const void* h_data, int dtype, uint32_t N, uint32_t dim, 
   QBoundSet qb{};
   DCHECK(build_qbound(cx.rows, qbuf, cx.s, &qb));
   DCHECK(launch_search(cx.rows, cx.st.g(), L, steps, alpha, start, nullptr, nullptr, qb, cx.s,
-                       (insert_bound_iters() & 1u) != 0));
+                       (insert_bound_iters() & 1u) != 0, false));  // cur comes from the caller
   return download_state(cx.st, cur, deg_cur, work, deg_work, wd, cx.s);
 }
 

@@ -344,6 +344,13 @@ __device__ __forceinline__ uint32_t vis_slot(uint32_t id) {
   return __umulhi(id * 0x9E3779B1u, kVis);
 }
 
+// Neighbour i of `node` in the random initial graph: the cur rows k_init
+// writes (init_random_graph, vnew2.cu:1066-1117).
+__device__ __forceinline__ uint32_t init_neighbor(uint32_t node, uint32_t i, uint32_t N) {
+  const uint32_t nb = d_det_neighbor(node, i, N);
+  return (N <= 1 || nb == DANCE_INV || nb >= N || nb == node) ? DANCE_INV : nb;
+}
+
 struct SearchArgs {
   RowSet rs;
   GraphBufs g;
@@ -362,8 +369,12 @@ __host__ __device__ constexpr uint32_t search_lds_words(uint32_t Cp) { return kV
 // when the bound is on for the launch); QB = false kernels carry no bound code
 // and keep their register budget for the exact path.
 // IB (with QB, fp32/fp16 rows and C <= 128 only) adds the insert bound: the
-// online insert's occlusion test decides pairs on the code rows first.
-template <int DT, int CPL, int PS, bool QB, bool IB = false>
+// online insert's occlusion test decides pairs on the code rows first. HC
+// (launched only while cur is still k_init's graph, i.e. in the first
+// iteration) takes an expanded vertex's neighbours from init_neighbor
+// instead of gathering its cur row and degree: the same values, without
+// three random cache lines per expansion.
+template <int DT, int CPL, int PS, bool QB, bool IB = false, bool HC = false>
 struct SearchWave {
   const SearchArgs& a;
   uint32_t node, lane, grp, sub, Cp;
@@ -851,9 +862,10 @@ struct SearchWave {
       if (x == DANCE_INV || x >= N) break;
       n_exp++;
       // Issue the adjacency gather of x before the online insert.
-      const uint32_t degx = min(g.deg_cur[x], R);
+      const uint32_t degx = HC ? (N > 1u ? R : 0u) : min(g.deg_cur[x], R);
       const size_t xb = (size_t)x * R;
-      const uint32_t c0 = lane < degx ? g.cur[xb + lane] : DANCE_INV;
+      uint32_t c0 = DANCE_INV;
+      if (lane < degx) c0 = HC ? init_neighbor(x, lane, N) : g.cur[xb + lane];
       const uint64_t ts1 = dclock();
       c_select += ts1 - ts0;
       robust_insert(x, dx);
@@ -861,7 +873,7 @@ struct SearchWave {
       process_batch(c0);
       for (uint32_t b = 64; b < degx; b += 64) {
         const uint32_t pidx = b + lane;
-        process_batch(pidx < degx ? g.cur[xb + pidx] : DANCE_INV);
+        process_batch(pidx < degx ? (HC ? init_neighbor(x, pidx, N) : g.cur[xb + pidx]) : DANCE_INV);
       }
     }
     for (uint32_t i = lane; i < C; i += 64) {
@@ -904,7 +916,10 @@ struct SearchWave {
 // (default 5) with the bound compiled in (the allocator would otherwise
 // settle at 4 by a few registers), and DANCE_SEARCH_WAVES (default 6)
 // without it; the exact search fits in 68 registers and runs 7 waves per
-// SIMD (asking for 7 changes nothing). The insert-bound variant asks for
+// SIMD (asking for 7 changes nothing); the first-iteration one-chunk exact
+// variant (uint8 rows of 128 bytes) asks for 8, which its LDS allows, so
+// that its neighbour hash does not push the scalar registers past the
+// 8-wave limit. The insert-bound variant asks for
 // DANCE_SEARCH_WAVES_IB (default 6: 79 registers at 3 chunks per lane, no
 // spills). No constraint elsewhere.
 #ifndef DANCE_SEARCH_WAVES
@@ -916,20 +931,21 @@ struct SearchWave {
 #ifndef DANCE_SEARCH_WAVES_IB
 #define DANCE_SEARCH_WAVES_IB 6
 #endif
-template <int CPL, int PS, bool QB, bool IB>
-constexpr int kSearchMinWaves = (CPL <= 3 && PS == 2)
-                                    ? (IB ? DANCE_SEARCH_WAVES_IB : QB ? DANCE_SEARCH_WAVES_QB : DANCE_SEARCH_WAVES)
-                                    : 1;
+template <int CPL, int PS, bool QB, bool IB, bool HC>
+constexpr int kSearchMinWaves =
+    (CPL <= 3 && PS == 2)
+        ? (IB ? DANCE_SEARCH_WAVES_IB : QB ? DANCE_SEARCH_WAVES_QB : (CPL == 1 && HC) ? 8 : DANCE_SEARCH_WAVES)
+        : 1;
 
 // search_prune_kernel_shared (vnew2.cu:1119-1439).
-template <int DT, int CPL, int PS, bool QB, bool IB = false>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kSearchMinWaves<CPL, PS, QB, IB>))) void k_search(SearchArgs a, uint32_t Cp) {
+template <int DT, int CPL, int PS, bool QB, bool IB = false, bool HC = false>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kSearchMinWaves<CPL, PS, QB, IB, HC>))) void k_search(SearchArgs a, uint32_t Cp) {
   extern __shared__ uint32_t smem[];
   const uint32_t w = wave_index();
   const uint32_t gw = xcd_block(grid_block(), grid_blocks()) * kWavesPerBlock + w;
   if (gw >= a.g.N) return;
   const uint32_t node = a.order ? a.order[gw] : gw;
-  SearchWave<DT, CPL, PS, QB, IB> sw(a, node, smem + w * search_lds_words(Cp), Cp);
+  SearchWave<DT, CPL, PS, QB, IB, HC> sw(a, node, smem + w * search_lds_words(Cp), Cp);
   sw.run();
 }
 
@@ -2170,8 +2186,7 @@ __global__ __launch_bounds__(kBlock) void k_init(RowSet rs, GraphBufs g) {
   load_row<CPL>(rs, node, true, sub, nv);
   for (uint32_t b = 0; b < R; b += 64) {
     const uint32_t i = b + lane;
-    uint32_t nb = i < R ? d_det_neighbor(node, i, N) : DANCE_INV;
-    if (N <= 1 || nb == DANCE_INV || nb >= N || nb == node) nb = DANCE_INV;
+    const uint32_t nb = i < R ? init_neighbor(node, i, N) : DANCE_INV;
     const bool v = i < R && nb != DANCE_INV;
     const uint64_t m = wballot(v);
     const uint32_t n = popc64(m);
