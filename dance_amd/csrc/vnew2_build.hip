@@ -885,8 +885,10 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     p.prune_bound_skips_iter[it] = c.prune_bound_skips - b.prune_bound_skips;
     p.insert_bound_checks_iter[it] = c.insert_bound_checks - b.insert_bound_checks;
     p.insert_bound_skips_iter[it] = c.insert_bound_skips - b.insert_bound_skips;
+    // the first iteration's L <= 128 variants recompute adjacency rows (no gather)
+    const double adj = (it == 0 && L <= 128) ? 0.0 : 4.0 * R + 4.0;
     p.search_bytes_iter[it] = (double)(p.search_dist_iter[it] + p.insert_dist_iter[it]) * V +
-                              (double)p.expansions_iter[it] * (4.0 * R + 4.0) + (double)N * (V + 4.0 * R + 4.0 + 16.0 * C) +
+                              (double)p.expansions_iter[it] * adj + (double)N * (V + 4.0 * R + 4.0 + 16.0 * C) +
                               (double)(p.bound_checks_iter[it] + p.insert_bound_checks_iter[it]) * (kQChunks * 16.0);
     // the rank kernel with the bound reads every candidate's code row once;
     // k_prune reads the code rows of the pairs it tests; the rank kernel's
@@ -903,6 +905,10 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   p.search_bytes = (double)(p.search_dist + p.insert_dist) * V + (double)p.expansions * (4.0 * R + 4.0) +
                    (double)iters * N * (V + 4.0 * R + 4.0 + 16.0 * C) +
                    (double)(p.bound_checks + p.insert_bound_checks) * (kQChunks * 16.0);
+  if (timed) {  // the per-launch figures know which launch recomputed its adjacency rows
+    p.search_bytes = 0.0;
+    for (uint32_t it = 0; it < iters; ++it) p.search_bytes += p.search_bytes_iter[it];
+  }
   p.merge_bytes = (double)p.merge_dist * 4.0 + (double)p.reverse_edges * 4.0 +
                   (double)p.touched_rows * (16.0 * C + 8.0);
   p.prune_bytes = (double)p.prune_dist * V + (double)iters * N * (24.0 * C) +
