@@ -916,10 +916,11 @@ struct SearchWave {
 // (default 5) with the bound compiled in (the allocator would otherwise
 // settle at 4 by a few registers), and DANCE_SEARCH_WAVES (default 6)
 // without it; the exact search fits in 68 registers and runs 7 waves per
-// SIMD (asking for 7 changes nothing); the first-iteration one-chunk exact
-// variant (uint8 rows of 128 bytes) asks for 8, which its LDS allows, so
-// that its neighbour hash does not push the scalar registers past the
-// 8-wave limit. The insert-bound variant asks for
+// SIMD (asking for 7 changes nothing); the first-iteration exact variants of
+// one and two chunks per lane (uint8 rows of up to 256 bytes) ask for 8,
+// which their LDS allows at C <= 128, so that the neighbour hash does not
+// push the scalar registers past the 8-wave limit. The insert-bound variant
+// asks for
 // DANCE_SEARCH_WAVES_IB (default 6: 79 registers at 3 chunks per lane, no
 // spills). No constraint elsewhere.
 #ifndef DANCE_SEARCH_WAVES
@@ -934,7 +935,7 @@ struct SearchWave {
 template <int CPL, int PS, bool QB, bool IB, bool HC>
 constexpr int kSearchMinWaves =
     (CPL <= 3 && PS == 2)
-        ? (IB ? DANCE_SEARCH_WAVES_IB : QB ? DANCE_SEARCH_WAVES_QB : (CPL == 1 && HC) ? 8 : DANCE_SEARCH_WAVES)
+        ? (IB ? DANCE_SEARCH_WAVES_IB : QB ? DANCE_SEARCH_WAVES_QB : (CPL <= 2 && HC) ? 8 : DANCE_SEARCH_WAVES)
         : 1;
 
 // search_prune_kernel_shared (vnew2.cu:1119-1439).
