@@ -590,7 +590,7 @@ struct SearchWave {
     const float xa = __uint_as_float(rdlane_u(xcode.z, 0));
     const float ub = q_ub_root_of<DT>(a.qb, dpx, a.alpha);
     const float lbT = (prune_bound_root(a.qb, dpx, a.alpha) + xr) * (1.0f + kQSlack);
-    uint32_t* open = lst;
+    uint32_t* pend = lst;
     uint32_t nopen = 0;
     for (uint32_t p = 0; p < nA; p += 8) {
       const uint32_t k0 = p + grp;
@@ -608,7 +608,7 @@ struct SearchWave {
       }
       const uint64_t und = wballot(lead && !q_pair_proves(xs, xa, lbT, sy, ry, ay, c));
       n_ibskip += np - popc64(und);
-      if (lead && ((und >> lane) & 1ull)) open[nopen + popc64(und & lanes_below(lane))] = y0;
+      if (lead && ((und >> lane) & 1ull)) pend[nopen + popc64(und & lanes_below(lane))] = y0;
       nopen += popc64(und);
     }
     if (nopen == 0) return false;
@@ -621,7 +621,7 @@ struct SearchWave {
       const uint32_t k = q + grp;
       const bool act = k < nopen;
       uint4 b0[CPL];
-      load_row<CPL>(a.rs, open[act ? k : 0u], act, sub, b0);
+      load_row<CPL>(a.rs, pend[act ? k : 0u], act, sub, b0);
       const float d0 = octet_finish<DT, CPL>(a.rs, sub, xv, b0, self_term<DT, CPL>(xv));
       occ = (wballot(a.alpha * d0 <= dpx) & kOctetLeads & lanes_below(8u * (nopen - q))) != 0;
     }
@@ -919,10 +919,9 @@ struct SearchWave {
 // SIMD (asking for 7 changes nothing); the first-iteration exact variants of
 // one and two chunks per lane (uint8 rows of up to 256 bytes) ask for 8,
 // which their LDS allows at C <= 128, so that the neighbour hash does not
-// push the scalar registers past the 8-wave limit. The insert-bound variant
-// asks for
-// DANCE_SEARCH_WAVES_IB (default 6: 79 registers at 3 chunks per lane, no
-// spills). No constraint elsewhere.
+// push the scalar registers past the 8-wave limit. The insert-bound variants
+// ask for DANCE_SEARCH_WAVES_IB (default 6: 79-80 registers at 3 chunks per
+// lane, no spills). No constraint elsewhere.
 #ifndef DANCE_SEARCH_WAVES
 #define DANCE_SEARCH_WAVES 6
 #endif
