@@ -350,6 +350,20 @@ def test_end_to_end_iteration_count(kind, iters, alpha_from, monkeypatch):
     assert all(t > 0 for t in kp["search_iter_ms"]) and all(t > 0 for t in kp["prune_iter_ms"])
 
 
+@pytest.mark.parametrize("kind,R,L,C,steps", [("f32", 96, 128, 128, 64), ("u8", 80, 100, 120, 48),
+                                              ("f32", 72, 100, 250, 64)])
+def test_end_to_end_wide_degree(kind, R, L, C, steps):
+    # degrees above one 64-lane batch: the first iteration's recomputed
+    # neighbours and every later gather take two batches; C = 128 is the
+    # largest work row of the insert bound's variant, C = 250 runs without it
+    data = make_data(kind, 3000, 96 if kind == "f32" else 128, seed=R)
+    res = D.vamana_build(data, R, L, C, steps)
+    og, od, om = O.vnew2_build(data, R, L, C, steps)
+    assert res.medoid == om
+    assert np.array_equal(res.degree, od)
+    assert np.array_equal(res.graph, og)
+
+
 @pytest.mark.parametrize("kind", ["f32", "u8"])
 @pytest.mark.parametrize("n", [1, 2, 3, 17, 130])
 def test_end_to_end_tiny_inputs(kind, n):
