@@ -251,9 +251,10 @@ static int build_qbound(const Rows& rows, DevBuf& buf, hipStream_t s, QBoundSet*
 // insert_bound: with the search bound on, the online insert's occlusion test
 // also decides pairs on the code rows (fp32/fp16 rows of at most 3 chunks
 // per lane, C <= 128, L <= 128; elsewhere the request is ignored).
-// hashed_cur: cur is still k_init's graph (the first iteration), so the L <=
-// 128 variants recompute expanded vertices' neighbours instead of gathering
-// them.
+// hashed_cur: the first iteration, whose graph is the random initial one: the
+// L <= 128 variants recompute expanded vertices' neighbours instead of
+// gathering them, and each vertex's own initial row with its distances (the
+// build then launches no k_init at L <= 128).
 static int launch_search(const Rows& rows, GraphBufs g, uint32_t L, uint32_t steps, float alpha, uint32_t start,
                          const uint32_t* order, VCounters* ctr, const QBoundSet& qb, hipStream_t s,
                          bool insert_bound, bool hashed_cur) {
@@ -724,7 +725,11 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
   const uint32_t start = best == DANCE_INV ? 0u : hc[best];
   if (stats) stats->medoid_seconds = now_sec() - t_med;
 
-  DCHECK(launch_init(rows, g, s));
+  // At L <= 128 the first search launch computes the initial rows itself
+  // (its hashed-neighbour variants), and nothing reads cur, work or wd
+  // before it; k_init runs for the other variants only.
+  const bool init_in_search = L <= 128;
+  if (!init_in_search) DCHECK(launch_init(rows, g, s));
   DevBuf qbuf;
   QBoundSet qb{};
   DCHECK(build_qbound(rows, qbuf, s, &qb));

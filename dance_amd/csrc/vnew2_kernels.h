@@ -370,10 +370,11 @@ __host__ __device__ constexpr uint32_t search_lds_words(uint32_t Cp) { return kV
 // and keep their register budget for the exact path.
 // IB (with QB, fp32/fp16 rows and C <= 128 only) adds the insert bound: the
 // online insert's occlusion test decides pairs on the code rows first. HC
-// (launched only while cur is still k_init's graph, i.e. in the first
-// iteration) takes an expanded vertex's neighbours from init_neighbor
-// instead of gathering its cur row and degree: the same values, without
-// three random cache lines per expansion.
+// (the first iteration, whose graph is the random initial one) takes an
+// expanded vertex's neighbours from init_neighbor instead of gathering its
+// cur row and degree: the same values, without three random cache lines per
+// expansion; and it computes the vertex's own initial row and distances as
+// k_init would, so that the build skips k_init.
 template <int DT, int CPL, int PS, bool QB, bool IB = false, bool HC = false>
 struct SearchWave {
   const SearchArgs& a;
@@ -760,20 +761,40 @@ struct SearchWave {
     av_sq = self_term<DT, CPL>(av);
     if (QB && a.qb.rows) q_load_self(a.qb, node, qme);
     // Work row := current row with its stored distances (vnew2.cu:1186-1212).
-    const uint32_t deg_self = min(g.deg_cur[node], R);
-    const size_t cb = (size_t)node * R, wb = (size_t)node * C;
-    for (uint32_t i = lane; i < Cp; i += 64) {
-      uint32_t nb = DANCE_INV;
-      float dist = FLT_MAX;
-      if (i < deg_self) {
-        nb = g.cur[cb + i];
-        if (valid_for(nb, N, node))
-          dist = g.wd[wb + i];
-        else
-          nb = DANCE_INV;
+    // With HC the current row is the random initial graph's, computed here
+    // with its distances as k_init computes them (init_neighbor, batch_dist
+    // from the cached row), so the build needs no k_init launch.
+    const uint32_t deg_self = HC ? (N > 1u ? R : 0u) : min(g.deg_cur[node], R);
+    const size_t wb = (size_t)node * C;
+    if constexpr (HC) {
+      for (uint32_t b = 0; b < Cp; b += 64) {  // Cp is a multiple of 64
+        const uint32_t i = b + lane;
+        const uint32_t nb = i < deg_self ? init_neighbor(node, i, N) : DANCE_INV;
+        const bool v = nb != DANCE_INV;
+        const uint64_t m = wballot(v);
+        const uint32_t n = popc64(m);
+        if (v) lst[mbcnt64(m)] = nb;
+        wave_sync();
+        if (n) batch_dist<DT, CPL>(a.rs, av, av_sq, lst, lsd, n, grp, sub);
+        wid[i] = nb;
+        wdd[i] = v ? lsd[mbcnt64(m)] : FLT_MAX;
+        wave_sync();
       }
-      wid[i] = nb;
-      wdd[i] = dist;
+    } else {
+      const size_t cb = (size_t)node * R;
+      for (uint32_t i = lane; i < Cp; i += 64) {
+        uint32_t nb = DANCE_INV;
+        float dist = FLT_MAX;
+        if (i < deg_self) {
+          nb = g.cur[cb + i];
+          if (valid_for(nb, N, node))
+            dist = g.wd[wb + i];
+          else
+            nb = DANCE_INV;
+        }
+        wid[i] = nb;
+        wdd[i] = dist;
+      }
     }
     wdeg = deg_self;
     P.init(a.L);
