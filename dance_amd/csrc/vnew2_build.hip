@@ -890,10 +890,15 @@ static int run_build(const Rows& rows, uint32_t R, uint32_t L, uint32_t C, uint3
     p.prune_bound_skips_iter[it] = c.prune_bound_skips - b.prune_bound_skips;
     p.insert_bound_checks_iter[it] = c.insert_bound_checks - b.insert_bound_checks;
     p.insert_bound_skips_iter[it] = c.insert_bound_skips - b.insert_bound_skips;
-    // the first iteration's L <= 128 variants recompute adjacency rows (no gather)
-    const double adj = (it == 0 && L <= 128) ? 0.0 : 4.0 * R + 4.0;
+    // The first iteration's L <= 128 variants compute the random initial graph:
+    // no adjacency or cur row is read, and each vertex gathers its R initial
+    // neighbours' rows and writes its work row (8C) instead of reading and
+    // writing it (16C).
+    const bool init_it = it == 0 && L <= 128;
+    const double adj = init_it ? 0.0 : 4.0 * R + 4.0;
+    const double per_vertex = init_it ? V + R * V + 8.0 * C : V + 4.0 * R + 4.0 + 16.0 * C;
     p.search_bytes_iter[it] = (double)(p.search_dist_iter[it] + p.insert_dist_iter[it]) * V +
-                              (double)p.expansions_iter[it] * adj + (double)N * (V + 4.0 * R + 4.0 + 16.0 * C) +
+                              (double)p.expansions_iter[it] * adj + (double)N * per_vertex +
                               (double)(p.bound_checks_iter[it] + p.insert_bound_checks_iter[it]) * (kQChunks * 16.0);
     // the rank kernel with the bound reads every candidate's code row once;
     // k_prune reads the code rows of the pairs it tests; the rank kernel's
