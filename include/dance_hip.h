@@ -27,7 +27,9 @@ enum { DANCE_DTYPE_F32 = 0, DANCE_DTYPE_U8 = 1, DANCE_DTYPE_F16 = 2 };
 /* Per-kernel timings (HIP events on the build stream) and algorithmic work
  * counted on the device by each wave. Bytes are algorithmic: one vector row
  * per distance gathered, plus adjacency and work rows as documented in
- * dance_amd/csrc/vnew2_build.hip. */
+ * dance_amd/csrc/vnew2_build.hip. init_ms covers the quantization and the
+ * locality schedule, and the random initial graph's kernel at L > 128 (at
+ * L <= 128 the first search launch computes that graph itself). */
 typedef struct DanceKernelProfile {
     double medoid_ms, init_ms, search_ms, reverse_ms, merge_ms, prune_ms, total_ms;
     uint32_t iterations;
