@@ -330,7 +330,8 @@ def test_end_to_end_wide_search_list(kind, L, steps):
 
 
 @pytest.mark.parametrize("kind,iters,alpha_from", [("f32", 5, None), ("f32", 6, None), ("f32", 6, 0),
-                                                    ("u8", 6, None), ("f32", 1, None), ("f32", 8, 5)])
+                                                    ("u8", 6, None), ("f32", 1, None), ("f32", 8, 5),
+                                                    ("u8", 1, None), ("f32", 2, None), ("u8", 2, 0)])
 def test_end_to_end_iteration_count(kind, iters, alpha_from, monkeypatch):
     """The reference's VAMANA_ITERS (gpu_vamana_config.h:78-79) through
     DANCE_VAMANA_ITERS, alone and with the alpha schedule knob; the kernel
