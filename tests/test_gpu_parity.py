@@ -315,11 +315,14 @@ def test_end_to_end_locality_schedule(kind, monkeypatch):
 
 
 @pytest.mark.parametrize("kind,L,steps", [("f32", 300, 64), ("u8", 500, 80), ("f32", 1000, 100),
-                                          ("f32", 257, 257)])
+                                          ("f32", 257, 257), ("f32", 200, 64), ("u8", 160, 96),
+                                          ("f32", 129, 64)])
 def test_end_to_end_wide_search_list(kind, L, steps):
-    """Build lists above 256 entries (the 16-slot pool; DiskANN callers build
-    with L of several hundred and the reference sizes its pool by L,
-    vnew2.cu:193-199, 2221), against the oracle."""
+    """Build lists above 128 entries: the 4-slot pool (L 129-256, with the
+    bound for fp32 rows and the random initial graph from k_init) and the
+    16-slot pool above 256 (DiskANN callers build with L of several hundred
+    and the reference sizes its pool by L, vnew2.cu:193-199, 2221), against
+    the oracle."""
     dim = 96 if kind != "u8" else 128
     data = make_data(kind, 3000, dim, seed=L)
     res = D.vamana_build(data, 32, L, 48, steps)
