@@ -545,20 +545,23 @@ static uint32_t alpha_from_iter(uint32_t iters) {
 }
 
 // Locality schedule (see k_cells_q / k_cells): order[] = vertices sorted by
-// nearest pivot. Pivots are K evenly spaced rows. K comes from
-// DANCE_LOCALITY_CELLS (default 1024, the fastest c3 build of 256..4096; 0
-// disables the schedule). Uses the reverse-sort buffers as scratch.
-static uint32_t locality_cells() {
+// their nearest pivots. Pivots are K evenly spaced rows. K comes from
+// DANCE_LOCALITY_CELLS (0 disables the schedule), by default 1024 for float
+// rows and 1536 for uint8 rows, the fastest counts with three-pivot keys
+// (c3 3.588 s at 1024 against 3.596 at 1536 and 3.594 / 3.630 at 512 / 256;
+// c4 2.525 s at 1024 against 2.516 at 1536 and 2.539 at 1625). Uses the
+// reverse-sort buffers as scratch.
+static uint32_t locality_cells(int dtype) {
   const char* e = std::getenv("DANCE_LOCALITY_CELLS");
   if (e && e[0]) return (uint32_t)std::strtoul(e, nullptr, 10);
-  return 1024;
+  return dtype == DANCE_U8 ? 1536u : 1024u;
 }
 
 
 static int build_schedule(const Rows& rows, const QBoundSet& qb, ReverseWs& ws, hipStream_t s,
                           const uint32_t** order_out) {
   const uint32_t N = rows.N;
-  const uint32_t K = std::min(locality_cells(), N);
+  const uint32_t K = std::min(locality_cells(rows.dtype), N);
   *order_out = nullptr;
   if (K < 2) return 0;
   DevBuf dpiv;
@@ -1221,7 +1224,7 @@ static size_t resident_build_bytes(const void* d_data, int dtype, int store, uin
   add(kMedoidCandidates * 4);       // scores
   add(kMedoidCandidates * 4);       // cands
   add((size_t)N * kQChunks * 16);   // code rows of the bound
-  add((size_t)std::min(locality_cells(), N) * 4);  // pivots
+  add((size_t)std::min(locality_cells(store), N) * 4);  // pivots
   add((size_t)N * 4);               // order
   for (size_t n : {(size_t)N, sort_items}) {  // the schedule's sort, then the reverse sort
     const size_t tiles = (n + kRadixTile - 1) / kRadixTile;
