@@ -575,9 +575,22 @@ static int build_schedule(const Rows& rows, const QBoundSet& qb, ReverseWs& ws, 
   // faces): c4 2.63 -> 2.57 s and c3 3.697 -> 3.689 s against the cell alone,
   // same graphs.
   const uint32_t lv = cell_levels(K, 3);
-  if (qb.rows) {
+  // the same cells from int8 MFMA tiles (DANCE_CELLS_MFMA=0: the dot-product
+  // kernel k_cells_q); one wave per 32 vertices
+  const char* em = std::getenv("DANCE_CELLS_MFMA");
+  const bool mfma_cells = !(em && em[0] == '0');
+  const dim3 mgrid((uint32_t)(((uint64_t)N + 127) / 128));
+  if (qb.rows && mfma_cells) {
+    hipLaunchKernelGGL(k_cells_mfma<false>, mgrid, dim3(256), 0, s, qb.rows, kQChunks, N, dpiv.as<uint32_t>(), K,
+                       lv, kb[0], vb[0]);
+    DHIP(hipGetLastError());
+  } else if (qb.rows) {
     // integer-code pivot search on the quantized rows
     hipLaunchKernelGGL(k_cells_q<false>, dim3((N + 255) / 256), dim3(256), 0, s, qb.rows, kQChunks, kQChunks, N,
+                       dpiv.as<uint32_t>(), K, lv, kb[0], vb[0]);
+    DHIP(hipGetLastError());
+  } else if (rows.dtype == DANCE_U8 && rows.rs.stride16 == 8u && mfma_cells) {  // 128-byte rows
+    hipLaunchKernelGGL(k_cells_mfma<true>, mgrid, dim3(256), 0, s, rows.rs.rows, rows.rs.stride16, N,
                        dpiv.as<uint32_t>(), K, lv, kb[0], vb[0]);
     DHIP(hipGetLastError());
   } else if (rows.dtype == DANCE_U8 && rows.rs.nch <= 8) {

@@ -2331,4 +2331,120 @@ __global__ __launch_bounds__(256) void k_cells_q(const uint4* __restrict__ rows,
   }
 }
 
+// k_cells_q on the matrix cores, for code rows (U8 = false) and uint8 rows of
+// one chunk group (128 bytes, U8 = true): one wave per 32 vertices, int8 MFMA
+// tiles of 32 pivots (rows) x 32 vertices (columns) over the 128 bytes (code
+// chunks 1-7, or the uint8 bytes shifted by -128). Lane l holds, for vertex
+// l % 32, pivots 8 (v >> 2) + (v & 3) + 4 (l >> 5) of each tile (v < 16), in
+// ascending order, keeps its own three nearest (first on ties), and the two
+// halves of a vertex merge by (distance, pivot) at the end. The distances
+// are k_cells_q's exactly (the same fp32 expression on the same integer dot
+// for code rows; the integer squared distance for uint8 rows, which
+// k_cells_q's fp32 expression also yields below 2^24), so the cells are too.
+template <bool U8>
+__global__ __launch_bounds__(256) void k_cells_mfma(const uint4* __restrict__ rows, uint32_t stride16, uint32_t N,
+                                                    const uint32_t* __restrict__ pivots, uint32_t K,
+                                                    uint32_t levels, uint32_t* __restrict__ cell,
+                                                    uint32_t* __restrict__ vid) {
+  __shared__ int pn_i[4][32];    // uint8 rows: |pivot'|^2
+  __shared__ float pn_f[4][32];  // code rows: a and s of the pivot
+  __shared__ float ps_f[4][32];
+  const uint32_t w = wave_index(), lane = lane_id(), jl = lane & 31u, half = lane >> 5;
+  const uint32_t v0 = (blockIdx.x * 4u + w) * 32u;
+  if (v0 >= N) return;  // the whole wave; no block-wide barrier follows
+  const uint32_t v = v0 + jl;
+  const bool act = v < N;
+  // 16 bytes of row `id` for K-step s: chunk 2 s + half of the uint8 row, or
+  // chunk 1 + 2 s + half of the code row (chunk 8 would be past the row: 0)
+  auto frag = [&](uint32_t id, bool ok, uint32_t step) -> v4i_t {
+    const uint32_t c = (U8 ? 0u : 1u) + 2u * step + half;
+    if (!ok || c >= 8u) return v4i_t{0, 0, 0, 0};
+    const uint4 q = rows[(size_t)id * stride16 + c];
+    if constexpr (U8)
+      return v4i_t{(int)(q.x ^ 0x80808080u), (int)(q.y ^ 0x80808080u), (int)(q.z ^ 0x80808080u),
+                   (int)(q.w ^ 0x80808080u)};
+    else
+      return v4i_t{(int)q.x, (int)q.y, (int)q.z, (int)q.w};
+  };
+  v4i_t B[4];
+#pragma unroll
+  for (uint32_t st = 0; st < 4; ++st) B[st] = frag(v, act, st);
+  int xn = 0;
+  float xa = 0.0f, xs = 1.0f;
+  if constexpr (U8) {
+    int part = 0;
+#pragma unroll
+    for (uint32_t st = 0; st < 4; ++st) part = i8_sq4(B[st], part);
+    xn = part + __shfl_xor(part, 32);
+  } else if (act) {
+    const uint4 h = rows[(size_t)v * stride16];
+    xs = __uint_as_float(h.x);
+    xa = __uint_as_float(h.z);
+  }
+  Nearest3 nb;
+  for (uint32_t t0 = 0; t0 < K; t0 += 32) {
+    const uint32_t pi = t0 + jl;
+    const bool pok = pi < K;
+    const uint32_t pid = pok ? pivots[pi] : 0u;
+    v4i_t A[4];
+#pragma unroll
+    for (uint32_t st = 0; st < 4; ++st) A[st] = frag(pid, pok, st);
+    wave_sync();  // the previous tile's reads of the pivot terms are done
+    if constexpr (U8) {
+      int part = 0;
+#pragma unroll
+      for (uint32_t st = 0; st < 4; ++st) part = i8_sq4(A[st], part);
+      part += __shfl_xor(part, 32);
+      if (lane < 32u) pn_i[w][jl] = part;
+    } else {
+      if (lane < 32u && pok) {
+        const uint4 h = rows[(size_t)pid * stride16];
+        pn_f[w][jl] = __uint_as_float(h.z);
+        ps_f[w][jl] = __uint_as_float(h.x);
+      }
+    }
+    v16i_t acc = {};
+#pragma unroll
+    for (uint32_t st = 0; st < 4; ++st) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[st], B[st], acc, 0, 0, 0);
+    wave_sync();
+    static_for<0, 16>([&](auto vc) {
+      constexpr uint32_t vv = decltype(vc)::value, ir0 = 8u * (vv >> 2) + (vv & 3u);
+      const uint32_t ir = ir0 + 4u * half, k = t0 + ir;
+      if (k < K) {
+        float d;
+        if constexpr (U8)
+          d = u8_gram_dist(xn, pn_i[w][ir], acc[vv]);
+        else
+          d = xa + pn_f[w][ir] - 2.0f * xs * ps_f[w][ir] * (float)acc[vv];
+        nb.add(d, k);
+      }
+    });
+  }
+  // merge the upper half's three into the lower half's, by (distance, pivot)
+  const float e1 = __shfl_xor(nb.d1, 32), e2 = __shfl_xor(nb.d2, 32), e3 = __shfl_xor(nb.d3, 32);
+  const uint32_t f1 = (uint32_t)__shfl_xor((int)nb.k1, 32), f2 = (uint32_t)__shfl_xor((int)nb.k2, 32),
+                 f3 = (uint32_t)__shfl_xor((int)nb.k3, 32);
+  if (half == 0u && act) {
+    // two sorted lists of three, popped from the front by selects
+    float a1 = nb.d1, a2 = nb.d2, a3 = nb.d3, b1 = e1, b2 = e2, b3 = e3;
+    uint32_t ka1 = nb.k1, ka2 = nb.k2, ka3 = nb.k3, kb1 = f1, kb2 = f2, kb3 = f3;
+    uint32_t out[3];
+#pragma unroll
+    for (int o = 0; o < 3; ++o) {
+      const bool ta = a1 < b1 || (a1 == b1 && ka1 < kb1);
+      out[o] = ta ? ka1 : kb1;
+      a1 = ta ? a2 : a1;
+      ka1 = ta ? ka2 : ka1;
+      a2 = ta ? a3 : a2;
+      ka2 = ta ? ka3 : ka2;
+      b1 = ta ? b1 : b2;
+      kb1 = ta ? kb1 : kb2;
+      b2 = ta ? b2 : b3;
+      kb2 = ta ? kb2 : kb3;
+    }
+    cell[v] = cell_key(out[0], out[1], out[2], K, levels);
+    vid[v] = v;
+  }
+}
+
 }  // namespace dance
